@@ -1,0 +1,192 @@
+/*
+ * mira_rocm.h -- C ABI of libmira_rocm.so, the gfx950 (MI355X) kernels behind
+ * MIRA's `rocm` target for W8A8 quantized inference.
+ *
+ * The reference (myramay/MIRA) has no native boundary: every op is a NumPy
+ * function in mira/ops.py, called through the Target/Executable protocol
+ * (mira/backends/base.py:13-26).  Each entry point below replaces one of those
+ * NumPy functions; the comment on each names it (file:line).
+ *
+ * Conventions
+ *  - Every pointer is a device pointer (hipMalloc'd or a torch-ROCm tensor's
+ *    data_ptr()).  No entry point allocates, frees or takes ownership.
+ *  - `stream` is a hipStream_t passed as void*; NULL means the null stream.
+ *    Work is enqueued asynchronously; nothing synchronises.
+ *  - Every entry point returns MR_OK (0) or an error code; mr_last_error()
+ *    then returns a message (thread-local, valid until the next call).
+ *    Arguments are validated on the host before any launch.
+ *  - Activations inside a rocm segment live in NHWC order.  int8 NHWC
+ *    tensors carry `c_pad` channels per pixel (a multiple of 16, or 4 for
+ *    the small-channel stem layout); channels >= c are never read as data
+ *    because the packed weights hold zeros there.
+ *  - Matmul-shaped tensors are row-major [M, K] with a row stride.
+ */
+#ifndef MIRA_ROCM_H
+#define MIRA_ROCM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MR_ABI_VERSION 1
+
+enum mr_status {
+  MR_OK = 0,
+  MR_EINVAL = 1,      /* bad argument (shape, pointer, alignment) */
+  MR_EHIP = 2,        /* a HIP runtime call failed */
+  MR_EUNSUPPORTED = 3 /* valid request this build has no kernel for */
+};
+
+/* Epilogue step functions: the fusable ops of mira/passes.py:151-152 that
+ * have exact IEEE-754 single-precision semantics (UNARY/BINARY tables,
+ * mira/ops.py:99-139).  relu == np.maximum(x, 0). */
+enum mr_epi_fn {
+  MR_EPI_ADD = 1,
+  MR_EPI_SUB = 2,
+  MR_EPI_MUL = 3,
+  MR_EPI_DIV = 4,
+  MR_EPI_MAX = 5,
+  MR_EPI_MIN = 6,
+  MR_EPI_RELU = 7
+};
+
+/* How an epilogue operand broadcasts onto the [rows, cols] result
+ * (rows = N*OH*OW pixels or matmul rows, cols = output channels). */
+enum mr_bcast {
+  MR_BC_SCALAR = 0, /* ptr[0]                       (0-d constants, e.g. ReLU6's 6) */
+  MR_BC_COL = 1,    /* ptr[col]                     (bias [N], [O,1,1], [1,O,1,1]) */
+  MR_BC_ROW = 2,    /* ptr[row * ld]                ([M,1] operands) */
+  MR_BC_FULL = 3    /* ptr[row * ld + col]          (residuals, same shape as result) */
+};
+
+#define MR_MAX_EPI 8
+
+/* One step of mira/ops.py:192-199 epilogue_ref: acc = fn(acc, other), or
+ * fn(other, acc) when swapped; `ptr` is unused for MR_EPI_RELU. */
+typedef struct mr_epi_step {
+  int32_t fn;
+  int32_t swapped;
+  int32_t mode;
+  int32_t reserved;
+  const float* ptr;
+  int64_t ld;
+} mr_epi_step;
+
+/* What happens to each result element after the contraction:
+ *   y = f32(f64(acc) * scale[col])          (mira/ops.py:618,633; skipped when scale == NULL)
+ *   y = steps[0..n_steps)(y)                (mira/ops.py:192-199)
+ *   out_f32[row*ldo+col] = y                (if out_f32)
+ *   out_i8[row*ldq+col]  = clip(rint(y / out_xs), +-127)
+ *                                           (mira/ops.py:602-603, the next q-op's input)
+ *   out_acc[row*ldacc+col] = acc            (int32 accumulator, if out_acc) */
+typedef struct mr_epilogue {
+  int32_t n_steps;
+  int32_t reserved0;
+  mr_epi_step steps[MR_MAX_EPI];
+  const double* scale;
+  float* out_f32;
+  int64_t ldo;
+  int8_t* out_i8;
+  int64_t ldq;
+  float out_xs;
+  int32_t reserved1;
+  int32_t* out_acc;
+  int64_t ldacc;
+} mr_epilogue;
+
+/* Geometry of an NHWC convolution (mira/ops.py:225-276 conv_params/_conv2d_infer).
+ * `c` real input channels, `c_pad` stored per pixel.  For groups == 1 convs
+ * c_pad % 16 == 0, or c_pad == 4 (stem layout: taps of one kernel row are
+ * packed 4 channels per tap, row_bytes = 16*ceil(kw/4) bytes per row). */
+typedef struct mr_conv_geom {
+  int32_t n, h, w, c, c_pad;
+  int32_t o, oh, ow;
+  int32_t kh, kw;
+  int32_t sh, sw;
+  int32_t ph, pw;
+  int32_t dh, dw;
+} mr_conv_geom;
+
+/* ---- library ----------------------------------------------------------- */
+int mr_abi_version(void);
+const char* mr_last_error(void);
+/* sizeof of the ABI structs, so bindings can check their mirrors. */
+int64_t mr_sizeof(const char* struct_name);
+/* Select the device and read its properties (CU count). */
+int mr_init(int device);
+
+/* ---- K1: activation quantize ------------------------------------------ */
+
+/* Replaces mira/ops.py:602-603 quantize_activation on a row-major matrix:
+ *   q[r*ldq + c] = clip(rint(x[r*ldx + c] / xs), -127, 127) for c < cols,
+ *   q[r*ldq + c] = 0 for cols <= c < ldq.
+ * Division is IEEE single precision, rint rounds half to even. */
+int mr_quantize_rows(const float* x, int64_t rows, int64_t cols, int64_t ldx,
+                     int8_t* q, int64_t ldq, float xs, void* stream);
+
+/* Same arithmetic, NCHW f32 in, NHWC int8 out with c_pad channels per pixel
+ * (channels c..c_pad-1 are zero).  Graph inputs of qconv2d
+ * (mira/ops.py:630-634) enter the device this way. */
+int mr_quantize_nchw_nhwc(const float* x, int32_t n, int32_t c, int32_t h, int32_t w,
+                          int8_t* q, int32_t c_pad, float xs, void* stream);
+
+/* ---- K2/K3: int8 GEMM with fused dequant/epilogue/requant -------------- */
+
+/* Replaces mira/ops.py:616-620 _qmatmul_ref (after quantize_activation):
+ * acc[M,N] = a[M,K] (int8, row stride lda) x b[N,k_pad]^T (packed int8
+ * weights, zero for k >= K and n >= N, N rounded up to n_pad rows),
+ * exact int32, then the epilogue.  lda % 16 == 0, k_pad % 64 == 0,
+ * n_pad % 32 == 0. */
+int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int64_t n_pad,
+               int64_t M, int64_t N, int64_t K, const mr_epilogue* epi, void* stream);
+
+/* Replaces mira/ops.py:630-634 _qconv2d_ref (after quantize_activation):
+ * implicit-GEMM convolution of NHWC int8 x with packed weights
+ * b[n_pad][k_pad] whose k index is (kh, kw, c) with c fastest over c_pad
+ * (or the stem row layout when c_pad == 4).  Result rows are NHWC pixels
+ * (n, oh, ow), columns output channels. */
+int mr_qconv2d(const int8_t* x, const mr_conv_geom* g, const int8_t* b, int64_t k_pad,
+               int64_t n_pad, const mr_epilogue* epi, void* stream);
+
+/* ---- K4a: f32 depthwise conv ------------------------------------------ */
+
+/* Replaces mira/ops.py:265-276 _conv2d_ref for groups == C, one output per
+ * group: acc = 0; for i, j: acc = acc + x_tap*w[i][j] (separate f32
+ * multiply and add, taps in (i, j) order), then the epilogue (scale must be
+ * NULL).  x NHWC f32 [n,h,w,c], w f32 [kh][kw][c]. */
+int mr_dwconv2d_f32(const float* x, const mr_conv_geom* g, const float* w,
+                    const mr_epilogue* epi, void* stream);
+
+/* ---- adjuncts ---------------------------------------------------------- */
+
+/* mira/ops.py:293-296 maxpool2d with the -inf/constant pad of
+ * mira/ops.py:461-470 folded in: NHWC f32 [n,h,w,c] -> [n,oh,ow,c].
+ * Optional int8 copy (quantized with xs) into yq with c_pad channels. */
+int mr_maxpool2d_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c,
+                     int32_t size, int32_t stride, int32_t pad_top, int32_t pad_left,
+                     float pad_value, int32_t oh, int32_t ow, float* y,
+                     int8_t* yq, int32_t c_pad, float xs, void* stream);
+
+/* mira/ops.py:318-343 reduce_mean over H,W (NumPy order: pairwise f32 sum,
+ * then f32(f64(sum) / count)).  NHWC f32 [n,hw,c] -> [n,c]; optional int8. */
+int mr_mean_hw_f32(const float* x, int32_t n, int32_t hw, int32_t c, float* y,
+                   int8_t* yq, int32_t ldq, float xs, void* stream);
+
+/* mira/ops.py:461-470 pad with a constant on H and W of an NHWC tensor. */
+int mr_pad_hw_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c,
+                  int32_t top, int32_t bottom, int32_t left, int32_t right,
+                  float value, float* y, void* stream);
+
+/* Layout changes at segment boundaries: NCHW <-> NHWC, f32. */
+int mr_nchw_to_nhwc_f32(const float* x, int32_t n, int32_t c, int32_t h, int32_t w,
+                        float* y, void* stream);
+int mr_nhwc_to_nchw_f32(const float* x, int32_t n, int32_t c, int32_t h, int32_t w,
+                        float* y, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIRA_ROCM_H */

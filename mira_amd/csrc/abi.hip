@@ -1,0 +1,101 @@
+// Library-level entry points: version, errors, device set-up, and the host
+// side validation of epilogue descriptors shared by every fused kernel.
+#include <cstring>
+#include <string>
+
+#include "mr_common.hpp"
+
+namespace mr {
+
+static thread_local char g_error[1024] = "";
+static int g_cu_count = 0;
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+}
+
+int device_cu_count() { return g_cu_count > 0 ? g_cu_count : 256; }
+
+int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out) {
+  MR_REQUIRE(epi != nullptr, "epilogue descriptor is NULL");
+  MR_REQUIRE(epi->n_steps >= 0 && epi->n_steps <= MR_MAX_EPI, "epilogue has %d steps (max %d)",
+             epi->n_steps, MR_MAX_EPI);
+  if (need_scale) {
+    MR_REQUIRE(epi->scale != nullptr, "epilogue needs a per-column dequant scale");
+  } else {
+    MR_REQUIRE(epi->scale == nullptr, "this kernel has no int32 accumulator to dequantize");
+  }
+  MR_REQUIRE(epi->out_f32 || epi->out_i8 || epi->out_acc, "epilogue writes no output");
+  if (epi->out_f32) MR_REQUIRE(epi->ldo >= cols, "ldo %lld < cols %lld", (long long)epi->ldo, (long long)cols);
+  if (epi->out_i8) {
+    MR_REQUIRE(epi->ldq >= cols, "ldq %lld < cols %lld", (long long)epi->ldq, (long long)cols);
+    MR_REQUIRE(epi->out_xs > 0.0f, "requant scale must be positive, got %g", (double)epi->out_xs);
+  }
+  if (epi->out_acc) {
+    MR_REQUIRE(need_scale, "int32 accumulators exist only for int8 contractions");
+    MR_REQUIRE(epi->ldacc >= cols, "ldacc < cols");
+  }
+  std::memset(out, 0, sizeof(*out));
+  out->n_steps = epi->n_steps;
+  out->has_scale = epi->scale != nullptr;
+  for (int s = 0; s < epi->n_steps; ++s) {
+    const mr_epi_step& st = epi->steps[s];
+    MR_REQUIRE(st.fn >= MR_EPI_ADD && st.fn <= MR_EPI_RELU, "epilogue step %d: unknown fn %d", s, st.fn);
+    if (st.fn != MR_EPI_RELU) {
+      MR_REQUIRE(st.ptr != nullptr, "epilogue step %d: operand pointer is NULL", s);
+      MR_REQUIRE(st.mode >= MR_BC_SCALAR && st.mode <= MR_BC_FULL, "epilogue step %d: bad mode %d", s,
+                 st.mode);
+      if (st.mode == MR_BC_FULL) MR_REQUIRE(st.ld >= cols, "epilogue step %d: ld < cols", s);
+    }
+    out->steps[s].fn = st.fn;
+    out->steps[s].swapped = st.swapped;
+    out->steps[s].mode = st.mode;
+    out->steps[s].ptr = st.ptr;
+    out->steps[s].ld = st.ld;
+  }
+  out->scale = epi->scale;
+  out->out_f32 = epi->out_f32;
+  out->ldo = epi->ldo;
+  out->out_i8 = epi->out_i8;
+  out->ldq = epi->ldq;
+  out->out_xs = epi->out_xs;
+  out->out_acc = epi->out_acc;
+  out->ldacc = epi->ldacc;
+  return MR_OK;
+}
+
+}  // namespace mr
+
+extern "C" {
+
+int mr_abi_version(void) { return MR_ABI_VERSION; }
+
+const char* mr_last_error(void) { return mr::g_error; }
+
+int64_t mr_sizeof(const char* name) {
+  if (!name) return -1;
+  if (!std::strcmp(name, "mr_epi_step")) return sizeof(mr_epi_step);
+  if (!std::strcmp(name, "mr_epilogue")) return sizeof(mr_epilogue);
+  if (!std::strcmp(name, "mr_conv_geom")) return sizeof(mr_conv_geom);
+  return -1;
+}
+
+int mr_init(int device) {
+  int count = 0;
+  MR_HIP_CHECK(hipGetDeviceCount(&count));
+  MR_REQUIRE(device >= 0 && device < count, "device %d out of range (%d devices)", device, count);
+  MR_HIP_CHECK(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  MR_HIP_CHECK(hipGetDeviceProperties(&prop, device));
+  mr::g_cu_count = prop.multiProcessorCount;
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    mr::set_error("device %d is %s; this library is built for gfx950 only", device, prop.gcnArchName);
+    return MR_EUNSUPPORTED;
+  }
+  return MR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,309 @@
+// Bandwidth-bound f32 kernels around the int8 contractions:
+//   K4a depthwise conv (mira/ops.py:265-276 with groups == C),
+//   maxpool with the pad folded in (mira/ops.py:293-296, 461-470),
+//   reduce_mean over H,W in NumPy's summation order (mira/ops.py:318-343),
+//   constant pad, and NCHW <-> NHWC layout changes at segment boundaries.
+// All tensors are NHWC inside a segment; threads run along channels so
+// every global access coalesces.
+#include "mr_common.hpp"
+
+namespace mr {
+
+static int grid_1d(int64_t total, int block) {
+  int64_t g = (total + block - 1) / block;
+  const int64_t cap = int64_t(device_cu_count()) * 64;
+  if (g > cap) g = cap;
+  if (g < 1) g = 1;
+  return static_cast<int>(g);
+}
+
+// ---------------------------------------------------------------- depthwise conv
+
+// One thread per output element (pixel, channel).  acc starts at +0 and
+// adds each tap's product in (i, j) order with separate roundings, exactly
+// like `acc += einsum(...)` per tap in the reference; taps that fall into
+// the zero padding still add 0 * w.
+__global__ void __launch_bounds__(256) dwconv_kernel(const float* __restrict__ x, mr_conv_geom G,
+                                                     const float* __restrict__ w, const EpiDev e) {
+  const int64_t total = int64_t(G.n) * G.oh * G.ow * G.c;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int c = static_cast<int>(t % G.c);
+    const int64_t pix = t / G.c;
+    const int ow = static_cast<int>(pix % G.ow);
+    const int64_t r = pix / G.ow;
+    const int oh = static_cast<int>(r % G.oh);
+    const int64_t img = r / G.oh;
+    float acc = 0.0f;
+    for (int i = 0; i < G.kh; ++i) {
+      const int ih = oh * G.sh - G.ph + i * G.dh;
+      const bool row_ok = unsigned(ih) < unsigned(G.h);
+      for (int j = 0; j < G.kw; ++j) {
+        const int iw = ow * G.sw - G.pw + j * G.dw;
+        const float xv =
+            (row_ok && unsigned(iw) < unsigned(G.w)) ? x[((img * G.h + ih) * G.w + iw) * G.c + c] : 0.0f;
+        acc = __fadd_rn(acc, __fmul_rn(xv, w[(i * G.kw + j) * G.c + c]));
+      }
+    }
+    const float y = epi_steps(e, acc, pix, c);
+    epi_store(e, y, pix, c);
+  }
+}
+
+// ---------------------------------------------------------------- maxpool
+
+__global__ void __launch_bounds__(256) maxpool_kernel(const float* __restrict__ x, int n, int h, int w, int c,
+                                                      int size, int stride, int pt, int pl, float pad_value, int oh,
+                                                      int ow, float* __restrict__ y, int8_t* __restrict__ yq,
+                                                      int c_pad, float xs) {
+  const int64_t total = int64_t(n) * oh * ow * c;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int ch = static_cast<int>(t % c);
+    const int64_t pix = t / c;
+    const int ox = static_cast<int>(pix % ow);
+    const int64_t r = pix / ow;
+    const int oy = static_cast<int>(r % oh);
+    const int64_t img = r / oh;
+    float m = 0.0f;
+    for (int i = 0; i < size; ++i) {
+      const int ih = oy * stride - pt + i;
+      for (int j = 0; j < size; ++j) {
+        const int iw = ox * stride - pl + j;
+        const float v = (unsigned(ih) < unsigned(h) && unsigned(iw) < unsigned(w))
+                            ? x[((img * h + ih) * w + iw) * c + ch]
+                            : pad_value;
+        m = (i == 0 && j == 0) ? v : np_maximum(m, v);
+      }
+    }
+    if (y) y[pix * c + ch] = m;
+    if (yq) yq[pix * c_pad + ch] = quantize_one(m, xs);
+  }
+}
+
+// ---------------------------------------------------------------- mean over H*W
+
+// NumPy's float32 pairwise summation (numpy/_core/src/umath/loops_utils.h.src,
+// @TYPE@_pairwise_sum, PW_BLOCKSIZE 128) over n values spaced `stride` apart.
+__device__ float pairwise_block(const float* a, int64_t n, int64_t stride) {
+  if (n < 8) {
+    float res = -0.0f;
+    for (int64_t i = 0; i < n; ++i) res = __fadd_rn(res, a[i * stride]);
+    return res;
+  }
+  float r[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = a[j * stride];
+  int64_t i = 8;
+  for (; i < n - (n % 8); i += 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = __fadd_rn(r[j], a[(i + j) * stride]);
+  }
+  float res = __fadd_rn(__fadd_rn(__fadd_rn(r[0], r[1]), __fadd_rn(r[2], r[3])),
+                        __fadd_rn(__fadd_rn(r[4], r[5]), __fadd_rn(r[6], r[7])));
+  for (; i < n; ++i) res = __fadd_rn(res, a[i * stride]);
+  return res;
+}
+
+// The recursion (split at n/2 rounded down to a multiple of 8, sum the two
+// halves) run with an explicit stack: depth <= 40 covers any int64 count.
+__device__ float pairwise_sum(const float* a, int64_t n, int64_t stride) {
+  if (n <= 128) return pairwise_block(a, n, stride);
+  int64_t off[40], cnt[40];
+  float left[40];
+  int state[40];
+  int sp = 0;
+  off[0] = 0;
+  cnt[0] = n;
+  state[0] = 0;
+  float ret = 0.0f;
+  while (true) {
+    if (cnt[sp] <= 128) {
+      ret = pairwise_block(a + off[sp] * stride, cnt[sp], stride);
+      --sp;
+      // unwind: finished children return into their parents
+      while (sp >= 0) {
+        if (state[sp] == 0) {
+          left[sp] = ret;
+          state[sp] = 1;
+          int64_t n2 = cnt[sp] / 2;
+          n2 -= n2 % 8;
+          off[sp + 1] = off[sp] + n2;
+          cnt[sp + 1] = cnt[sp] - n2;
+          state[sp + 1] = 0;
+          ++sp;
+          break;
+        }
+        ret = __fadd_rn(left[sp], ret);
+        --sp;
+      }
+      if (sp < 0) return ret;
+      continue;
+    }
+    int64_t n2 = cnt[sp] / 2;
+    n2 -= n2 % 8;
+    state[sp] = 0;
+    off[sp + 1] = off[sp];
+    cnt[sp + 1] = n2;
+    state[sp + 1] = 0;
+    ++sp;
+  }
+}
+
+// y[img, ch] = f32(f64(pairwise_sum) / f64(hw)): NumPy's mean divides the f32
+// sum by the intp count in a double-precision loop and casts back.
+__global__ void __launch_bounds__(256) mean_hw_kernel(const float* __restrict__ x, int n, int hw, int c,
+                                                      float* __restrict__ y, int8_t* __restrict__ yq, int ldq,
+                                                      float xs) {
+  const int64_t total = int64_t(n) * c;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int ch = static_cast<int>(t % c);
+    const int64_t img = t / c;
+    const float s = pairwise_sum(x + img * hw * c + ch, hw, c);
+    const float m = static_cast<float>(__ddiv_rn(static_cast<double>(s), static_cast<double>(hw)));
+    if (y) y[t] = m;
+    if (yq) yq[img * ldq + ch] = quantize_one(m, xs);
+  }
+}
+
+// ---------------------------------------------------------------- pad / layout
+
+__global__ void __launch_bounds__(256) pad_kernel(const float* __restrict__ x, int n, int h, int w, int c, int top,
+                                                  int left, int oh, int ow, float value, float* __restrict__ y) {
+  const int64_t total = int64_t(n) * oh * ow * c;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int ch = static_cast<int>(t % c);
+    const int64_t pix = t / c;
+    const int ox = static_cast<int>(pix % ow);
+    const int64_t r = pix / ow;
+    const int oy = static_cast<int>(r % oh);
+    const int64_t img = r / oh;
+    const int ih = oy - top, iw = ox - left;
+    y[t] = (unsigned(ih) < unsigned(h) && unsigned(iw) < unsigned(w)) ? x[((img * h + ih) * w + iw) * c + ch]
+                                                                       : value;
+  }
+}
+
+// Tiled transpose of a [rows, cols] matrix per image (32x32 tiles in LDS):
+// NCHW -> NHWC is rows = C, cols = H*W; NHWC -> NCHW swaps them.
+__global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict__ x, int rows, int cols,
+                                                        float* __restrict__ y) {
+  __shared__ float tile[32][33];
+  const int64_t img = blockIdx.z;
+  const float* xi = x + img * int64_t(rows) * cols;
+  float* yi = y + img * int64_t(rows) * cols;
+  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  for (int i = threadIdx.y; i < 32; i += 8) {
+    const int r = r0 + i, cc = c0 + threadIdx.x;
+    if (r < rows && cc < cols) tile[i][threadIdx.x] = xi[int64_t(r) * cols + cc];
+  }
+  __syncthreads();
+  for (int i = threadIdx.y; i < 32; i += 8) {
+    const int cc = c0 + i, r = r0 + threadIdx.x;
+    if (r < rows && cc < cols) yi[int64_t(cc) * rows + r] = tile[threadIdx.x][i];
+  }
+}
+
+static int transpose(const float* x, int n, int rows, int cols, float* y, hipStream_t s) {
+  dim3 grid((cols + 31) / 32, (rows + 31) / 32, n);
+  hipLaunchKernelGGL(transpose_kernel, grid, dim3(32, 8), 0, s, x, rows, cols, y);
+  MR_LAUNCH_CHECK("transpose");
+  return MR_OK;
+}
+
+}  // namespace mr
+
+extern "C" {
+
+int mr_dwconv2d_f32(const float* x, const mr_conv_geom* cg, const float* w, const mr_epilogue* epi, void* stream) {
+  MR_REQUIRE(x && cg && w, "mr_dwconv2d_f32: NULL argument");
+  const mr_conv_geom& G = *cg;
+  MR_REQUIRE(G.n >= 0 && G.h > 0 && G.w > 0 && G.c > 0, "mr_dwconv2d_f32: bad shape");
+  MR_REQUIRE(G.o == G.c && G.c_pad == G.c, "mr_dwconv2d_f32: depthwise needs o == c == c_pad");
+  MR_REQUIRE(G.kh > 0 && G.kw > 0 && G.sh > 0 && G.sw > 0 && G.dh > 0 && G.dw > 0 && G.ph >= 0 && G.pw >= 0,
+             "mr_dwconv2d_f32: bad kernel/stride/padding/dilation");
+  const int32_t oh = (G.h + 2 * G.ph - G.dh * (G.kh - 1) - 1) / G.sh + 1;
+  const int32_t ow = (G.w + 2 * G.pw - G.dw * (G.kw - 1) - 1) / G.sw + 1;
+  MR_REQUIRE(oh == G.oh && ow == G.ow && oh > 0 && ow > 0, "mr_dwconv2d_f32: output size mismatch");
+  mr::EpiDev e;
+  const int rc = mr::make_epi(epi, G.c, false, &e);
+  if (rc != MR_OK) return rc;
+  MR_REQUIRE(!epi->out_acc, "mr_dwconv2d_f32: no int32 accumulators");
+  const int64_t total = int64_t(G.n) * oh * ow * G.c;
+  if (total == 0) return MR_OK;
+  hipLaunchKernelGGL(mr::dwconv_kernel, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, G, w, e);
+  MR_LAUNCH_CHECK("dwconv2d");
+  return MR_OK;
+}
+
+int mr_maxpool2d_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, int32_t size, int32_t stride,
+                     int32_t pad_top, int32_t pad_left, float pad_value, int32_t oh, int32_t ow, float* y,
+                     int8_t* yq, int32_t c_pad, float xs, void* stream) {
+  MR_REQUIRE(x && (y || yq), "mr_maxpool2d_f32: NULL argument");
+  MR_REQUIRE(n >= 0 && h > 0 && w > 0 && c > 0 && size > 0 && stride > 0 && pad_top >= 0 && pad_left >= 0,
+             "mr_maxpool2d_f32: bad shape");
+  MR_REQUIRE(oh > 0 && ow > 0, "mr_maxpool2d_f32: empty output");
+  // every window must start inside the padded extent the host described
+  MR_REQUIRE((oh - 1) * stride - pad_top < h && (ow - 1) * stride - pad_left < w,
+             "mr_maxpool2d_f32: output %dx%d too large for input %dx%d", oh, ow, h, w);
+  if (yq) {
+    MR_REQUIRE(c_pad >= c, "mr_maxpool2d_f32: c_pad < c");
+    MR_REQUIRE(xs > 0.0f, "mr_maxpool2d_f32: requant scale must be positive");
+  }
+  const int64_t total = int64_t(n) * oh * ow * c;
+  if (total == 0) return MR_OK;
+  hipLaunchKernelGGL(mr::maxpool_kernel, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, n, h, w, c, size, stride, pad_top, pad_left, pad_value, oh,
+                     ow, y, yq, c_pad, xs);
+  MR_LAUNCH_CHECK("maxpool2d");
+  return MR_OK;
+}
+
+int mr_mean_hw_f32(const float* x, int32_t n, int32_t hw, int32_t c, float* y, int8_t* yq, int32_t ldq, float xs,
+                   void* stream) {
+  MR_REQUIRE(x && (y || yq), "mr_mean_hw_f32: NULL argument");
+  MR_REQUIRE(n >= 0 && hw > 0 && c > 0, "mr_mean_hw_f32: bad shape");
+  if (yq) {
+    MR_REQUIRE(ldq >= c, "mr_mean_hw_f32: ldq < c");
+    MR_REQUIRE(xs > 0.0f, "mr_mean_hw_f32: requant scale must be positive");
+  }
+  const int64_t total = int64_t(n) * c;
+  if (total == 0) return MR_OK;
+  hipLaunchKernelGGL(mr::mean_hw_kernel, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, n, hw, c, y, yq, ldq, xs);
+  MR_LAUNCH_CHECK("mean_hw");
+  return MR_OK;
+}
+
+int mr_pad_hw_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, int32_t top, int32_t bottom,
+                  int32_t left, int32_t right, float value, float* y, void* stream) {
+  MR_REQUIRE(x && y, "mr_pad_hw_f32: NULL argument");
+  MR_REQUIRE(n >= 0 && h > 0 && w > 0 && c > 0 && top >= 0 && bottom >= 0 && left >= 0 && right >= 0,
+             "mr_pad_hw_f32: bad shape");
+  const int oh = h + top + bottom, ow = w + left + right;
+  const int64_t total = int64_t(n) * oh * ow * c;
+  if (total == 0) return MR_OK;
+  hipLaunchKernelGGL(mr::pad_kernel, dim3(mr::grid_1d(total, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     x, n, h, w, c, top, left, oh, ow, value, y);
+  MR_LAUNCH_CHECK("pad_hw");
+  return MR_OK;
+}
+
+int mr_nchw_to_nhwc_f32(const float* x, int32_t n, int32_t c, int32_t h, int32_t w, float* y, void* stream) {
+  MR_REQUIRE(x && y && x != y, "mr_nchw_to_nhwc_f32: bad pointers");
+  MR_REQUIRE(n >= 0 && c > 0 && h > 0 && w > 0 && n < 65536, "mr_nchw_to_nhwc_f32: bad shape");
+  if (n == 0) return MR_OK;
+  return mr::transpose(x, n, c, h * w, y, static_cast<hipStream_t>(stream));
+}
+
+int mr_nhwc_to_nchw_f32(const float* x, int32_t n, int32_t c, int32_t h, int32_t w, float* y, void* stream) {
+  MR_REQUIRE(x && y && x != y, "mr_nhwc_to_nchw_f32: bad pointers");
+  MR_REQUIRE(n >= 0 && c > 0 && h > 0 && w > 0 && n < 65536, "mr_nhwc_to_nchw_f32: bad shape");
+  if (n == 0) return MR_OK;
+  return mr::transpose(x, n, h * w, c, y, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

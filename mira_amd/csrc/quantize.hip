@@ -1,0 +1,100 @@
+// K1: the activation quantizer of mira/ops.py:602-603 (f32 -> int8),
+// bandwidth-bound: 4 bytes read and 1 byte written per element.
+#include "mr_common.hpp"
+
+namespace mr {
+
+// Row-major [rows, cols] f32 (row stride ldx) -> [rows, ldq] int8, zero pad.
+// One thread writes 4 consecutive output bytes (one dword store).
+__global__ void __launch_bounds__(256) quantize_rows_kernel(const float* __restrict__ x, int64_t rows,
+                                                            int64_t cols, int64_t ldx, int8_t* __restrict__ q,
+                                                            int64_t ldq, float xs) {
+  const int64_t groups = ldq >> 2;
+  const int64_t total = rows * groups;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = t / groups;
+    const int64_t c0 = (t - r * groups) << 2;
+    const float* xr = x + r * ldx;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t c = c0 + j;
+      const int8_t v = c < cols ? quantize_one(xr[c], xs) : int8_t(0);
+      packed |= uint32_t(uint8_t(v)) << (8 * j);
+    }
+    *reinterpret_cast<uint32_t*>(q + r * ldq + c0) = packed;
+  }
+}
+
+// NCHW f32 -> NHWC int8 with c_pad channels.  Thread t handles one pixel and
+// one group of 4 channels; pixels are fastest so the f32 reads coalesce and
+// for c_pad == 4 the dword stores do too.
+__global__ void __launch_bounds__(256) quantize_nchw_nhwc_kernel(const float* __restrict__ x, int n, int c,
+                                                                 int hw, int8_t* __restrict__ q, int c_pad,
+                                                                 float xs) {
+  const int groups = c_pad >> 2;
+  const int64_t total = (int64_t)n * groups * hw;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t p = t % hw;
+    const int64_t rest = t / hw;
+    const int g = static_cast<int>(rest % groups);
+    const int64_t img = rest / groups;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ch = g * 4 + j;
+      const int8_t v = ch < c ? quantize_one(x[(img * c + ch) * hw + p], xs) : int8_t(0);
+      packed |= uint32_t(uint8_t(v)) << (8 * j);
+    }
+    *reinterpret_cast<uint32_t*>(q + (img * hw + p) * c_pad + g * 4) = packed;
+  }
+}
+
+static int grid_for(int64_t total, int block) {
+  int64_t g = (total + block - 1) / block;
+  const int64_t cap = int64_t(device_cu_count()) * 64;
+  if (g > cap) g = cap;
+  if (g < 1) g = 1;
+  return static_cast<int>(g);
+}
+
+}  // namespace mr
+
+extern "C" {
+
+int mr_quantize_rows(const float* x, int64_t rows, int64_t cols, int64_t ldx, int8_t* q, int64_t ldq, float xs,
+                     void* stream) {
+  MR_REQUIRE(x && q, "mr_quantize_rows: NULL pointer");
+  MR_REQUIRE(rows >= 0 && cols >= 0, "mr_quantize_rows: negative size");
+  MR_REQUIRE(ldx >= cols, "mr_quantize_rows: ldx %lld < cols %lld", (long long)ldx, (long long)cols);
+  MR_REQUIRE(ldq >= cols && ldq % 4 == 0, "mr_quantize_rows: ldq %lld must be >= cols and a multiple of 4",
+             (long long)ldq);
+  MR_REQUIRE(reinterpret_cast<uintptr_t>(q) % 4 == 0, "mr_quantize_rows: q must be 4-byte aligned");
+  MR_REQUIRE(xs > 0.0f, "mr_quantize_rows: scale must be positive");
+  if (rows == 0 || ldq == 0) return MR_OK;
+  const int64_t total = rows * (ldq / 4);
+  hipLaunchKernelGGL(mr::quantize_rows_kernel, dim3(mr::grid_for(total, 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, rows, cols, ldx, q, ldq, xs);
+  MR_LAUNCH_CHECK("quantize_rows");
+  return MR_OK;
+}
+
+int mr_quantize_nchw_nhwc(const float* x, int32_t n, int32_t c, int32_t h, int32_t w, int8_t* q, int32_t c_pad,
+                          float xs, void* stream) {
+  MR_REQUIRE(x && q, "mr_quantize_nchw_nhwc: NULL pointer");
+  MR_REQUIRE(n >= 0 && c > 0 && h > 0 && w > 0, "mr_quantize_nchw_nhwc: bad shape");
+  MR_REQUIRE(c_pad >= c && c_pad % 4 == 0, "mr_quantize_nchw_nhwc: c_pad %d must be >= c %d and a multiple of 4",
+             c_pad, c);
+  MR_REQUIRE(reinterpret_cast<uintptr_t>(q) % 4 == 0, "mr_quantize_nchw_nhwc: q must be 4-byte aligned");
+  MR_REQUIRE(xs > 0.0f, "mr_quantize_nchw_nhwc: scale must be positive");
+  if (n == 0) return MR_OK;
+  const int64_t total = int64_t(n) * (c_pad / 4) * h * w;
+  hipLaunchKernelGGL(mr::quantize_nchw_nhwc_kernel, dim3(mr::grid_for(total, 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, n, c, h * w, q, c_pad, xs);
+  MR_LAUNCH_CHECK("quantize_nchw_nhwc");
+  return MR_OK;
+}
+
+}  // extern "C"
