@@ -1,0 +1,170 @@
+"""Benchmark: W8A8 ResNet-18 inference on one MI355X through the rocm target.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 256] [--no-cpu-baseline]
+
+A step is one inference of the whole batch (all 20 int8 implicit-GEMM convs,
+pooling, the fc layer) with the input already resident in HBM.  Prints ONE
+JSON line on stdout; progress goes to stderr.
+
+value      = int8 TOPS over the whole network: 2 * (conv + fc MACs) / step time
+roofline   = the qconv2d kernels (the dominant kernel class): their algorithmic
+             ops / their summed launch durations (HIP events around each launch
+             on the stream they run on), against the 5.0 POPS int8 dense peak
+cpu_baseline = the NumPy golden model (oracle/golden.py, the reference cpu
+             target's algorithms) on a 2-image sample with the same attrs,
+             timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+INT8_PEAK_TOPS = 5000.0          # MI355X dense int8 MFMA peak (5.0 POPS)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build(batch: int, seed: int = 0, peaks=None):
+    from mira_amd import models, passes
+    from mira_amd.quantize import calibration_peaks, quantize_w8a8
+    g = models.resnet18(batch=batch, seed=seed)
+    passes.optimize(g)
+    if peaks is None:
+        twin = models.resnet18(batch=2, seed=seed)
+        passes.optimize(twin)
+        peaks = calibration_peaks(twin, [{"x": models.image_batch((2, 3, 224, 224), s)} for s in (11, 12)])
+    quantize_w8a8(g, peaks=peaks)
+    return g, peaks
+
+
+def cpu_baseline(peaks, macs_per_image: int) -> dict:
+    """The golden model on a bounded 2-image sample: 1 warm-up + 3 timed runs, median."""
+    from oracle import golden as G
+    from mira_amd import models
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:
+        threads = os.cpu_count() or 1
+    g, _ = build(2, peaks=peaks)
+    x = models.image_batch((2, 3, 224, 224), 7)
+    G.run_graph(g, {"x": x})
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        G.run_graph(g, {"x": x})
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    return {"value": round(2 * macs_per_image * 2 / t / 1e12, 6), "unit": "TOPS", "cores": int(threads),
+            "kind": "port", "ms_per_image": round(t / 2 * 1e3, 2),
+            "sample": "2 images of the same W8A8 ResNet-18 (same attrs), NumPy golden model "
+                      "(int64 matmul, per-tap f32 einsum convs), median of 3 after 1 warm-up"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=256)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the batch would shard by "
+              "data parallelism; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+    from mira_amd import models
+    from mira_amd.compiler import compile_graph
+    from mira_amd.target import RocmTarget
+
+    t0 = time.perf_counter()
+    g, peaks = build(args.batch)
+    macs = models.conv_macs(g)
+    conv_macs = sum(int(np.prod(op.result.type.shape)) * int(np.prod(op.attrs["q"].shape[1:]))
+                    for op in g.ops if op.kind == "qconv2d")
+    runner = compile_graph(g, RocmTarget())
+    (seg,) = runner.segments
+    exe = seg.executable
+    log(f"compiled in {time.perf_counter() - t0:.1f}s: {exe.report()}")
+    x = models.image_batch((args.batch, 3, 224, 224), 7)
+    exe.upload({g.inputs[0]: x})
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        exe.launch()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        exe.launch()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / args.steps
+    log(f"{args.steps} steps: {ms:.3f} ms/step")
+
+    # per-launch durations (events around every launch, same stream), 3 instrumented passes
+    handle = stream.cuda_stream
+    per_kind: dict[str, float] = {}
+    reps = 3
+    for _ in range(reps):
+        evs = []
+        for name, fn in exe.launches:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn(handle)
+            b.record(stream)
+            evs.append((name, a, b))
+        torch.cuda.synchronize()
+        for name, a, b in evs:
+            per_kind[name] = per_kind.get(name, 0.0) + a.elapsed_time(b) / reps
+    conv_ms = per_kind.get("qconv2d", 0.0)
+    n_conv = exe.kernel_counts.get("qconv2d", 0)
+    conv_tops = 2 * conv_macs / (conv_ms * 1e-3) / 1e12
+    log("per-kind ms/step: " + ", ".join(f"{k} {v:.3f}" for k, v in sorted(per_kind.items(), key=lambda kv: -kv[1])))
+
+    tops = 2 * macs / (ms * 1e-3) / 1e12
+    out = {
+        "metric": "int8 TOPS (% of MFMA peak) + ms/inference, W8A8 ResNet-18 shape, 1 MI355X",
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "ms_per_inference": round(ms / args.batch, 5),
+        "pct_of_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "resnet18_w8a8", "batch": args.batch, "input": f"f32[{args.batch},3,224,224] U(0,1)",
+                   "weights": "random Kaiming-normal, BN folded", "int8_macs_per_image": macs // args.batch,
+                   "calibration": "2 batches of 2 images U(0,1)"},
+        "roofline": {"bound": "mfma", "kernel": "qconv2d (implicit GEMM, all 20 convs)",
+                     "achieved": round(conv_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                     "frac": round(conv_tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                     "launches_per_step": n_conv, "ms_per_step": round(conv_ms, 4)},
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU golden model on a 2-image sample ...")
+        out["cpu_baseline"] = cpu_baseline(peaks, macs // args.batch)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

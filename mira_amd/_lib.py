@@ -79,6 +79,13 @@ def load(path: Optional[Path] = None) -> C.CDLL:
     if not p.exists():
         raise RocmError(f"{p} is not built: run `python -m mira_amd.build` (the rocm target has no other "
                         f"compute path)")
+    # PyTorch-ROCm ships its own libamdhip64.so (soname libamdhip64.so.7).  Loading torch
+    # first makes this library bind to that same HIP runtime, so torch's device pointers
+    # and streams are valid here; loading it first would put two runtimes in the process.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = C.CDLL(str(p))
     for name, (args, res) in _SIGS.items():
         fn = getattr(lib, name)

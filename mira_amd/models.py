@@ -1,0 +1,237 @@
+"""Float graph builders for the W8A8 benchmark configurations.
+
+Each builder returns an unoptimized float32 IR graph with constant weights,
+laid out as MIRA's front ends produce it, so the reference pass pipeline
+(optimize -> fuse_epilogues -> quantize_w8a8) gives the same op and epilogue
+structure:
+
+* dense layers are `matmul` + `add(bias)` (+ activation), as in
+  examples/mlp.mira (`x @ w + b`);
+* convolutions with folded batch norm are `conv2d` + `add(bias [O,1,1])`,
+  ReLU is `relu`, ReLU6 is `maximum(0)` then `minimum(6)` with 0-d constants
+  (how mira/frontends/onnx_import.py:477-485 imports Clip);
+* max pooling with padding is `pad(-inf)` + `maxpool2d`
+  (mira/frontends/onnx_import.py:391-395), global average pooling is
+  `reduce_mean(axes=(2, 3), keepdims)` (:416-420), flatten is `reshape`.
+
+Weights are drawn from one seeded generator in a fixed order; the same
+(seed, architecture) at any batch size gives the same weights, so a
+small-batch twin can be used for calibration.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .ir import Graph
+from .ops import conv_out
+
+
+def _normal(rng, shape, std):
+    return (rng.standard_normal(shape) * std).astype(np.float32)
+
+
+def mira_random_weight(rng, shape) -> np.ndarray:
+    """The distribution of mira/elaborate.py:1114-1123 (rank 1: 1 + 0.1 N; else N / sqrt(fan_in))."""
+    if len(shape) == 1:
+        return (1.0 + 0.1 * rng.standard_normal(shape)).astype(np.float32)
+    fan_in = int(np.prod(shape[1:])) if len(shape) == 4 else shape[-2]
+    return (rng.standard_normal(shape) / np.sqrt(fan_in)).astype(np.float32)
+
+
+# ---------------------------------------------------------------- MLPs
+
+def mlp_dense(batch: int = 256, k: int = 64, n: int = 10, seed: int = 0) -> Graph:
+    """x f32[batch, k] @ w f32[k, n] ~ N(0, 0.1) + b zeros (a zero bias is removed by simplify)."""
+    rng = np.random.default_rng(seed)
+    g = Graph("mlp_dense", [], [], [])
+    x = g.input("x", (batch, k))
+    w = g.const(_normal(rng, (k, n), 0.1))
+    b = g.const(np.zeros(n, np.float32))
+    g.outputs = [g.add("add", [g.add("matmul", [x, w]), b])]
+    return g
+
+
+def mlp_mira(batch: int = 64, seed: int = 0) -> Graph:
+    """examples/mlp.mira: 784 -> 512 -> 256 -> 10 with ReLU, then softmax(axis=1)."""
+    rng = np.random.default_rng(seed)
+    g = Graph("mlp", [], [], [])
+    h = g.input("x", (batch, 784))
+    dims = [(784, 512), (512, 256), (256, 10)]
+    params = [(mira_random_weight(rng, d), mira_random_weight(rng, (d[1],))) for d in dims]
+    for i, (w, b) in enumerate(params):
+        h = g.add("add", [g.add("matmul", [h, g.const(w)]), g.const(b)])
+        if i < 2:
+            h = g.add("relu", [h])
+    g.outputs = [g.add("softmax", [h], {"axis": 1})]
+    return g
+
+
+def mlp_50m(batch: int = 4096, seed: int = 0) -> Graph:
+    """4 dense layers 4096->4096 (x3) and 4096->1000, ReLU between, W ~ N(0, 1/sqrt(4096)),
+    biases ~ N(0, 0.1): 54.4 M parameters."""
+    rng = np.random.default_rng(seed)
+    g = Graph("mlp50m", [], [], [])
+    h = g.input("x", (batch, 4096))
+    dims = [(4096, 4096)] * 3 + [(4096, 1000)]
+    for i, (k, n) in enumerate(dims):
+        w = g.const(_normal(rng, (k, n), 1.0 / np.sqrt(4096)))
+        b = g.const(_normal(rng, (n,), 0.1))
+        h = g.add("add", [g.add("matmul", [h, w]), b])
+        if i < len(dims) - 1:
+            h = g.add("relu", [h])
+    g.outputs = [h]
+    return g
+
+
+# ---------------------------------------------------------------- CNNs
+
+class _ConvNet:
+    """Helper that draws folded conv+BN parameters in a fixed order."""
+
+    def __init__(self, g: Graph, seed: int):
+        self.g = g
+        self.rng = np.random.default_rng(seed)
+
+    def conv(self, x, o: int, k: int, stride: int = 1, pad: int = 0, groups: int = 1, bn: bool = True):
+        """conv2d + folded BatchNorm: Kaiming-normal (fan_out) weights scaled by gamma/sqrt(var+eps),
+        bias beta - mean*gamma/sqrt(var+eps), with random BN statistics so the bias is not zero."""
+        rng = self.rng
+        c = x.type.shape[1]
+        w = _normal(rng, (o, c // groups, k, k), np.sqrt(2.0 / (o * k * k / groups)))
+        attrs = {"stride": (stride, stride), "padding": (pad, pad)}
+        if groups != 1:
+            attrs["groups"] = groups
+        if bn:
+            gamma = rng.uniform(0.5, 1.5, o)
+            beta = rng.normal(0.0, 0.1, o)
+            mean = rng.normal(0.0, 0.1, o)
+            var = rng.uniform(0.5, 1.5, o)
+            s = gamma / np.sqrt(var + 1e-5)
+            w = (w * s.reshape(-1, 1, 1, 1)).astype(np.float32)
+            bias = (beta - mean * s).astype(np.float32)
+        else:
+            bias = np.zeros(o, np.float32)
+        y = self.g.add("conv2d", [x, self.g.const(w)], attrs)
+        return self.g.add("add", [y, self.g.const(bias.reshape(o, 1, 1))])
+
+    def relu(self, x):
+        return self.g.add("relu", [x])
+
+    def relu6(self, x):
+        g = self.g
+        y = g.add("maximum", [x, g.const(np.array(0.0, np.float32))])
+        return g.add("minimum", [y, g.const(np.array(6.0, np.float32))])
+
+    def head(self, x, classes: int):
+        """Global average pool, flatten, fully connected."""
+        g = self.g
+        n, c = x.type.shape[:2]
+        pooled = g.add("reduce_mean", [x], {"axes": (2, 3), "keepdims": True})
+        flat = g.add("reshape", [pooled], {"shape": (n, c)})
+        w = _normal(self.rng, (c, classes), 1.0 / np.sqrt(c))
+        b = _normal(self.rng, (classes,), 0.01)
+        return g.add("add", [g.add("matmul", [flat, g.const(w)]), g.const(b)])
+
+
+def resnet18(batch: int = 256, seed: int = 0, classes: int = 1000) -> Graph:
+    """torchvision ResNet-18 with BN folded: 7x7/2 stem, 3x3/2 max pool, 4 stages of two basic
+    blocks (64, 128, 256, 512 channels; stride-2 1x1 downsample convs), GAP, fc."""
+    g = Graph("resnet18", [], [], [])
+    net = _ConvNet(g, seed)
+    x = g.input("x", (batch, 3, 224, 224))
+    h = net.relu(net.conv(x, 64, 7, 2, 3))
+    h = g.add("pad", [h], {"pads": ((0, 0), (0, 0), (1, 1), (1, 1)), "value": -np.inf})
+    h = g.add("maxpool2d", [h], {"size": 3, "stride": 2})
+    c_in = 64
+    for stage, c in enumerate((64, 128, 256, 512)):
+        for blk in range(2):
+            stride = 2 if stage > 0 and blk == 0 else 1
+            y = net.relu(net.conv(h, c, 3, stride, 1))
+            y = net.conv(y, c, 3, 1, 1)
+            shortcut = net.conv(h, c, 1, stride, 0) if (stride != 1 or c_in != c) else h
+            h = net.relu(g.add("add", [y, shortcut]))
+            c_in = c
+    g.outputs = [net.head(h, classes)]
+    return g
+
+
+def mobilenet_v2(batch: int = 128, seed: int = 0, classes: int = 1000) -> Graph:
+    """torchvision MobileNetV2 with BN folded: 3x3/2 stem, 17 inverted residual blocks
+    (1x1 expand + ReLU6, 3x3 depthwise + ReLU6, 1x1 linear projection, residual when
+    shapes allow), 1x1 conv to 1280 + ReLU6, GAP, fc."""
+    g = Graph("mobilenet_v2", [], [], [])
+    net = _ConvNet(g, seed)
+    x = g.input("x", (batch, 3, 224, 224))
+    h = net.relu6(net.conv(x, 32, 3, 2, 1))
+    c_in = 32
+    for t, c, n, s in ((1, 16, 1, 1), (6, 24, 2, 2), (6, 32, 3, 2), (6, 64, 4, 2), (6, 96, 3, 1), (6, 160, 3, 2),
+                       (6, 320, 1, 1)):
+        for i in range(n):
+            stride = s if i == 0 else 1
+            hidden = c_in * t
+            y = h
+            if t != 1:
+                y = net.relu6(net.conv(y, hidden, 1))
+            y = net.relu6(net.conv(y, hidden, 3, stride, 1, groups=hidden))
+            y = net.conv(y, c, 1)
+            h = g.add("add", [y, h]) if (stride == 1 and c_in == c) else y
+            c_in = c
+    h = net.relu6(net.conv(h, 1280, 1))
+    g.outputs = [net.head(h, classes)]
+    return g
+
+
+def cnn_mira(batch: int = 16, seed: int = 0) -> Graph:
+    """examples/cnn.mira: two conv(3x3, pad 1) + bias + relu + maxpool(2) blocks, flatten, dense, softmax."""
+    rng = np.random.default_rng(seed)
+    g = Graph("cnn", [], [], [])
+    h = g.input("img", (batch, 1, 28, 28))
+    for o, c in ((16, 1), (32, 16)):
+        k = mira_random_weight(rng, (o, c, 3, 3))
+        b = (1.0 + 0.1 * rng.standard_normal((o, 1, 1))).astype(np.float32)
+        y = g.add("conv2d", [h, g.const(k)], {"stride": (1, 1), "padding": (1, 1)})
+        y = g.add("relu", [g.add("add", [y, g.const(b)])])
+        h = g.add("maxpool2d", [y], {"size": 2, "stride": 2})
+    n = h.type.numel // batch
+    flat = g.add("reshape", [h], {"shape": (batch, n)})
+    wf = mira_random_weight(rng, (n, 10))
+    bf = mira_random_weight(rng, (10,))
+    g.outputs = [g.add("softmax", [g.add("add", [g.add("matmul", [flat, g.const(wf)]), g.const(bf)])],
+                       {"axis": -1})]
+    return g
+
+
+BUILDERS = {
+    "mlp_dense": mlp_dense,
+    "mlp": mlp_mira,
+    "cnn": cnn_mira,
+    "mlp50m": mlp_50m,
+    "resnet18": resnet18,
+    "mobilenet_v2": mobilenet_v2,
+}
+
+
+def image_batch(shape, seed: int) -> np.ndarray:
+    """Synthetic images ~ U(0, 1)."""
+    return np.random.default_rng(seed).uniform(0.0, 1.0, shape).astype(np.float32)
+
+
+def normal_batch(shape, seed: int) -> np.ndarray:
+    return np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
+
+
+def conv_macs(g: Graph) -> int:
+    """Multiply-accumulates of every int8 contraction (qconv2d/qmatmul) in a quantized graph."""
+    total = 0
+    for op in g.ops:
+        if op.kind == "qconv2d":
+            n, o, oh, ow = op.result.type.shape
+            _, c, kh, kw = op.attrs["q"].shape
+            total += n * o * oh * ow * c * kh * kw
+        elif op.kind == "qmatmul":
+            k, n = op.attrs["q"].shape
+            total += (op.result.type.numel // n) * n * k
+    return total
+
+
+__all__ = ["BUILDERS", "conv_out", "conv_macs"]

@@ -1,0 +1,620 @@
+"""The `rocm` target: MIRA's Target/Executable plugin protocol on MI355X.
+
+Protocol (mira/backends/base.py:13-26):
+    Target.name, Target.check(op) -> None | reason, Target.compile(graph) -> Executable
+    Executable.run(feeds: {Value: ndarray}) -> {Value: ndarray}, Executable.report() -> str
+An op check() rejects runs on the CPU through the partitioner
+(mira/partition.py:70-93), exactly as for the reference's other targets.
+
+compile() plans one device layout per value, packs and uploads every constant
+once (int8 weights, f64 combined scales, epilogue operands), allocates every
+activation buffer, and turns the segment into a list of launches of
+libmira_rocm.so.  run() copies the inputs in, replays the launches on the
+current HIP stream and copies the outputs out.  There is no other compute
+path: without the library, compile() raises.
+
+Device layouts.  Rank-4 values live in NHWC; every other value row-major
+(C order, the last axis contiguous).  A value can exist as f32 and as one or
+more int8 copies (one per x_scale its q-op consumers use); producers write the
+f32 copy only if something reads it and fuse the first int8 copy into their
+epilogue (requantization, mira/ops.py:602-603 applied to the result).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Callable, Optional
+
+import numpy as np
+
+from . import _lib as L
+from . import ir
+from . import pack
+from .ops import conv_out, conv_params
+
+
+EPI_FNS = {"add", "sub", "mul", "div", "maximum", "minimum", "relu"}
+
+_torch = None
+
+
+def _t():
+    global _torch
+    if _torch is None:
+        import torch
+        _torch = torch
+    return _torch
+
+
+def _f32key(x: float) -> float:
+    """x_scale as the quantizer sees it: rounded to f32 (mira/ops.py:603)."""
+    return float(np.float32(x))
+
+
+@dataclass
+class DevValue:
+    """Device copies of one IR value."""
+    value: ir.Value
+    nhwc: bool                                   # rank-4 values are stored NHWC
+    f32: object = None                           # torch tensor (NHWC or row-major)
+    i8: dict = field(default_factory=dict)       # f32 x_scale -> (torch int8 tensor, row stride)
+    alias_of: Optional["DevValue"] = None
+
+    @property
+    def rows(self) -> int:
+        s = self.value.type.shape
+        if self.nhwc:
+            return s[0] * s[2] * s[3]
+        return int(np.prod(s[:-1], dtype=np.int64)) if len(s) > 1 else 1
+
+    @property
+    def cols(self) -> int:
+        s = self.value.type.shape
+        if self.nhwc:
+            return s[1]
+        return s[-1] if s else 1
+
+    def i8_ld(self) -> int:
+        return pack.c_pad_for(self.cols) if self.nhwc else pack.row_stride_for(self.cols)
+
+
+def _ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+class RocmTarget:
+    """MIRA Target for one MI355X (gfx950)."""
+    name = "rocm"
+    supports_control_flow = False
+
+    def __init__(self, device: int = 0, debug_acc: bool = False):
+        self.device = device
+        self.debug_acc = debug_acc
+
+    # ---------------------------------------------------------------- check
+
+    def check(self, op: ir.Op) -> Optional[str]:
+        """None if the rocm kernels run `op` with the golden model's exact arithmetic."""
+        if op.is_control:
+            return "control flow runs on the host"
+        if any(r.type.dtype != "f32" for r in op.results):
+            return "the rocm target computes the f32 graph (W8A8 parity needs f32 epilogues)"
+        k = op.kind
+        if k in ("qmatmul", "qconv2d"):
+            if k == "qconv2d" and op.attrs.get("groups", 1) != 1:
+                return "grouped int8 convolution has no kernel"
+            return self._check_epilogue(op, op.result.type.shape, k == "qconv2d")
+        if k == "conv2d":
+            x, w = op.inputs[0], op.inputs[1]
+            (_, _, _, g) = conv_params(op.attrs)
+            if not (g == x.type.shape[1] == w.type.shape[0] and w.type.shape[1] == 1):
+                return "only depthwise f32 convolution runs on rocm (dense f32 conv is not on the W8A8 path)"
+            if w.producer is None or not w.producer.is_constant_like:
+                return "depthwise weights must be constants"
+            return self._check_epilogue(op, op.result.type.shape, True, first_operand=2)
+        if k == "maxpool2d":
+            return None
+        if k == "pad":
+            pads = tuple(tuple(p) for p in op.attrs["pads"])
+            if op.inputs[0].type.rank != 4 or pads[0] != (0, 0) or pads[1] != (0, 0):
+                return "pad runs on rocm only over H and W of an NCHW tensor"
+            return None
+        if k == "reduce_mean":
+            axes = sorted(a % max(op.inputs[0].type.rank, 1) for a in op.attrs["axes"])
+            if op.inputs[0].type.rank != 4 or axes != [2, 3]:
+                return "reduce_mean runs on rocm only over H and W (global average pooling)"
+            return None
+        if k == "reshape":
+            return None
+        if k == "matmul":
+            return "f32 matmul stays on the CPU (its summation order is BLAS's, not reproducible bit for bit)"
+        return f"'{k}' has no rocm kernel"
+
+    def _check_epilogue(self, op: ir.Op, shape: tuple, is_conv: bool, first_operand: int = 1) -> Optional[str]:
+        for fn, idx, _sw in op.attrs.get("epilogue", ()):
+            if fn not in EPI_FNS:
+                return f"epilogue step '{fn}' is not bit-reproducible on rocm (libm)"
+            if idx is None:
+                continue
+            v = op.inputs[idx]
+            if v.type.dtype != "f32":
+                return "epilogue operands must be f32"
+            if v.producer is not None and v.producer.is_constant_like:
+                continue
+            if _bcast_mode(v.type.shape, shape, is_conv) is None:
+                return f"runtime epilogue operand {v.type} broadcasts onto {list(shape)} in a way rocm can't index"
+        return None
+
+    def compile(self, g: ir.Graph) -> "RocmExecutable":
+        return RocmExecutable(g, self)
+
+
+def _bcast_mode(oshape: tuple, rshape: tuple, is_conv: bool) -> Optional[int]:
+    """How an operand of shape `oshape` broadcasts onto result `rshape` as device rows x cols."""
+    r = len(rshape)
+    o = (1,) * (r - len(oshape)) + tuple(oshape)
+    if all(d == 1 for d in o):
+        return L.BC_SCALAR
+    if o == tuple(rshape):
+        return L.BC_FULL
+    ch = 1 if is_conv else r - 1                 # axis that becomes device columns
+    if all(d == 1 for i, d in enumerate(o) if i != ch) and o[ch] == rshape[ch]:
+        return L.BC_COL
+    if o[ch] == 1 and all(d == rshape[i] for i, d in enumerate(o) if i != ch):
+        return L.BC_ROW
+    return None
+
+
+class RocmExecutable:
+    """A compiled rocm segment: device buffers, packed constants and a launch list."""
+
+    def __init__(self, g: ir.Graph, target: RocmTarget):
+        torch = _t()
+        self.g = g
+        self.target = target
+        self.lib = L.load()
+        if not torch.cuda.is_available():
+            raise L.RocmError("the rocm target needs a ROCm GPU (torch.cuda.is_available() is False)")
+        self.dev = torch.device("cuda", target.device)
+        torch.cuda.set_device(self.dev)
+        L.check(self.lib.mr_init(target.device), "mr_init")
+        for op in g.ops:
+            if not op.is_constant_like:
+                reason = target.check(op)
+                if reason:
+                    raise L.RocmError(f"rocm cannot run {op.kind}: {reason}")
+        self.launches: list[tuple[str, Callable[[int], None]]] = []
+        self.keep: list = []          # host objects (ctypes structs, tensors) the launches refer to
+        self.dv: dict[ir.Value, DevValue] = {}
+        self.acc: dict[ir.Value, object] = {}      # debug int32 accumulators per q-op result
+        self.kernel_counts: dict[str, int] = {}
+        self.const_bytes = 0
+        self._plan()
+
+    # ---------------------------------------------------------------- planning
+
+    def _plan(self) -> None:
+        g = self.g
+        users = g.users()
+        self.users = users
+        self.consts = {op.result: op for op in g.ops if op.is_constant_like}
+        # which forms each value needs
+        self.need_f32: set = set(g.outputs)
+        self.need_i8: dict[ir.Value, list[float]] = {}
+        self.folded_pads: set = set()
+        for op in g.ops:
+            if op.is_constant_like:
+                continue
+            if op.kind in ("qmatmul", "qconv2d"):
+                s = _f32key(op.attrs["x_scale"])
+                lst = self.need_i8.setdefault(op.inputs[0], [])
+                if s not in lst:
+                    lst.append(s)
+                for v in op.inputs[1:]:
+                    self.need_f32.add(v)
+            elif op.kind == "maxpool2d" and self._foldable_pad(op.inputs[0]):
+                pad_op = op.inputs[0].producer
+                self.folded_pads.add(pad_op)
+                self.need_f32.add(pad_op.inputs[0])
+            else:
+                for v in op.inputs:
+                    if v not in self.consts or op.kind != "conv2d" or v is op.inputs[0]:
+                        self.need_f32.add(v)
+        # reshapes: the input must provide what the output's consumers read
+        for op in reversed(g.ops):
+            if op.kind == "reshape":
+                r = op.result
+                if r in self.need_f32 or r in self.need_i8:
+                    self.need_f32.add(op.inputs[0])
+        for v in g.inputs:
+            self._new_dv(v, with_i8=True)
+        for op in g.ops:
+            if op.is_constant_like:
+                continue
+            if op in self.folded_pads:
+                continue
+            getattr(self, f"_emit_{op.kind}")(op)
+        for v in g.outputs:
+            if v in self.consts and v not in self.dv:
+                self._const_dv(v)
+
+    def _foldable_pad(self, v: ir.Value) -> bool:
+        p = v.producer
+        if p is None or p.kind != "pad" or v in self.g.outputs or len(self.users.get(v, [])) != 1:
+            return False
+        pads = tuple(tuple(x) for x in p.attrs["pads"])
+        return p.inputs[0].type.rank == 4 and pads[0] == (0, 0) and pads[1] == (0, 0)
+
+    def _new_dv(self, v: ir.Value, with_i8: bool = False) -> DevValue:
+        """Allocate v's f32 copy if anything reads it; int8 copies only for segment inputs
+        (producers allocate the ones they write)."""
+        torch = _t()
+        d = DevValue(v, nhwc=v.type.rank == 4)
+        if v in self.need_f32:
+            s = v.type.shape
+            shape = (s[0], s[2], s[3], s[1]) if d.nhwc else s
+            d.f32 = torch.empty(shape, dtype=torch.float32, device=self.dev)
+        if with_i8:
+            for xs in self.need_i8.get(v, []):
+                d.i8[xs] = (torch.empty((d.rows, d.i8_ld()), dtype=torch.int8, device=self.dev), d.i8_ld())
+        self.dv[v] = d
+        return d
+
+    def _upload(self, arr: np.ndarray, dtype=None):
+        torch = _t()
+        a = np.ascontiguousarray(arr if dtype is None else arr.astype(dtype))
+        t = torch.from_numpy(a).to(self.dev)
+        self.const_bytes += a.nbytes
+        self.keep.append(t)
+        return t
+
+    def _const_value(self, v: ir.Value) -> np.ndarray:
+        op = self.consts[v]
+        if op.kind == "const":
+            return np.asarray(op.attrs["value"])
+        from .hosteval import evaluate            # a dequantize constant, materialized once
+        return evaluate("dequantize", [], op.attrs)
+
+    def _const_dv(self, v: ir.Value) -> DevValue:
+        """A constant used as a data input: upload it in its device layout."""
+        if v in self.dv:
+            return self.dv[v]
+        a = self._const_value(v).astype(np.float32)
+        d = DevValue(v, nhwc=v.type.rank == 4)
+        d.f32 = self._upload(a.transpose(0, 2, 3, 1) if d.nhwc else a)
+        self.dv[v] = d
+        for xs in self.need_i8.get(v, []):
+            d.i8[xs] = self._quantize_to(d, xs)
+        return d
+
+    def _src(self, v: ir.Value) -> DevValue:
+        if v in self.consts:
+            return self._const_dv(v)
+        return self.dv[v]
+
+    def _add(self, name: str, fn: Callable[[int], None]) -> None:
+        self.launches.append((name, fn))
+        self.kernel_counts[name] = self.kernel_counts.get(name, 0) + 1
+
+    # ---------------------------------------------------------------- int8 copies
+
+    def _quantize_to(self, d: DevValue, xs: float):
+        """Schedule a standalone quantize of d's f32 copy (mira/ops.py:602-603)."""
+        torch = _t()
+        ld = d.i8_ld()
+        q = torch.empty((d.rows, ld), dtype=torch.int8, device=self.dev)
+        lib, src, rows, cols = self.lib, d.f32, d.rows, d.cols
+        self._add("quantize", lambda s: L.check(lib.mr_quantize_rows(src.data_ptr(), rows, cols, cols, q.data_ptr(),
+                                                                     ld, xs, s), "mr_quantize_rows"))
+        return q, ld
+
+    def _finish_i8(self, d: DevValue, fused: Optional[float]) -> None:
+        """int8 copies the producer did not write itself come from its f32 copy."""
+        for xs in self.need_i8.get(d.value, []):
+            if xs != fused:
+                d.i8[xs] = self._quantize_to(d, xs)
+
+    # ---------------------------------------------------------------- epilogue descriptors
+
+    def _epilogue(self, op: ir.Op, out: DevValue, is_conv: bool, first: int, scale) -> tuple:
+        """Build the mr_epilogue for `op` writing into `out` (f32 and the first int8 copy)."""
+        e = L.Epilogue()
+        steps = op.attrs.get("epilogue", ())
+        if len(steps) > L.MAX_EPI:
+            raise L.RocmError(f"epilogue has {len(steps)} steps; the kernels take at most {L.MAX_EPI}")
+        rshape = op.result.type.shape
+        e.n_steps = len(steps)
+        for i, (fn, idx, sw) in enumerate(steps):
+            st = e.steps[i]
+            st.fn = L.EPI_FN[fn]
+            st.swapped = int(bool(sw))
+            if idx is None:
+                continue
+            v = op.inputs[idx]
+            if v in self.consts:
+                mode, t, ld = self._const_operand(v, rshape, is_conv)
+            else:
+                mode = _bcast_mode(v.type.shape, rshape, is_conv)
+                t = self.dv[v].f32
+                ld = out.cols if mode == L.BC_FULL else 1
+            st.mode, st.ptr, st.ld = mode, t.data_ptr(), ld
+        e.scale = _ptr(scale)
+        e.out_f32 = _ptr(out.f32)
+        e.ldo = out.cols
+        fused = None
+        wants = self.need_i8.get(out.value, [])
+        if wants:
+            fused = wants[0]
+            q = _t().empty((out.rows, out.i8_ld()), dtype=_t().int8, device=self.dev)
+            out.i8[fused] = (q, out.i8_ld())
+            e.out_i8 = q.data_ptr()
+            e.ldq = out.i8_ld()
+            e.out_xs = fused
+        if out.f32 is None and not wants:
+            raise L.RocmError(f"{op.kind} result is never read")
+        self.keep.append(e)
+        return e, fused
+
+    def _const_operand(self, v: ir.Value, rshape: tuple, is_conv: bool):
+        a = self._const_value(v).astype(np.float32)
+        mode = _bcast_mode(a.shape, rshape, is_conv)
+        if mode is None:                     # partial broadcast: materialize the full operand
+            a = np.broadcast_to(a, rshape)
+            mode = L.BC_FULL
+        if mode == L.BC_SCALAR:
+            return mode, self._upload(a.reshape(1)), 0
+        if mode in (L.BC_COL, L.BC_ROW):
+            return mode, self._upload(a.reshape(-1)), 1
+        full = np.broadcast_to(a, rshape)
+        if is_conv:
+            full = full.transpose(0, 2, 3, 1)
+        cols = rshape[1] if is_conv else rshape[-1]
+        return L.BC_FULL, self._upload(np.ascontiguousarray(full).reshape(-1, cols)), cols
+
+    # ---------------------------------------------------------------- emitters
+
+    def _acc_buffer(self, op: ir.Op, rows: int, cols: int):
+        if not self.target.debug_acc:
+            return None
+        t = _t().empty((rows, cols), dtype=_t().int32, device=self.dev)
+        self.acc[op.result] = t
+        return t
+
+    def _emit_qmatmul(self, op: ir.Op) -> None:
+        a = op.attrs
+        x = self._src(op.inputs[0])
+        q = np.asarray(a["q"], np.int8)
+        K, N = q.shape
+        xs = _f32key(a["x_scale"])
+        xq, lda = x.i8[xs] if xs in x.i8 else self._quantize_to(x, xs)
+        b = self._upload(pack.pack_matmul(q))
+        scale = self._upload(pack.combined_scale(a["x_scale"], a["w_scale"]))
+        out = self._new_dv(op.result)
+        e, fused = self._epilogue(op, out, False, 1, scale)
+        acc = self._acc_buffer(op, out.rows, N)
+        if acc is not None:
+            e.out_acc, e.ldacc = acc.data_ptr(), N
+        M = out.rows
+        lib, kp, npad = self.lib, b.shape[1], b.shape[0]
+        self._add("qmatmul", lambda s: L.check(
+            lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), kp, npad, M, N, K, C.byref(e), s), "mr_qmatmul"))
+        self._finish_i8(out, fused)
+
+    def _emit_qconv2d(self, op: ir.Op) -> None:
+        a = op.attrs
+        xv = op.inputs[0]
+        x = self._src(xv)
+        q = np.asarray(a["q"], np.int8)
+        n, c, h, w = xv.type.shape
+        o, _, kh, kw = q.shape
+        (sh, sw), (ph, pw), (dh, dw), _ = conv_params(a)
+        oh, ow = conv_out(h, kh, sh, ph, dh), conv_out(w, kw, sw, pw, dw)
+        xs = _f32key(a["x_scale"])
+        if xs in x.i8:
+            xq, cp = x.i8[xs]
+        else:
+            xq, cp = self._quantize_to(x, xs)
+        b = self._upload(pack.pack_conv(q, cp))
+        scale = self._upload(pack.combined_scale(a["x_scale"], a["w_scale"]))
+        geom = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=cp, o=o, oh=oh, ow=ow, kh=kh, kw=kw, sh=sh, sw=sw, ph=ph,
+                          pw=pw, dh=dh, dw=dw)
+        self.keep.append(geom)
+        out = self._new_dv(op.result)
+        e, fused = self._epilogue(op, out, True, 1, scale)
+        acc = self._acc_buffer(op, out.rows, o)
+        if acc is not None:
+            e.out_acc, e.ldacc = acc.data_ptr(), o
+        lib, kp, npad = self.lib, b.shape[1], b.shape[0]
+        self._add("qconv2d", lambda s: L.check(
+            lib.mr_qconv2d(xq.data_ptr(), C.byref(geom), b.data_ptr(), kp, npad, C.byref(e), s), "mr_qconv2d"))
+        self._finish_i8(out, fused)
+
+    def _emit_conv2d(self, op: ir.Op) -> None:
+        """Depthwise f32 convolution (groups == C, one filter per channel)."""
+        a = op.attrs
+        xv = op.inputs[0]
+        x = self._src(xv)
+        n, c, h, w = xv.type.shape
+        wt = self._const_value(op.inputs[1]).astype(np.float32)        # [C, 1, KH, KW]
+        _, _, kh, kw = wt.shape
+        (sh, sw), (ph, pw), (dh, dw), _ = conv_params(a)
+        oh, ow = conv_out(h, kh, sh, ph, dh), conv_out(w, kw, sw, pw, dw)
+        wdev = self._upload(np.ascontiguousarray(wt[:, 0].transpose(1, 2, 0)))   # [KH, KW, C]
+        geom = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=c, o=c, oh=oh, ow=ow, kh=kh, kw=kw, sh=sh, sw=sw, ph=ph, pw=pw,
+                          dh=dh, dw=dw)
+        self.keep.append(geom)
+        out = self._new_dv(op.result)
+        e, fused = self._epilogue(op, out, True, 2, None)
+        lib, xt = self.lib, x.f32
+        self._add("dwconv2d", lambda s: L.check(
+            lib.mr_dwconv2d_f32(xt.data_ptr(), C.byref(geom), wdev.data_ptr(), C.byref(e), s), "mr_dwconv2d_f32"))
+        self._finish_i8(out, fused)
+
+    def _emit_maxpool2d(self, op: ir.Op) -> None:
+        v = op.inputs[0]
+        pt = pl = 0
+        pad_value = 0.0
+        if v.producer is not None and v.producer in self.folded_pads:
+            p = v.producer
+            pads = tuple(tuple(x) for x in p.attrs["pads"])
+            pt, pl = pads[2][0], pads[3][0]
+            pad_value = float(np.asarray(p.attrs.get("value", 0)).astype(np.float32))
+            v = p.inputs[0]
+        x = self._src(v)
+        n, c, h, w = v.type.shape
+        _, _, oh, ow = op.result.type.shape
+        k, st = op.attrs["size"], op.attrs["stride"]
+        out = self._new_dv(op.result)
+        wants = self.need_i8.get(op.result, [])
+        fused = wants[0] if wants else None
+        yq, cp = None, 0
+        if fused is not None:
+            cp = out.i8_ld()
+            yq = _t().empty((out.rows, cp), dtype=_t().int8, device=self.dev)
+            out.i8[fused] = (yq, cp)
+        lib, xt, yt = self.lib, x.f32, out.f32
+        xsv = fused if fused is not None else 1.0
+        self._add("maxpool2d", lambda s: L.check(lib.mr_maxpool2d_f32(
+            xt.data_ptr(), n, h, w, c, k, st, pt, pl, pad_value, oh, ow, _ptr(yt), _ptr(yq), cp, xsv, s),
+            "mr_maxpool2d_f32"))
+        self._finish_i8(out, fused)
+
+    def _emit_pad(self, op: ir.Op) -> None:
+        x = self._src(op.inputs[0])
+        n, c, h, w = op.inputs[0].type.shape
+        pads = tuple(tuple(p) for p in op.attrs["pads"])
+        (t, b), (l, r) = pads[2], pads[3]
+        value = float(np.asarray(op.attrs.get("value", 0)).astype(np.float32))
+        out = self._new_dv(op.result)
+        if out.f32 is None:
+            out.f32 = _t().empty((n, h + t + b, w + l + r, c), dtype=_t().float32, device=self.dev)
+        lib, xt, yt = self.lib, x.f32, out.f32
+        self._add("pad", lambda s: L.check(lib.mr_pad_hw_f32(xt.data_ptr(), n, h, w, c, t, b, l, r, value,
+                                                             yt.data_ptr(), s), "mr_pad_hw_f32"))
+        self._finish_i8(out, None)
+
+    def _emit_reduce_mean(self, op: ir.Op) -> None:
+        x = self._src(op.inputs[0])
+        n, c, h, w = op.inputs[0].type.shape
+        out = self._new_dv(op.result)
+        wants = self.need_i8.get(op.result, [])
+        fused = wants[0] if wants else None
+        yq, ld = None, 0
+        if fused is not None:
+            ld = out.i8_ld()
+            yq = _t().empty((out.rows, ld), dtype=_t().int8, device=self.dev)
+            out.i8[fused] = (yq, ld)
+        lib, xt, yt = self.lib, x.f32, out.f32
+        xsv = fused if fused is not None else 1.0
+        self._add("mean_hw", lambda s: L.check(lib.mr_mean_hw_f32(
+            xt.data_ptr(), n, h * w, c, _ptr(yt), _ptr(yq), ld, xsv, s), "mr_mean_hw_f32"))
+        self._finish_i8(out, fused)
+
+    def _emit_reshape(self, op: ir.Op) -> None:
+        torch = _t()
+        src_v, r = op.inputs[0], op.result
+        x = self._src(src_v)
+        d = DevValue(r, nhwc=r.type.rank == 4)
+        self.dv[r] = d
+        if r not in self.need_f32 and r not in self.need_i8:
+            return
+        s_in = src_v.type.shape
+        s_out = r.type.shape
+        # NHWC of an [n, c, 1, 1] tensor is the same memory as C order of [n, c]
+        same_order = (not x.nhwc and not d.nhwc) or (x.nhwc and s_in[2] * s_in[3] == 1 and not d.nhwc) or \
+                     (not x.nhwc and d.nhwc and s_out[2] * s_out[3] == 1) or \
+                     (x.nhwc and d.nhwc and s_in[1] == s_out[1] and s_in[2] * s_in[3] == 1)
+        if same_order and x.f32 is not None:
+            d.f32 = x.f32.view(-1)
+        elif x.f32 is not None:
+            # go through the canonical (NCHW / C-order) copy
+            canon = x.f32
+            if x.nhwc:
+                n, c, h, w = s_in
+                canon = torch.empty((n, c, h, w), dtype=torch.float32, device=self.dev)
+                lib, xt, ct = self.lib, x.f32, canon
+                self._add("nhwc_to_nchw", lambda s: L.check(lib.mr_nhwc_to_nchw_f32(
+                    xt.data_ptr(), n, c, h, w, ct.data_ptr(), s), "mr_nhwc_to_nchw_f32"))
+            if d.nhwc:
+                n, c, h, w = r.type.shape
+                d.f32 = torch.empty((n, h, w, c), dtype=torch.float32, device=self.dev)
+                lib, ct, yt = self.lib, canon, d.f32
+                self._add("nchw_to_nhwc", lambda s: L.check(lib.mr_nchw_to_nhwc_f32(
+                    ct.data_ptr(), n, c, h, w, yt.data_ptr(), s), "mr_nchw_to_nhwc_f32"))
+            else:
+                d.f32 = canon
+        else:
+            raise L.RocmError("reshape input has no f32 copy")
+        self._finish_i8(d, None)
+
+    # ---------------------------------------------------------------- run
+
+    def upload(self, feeds: dict) -> None:
+        """Copy segment inputs to the device and build their device copies (queued on the stream)."""
+        torch = _t()
+        stream = torch.cuda.current_stream(self.dev).cuda_stream
+        self._staging = []
+        for v in self.g.inputs:
+            arr = np.ascontiguousarray(np.asarray(feeds[v]).astype(np.float32))
+            host = torch.from_numpy(arr)
+            d = self.dv[v]
+            if d.nhwc:
+                n, c, h, w = v.type.shape
+                stage = host.to(self.dev, non_blocking=False)
+                self._staging.append(stage)
+                if d.f32 is not None:
+                    L.check(self.lib.mr_nchw_to_nhwc_f32(stage.data_ptr(), n, c, h, w, d.f32.data_ptr(), stream),
+                            "mr_nchw_to_nhwc_f32")
+                for xs, (q, cp) in d.i8.items():
+                    L.check(self.lib.mr_quantize_nchw_nhwc(stage.data_ptr(), n, c, h, w, q.data_ptr(), cp, xs,
+                                                           stream), "mr_quantize_nchw_nhwc")
+            else:
+                stage = host.to(self.dev).reshape(d.rows, d.cols)
+                self._staging.append(stage)
+                if d.f32 is not None:
+                    d.f32.copy_(stage.reshape(d.f32.shape))
+                for xs, (q, ld) in d.i8.items():
+                    L.check(self.lib.mr_quantize_rows(stage.data_ptr(), d.rows, d.cols, d.cols, q.data_ptr(), ld,
+                                                      xs, stream), "mr_quantize_rows")
+
+    def launch(self) -> None:
+        """Queue every kernel of the segment on the current stream (inputs already uploaded)."""
+        stream = _t().cuda.current_stream(self.dev).cuda_stream
+        for _name, fn in self.launches:
+            fn(stream)
+
+    def download(self) -> dict:
+        torch = _t()
+        out = {}
+        for v in self.g.outputs:
+            d = self._src(v)
+            t = d.f32
+            if d.nhwc:
+                n, c, h, w = v.type.shape
+                canon = torch.empty((n, c, h, w), dtype=torch.float32, device=self.dev)
+                L.check(self.lib.mr_nhwc_to_nchw_f32(t.data_ptr(), n, c, h, w, canon.data_ptr(),
+                                                     torch.cuda.current_stream(self.dev).cuda_stream),
+                        "mr_nhwc_to_nchw_f32")
+                t = canon
+            out[v] = t.reshape(v.type.shape).cpu().numpy().astype(v.type.np_dtype)
+        return out
+
+    def run(self, feeds: dict) -> dict:
+        """mira/backends/base.py:13-14: host arrays in, finished host arrays out."""
+        self.upload(feeds)
+        self.launch()
+        out = self.download()
+        _t().cuda.synchronize(self.dev)
+        return out
+
+    def accumulators(self) -> dict:
+        """int32 accumulators of every q-op from the last run (needs RocmTarget(debug_acc=True))."""
+        return {v: t.cpu().numpy() for v, t in self.acc.items()}
+
+    def device_of(self, v: ir.Value) -> Optional[str]:
+        return "rocm" if v in self.dv else None
+
+    def report(self) -> str:
+        ks = ", ".join(f"{k} x{n}" for k, n in sorted(self.kernel_counts.items()))
+        return (f"rocm (MI355X gfx950): {len(self.g.compute_ops())} ops -> {len(self.launches)} kernel launches "
+                f"[{ks}]; {self.const_bytes / 2**20:.2f} MiB of packed constants on device")

@@ -1,0 +1,281 @@
+"""Per-kernel parity of libmira_rocm.so against the oracle, through the C ABI.
+
+int8 tensors and int32 accumulators must be bit-exact; f32 results are
+compared bit for bit too (every epilogue step is a single IEEE operation), which
+is stricter than the 1e-5 relative bound the W8A8 contract allows.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from mira_amd import _lib as L
+from mira_amd import pack
+from oracle import golden as G
+
+from conftest import bits_equal
+from gpu_util import T, empty, epilogue, stream, sync
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+    return torch
+
+
+# ---------------------------------------------------------------- K1 quantize
+
+@pytest.mark.parametrize("rows,cols,xs", [(513, 100, 0.0371), (1, 64, 1.0), (4096, 4096, 0.031), (7, 3, 0.5)])
+def test_quantize_rows(lib, rows, cols, xs):
+    torch = _torch()
+    rng = np.random.default_rng(rows + cols)
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    x.ravel()[:6] = np.float32([0.5, 1.5, 2.5, -2.5, 1000, -1000]) * np.float32(xs)
+    ldq = pack.row_stride_for(cols)
+    q = empty((rows, ldq), torch.int8)
+    L.check(lib.mr_quantize_rows(T(x).data_ptr(), rows, cols, cols, q.data_ptr(), ldq, xs, stream()), "q")
+    sync()
+    got = q.cpu().numpy()
+    assert bits_equal(got[:, :cols], G.quantize_activation(x, xs).astype(np.int8))
+    assert not got[:, cols:].any()
+
+
+@pytest.mark.parametrize("n,c,h,w", [(3, 3, 21, 19), (2, 20, 5, 6), (1, 1, 28, 28)])
+def test_quantize_nchw_nhwc(lib, n, c, h, w):
+    torch = _torch()
+    rng = np.random.default_rng(c)
+    x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    cp = pack.c_pad_for(c)
+    q = empty((n, h, w, cp), torch.int8)
+    xs = float(np.float32(1 / 127))
+    L.check(lib.mr_quantize_nchw_nhwc(T(x).data_ptr(), n, c, h, w, q.data_ptr(), cp, xs, stream()), "q")
+    sync()
+    got = q.cpu().numpy()
+    want = G.quantize_activation(x, xs).astype(np.int8).transpose(0, 2, 3, 1)
+    assert bits_equal(got[..., :c], want) and not got[..., c:].any()
+
+
+# ---------------------------------------------------------------- K2/K3 qmatmul
+
+def _run_qmatmul(lib, x, q, ws, xs, steps_np, next_xs=None):
+    """steps_np: (fn, mode, operand array or None, swapped). Returns (acc, y f32, y int8)."""
+    torch = _torch()
+    M, K = x.shape
+    N = q.shape[1]
+    lda = pack.row_stride_for(K)
+    xq = empty((M, lda), torch.int8)
+    L.check(lib.mr_quantize_rows(T(x).data_ptr(), M, K, K, xq.data_ptr(), lda, xs, stream()), "q")
+    b = T(pack.pack_matmul(q))
+    scale = T(pack.combined_scale(xs, ws))
+    keep, steps = [], []
+    for fn, mode, arr, sw in steps_np:
+        if arr is None:
+            steps.append((fn, mode, None, 0, sw))
+            continue
+        t = T(np.ascontiguousarray(arr, np.float32))
+        keep.append(t)
+        ld = N if mode == L.BC_FULL else (1 if mode == L.BC_ROW else 0)
+        steps.append((fn, mode, t, ld, sw))
+    acc = empty((M, N), torch.int32)
+    y = empty((M, N), torch.float32)
+    ldq = pack.row_stride_for(N)
+    yq = empty((M, ldq), torch.int8) if next_xs else None
+    e = epilogue(steps, scale=scale, out_f32=y, ldo=N, out_i8=yq, ldq=ldq, xs=next_xs or 1.0, out_acc=acc, ldacc=N)
+    L.check(lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), b.shape[1], b.shape[0], M, N, K, C.byref(e), stream()),
+            "mr_qmatmul")
+    sync()
+    return acc.cpu().numpy(), y.cpu().numpy(), (yq.cpu().numpy()[:, :N] if yq is not None else None)
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 64, 10), (64, 784, 512), (300, 512, 1000), (1, 4096, 4096),
+                                   (4096, 4096, 1000), (33, 128, 65), (70000, 64, 128)])
+def test_qmatmul_bias_relu_requant(lib, M, K, N):
+    rng = np.random.default_rng(M * 7 + N)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    q, ws = G.quantize_array(w, 1)
+    xs = float(np.abs(x).max()) / 127
+    bias = rng.standard_normal(N).astype(np.float32) * 0.1
+    attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32",
+             "epilogue": (("add", 1, False), ("relu", None, False))}
+    want_acc = G.qmatmul_acc(x, attrs)
+    want = G.qmatmul([x, bias], attrs)
+    next_xs = float(want.max()) / 127 or 1.0
+    acc, y, yq = _run_qmatmul(lib, x, q, ws, xs, [("add", L.BC_COL, bias, False), ("relu", 0, None, False)], next_xs)
+    assert np.array_equal(acc, want_acc.astype(np.int32))
+    assert bits_equal(y, want)
+    assert bits_equal(yq, G.quantize_activation(want, next_xs).astype(np.int8))
+
+
+def test_qmatmul_every_epilogue_step(lib):
+    rng = np.random.default_rng(11)
+    M, K, N = 200, 96, 48
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    q = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    ws = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    xs = 0.025
+    full = rng.standard_normal((M, N)).astype(np.float32)
+    row = rng.uniform(0.5, 2, (M, 1)).astype(np.float32)
+    col = rng.uniform(0.5, 2, N).astype(np.float32)
+    lo, hi = np.array(-0.5, np.float32), np.array(0.75, np.float32)
+    epi = (("sub", 1, True), ("mul", 2, False), ("div", 3, True), ("add", 4, False), ("maximum", 5, False),
+           ("minimum", 6, True))
+    attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "epilogue": epi}
+    want = G.qmatmul([x, full, col, row, full, lo, hi], attrs)
+    _, y, _ = _run_qmatmul(lib, x, q, ws, xs, [
+        ("sub", L.BC_FULL, full, True), ("mul", L.BC_COL, col, False), ("div", L.BC_ROW, row, True),
+        ("add", L.BC_FULL, full, False), ("maximum", L.BC_SCALAR, lo.reshape(1), False),
+        ("minimum", L.BC_SCALAR, hi.reshape(1), True)])
+    assert bits_equal(y, want)
+
+
+def test_qmatmul_rejects_bad_shapes(lib):
+    torch = _torch()
+    a = empty((4, 16), torch.int8)
+    b = empty((32, 64), torch.int8)
+    e = epilogue(out_f32=empty((4, 8), torch.float32), ldo=8, scale=T(np.ones(8)))
+    assert lib.mr_qmatmul(a.data_ptr(), 15, b.data_ptr(), 64, 32, 4, 8, 16, C.byref(e), stream()) == 1
+    assert b"lda" in lib.mr_last_error()
+    assert lib.mr_qmatmul(a.data_ptr(), 16, b.data_ptr(), 60, 32, 4, 8, 16, C.byref(e), stream()) == 1
+
+
+# ---------------------------------------------------------------- K2c qconv2d
+
+CONV_CASES = [
+    # n, c, h, w, o, k, stride, pad, dilation
+    (2, 3, 32, 32, 64, 7, 2, 3, 1),       # ResNet stem layout (c_pad 4, 7 taps per row)
+    (2, 3, 17, 19, 32, 3, 2, 1, 1),       # MobileNetV2 stem layout (3 taps per row)
+    (2, 64, 14, 14, 64, 3, 1, 1, 1),
+    (2, 64, 15, 15, 128, 3, 2, 1, 1),
+    (2, 64, 14, 14, 128, 1, 2, 0, 1),     # downsample
+    (1, 256, 7, 7, 512, 3, 1, 1, 1),
+    (3, 24, 9, 9, 144, 1, 1, 0, 1),       # c_pad 32
+    (2, 16, 11, 11, 24, 3, 1, 2, 2),      # dilation 2
+    (2, 1, 28, 28, 16, 3, 1, 1, 1),       # single channel (cnn.mira)
+]
+
+
+@pytest.mark.parametrize("n,c,h,w,o,k,s,p,d", CONV_CASES)
+def test_qconv2d(lib, n, c, h, w, o, k, s, p, d):
+    torch = _torch()
+    rng = np.random.default_rng(n * 1000 + c * 10 + k)
+    x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    wt = rng.standard_normal((o, c, k, k)).astype(np.float32)
+    q, ws = G.quantize_array(wt, 0)
+    xs = float(np.abs(x).max()) / 127
+    oh = G.conv_out(h, k, s, p, d)
+    ow = G.conv_out(w, k, s, p, d)
+    bias = (rng.standard_normal((o, 1, 1)) * 0.1).astype(np.float32)
+    res = rng.standard_normal((n, o, oh, ow)).astype(np.float32)
+    attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "stride": (s, s), "padding": (p, p),
+             "dilation": (d, d), "epilogue": (("add", 1, False), ("add", 2, False), ("relu", None, False))}
+    assert G.qconv2d_certificate(x, attrs) < 2 ** 24
+    want_acc = G.qconv2d_acc(x, attrs)
+    want = G.qconv2d([x, bias, res], attrs)
+    next_xs = float(want.max()) / 127 or 1.0
+    cp = pack.c_pad_for(c)
+    xq = empty((n, h, w, cp), torch.int8)
+    L.check(lib.mr_quantize_nchw_nhwc(T(x).data_ptr(), n, c, h, w, xq.data_ptr(), cp, xs, stream()), "q")
+    b = T(pack.pack_conv(q, cp))
+    scale = T(pack.combined_scale(xs, ws))
+    g = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=cp, o=o, oh=oh, ow=ow, kh=k, kw=k, sh=s, sw=s, ph=p, pw=p, dh=d, dw=d)
+    M = n * oh * ow
+    bias_t = T(bias.reshape(o))
+    res_t = T(res.transpose(0, 2, 3, 1).reshape(M, o))
+    acc = empty((M, o), torch.int32)
+    y = empty((M, o), torch.float32)
+    ocp = pack.c_pad_for(o)
+    yq = empty((M, ocp), torch.int8)
+    e = epilogue([("add", L.BC_COL, bias_t, 0, False), ("add", L.BC_FULL, res_t, o, False),
+                  ("relu", 0, None, 0, False)], scale=scale, out_f32=y, ldo=o, out_i8=yq, ldq=ocp, xs=next_xs,
+                 out_acc=acc, ldacc=o)
+    L.check(lib.mr_qconv2d(xq.data_ptr(), C.byref(g), b.data_ptr(), b.shape[1], b.shape[0], C.byref(e), stream()),
+            "mr_qconv2d")
+    sync()
+    to_nhwc = lambda a: a.transpose(0, 2, 3, 1).reshape(M, o)
+    assert np.array_equal(acc.cpu().numpy(), to_nhwc(want_acc).astype(np.int32))
+    assert bits_equal(y.cpu().numpy(), to_nhwc(want))
+    assert bits_equal(yq.cpu().numpy()[:, :o], to_nhwc(G.quantize_activation(want, next_xs)).astype(np.int8))
+
+
+# ---------------------------------------------------------------- K4a depthwise, adjuncts
+
+@pytest.mark.parametrize("n,c,h,s", [(2, 32, 16, 1), (2, 144, 15, 2), (1, 960, 7, 1)])
+def test_dwconv_relu6(lib, n, c, h, s):
+    torch = _torch()
+    rng = np.random.default_rng(c)
+    x = (rng.standard_normal((n, c, h, h)) * 2).astype(np.float32)
+    wt = rng.standard_normal((c, 1, 3, 3)).astype(np.float32)
+    bias = (rng.standard_normal((c, 1, 1)) * 0.1).astype(np.float32)
+    zero, six = np.array(0, np.float32), np.array(6, np.float32)
+    attrs = {"stride": (s, s), "padding": (1, 1), "groups": c,
+             "epilogue": (("add", 2, False), ("maximum", 3, False), ("minimum", 4, False))}
+    want = G.conv2d([x, wt, bias, zero, six], attrs)
+    oh = want.shape[2]
+    xs_next = float(want.max()) / 127 or 1.0
+    xd = T(x.transpose(0, 2, 3, 1))
+    wd = T(np.ascontiguousarray(wt[:, 0].transpose(1, 2, 0)))
+    g = L.ConvGeom(n=n, h=h, w=h, c=c, c_pad=c, o=c, oh=oh, ow=oh, kh=3, kw=3, sh=s, sw=s, ph=1, pw=1, dh=1, dw=1)
+    M = n * oh * oh
+    y = empty((M, c), torch.float32)
+    cp = pack.c_pad_for(c)
+    yq = empty((M, cp), torch.int8)
+    bt, zt, st = T(bias.reshape(c)), T(zero.reshape(1)), T(six.reshape(1))
+    e = epilogue([("add", L.BC_COL, bt, 0, False), ("maximum", L.BC_SCALAR, zt, 0, False),
+                  ("minimum", L.BC_SCALAR, st, 0, False)], out_f32=y, ldo=c, out_i8=yq, ldq=cp, xs=xs_next)
+    L.check(lib.mr_dwconv2d_f32(xd.data_ptr(), C.byref(g), wd.data_ptr(), C.byref(e), stream()), "dw")
+    sync()
+    assert bits_equal(y.cpu().numpy(), want.transpose(0, 2, 3, 1).reshape(M, c))
+    assert bits_equal(yq.cpu().numpy()[:, :c],
+                      G.quantize_activation(want, xs_next).astype(np.int8).transpose(0, 2, 3, 1).reshape(M, c))
+
+
+def test_maxpool_with_folded_pad(lib):
+    torch = _torch()
+    rng = np.random.default_rng(12)
+    n, c, h = 2, 64, 112
+    x = np.maximum(rng.standard_normal((n, c, h, h)), 0).astype(np.float32)
+    p = G.pad([x], {"pads": ((0, 0), (0, 0), (1, 1), (1, 1)), "value": -np.inf})
+    want = G.maxpool2d([p], {"size": 3, "stride": 2})
+    oh = want.shape[2]
+    xs = float(want.max()) / 127
+    y = empty((n, oh, oh, c), torch.float32)
+    yq = empty((n, oh, oh, c), torch.int8)
+    L.check(lib.mr_maxpool2d_f32(T(x.transpose(0, 2, 3, 1)).data_ptr(), n, h, h, c, 3, 2, 1, 1, float("-inf"), oh, oh,
+                                 y.data_ptr(), yq.data_ptr(), c, xs, stream()), "maxpool")
+    sync()
+    assert bits_equal(y.cpu().numpy(), want.transpose(0, 2, 3, 1))
+    assert bits_equal(yq.cpu().numpy(), G.quantize_activation(want, xs).astype(np.int8).transpose(0, 2, 3, 1))
+
+
+@pytest.mark.parametrize("hw", [(7, 7), (1, 5), (14, 14), (56, 56)])
+def test_mean_hw(lib, hw):
+    torch = _torch()
+    rng = np.random.default_rng(hw[0])
+    n, c = 3, 512
+    x = (rng.standard_normal((n, c) + hw) * 4).astype(np.float32)
+    want = G.reduce("reduce_mean", [x], {"axes": (2, 3), "keepdims": True}).reshape(n, c)
+    y = empty((n, c), torch.float32)
+    L.check(lib.mr_mean_hw_f32(T(x.transpose(0, 2, 3, 1)).data_ptr(), n, hw[0] * hw[1], c, y.data_ptr(), None, 0,
+                               1.0, stream()), "mean")
+    sync()
+    assert bits_equal(y.cpu().numpy(), want)
+
+
+def test_pad_and_layouts(lib):
+    torch = _torch()
+    rng = np.random.default_rng(13)
+    x = rng.standard_normal((2, 5, 7, 9)).astype(np.float32)
+    xd = T(x)
+    nhwc = empty((2, 7, 9, 5), torch.float32)
+    back = empty((2, 5, 7, 9), torch.float32)
+    L.check(lib.mr_nchw_to_nhwc_f32(xd.data_ptr(), 2, 5, 7, 9, nhwc.data_ptr(), stream()), "t")
+    L.check(lib.mr_nhwc_to_nchw_f32(nhwc.data_ptr(), 2, 5, 7, 9, back.data_ptr(), stream()), "t")
+    padded = empty((2, 7 + 3, 9 + 1, 5), torch.float32)
+    L.check(lib.mr_pad_hw_f32(nhwc.data_ptr(), 2, 7, 9, 5, 1, 2, 0, 1, -7.5, padded.data_ptr(), stream()), "pad")
+    sync()
+    assert bits_equal(nhwc.cpu().numpy(), x.transpose(0, 2, 3, 1))
+    assert bits_equal(back.cpu().numpy(), x)
+    want = G.pad([x], {"pads": ((0, 0), (0, 0), (1, 2), (0, 1)), "value": -7.5}).transpose(0, 2, 3, 1)
+    assert bits_equal(padded.cpu().numpy(), want)

@@ -1,0 +1,128 @@
+"""End-to-end parity of the rocm target on the W8A8 configurations.
+
+Each graph is optimized and W8A8-quantized once; the same quantized graph (the
+same attrs) then runs on the rocm target and on the oracle's CPU executor.
+Every int32 accumulator, and every output, must match bit for bit.  Ops the
+rocm target rejects (softmax) run on the oracle's CPU target, as MIRA's
+partitioner would send them to its cpu target.
+
+Full-size configurations are checked through batch independence: rows of the
+batch-256 (or 4096) run must equal the oracle's results for those rows run on
+their own, with the same attrs.
+"""
+import numpy as np
+import pytest
+
+from mira_amd import models, passes
+from mira_amd.compiler import compile_graph
+from mira_amd.quantize import calibration_peaks, quantize_w8a8
+from mira_amd.target import RocmTarget
+from oracle import golden as G
+
+from conftest import bits_equal
+from gpu_util import oracle_env
+
+pytestmark = pytest.mark.gpu
+
+
+def _quantized(builder, batch, seed, calib_seeds, input_name="x", dist="normal", calib_batch=None, peaks=None):
+    g = builder(batch=batch, seed=seed)
+    passes.optimize(g)
+    if peaks is None:
+        cb = calib_batch or batch
+        twin = builder(batch=cb, seed=seed) if cb != batch else g
+        if twin is not g:
+            passes.optimize(twin)
+        shape = twin.inputs[0].type.shape
+        gen = models.image_batch if dist == "uniform" else models.normal_batch
+        peaks = calibration_peaks(twin, [{input_name: gen(shape, s)} for s in calib_seeds])
+    quantize_w8a8(g, peaks=peaks)
+    return g, peaks
+
+
+def _compare(g, feeds, check_acc=True, fallback=True):
+    runner = compile_graph(g, RocmTarget(debug_acc=True), fallback=G.CPUTarget() if fallback else None)
+    got = runner.run_list([feeds[v.name] for v in g.inputs])
+    env = oracle_env(g, feeds)
+    for v, out in zip(g.outputs, got):
+        assert bits_equal(out, env[v]), f"output {v} differs: max abs {np.abs(out - env[v]).max()}"
+    if check_acc:
+        n_acc = 0
+        for seg in runner.segments:
+            if seg.device != "rocm":
+                continue
+            accs = seg.executable.accumulators()
+            for op in seg.graph.ops:
+                if op.kind == "qmatmul":
+                    want = G.qmatmul_acc(env[op.inputs[0]], op.attrs)
+                    want = want.reshape(-1, want.shape[-1])
+                elif op.kind == "qconv2d":
+                    x = env[op.inputs[0]]
+                    assert G.qconv2d_certificate(x, op.attrs) < 2 ** 24
+                    want = G.qconv2d_acc(x, op.attrs)
+                    want = want.transpose(0, 2, 3, 1).reshape(-1, want.shape[1])
+                else:
+                    continue
+                assert np.array_equal(accs[op.result], want.astype(np.int32)), f"{op.kind} accumulators differ"
+                n_acc += 1
+        assert n_acc > 0
+    return runner
+
+
+def test_c1_dense_256x64_to_10():
+    """x f32[256,64] ~ N(0,1), w ~ N(0,0.1), b = 0; calibration on 8 seeded batches."""
+    g, _ = _quantized(models.mlp_dense, 256, 0, range(1, 9))
+    kinds = [op.kind for op in g.compute_ops()]
+    assert kinds == ["qmatmul"] and "epilogue" not in g.compute_ops()[0].attrs   # zero bias simplified away
+    _compare(g, {"x": models.normal_batch((256, 64), 100)}, fallback=False)
+
+
+def test_mlp_mira_with_softmax_fallback():
+    g, _ = _quantized(models.mlp_mira, 64, 0, (2, 3))
+    runner = _compare(g, {"x": models.normal_batch((64, 784), 1)})
+    assert [s.device for s in runner.segments] == ["rocm", "cpu"]
+    soft = next(op for op in g.compute_ops() if op.kind == "softmax")
+    assert "softmax" in runner.placement.reason[soft]
+
+
+def test_cnn_mira():
+    g, _ = _quantized(models.cnn_mira, 16, 0, (2, 3), input_name="img")
+    _compare(g, {"img": models.normal_batch((16, 1, 28, 28), 1)})
+
+
+def test_resnet18_batch2():
+    g, _ = _quantized(models.resnet18, 2, 0, (11, 12), dist="uniform")
+    runner = _compare(g, {"x": models.image_batch((2, 3, 224, 224), 5)}, fallback=False)
+    assert [s.device for s in runner.segments] == ["rocm"]
+
+
+def test_mobilenet_v2_batch2():
+    g, _ = _quantized(models.mobilenet_v2, 2, 0, (11, 12), dist="uniform")
+    runner = _compare(g, {"x": models.image_batch((2, 3, 224, 224), 5)}, fallback=False)
+    assert [s.device for s in runner.segments] == ["rocm"]
+
+
+def test_mlp50m_batch8():
+    g, _ = _quantized(models.mlp_50m, 8, 0, (2, 3))
+    _compare(g, {"x": models.normal_batch((8, 4096), 1)}, fallback=False)
+
+
+def _rows_match_small_run(builder, big, small_rows, seed, calib_seeds, dist, input_shape_tail, input_name="x"):
+    """Run the full-size batch on rocm; rerun chosen rows alone on the oracle with the same attrs."""
+    g_big, peaks = _quantized(builder, big, seed, calib_seeds, dist=dist, calib_batch=2)
+    gen = models.image_batch if dist == "uniform" else models.normal_batch
+    x = gen((big,) + input_shape_tail, 7)
+    runner = compile_graph(g_big, RocmTarget())
+    (out,) = runner.run_list([x])
+    g_small, _ = _quantized(builder, len(small_rows), seed, calib_seeds, dist=dist, peaks=peaks)
+    (want,) = G.run_graph(g_small, {input_name: x[small_rows]})
+    assert bits_equal(out[small_rows], want)
+    assert np.isfinite(out).all()
+
+
+def test_resnet18_batch256_rows():
+    _rows_match_small_run(models.resnet18, 256, [0, 255], 0, (11, 12), "uniform", (3, 224, 224))
+
+
+def test_mlp50m_batch4096_rows():
+    _rows_match_small_run(models.mlp_50m, 4096, [0, 1234, 4095], 0, (2, 3), "normal", (4096,))
