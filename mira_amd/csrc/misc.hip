@@ -23,17 +23,19 @@ static int grid_1d(int64_t total, int block) {
 // adds each tap's product in (i, j) order with separate roundings, exactly
 // like `acc += einsum(...)` per tap in the reference; taps that fall into
 // the zero padding still add 0 * w.
+// Idx is uint32_t when every index fits (the host checks), else uint64_t:
+// 64-bit division is a long software sequence on the GPU.
+template <typename Idx>
 __global__ void __launch_bounds__(256) dwconv_kernel(const float* __restrict__ x, mr_conv_geom G,
                                                      const float* __restrict__ w, const EpiDev e) {
-  const int64_t total = int64_t(G.n) * G.oh * G.ow * G.c;
-  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
-       t += (int64_t)gridDim.x * blockDim.x) {
-    const int c = static_cast<int>(t % G.c);
-    const int64_t pix = t / G.c;
-    const int ow = static_cast<int>(pix % G.ow);
-    const int64_t r = pix / G.ow;
-    const int oh = static_cast<int>(r % G.oh);
-    const int64_t img = r / G.oh;
+  const Idx total = Idx(G.n) * G.oh * G.ow * G.c;
+  for (Idx t = blockIdx.x * Idx(blockDim.x) + threadIdx.x; t < total; t += Idx(gridDim.x) * blockDim.x) {
+    const int c = static_cast<int>(t % Idx(G.c));
+    const Idx pix = t / Idx(G.c);
+    const int ow = static_cast<int>(pix % Idx(G.ow));
+    const Idx r = pix / Idx(G.ow);
+    const int oh = static_cast<int>(r % Idx(G.oh));
+    const int64_t img = r / Idx(G.oh);
     float acc = 0.0f;
     for (int i = 0; i < G.kh; ++i) {
       const int ih = oh * G.sh - G.ph + i * G.dh;
@@ -45,26 +47,26 @@ __global__ void __launch_bounds__(256) dwconv_kernel(const float* __restrict__ x
         acc = __fadd_rn(acc, __fmul_rn(xv, w[(i * G.kw + j) * G.c + c]));
       }
     }
-    const float y = epi_steps(e, acc, pix, c);
-    epi_store(e, y, pix, c);
+    const float y = epi_steps(e, acc, int64_t(pix), c);
+    epi_store(e, y, int64_t(pix), c);
   }
 }
 
 // ---------------------------------------------------------------- maxpool
 
+template <typename Idx>
 __global__ void __launch_bounds__(256) maxpool_kernel(const float* __restrict__ x, int n, int h, int w, int c,
                                                       int size, int stride, int pt, int pl, float pad_value, int oh,
                                                       int ow, float* __restrict__ y, int8_t* __restrict__ yq,
                                                       int c_pad, float xs) {
-  const int64_t total = int64_t(n) * oh * ow * c;
-  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
-       t += (int64_t)gridDim.x * blockDim.x) {
-    const int ch = static_cast<int>(t % c);
-    const int64_t pix = t / c;
-    const int ox = static_cast<int>(pix % ow);
-    const int64_t r = pix / ow;
-    const int oy = static_cast<int>(r % oh);
-    const int64_t img = r / oh;
+  const Idx total = Idx(n) * oh * ow * c;
+  for (Idx t = blockIdx.x * Idx(blockDim.x) + threadIdx.x; t < total; t += Idx(gridDim.x) * blockDim.x) {
+    const int ch = static_cast<int>(t % Idx(c));
+    const int64_t pix = t / Idx(c);
+    const int ox = static_cast<int>(Idx(pix) % Idx(ow));
+    const Idx r = Idx(pix) / Idx(ow);
+    const int oy = static_cast<int>(r % Idx(oh));
+    const int64_t img = r / Idx(oh);
     float m = 0.0f;
     for (int i = 0; i < size; ++i) {
       const int ih = oy * stride - pt + i;
@@ -169,17 +171,17 @@ __global__ void __launch_bounds__(256) mean_hw_kernel(const float* __restrict__ 
 
 // ---------------------------------------------------------------- pad / layout
 
+template <typename Idx>
 __global__ void __launch_bounds__(256) pad_kernel(const float* __restrict__ x, int n, int h, int w, int c, int top,
                                                   int left, int oh, int ow, float value, float* __restrict__ y) {
-  const int64_t total = int64_t(n) * oh * ow * c;
-  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
-       t += (int64_t)gridDim.x * blockDim.x) {
-    const int ch = static_cast<int>(t % c);
-    const int64_t pix = t / c;
-    const int ox = static_cast<int>(pix % ow);
-    const int64_t r = pix / ow;
-    const int oy = static_cast<int>(r % oh);
-    const int64_t img = r / oh;
+  const Idx total = Idx(n) * oh * ow * c;
+  for (Idx t = blockIdx.x * Idx(blockDim.x) + threadIdx.x; t < total; t += Idx(gridDim.x) * blockDim.x) {
+    const int ch = static_cast<int>(t % Idx(c));
+    const Idx pix = t / Idx(c);
+    const int ox = static_cast<int>(pix % Idx(ow));
+    const Idx r = pix / Idx(ow);
+    const int oy = static_cast<int>(r % Idx(oh));
+    const int64_t img = r / Idx(oh);
     const int ih = oy - top, iw = ox - left;
     y[t] = (unsigned(ih) < unsigned(h) && unsigned(iw) < unsigned(w)) ? x[((img * h + ih) * w + iw) * c + ch]
                                                                        : value;
@@ -233,8 +235,13 @@ int mr_dwconv2d_f32(const float* x, const mr_conv_geom* cg, const float* w, cons
   MR_REQUIRE(!epi->out_acc, "mr_dwconv2d_f32: no int32 accumulators");
   const int64_t total = int64_t(G.n) * oh * ow * G.c;
   if (total == 0) return MR_OK;
-  hipLaunchKernelGGL(mr::dwconv_kernel, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), x, G, w, e);
+  const int64_t in_total = int64_t(G.n) * G.h * G.w * G.c;
+  if (total < (int64_t(1) << 32) - 65536 * 256 && in_total < (int64_t(1) << 32))
+    hipLaunchKernelGGL(mr::dwconv_kernel<uint32_t>, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, G, w, e);
+  else
+    hipLaunchKernelGGL(mr::dwconv_kernel<uint64_t>, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, G, w, e);
   MR_LAUNCH_CHECK("dwconv2d");
   return MR_OK;
 }
@@ -255,9 +262,14 @@ int mr_maxpool2d_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c,
   }
   const int64_t total = int64_t(n) * oh * ow * c;
   if (total == 0) return MR_OK;
-  hipLaunchKernelGGL(mr::maxpool_kernel, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), x, n, h, w, c, size, stride, pad_top, pad_left, pad_value, oh,
-                     ow, y, yq, c_pad, xs);
+  if (total < (int64_t(1) << 32) - 65536 * 256)
+    hipLaunchKernelGGL(mr::maxpool_kernel<uint32_t>, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, n, h, w, c, size, stride, pad_top, pad_left, pad_value,
+                       oh, ow, y, yq, c_pad, xs);
+  else
+    hipLaunchKernelGGL(mr::maxpool_kernel<uint64_t>, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, n, h, w, c, size, stride, pad_top, pad_left, pad_value,
+                       oh, ow, y, yq, c_pad, xs);
   MR_LAUNCH_CHECK("maxpool2d");
   return MR_OK;
 }
@@ -286,8 +298,12 @@ int mr_pad_hw_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, in
   const int oh = h + top + bottom, ow = w + left + right;
   const int64_t total = int64_t(n) * oh * ow * c;
   if (total == 0) return MR_OK;
-  hipLaunchKernelGGL(mr::pad_kernel, dim3(mr::grid_1d(total, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     x, n, h, w, c, top, left, oh, ow, value, y);
+  if (total < (int64_t(1) << 32) - 65536 * 256)
+    hipLaunchKernelGGL(mr::pad_kernel<uint32_t>, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, n, h, w, c, top, left, oh, ow, value, y);
+  else
+    hipLaunchKernelGGL(mr::pad_kernel<uint64_t>, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, n, h, w, c, top, left, oh, ow, value, y);
   MR_LAUNCH_CHECK("pad_hw");
   return MR_OK;
 }

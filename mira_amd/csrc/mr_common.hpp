@@ -3,8 +3,10 @@
 // Numerics follow NumPy's float32 semantics as used by MIRA's golden model:
 // every epilogue step is one correctly rounded IEEE-754 single operation
 // (the library is built with -ffp-contract=off so nothing is fused), the
-// activation quantizer divides (never multiplies by a reciprocal) and rounds
-// half to even, and dequantization multiplies in double precision.
+// activation quantizer rounds the correctly rounded float32 quotient half to
+// even (computed either by IEEE division or by the provably equivalent
+// double-precision reciprocal multiply below, never by a float32 reciprocal),
+// and dequantization multiplies in double precision.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -66,6 +68,17 @@ __device__ __forceinline__ int8_t quantize_one(float x, float xs) {
   return static_cast<int8_t>(static_cast<int>(t));
 }
 
+// The same quantizer with the division replaced by a double-precision
+// multiply with rxs = fl64(1 / xs): for float32 y and xs the exact quotient
+// is never within 2^-49 (relative) of a float32 rounding midpoint, and
+// fl64(fl64(y) * rxs) is within 2^-51 of it, so rounding it to float32 gives
+// exactly fl32(y / xs).  Checked against IEEE division in the test suite.
+__device__ __forceinline__ int8_t quantize_rcp(float y, double rxs) {
+  float t = rintf(static_cast<float>(__dmul_rn(static_cast<double>(y), rxs)));
+  t = fminf(fmaxf(t, -127.0f), 127.0f);
+  return static_cast<int8_t>(static_cast<int>(t));
+}
+
 // NumPy float32 maximum/minimum on x86: NaN in either operand propagates, and
 // on equality (including +0 vs -0) the second operand is returned.
 __device__ __forceinline__ float np_maximum(float a, float b) {
@@ -116,66 +129,61 @@ struct EpiDev {
   int32_t reserved;
   int32_t* out_acc;
   int64_t ldacc;
+  double out_rxs;  // fl64(1 / out_xs), computed on the host
+  // Fixed form recognised on the host (make_epi): the steps are, in this order
+  // and each optional, add(per-column) -> add(full) -> maximum(scalar) or relu
+  // -> minimum(scalar), none swapped.  Every bias/residual/ReLU/ReLU6 epilogue
+  // has this form; kernels then run it without the general step interpreter.
+  int32_t fixed;
+  int32_t f_col, f_full, f_lo, f_hi;
+  int32_t reserved2;
+  const float* col_ptr;
+  const float* full_ptr;
+  int64_t full_ld;
+  const float* lo_ptr;  // NULL with f_lo set: relu (maximum with +0)
+  const float* hi_ptr;
 };
 
-// Apply the f32 epilogue steps to NV values of one column `col` at rows
-// row[v] (callers clamp rows past the end to a valid row and skip their
-// stores).  The step loop is unrolled with static indices so the descriptor
-// stays in the kernel-argument segment (a dynamic index would copy it to
-// scratch); the value loop is innermost so each step's branch is uniform.
-template <int NV>
-__device__ __forceinline__ void epi_steps_col(const EpiDev& e, float (&y)[NV], const int64_t (&row)[NV],
-                                              int64_t col) {
-#pragma unroll
-  for (int s = 0; s < MR_MAX_EPI; ++s) {
-    if (s >= e.n_steps) break;
+// The general step interpreter (mira/ops.py:192-199) for one element at
+// (row, col): a rolled loop, so its code stays small; the descriptor is a
+// by-reference kernel argument and is read from the kernel-argument segment.
+__device__ __forceinline__ float epi_generic(const EpiDev& e, float y, int64_t row, int64_t col) {
+#pragma unroll 1
+  for (int s = 0; s < e.n_steps; ++s) {
     const int fn = e.steps[s].fn;
-    const int mode = e.steps[s].mode;
-    const float* p = e.steps[s].ptr;
-    const int64_t ld = e.steps[s].ld;
     if (fn == MR_EPI_RELU) {
-#pragma unroll
-      for (int v = 0; v < NV; ++v) y[v] = np_maximum(y[v], 0.0f);
+      y = np_maximum(y, 0.0f);
       continue;
     }
-    float o[NV];
-    if (mode == MR_BC_SCALAR) {
-      const float c = p[0];
-#pragma unroll
-      for (int v = 0; v < NV; ++v) o[v] = c;
-    } else if (mode == MR_BC_COL) {
-      const float c = p[col];
-#pragma unroll
-      for (int v = 0; v < NV; ++v) o[v] = c;
-    } else if (mode == MR_BC_ROW) {
-#pragma unroll
-      for (int v = 0; v < NV; ++v) o[v] = p[row[v] * ld];
-    } else {
-#pragma unroll
-      for (int v = 0; v < NV; ++v) o[v] = p[row[v] * ld + col];
-    }
-    if (e.steps[s].swapped) {
-#pragma unroll
-      for (int v = 0; v < NV; ++v) y[v] = epi_binary(fn, o[v], y[v]);
-    } else {
-#pragma unroll
-      for (int v = 0; v < NV; ++v) y[v] = epi_binary(fn, y[v], o[v]);
-    }
+    const float* p = e.steps[s].ptr;
+    const int mode = e.steps[s].mode;
+    float o;
+    if (mode == MR_BC_SCALAR) o = p[0];
+    else if (mode == MR_BC_COL) o = p[col];
+    else if (mode == MR_BC_ROW) o = p[row * e.steps[s].ld];
+    else o = p[row * e.steps[s].ld + col];
+    y = e.steps[s].swapped ? epi_binary(fn, o, y) : epi_binary(fn, y, o);
   }
+  return y;
 }
 
-// Single-element form for the elementwise kernels.
+// The fixed form (see EpiDev): add(col)? add(full)? maximum(lo)? minimum(hi)?
+__device__ __forceinline__ float epi_fixed(const EpiDev& e, float y, int64_t row, int64_t col) {
+  if (e.f_col) y = __fadd_rn(y, e.col_ptr[col]);
+  if (e.f_full) y = __fadd_rn(y, e.full_ptr[row * e.full_ld + col]);
+  if (e.f_lo) y = np_maximum(y, e.lo_ptr ? e.lo_ptr[0] : 0.0f);
+  if (e.f_hi) y = np_minimum(y, e.hi_ptr[0]);
+  return y;
+}
+
 __device__ __forceinline__ float epi_steps(const EpiDev& e, float y, int64_t row, int64_t col) {
-  float v[1] = {y};
-  const int64_t r[1] = {row};
-  epi_steps_col<1>(e, v, r, col);
-  return v[0];
+  return e.fixed ? epi_fixed(e, y, row, col) : epi_generic(e, y, row, col);
 }
 
 // Write the outputs for one finished result element.
 __device__ __forceinline__ void epi_store(const EpiDev& e, float y, int64_t row, int64_t col) {
   if (e.out_f32) e.out_f32[row * e.ldo + col] = y;
-  if (e.out_i8) e.out_i8[row * e.ldq + col] = quantize_one(y, e.out_xs);
+  if (e.out_i8) e.out_i8[row * e.ldq + col] = quantize_rcp(y, e.out_rxs);
 }
 
 // Dequantize one int32 accumulator (mira/ops.py:618 / :633):

@@ -2,27 +2,47 @@
 // (v_mfma_i32_32x32x32_i8) with the dequant / epilogue / requant fused into
 // the store.  One kernel template serves the dense GEMM of qmatmul
 // (mira/ops.py:616-620) and the implicit-GEMM convolution of qconv2d
-// (mira/ops.py:630-634): only the loader of the activation tile differs.
+// (mira/ops.py:630-634): only the address generation of the activation
+// (A) tile differs.
 //
-// Tiling: a workgroup owns a BM x BN tile of the result and walks K in
-// 64-byte steps.  Each step's A (activations, BM x 64) and B (weights,
-// BN x 64) slices are fetched from global memory into registers while the
-// previous slice is consumed from LDS (double-buffered LDS, one barrier per
-// step).  Each wave computes a (BM/WM) x (BN/WN) sub-tile as 32x32 MFMA
-// blocks.  Integer accumulation is exact and order-free, so A and B
-// fragments only need the same byte order along K, which they get by
-// construction (both read 16 contiguous K bytes per lane).
+// Pipeline.  A workgroup owns a BM x BN tile of the result and walks K in
+// 64-byte steps.  Each step's A slice (BM x 64 bytes) and B slice (weights,
+// BN x 64 bytes) travel global -> LDS by direct-to-LDS loads
+// (global_load_lds_dwordx4: no VGPR staging), STAGES-1 steps ahead of the
+// MFMAs, through a ring of STAGES LDS buffers.  One s_barrier per step; the
+// only wait is a counted vmcnt for the step about to be consumed.  Padding
+// taps and rows/columns past the end load from a 256-byte zero page, so the
+// LDS copy is always complete and no lane needs a masked write.
+//
+// LDS layout.  Each row of a slice is 64 bytes = four 16-byte chunks; chunk c
+// of row r sits at position c ^ ((r >> 2) & 3).  gfx950's LDS serves 256 bytes
+// (64 banks) per clock, i.e. 16 lanes of a ds_read_b128; 16 consecutive rows of
+// one chunk then land on 16 distinct 16-byte bank groups.
+//
+// MFMA fragments.  Integer accumulation is exact and order-free, so the A and
+// B fragments only need the same byte order along K: both read 16 contiguous
+// K bytes per lane.  Result layout of the 32x32 block: lane holds column
+// (lane & 31) and rows 8*(r/4) + 4*(lane/32) + (r%4), r = 0..15.
 #include "mr_common.hpp"
 
 namespace mr {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
 
-enum AMode { A_DENSE = 0, A_CONV16 = 1, A_CONV4 = 2 };
+// Source of every padding or out-of-range chunk (zero-initialised at load time).
+__device__ __attribute__((aligned(256))) int8_t g_zero_page[256];
+
+enum AMode {
+  A_DENSE = 0,   // row-major [M, lda] int8
+  A_CONV64 = 1,  // NHWC, c_pad % 64 == 0: a 64-byte K step is one tap, one channel block
+  A_CONV16 = 2,  // NHWC, c_pad % 16 == 0: K steps may span taps
+  A_CONV4 = 3    // NHWC, c_pad == 4: each 16-byte chunk is 4 taps of one kernel row
+};
 
 struct GemmArgs {
-  const int8_t* a;  // dense: [M, lda] int8; conv: NHWC int8 input
+  const int8_t* a;  // dense: [M, lda]; conv: NHWC input
   int64_t lda;
   const int8_t* b;  // packed weights [n_pad, k_pad]
   int64_t k_pad;
@@ -32,95 +52,147 @@ struct GemmArgs {
   int32_t k_tiles;
   int32_t tiles_m;
   int32_t tiles_n;
-  // convolution geometry (A_CONV16 / A_CONV4)
+  // convolution geometry
   int32_t H, W, C_pad, OH, OW, KH, KW, SH, SW, PH, PW, DH, DW;
   int32_t row_bytes;  // A_CONV4: packed bytes per kernel row
-  int32_t k_real;     // A_CONV16: KH*KW*C_pad (k beyond is padding)
+  int32_t k_real;     // A_CONV16: KH*KW*C_pad
+  int32_t cb_per_tap; // A_CONV64: C_pad / 64
 };
 
-constexpr int BK = 64;         // K bytes per pipeline step
-constexpr int LDS_STRIDE = 80; // bytes per LDS row (64 data + 16 pad: conflict-free b128 reads)
+constexpr int BK = 64;
 
-// Dequantize, run the epilogue on, and store the 16 values of one 32x32 MFMA
-// block that this lane holds: column `col`, rows rbase + 8*(r/4) + (r%4).
-// The step loop runs at run time: the descriptor is a by-reference kernel
-// argument, so indexing it dynamically reads the kernel-argument segment.
-__device__ __forceinline__ void store_block(const EpiDev* __restrict__ e, const v16i& acc, int64_t rbase, int col,
-                                            int64_t M, int N) {
-  if (col >= N) return;
-  const double scale = e->scale[col];
-  int64_t rows[16];
-  float y[16];
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier without a memory fence: the LDS-DMA completion it orders
+// is established by the counted vmcnt wait before it.  The signal fences keep
+// the compiler from moving memory accesses across it.
+__device__ __forceinline__ void block_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+__device__ __forceinline__ void dma16(const void* src, int8_t* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)lds_dst, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* src, int8_t* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)lds_dst, 4, 0, 0);
+}
+
+// Per-thread constants of the 4 result columns col0 .. col0+3 a thread owns
+// in the epilogue: dequant scales and, for the fixed form, the per-column
+// operand and the scalar bounds.
+struct EpiCols4 {
+  double scale[4];
+  float colv[4];
+  float lo, hi;
+  bool vec;  // four valid columns and every access 16-byte (f32) / 4-byte (int8) aligned
+};
+
+__device__ __forceinline__ void load_cols4(const EpiDev& e, int col0, int N, EpiCols4& c) {
+  bool vec = col0 + 3 < N && (e.ldo % 4 == 0) && (e.ldq % 4 == 0) && (e.ldacc % 4 == 0) &&
+             (reinterpret_cast<uintptr_t>(e.out_f32) % 16 == 0) && (reinterpret_cast<uintptr_t>(e.out_i8) % 4 == 0) &&
+             (reinterpret_cast<uintptr_t>(e.out_acc) % 16 == 0);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t row = rbase + 8 * (r >> 2) + (r & 3);
-    rows[r] = row < M ? row : M - 1;
-    y[r] = dequant(acc[r], scale);
+  for (int k = 0; k < 4; ++k) {
+    c.scale[k] = col0 + k < N ? e.scale[col0 + k] : 0.0;
+    c.colv[k] = (e.f_col && col0 + k < N) ? e.col_ptr[col0 + k] : 0.0f;
   }
-  for (int s = 0; s < e->n_steps; ++s) {
-    const EpiStepDev st = e->steps[s];
-    if (st.fn == MR_EPI_RELU) {
+  c.lo = e.f_lo && e.lo_ptr ? e.lo_ptr[0] : 0.0f;
+  c.hi = e.f_hi ? e.hi_ptr[0] : 0.0f;
+  if (e.f_full) vec = vec && (e.full_ld % 4 == 0) && (reinterpret_cast<uintptr_t>(e.full_ptr) % 16 == 0);
+  c.vec = vec;
+}
+
+// Dequantize, apply the epilogue to, and store result row `row`, columns
+// col0 .. col0+3 (mira/ops.py:616-620 / 630-634, then 192-199).
+template <bool FIXED>
+__device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, const v4i& acc, int64_t row, int col0,
+                                          int N) {
+  float y[4];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) y[v] = np_maximum(y[v], 0.0f);
-      continue;
+  for (int k = 0; k < 4; ++k) y[k] = dequant(acc[k], c.scale[k]);
+  if constexpr (FIXED) {
+    if (e.f_col) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) y[k] = __fadd_rn(y[k], c.colv[k]);
     }
-    float o[16];
-    if (st.mode == MR_BC_SCALAR) {
-      const float c = st.ptr[0];
+    if (e.f_full) {
+      const float* p = e.full_ptr + row * e.full_ld + col0;
+      float o[4];
+      if (c.vec) {
+        const float4 v = *reinterpret_cast<const float4*>(p);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+      } else {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) o[v] = c;
-    } else if (st.mode == MR_BC_COL) {
-      const float c = st.ptr[col];
+        for (int k = 0; k < 4; ++k) o[k] = col0 + k < N ? p[k] : 0.0f;
+      }
 #pragma unroll
-      for (int v = 0; v < 16; ++v) o[v] = c;
-    } else if (st.mode == MR_BC_ROW) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) o[v] = st.ptr[rows[v] * st.ld];
-    } else {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) o[v] = st.ptr[rows[v] * st.ld + col];
+      for (int k = 0; k < 4; ++k) y[k] = __fadd_rn(y[k], o[k]);
     }
-    if (st.swapped) {
+    if (e.f_lo) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) y[v] = epi_binary(st.fn, o[v], y[v]);
-    } else {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) y[v] = epi_binary(st.fn, y[v], o[v]);
+      for (int k = 0; k < 4; ++k) y[k] = np_maximum(y[k], c.lo);
     }
+    if (e.f_hi) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) y[k] = np_minimum(y[k], c.hi);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (col0 + k < N) y[k] = epi_generic(e, y[k], row, col0 + k);
   }
+  if (c.vec) {
+    if (e.out_acc) *reinterpret_cast<v4i*>(e.out_acc + row * e.ldacc + col0) = acc;
+    if (e.out_f32) *reinterpret_cast<float4*>(e.out_f32 + row * e.ldo + col0) = make_float4(y[0], y[1], y[2], y[3]);
+    if (e.out_i8) {
+      uint32_t packed = 0;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t row = rbase + 8 * (r >> 2) + (r & 3);
-    if (row < M) {
-      if (e->out_acc) e->out_acc[row * e->ldacc + col] = acc[r];
-      epi_store(*e, y[r], row, col);
+      for (int k = 0; k < 4; ++k) packed |= uint32_t(uint8_t(quantize_rcp(y[k], e.out_rxs))) << (8 * k);
+      *reinterpret_cast<uint32_t*>(e.out_i8 + row * e.ldq + col0) = packed;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (col0 + k >= N) break;
+      if (e.out_acc) e.out_acc[row * e.ldacc + col0 + k] = acc[k];
+      epi_store(e, y[k], row, col0 + k);
     }
   }
 }
 
-template <int BM, int BN, int WM, int WN, int AMODE>
+template <int BM, int BN, int WM, int WN, int STAGES, int AMODE, bool FIXED>
 __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, const EpiDev e) {
-  constexpr int NT = WM * WN * 64;
+  constexpr int NW = WM * WN;
   constexpr int TM = BM / WM;
   constexpr int TN = BN / WN;
   constexpr int FM = TM / 32;
   constexpr int FN = TN / 32;
-  constexpr int A_PER_T = BM * 4 / NT;
-  constexpr int B_PER_T = BN * 4 / NT;
+  constexpr int NB = FM * FN;
+  constexpr int A_ROWS_PER_OP = AMODE == A_CONV4 ? 4 : 16;   // rows one wave-wide DMA covers
+  constexpr int A_OPS = BM / A_ROWS_PER_OP / NW;               // A DMAs per wave per K step
+  constexpr int B_OPS = BN / 16 / NW;
+  constexpr int OPS = A_OPS + B_OPS;
+  constexpr int STAGE_BYTES = (BM + BN) * BK;
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32");
-  static_assert(A_PER_T * NT == BM * 4 && B_PER_T * NT == BN * 4, "loader mapping");
+  static_assert(A_OPS * A_ROWS_PER_OP * NW == BM && B_OPS * 16 * NW == BN, "loader mapping");
+  static_assert((STAGES - 2) * OPS < 64, "vmcnt range");
 
-  __shared__ __attribute__((aligned(16))) int8_t lds[2 * (BM + BN) * LDS_STRIDE];
+  __shared__ __attribute__((aligned(1024))) int8_t lds[STAGES * STAGE_BYTES];
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int wm = wave / WN;
-  const int wn = wave % WN;
+  const int wn = wave - wm * WN;
 
-  // XCD-aware tile order: consecutive workgroup ids land on different XCDs
-  // (round-robin over 8), so give each XCD a contiguous run of tiles; the
-  // N-tiles of one M-tile then share that XCD's L2 for their A rows.
+  // XCD-aware tile order: workgroup ids are dealt round-robin to the 8 XCDs,
+  // so give each XCD a contiguous run of tiles; the N-tiles of one M-tile
+  // then share that XCD's L2 for their A rows.
   const int total = g.tiles_m * g.tiles_n;
   int t = blockIdx.x;
   const int full = total & ~7;
@@ -130,175 +202,229 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
   const int64_t m0 = int64_t(tile_m) * BM;
   const int n0 = tile_n * BN;
 
-  // ---- per-thread loader state
-  const int kc = tid & 3;  // which 16-byte chunk of the 64-byte K step
-  int64_t a_row_off[A_PER_T];  // dense: row byte offset; conv: image pixel base
-  int32_t a_ih0[A_PER_T], a_iw0[A_PER_T];
-  bool a_valid[A_PER_T];
+  // ---- A loader state, one entry per DMA this lane takes part in
+  int64_t a_base[A_OPS];   // dense: m*lda + chunk offset; conv: image pixel base
+  int32_t a_ih0[A_OPS], a_iw0[A_OPS], a_k[A_OPS];
+  bool a_ok[A_OPS];
 #pragma unroll
-  for (int i = 0; i < A_PER_T; ++i) {
-    const int64_t m = m0 + (tid >> 2) + i * (NT >> 2);
-    a_valid[i] = m < g.M;
-    if (AMODE == A_DENSE) {
-      a_row_off[i] = m * g.lda;
-      a_ih0[i] = a_iw0[i] = 0;
+  for (int j = 0; j < A_OPS; ++j) {
+    const int slot = (wave * A_OPS + j) * 64 + lane;
+    int row, koff;
+    if constexpr (AMODE == A_CONV4) {
+      row = slot >> 4;
+      const int p = (slot >> 2) & 3;
+      koff = ((p ^ ((row >> 2) & 3)) << 4) + ((slot & 3) << 2);
     } else {
-      const int64_t mm = a_valid[i] ? m : 0;
-      const int64_t ohw = int64_t(g.OH) * g.OW;
-      const int64_t img = mm / ohw;
-      const int32_t rem = static_cast<int32_t>(mm - img * ohw);
+      row = slot >> 2;
+      koff = ((slot & 3) ^ ((row >> 2) & 3)) << 4;
+    }
+    a_k[j] = koff;
+    const int64_t m = m0 + row;
+    a_ok[j] = m < g.M;
+    if constexpr (AMODE == A_DENSE) {
+      a_base[j] = m * g.lda;
+      a_ih0[j] = a_iw0[j] = 0;
+    } else {
+      const int32_t mm = a_ok[j] ? static_cast<int32_t>(m) : 0;
+      const int32_t ohw = g.OH * g.OW;
+      const int32_t img = mm / ohw;
+      const int32_t rem = mm - img * ohw;
       const int32_t oh = rem / g.OW;
       const int32_t ow = rem - oh * g.OW;
-      a_row_off[i] = img * g.H * g.W;
-      a_ih0[i] = oh * g.SH - g.PH;
-      a_iw0[i] = ow * g.SW - g.PW;
+      a_base[j] = int64_t(img) * g.H * g.W;
+      a_ih0[j] = oh * g.SH - g.PH;
+      a_iw0[j] = ow * g.SW - g.PW;
     }
   }
-
-  v4i ra[A_PER_T], rb[B_PER_T];
-
-  auto load_global = [&](int kt) {
-    const int32_t k = kt * BK + kc * 16;
+  // ---- B loader state
+  const int8_t* b_src[B_OPS];
+  bool b_ok[B_OPS];
 #pragma unroll
-    for (int i = 0; i < A_PER_T; ++i) {
-      v4i v = {0, 0, 0, 0};
-      if (AMODE == A_DENSE) {
-        if (a_valid[i] && k < g.lda) v = *reinterpret_cast<const v4i*>(g.a + a_row_off[i] + k);
-      } else if (AMODE == A_CONV16) {
-        if (a_valid[i] && k < g.k_real) {
+  for (int j = 0; j < B_OPS; ++j) {
+    const int slot = (wave * B_OPS + j) * 64 + lane;
+    const int row = slot >> 2;
+    const int koff = ((slot & 3) ^ ((row >> 2) & 3)) << 4;
+    const int n = n0 + row;
+    b_ok[j] = n < g.n_pad;
+    b_src[j] = g.b + int64_t(n) * g.k_pad + koff;
+  }
+
+  // load cursor of A_CONV64: (kernel row, kernel column, 64-channel block) of the next step
+  int l_kh = 0, l_kw = 0, l_cb = 0;
+
+  auto issue = [&](int kt, int stage) {
+    int8_t* As = lds + stage * STAGE_BYTES;
+    int8_t* Bs = As + BM * BK;
+#pragma unroll
+    for (int j = 0; j < A_OPS; ++j) {
+      const void* src = g_zero_page;
+      if constexpr (AMODE == A_DENSE) {
+        const int64_t k = int64_t(kt) * BK + a_k[j];
+        if (a_ok[j] && k < g.lda) src = g.a + a_base[j] + k;
+      } else if constexpr (AMODE == A_CONV64) {
+        const int32_t ih = a_ih0[j] + l_kh * g.DH;
+        const int32_t iw = a_iw0[j] + l_kw * g.DW;
+        if (a_ok[j] && l_kh < g.KH && unsigned(ih) < unsigned(g.H) && unsigned(iw) < unsigned(g.W))
+          src = g.a + (a_base[j] + int64_t(ih) * g.W + iw) * g.C_pad + l_cb * BK + a_k[j];
+      } else if constexpr (AMODE == A_CONV16) {
+        const int32_t k = kt * BK + a_k[j];
+        if (a_ok[j] && k < g.k_real) {
           const int32_t tap = k / g.C_pad;
           const int32_t c0 = k - tap * g.C_pad;
           const int32_t kh = tap / g.KW;
           const int32_t kw = tap - kh * g.KW;
-          const int32_t ih = a_ih0[i] + kh * g.DH;
-          const int32_t iw = a_iw0[i] + kw * g.DW;
-          if (unsigned(ih) < unsigned(g.H) && unsigned(iw) < unsigned(g.W)) {
-            const int64_t pix = a_row_off[i] + int64_t(ih) * g.W + iw;
-            v = *reinterpret_cast<const v4i*>(g.a + pix * g.C_pad + c0);
-          }
+          const int32_t ih = a_ih0[j] + kh * g.DH;
+          const int32_t iw = a_iw0[j] + kw * g.DW;
+          if (unsigned(ih) < unsigned(g.H) && unsigned(iw) < unsigned(g.W))
+            src = g.a + (a_base[j] + int64_t(ih) * g.W + iw) * g.C_pad + c0;
         }
-      } else {  // A_CONV4: 4 taps of one kernel row, 4 channels (one dword) each
+      } else {  // A_CONV4: one dword = one tap (4 channels) of kernel row kh
+        const int32_t k = kt * BK + a_k[j];
         const int32_t kh = k / g.row_bytes;
-        const int32_t kw0 = (k - kh * g.row_bytes) >> 2;
-        const int32_t ih = a_ih0[i] + kh * g.DH;
-        if (a_valid[i] && kh < g.KH && unsigned(ih) < unsigned(g.H)) {
-          const int32_t* rowp = reinterpret_cast<const int32_t*>(g.a) + (a_row_off[i] + int64_t(ih) * g.W);
+        const int32_t kw = (k - kh * g.row_bytes) >> 2;
+        const int32_t ih = a_ih0[j] + kh * g.DH;
+        const int32_t iw = a_iw0[j] + kw * g.DW;
+        if (a_ok[j] && kh < g.KH && kw < g.KW && unsigned(ih) < unsigned(g.H) && unsigned(iw) < unsigned(g.W))
+          src = g.a + (a_base[j] + int64_t(ih) * g.W + iw) * 4;
+      }
+      if constexpr (AMODE == A_CONV4)
+        dma4(src, As + (wave * A_OPS + j) * (A_ROWS_PER_OP * BK));
+      else
+        dma16(src, As + (wave * A_OPS + j) * (A_ROWS_PER_OP * BK));
+    }
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int32_t kw = kw0 + j;
-            const int32_t iw = a_iw0[i] + kw * g.DW;
-            if (kw < g.KW && unsigned(iw) < unsigned(g.W)) v[j] = rowp[iw];
-          }
+    for (int j = 0; j < B_OPS; ++j)
+      dma16(b_ok[j] ? static_cast<const void*>(b_src[j] + int64_t(kt) * BK) : g_zero_page,
+            Bs + (wave * B_OPS + j) * (16 * BK));
+    if constexpr (AMODE == A_CONV64) {
+      if (++l_cb == g.cb_per_tap) {
+        l_cb = 0;
+        if (++l_kw == g.KW) {
+          l_kw = 0;
+          ++l_kh;
         }
       }
-      ra[i] = v;
-    }
-#pragma unroll
-    for (int i = 0; i < B_PER_T; ++i) {
-      const int n = n0 + (tid >> 2) + i * (NT >> 2);
-      v4i v = {0, 0, 0, 0};
-      if (n < g.n_pad) v = *reinterpret_cast<const v4i*>(g.b + int64_t(n) * g.k_pad + k);
-      rb[i] = v;
     }
   };
 
-  auto store_lds = [&](int buf) {
-    int8_t* As = lds + buf * (BM + BN) * LDS_STRIDE;
-    int8_t* Bs = As + BM * LDS_STRIDE;
+  v16i acc[NB];
 #pragma unroll
-    for (int i = 0; i < A_PER_T; ++i)
-      *reinterpret_cast<v4i*>(As + ((tid >> 2) + i * (NT >> 2)) * LDS_STRIDE + kc * 16) = ra[i];
+  for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int i = 0; i < B_PER_T; ++i)
-      *reinterpret_cast<v4i*>(Bs + ((tid >> 2) + i * (NT >> 2)) * LDS_STRIDE + kc * 16) = rb[i];
-  };
+    for (int r = 0; r < 16; ++r) acc[b][r] = 0;
 
-  v16i acc[FM][FN];
+  const int KT = g.k_tiles;
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-
-  load_global(0);
-  store_lds(0);
-  __syncthreads();
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < KT) issue(s, s);
 
   const int frag_row = lane & 31;
-  const int frag_k = (lane >> 5) * 16;
-  for (int kt = 0; kt < g.k_tiles; ++kt) {
-    const bool more = kt + 1 < g.k_tiles;
-    if (more) load_global(kt + 1);
-    const int8_t* As = lds + (kt & 1) * (BM + BN) * LDS_STRIDE;
-    const int8_t* Bs = As + BM * LDS_STRIDE;
+  const int swz = (frag_row >> 2) & 3;
+  for (int kt = 0; kt < KT; ++kt) {
+    if (kt + STAGES - 2 < KT)
+      wait_vmcnt<(STAGES - 2) * OPS>();
+    else
+      wait_vmcnt<0>();
+    block_barrier();
+    if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+    const int8_t* As = lds + (kt % STAGES) * STAGE_BYTES;
+    const int8_t* Bs = As + BM * BK;
+    // every fragment of the step is requested before the first MFMA, so the
+    // LDS latency overlaps the matrix work
+    v4i af[2][FM], bf[2][FN];
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 32) {
-      v4i af[FM], bf[FN];
+    for (int kk = 0; kk < 2; ++kk) {
+      const int pc = ((2 * kk + (lane >> 5)) ^ swz) << 4;
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        af[i] = *reinterpret_cast<const v4i*>(As + (wm * TM + i * 32 + frag_row) * LDS_STRIDE + kk + frag_k);
+        af[kk][i] = *reinterpret_cast<const v4i*>(As + (wm * TM + i * 32 + frag_row) * BK + pc);
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bf[j] = *reinterpret_cast<const v4i*>(Bs + (wn * TN + j * 32 + frag_row) * LDS_STRIDE + kk + frag_k);
+        bf[kk][j] = *reinterpret_cast<const v4i*>(Bs + (wn * TN + j * 32 + frag_row) * BK + pc);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    if (more) store_lds((kt + 1) & 1);
-    __syncthreads();
+          acc[i * FN + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[kk][i], bf[kk][j], acc[i * FN + j], 0, 0, 0);
   }
 
-  // ---- fused epilogue.  32x32 MFMA result layout: lane holds column
-  // (lane & 31) and rows 8*(r/4) + 4*(lane/32) + (r%4), r = 0..15.
+  // ---- fused epilogue.  The int32 tile goes through LDS one 32-row block row
+  // per wave at a time; the whole workgroup then walks those rows with each
+  // thread owning 4 adjacent columns: per-column constants are read once,
+  // operands and results move as 16-byte (f32) / 4-byte (int8) accesses.
+  constexpr int EP_ROWS = WM * 32;
+  constexpr int EP_LD = BN + 4;                     // int32 row stride (16-byte pad)
+  constexpr int CG = BN / 4;                        // 4-column groups per row
+  constexpr int RSTEP = (WM * WN * 64) / CG;        // rows walked concurrently
+  static_assert(EP_ROWS * EP_LD * 4 <= STAGES * STAGE_BYTES, "epilogue staging exceeds LDS");
+  static_assert((WM * WN * 64) % CG == 0, "epilogue thread mapping");
+  int32_t* ep = reinterpret_cast<int32_t*>(lds);
+  const int cgi = threadIdx.x % CG;
+  const int col0 = n0 + cgi * 4;
+  EpiCols4 cols;
+  load_cols4(e, col0, g.N, cols);
+
+#pragma unroll 1
+  for (int pass = 0; pass < FM; ++pass) {
+    block_barrier();   // LDS free: main-loop reads / previous pass's reads are done
 #pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int col = n0 + wn * TN + j * 32 + (lane & 31);
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
-      store_block(&e, acc[i][j], m0 + wm * TM + i * 32 + 4 * (lane >> 5), col, g.M, g.N);
+      for (int r = 0; r < 16; ++r)
+        ep[(wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * EP_LD + wn * TN + j * 32 + (lane & 31)] =
+            acc[j][r];
+    block_barrier();
+    for (int rr = threadIdx.x / CG; rr < EP_ROWS; rr += RSTEP) {
+      const int64_t row = m0 + (rr >> 5) * TM + pass * 32 + (rr & 31);
+      if (row >= g.M || col0 >= g.N) continue;
+      const v4i a = *reinterpret_cast<const v4i*>(ep + rr * EP_LD + cgi * 4);
+      store_row4<FIXED>(e, cols, a, row, col0, g.N);
+    }
+    // rotate the next block row into acc[0 .. FN)
+#pragma unroll
+    for (int b = 0; b + FN < NB; ++b) acc[b] = acc[b + FN];
   }
 }
 
 // ---------------------------------------------------------------- host dispatch
 
-struct TileCfg {
-  int bm, bn;
-};
+template <int BM, int BN, int WM, int WN, int STAGES, int AMODE>
+static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
+  g.tiles_m = static_cast<int32_t>((g.M + BM - 1) / BM);
+  g.tiles_n = (g.N + BN - 1) / BN;
+  const unsigned blocks = static_cast<unsigned>(int64_t(g.tiles_m) * g.tiles_n);
+  if (e.fixed)
+    hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, STAGES, AMODE, true>), dim3(blocks), dim3(WM * WN * 64), 0,
+                       stream, g, e);
+  else
+    hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, STAGES, AMODE, false>), dim3(blocks), dim3(WM * WN * 64), 0,
+                       stream, g, e);
+}
 
 template <int AMODE>
-static int launch(const GemmArgs& g0, const EpiDev& e, hipStream_t stream) {
-  GemmArgs g = g0;
-  // Pick the tile: wide N tiles when N allows, and enough workgroups to
-  // cover the CUs (smaller M tiles for small problems).
-  const int cus = device_cu_count();
-  int bm, bn;
+static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
+  // Tile choice: wide tiles when there are enough of them to cover every CU
+  // (a 256-row tile per CU at least), narrower ones otherwise.
+  const int64_t cus = device_cu_count();
+  const int64_t mt256 = (g.M + 255) / 256;
+  MR_REQUIRE((g.M + 63) / 64 * ((g.N + 31) / 32) < (int64_t(1) << 31), "problem too large");
   if (g.N <= 32) {
-    bm = 64; bn = 32;
+    launch_cfg<64, 32, 2, 1, 4, AMODE>(g, e, stream);
   } else if (g.N <= 64) {
-    bm = ((g.M + 255) / 256 >= cus) ? 256 : 128;
-    bn = 64;
+    if (mt256 >= 2 * cus)
+      launch_cfg<256, 64, 4, 1, 4, AMODE>(g, e, stream);
+    else
+      launch_cfg<128, 64, 2, 1, 4, AMODE>(g, e, stream);
+  } else if (g.N <= 128 || mt256 * ((g.N + 255) / 256) < cus) {
+    if (mt256 * ((g.N + 127) / 128) >= cus)
+      launch_cfg<256, 128, 2, 2, 3, AMODE>(g, e, stream);
+    else
+      launch_cfg<128, 128, 2, 2, 4, AMODE>(g, e, stream);
   } else {
-    bn = 128;
-    bm = ((g.M + 255) / 256) * ((g.N + 127) / 128) >= 2 * cus ? 256 : 128;
-  }
-  g.tiles_m = static_cast<int32_t>((g.M + bm - 1) / bm);
-  g.tiles_n = (g.N + bn - 1) / bn;
-  const int64_t blocks = int64_t(g.tiles_m) * g.tiles_n;
-  MR_REQUIRE(blocks < (int64_t(1) << 31), "problem too large: %lld tiles", (long long)blocks);
-  dim3 grid(static_cast<unsigned>(blocks));
-  if (bm == 64 && bn == 32) {
-    hipLaunchKernelGGL((qgemm_kernel<64, 32, 2, 1, AMODE>), grid, dim3(128), 0, stream, g, e);
-  } else if (bm == 128 && bn == 64) {
-    hipLaunchKernelGGL((qgemm_kernel<128, 64, 2, 1, AMODE>), grid, dim3(128), 0, stream, g, e);
-  } else if (bm == 256 && bn == 64) {
-    hipLaunchKernelGGL((qgemm_kernel<256, 64, 4, 1, AMODE>), grid, dim3(256), 0, stream, g, e);
-  } else if (bm == 128 && bn == 128) {
-    hipLaunchKernelGGL((qgemm_kernel<128, 128, 2, 2, AMODE>), grid, dim3(256), 0, stream, g, e);
-  } else {
-    hipLaunchKernelGGL((qgemm_kernel<256, 128, 2, 2, AMODE>), grid, dim3(256), 0, stream, g, e);
+    launch_cfg<256, 256, 2, 2, 3, AMODE>(g, e, stream);
   }
   MR_LAUNCH_CHECK("qgemm");
   return MR_OK;
@@ -320,7 +446,8 @@ int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int
              (long long)k_pad);
   MR_REQUIRE(n_pad >= N && n_pad % 32 == 0, "mr_qmatmul: n_pad %lld must be >= N and a multiple of 32",
              (long long)n_pad);
-  MR_REQUIRE(N < (int64_t(1) << 30) && k_pad < (int64_t(1) << 30), "mr_qmatmul: N or K too large");
+  MR_REQUIRE(N < (int64_t(1) << 30) && k_pad < (int64_t(1) << 30) && M < (int64_t(1) << 31),
+             "mr_qmatmul: problem too large");
   MR_REQUIRE(mr::aligned16(a) && mr::aligned16(b), "mr_qmatmul: operands must be 16-byte aligned");
   mr::EpiDev e;
   int rc = mr::make_epi(epi, N, true, &e);
@@ -359,14 +486,16 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
   } else {
     MR_REQUIRE(G.c_pad % 16 == 0 && G.c_pad >= G.c, "mr_qconv2d: c_pad %d must be 4 or a multiple of 16 >= c",
                G.c_pad);
-    mode = mr::A_CONV16;
+    mode = G.c_pad % 64 == 0 ? mr::A_CONV64 : mr::A_CONV16;
     k_real = G.kh * G.kw * G.c_pad;
   }
   MR_REQUIRE(k_pad >= k_real && k_pad % 64 == 0, "mr_qconv2d: k_pad %lld must be >= %d and a multiple of 64",
              (long long)k_pad, k_real);
+  MR_REQUIRE(mode != mr::A_CONV64 || k_pad == k_real, "mr_qconv2d: k_pad must equal kh*kw*c_pad");
   MR_REQUIRE(n_pad >= G.o && n_pad % 32 == 0, "mr_qconv2d: n_pad %lld must be >= o and a multiple of 32",
              (long long)n_pad);
-  MR_REQUIRE(int64_t(G.n) * G.h * G.w < (int64_t(1) << 31), "mr_qconv2d: input has too many pixels");
+  MR_REQUIRE(int64_t(G.n) * oh * ow < (int64_t(1) << 31) && int64_t(G.n) * G.h * G.w < (int64_t(1) << 31),
+             "mr_qconv2d: too many pixels");
   MR_REQUIRE(mr::aligned16(x) && mr::aligned16(b), "mr_qconv2d: operands must be 16-byte aligned");
   mr::EpiDev e;
   const int rc = mr::make_epi(epi, G.o, true, &e);
@@ -397,8 +526,13 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
   g.DW = G.dw;
   g.row_bytes = row_bytes;
   g.k_real = k_real;
+  g.cb_per_tap = G.c_pad / 64;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return mode == mr::A_CONV4 ? mr::launch<mr::A_CONV4>(g, e, s) : mr::launch<mr::A_CONV16>(g, e, s);
+  switch (mode) {
+    case mr::A_CONV4: return mr::launch<mr::A_CONV4>(g, e, s);
+    case mr::A_CONV64: return mr::launch<mr::A_CONV64>(g, e, s);
+    default: return mr::launch<mr::A_CONV16>(g, e, s);
+  }
 }
 
 }  // extern "C"

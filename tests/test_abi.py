@@ -1,0 +1,46 @@
+"""The C ABI library loads, exports every entry point include/mira_rocm.h declares,
+and its struct layouts match the ctypes binding (no GPU needed)."""
+import ctypes as C
+import os
+import re
+
+from mira_amd import _lib as L
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "mira_rocm.h")
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mr_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_exports():
+    assert declared_functions() == sorted(L.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_struct_sizes():
+    lib = L.load()
+    assert lib.mr_abi_version() == L.ABI_VERSION
+    assert lib.mr_sizeof(b"mr_epi_step") == C.sizeof(L.EpiStep) == 32
+    assert lib.mr_sizeof(b"mr_epilogue") == C.sizeof(L.Epilogue)
+    assert lib.mr_sizeof(b"mr_conv_geom") == C.sizeof(L.ConvGeom) == 64
+    assert lib.mr_sizeof(b"nope") == -1
+
+
+def test_invalid_arguments_are_rejected_before_any_launch():
+    """Host-side validation returns MR_EINVAL with a message; no device call is made."""
+    lib = L.load()
+    e = L.Epilogue()
+    assert lib.mr_qmatmul(None, 16, None, 64, 32, 4, 8, 16, C.byref(e), None) == 1
+    assert b"NULL" in lib.mr_last_error()
+    assert lib.mr_quantize_rows(None, 1, 1, 1, None, 4, 1.0, None) == 1
+    g = L.ConvGeom(n=1, h=8, w=8, c=3, c_pad=8, o=4, oh=8, ow=8, kh=3, kw=3, sh=1, sw=1, ph=1, pw=1, dh=1, dw=1)
+    assert lib.mr_qconv2d(C.c_void_p(16), C.byref(g), C.c_void_p(16), 64, 32, C.byref(e), None) == 1
+    assert b"c_pad" in lib.mr_last_error()

@@ -1,0 +1,169 @@
+"""Host-side logic of the rocm target on the CPU: the pass/quantizer mirrors, the
+partitioner and fallback, check() decisions, weight packing and broadcast modes.
+Structure tests follow the reference's own (tests/test_passes.py:51-72,
+tests/test_backends.py:40-55)."""
+import numpy as np
+import pytest
+
+from mira_amd import _lib as L
+from mira_amd import models, pack, passes
+from mira_amd.compiler import compile_graph
+from mira_amd.ir import Graph
+from mira_amd.partition import partition
+from mira_amd.quantize import quantize_array, quantize_w8a8
+from mira_amd.target import RocmTarget, _bcast_mode
+from oracle import golden as G
+
+
+def _dense_graph(bias_shape=(4,), relu=True, sub_from_bias=False):
+    g = Graph("t", [], [], [])
+    x = g.input("x", (8, 16))
+    w = g.const(np.random.default_rng(0).standard_normal((16, 4)).astype(np.float32))
+    b = g.const(np.random.default_rng(1).standard_normal(bias_shape).astype(np.float32))
+    y = g.add("matmul", [x, w])
+    y = g.add("sub", [b, y]) if sub_from_bias else g.add("add", [y, b])
+    if relu:
+        y = g.add("relu", [y])
+    g.outputs = [y]
+    return g
+
+
+def test_fusion_builds_epilogue():
+    g = _dense_graph()
+    passes.optimize(g)
+    (op,) = g.compute_ops()
+    assert op.kind == "matmul" and [s[0] for s in op.attrs["epilogue"]] == ["add", "relu"]
+
+
+def test_fusion_respects_operand_order():
+    g = _dense_graph(bias_shape=(8, 4), relu=False, sub_from_bias=True)
+    passes.optimize(g)
+    (op,) = g.compute_ops()
+    assert op.attrs["epilogue"][0][0] == "sub" and op.attrs["epilogue"][0][2] is True
+
+
+def test_fusion_skips_multi_use_results():
+    g = Graph("t", [], [], [])
+    x = g.input("x", (8, 16))
+    h = g.add("matmul", [x, g.const(np.ones((16, 16), np.float32))])
+    g.outputs = [g.add("add", [g.add("relu", [h]), h])]
+    passes.optimize(g)
+    assert "epilogue" not in g.compute_ops()[0].attrs
+
+
+def test_zero_bias_is_simplified_away():
+    g = models.mlp_dense(batch=4)
+    passes.optimize(g)
+    (op,) = g.compute_ops()
+    assert op.kind == "matmul" and "epilogue" not in op.attrs
+
+
+def test_quantizer_matches_oracle():
+    g = models.mlp_mira(batch=4)
+    passes.optimize(g)
+    calib = [{"x": models.normal_batch((4, 784), s)} for s in (2, 3)]
+    want = G.w8a8_attrs(g, calib)
+    wanted = [(op.inputs[0], want[op]) for op in g.ops if op in want]
+    n = quantize_w8a8(g, calib)
+    assert n == 3
+    qops = [op for op in g.ops if op.kind == "qmatmul"]
+    for op, (_x, a) in zip(qops, wanted):
+        assert np.array_equal(op.attrs["q"], a["q"]) and np.array_equal(op.attrs["w_scale"], a["w_scale"])
+        assert op.attrs["epilogue"] == a["epilogue"]
+        assert abs(op.attrs["x_scale"] - a["x_scale"]) <= 1e-6 * a["x_scale"]   # BLAS order differs
+
+
+def test_quantize_array_matches_oracle():
+    w = np.random.default_rng(3).standard_normal((64, 3, 7, 7)).astype(np.float32)
+    for axis in (0, 1):
+        q1, s1 = quantize_array(w.reshape(64, -1) if axis == 1 else w, axis)
+        q2, s2 = G.quantize_array(w.reshape(64, -1) if axis == 1 else w, axis)
+        assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
+
+
+def test_check_decisions():
+    t = RocmTarget()
+    g = models.mlp_mira(batch=4)
+    passes.optimize(g)
+    quantize_w8a8(g, [{"x": models.normal_batch((4, 784), 2)}])
+    reasons = {op.kind: t.check(op) for op in g.compute_ops()}
+    assert reasons["qmatmul"] is None
+    assert "softmax" in reasons["softmax"]
+    gg = Graph("t", [], [], [])
+    x = gg.input("x", (2, 3))
+    m = gg.add("matmul", [x, gg.input("w", (3, 4))])
+    assert "BLAS" in t.check(m.producer)
+    gelu = _dense_graph(relu=False)
+    y = gelu.add("gelu", [gelu.outputs[0]])
+    gelu.outputs = [y]
+    passes.optimize(gelu)
+    quantize_w8a8(gelu, [{"x": models.normal_batch((8, 16), 2)}])
+    assert "not bit-reproducible" in t.check(gelu.compute_ops()[0])
+
+
+def test_partition_falls_back_and_requires_a_fallback_target():
+    g = models.mlp_mira(batch=4)
+    passes.optimize(g)
+    quantize_w8a8(g, [{"x": models.normal_batch((4, 784), 2)}])
+    segs, placement = partition(g, RocmTarget())
+    assert [s.device for s in segs] == ["rocm", "cpu"]
+    soft = next(op for op in g.compute_ops() if op.kind == "softmax")
+    assert placement.device[soft] == "cpu"
+
+    class NoCompile(RocmTarget):
+        def compile(self, g):
+            return object()
+    with pytest.raises(RuntimeError, match="fallback"):
+        compile_graph(g, NoCompile())
+
+
+def test_cost_model_keeps_tiny_segments_on_cpu():
+    g = Graph("t", [], [], [])
+    x = g.input("x", (1, 4, 6, 6))
+    y = g.add("pad", [x], {"pads": ((0, 0), (0, 0), (1, 1), (1, 1)), "value": 0.0})
+    g.outputs = [y]
+    segs, placement = partition(g, RocmTarget())
+    assert [s.device for s in segs] == ["cpu"]
+    segs, _ = partition(g, RocmTarget(), cost_model=False)
+    assert [s.device for s in segs] == ["rocm"]
+
+
+def test_pack_conv_layouts():
+    rng = np.random.default_rng(4)
+    q = rng.integers(-127, 128, (5, 3, 7, 7)).astype(np.int8)
+    b = pack.pack_conv(q, 4)
+    assert b.shape == (32, 256)
+    for o in range(5):
+        for kh in range(7):
+            for kw in range(7):
+                for c in range(3):
+                    assert b[o, kh * 32 + kw * 4 + c] == q[o, c, kh, kw]
+    assert not b[5:].any() and not b[:, 7 * 32:].any()
+    q2 = rng.integers(-127, 128, (40, 24, 3, 3)).astype(np.int8)
+    b2 = pack.pack_conv(q2, 32)
+    assert b2.shape == (64, 320)
+    assert b2[7, (2 * 3 + 1) * 32 + 5] == q2[7, 5, 2, 1] and b2[7, (2 * 3 + 1) * 32 + 30] == 0
+    m = rng.integers(-127, 128, (100, 10)).astype(np.int8)
+    bm = pack.pack_matmul(m)
+    assert bm.shape == (32, 128) and np.array_equal(bm[:10, :100], m.T)
+
+
+def test_broadcast_modes():
+    assert _bcast_mode((), (2, 8, 5, 5), True) == L.BC_SCALAR
+    assert _bcast_mode((8, 1, 1), (2, 8, 5, 5), True) == L.BC_COL
+    assert _bcast_mode((1, 8, 1, 1), (2, 8, 5, 5), True) == L.BC_COL
+    assert _bcast_mode((2, 8, 5, 5), (2, 8, 5, 5), True) == L.BC_FULL
+    assert _bcast_mode((2, 1, 5, 5), (2, 8, 5, 5), True) == L.BC_ROW
+    assert _bcast_mode((5,), (2, 8, 5, 5), True) is None            # broadcasts along W, not channels
+    assert _bcast_mode((4,), (8, 4), False) == L.BC_COL
+    assert _bcast_mode((8, 1), (8, 4), False) == L.BC_ROW
+
+
+def test_model_mac_counts():
+    g = models.resnet18(batch=1)
+    passes.optimize(g)
+    quantize_w8a8(g, peaks=[1.0] * 21)
+    assert models.conv_macs(g) == 1_814_073_344
+    g = models.mlp_50m(batch=1)
+    n_params = sum(op.attrs["value"].size for op in g.ops if op.is_const)
+    assert 54_000_000 < n_params < 54_500_000
