@@ -150,6 +150,19 @@ int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int
 int mr_qconv2d(const int8_t* x, const mr_conv_geom* g, const int8_t* b, int64_t k_pad,
                int64_t n_pad, const mr_epilogue* epi, void* stream);
 
+/* Fused stem: mr_qconv2d of a <= 4-channel input (c_pad == 4, o <= 64,
+ * output width <= 128, weights packed to n_pad >= 64 rows, k_pad <= 256) whose
+ * epilogue result feeds a constant pad (pool_pad_* rows/columns of
+ * pad_value, mira/ops.py:461-470) and maxpool2d(pool_size, pool_stride)
+ * (mira/ops.py:293-296).  Replaces that qconv2d -> pad -> maxpool2d chain;
+ * the convolution result is never stored.  `epi` carries the convolution's
+ * scale and epilogue steps, while its outputs (out_f32/ldo, out_i8/ldq/out_xs)
+ * receive the pooled [n, poh, pow_, o] result in NHWC rows; out_acc must be
+ * NULL. */
+int mr_qconv2d_maxpool(const int8_t* x, const mr_conv_geom* g, const int8_t* b, int64_t k_pad, int64_t n_pad,
+                       const mr_epilogue* epi, int32_t pool_size, int32_t pool_stride, int32_t pool_pad_top,
+                       int32_t pool_pad_left, float pad_value, int32_t poh, int32_t pow_, void* stream);
+
 /* ---- K4a: f32 depthwise conv ------------------------------------------ */
 
 /* Replaces mira/ops.py:265-276 _conv2d_ref for groups == C, one output per

@@ -36,14 +36,18 @@ __global__ void __launch_bounds__(256) dwconv_kernel(const float* __restrict__ x
     const Idx r = pix / Idx(G.ow);
     const int oh = static_cast<int>(r % Idx(G.oh));
     const int64_t img = r / Idx(G.oh);
+    // Loads go to clamped (always valid) addresses and are selected afterwards,
+    // so every tap's load is in flight at once instead of one after another.
     float acc = 0.0f;
     for (int i = 0; i < G.kh; ++i) {
       const int ih = oh * G.sh - G.ph + i * G.dh;
       const bool row_ok = unsigned(ih) < unsigned(G.h);
+      const int ihc = min(max(ih, 0), G.h - 1);
       for (int j = 0; j < G.kw; ++j) {
         const int iw = ow * G.sw - G.pw + j * G.dw;
-        const float xv =
-            (row_ok && unsigned(iw) < unsigned(G.w)) ? x[((img * G.h + ih) * G.w + iw) * G.c + c] : 0.0f;
+        const int iwc = min(max(iw, 0), G.w - 1);
+        const float v = x[((img * G.h + ihc) * G.w + iwc) * G.c + c];
+        const float xv = (row_ok && unsigned(iw) < unsigned(G.w)) ? v : 0.0f;
         acc = __fadd_rn(acc, __fmul_rn(xv, w[(i * G.kw + j) * G.c + c]));
       }
     }
@@ -70,11 +74,12 @@ __global__ void __launch_bounds__(256) maxpool_kernel(const float* __restrict__ 
     float m = 0.0f;
     for (int i = 0; i < size; ++i) {
       const int ih = oy * stride - pt + i;
+      const int ihc = min(max(ih, 0), h - 1);
       for (int j = 0; j < size; ++j) {
         const int iw = ox * stride - pl + j;
-        const float v = (unsigned(ih) < unsigned(h) && unsigned(iw) < unsigned(w))
-                            ? x[((img * h + ih) * w + iw) * c + ch]
-                            : pad_value;
+        const int iwc = min(max(iw, 0), w - 1);
+        const float ld = x[((img * h + ihc) * w + iwc) * c + ch];   // unpredicated: all taps in flight
+        const float v = (unsigned(ih) < unsigned(h) && unsigned(iw) < unsigned(w)) ? ld : pad_value;
         m = (i == 0 && j == 0) ? v : np_maximum(m, v);
       }
     }

@@ -79,17 +79,18 @@ __device__ __forceinline__ int8_t quantize_rcp(float y, double rxs) {
   return static_cast<int8_t>(static_cast<int>(t));
 }
 
-// NumPy float32 maximum/minimum on x86: NaN in either operand propagates, and
-// on equality (including +0 vs -0) the second operand is returned.
+// NumPy float32 maximum/minimum on x86: NaN in either operand propagates
+// (the first one if both are NaN), and on equality (including +0 vs -0) the
+// second operand is returned.  Written as selects so no lane branches.
 __device__ __forceinline__ float np_maximum(float a, float b) {
-  if (a != a) return a;
-  if (b != b) return b;
-  return a > b ? a : b;
+  float r = a > b ? a : b;
+  r = b != b ? b : r;
+  return a != a ? a : r;
 }
 __device__ __forceinline__ float np_minimum(float a, float b) {
-  if (a != a) return a;
-  if (b != b) return b;
-  return a < b ? a : b;
+  float r = a < b ? a : b;
+  r = b != b ? b : r;
+  return a != a ? a : r;
 }
 
 // One epilogue step (mira/ops.py:192-199): fn(acc, other), or fn(other, acc)

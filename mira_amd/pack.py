@@ -47,8 +47,9 @@ def conv_row_bytes(kw: int) -> int:
     return 16 * ((kw + 3) // 4)
 
 
-def pack_conv(q: np.ndarray, c_pad: int) -> np.ndarray:
-    """int8 weights q[O, C, KH, KW] (OIHW, axis 0 = output channel) -> b[n_pad, k_pad]."""
+def pack_conv(q: np.ndarray, c_pad: int, min_rows: int = 0) -> np.ndarray:
+    """int8 weights q[O, C, KH, KW] (OIHW, axis 0 = output channel) -> b[n_pad, k_pad]
+    (n_pad at least min_rows)."""
     o, c, kh, kw = q.shape
     if c_pad == 4:
         rb = conv_row_bytes(kw)
@@ -59,7 +60,7 @@ def pack_conv(q: np.ndarray, c_pad: int) -> np.ndarray:
         body = np.zeros((o, kh, kw, c_pad), np.int8)
         body[..., :c] = q.transpose(0, 2, 3, 1)
         body = body.reshape(o, kh * kw * c_pad)
-    out = np.zeros((roundup(o, N_STEP), roundup(body.shape[1], K_STEP)), np.int8)
+    out = np.zeros((max(roundup(o, N_STEP), min_rows), roundup(body.shape[1], K_STEP)), np.int8)
     out[:o, :body.shape[1]] = body
     return out
 

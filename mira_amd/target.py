@@ -202,6 +202,8 @@ class RocmExecutable:
         self.need_f32: set = set(g.outputs)
         self.need_i8: dict[ir.Value, list[float]] = {}
         self.folded_pads: set = set()
+        self.fused_stem: dict = {}          # maxpool op -> (qconv2d op, pad op) run as one kernel
+        self.skip: set = set()
         for op in g.ops:
             if op.is_constant_like:
                 continue
@@ -215,7 +217,12 @@ class RocmExecutable:
             elif op.kind == "maxpool2d" and self._foldable_pad(op.inputs[0]):
                 pad_op = op.inputs[0].producer
                 self.folded_pads.add(pad_op)
-                self.need_f32.add(pad_op.inputs[0])
+                conv = pad_op.inputs[0].producer
+                if self._stem_fusable(conv, pad_op, op):
+                    self.fused_stem[op] = (conv, pad_op)
+                    self.skip.add(conv)
+                else:
+                    self.need_f32.add(pad_op.inputs[0])
             else:
                 for v in op.inputs:
                     if v not in self.consts or op.kind != "conv2d" or v is op.inputs[0]:
@@ -229,14 +236,28 @@ class RocmExecutable:
         for v in g.inputs:
             self._new_dv(v, with_i8=True)
         for op in g.ops:
-            if op.is_constant_like:
-                continue
-            if op in self.folded_pads:
+            if op.is_constant_like or op in self.folded_pads or op in self.skip:
                 continue
             getattr(self, f"_emit_{op.kind}")(op)
         for v in g.outputs:
             if v in self.consts and v not in self.dv:
                 self._const_dv(v)
+
+    def _stem_fusable(self, conv: Optional[ir.Op], pad_op: ir.Op, pool: ir.Op) -> bool:
+        """Can qconv2d -> pad -> maxpool2d run as mr_qconv2d_maxpool (the convolution is never stored)?"""
+        if conv is None or conv.kind != "qconv2d" or self.target.debug_acc:
+            return False
+        r = conv.result
+        if r in self.g.outputs or len(self.users.get(r, [])) != 1:
+            return False
+        n, c, h, w = conv.inputs[0].type.shape
+        o, _, kh, kw = conv.attrs["q"].shape
+        ow = r.type.shape[3]
+        row_bytes = pack.conv_row_bytes(kw)
+        pads = tuple(tuple(x) for x in pad_op.attrs["pads"])
+        size = pool.attrs["size"]
+        return (c <= 4 and o <= 64 and ow <= 128 and row_bytes <= 32 and pack.roundup(kh * row_bytes, 64) <= 256
+                and pads[2][0] < size and pads[3][0] < size and pool.result.type.shape[3] <= 64)
 
     def _foldable_pad(self, v: ir.Value) -> bool:
         p = v.producer
@@ -450,7 +471,38 @@ class RocmExecutable:
             lib.mr_dwconv2d_f32(xt.data_ptr(), C.byref(geom), wdev.data_ptr(), C.byref(e), s), "mr_dwconv2d_f32"))
         self._finish_i8(out, fused)
 
+    def _emit_fused_stem(self, op: ir.Op) -> None:
+        conv, pad_op = self.fused_stem[op]
+        a = conv.attrs
+        x = self._src(conv.inputs[0])
+        q = np.asarray(a["q"], np.int8)
+        n, c, h, w = conv.inputs[0].type.shape
+        o, _, kh, kw = q.shape
+        (sh, sw), (ph, pw), (dh, dw), _ = conv_params(a)
+        _, _, oh, ow = conv.result.type.shape
+        xs = _f32key(a["x_scale"])
+        xq, cp = x.i8[xs] if xs in x.i8 else self._quantize_to(x, xs)
+        b = self._upload(pack.pack_conv(q, cp, min_rows=64))
+        scale = self._upload(pack.combined_scale(a["x_scale"], a["w_scale"]))
+        geom = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=cp, o=o, oh=oh, ow=ow, kh=kh, kw=kw, sh=sh, sw=sw, ph=ph,
+                          pw=pw, dh=dh, dw=dw)
+        self.keep.append(geom)
+        out = self._new_dv(op.result)
+        e, fused = self._epilogue(conv, out, True, 1, scale)
+        pads = tuple(tuple(p) for p in pad_op.attrs["pads"])
+        value = float(np.asarray(pad_op.attrs.get("value", 0)).astype(np.float32))
+        size, stride = op.attrs["size"], op.attrs["stride"]
+        _, _, poh, pw_ = op.result.type.shape
+        lib, kp, npad = self.lib, b.shape[1], b.shape[0]
+        pt, pl = pads[2][0], pads[3][0]
+        self._add("qconv2d_maxpool", lambda s: L.check(lib.mr_qconv2d_maxpool(
+            xq.data_ptr(), C.byref(geom), b.data_ptr(), kp, npad, C.byref(e), size, stride, pt, pl, value, poh, pw_,
+            s), "mr_qconv2d_maxpool"))
+        self._finish_i8(out, fused)
+
     def _emit_maxpool2d(self, op: ir.Op) -> None:
+        if op in self.fused_stem:
+            return self._emit_fused_stem(op)
         v = op.inputs[0]
         pt = pl = 0
         pad_value = 0.0

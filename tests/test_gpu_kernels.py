@@ -279,3 +279,48 @@ def test_pad_and_layouts(lib):
     assert bits_equal(back.cpu().numpy(), x)
     want = G.pad([x], {"pads": ((0, 0), (0, 0), (1, 2), (0, 1)), "value": -7.5}).transpose(0, 2, 3, 1)
     assert bits_equal(padded.cpu().numpy(), want)
+
+
+# ---------------------------------------------------------------- fused stem (conv -> pad -> maxpool)
+
+@pytest.mark.parametrize("n,c,h,o,k,s,p,pool,pst,ppad,pval", [
+    (2, 3, 224, 64, 7, 2, 3, 3, 2, 1, float("-inf")),   # ResNet-18 stem
+    (3, 3, 37, 32, 3, 2, 1, 3, 2, 1, float("-inf")),    # odd sizes, 3 taps per row
+    (2, 1, 30, 16, 5, 1, 2, 2, 2, 0, 0.0),              # no pool padding
+    (2, 4, 29, 48, 7, 2, 3, 3, 2, 1, 0.25),             # finite pad value
+])
+def test_qconv2d_maxpool(lib, n, c, h, o, k, s, p, pool, pst, ppad, pval):
+    torch = _torch()
+    rng = np.random.default_rng(h + o)
+    x = rng.uniform(-1, 1, (n, c, h, h)).astype(np.float32)
+    wt = rng.standard_normal((o, c, k, k)).astype(np.float32)
+    q, ws = G.quantize_array(wt, 0)
+    xs = float(np.abs(x).max()) / 127
+    bias = (rng.standard_normal((o, 1, 1)) * 0.3).astype(np.float32)
+    attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "stride": (s, s), "padding": (p, p),
+             "epilogue": (("add", 1, False), ("relu", None, False))}
+    conv = G.qconv2d([x, bias], attrs)
+    padded = G.pad([conv], {"pads": ((0, 0), (0, 0), (ppad, ppad), (ppad, ppad)), "value": pval})
+    want = G.maxpool2d([padded], {"size": pool, "stride": pst})
+    oh = conv.shape[2]
+    poh = want.shape[2]
+    next_xs = float(want.max()) / 127
+    cp = 4
+    xq = empty((n, h, h, cp), torch.int8)
+    L.check(lib.mr_quantize_nchw_nhwc(T(x).data_ptr(), n, c, h, h, xq.data_ptr(), cp, xs, stream()), "q")
+    b = T(pack.pack_conv(q, cp, min_rows=64))
+    scale = T(pack.combined_scale(xs, ws))
+    g = L.ConvGeom(n=n, h=h, w=h, c=c, c_pad=cp, o=o, oh=oh, ow=oh, kh=k, kw=k, sh=s, sw=s, ph=p, pw=p, dh=1, dw=1)
+    M = n * poh * poh
+    y = empty((M, o), torch.float32)
+    ocp = pack.c_pad_for(o)
+    yq = empty((M, ocp), torch.int8)
+    bt = T(bias.reshape(o))
+    e = epilogue([("add", L.BC_COL, bt, 0, False), ("relu", 0, None, 0, False)], scale=scale, out_f32=y, ldo=o,
+                 out_i8=yq, ldq=ocp, xs=next_xs)
+    L.check(lib.mr_qconv2d_maxpool(xq.data_ptr(), C.byref(g), b.data_ptr(), b.shape[1], b.shape[0], C.byref(e),
+                                   pool, pst, ppad, ppad, pval, poh, poh, stream()), "mr_qconv2d_maxpool")
+    sync()
+    to_rows = lambda a: a.transpose(0, 2, 3, 1).reshape(M, o)
+    assert bits_equal(y.cpu().numpy(), to_rows(want))
+    assert bits_equal(yq.cpu().numpy()[:, :o], to_rows(G.quantize_activation(want, next_xs)).astype(np.int8))

@@ -126,3 +126,15 @@ def test_resnet18_batch256_rows():
 
 def test_mlp50m_batch4096_rows():
     _rows_match_small_run(models.mlp_50m, 4096, [0, 1234, 4095], 0, (2, 3), "normal", (4096,))
+
+
+def test_resnet18_batch2_fused_stem():
+    """Without debug accumulators the stem conv, pad and max pool run as one kernel."""
+    g, _ = _quantized(models.resnet18, 2, 0, (11, 12), dist="uniform")
+    runner = compile_graph(g, RocmTarget())
+    exe = runner.segments[0].executable
+    assert exe.kernel_counts.get("qconv2d_maxpool") == 1 and "maxpool2d" not in exe.kernel_counts
+    x = models.image_batch((2, 3, 224, 224), 5)
+    (got,) = runner.run_list([x])
+    (want,) = G.run_graph(g, {"x": x})
+    assert bits_equal(got, want)
