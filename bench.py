@@ -71,6 +71,74 @@ def cpu_baseline(peaks, macs_per_image: int) -> dict:
                       "(int64 matmul, per-tap f32 einsum convs), median of 3 after 1 warm-up"}
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qconv2d_resnet18_b256_traffic.txt")
+
+
+def measured_traffic(batch: int):
+    """HBM bytes per qconv2d launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated) from the
+    committed counter summary of this workload, or None if there is none for this batch."""
+    if batch != 256 or not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        if line.startswith("qconv2d_hbm_bytes_per_launch:"):
+            return int(float(line.split(":")[1]))
+    return None
+
+
+def copy_calibration() -> int:
+    """A plain 1 GiB device-to-device copy, 3 times: FETCH_SIZE / WRITE_SIZE read for it
+    give the factor from counter units to bytes."""
+    import torch
+    n = 1 << 28
+    x = torch.ones(n, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    log(f"copied {4 * n} bytes x3")
+    return 0
+
+
+def summarize_counters(d: str) -> int:
+    """Summarize rocprofv3 --pmc CSV output of bench.py and of --copy-calibration.
+
+    d/fetch, d/write: `rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE --output-format csv -- python3 bench.py ...`
+    d/cfetch, d/cwrite: the same counters over `python3 bench.py --copy-calibration`.
+    Counters are KiB per dispatch; each is scaled by (bytes copied) / (what it reads for the copy)."""
+    import csv
+    import collections
+
+    def rows(sub):
+        p = os.path.join(d, sub, "run_counter_collection.csv")
+        return list(csv.DictReader(open(p)))
+
+    copy_kib = (4 << 28) / 1024
+    ff = copy_kib / float(rows("cfetch")[-1]["Counter_Value"])
+    wf = copy_kib / float(rows("cwrite")[-1]["Counter_Value"])
+    per = collections.defaultdict(lambda: [0, 0.0, 0.0])
+    for sub, fac, slot in (("fetch", ff, 1), ("write", wf, 2)):
+        for r in rows(sub):
+            k = r["Kernel_Name"]
+            per[k][slot] += float(r["Counter_Value"]) * 1024 * fac
+            if slot == 1:
+                per[k][0] += 1
+    print(f"copy calibration: FETCH_SIZE x{ff:.4f}, WRITE_SIZE x{wf:.4f} (1 GiB copy)")
+    print(f"{'kernel':72s} {'launches':>8s} {'fetch MB/launch':>16s} {'write MB/launch':>16s}")
+    conv_n, conv_b = 0, 0.0
+    for k, (n, f, w) in sorted(per.items(), key=lambda kv: -(kv[1][1] + kv[1][2])):
+        if "rocclr" in k or n == 0:
+            continue
+        print(f"{k[:72]:72s} {n:8d} {f / n / 1e6:16.2f} {w / n / 1e6:16.2f}")
+        targs = k[k.find("<") + 1:k.find(">")].split(",") if "qgemm_kernel<" in k else []
+        if len(targs) >= 6 and int(targs[5]) != 0:          # A operand mode 0 = dense matmul
+
+            conv_n += n
+            conv_b += f + w
+    if conv_n:
+        print(f"qconv2d_hbm_bytes_per_launch: {conv_b / conv_n:.0f}")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -78,7 +146,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true", help="run the plain copy used to scale counters")
+    ap.add_argument("--summarize-counters", metavar="DIR", help="summarize rocprofv3 --pmc CSV output in DIR")
     args = ap.parse_args()
+    if args.summarize_counters:
+        return summarize_counters(args.summarize_counters)
+    if args.copy_calibration:
+        return copy_calibration()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the batch would shard by "
               "data parallelism; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
@@ -92,8 +166,6 @@ def main() -> int:
     t0 = time.perf_counter()
     g, peaks = build(args.batch)
     macs = models.conv_macs(g)
-    conv_macs = sum(int(np.prod(op.result.type.shape)) * int(np.prod(op.attrs["q"].shape[1:]))
-                    for op in g.ops if op.kind == "qconv2d")
     runner = compile_graph(g, RocmTarget())
     (seg,) = runner.segments
     exe = seg.executable
@@ -132,8 +204,21 @@ def main() -> int:
             per_kind[name] = per_kind.get(name, 0.0) + a.elapsed_time(b) / reps
     conv_ms = per_kind.get("qconv2d", 0.0)
     n_conv = exe.kernel_counts.get("qconv2d", 0)
-    conv_tops = 2 * conv_macs / (conv_ms * 1e-3) / 1e12
+    conv_cost = [(b, o) for name, b, o in exe.launch_cost if name == "qconv2d"]
+    conv_tops = sum(o for _, o in conv_cost) / (conv_ms * 1e-3) / 1e12
+    conv_alg_bytes = sum(b for b, _ in conv_cost) / max(1, len(conv_cost))
     log("per-kind ms/step: " + ", ".join(f"{k} {v:.3f}" for k, v in sorted(per_kind.items(), key=lambda kv: -kv[1])))
+
+    # PCIe-inclusive: host f32 input in, host logits out (Executable.run), 3 runs, median
+    feeds = {g.inputs[0]: x}
+    io_ms = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        exe.run(feeds)
+        io_ms.append(1e3 * (time.perf_counter() - t1))
+    io_ms = float(np.median(io_ms))
+    log(f"run() with host input/output copies: {io_ms:.3f} ms")
 
     tops = 2 * macs / (ms * 1e-3) / 1e12
     out = {
@@ -145,6 +230,7 @@ def main() -> int:
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
         "ms_per_inference": round(ms / args.batch, 5),
+        "ms_per_step_host_io": round(io_ms, 3),
         "pct_of_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
         "higher_is_better": True,
         "scaling": "weak",
@@ -154,10 +240,12 @@ def main() -> int:
         "config": {"workload": "resnet18_w8a8", "batch": args.batch, "input": f"f32[{args.batch},3,224,224] U(0,1)",
                    "weights": "random Kaiming-normal, BN folded", "int8_macs_per_image": macs // args.batch,
                    "calibration": "2 batches of 2 images U(0,1)"},
-        "roofline": {"bound": "mfma", "kernel": "qconv2d (implicit GEMM, all 20 convs)",
+        "roofline": {"bound": "mfma", "kernel": "qconv2d implicit GEMM (19 convs; the stem conv runs fused with its max pool)",
                      "achieved": round(conv_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
-                     "frac": round(conv_tops / INT8_PEAK_TOPS, 4), "traffic": None,
-                     "launches_per_step": n_conv, "ms_per_step": round(conv_ms, 4)},
+                     "frac": round(conv_tops / INT8_PEAK_TOPS, 4), "traffic": measured_traffic(args.batch),
+                     "algorithmic_bytes_per_launch": int(conv_alg_bytes),
+                     "launches_per_step": n_conv, "ms_per_step": round(conv_ms, 4),
+                     "us_per_launch": round(1e3 * conv_ms / max(1, n_conv), 2)},
     }
     if not args.no_cpu_baseline:
         log("timing the CPU golden model on a 2-image sample ...")

@@ -24,6 +24,10 @@ namespace mr {
 void set_error(const char* fmt, ...);
 int device_cu_count();
 
+// Largest contraction length whose int32 accumulator cannot overflow:
+// K * 127 * 127 <= 2^31 - 1 (both operands are clipped to [-127, 127]).
+constexpr int64_t MAX_EXACT_K = 133144;
+
 }  // namespace mr
 
 #define MR_REQUIRE(cond, ...)            \

@@ -448,6 +448,8 @@ int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int
              (long long)n_pad);
   MR_REQUIRE(N < (int64_t(1) << 30) && k_pad < (int64_t(1) << 30) && M < (int64_t(1) << 31),
              "mr_qmatmul: problem too large");
+  MR_REQUIRE(K <= mr::MAX_EXACT_K, "mr_qmatmul: K %lld > %lld: int32 accumulation could overflow", (long long)K,
+             (long long)mr::MAX_EXACT_K);
   MR_REQUIRE(mr::aligned16(a) && mr::aligned16(b), "mr_qmatmul: operands must be 16-byte aligned");
   mr::EpiDev e;
   int rc = mr::make_epi(epi, N, true, &e);
@@ -496,6 +498,8 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
              (long long)n_pad);
   MR_REQUIRE(int64_t(G.n) * oh * ow < (int64_t(1) << 31) && int64_t(G.n) * G.h * G.w < (int64_t(1) << 31),
              "mr_qconv2d: too many pixels");
+  MR_REQUIRE(int64_t(G.c) * G.kh * G.kw <= mr::MAX_EXACT_K, "mr_qconv2d: c*kh*kw > %lld: int32 accumulation could "
+             "overflow", (long long)mr::MAX_EXACT_K);
   MR_REQUIRE(mr::aligned16(x) && mr::aligned16(b), "mr_qconv2d: operands must be 16-byte aligned");
   mr::EpiDev e;
   const int rc = mr::make_epi(epi, G.o, true, &e);

@@ -188,6 +188,7 @@ class RocmExecutable:
         self.dv: dict[ir.Value, DevValue] = {}
         self.acc: dict[ir.Value, object] = {}      # debug int32 accumulators per q-op result
         self.kernel_counts: dict[str, int] = {}
+        self.launch_cost: list[tuple[str, int, int]] = []
         self.const_bytes = 0
         self._plan()
 
@@ -233,8 +234,9 @@ class RocmExecutable:
                 r = op.result
                 if r in self.need_f32 or r in self.need_i8:
                     self.need_f32.add(op.inputs[0])
+        self.staging: dict[ir.Value, object] = {}
         for v in g.inputs:
-            self._new_dv(v, with_i8=True)
+            self._emit_input(v)
         for op in g.ops:
             if op.is_constant_like or op in self.folded_pads or op in self.skip:
                 continue
@@ -281,6 +283,35 @@ class RocmExecutable:
         self.dv[v] = d
         return d
 
+    def _emit_input(self, v: ir.Value) -> None:
+        """A segment input lives on the device as f32 in the graph's own layout (NCHW for
+        images); the launch list starts by building the copies the kernels read from it: the
+        NHWC f32 copy and the int8 copies its q-op consumers need (their quantize_activation,
+        mira/ops.py:602-603)."""
+        torch = _t()
+        lib = self.lib
+        stage = torch.empty(v.type.shape, dtype=torch.float32, device=self.dev)
+        self.staging[v] = stage
+        d = self._new_dv(v, with_i8=True)
+        if d.nhwc:
+            n, c, h, w = v.type.shape
+            if d.f32 is not None:
+                dst = d.f32
+                self._add("input", lambda s: L.check(lib.mr_nchw_to_nhwc_f32(stage.data_ptr(), n, c, h, w,
+                                                                             dst.data_ptr(), s), "mr_nchw_to_nhwc_f32"))
+            for xs, (q, cp) in d.i8.items():
+                self._add("input", lambda s, q=q, cp=cp, xs=xs: L.check(
+                    lib.mr_quantize_nchw_nhwc(stage.data_ptr(), n, c, h, w, q.data_ptr(), cp, xs, s),
+                    "mr_quantize_nchw_nhwc"))
+        else:
+            if d.f32 is not None:
+                d.f32 = stage.reshape(d.f32.shape)       # same layout: the kernels read the input itself
+            rows, cols = d.rows, d.cols
+            for xs, (q, ld) in d.i8.items():
+                self._add("input", lambda s, q=q, ld=ld, xs=xs: L.check(
+                    lib.mr_quantize_rows(stage.data_ptr(), rows, cols, cols, q.data_ptr(), ld, xs, s),
+                    "mr_quantize_rows"))
+
     def _upload(self, arr: np.ndarray, dtype=None):
         torch = _t()
         a = np.ascontiguousarray(arr if dtype is None else arr.astype(dtype))
@@ -313,9 +344,26 @@ class RocmExecutable:
             return self._const_dv(v)
         return self.dv[v]
 
-    def _add(self, name: str, fn: Callable[[int], None]) -> None:
+    def _add(self, name: str, fn: Callable[[int], None], nbytes: int = 0, nops: int = 0) -> None:
+        """Append a launch; nbytes/nops are its algorithmic HBM bytes and integer ops (each
+        operand read once, each result written once; 2 ops per multiply-accumulate)."""
         self.launches.append((name, fn))
+        self.launch_cost.append((name, int(nbytes), int(nops)))
         self.kernel_counts[name] = self.kernel_counts.get(name, 0) + 1
+
+    @staticmethod
+    def _epi_bytes(e, rows: int, cols: int) -> int:
+        """Bytes the epilogue moves: full-shape operands read, f32/int8 results written."""
+        n = 8 * cols if e.scale else 0
+        for i in range(e.n_steps):
+            st = e.steps[i]
+            if st.fn != L.EPI_FN["relu"]:
+                n += {L.BC_SCALAR: 4, L.BC_COL: 4 * cols, L.BC_ROW: 4 * rows, L.BC_FULL: 4 * rows * cols}[st.mode]
+        if e.out_f32:
+            n += 4 * rows * cols
+        if e.out_i8:
+            n += rows * cols
+        return n
 
     # ---------------------------------------------------------------- int8 copies
 
@@ -418,7 +466,8 @@ class RocmExecutable:
         M = out.rows
         lib, kp, npad = self.lib, b.shape[1], b.shape[0]
         self._add("qmatmul", lambda s: L.check(
-            lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), kp, npad, M, N, K, C.byref(e), s), "mr_qmatmul"))
+            lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), kp, npad, M, N, K, C.byref(e), s), "mr_qmatmul"),
+            nbytes=M * K + K * N + self._epi_bytes(e, M, N), nops=2 * M * N * K)
         self._finish_i8(out, fused)
 
     def _emit_qconv2d(self, op: ir.Op) -> None:
@@ -446,8 +495,10 @@ class RocmExecutable:
         if acc is not None:
             e.out_acc, e.ldacc = acc.data_ptr(), o
         lib, kp, npad = self.lib, b.shape[1], b.shape[0]
+        rows = n * oh * ow
         self._add("qconv2d", lambda s: L.check(
-            lib.mr_qconv2d(xq.data_ptr(), C.byref(geom), b.data_ptr(), kp, npad, C.byref(e), s), "mr_qconv2d"))
+            lib.mr_qconv2d(xq.data_ptr(), C.byref(geom), b.data_ptr(), kp, npad, C.byref(e), s), "mr_qconv2d"),
+            nbytes=n * h * w * c + o * c * kh * kw + self._epi_bytes(e, rows, o), nops=2 * rows * o * c * kh * kw)
         self._finish_i8(out, fused)
 
     def _emit_conv2d(self, op: ir.Op) -> None:
@@ -497,7 +548,8 @@ class RocmExecutable:
         pt, pl = pads[2][0], pads[3][0]
         self._add("qconv2d_maxpool", lambda s: L.check(lib.mr_qconv2d_maxpool(
             xq.data_ptr(), C.byref(geom), b.data_ptr(), kp, npad, C.byref(e), size, stride, pt, pl, value, poh, pw_,
-            s), "mr_qconv2d_maxpool"))
+            s), "mr_qconv2d_maxpool"), nbytes=n * h * w * c + o * c * kh * kw + self._epi_bytes(e, n * poh * pw_, o),
+            nops=2 * n * oh * ow * o * c * kh * kw)
         self._finish_i8(out, fused)
 
     def _emit_maxpool2d(self, op: ir.Op) -> None:
@@ -602,35 +654,19 @@ class RocmExecutable:
     # ---------------------------------------------------------------- run
 
     def upload(self, feeds: dict) -> None:
-        """Copy segment inputs to the device and build their device copies (queued on the stream)."""
+        """Copy the segment inputs (host arrays, the graph's layout) into their device buffers."""
         torch = _t()
-        stream = torch.cuda.current_stream(self.dev).cuda_stream
-        self._staging = []
         for v in self.g.inputs:
-            arr = np.ascontiguousarray(np.asarray(feeds[v]).astype(np.float32))
-            host = torch.from_numpy(arr)
-            d = self.dv[v]
-            if d.nhwc:
-                n, c, h, w = v.type.shape
-                stage = host.to(self.dev, non_blocking=False)
-                self._staging.append(stage)
-                if d.f32 is not None:
-                    L.check(self.lib.mr_nchw_to_nhwc_f32(stage.data_ptr(), n, c, h, w, d.f32.data_ptr(), stream),
-                            "mr_nchw_to_nhwc_f32")
-                for xs, (q, cp) in d.i8.items():
-                    L.check(self.lib.mr_quantize_nchw_nhwc(stage.data_ptr(), n, c, h, w, q.data_ptr(), cp, xs,
-                                                           stream), "mr_quantize_nchw_nhwc")
-            else:
-                stage = host.to(self.dev).reshape(d.rows, d.cols)
-                self._staging.append(stage)
-                if d.f32 is not None:
-                    d.f32.copy_(stage.reshape(d.f32.shape))
-                for xs, (q, ld) in d.i8.items():
-                    L.check(self.lib.mr_quantize_rows(stage.data_ptr(), d.rows, d.cols, d.cols, q.data_ptr(), ld,
-                                                      xs, stream), "mr_quantize_rows")
+            arr = np.ascontiguousarray(np.asarray(feeds[v]).astype(np.float32)).reshape(v.type.shape)
+            self.staging[v].copy_(torch.from_numpy(arr), non_blocking=False)
+
+    def device_input(self, v: ir.Value):
+        """The device f32 buffer (graph layout) that `launch` reads segment input v from."""
+        return self.staging[v]
 
     def launch(self) -> None:
-        """Queue every kernel of the segment on the current stream (inputs already uploaded)."""
+        """Queue every kernel of the segment on the current stream, starting from the f32 inputs
+        already on the device (quantizing them is part of the work)."""
         stream = _t().cuda.current_stream(self.dev).cuda_stream
         for _name, fn in self.launches:
             fn(stream)

@@ -167,3 +167,47 @@ def test_model_mac_counts():
     g = models.mlp_50m(batch=1)
     n_params = sum(op.attrs["value"].size for op in g.ops if op.is_const)
     assert 54_000_000 < n_params < 54_500_000
+
+
+def _quantize_by_division(y, xs):
+    return np.clip(np.rint(np.float32(y) / np.float32(xs)), -127, 127)
+
+
+def _quantize_by_f64_reciprocal(y, xs):
+    """What the GEMM epilogues compute: f32(f64(y) * f64(1/f64(xs))), then rint and clip."""
+    q = (y.astype(np.float64) * (1.0 / xs.astype(np.float64))).astype(np.float32)
+    return q, np.clip(np.rint(q), -127, 127)
+
+
+@np.errstate(over="ignore", divide="ignore", invalid="ignore")
+def test_requant_reciprocal_is_exact():
+    """The fused requant replaces the IEEE f32 division of mira/ops.py:602-603 by a
+    multiply with a double-precision reciprocal.  For normal-range quotients the f32
+    result is the correctly rounded quotient (no f32 midpoint is an exact quotient of
+    two 24-bit significands, and the f64 error is far below the distance to one);
+    subnormal quotients may differ in the last place but quantize to 0 either way."""
+    rng = np.random.default_rng(0)
+    n = 4_000_000
+    y = (rng.standard_normal(n) * np.exp2(rng.integers(-30, 30, n))).astype(np.float32)
+    xs = (rng.random(n) * np.exp2(rng.integers(-20, 20, n)) + 1e-30).astype(np.float32)
+    q64, r64 = _quantize_by_f64_reciprocal(y, xs)
+    q32 = y / xs
+    normal = np.abs(q32) >= np.float32(2.0 ** -126)
+    assert np.array_equal(q64[normal], q32[normal])
+    assert np.array_equal(r64, _quantize_by_division(y, xs))
+    # exact rint ties: y = (k + 1/2) * xs whenever that product is an f32
+    k = rng.integers(-130, 130, n).astype(np.float64) + 0.5
+    xs2 = rng.random(n).astype(np.float32) * np.float32(0.05) + np.float32(1e-3)
+    y2 = (k * xs2.astype(np.float64)).astype(np.float32)
+    exact = y2.astype(np.float64) == k * xs2.astype(np.float64)
+    assert exact.sum() > 1000
+    q64, r64 = _quantize_by_f64_reciprocal(y2[exact], xs2[exact])
+    assert np.array_equal(r64, _quantize_by_division(y2[exact], xs2[exact]))
+    assert np.array_equal(q64, np.float32(k[exact]))
+    # extremes
+    f = np.finfo(np.float32)
+    ys = np.array([0.0, -0.0, f.max, -f.max, f.tiny, np.inf, -np.inf, 1e-45, 127.5, -127.5, 126.5], np.float32)
+    for x in (np.float32(1e-30), np.float32(1.0), np.float32(3.0), f.max):
+        xv = np.full(ys.shape, x, np.float32)
+        _, r = _quantize_by_f64_reciprocal(ys, xv)
+        assert np.array_equal(r, _quantize_by_division(ys, xv))
