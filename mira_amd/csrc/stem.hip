@@ -1,214 +1,301 @@
 // Fused stem: int8 implicit-GEMM convolution of a <= 4-channel NHWC input
-// (mira/ops.py:630-634), its epilogue (bias, ReLU: mira/ops.py:192-199), the
-// -inf pad (mira/ops.py:461-470) and max pooling (mira/ops.py:293-296), for
-// graphs such as ResNet's 7x7/2 stem followed by a 3x3/2 max pool.
+// (mira/ops.py:630-634), its epilogue (mira/ops.py:192-199), a constant pad
+// (mira/ops.py:461-470) and max pooling (mira/ops.py:293-296), for graphs such
+// as ResNet's 7x7/2 stem followed by a 3x3/2 max pool.
 //
-// Unfused, the convolution writes its full-resolution f32 output
-// (822 MB for ResNet-18 at batch 256) only for the pool to read it back.
-// Here a workgroup owns POOL_ROWS output rows of the pool for one image; it
-// computes the convolution rows their windows cover, one row at a time
-// (<= 128 output pixels x 64 channels: 4 waves x one 32-row MFMA block row),
-// applies the epilogue, stages the f32 row in LDS, pools it horizontally and
-// folds it into running window maxima kept in registers.  Only the pooled
-// f32 / int8 results reach memory.  Max is exact in any order for the
-// non-NaN values an epilogue of a finite accumulator produces, so the
-// result equals the reference's window maximum bit for bit.
+// Unfused, the convolution writes its full-resolution result (822 MB of f32
+// for ResNet-18 at batch 256) only for the pool to read it back.  Here the
+// pool runs on the int32 accumulators and the epilogue only on the pooled
+// values: for a fixed output channel the epilogue is a non-decreasing
+// function of the accumulator (dequant by a positive scale, then adds,
+// subtractions of a constant, maximum/minimum with constants: the host only
+// fuses such epilogues), so the maximum over a window commutes with it, and
+// max(f(a1), .., f(ak)) == f(max(a1, .., ak)) bit for bit (the values are never
+// NaN unless an epilogue operand is, in which case both sides are NaN).  The
+// pad value joins a window through NumPy's maximum after the epilogue.
 //
-// A fragments are loaded straight from global memory (one dword per tap of
-// 4 channels, zero outside the image); the weights (<= 64 x k_pad bytes) are
-// copied to LDS once per workgroup.
+// A workgroup owns BAND pooled rows of one image.  It walks the convolution
+// rows their windows cover, one at a time: 4 waves x one 32-pixel MFMA block
+// row (<= 128 output columns x 64 channels, weights held in registers), the
+// int32 row goes to LDS as [channel][column], and each lane (one channel)
+// max-pools its wave's 16 pooled columns horizontally and folds them into the
+// running maxima of the pooled rows whose windows contain the row.  A pooled
+// row is finished (epilogue, f32 and int8 stores, 64 channels per store)
+// when its last convolution row has been folded in.
 #include "mr_common.hpp"
+
+#include <climits>
 
 namespace mr {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int POOL_ROWS = 2;      // pooled output rows per workgroup
+constexpr int BAND = 8;           // pooled rows per workgroup
+constexpr int CRW = 132;          // int32 slots per channel in a staged row: columns -4 .. 127
+constexpr int COL_OFF = 4;        // slot of convolution column 0
+constexpr int BUF_DWORD3 = 0x00020000;   // buffer resource word 3 for raw 32-bit loads on gfx9
 
 // Source of every padding tap: loads are never predicated, their address is
 // (a select before the load keeps all of a row's loads in flight at once).
 __device__ __attribute__((aligned(64))) int32_t g_stem_zero[16];
-constexpr int CROW_LD = 64 + 1;   // f32 stride of a staged convolution row (bank offset)
-constexpr int BROW_PAD = 16;      // bytes added to each weight row in LDS (16 rows hit 16 bank groups)
 
 struct StemArgs {
   const int8_t* x;     // NHWC int8, 4 bytes per pixel
-  const int8_t* b;     // packed weights [64][k_pad]
+  const int8_t* b;     // packed weights [>= 64][k_pad]
   int32_t k_pad;
   int32_t row_bytes;   // packed bytes per kernel row
   int32_t N, H, W, O, OH, OW, KH, KW, SH, SW, PH, PW, DH, DW;
-  int32_t pk, ps, ppt, ppl, POH, POW;  // pool size, stride, top/left pad, pooled size
+  int32_t ppt, POH, POW;  // pool top pad, pooled size
   float pad_value;
 };
 
-template <int KSUB, int RB, bool FIXED>
+// KSUB: 32-byte K steps holding kernel rows; RB: 16-byte chunks per kernel
+// row; PK: pool window (3: rows/columns 2p-1 .. 2p+1, pad 1; 2: 2p .. 2p+1,
+// pad 0), stride 2.
+template <int KSUB, int RB, int PK, bool FIXED>
 __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const EpiDev e) {
-  constexpr int KB = KSUB * 32;                // k_pad
-  constexpr int BLD = KB + BROW_PAD;
-  __shared__ float crow[128 * CROW_LD];
-  __shared__ __attribute__((aligned(16))) int8_t bs[64 * BLD];
+  constexpr int PS = 2;
+  constexpr int PPL = PK == 3 ? 1 : 0;
+  // pooled columns of wave w: 16w .. 16w+15; their windows read staged slots
+  // [RD0 + 32w, + 4*NRD) of the lane's channel
+  constexpr int SPAN_LO = COL_OFF - PPL;                  // slot of the first window column of pooled column 0
+  constexpr int RD0 = SPAN_LO & ~3;                       // aligned start of a wave's reads (wave 0)
+  constexpr int REL = SPAN_LO - RD0;                      // first window slot relative to the read start
+  constexpr int NRD = (REL + 15 * PS + PK + 3) / 4;       // 16-byte reads per lane
+  static_assert(RD0 + 48 * PS + 4 * NRD <= CRW, "pool reads stay inside the staged row");
+
+  __shared__ __attribute__((aligned(16))) int32_t crow[2][64 * CRW];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int img = blockIdx.x / ((a.POH + POOL_ROWS - 1) / POOL_ROWS);
-  const int pr0 = (blockIdx.x - img * ((a.POH + POOL_ROWS - 1) / POOL_ROWS)) * POOL_ROWS;
+  const int bands = (a.POH + BAND - 1) / BAND;
+  const int img = blockIdx.x / bands;
+  const int pr0 = (blockIdx.x - img * bands) * BAND;
+  const int pr_end = min(pr0 + BAND, a.POH);
 
-  // weights to LDS: 64 rows x KB bytes, 16 bytes per thread per step
-  for (int c = threadIdx.x; c < 64 * KB / 16; c += 256) {
-    const int row = c / (KB / 16), k16 = c - row * (KB / 16);
-    *reinterpret_cast<v4i*>(bs + row * BLD + k16 * 16) =
-        *reinterpret_cast<const v4i*>(a.b + int64_t(row) * a.k_pad + k16 * 16);
-  }
-
-  // per-column constants (the column index is lane-fixed): dequant scale and,
-  // for the fixed epilogue form, the per-column operand and the scalar bounds
-  double scale[2];
-  float colv[2];
+  // weights: lane holds rows (32j + lane%32), K bytes 32s + 16*(lane/32) .. +16
+  v4i bw[KSUB][2];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = min(j * 32 + (lane & 31), a.O - 1);
-    scale[j] = e.scale[col];
-    colv[j] = FIXED && e.f_col ? e.col_ptr[col] : 0.0f;
-  }
+  for (int s = 0; s < KSUB; ++s)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      bw[s][j] = *reinterpret_cast<const v4i*>(a.b + int64_t(j * 32 + (lane & 31)) * a.k_pad + s * 32 +
+                                               (lane >> 5) * 16);
+
+  // pool-phase role: this lane is output channel `lane`
+  const int ch = lane;
+  const int chc = min(ch, a.O - 1);
+  const double scale = e.scale[chc];
+  const float colv = FIXED && e.f_col ? e.col_ptr[chc] : 0.0f;
   const float lo = FIXED && e.f_lo && e.lo_ptr ? e.lo_ptr[0] : 0.0f;
   const float hi = FIXED && e.f_hi ? e.hi_ptr[0] : 0.0f;
 
-  // running window maxima: this thread owns pooled positions idx = t + 256*i.
-  // A window that reaches above or below the convolution output includes the
-  // pad value; otherwise it starts empty (-inf is max's identity).
-  constexpr int PER_T = (64 * 64 + 255) / 256;   // POW <= 64 positions x 64 channels
-  float pmax[POOL_ROWS][PER_T];
-#pragma unroll
-  for (int r = 0; r < POOL_ROWS; ++r) {
-    const int top = (pr0 + r) * a.ps - a.ppt;
-    const float init = (top < 0 || top + a.pk > a.OH) ? a.pad_value : -INFINITY;
-#pragma unroll
-    for (int i = 0; i < PER_T; ++i) pmax[r][i] = init;
-  }
-
-  // convolution rows the band's windows touch
-  const int cr_lo = max(pr0 * a.ps - a.ppt, 0);
-  const int cr_hi = min((pr0 + POOL_ROWS - 1) * a.ps - a.ppt + a.pk - 1, a.OH - 1);
   const int ow = wave * 32 + (lane & 31);           // this lane's A row (output column)
   const int iw0 = ow * a.SW - a.PW;
 
   // A fragments of convolution row cr straight from global memory.  A 32-byte
   // K step is one kernel row of up to 8 taps (RB == 2: lane halves take taps
   // 0-3 / 4-7) or two kernel rows of up to 4 taps (RB == 1: one row per half).
+  // Each input row is read through a buffer resource spanning exactly that row
+  // (none for rows outside the image), and each lane's tap columns are fixed
+  // byte offsets into it: the hardware returns 0 for every tap outside the
+  // image, so the loads need no address arithmetic, masking or branches.  Taps
+  // past the kernel (kh >= KH, kw >= KW) read whatever is there: their packed
+  // weights are zero.
   const int32_t* ximg = reinterpret_cast<const int32_t*>(a.x) + int64_t(img) * a.H * a.W;
+  const int kw0 = RB == 2 ? 4 * (lane >> 5) : 0;
+  int cofs[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) cofs[q] = (iw0 + (kw0 + q) * a.DW) * 4;   // negative -> out of range
   auto load_row = [&](int cr, v4i (&af)[KSUB]) {
-    const int ih0 = cr * a.SH - a.PH;
 #pragma unroll
     for (int s = 0; s < KSUB; ++s) {
-      const int kh = RB == 2 ? s : 2 * s + (lane >> 5);
-      const int kw0 = RB == 2 ? 4 * (lane >> 5) : 0;
-      const int ih = ih0 + kh * a.DH;
-      const bool row_ok = ow < a.OW && kh < a.KH && unsigned(ih) < unsigned(a.H);
-      const int32_t* p = ximg + int64_t(row_ok ? ih : 0) * a.W;
+      if constexpr (RB == 2) {
+        const int ih = cr * a.SH - a.PH + s * a.DH;
+        const bool ok = unsigned(ih) < unsigned(a.H);
+        const __amdgpu_buffer_rsrc_t row = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int32_t*>(ximg + int64_t(ok ? ih : 0) * a.W), 0, ok ? a.W * 4 : 0, BUF_DWORD3);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int kw = kw0 + q;
-        const int iw = iw0 + kw * a.DW;
-        const bool ok = row_ok && kw < a.KW && unsigned(iw) < unsigned(a.W);
-        af[s][q] = *(ok ? p + iw : g_stem_zero);
+        for (int q = 0; q < 4; ++q) af[s][q] = __builtin_amdgcn_raw_buffer_load_b32(row, cofs[q], 0, 0);
+      } else {
+        // lane halves read different kernel rows 2s and 2s+1
+        const int ih = cr * a.SH - a.PH + (2 * s + (lane >> 5)) * a.DH;
+        const bool ok = unsigned(ih) < unsigned(a.H);
+        const int32_t* rp = ximg + int64_t(ok ? ih : 0) * a.W;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int v = rp[min(max(cofs[q] / 4, 0), a.W - 1)];
+          af[s][q] = ok && unsigned(cofs[q] / 4) < unsigned(a.W) ? v : 0;
+        }
       }
     }
   };
 
-  v4i anext[KSUB];
-  if (cr_lo <= cr_hi) load_row(cr_lo, anext);
-  for (int cr = cr_lo; cr <= cr_hi; ++cr) {
-    v4i afrag[KSUB];
-#pragma unroll
-    for (int s = 0; s < KSUB; ++s) afrag[s] = anext[s];
-    if (cr < cr_hi) load_row(cr + 1, anext);   // in flight during this row's MFMA, epilogue and pooling
-    v16i acc[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[j][r] = 0;
-    __syncthreads();   // weights staged (first row) / previous row's pooling reads done
-#pragma unroll
-    for (int s = 0; s < KSUB; ++s)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const v4i bf = *reinterpret_cast<const v4i*>(bs + (j * 32 + (lane & 31)) * BLD + s * 32 + (lane >> 5) * 16);
-        acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afrag[s], bf, acc[j], 0, 0, 0);
-      }
+  // Columns outside the convolution output read as INT_MIN (max's identity):
+  // slots of columns -4..-1 once here, columns >= OW at every staging.
+  for (int i = threadIdx.x; i < 2 * 64 * COL_OFF; i += 256)
+    crow[i / (64 * COL_OFF)][(i / COL_OFF) % 64 * CRW + i % COL_OFF] = INT_MIN;
+  const bool edge_wave = wave * 32 + 32 > a.OW;
 
-    // ---- epilogue of the convolution row, staged in LDS as f32
-    // Every lane stores all 32 of its values: rows >= OW and columns >= O land
-    // in the padded part of the row buffer and are never read; their operand
-    // indices are clamped so every load stays inside the operand.
-    const int64_t pix_base = (int64_t(img) * a.OH + cr) * a.OW;
+  // Convolution row cr -> h[j]: this lane's channel, max over the window
+  // columns of pooled column 16*wave + j.  The A fragments of row cr are in
+  // afrag on entry; those of row `next` are on their way on return.
+  v4i afrag[KSUB];
+  auto conv_row = [&](int cr, int next, int (&h)[16]) {
+    int32_t* buf = crow[cr & 1];
+    {
+      v16i acc[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = j * 32 + (lane & 31);
-      const int colc = min(col, a.O - 1);
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rw = wave * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int64_t pix = pix_base + min(rw, a.OW - 1);
-        float y = dequant(acc[j][r], scale[j]);
-        if constexpr (FIXED) {
-          if (e.f_col) y = __fadd_rn(y, colv[j]);
-          if (e.f_full) y = __fadd_rn(y, e.full_ptr[pix * e.full_ld + colc]);
-          if (e.f_lo) y = np_maximum(y, lo);
-          if (e.f_hi) y = np_minimum(y, hi);
-        } else {
-          y = epi_generic(e, y, pix, colc);
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0;
+#pragma unroll
+      for (int s = 0; s < KSUB; ++s)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afrag[s], bw[s][j], acc[j], 0, 0, 0);
+      load_row(next, afrag);   // in flight during the staging and pooling of this row
+      // stage as [channel][column]: the lane's 4 consecutive rows (columns) per group
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = wave * 32 + 8 * g + 4 * (lane >> 5);
+          v4i v = {acc[j][4 * g], acc[j][4 * g + 1], acc[j][4 * g + 2], acc[j][4 * g + 3]};
+          if (edge_wave) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) v[b] = col + b < a.OW ? v[b] : INT_MIN;
+          }
+          *reinterpret_cast<v4i*>(buf + (j * 32 + (lane & 31)) * CRW + COL_OFF + col) = v;
         }
-        crow[rw * CROW_LD + col] = y;
-      }
     }
-    __syncthreads();
+    __syncthreads();   // the row is staged; the other buffer's readers (row cr-1) are done
+    v4i rd[NRD];
+    const int32_t* src = buf + ch * CRW + RD0 + wave * 16 * PS;
+#pragma unroll
+    for (int q = 0; q < NRD; ++q) rd[q] = *reinterpret_cast<const v4i*>(src + 4 * q);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      int m = INT_MIN;
+#pragma unroll
+      for (int t = 0; t < PK; ++t) {
+        const int slot = REL + j * PS + t;                   // compile-time
+        m = max(m, rd[slot >> 2][slot & 3]);
+      }
+      h[j] = m;
+    }
+  };
 
-    // ---- pool horizontally and fold into the windows containing this row.
-    // Branch-free: positions past the pooled row (pc >= POW) or channel count
-    // compute on clamped indices and are simply never stored.
-    bool in_win[POOL_ROWS];
-#pragma unroll
-    for (int r = 0; r < POOL_ROWS; ++r) {
-      const int top = (pr0 + r) * a.ps - a.ppt;
-      in_win[r] = cr >= top && cr < top + a.pk;
-    }
-#pragma unroll
-    for (int i = 0; i < PER_T; ++i) {
-      const int idx = threadIdx.x + 256 * i;
-      const int pc = min(idx >> 6, a.POW - 1), ch = min(idx & 63, a.O - 1);
-      float h = -INFINITY;
-      for (int t = 0; t < a.pk; ++t) {
-        const int c = pc * a.ps - a.ppl + t;
-        const float v = crow[min(max(c, 0), a.OW - 1) * CROW_LD + ch];
-        h = np_maximum(h, unsigned(c) < unsigned(a.OW) ? v : a.pad_value);
-      }
-#pragma unroll
-      for (int r = 0; r < POOL_ROWS; ++r) pmax[r][i] = in_win[r] ? np_maximum(pmax[r][i], h) : pmax[r][i];
-    }
+  // Finish pooled row p from its window maxima v[j]: epilogue on the pooled
+  // accumulators, the pad value where the window covers padding, stores (the
+  // 64 lanes of a wave write one pooled pixel's channels).  Windows reaching
+  // into the left/right padding: bit j of pad_cols.  Stores go through buffer
+  // resources spanning the npx finished pixels of the pooled row; lanes past
+  // the channel count get an offset out of range, so the hardware drops them.
+  const int npx = min(16, a.POW - wave * 16);
+  uint32_t pad_cols = 0;
+  for (int j = 0; j < 16; ++j) {
+    const int left = (wave * 16 + j) * PS - PPL;
+    if (left < 0 || left + PK > a.OW) pad_cols |= 1u << j;
   }
-
-  // ---- pooled results
+  const bool pad_inert = a.pad_value == -INFINITY;   // max with -inf changes nothing
+  const uint32_t vf = ch < a.O ? uint32_t(ch) * 4u : 0x80000000u;
+  const uint32_t vq = ch < a.O ? uint32_t(ch) : 0x80000000u;
+  auto finish = [&](int p, const int (&v)[16]) {
+    const int top = p * PS - PPL;
+    const bool pad_rows = top < 0 || top + PK > a.OH;
+    const int64_t row0 = (int64_t(img) * a.POH + p) * a.POW + wave * 16;
+    const __amdgpu_buffer_rsrc_t rf = __builtin_amdgcn_make_buffer_rsrc(
+        e.out_f32 + row0 * e.ldo, 0, e.out_f32 ? npx * int(e.ldo) * 4 : 0, BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        e.out_i8 + row0 * e.ldq, 0, e.out_i8 ? npx * int(e.ldq) : 0, BUF_DWORD3);
 #pragma unroll
-  for (int r = 0; r < POOL_ROWS; ++r) {
-    const int pr = pr0 + r;
-    if (pr >= a.POH) break;
-#pragma unroll
-    for (int i = 0; i < PER_T; ++i) {
-      const int idx = threadIdx.x + 256 * i;
-      const int pc = idx >> 6, ch = idx & 63;
-      if (pc >= a.POW || ch >= a.O) continue;
-      const int64_t pix = (int64_t(img) * a.POH + pr) * a.POW + pc;
-      epi_store(e, pmax[r][i], pix, ch);
+    for (int j = 0; j < 16; ++j) {
+      float y = dequant(v[j], scale);
+      if constexpr (FIXED) {
+        if (e.f_col) y = __fadd_rn(y, colv);
+        if (e.f_lo) y = np_maximum(y, lo);
+        if (e.f_hi) y = np_minimum(y, hi);
+      } else {
+        y = epi_generic(e, y, row0 + j, chc);
+      }
+      if (!pad_inert) y = np_maximum(y, pad_rows || ((pad_cols >> j) & 1) ? a.pad_value : -INFINITY);
+      if (j < npx) {
+        if (e.out_f32) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rf, vf + uint32_t(j * e.ldo * 4), 0, 0);
+        if (e.out_i8)
+          __builtin_amdgcn_raw_buffer_store_b8(quantize_rcp(y, e.out_rxs), rq, vq + uint32_t(j * e.ldq), 0, 0);
+      }
     }
+  };
+
+  // Pooled row p takes convolution rows 2p-1 (PK == 3), 2p and 2p+1; the host
+  // guarantees 2p - PPL < OH for every pooled row.  Rows are walked in order,
+  // row 2p+1 carrying over into pooled row p+1.
+  const int cr_first = max(2 * pr0 - PPL, 0);
+  const int cr_last = min(2 * (pr_end - 1) + 1, a.OH - 1);
+  int carry[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) carry[j] = INT_MIN;
+  load_row(cr_first, afrag);
+  if (PK == 3 && pr0 > 0) conv_row(2 * pr0 - 1, min(2 * pr0, cr_last), carry);
+  for (int p = pr0; p < pr_end; ++p) {
+    const int r0 = 2 * p, r1 = 2 * p + 1;
+    int h0[16], h1[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) h0[j] = h1[j] = INT_MIN;
+    if (r0 < a.OH) conv_row(r0, min(r1, cr_last), h0);
+    if (r1 < a.OH) conv_row(r1, min(r1 + 1, cr_last), h1);
+    int v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      v[j] = max(h0[j], h1[j]);
+      if constexpr (PK == 3) v[j] = max(v[j], carry[j]);
+      carry[j] = h1[j];
+    }
+    finish(p, v);
   }
 }
 
-template <int KS, int RBV>
+template <int KS, int RBV, int PK>
 static void launch_stem(dim3 grid, hipStream_t s, const StemArgs& a, const EpiDev& e) {
   if (e.fixed)
-    hipLaunchKernelGGL((stem_pool_kernel<KS, RBV, true>), grid, dim3(256), 0, s, a, e);
+    hipLaunchKernelGGL((stem_pool_kernel<KS, RBV, PK, true>), grid, dim3(256), 0, s, a, e);
   else
-    hipLaunchKernelGGL((stem_pool_kernel<KS, RBV, false>), grid, dim3(256), 0, s, a, e);
+    hipLaunchKernelGGL((stem_pool_kernel<KS, RBV, PK, false>), grid, dim3(256), 0, s, a, e);
+}
+
+template <int PK>
+static bool launch_stem_pool(int ksub, bool rb2, dim3 grid, hipStream_t s, const StemArgs& a, const EpiDev& e) {
+  if (rb2) {
+    switch (ksub) {
+      case 5: launch_stem<5, 2, PK>(grid, s, a, e); return true;
+      case 6: launch_stem<6, 2, PK>(grid, s, a, e); return true;
+      case 7: launch_stem<7, 2, PK>(grid, s, a, e); return true;
+      case 8: launch_stem<8, 2, PK>(grid, s, a, e); return true;
+      default: return false;
+    }
+  }
+  switch (ksub) {
+    case 1: launch_stem<1, 1, PK>(grid, s, a, e); return true;
+    case 2: launch_stem<2, 1, PK>(grid, s, a, e); return true;
+    default: return false;
+  }
+}
+
+// The pool commutes with the epilogue only if every step is a non-decreasing
+// function of the value with an operand that is the same across a window
+// (a scalar or a per-channel vector).
+static bool monotone_epilogue(const mr_epilogue* epi) {
+  for (int i = 0; i < epi->n_steps; ++i) {
+    const mr_epi_step& st = epi->steps[i];
+    if (st.fn == MR_EPI_RELU) continue;
+    if (st.mode != MR_BC_SCALAR && st.mode != MR_BC_COL) return false;
+    switch (st.fn) {
+      case MR_EPI_ADD: case MR_EPI_MAX: case MR_EPI_MIN: break;
+      case MR_EPI_SUB: if (st.swapped) return false; break;
+      default: return false;
+    }
+  }
+  return true;
 }
 
 }  // namespace mr
@@ -241,6 +328,19 @@ int mr_qconv2d_maxpool(const int8_t* x, const mr_conv_geom* cg, const int8_t* b,
   MR_REQUIRE(poh > 0 && pow_ > 0 && pow_ <= 64 && (poh - 1) * pool_stride - pool_pad_top < oh &&
                  (pow_ - 1) * pool_stride - pool_pad_left < ow,
              "mr_qconv2d_maxpool: pooled size %dx%d does not fit the %dx%d convolution output", poh, pow_, oh, ow);
+  const bool pool_3_2_1 = pool_size == 3 && pool_stride == 2 && pool_pad_left == 1 && pool_pad_top == 1;
+  const bool pool_2_2_0 = pool_size == 2 && pool_stride == 2 && pool_pad_left == 0 && pool_pad_top == 0;
+  if (!pool_3_2_1 && !pool_2_2_0) {
+    mr::set_error("mr_qconv2d_maxpool: pool %dx%d/%d with top/left pad %d/%d has no kernel (3/2 pad 1 and 2/2 pad 0 "
+                  "do)", pool_size, pool_size, pool_stride, pool_pad_top, pool_pad_left);
+    return MR_EUNSUPPORTED;
+  }
+  MR_REQUIRE(epi != nullptr, "mr_qconv2d_maxpool: NULL epilogue");
+  if (!mr::monotone_epilogue(epi)) {
+    mr::set_error("mr_qconv2d_maxpool: the epilogue must be non-decreasing with scalar or per-channel operands "
+                  "(add, sub, maximum, minimum, relu)");
+    return MR_EUNSUPPORTED;
+  }
   MR_REQUIRE(reinterpret_cast<uintptr_t>(x) % 4 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0,
              "mr_qconv2d_maxpool: misaligned operands");
   mr::EpiDev e;
@@ -267,24 +367,23 @@ int mr_qconv2d_maxpool(const int8_t* x, const mr_conv_geom* cg, const int8_t* b,
   a.PW = G.pw;
   a.DH = G.dh;
   a.DW = G.dw;
-  a.pk = pool_size;
-  a.ps = pool_stride;
   a.ppt = pool_pad_top;
-  a.ppl = pool_pad_left;
   a.POH = poh;
   a.POW = pow_;
   a.pad_value = pad_value;
-  const int64_t bands = (poh + mr::POOL_ROWS - 1) / mr::POOL_ROWS;
+  const int64_t bands = (poh + mr::BAND - 1) / mr::BAND;
   const int64_t blocks = int64_t(G.n) * bands;
   MR_REQUIRE(blocks < (int64_t(1) << 31), "mr_qconv2d_maxpool: too many images");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool rb2 = row_bytes == 32;   // kw 5..8 (else kw <= 4, 16 bytes per kernel row)
   const dim3 grid(static_cast<unsigned>(blocks));
-  switch (k_pad / 32) {
-    case 2: rb2 ? mr::launch_stem<2, 2>(grid, s, a, e) : mr::launch_stem<2, 1>(grid, s, a, e); break;
-    case 4: rb2 ? mr::launch_stem<4, 2>(grid, s, a, e) : mr::launch_stem<4, 1>(grid, s, a, e); break;
-    case 6: rb2 ? mr::launch_stem<6, 2>(grid, s, a, e) : mr::launch_stem<6, 1>(grid, s, a, e); break;
-    default: rb2 ? mr::launch_stem<8, 2>(grid, s, a, e) : mr::launch_stem<8, 1>(grid, s, a, e); break;
+  const int ksub = rb2 ? G.kh : (G.kh + 1) / 2;        // 32-byte K steps holding real kernel rows
+  const bool launched = pool_3_2_1 ? mr::launch_stem_pool<3>(ksub, rb2, grid, s, a, e)
+                                   : mr::launch_stem_pool<2>(ksub, rb2, grid, s, a, e);
+  if (!launched) {
+    mr::set_error("mr_qconv2d_maxpool: %dx%d kernels have no kernel here (kh 1-4 with kw <= 4, kh 5-8 with kw 5-8)",
+                  G.kh, G.kw);
+    return MR_EUNSUPPORTED;
   }
   MR_LAUNCH_CHECK("qconv2d_maxpool");
   return MR_OK;

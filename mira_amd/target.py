@@ -246,7 +246,8 @@ class RocmExecutable:
                 self._const_dv(v)
 
     def _stem_fusable(self, conv: Optional[ir.Op], pad_op: ir.Op, pool: ir.Op) -> bool:
-        """Can qconv2d -> pad -> maxpool2d run as mr_qconv2d_maxpool (the convolution is never stored)?"""
+        """Can qconv2d -> pad -> maxpool2d run as mr_qconv2d_maxpool (the convolution is never stored)?
+        The kernel pools the int32 accumulators, so the epilogue must commute with max."""
         if conv is None or conv.kind != "qconv2d" or self.target.debug_acc:
             return False
         r = conv.result
@@ -255,11 +256,27 @@ class RocmExecutable:
         n, c, h, w = conv.inputs[0].type.shape
         o, _, kh, kw = conv.attrs["q"].shape
         ow = r.type.shape[3]
-        row_bytes = pack.conv_row_bytes(kw)
         pads = tuple(tuple(x) for x in pad_op.attrs["pads"])
-        size = pool.attrs["size"]
-        return (c <= 4 and o <= 64 and ow <= 128 and row_bytes <= 32 and pack.roundup(kh * row_bytes, 64) <= 256
-                and pads[2][0] < size and pads[3][0] < size and pool.result.type.shape[3] <= 64)
+        pool_cfg = (pool.attrs["size"], pool.attrs["stride"], pads[2][0], pads[3][0])
+        kernel_ok = (5 <= kh <= 8) if kw >= 5 else (kh <= 4)
+        return (c <= 4 and o <= 64 and ow <= 128 and kw <= 8 and kernel_ok
+                and pool_cfg in ((3, 2, 1, 1), (2, 2, 0, 0)) and pool.result.type.shape[3] <= 64
+                and self._monotone_epilogue(conv))
+
+    def _monotone_epilogue(self, op: ir.Op) -> bool:
+        """Every step non-decreasing in the value, with an operand that is the same across a
+        pooling window (scalar or per-channel)."""
+        rshape = op.result.type.shape
+        for fn, idx, swapped in op.attrs.get("epilogue", ()):
+            if fn == "relu":
+                continue
+            if fn not in ("add", "sub", "maximum", "minimum") or (fn == "sub" and swapped):
+                return False
+            v = op.inputs[idx]
+            shape = np.shape(self._const_value(v)) if v in self.consts else v.type.shape
+            if _bcast_mode(shape, rshape, True) not in (L.BC_SCALAR, L.BC_COL):
+                return False
+        return True
 
     def _foldable_pad(self, v: ir.Value) -> bool:
         p = v.producer

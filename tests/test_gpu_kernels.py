@@ -101,7 +101,7 @@ def test_qmatmul_bias_relu_requant(lib, M, K, N):
              "epilogue": (("add", 1, False), ("relu", None, False))}
     want_acc = G.qmatmul_acc(x, attrs)
     want = G.qmatmul([x, bias], attrs)
-    next_xs = float(want.max()) / 127 or 1.0
+    next_xs = float(np.abs(want[np.isfinite(want)]).max()) / 127 or 1.0
     acc, y, yq = _run_qmatmul(lib, x, q, ws, xs, [("add", L.BC_COL, bias, False), ("relu", 0, None, False)], next_xs)
     assert np.array_equal(acc, want_acc.astype(np.int32))
     assert bits_equal(y, want)
@@ -173,7 +173,7 @@ def test_qconv2d(lib, n, c, h, w, o, k, s, p, d):
     assert G.qconv2d_certificate(x, attrs) < 2 ** 24
     want_acc = G.qconv2d_acc(x, attrs)
     want = G.qconv2d([x, bias, res], attrs)
-    next_xs = float(want.max()) / 127 or 1.0
+    next_xs = float(np.abs(want[np.isfinite(want)]).max()) / 127 or 1.0
     cp = pack.c_pad_for(c)
     xq = empty((n, h, w, cp), torch.int8)
     L.check(lib.mr_quantize_nchw_nhwc(T(x).data_ptr(), n, c, h, w, xq.data_ptr(), cp, xs, stream()), "q")
@@ -283,28 +283,32 @@ def test_pad_and_layouts(lib):
 
 # ---------------------------------------------------------------- fused stem (conv -> pad -> maxpool)
 
-@pytest.mark.parametrize("n,c,h,o,k,s,p,pool,pst,ppad,pval", [
-    (2, 3, 224, 64, 7, 2, 3, 3, 2, 1, float("-inf")),   # ResNet-18 stem
-    (3, 3, 37, 32, 3, 2, 1, 3, 2, 1, float("-inf")),    # odd sizes, 3 taps per row
-    (2, 1, 30, 16, 5, 1, 2, 2, 2, 0, 0.0),              # no pool padding
-    (2, 4, 29, 48, 7, 2, 3, 3, 2, 1, 0.25),             # finite pad value
+@pytest.mark.parametrize("n,c,h,o,k,s,p,pool,pst,ppad,pval,neg", [
+    (2, 3, 224, 64, 7, 2, 3, 3, 2, 1, float("-inf"), False),   # ResNet-18 stem
+    (2, 3, 224, 64, 7, 2, 3, 3, 2, 1, float("-inf"), True),    # every accumulator negative
+    (3, 3, 37, 32, 3, 2, 1, 3, 2, 1, float("-inf"), False),    # odd sizes, 3 taps per row
+    (2, 1, 30, 16, 5, 1, 2, 2, 2, 0, 0.0, False),              # no pool padding
+    (2, 4, 29, 48, 7, 2, 3, 3, 2, 1, 0.25, True),              # finite pad value
 ])
-def test_qconv2d_maxpool(lib, n, c, h, o, k, s, p, pool, pst, ppad, pval):
+def test_qconv2d_maxpool(lib, n, c, h, o, k, s, p, pool, pst, ppad, pval, neg):
     torch = _torch()
     rng = np.random.default_rng(h + o)
     x = rng.uniform(-1, 1, (n, c, h, h)).astype(np.float32)
     wt = rng.standard_normal((o, c, k, k)).astype(np.float32)
+    if neg:      # x > 0, w < 0: window maxima are negative, so the identity of max matters
+        x, wt = np.abs(x) + 0.01, -np.abs(wt)
     q, ws = G.quantize_array(wt, 0)
     xs = float(np.abs(x).max()) / 127
     bias = (rng.standard_normal((o, 1, 1)) * 0.3).astype(np.float32)
+    steps = (("add", 1, False),) if neg else (("add", 1, False), ("relu", None, False))
     attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "stride": (s, s), "padding": (p, p),
-             "epilogue": (("add", 1, False), ("relu", None, False))}
+             "epilogue": steps}
     conv = G.qconv2d([x, bias], attrs)
     padded = G.pad([conv], {"pads": ((0, 0), (0, 0), (ppad, ppad), (ppad, ppad)), "value": pval})
     want = G.maxpool2d([padded], {"size": pool, "stride": pst})
     oh = conv.shape[2]
     poh = want.shape[2]
-    next_xs = float(want.max()) / 127
+    next_xs = float(np.abs(want[np.isfinite(want)]).max()) / 127
     cp = 4
     xq = empty((n, h, h, cp), torch.int8)
     L.check(lib.mr_quantize_nchw_nhwc(T(x).data_ptr(), n, c, h, h, xq.data_ptr(), cp, xs, stream()), "q")
@@ -316,8 +320,8 @@ def test_qconv2d_maxpool(lib, n, c, h, o, k, s, p, pool, pst, ppad, pval):
     ocp = pack.c_pad_for(o)
     yq = empty((M, ocp), torch.int8)
     bt = T(bias.reshape(o))
-    e = epilogue([("add", L.BC_COL, bt, 0, False), ("relu", 0, None, 0, False)], scale=scale, out_f32=y, ldo=o,
-                 out_i8=yq, ldq=ocp, xs=next_xs)
+    dev_steps = [("add", L.BC_COL, bt, 0, False)] + ([] if neg else [("relu", 0, None, 0, False)])
+    e = epilogue(dev_steps, scale=scale, out_f32=y, ldo=o, out_i8=yq, ldq=ocp, xs=next_xs)
     L.check(lib.mr_qconv2d_maxpool(xq.data_ptr(), C.byref(g), b.data_ptr(), b.shape[1], b.shape[0], C.byref(e),
                                    pool, pst, ppad, ppad, pval, poh, poh, stream()), "mr_qconv2d_maxpool")
     sync()
