@@ -132,10 +132,14 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
   };
 
   // Columns outside the convolution output read as INT_MIN (max's identity):
-  // slots of columns -4..-1 once here, columns >= OW at every staging.
-  for (int i = threadIdx.x; i < 2 * 64 * COL_OFF; i += 256)
-    crow[i / (64 * COL_OFF)][(i / COL_OFF) % 64 * CRW + i % COL_OFF] = INT_MIN;
-  const bool edge_wave = wave * 32 + 32 > a.OW;
+  // the slots of columns -4..-1 and OW4..127 (OW4 = OW rounded down to a
+  // multiple of 4) are set once here and never staged into; a last group
+  // of 1..3 real columns is staged with its tail masked.
+  const int ow4 = a.OW & ~3;
+  for (int i = threadIdx.x; i < 2 * 64 * CRW; i += 256) {
+    const int slot = i % CRW;
+    if (slot < COL_OFF || slot >= COL_OFF + ow4) crow[i / (64 * CRW)][i % (64 * CRW)] = INT_MIN;
+  }
 
   // Convolution row cr -> h[j]: this lane's channel, max over the window
   // columns of pooled column 16*wave + j.  The A fragments of row cr are in
@@ -161,11 +165,13 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
         for (int g = 0; g < 4; ++g) {
           const int col = wave * 32 + 8 * g + 4 * (lane >> 5);
           v4i v = {acc[j][4 * g], acc[j][4 * g + 1], acc[j][4 * g + 2], acc[j][4 * g + 3]};
-          if (edge_wave) {
+          int32_t* dst = buf + (j * 32 + (lane & 31)) * CRW + COL_OFF + col;
+          if (col < ow4) {
+            *reinterpret_cast<v4i*>(dst) = v;
+          } else if (col < a.OW) {
 #pragma unroll
-            for (int b = 0; b < 4; ++b) v[b] = col + b < a.OW ? v[b] : INT_MIN;
+            for (int b = 0; b < 4; ++b) dst[b] = col + b < a.OW ? v[b] : INT_MIN;
           }
-          *reinterpret_cast<v4i*>(buf + (j * 32 + (lane & 31)) * CRW + COL_OFF + col) = v;
         }
     }
     __syncthreads();   // the row is staged; the other buffer's readers (row cr-1) are done
@@ -191,7 +197,7 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
   // into the left/right padding: bit j of pad_cols.  Stores go through buffer
   // resources spanning the npx finished pixels of the pooled row; lanes past
   // the channel count get an offset out of range, so the hardware drops them.
-  const int npx = min(16, a.POW - wave * 16);
+  const int npx = max(0, min(16, a.POW - wave * 16));   // pooled pixels this wave stores (0 past POW)
   uint32_t pad_cols = 0;
   for (int j = 0; j < 16; ++j) {
     const int left = (wave * 16 + j) * PS - PPL;
@@ -200,6 +206,12 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
   const bool pad_inert = a.pad_value == -INFINITY;   // max with -inf changes nothing
   const uint32_t vf = ch < a.O ? uint32_t(ch) * 4u : 0x80000000u;
   const uint32_t vq = ch < a.O ? uint32_t(ch) : 0x80000000u;
+  // With a finite scale and bias and no NaN bound (the usual case, checked once
+  // for the whole wave) the epilogue values are never NaN, NumPy's
+  // maximum/minimum reduce to one compare and select, and the int8 clamp to a
+  // median.
+  const bool nan_free = FIXED && !__any(!(fabs(scale) < INFINITY) || !(fabsf(colv) < INFINITY) || lo != lo ||
+                                        hi != hi) && !(a.pad_value != a.pad_value);
   auto finish = [&](int p, const int (&v)[16]) {
     const int top = p * PS - PPL;
     const bool pad_rows = top < 0 || top + PK > a.OH;
@@ -208,21 +220,34 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
         e.out_f32 + row0 * e.ldo, 0, e.out_f32 ? npx * int(e.ldo) * 4 : 0, BUF_DWORD3);
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
         e.out_i8 + row0 * e.ldq, 0, e.out_i8 ? npx * int(e.ldq) : 0, BUF_DWORD3);
+    auto store = [&](int j, float y, int8_t q) {   // pixels j >= npx fall outside the resources
+      if (e.out_f32) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rf, vf + uint32_t(j * e.ldo * 4), 0, 0);
+      if (e.out_i8) __builtin_amdgcn_raw_buffer_store_b8(q, rq, vq + uint32_t(j * e.ldq), 0, 0);
+    };
+    if (nan_free) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      float y = dequant(v[j], scale);
-      if constexpr (FIXED) {
+      for (int j = 0; j < 16; ++j) {
+        float y = dequant(v[j], scale);
         if (e.f_col) y = __fadd_rn(y, colv);
-        if (e.f_lo) y = np_maximum(y, lo);
-        if (e.f_hi) y = np_minimum(y, hi);
-      } else {
-        y = epi_generic(e, y, row0 + j, chc);
+        if (e.f_lo) y = y > lo ? y : lo;
+        if (e.f_hi) y = y < hi ? y : hi;
+        if (!pad_inert && (pad_rows || ((pad_cols >> j) & 1))) y = y > a.pad_value ? y : a.pad_value;
+        const float t = rintf(static_cast<float>(__dmul_rn(static_cast<double>(y), e.out_rxs)));
+        store(j, y, static_cast<int8_t>(static_cast<int>(__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f))));
       }
-      if (!pad_inert) y = np_maximum(y, pad_rows || ((pad_cols >> j) & 1) ? a.pad_value : -INFINITY);
-      if (j < npx) {
-        if (e.out_f32) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rf, vf + uint32_t(j * e.ldo * 4), 0, 0);
-        if (e.out_i8)
-          __builtin_amdgcn_raw_buffer_store_b8(quantize_rcp(y, e.out_rxs), rq, vq + uint32_t(j * e.ldq), 0, 0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float y = dequant(v[j], scale);
+        if constexpr (FIXED) {
+          if (e.f_col) y = __fadd_rn(y, colv);
+          if (e.f_lo) y = np_maximum(y, lo);
+          if (e.f_hi) y = np_minimum(y, hi);
+        } else {
+          y = epi_generic(e, y, row0 + j, chc);
+        }
+        if (!pad_inert) y = np_maximum(y, pad_rows || ((pad_cols >> j) & 1) ? a.pad_value : -INFINITY);
+        store(j, y, quantize_rcp(y, e.out_rxs));
       }
     }
   };
@@ -239,17 +264,20 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
   if (PK == 3 && pr0 > 0) conv_row(2 * pr0 - 1, min(2 * pr0, cr_last), carry);
   for (int p = pr0; p < pr_end; ++p) {
     const int r0 = 2 * p, r1 = 2 * p + 1;
-    int h0[16], h1[16];
+    int v[16], h[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) h0[j] = h1[j] = INT_MIN;
-    if (r0 < a.OH) conv_row(r0, min(r1, cr_last), h0);
-    if (r1 < a.OH) conv_row(r1, min(r1 + 1, cr_last), h1);
-    int v[16];
+    for (int j = 0; j < 16; ++j) v[j] = PK == 3 ? carry[j] : INT_MIN;
+    if (r0 < a.OH) {
+      conv_row(r0, min(r1, cr_last), h);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      v[j] = max(h0[j], h1[j]);
-      if constexpr (PK == 3) v[j] = max(v[j], carry[j]);
-      carry[j] = h1[j];
+      for (int j = 0; j < 16; ++j) v[j] = max(v[j], h[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) carry[j] = INT_MIN;
+    if (r1 < a.OH) {
+      conv_row(r1, min(r1 + 1, cr_last), carry);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = max(v[j], carry[j]);
     }
     finish(p, v);
   }
