@@ -61,6 +61,7 @@ struct GemmArgs {
 
 constexpr int BK = 64;
 
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -90,8 +91,24 @@ struct EpiCols4 {
   double scale[4];
   float colv[4];
   float lo, hi;
+  bool lo_nan, hi_nan;
   bool vec;  // four valid columns and every access 16-byte (f32) / 4-byte (int8) aligned
 };
+
+// NumPy's maximum(y, b) / minimum(y, b) for a bound b that is the same for the
+// whole wave: one unordered compare and a select.  !(y <= b) holds for y > b
+// and for NaN y, so a NaN y propagates and equality returns b, as NumPy does;
+// a NaN bound is returned as is.
+__device__ __forceinline__ float max_bound(float y, float b, bool b_nan) { return !(y <= b) && !b_nan ? y : b; }
+__device__ __forceinline__ float min_bound(float y, float b, bool b_nan) { return !(y >= b) && !b_nan ? y : b; }
+
+// clip(rint(y / xs), -127, 127) with the division done as a multiplication by
+// the double-precision reciprocal (equal to the IEEE quotient; see
+// quantize_rcp) and the clip as a median.
+__device__ __forceinline__ int quantize_med3(float y, double rxs) {
+  const float t = rintf(static_cast<float>(__dmul_rn(static_cast<double>(y), rxs)));
+  return static_cast<int>(__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f));
+}
 
 __device__ __forceinline__ void load_cols4(const EpiDev& e, int col0, int N, EpiCols4& c) {
   bool vec = col0 + 3 < N && (e.ldo % 4 == 0) && (e.ldq % 4 == 0) && (e.ldacc % 4 == 0) &&
@@ -104,6 +121,8 @@ __device__ __forceinline__ void load_cols4(const EpiDev& e, int col0, int N, Epi
   }
   c.lo = e.f_lo && e.lo_ptr ? e.lo_ptr[0] : 0.0f;
   c.hi = e.f_hi ? e.hi_ptr[0] : 0.0f;
+  c.lo_nan = c.lo != c.lo;
+  c.hi_nan = c.hi != c.hi;
   if (e.f_full) vec = vec && (e.full_ld % 4 == 0) && (reinterpret_cast<uintptr_t>(e.full_ptr) % 16 == 0);
   c.vec = vec;
 }
@@ -136,11 +155,11 @@ __device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, c
     }
     if (e.f_lo) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) y[k] = np_maximum(y[k], c.lo);
+      for (int k = 0; k < 4; ++k) y[k] = max_bound(y[k], c.lo, c.lo_nan);
     }
     if (e.f_hi) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) y[k] = np_minimum(y[k], c.hi);
+      for (int k = 0; k < 4; ++k) y[k] = min_bound(y[k], c.hi, c.hi_nan);
     }
   } else {
 #pragma unroll
@@ -153,7 +172,7 @@ __device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, c
     if (e.out_i8) {
       uint32_t packed = 0;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) packed |= uint32_t(uint8_t(quantize_rcp(y[k], e.out_rxs))) << (8 * k);
+      for (int k = 0; k < 4; ++k) packed |= uint32_t(quantize_med3(y[k], e.out_rxs) & 0xff) << (8 * k);
       *reinterpret_cast<uint32_t*>(e.out_i8 + row * e.ldq + col0) = packed;
     }
   } else {
@@ -181,7 +200,7 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
   constexpr int STAGE_BYTES = (BM + BN) * BK;
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32");
   static_assert(A_OPS * A_ROWS_PER_OP * NW == BM && B_OPS * 16 * NW == BN, "loader mapping");
-  static_assert((STAGES - 2) * OPS < 64, "vmcnt range");
+  static_assert(STAGES >= 3 && (STAGES - 2) * OPS < 64, "stages / vmcnt range");
 
   __shared__ __attribute__((aligned(1024))) int8_t lds[STAGES * STAGE_BYTES];
 
@@ -197,8 +216,16 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
   int t = blockIdx.x;
   const int full = total & ~7;
   if (t < full) t = (t & 7) * (full >> 3) + (t >> 3);
-  const int tile_m = t / g.tiles_n;
-  const int tile_n = t - tile_m * g.tiles_n;
+  // grouped order: runs of GROUP_M M-tiles walked column by column, so the
+  // tiles running together on an XCD share both A and B panels in its L2
+  constexpr int GROUP_M = 8;
+  const int gm_span = GROUP_M * g.tiles_n;
+  const int group = t / gm_span;
+  const int first_m = group * GROUP_M;
+  const int gsize = min(g.tiles_m - first_m, GROUP_M);
+  const int tin = t - group * gm_span;
+  const int tile_m = first_m + tin % gsize;
+  const int tile_n = tin / gsize;
   const int64_t m0 = int64_t(tile_m) * BM;
   const int n0 = tile_n * BN;
 
@@ -318,37 +345,51 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < KT) issue(s, s);
 
+  // Fragments of one 32-byte half (kk) of a K step: lane (row r, half h) holds
+  // bytes 16h .. 16h+15 of the half for row r of each 32-row block.
   const int frag_row = lane & 31;
   const int swz = (frag_row >> 2) & 3;
-  for (int kt = 0; kt < KT; ++kt) {
-    if (kt + STAGES - 2 < KT)
-      wait_vmcnt<(STAGES - 2) * OPS>();
-    else
-      wait_vmcnt<0>();
-    block_barrier();
-    if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-    const int8_t* As = lds + (kt % STAGES) * STAGE_BYTES;
+  auto load_frags = [&](int stage, int kk, v4i (&af)[FM], v4i (&bf)[FN]) {
+    const int8_t* As = lds + stage * STAGE_BYTES;
     const int8_t* Bs = As + BM * BK;
-    // every fragment of the step is requested before the first MFMA, so the
-    // LDS latency overlaps the matrix work
-    v4i af[2][FM], bf[2][FN];
+    const int pc = ((2 * kk + (lane >> 5)) ^ swz) << 4;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int pc = ((2 * kk + (lane >> 5)) ^ swz) << 4;
+    for (int i = 0; i < FM; ++i)
+      af[i] = *reinterpret_cast<const v4i*>(As + (wm * TM + i * 32 + frag_row) * BK + pc);
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
-        af[kk][i] = *reinterpret_cast<const v4i*>(As + (wm * TM + i * 32 + frag_row) * BK + pc);
+    for (int j = 0; j < FN; ++j)
+      bf[j] = *reinterpret_cast<const v4i*>(Bs + (wn * TN + j * 32 + frag_row) * BK + pc);
+  };
+  auto mfma_all = [&](const v4i (&af)[FM], const v4i (&bf)[FN]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bf[kk][j] = *reinterpret_cast<const v4i*>(Bs + (wn * TN + j * 32 + frag_row) * BK + pc);
+        acc[i * FN + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i * FN + j], 0, 0, 0);
+  };
+
+  // Software pipeline, one barrier per K step: the MFMAs of each half run
+  // on fragments read during the previous half, and the first half of step
+  // t+1 is read (after the barrier that publishes it) while the second half
+  // of step t multiplies.
+  v4i a0[FM], b0[FN], a1[FM], b1[FN];
+  if (KT >= STAGES - 1) wait_vmcnt<(STAGES - 2) * OPS>(); else wait_vmcnt<0>();
+  block_barrier();
+  load_frags(0, 0, a0, b0);
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt % STAGES;
+    load_frags(cur, 1, a1, b1);
+    mfma_all(a0, b0);
+    if (kt + 1 < KT) {
+      if (kt + STAGES - 2 < KT)
+        wait_vmcnt<(STAGES - 3) * OPS>();
+      else
+        wait_vmcnt<0>();
+      block_barrier();
+      if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+      load_frags((kt + 1) % STAGES, 0, a0, b0);
     }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i * FN + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[kk][i], bf[kk][j], acc[i * FN + j], 0, 0, 0);
+    mfma_all(a1, b1);
   }
 
   // ---- fused epilogue.  The int32 tile goes through LDS one 32-row block row
@@ -367,7 +408,7 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
   EpiCols4 cols;
   load_cols4(e, col0, g.N, cols);
 
-#pragma unroll 1
+#pragma unroll
   for (int pass = 0; pass < FM; ++pass) {
     block_barrier();   // LDS free: main-loop reads / previous pass's reads are done
 #pragma unroll
@@ -375,7 +416,7 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         ep[(wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * EP_LD + wn * TN + j * 32 + (lane & 31)] =
-            acc[j][r];
+            acc[pass * FN + j][r];
     block_barrier();
     for (int rr = threadIdx.x / CG; rr < EP_ROWS; rr += RSTEP) {
       const int64_t row = m0 + (rr >> 5) * TM + pass * 32 + (rr & 31);
@@ -383,9 +424,6 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
       const v4i a = *reinterpret_cast<const v4i*>(ep + rr * EP_LD + cgi * 4);
       store_row4<FIXED>(e, cols, a, row, col0, g.N);
     }
-    // rotate the next block row into acc[0 .. FN)
-#pragma unroll
-    for (int b = 0; b + FN < NB; ++b) acc[b] = acc[b + FN];
   }
 }
 
@@ -406,8 +444,10 @@ static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
 
 template <int AMODE>
 static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
-  // Tile choice: wide tiles when there are enough of them to cover every CU
-  // (a 256-row tile per CU at least), narrower ones otherwise.
+  // Tile choice (measured on the ResNet-18 conv shapes and dense GEMMs):
+  // 256x256 tiles with 8 waves (2 per SIMD) once there are enough of them to
+  // cover most CUs; otherwise 128x128 tiles (three workgroups fit a CU);
+  // narrow tiles for N <= 64.
   const int64_t cus = device_cu_count();
   const int64_t mt256 = (g.M + 255) / 256;
   MR_REQUIRE((g.M + 63) / 64 * ((g.N + 31) / 32) < (int64_t(1) << 31), "problem too large");
@@ -418,13 +458,10 @@ static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
       launch_cfg<256, 64, 4, 1, 4, AMODE>(g, e, stream);
     else
       launch_cfg<128, 64, 2, 1, 4, AMODE>(g, e, stream);
-  } else if (g.N <= 128 || mt256 * ((g.N + 255) / 256) < cus) {
-    if (mt256 * ((g.N + 127) / 128) >= cus)
-      launch_cfg<256, 128, 2, 2, 3, AMODE>(g, e, stream);
-    else
-      launch_cfg<128, 128, 2, 2, 4, AMODE>(g, e, stream);
+  } else if (g.N > 128 && 4 * mt256 * ((g.N + 255) / 256) >= 3 * cus) {
+    launch_cfg<256, 256, 2, 4, 3, AMODE>(g, e, stream);
   } else {
-    launch_cfg<256, 256, 2, 2, 3, AMODE>(g, e, stream);
+    launch_cfg<128, 128, 2, 2, 3, AMODE>(g, e, stream);
   }
   MR_LAUNCH_CHECK("qgemm");
   return MR_OK;

@@ -89,7 +89,8 @@ def _run_qmatmul(lib, x, q, ws, xs, steps_np, next_xs=None):
 
 
 @pytest.mark.parametrize("M,K,N", [(256, 64, 10), (64, 784, 512), (300, 512, 1000), (1, 4096, 4096),
-                                   (4096, 4096, 1000), (33, 128, 65), (70000, 64, 128)])
+                                   (4096, 4096, 1000), (33, 128, 65), (70000, 64, 128),
+                                   (49920, 160, 272)])    # 256x256 tiles, ragged K and N
 def test_qmatmul_bias_relu_requant(lib, M, K, N):
     rng = np.random.default_rng(M * 7 + N)
     x = rng.standard_normal((M, K)).astype(np.float32)
