@@ -501,6 +501,7 @@ int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int
   g.N = static_cast<int32_t>(N);
   g.n_pad = static_cast<int32_t>(n_pad);
   g.k_tiles = static_cast<int32_t>(k_pad / mr::BK);
+  if (M <= 8) return mr::gemv_launch(a, lda, b, k_pad, M, N, e, static_cast<hipStream_t>(stream));
   return mr::launch<mr::A_DENSE>(g, e, static_cast<hipStream_t>(stream));
 }
 

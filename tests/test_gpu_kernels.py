@@ -90,7 +90,8 @@ def _run_qmatmul(lib, x, q, ws, xs, steps_np, next_xs=None):
 
 @pytest.mark.parametrize("M,K,N", [(256, 64, 10), (64, 784, 512), (300, 512, 1000), (1, 4096, 4096),
                                    (4096, 4096, 1000), (33, 128, 65), (70000, 64, 128),
-                                   (49920, 160, 272)])    # 256x256 tiles, ragged K and N
+                                   (49920, 160, 272),     # 256x256 tiles, ragged K and N
+                                   (3, 4096, 1000), (8, 512, 65), (2, 64, 64), (5, 192, 130)])   # weight stream
 def test_qmatmul_bias_relu_requant(lib, M, K, N):
     rng = np.random.default_rng(M * 7 + N)
     x = rng.standard_normal((M, K)).astype(np.float32)
@@ -109,9 +110,10 @@ def test_qmatmul_bias_relu_requant(lib, M, K, N):
     assert bits_equal(yq, G.quantize_activation(want, next_xs).astype(np.int8))
 
 
-def test_qmatmul_every_epilogue_step(lib):
+@pytest.mark.parametrize("M", [200, 4])
+def test_qmatmul_every_epilogue_step(lib, M):
     rng = np.random.default_rng(11)
-    M, K, N = 200, 96, 48
+    K, N = 96, 48
     x = rng.standard_normal((M, K)).astype(np.float32)
     q = rng.integers(-127, 128, (K, N)).astype(np.int8)
     ws = rng.uniform(0.001, 0.01, N).astype(np.float32)
