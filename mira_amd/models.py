@@ -235,3 +235,109 @@ def conv_macs(g: Graph) -> int:
 
 
 __all__ = ["BUILDERS", "conv_out", "conv_macs"]
+
+
+# ---------------------------------------------------------------- character-level GPT, one decode step
+
+class GPTConfig:
+    """The decode configuration of the character-level GPT of examples/gpt_text.mira (with the
+    widths of examples/gpt_text_train.py:30): L layers of width D with H heads, MLP width F,
+    vocabulary V, and a KV cache of T positions (prompt + generated tokens)."""
+
+    def __init__(self, L: int = 2, D: int = 64, H: int = 4, F: int = 128, V: int = 65, T: int = 272):
+        self.L, self.D, self.H, self.F, self.V, self.T = L, D, H, F, V, T
+
+
+def gpt_params(cfg: GPTConfig, seed: int = 0) -> dict:
+    """Random weights with the distribution of mira/elaborate.py:1114-1123 (as `generate`'s
+    const parameters would get): embedding and position tables, per-layer projections and
+    layernorm gains/biases, final layernorm and output projection."""
+    rng = np.random.default_rng(seed)
+    D, F, V, T = cfg.D, cfg.F, cfg.V, cfg.T
+    p = {"emb": mira_random_weight(rng, (V, D)), "pos": mira_random_weight(rng, (T, D))}
+    for l in range(cfg.L):
+        for name, shape in (("wq", (D, D)), ("wk", (D, D)), ("wv", (D, D)), ("wo", (D, D)), ("w1", (D, F)),
+                            ("w2", (F, D)), ("g1", (D,)), ("b1", (D,)), ("g2", (D,)), ("b2", (D,))):
+            p[f"{name}{l}"] = mira_random_weight(rng, shape)
+    p["gf"], p["bf"] = mira_random_weight(rng, (D,)), mira_random_weight(rng, (D,))
+    p["wout"] = mira_random_weight(rng, (D, V))
+    return p
+
+
+def gpt_decode_step(cfg: GPTConfig, batch: int, params: dict) -> Graph:
+    """One decode step of `generate` (examples/gpt_text.mira, the while-loop body) as a graph
+    without control flow, so W8A8 can quantize it (mira/quantize.py:84-85 refuses control flow).
+
+    Inputs:  h     f32[B, D]        token embedding + position embedding of the current token
+             mask  f32[1,1,1,T+1]   0 for cache rows already written and for the current token,
+                                    -10000 elsewhere (the `(seen - 1) * 10000` of the reference)
+             kc{l}, vc{l} f32[B, T, D]  the layer's key/value cache
+    Outputs: logits f32[B, V], then k{l}, v{l} f32[B, D] for the host to write at the position.
+    The current token's key/value join the cache by concatenation (slot T), so the graph keeps
+    static shapes at every position."""
+    L, D, H, V, T = cfg.L, cfg.D, cfg.H, cfg.V, cfg.T
+    hd = D // H
+    g = Graph("gpt_step", [], [], [])
+    h = g.input("h", (batch, D))
+    mask = g.input("mask", (1, 1, 1, T + 1))
+    caches = [(g.input(f"kc{l}", (batch, T, D)), g.input(f"vc{l}", (batch, T, D))) for l in range(L)]
+    c = lambda name: g.const(params[name])
+    scale = g.const(np.float32(1.0 / np.sqrt(hd)))
+    kv_out = []
+    for l in range(L):
+        kc, vc = caches[l]
+        x = g.add("layernorm", [h, c(f"g1{l}"), c(f"b1{l}")], {"eps": 1e-5})
+        q = g.add("matmul", [x, c(f"wq{l}")])
+        k = g.add("matmul", [x, c(f"wk{l}")])
+        v = g.add("matmul", [x, c(f"wv{l}")])
+        kv_out += [k, v]
+        q4 = g.add("transpose", [g.add("reshape", [q], {"shape": (batch, 1, H, hd)})], {"perm": (0, 2, 1, 3)})
+        keys = g.add("concat", [kc, g.add("reshape", [k], {"shape": (batch, 1, D)})], {"axis": 1})
+        vals = g.add("concat", [vc, g.add("reshape", [v], {"shape": (batch, 1, D)})], {"axis": 1})
+        k4 = g.add("transpose", [g.add("reshape", [keys], {"shape": (batch, T + 1, H, hd)})], {"perm": (0, 2, 3, 1)})
+        v4 = g.add("transpose", [g.add("reshape", [vals], {"shape": (batch, T + 1, H, hd)})], {"perm": (0, 2, 1, 3)})
+        s = g.add("add", [g.add("mul", [g.add("matmul", [q4, k4]), scale]), mask])
+        o4 = g.add("matmul", [g.add("softmax", [s], {"axis": -1}), v4])
+        o = g.add("reshape", [g.add("transpose", [o4], {"perm": (0, 2, 1, 3)})], {"shape": (batch, D)})
+        h = g.add("add", [h, g.add("matmul", [o, c(f"wo{l}")])])
+        y = g.add("layernorm", [h, c(f"g2{l}"), c(f"b2{l}")], {"eps": 1e-5})
+        h = g.add("add", [h, g.add("matmul", [g.add("gelu", [g.add("matmul", [y, c(f"w1{l}")])]), c(f"w2{l}")])])
+    logits = g.add("matmul", [g.add("layernorm", [h, c("gf"), c("bf")], {"eps": 1e-5}), c("wout")])
+    g.outputs = [logits] + kv_out
+    return g
+
+
+def gpt_step_feeds(cfg: GPTConfig, params: dict, tokens: np.ndarray, t: int, caches: list) -> dict:
+    """Host side of one decode step at position t: embedding gather, position row, cache mask."""
+    h = (params["emb"][tokens[:, t]] + params["pos"][t]).astype(np.float32)
+    mask = np.full((1, 1, 1, cfg.T + 1), -10000.0, np.float32)
+    mask[..., :t] = 0.0
+    mask[..., cfg.T] = 0.0
+    feeds = {"h": h, "mask": mask}
+    for l, (kc, vc) in enumerate(caches):
+        feeds[f"kc{l}"], feeds[f"vc{l}"] = kc, vc
+    return feeds
+
+
+def gpt_decode(run, cfg: GPTConfig, params: dict, prompt: np.ndarray, new_tokens: int):
+    """Greedy decoding as `generate` does it (keep the prompt, then argmax), with `run(feeds) ->
+    [logits, k0, v0, ...]` executing one decode step.  Returns tokens [B, P + new_tokens] and the
+    logits of every step."""
+    B, P = prompt.shape
+    total = P + new_tokens
+    assert total <= cfg.T
+    tokens = np.zeros((B, total), np.int32)
+    tokens[:, :P] = prompt
+    caches = [(np.zeros((B, cfg.T, cfg.D), np.float32), np.zeros((B, cfg.T, cfg.D), np.float32))
+              for _ in range(cfg.L)]
+    all_logits = []
+    for t in range(total - 1):
+        out = run(gpt_step_feeds(cfg, params, tokens, t, caches))
+        logits = out[0]
+        all_logits.append(logits)
+        for l in range(cfg.L):
+            caches[l][0][:, t] = out[1 + 2 * l]
+            caches[l][1][:, t] = out[2 + 2 * l]
+        if t + 1 >= P:
+            tokens[:, t + 1] = np.argmax(logits, axis=1)
+    return tokens, all_logits

@@ -138,3 +138,77 @@ def test_resnet18_batch2_fused_stem():
     (got,) = runner.run_list([x])
     (want,) = G.run_graph(g, {"x": x})
     assert bits_equal(got, want)
+
+
+# ---------------------------------------------------------------- character-level GPT decode (small-M qmatmul)
+
+def _gpt_quantized(batch, peaks=None):
+    cfg = models.GPTConfig()
+    params = models.gpt_params(cfg, 0)
+    g = models.gpt_decode_step(cfg, batch, params)
+    passes.optimize(g)
+    if peaks is None:
+        calib = []
+        for s in (2, 3):
+            r = np.random.default_rng(s)
+            toks = r.integers(0, cfg.V, (batch, cfg.T)).astype(np.int32)
+            caches = [(r.standard_normal((batch, cfg.T, cfg.D)).astype(np.float32),
+                       r.standard_normal((batch, cfg.T, cfg.D)).astype(np.float32)) for _ in range(cfg.L)]
+            calib.append(models.gpt_step_feeds(cfg, params, toks, 16, caches))
+        peaks = calibration_peaks(g, calib)
+    quantize_w8a8(g, peaks=peaks)
+    return cfg, params, g, peaks
+
+
+def _gpt_runner(g, debug_acc=False):
+    runner = compile_graph(g, RocmTarget(debug_acc=debug_acc), fallback=G.CPUTarget())
+    assert "rocm" in [s.device for s in runner.segments]
+    return runner
+
+
+def test_gpt_decode_step_batch2():
+    """One decode step: the W8A8 projections on rocm (weight-streaming kernel, M = 2), attention,
+    softmax, layernorm and the gelu-fused projection on the cpu fallback; every accumulator and
+    output bit-exact."""
+    cfg, params, g, _ = _gpt_quantized(2)
+    r = np.random.default_rng(9)
+    toks = r.integers(0, cfg.V, (2, cfg.T)).astype(np.int32)
+    caches = [(r.standard_normal((2, cfg.T, cfg.D)).astype(np.float32),
+               r.standard_normal((2, cfg.T, cfg.D)).astype(np.float32)) for _ in range(cfg.L)]
+    feeds = models.gpt_step_feeds(cfg, params, toks, 20, caches)
+    runner = _compare(g, feeds)
+    gelu_q = [op for op in g.compute_ops() if op.kind == "qmatmul" and op.attrs.get("epilogue", ())
+              and op.attrs["epilogue"][0][0] == "gelu"]
+    assert len(gelu_q) == cfg.L and all("gelu" in runner.placement.reason[op] for op in gelu_q)
+
+
+def test_gpt_greedy_decode_batch2():
+    """Autoregressive greedy decoding from a seeded 16-token prompt: rocm and the oracle produce
+    the same tokens and the same logits at every step."""
+    cfg, params, g, _ = _gpt_quantized(2)
+    prompt = np.random.default_rng(4).integers(0, cfg.V, (2, 16)).astype(np.int32)
+    runner = _gpt_runner(g)
+    names = [v.name for v in g.inputs]
+    got_tok, got_logits = models.gpt_decode(lambda f: runner.run_list([f[n] for n in names]), cfg, params, prompt, 8)
+    want_tok, want_logits = models.gpt_decode(lambda f: G.run_graph(g, f), cfg, params, prompt, 8)
+    assert np.array_equal(got_tok, want_tok)
+    for a, b in zip(got_logits, want_logits):
+        assert bits_equal(a, b)
+
+
+def test_gpt_decode_step_batch512_rows():
+    cfg, params, g2, peaks = _gpt_quantized(2)
+    _, _, g, _ = _gpt_quantized(512, peaks=peaks)
+    r = np.random.default_rng(5)
+    toks = r.integers(0, cfg.V, (512, cfg.T)).astype(np.int32)
+    caches = [(r.standard_normal((512, cfg.T, cfg.D)).astype(np.float32),
+               r.standard_normal((512, cfg.T, cfg.D)).astype(np.float32)) for _ in range(cfg.L)]
+    feeds = models.gpt_step_feeds(cfg, params, toks, 100, caches)
+    runner = _gpt_runner(g)
+    got = runner.run_list([feeds[v.name] for v in g.inputs])
+    rows = [0, 317, 511]
+    small = {k: (v[rows] if k != "mask" else v) for k, v in feeds.items()}
+    _, _, g3, _ = _gpt_quantized(3, peaks=peaks)
+    want = G.run_graph(g3, small)
+    for a, b in zip(got, want):
+        assert bits_equal(a[rows], b)

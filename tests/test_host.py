@@ -211,3 +211,27 @@ def test_requant_reciprocal_is_exact():
         xv = np.full(ys.shape, x, np.float32)
         _, r = _quantize_by_f64_reciprocal(ys, xv)
         assert np.array_equal(r, _quantize_by_division(ys, xv))
+
+
+def test_gpt_decode_step_graph_and_placement():
+    """The decode step verifies, W8A8 quantizes its 6 projections per layer plus the output
+    projection, and the rocm target takes every projection except the gelu-fused ones (gelu's
+    tanh is libm-dependent, so it stays with the cpu target as MIRA's partitioner would send it)."""
+    cfg = models.GPTConfig()
+    params = models.gpt_params(cfg, 0)
+    g = models.gpt_decode_step(cfg, 2, params)
+    passes.optimize(g)
+    r = np.random.default_rng(2)
+    toks = r.integers(0, cfg.V, (2, cfg.T)).astype(np.int32)
+    caches = [(r.standard_normal((2, cfg.T, cfg.D)).astype(np.float32),
+               r.standard_normal((2, cfg.T, cfg.D)).astype(np.float32)) for _ in range(cfg.L)]
+    feeds = models.gpt_step_feeds(cfg, params, toks, 16, caches)
+    from mira_amd.quantize import calibration_peaks
+    quantize_w8a8(g, peaks=calibration_peaks(g, [feeds]))
+    qops = [op for op in g.compute_ops() if op.kind == "qmatmul"]
+    assert len(qops) == 6 * cfg.L + 1
+    tgt = RocmTarget()
+    rejected = [op for op in qops if tgt.check(op)]
+    assert len(rejected) == cfg.L and all(op.attrs["epilogue"][0][0] == "gelu" for op in rejected)
+    logits, *kv = G.run_graph(g, feeds)
+    assert logits.shape == (2, cfg.V) and np.isfinite(logits).all() and len(kv) == 2 * cfg.L
