@@ -444,24 +444,24 @@ static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
 
 template <int AMODE>
 static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
-  // Tile choice (measured on the ResNet-18 conv shapes and dense GEMMs):
-  // 256x256 tiles with 8 waves (2 per SIMD) once there are enough of them to
-  // cover most CUs; otherwise 128x128 tiles (three workgroups fit a CU);
-  // narrow tiles for N <= 64.
+  // Tile choice, measured on the ResNet-18 conv shapes and dense GEMMs: three
+  // LDS stages and small enough tiles that 3-4 workgroups share a CU (their
+  // epilogues and barrier waits overlap each other's MFMAs), with wave tiles
+  // of 32x64 (N <= 64), 64x64 (N <= 128) or 64x64 with 8 waves over a
+  // 128x256 tile (larger N; 256x256 once the grid is large).
   const int64_t cus = device_cu_count();
   const int64_t mt256 = (g.M + 255) / 256;
   MR_REQUIRE((g.M + 63) / 64 * ((g.N + 31) / 32) < (int64_t(1) << 31), "problem too large");
   if (g.N <= 32) {
     launch_cfg<64, 32, 2, 1, 4, AMODE>(g, e, stream);
   } else if (g.N <= 64) {
-    if (mt256 >= 2 * cus)
-      launch_cfg<256, 64, 4, 1, 4, AMODE>(g, e, stream);
-    else
-      launch_cfg<128, 64, 2, 1, 4, AMODE>(g, e, stream);
-  } else if (g.N > 128 && 4 * mt256 * ((g.N + 255) / 256) >= 3 * cus) {
+    launch_cfg<128, 64, 4, 1, 3, AMODE>(g, e, stream);
+  } else if (g.N <= 128) {
+    launch_cfg<128, 128, 2, 2, 3, AMODE>(g, e, stream);
+  } else if (mt256 * ((g.N + 255) / 256) >= 4 * cus) {
     launch_cfg<256, 256, 2, 4, 3, AMODE>(g, e, stream);
   } else {
-    launch_cfg<128, 128, 2, 2, 3, AMODE>(g, e, stream);
+    launch_cfg<128, 256, 2, 4, 3, AMODE>(g, e, stream);
   }
   MR_LAUNCH_CHECK("qgemm");
   return MR_OK;
