@@ -41,11 +41,17 @@ def test_quantize_rows(lib, rows, cols, xs):
     assert not got[:, cols:].any()
 
 
-@pytest.mark.parametrize("n,c,h,w", [(3, 3, 21, 19), (2, 20, 5, 6), (1, 1, 28, 28)])
-def test_quantize_nchw_nhwc(lib, n, c, h, w):
+@pytest.mark.parametrize("n,c,h,w,ties", [(3, 3, 21, 19, False), (2, 20, 5, 6, False), (1, 1, 28, 28, False),
+                                           (2, 3, 8, 12, True), (2, 20, 6, 6, True), (3, 4, 7, 4, False)])
+def test_quantize_nchw_nhwc(lib, n, c, h, w, ties):
+    """Both kernels: any pixel count, and four pixels per thread when h*w % 4 == 0."""
     torch = _torch()
-    rng = np.random.default_rng(c)
+    rng = np.random.default_rng(c + h)
     x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    if ties:    # values on and next to the half-way points of the int8 grid
+        k = rng.integers(-140, 140, x.shape) + 0.5
+        x = (k / 127).astype(np.float32)
+        x.reshape(-1)[::3] = np.nextafter(x.reshape(-1)[::3], np.float32(np.inf))
     cp = pack.c_pad_for(c)
     q = empty((n, h, w, cp), torch.int8)
     xs = float(np.float32(1 / 127))
