@@ -25,6 +25,8 @@
 // (lane & 31) and rows 8*(r/4) + 4*(lane/32) + (r%4), r = 0..15.
 #include "mr_common.hpp"
 
+#include <algorithm>
+
 namespace mr {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -38,8 +40,14 @@ enum AMode {
   A_DENSE = 0,   // row-major [M, lda] int8
   A_CONV64 = 1,  // NHWC, c_pad % 64 == 0: a 64-byte K step is one tap, one channel block
   A_CONV16 = 2,  // NHWC, c_pad % 16 == 0: K steps may span taps
-  A_CONV4 = 3    // NHWC, c_pad == 4: each 16-byte chunk is 4 taps of one kernel row
+  A_CONV4 = 3,   // NHWC, c_pad == 4: each 16-byte chunk is 4 taps of one kernel row
+  A_PATCH = 4    // NHWC, c_pad % 64 == 0, stride 1, dilation 1: A fragments read from a
+                 // per-tile input patch (tile rows plus the kernel's halo) held in LDS
 };
+
+// A_PATCH: LDS bytes reserved for one tile's input patch, and the tile height.
+constexpr int PATCH_MAX = 24576;
+constexpr int PATCH_BM = 128;
 
 struct GemmArgs {
   const int8_t* a;  // dense: [M, lda]; conv: NHWC input
@@ -56,7 +64,10 @@ struct GemmArgs {
   int32_t H, W, C_pad, OH, OW, KH, KW, SH, SW, PH, PW, DH, DW;
   int32_t row_bytes;  // A_CONV4: packed bytes per kernel row
   int32_t k_real;     // A_CONV16: KH*KW*C_pad
-  int32_t cb_per_tap; // A_CONV64: C_pad / 64
+  int32_t cb_per_tap; // A_CONV64 / A_PATCH: C_pad / 64
+  // A_PATCH: a tile is `tr` output rows of one image (tr * OW <= BM pixels);
+  // its patch is pr x pc input pixels (rows oh0-PH .. oh0-PH+pr-1, columns -PW .. pc-PW-1)
+  int32_t tr, rg_per_img, pr, pc, patch_slots;
 };
 
 constexpr int BK = 64;
@@ -193,16 +204,25 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
   constexpr int FM = TM / 32;
   constexpr int FN = TN / 32;
   constexpr int NB = FM * FN;
+  constexpr bool PATCH = AMODE == A_PATCH;
   constexpr int A_ROWS_PER_OP = AMODE == A_CONV4 ? 4 : 16;   // rows one wave-wide DMA covers
-  constexpr int A_OPS = BM / A_ROWS_PER_OP / NW;               // A DMAs per wave per K step
+  constexpr int A_OPS = PATCH ? 0 : BM / A_ROWS_PER_OP / NW;   // A DMAs per wave per K step
+  constexpr int A_OPS1 = A_OPS > 0 ? A_OPS : 1;
   constexpr int B_OPS = BN / 16 / NW;
   constexpr int OPS = A_OPS + B_OPS;
-  constexpr int STAGE_BYTES = (BM + BN) * BK;
+  constexpr int A_STAGE = PATCH ? 0 : BM * BK;                  // A bytes in one ring stage
+  constexpr int STAGE_BYTES = A_STAGE + BN * BK;
+  constexpr int PATCH_OPS = PATCH ? PATCH_MAX / 16 / (NW * 64) : 0;   // patch DMAs per wave
+  constexpr int RING_BYTES = STAGES * STAGE_BYTES;
+  constexpr int LDS_BYTES = RING_BYTES + (PATCH ? PATCH_MAX : 0);
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32");
-  static_assert(A_OPS * A_ROWS_PER_OP * NW == BM && B_OPS * 16 * NW == BN, "loader mapping");
+  static_assert(PATCH || (A_OPS * A_ROWS_PER_OP * NW == BM), "loader mapping");
+  static_assert(B_OPS * 16 * NW == BN, "loader mapping");
+  static_assert(!PATCH || PATCH_OPS * 16 * NW * 64 == PATCH_MAX, "patch loader mapping");
   static_assert(STAGES >= 3 && (STAGES - 2) * OPS < 64, "stages / vmcnt range");
 
-  __shared__ __attribute__((aligned(1024))) int8_t lds[STAGES * STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) int8_t lds[LDS_BYTES];
+  int8_t* const patch = lds + RING_BYTES;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -228,11 +248,21 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
   const int tile_n = tin / gsize;
   const int64_t m0 = int64_t(tile_m) * BM;
   const int n0 = tile_n * BN;
+  // result rows of the tile: mbase + 0 .. mbase + mvalid - 1
+  int64_t mbase = m0;
+  int mvalid = static_cast<int>(min(int64_t(BM), g.M - m0));
+  int p_img = 0, p_oh0 = 0;
+  if constexpr (PATCH) {
+    p_img = tile_m / g.rg_per_img;
+    p_oh0 = (tile_m - p_img * g.rg_per_img) * g.tr;
+    mbase = (int64_t(p_img) * g.OH + p_oh0) * g.OW;
+    mvalid = min(g.tr, g.OH - p_oh0) * g.OW;
+  }
 
   // ---- A loader state, one entry per DMA this lane takes part in
-  int64_t a_base[A_OPS];   // dense: m*lda + chunk offset; conv: image pixel base
-  int32_t a_ih0[A_OPS], a_iw0[A_OPS], a_k[A_OPS];
-  bool a_ok[A_OPS];
+  int64_t a_base[A_OPS1];   // dense: m*lda + chunk offset; conv: image pixel base
+  int32_t a_ih0[A_OPS1], a_iw0[A_OPS1], a_k[A_OPS1];
+  bool a_ok[A_OPS1];
 #pragma unroll
   for (int j = 0; j < A_OPS; ++j) {
     const int slot = (wave * A_OPS + j) * 64 + lane;
@@ -281,7 +311,7 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
 
   auto issue = [&](int kt, int stage) {
     int8_t* As = lds + stage * STAGE_BYTES;
-    int8_t* Bs = As + BM * BK;
+    int8_t* Bs = As + A_STAGE;
 #pragma unroll
     for (int j = 0; j < A_OPS; ++j) {
       const void* src = g_zero_page;
@@ -340,6 +370,32 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[b][r] = 0;
 
+  // A_PATCH: 16-byte chunk j of patch pixel P (P = r * pc + c) sits at slot
+  // P * U + (j ^ patch_swz(P)), U = C_pad / 16 in {4, 8, 16}: 16 consecutive
+  // pixels of one chunk then fall on 16 distinct 16-byte bank groups, as in
+  // the ring.
+  const int pU = g.C_pad >> 4;
+  auto patch_swz = [&](int P) __attribute__((always_inline)) {
+    return ((P * pU) >> 4) & (pU - 1);
+  };
+  if constexpr (PATCH) {
+#pragma unroll
+    for (int j = 0; j < PATCH_OPS; ++j) {
+      const int slot = (wave * PATCH_OPS + j) * 64 + lane;
+      const void* src = g_zero_page;
+      if (slot < g.patch_slots) {
+        const int P = slot / pU;
+        const int chunk = (slot - P * pU) ^ patch_swz(P);
+        const int r = P / g.pc;
+        const int ih = p_oh0 - g.PH + r;
+        const int iw = P - r * g.pc - g.PW;
+        if (unsigned(ih) < unsigned(g.H) && unsigned(iw) < unsigned(g.W))
+          src = g.a + ((int64_t(p_img) * g.H + ih) * g.W + iw) * g.C_pad + chunk * 16;
+      }
+      dma16(src, patch + (wave * PATCH_OPS + j) * 1024);
+    }
+  }
+
   const int KT = g.k_tiles;
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
@@ -349,13 +405,35 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
   // bytes 16h .. 16h+15 of the half for row r of each 32-row block.
   const int frag_row = lane & 31;
   const int swz = (frag_row >> 2) & 3;
-  auto load_frags = [&](int stage, int kk, v4i (&af)[FM], v4i (&bf)[FN]) {
+  // A_PATCH: patch pixel of each fragment row at tap (0, 0); rows past the
+  // tile's valid pixels read pixel 0 (their results are never stored)
+  int p_pix0[PATCH ? FM : 1];
+  if constexpr (PATCH) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      int p = wm * TM + i * 32 + frag_row;
+      if (p >= mvalid) p = 0;
+      const int orow = p / g.OW;
+      p_pix0[i] = orow * g.pc + (p - orow * g.OW);
+    }
+  }
+  // read cursor of A_PATCH for the step being read: patch offset kh * pc + kw
+  // of its tap, that tap's kw, and its channel block (scalars in registers)
+  int q_off = 0, q_kw = 0, q_cb = 0;
+  auto load_frags = [&](int stage, int kk, int off, int cb, v4i (&af)[FM], v4i (&bf)[FN]) {
     const int8_t* As = lds + stage * STAGE_BYTES;
-    const int8_t* Bs = As + BM * BK;
+    const int8_t* Bs = As + A_STAGE;
     const int pc = ((2 * kk + (lane >> 5)) ^ swz) << 4;
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
-      af[i] = *reinterpret_cast<const v4i*>(As + (wm * TM + i * 32 + frag_row) * BK + pc);
+    for (int i = 0; i < FM; ++i) {
+      if constexpr (PATCH) {
+        const int P = p_pix0[i] + off;
+        const int chunk = (cb * 4 + 2 * kk + (lane >> 5)) ^ patch_swz(P);
+        af[i] = *reinterpret_cast<const v4i*>(patch + (P * pU + chunk) * 16);
+      } else {
+        af[i] = *reinterpret_cast<const v4i*>(As + (wm * TM + i * 32 + frag_row) * BK + pc);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < FN; ++j)
       bf[j] = *reinterpret_cast<const v4i*>(Bs + (wn * TN + j * 32 + frag_row) * BK + pc);
@@ -375,10 +453,20 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
   v4i a0[FM], b0[FN], a1[FM], b1[FN];
   if (KT >= STAGES - 1) wait_vmcnt<(STAGES - 2) * OPS>(); else wait_vmcnt<0>();
   block_barrier();
-  load_frags(0, 0, a0, b0);
+  load_frags(0, 0, q_off, q_cb, a0, b0);
   for (int kt = 0; kt < KT; ++kt) {
     const int cur = kt % STAGES;
-    load_frags(cur, 1, a1, b1);
+    load_frags(cur, 1, q_off, q_cb, a1, b1);
+    if constexpr (PATCH) {   // advance the cursor to step kt + 1
+      if (++q_cb == g.cb_per_tap) {
+        q_cb = 0;
+        ++q_off;
+        if (++q_kw == g.KW) {
+          q_kw = 0;
+          q_off += g.pc - g.KW;
+        }
+      }
+    }
     mfma_all(a0, b0);
     if (kt + 1 < KT) {
       if (kt + STAGES - 2 < KT)
@@ -387,7 +475,7 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
         wait_vmcnt<0>();
       block_barrier();
       if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-      load_frags((kt + 1) % STAGES, 0, a0, b0);
+      load_frags((kt + 1) % STAGES, 0, q_off, q_cb, a0, b0);
     }
     mfma_all(a1, b1);
   }
@@ -400,7 +488,7 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
   constexpr int EP_LD = BN + 4;                     // int32 row stride (16-byte pad)
   constexpr int CG = BN / 4;                        // 4-column groups per row
   constexpr int RSTEP = (WM * WN * 64) / CG;        // rows walked concurrently
-  static_assert(EP_ROWS * EP_LD * 4 <= STAGES * STAGE_BYTES, "epilogue staging exceeds LDS");
+  static_assert(EP_ROWS * EP_LD * 4 <= LDS_BYTES, "epilogue staging exceeds LDS");
   static_assert((WM * WN * 64) % CG == 0, "epilogue thread mapping");
   int32_t* ep = reinterpret_cast<int32_t*>(lds);
   const int cgi = threadIdx.x % CG;
@@ -419,8 +507,9 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
             acc[pass * FN + j][r];
     block_barrier();
     for (int rr = threadIdx.x / CG; rr < EP_ROWS; rr += RSTEP) {
-      const int64_t row = m0 + (rr >> 5) * TM + pass * 32 + (rr & 31);
-      if (row >= g.M || col0 >= g.N) continue;
+      const int local = (rr >> 5) * TM + pass * 32 + (rr & 31);
+      if (local >= mvalid || col0 >= g.N) continue;
+      const int64_t row = mbase + local;
       const v4i a = *reinterpret_cast<const v4i*>(ep + rr * EP_LD + cgi * 4);
       store_row4<FIXED>(e, cols, a, row, col0, g.N);
     }
@@ -431,7 +520,8 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
 
 template <int BM, int BN, int WM, int WN, int STAGES, int AMODE>
 static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
-  g.tiles_m = static_cast<int32_t>((g.M + BM - 1) / BM);
+  g.tiles_m = AMODE == A_PATCH ? static_cast<int32_t>(g.M / (int64_t(g.OH) * g.OW)) * g.rg_per_img
+                               : static_cast<int32_t>((g.M + BM - 1) / BM);
   g.tiles_n = (g.N + BN - 1) / BN;
   const unsigned blocks = static_cast<unsigned>(int64_t(g.tiles_m) * g.tiles_n);
   if (e.fixed)
@@ -452,7 +542,12 @@ static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
   const int64_t cus = device_cu_count();
   const int64_t mt256 = (g.M + 255) / 256;
   MR_REQUIRE((g.M + 63) / 64 * ((g.N + 31) / 32) < (int64_t(1) << 31), "problem too large");
-  if (g.N <= 32) {
+  if constexpr (AMODE == A_PATCH) {   // the host picks this mode for N <= 128 only
+    if (g.N <= 64)
+      launch_cfg<PATCH_BM, 64, 4, 1, 3, AMODE>(g, e, stream);
+    else
+      launch_cfg<PATCH_BM, 128, 2, 2, 3, AMODE>(g, e, stream);
+  } else if (g.N <= 32) {
     launch_cfg<64, 32, 2, 1, 4, AMODE>(g, e, stream);
   } else if (g.N <= 64) {
     launch_cfg<128, 64, 4, 1, 3, AMODE>(g, e, stream);
@@ -569,8 +664,27 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
   g.row_bytes = row_bytes;
   g.k_real = k_real;
   g.cb_per_tap = G.c_pad / 64;
+  // stride-1 convolutions with a halo (3x3 and the like) read A from a
+  // per-tile input patch: each input pixel crosses L2 -> LDS about
+  // (tr + kh - 1) / tr times instead of kh * kw times
+  if (mode == mr::A_CONV64 && (G.c_pad & (G.c_pad - 1)) == 0 && G.c_pad <= 256 && G.sh == 1 && G.sw == 1 &&
+      G.dh == 1 && G.dw == 1 && G.kh * G.kw > 1 && G.o <= 128 && ow <= mr::PATCH_BM) {
+    const int32_t tr = std::min(mr::PATCH_BM / ow, oh);
+    const int32_t pr = tr + G.kh - 1, pc = ow + G.kw - 1;
+    const int64_t slots = int64_t(pr) * pc * (G.c_pad / 16);
+    if (slots * 16 <= mr::PATCH_MAX) {
+      g.tr = tr;
+      g.rg_per_img = (oh + tr - 1) / tr;
+      g.pr = pr;
+      g.pc = pc;
+      g.patch_slots = static_cast<int32_t>(slots);
+      MR_REQUIRE(int64_t(G.n) * g.rg_per_img < (int64_t(1) << 31), "mr_qconv2d: too many tiles");
+      mode = mr::A_PATCH;
+    }
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (mode) {
+    case mr::A_PATCH: return mr::launch<mr::A_PATCH>(g, e, s);
     case mr::A_CONV4: return mr::launch<mr::A_CONV4>(g, e, s);
     case mr::A_CONV64: return mr::launch<mr::A_CONV64>(g, e, s);
     default: return mr::launch<mr::A_CONV16>(g, e, s);

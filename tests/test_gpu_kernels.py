@@ -162,6 +162,14 @@ CONV_CASES = [
     (3, 24, 9, 9, 144, 1, 1, 0, 1),       # c_pad 32
     (2, 16, 11, 11, 24, 3, 1, 2, 2),      # dilation 2
     (2, 1, 28, 28, 16, 3, 1, 1, 1),       # single channel (cnn.mira)
+    # stride-1 convolutions read through the per-tile input patch
+    (2, 64, 56, 56, 64, 3, 1, 1, 1),      # ResNet layer 1 (2 output rows per tile)
+    (2, 128, 28, 28, 128, 3, 1, 1, 1),    # ResNet layer 2 (4 rows per tile, 8 chunks per pixel)
+    (1, 256, 7, 7, 96, 3, 1, 1, 1),       # 16 chunks per pixel, 96 of 128 columns
+    (3, 64, 20, 20, 40, 3, 1, 1, 1),      # last tile of each image 2 of 6 rows
+    (2, 64, 11, 120, 64, 3, 1, 1, 1),     # one output row per tile
+    (2, 64, 12, 12, 32, 5, 1, 2, 1),      # 5x5, pad 2
+    (1, 64, 6, 9, 64, 3, 1, 0, 1),        # no padding
 ]
 
 
