@@ -45,6 +45,49 @@ enum AMode {
                  // per-tile input patch (tile rows plus the kernel's halo) held in LDS
 };
 
+// Epilogue forms a kernel is compiled for: EF_GENERIC runs the step
+// interpreter, EF_FIXED the fixed form (see EpiDev) with its flags read at run
+// time, and EF_SPEC | SF_* the fixed form with its steps and outputs known at
+// compile time: a tile whose columns are all in range then runs its rows as
+// straight-line code (all LDS reads, then all operand loads, then the math and
+// the stores), so the rows' latencies overlap.
+constexpr int EF_GENERIC = 0, EF_FIXED = 1, EF_SPEC = 0x100;
+constexpr int SF_COL = 1, SF_FULL = 2, SF_LO = 4, SF_HI = 8, SF_F32 = 16, SF_I8 = 32;
+// the forms with compiled kernels: bias+ReLU -> int8; bias+residual+ReLU -> f32
+// and/or int8; bias -> f32 (ResNet blocks, downsample and fc layers, MLPs)
+constexpr int SPEC_RELU_I8 = SF_COL | SF_LO | SF_I8;
+constexpr int SPEC_RES_F32_I8 = SF_COL | SF_FULL | SF_LO | SF_F32 | SF_I8;
+constexpr int SPEC_RES_I8 = SF_COL | SF_FULL | SF_LO | SF_I8;
+constexpr int SPEC_RES_F32 = SF_COL | SF_FULL | SF_LO | SF_F32;
+constexpr int SPEC_BIAS_F32 = SF_COL | SF_F32;
+
+// The compile-time form of an epilogue, or -1 when it has none: the fixed
+// form without an int32 accumulator output, every output and operand row
+// 16-byte (f32) / 4-byte (int8) aligned.
+static int spec_form(const EpiDev& e) {
+  if (!e.fixed || e.out_acc) return -1;
+  auto al = [](const void* p, int64_t ld, int bytes) {
+    return reinterpret_cast<uintptr_t>(p) % bytes == 0 && ld % 4 == 0;
+  };
+  int f = 0;
+  if (e.f_col) f |= SF_COL;
+  if (e.f_full) {
+    if (!al(e.full_ptr, e.full_ld, 16)) return -1;
+    f |= SF_FULL;
+  }
+  if (e.f_lo) f |= SF_LO;
+  if (e.f_hi) f |= SF_HI;
+  if (e.out_f32) {
+    if (!al(e.out_f32, e.ldo, 16)) return -1;
+    f |= SF_F32;
+  }
+  if (e.out_i8) {
+    if (!al(e.out_i8, e.ldq, 4)) return -1;
+    f |= SF_I8;
+  }
+  return f;
+}
+
 // A_PATCH: LDS bytes reserved for one tile's input patch, and the tile height.
 constexpr int PATCH_MAX = 24576;
 constexpr int PATCH_BM = 128;
@@ -196,7 +239,7 @@ __device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, c
   }
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int AMODE, bool FIXED>
+template <int BM, int BN, int WM, int WN, int STAGES, int AMODE, int EF>
 __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, const EpiDev e) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM;
@@ -506,12 +549,68 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
         ep[(wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * EP_LD + wn * TN + j * 32 + (lane & 31)] =
             acc[pass * FN + j][r];
     block_barrier();
+    if constexpr (EF >= EF_SPEC) {
+      if (n0 + BN <= g.N) {
+        constexpr bool S_COL = EF & SF_COL, S_FULL = EF & SF_FULL, S_LO = EF & SF_LO, S_HI = EF & SF_HI;
+        constexpr bool S_F32 = EF & SF_F32, S_I8 = EF & SF_I8;
+        constexpr int NR = EP_ROWS / RSTEP;
+        static_assert(EP_ROWS % RSTEP == 0, "epilogue rows per thread");
+        // rows in flight at once: all of them, or 4 when each also holds a residual
+        constexpr int NRC = S_FULL && NR > 4 ? 4 : NR;
+        static_assert(NR % NRC == 0, "epilogue row chunks");
+#pragma unroll
+        for (int k0 = 0; k0 < NR; k0 += NRC) {
+        int local[NRC];
+        v4i a[NRC];
+        float4 res[S_FULL ? NRC : 1];
+#pragma unroll
+        for (int k = 0; k < NRC; ++k) {
+          const int rr = threadIdx.x / CG + (k0 + k) * RSTEP;
+          local[k] = (rr >> 5) * TM + pass * 32 + (rr & 31);
+          a[k] = *reinterpret_cast<const v4i*>(ep + rr * EP_LD + cgi * 4);
+        }
+        if constexpr (S_FULL) {
+#pragma unroll
+          for (int k = 0; k < NRC; ++k) {   // rows past the tile re-read its last row
+            const int64_t r = mbase + min(local[k], mvalid - 1);
+            res[k] = *reinterpret_cast<const float4*>(e.full_ptr + r * e.full_ld + col0);
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < NRC; ++k) {
+          float y[4];
+          const float o[4] = {res[S_FULL ? k : 0].x, res[S_FULL ? k : 0].y, res[S_FULL ? k : 0].z,
+                              res[S_FULL ? k : 0].w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            y[c] = dequant(a[k][c], cols.scale[c]);
+            if constexpr (S_COL) y[c] = __fadd_rn(y[c], cols.colv[c]);
+            if constexpr (S_FULL) y[c] = __fadd_rn(y[c], o[c]);
+            if constexpr (S_LO) y[c] = max_bound(y[c], cols.lo, cols.lo_nan);
+            if constexpr (S_HI) y[c] = min_bound(y[c], cols.hi, cols.hi_nan);
+          }
+          if (local[k] < mvalid) {
+            const int64_t row = mbase + local[k];
+            if constexpr (S_F32)
+              *reinterpret_cast<float4*>(e.out_f32 + row * e.ldo + col0) = make_float4(y[0], y[1], y[2], y[3]);
+            if constexpr (S_I8) {
+              uint32_t packed = 0;
+#pragma unroll
+              for (int c = 0; c < 4; ++c) packed |= uint32_t(quantize_med3(y[c], e.out_rxs) & 0xff) << (8 * c);
+              *reinterpret_cast<uint32_t*>(e.out_i8 + row * e.ldq + col0) = packed;
+            }
+          }
+        }
+        }
+        continue;
+      }
+    }
     for (int rr = threadIdx.x / CG; rr < EP_ROWS; rr += RSTEP) {
       const int local = (rr >> 5) * TM + pass * 32 + (rr & 31);
       if (local >= mvalid || col0 >= g.N) continue;
       const int64_t row = mbase + local;
       const v4i a = *reinterpret_cast<const v4i*>(ep + rr * EP_LD + cgi * 4);
-      store_row4<FIXED>(e, cols, a, row, col0, g.N);
+      store_row4<EF != EF_GENERIC>(e, cols, a, row, col0, g.N);
     }
   }
 }
@@ -523,13 +622,31 @@ static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
   g.tiles_m = AMODE == A_PATCH ? static_cast<int32_t>(g.M / (int64_t(g.OH) * g.OW)) * g.rg_per_img
                                : static_cast<int32_t>((g.M + BM - 1) / BM);
   g.tiles_n = (g.N + BN - 1) / BN;
-  const unsigned blocks = static_cast<unsigned>(int64_t(g.tiles_m) * g.tiles_n);
+  const dim3 grid(static_cast<unsigned>(int64_t(g.tiles_m) * g.tiles_n)), block(WM * WN * 64);
+#define MR_QGEMM_LAUNCH(EFV) hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, STAGES, AMODE, EFV>), grid, block, 0, \
+                                                stream, g, e)
+  // compiled forms: the conv modes of the ResNet-style networks and the dense GEMM
+  constexpr bool CONV_SPEC = AMODE == A_CONV64 || AMODE == A_PATCH;
+  if constexpr (CONV_SPEC || AMODE == A_DENSE) {
+    switch (spec_form(e)) {
+      case SPEC_RELU_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RELU_I8); return;
+      case SPEC_BIAS_F32: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_F32); return;
+      default: break;
+    }
+  }
+  if constexpr (CONV_SPEC) {
+    switch (spec_form(e)) {
+      case SPEC_RES_F32_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_F32_I8); return;
+      case SPEC_RES_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_I8); return;
+      case SPEC_RES_F32: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_F32); return;
+      default: break;
+    }
+  }
   if (e.fixed)
-    hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, STAGES, AMODE, true>), dim3(blocks), dim3(WM * WN * 64), 0,
-                       stream, g, e);
+    MR_QGEMM_LAUNCH(EF_FIXED);
   else
-    hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, STAGES, AMODE, false>), dim3(blocks), dim3(WM * WN * 64), 0,
-                       stream, g, e);
+    MR_QGEMM_LAUNCH(EF_GENERIC);
+#undef MR_QGEMM_LAUNCH
 }
 
 template <int AMODE>

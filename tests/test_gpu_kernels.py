@@ -216,6 +216,108 @@ def test_qconv2d(lib, n, c, h, w, o, k, s, p, d):
     assert bits_equal(yq.cpu().numpy()[:, :o], to_nhwc(G.quantize_activation(want, next_xs)).astype(np.int8))
 
 
+# Epilogue forms the kernels compile straight-line code for (no int32
+# accumulator output): each output kind and step combination on the conv
+# loader modes that carry them, plus a form outside the list (fallback).
+FORMS = {
+    "relu_i8": ((("add", 1, False), ("relu", None, False)), False, True),
+    "res_f32_i8": ((("add", 1, False), ("add", 2, False), ("relu", None, False)), True, True),
+    "res_i8": ((("add", 1, False), ("add", 2, False), ("relu", None, False)), False, True),
+    "res_f32": ((("add", 1, False), ("add", 2, False), ("relu", None, False)), True, False),
+    "bias_f32": ((("add", 1, False),), True, False),
+    "bias_relu6_f32": ((("add", 1, False), ("maximum", 3, False), ("minimum", 4, False)), True, False),
+}
+FORM_CONV_CASES = [
+    (2, 64, 56, 56, 64, 3, 1, 1, 1),      # patch, 128x64 tiles
+    (2, 128, 28, 28, 128, 3, 1, 1, 1),    # patch, 128x128 tiles
+    (1, 256, 7, 7, 96, 3, 1, 1, 1),       # patch, last column tile partial (run-time-flag rows)
+    (2, 64, 15, 15, 128, 3, 2, 1, 1),     # stride 2, 64-channel loader
+    (1, 256, 7, 7, 512, 3, 1, 1, 1),      # 128x256 tiles
+    (2, 64, 14, 14, 128, 1, 2, 0, 1),     # downsample
+]
+
+
+@pytest.mark.parametrize("form", list(FORMS))
+@pytest.mark.parametrize("n,c,h,w,o,k,s,p,d", FORM_CONV_CASES)
+def test_qconv2d_epilogue_forms(lib, form, n, c, h, w, o, k, s, p, d):
+    torch = _torch()
+    steps, want_f32, want_i8 = FORMS[form]
+    rng = np.random.default_rng(n * 1000 + c * 10 + k + 7)
+    x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    wt = rng.standard_normal((o, c, k, k)).astype(np.float32)
+    q, ws = G.quantize_array(wt, 0)
+    xs = float(np.abs(x).max()) / 127
+    oh, ow = G.conv_out(h, k, s, p, d), G.conv_out(w, k, s, p, d)
+    M = n * oh * ow
+    bias = (rng.standard_normal((o, 1, 1)) * 0.1).astype(np.float32)
+    res = rng.standard_normal((n, o, oh, ow)).astype(np.float32)
+    zero, six = np.array(0, np.float32), np.array(6, np.float32)
+    attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "stride": (s, s), "padding": (p, p),
+             "dilation": (d, d), "epilogue": steps}
+    want = G.qconv2d([x, bias, res, zero, six], attrs)
+    next_xs = float(np.abs(want[np.isfinite(want)]).max()) / 127 or 1.0
+    cp = pack.c_pad_for(c)
+    xq = empty((n, h, w, cp), torch.int8)
+    L.check(lib.mr_quantize_nchw_nhwc(T(x).data_ptr(), n, c, h, w, xq.data_ptr(), cp, xs, stream()), "q")
+    b = T(pack.pack_conv(q, cp))
+    scale = T(pack.combined_scale(xs, ws))
+    g = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=cp, o=o, oh=oh, ow=ow, kh=k, kw=k, sh=s, sw=s, ph=p, pw=p, dh=d, dw=d)
+    operands = {1: (L.BC_COL, T(bias.reshape(o)), 0), 2: (L.BC_FULL, T(res.transpose(0, 2, 3, 1).reshape(M, o)), o),
+                3: (L.BC_SCALAR, T(zero.reshape(1)), 0), 4: (L.BC_SCALAR, T(six.reshape(1)), 0)}
+    dev_steps = [(fn, 0, None, 0, sw) if idx is None else (fn, operands[idx][0], operands[idx][1], operands[idx][2], sw)
+                 for fn, idx, sw in steps]
+    y = empty((M, o), torch.float32) if want_f32 else None
+    ocp = pack.c_pad_for(o)
+    yq = empty((M, ocp), torch.int8) if want_i8 else None
+    e = epilogue(dev_steps, scale=scale, out_f32=y, ldo=o if want_f32 else 0, out_i8=yq, ldq=ocp if want_i8 else 0,
+                 xs=next_xs)
+    L.check(lib.mr_qconv2d(xq.data_ptr(), C.byref(g), b.data_ptr(), b.shape[1], b.shape[0], C.byref(e), stream()),
+            "mr_qconv2d")
+    sync()
+    to_nhwc = lambda a: a.transpose(0, 2, 3, 1).reshape(M, o)
+    if want_f32:
+        assert bits_equal(y.cpu().numpy(), to_nhwc(want))
+    if want_i8:
+        assert bits_equal(yq.cpu().numpy()[:, :o], to_nhwc(G.quantize_activation(want, next_xs)).astype(np.int8))
+
+
+@pytest.mark.parametrize("form", ["relu_i8", "bias_f32", "res_f32_i8"])
+@pytest.mark.parametrize("M,K,N", [(300, 512, 1000), (512, 256, 128), (64, 64, 10)])
+def test_qmatmul_epilogue_forms(lib, form, M, K, N):
+    torch = _torch()
+    steps, want_f32, want_i8 = FORMS[form]
+    rng = np.random.default_rng(M + N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    q, ws = G.quantize_array(w, 1)
+    xs = float(np.abs(x).max()) / 127
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "epilogue": steps}
+    want = G.qmatmul([x, bias, res], attrs)
+    next_xs = float(np.abs(want[np.isfinite(want)]).max()) / 127 or 1.0
+    lda = pack.row_stride_for(K)
+    xq = empty((M, lda), torch.int8)
+    L.check(lib.mr_quantize_rows(T(x).data_ptr(), M, K, K, xq.data_ptr(), lda, xs, stream()), "q")
+    b = T(pack.pack_matmul(q))
+    bias_t, res_t = T(bias), T(res)
+    dev_steps = [(fn, 0, None, 0, sw) if idx is None else
+                 ((fn, L.BC_COL, bias_t, 0, sw) if idx == 1 else (fn, L.BC_FULL, res_t, N, sw))
+                 for fn, idx, sw in steps]
+    y = empty((M, N), torch.float32) if want_f32 else None
+    ldq = pack.row_stride_for(N)
+    yq = empty((M, ldq), torch.int8) if want_i8 else None
+    e = epilogue(dev_steps, scale=T(pack.combined_scale(xs, ws)), out_f32=y, ldo=N if want_f32 else 0, out_i8=yq,
+                 ldq=ldq if want_i8 else 0, xs=next_xs)
+    L.check(lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), b.shape[1], b.shape[0], M, N, K, C.byref(e), stream()),
+            "mr_qmatmul")
+    sync()
+    if want_f32:
+        assert bits_equal(y.cpu().numpy(), want)
+    if want_i8:
+        assert bits_equal(yq.cpu().numpy()[:, :N], G.quantize_activation(want, next_xs).astype(np.int8))
+
+
 # ---------------------------------------------------------------- K4a depthwise, adjuncts
 
 @pytest.mark.parametrize("n,c,h,s", [(2, 32, 16, 1), (2, 144, 15, 2), (1, 960, 7, 1)])
