@@ -90,7 +90,9 @@ static int spec_form(const EpiDev& e) {
 
 // A_PATCH: LDS bytes reserved for one tile's input patch, and the tile height.
 constexpr int PATCH_MAX = 24576;
-constexpr int PATCH_BM = 128;
+// tile rows (pixels) of the A_PATCH configurations: N <= 64 and N <= 128
+constexpr int PATCH_BM64 = 256, PATCH_BM128 = 128;
+static int patch_bm(int n) { return n <= 64 ? PATCH_BM64 : PATCH_BM128; }
 
 struct GemmArgs {
   const int8_t* a;  // dense: [M, lda]; conv: NHWC input
@@ -661,9 +663,9 @@ static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
   MR_REQUIRE((g.M + 63) / 64 * ((g.N + 31) / 32) < (int64_t(1) << 31), "problem too large");
   if constexpr (AMODE == A_PATCH) {   // the host picks this mode for N <= 128 only
     if (g.N <= 64)
-      launch_cfg<PATCH_BM, 64, 4, 1, 3, AMODE>(g, e, stream);
+      launch_cfg<PATCH_BM64, 64, 4, 1, 3, AMODE>(g, e, stream);
     else
-      launch_cfg<PATCH_BM, 128, 2, 2, 3, AMODE>(g, e, stream);
+      launch_cfg<PATCH_BM128, 128, 2, 2, 3, AMODE>(g, e, stream);
   } else if (g.N <= 32) {
     launch_cfg<64, 32, 2, 1, 4, AMODE>(g, e, stream);
   } else if (g.N <= 64) {
@@ -785,8 +787,8 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
   // per-tile input patch: each input pixel crosses L2 -> LDS about
   // (tr + kh - 1) / tr times instead of kh * kw times
   if (mode == mr::A_CONV64 && (G.c_pad & (G.c_pad - 1)) == 0 && G.c_pad <= 256 && G.sh == 1 && G.sw == 1 &&
-      G.dh == 1 && G.dw == 1 && G.kh * G.kw > 1 && G.o <= 128 && ow <= mr::PATCH_BM) {
-    const int32_t tr = std::min(mr::PATCH_BM / ow, oh);
+      G.dh == 1 && G.dw == 1 && G.kh * G.kw > 1 && G.o <= 128 && ow <= mr::patch_bm(G.o)) {
+    const int32_t tr = std::min(mr::patch_bm(G.o) / ow, oh);
     const int32_t pr = tr + G.kh - 1, pc = ow + G.kw - 1;
     const int64_t slots = int64_t(pr) * pc * (G.c_pad / 16);
     if (slots * 16 <= mr::PATCH_MAX) {

@@ -167,7 +167,7 @@ CONV_CASES = [
     (2, 128, 28, 28, 128, 3, 1, 1, 1),    # ResNet layer 2 (4 rows per tile, 8 chunks per pixel)
     (1, 256, 7, 7, 96, 3, 1, 1, 1),       # 16 chunks per pixel, 96 of 128 columns
     (3, 64, 20, 20, 40, 3, 1, 1, 1),      # last tile of each image 2 of 6 rows
-    (2, 64, 11, 120, 64, 3, 1, 1, 1),     # one output row per tile
+    (2, 64, 11, 120, 96, 3, 1, 1, 1),     # one output row per tile (128-row tiles)
     (2, 64, 12, 12, 32, 5, 1, 2, 1),      # 5x5, pad 2
     (1, 64, 6, 9, 64, 3, 1, 0, 1),        # no padding
 ]
