@@ -206,4 +206,49 @@ int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out)
 int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int64_t M, int64_t N,
                 const EpiDev& e, hipStream_t stream);
 
+// Epilogue forms a kernel is compiled for: EF_GENERIC runs the step
+// interpreter, EF_FIXED the fixed form (see EpiDev) with its flags read at run
+// time, and EF_SPEC | SF_* the fixed form with its steps and outputs known at
+// compile time: a tile whose columns are all in range then runs its rows as
+// straight-line code (all LDS reads, then all operand loads, then the math and
+// the stores), so the rows' latencies overlap.
+constexpr int EF_GENERIC = 0, EF_FIXED = 1, EF_SPEC = 0x100;
+constexpr int SF_COL = 1, SF_FULL = 2, SF_LO = 4, SF_HI = 8, SF_F32 = 16, SF_I8 = 32;
+// the forms with compiled kernels: bias+ReLU -> int8; bias+residual+ReLU -> f32
+// and/or int8; bias -> f32 (ResNet blocks, downsample and fc layers, MLPs)
+constexpr int SPEC_RELU_I8 = SF_COL | SF_LO | SF_I8;
+constexpr int SPEC_RES_F32_I8 = SF_COL | SF_FULL | SF_LO | SF_F32 | SF_I8;
+constexpr int SPEC_RES_I8 = SF_COL | SF_FULL | SF_LO | SF_I8;
+constexpr int SPEC_RES_F32 = SF_COL | SF_FULL | SF_LO | SF_F32;
+constexpr int SPEC_BIAS_F32 = SF_COL | SF_F32;
+// the fused stem's usual form: bias + ReLU, pooled, to f32 and int8
+constexpr int SPEC_RELU_F32_I8 = SF_COL | SF_LO | SF_F32 | SF_I8;
+
+// The compile-time form of an epilogue, or -1 when it has none: the fixed
+// form without an int32 accumulator output, every output and operand row
+// 16-byte (f32) / 4-byte (int8) aligned.
+inline int spec_form(const EpiDev& e) {
+  if (!e.fixed || e.out_acc) return -1;
+  auto al = [](const void* p, int64_t ld, int bytes) {
+    return reinterpret_cast<uintptr_t>(p) % bytes == 0 && ld % 4 == 0;
+  };
+  int f = 0;
+  if (e.f_col) f |= SF_COL;
+  if (e.f_full) {
+    if (!al(e.full_ptr, e.full_ld, 16)) return -1;
+    f |= SF_FULL;
+  }
+  if (e.f_lo) f |= SF_LO;
+  if (e.f_hi) f |= SF_HI;
+  if (e.out_f32) {
+    if (!al(e.out_f32, e.ldo, 16)) return -1;
+    f |= SF_F32;
+  }
+  if (e.out_i8) {
+    if (!al(e.out_i8, e.ldq, 4)) return -1;
+    f |= SF_I8;
+  }
+  return f;
+}
+
 }  // namespace mr

@@ -53,7 +53,7 @@ struct StemArgs {
 // KSUB: 32-byte K steps holding kernel rows; RB: 16-byte chunks per kernel
 // row; PK: pool window (3: rows/columns 2p-1 .. 2p+1, pad 1; 2: 2p .. 2p+1,
 // pad 0), stride 2.
-template <int KSUB, int RB, int PK, bool FIXED>
+template <int KSUB, int RB, int PK, int EF>
 __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const EpiDev e) {
   constexpr int PS = 2;
   constexpr int PPL = PK == 3 ? 1 : 0;
@@ -67,7 +67,7 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
 
   __shared__ __attribute__((aligned(16))) int32_t crow[2][64 * CRW];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: keeps per-wave values scalar
   const int bands = (a.POH + BAND - 1) / BAND;
   const int img = blockIdx.x / bands;
   const int pr0 = (blockIdx.x - img * bands) * BAND;
@@ -86,6 +86,7 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
   const int ch = lane;
   const int chc = min(ch, a.O - 1);
   const double scale = e.scale[chc];
+  constexpr bool FIXED = EF != EF_GENERIC;
   const float colv = FIXED && e.f_col ? e.col_ptr[chc] : 0.0f;
   const float lo = FIXED && e.f_lo && e.lo_ptr ? e.lo_ptr[0] : 0.0f;
   const float hi = FIXED && e.f_hi ? e.hi_ptr[0] : 0.0f;
@@ -224,6 +225,25 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
       if (e.out_f32) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rf, vf + uint32_t(j * e.ldo * 4), 0, 0);
       if (e.out_i8) __builtin_amdgcn_raw_buffer_store_b8(q, rq, vq + uint32_t(j * e.ldq), 0, 0);
     };
+    if constexpr (EF >= EF_SPEC) {
+      if (nan_free && pad_inert) {   // steps and outputs known at compile time: straight-line code
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          float y = dequant(v[j], scale);
+          if constexpr ((EF & SF_COL) != 0) y = __fadd_rn(y, colv);
+          if constexpr ((EF & SF_LO) != 0) y = y > lo ? y : lo;
+          if constexpr ((EF & SF_HI) != 0) y = y < hi ? y : hi;
+          if constexpr ((EF & SF_F32) != 0)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rf, vf + uint32_t(j * e.ldo * 4), 0, 0);
+          if constexpr ((EF & SF_I8) != 0) {
+            const float t = rintf(static_cast<float>(__dmul_rn(static_cast<double>(y), e.out_rxs)));
+            __builtin_amdgcn_raw_buffer_store_b8(static_cast<int8_t>(static_cast<int>(__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f))),
+                                                 rq, vq + uint32_t(j * e.ldq), 0, 0);
+          }
+        }
+        return;
+      }
+    }
     if (nan_free) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
@@ -285,10 +305,12 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
 
 template <int KS, int RBV, int PK>
 static void launch_stem(dim3 grid, hipStream_t s, const StemArgs& a, const EpiDev& e) {
-  if (e.fixed)
-    hipLaunchKernelGGL((stem_pool_kernel<KS, RBV, PK, true>), grid, dim3(256), 0, s, a, e);
+  if (spec_form(e) == SPEC_RELU_F32_I8)
+    hipLaunchKernelGGL((stem_pool_kernel<KS, RBV, PK, EF_SPEC | SPEC_RELU_F32_I8>), grid, dim3(256), 0, s, a, e);
+  else if (e.fixed)
+    hipLaunchKernelGGL((stem_pool_kernel<KS, RBV, PK, EF_FIXED>), grid, dim3(256), 0, s, a, e);
   else
-    hipLaunchKernelGGL((stem_pool_kernel<KS, RBV, PK, false>), grid, dim3(256), 0, s, a, e);
+    hipLaunchKernelGGL((stem_pool_kernel<KS, RBV, PK, EF_GENERIC>), grid, dim3(256), 0, s, a, e);
 }
 
 template <int PK>
