@@ -227,7 +227,7 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
   int8_t* const patch = lds + RING_BYTES;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: per-wave offsets stay scalar
   const int wm = wave / WN;
   const int wn = wave - wm * WN;
 
