@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MR_ABI_VERSION 1
+#define MR_ABI_VERSION 2
 
 enum mr_status {
   MR_OK = 0,
@@ -135,16 +135,19 @@ int mr_quantize_nchw_nhwc(const float* x, int32_t n, int32_t c, int32_t h, int32
 /* ---- K2/K3: int8 GEMM with fused dequant/epilogue/requant -------------- */
 
 /* Replaces mira/ops.py:616-620 _qmatmul_ref (after quantize_activation):
- * acc[M,N] = a[M,K] (int8, row stride lda) x b[N,k_pad]^T (packed int8
+ * acc[M,N] = a[M,K] (int8, row stride lda) x B[N,k_pad]^T (packed int8
  * weights, zero for k >= K and n >= N, N rounded up to n_pad rows),
  * exact int32, then the epilogue.  lda % 16 == 0, k_pad % 64 == 0,
- * n_pad % 32 == 0. */
+ * n_pad % 32 == 0.  Every packed weight argument of this library stores the
+ * logical B[n_pad][k_pad] K-step-major: byte k of row n at
+ * ((k / 64) * n_pad + n) * 64 + k % 64. */
 int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int64_t n_pad,
                int64_t M, int64_t N, int64_t K, const mr_epilogue* epi, void* stream);
 
 /* Replaces mira/ops.py:630-634 _qconv2d_ref (after quantize_activation):
  * implicit-GEMM convolution of NHWC int8 x with packed weights
- * b[n_pad][k_pad] whose k index is (kh, kw, c) with c fastest over c_pad
+ * B[n_pad][k_pad] (stored K-step-major as for mr_qmatmul) whose k index is
+ * (kh, kw, c) with c fastest over c_pad
  * (or the stem row layout when c_pad == 4).  Result rows are NHWC pixels
  * (n, oh, ow), columns output channels. */
 int mr_qconv2d(const int8_t* x, const mr_conv_geom* g, const int8_t* b, int64_t k_pad,

@@ -10,7 +10,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "libmira_rocm.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 MAX_EPI = 8
 
 # enum mr_epi_fn

@@ -203,7 +203,7 @@ __device__ __forceinline__ float dequant(int32_t acc, double scale) {
 int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out);
 
 // Decode-shaped qmatmul (M <= 8 rows): weight-streaming kernel; MR_EUNSUPPORTED for larger M.
-int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int64_t M, int64_t N,
+int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int64_t n_pad, int64_t M, int64_t N,
                 const EpiDev& e, hipStream_t stream);
 
 // Epilogue forms a kernel is compiled for: EF_GENERIC runs the step

@@ -7,7 +7,8 @@
 //
 // Pipeline.  A workgroup owns a BM x BN tile of the result and walks K in
 // 64-byte steps.  Each step's A slice (BM x 64 bytes) and B slice (weights,
-// BN x 64 bytes) travel global -> LDS by direct-to-LDS loads
+// BN x 64 bytes, contiguous: weights are stored K-step-major,
+// [k_pad / 64][n_pad][64]) travel global -> LDS by direct-to-LDS loads
 // (global_load_lds_dwordx4: no VGPR staging), STAGES-1 steps ahead of the
 // MFMAs, through a ring of STAGES LDS buffers.  One s_barrier per step; the
 // only wait is a counted vmcnt for the step about to be consumed.  Padding
@@ -305,7 +306,7 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
     const int koff = ((slot & 3) ^ ((row >> 2) & 3)) << 4;
     const int n = n0 + row;
     b_ok[j] = n < g.n_pad;
-    b_src[j] = g.b + int64_t(n) * g.k_pad + koff;
+    b_src[j] = g.b + int64_t(n) * BK + koff;   // K step kt of row n: + kt * n_pad * BK
   }
 
   // load cursor of A_CONV64: (kernel row, kernel column, 64-channel block) of the next step
@@ -353,7 +354,7 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
     }
 #pragma unroll
     for (int j = 0; j < B_OPS; ++j)
-      dma16(b_ok[j] ? static_cast<const void*>(b_src[j] + int64_t(kt) * BK) : g_zero_page,
+      dma16(b_ok[j] ? static_cast<const void*>(b_src[j] + int64_t(kt) * g.n_pad * BK) : g_zero_page,
             Bs + (wave * B_OPS + j) * (16 * BK));
     if constexpr (AMODE == A_CONV64) {
       if (++l_cb == g.cb_per_tap) {
@@ -672,7 +673,7 @@ int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int
   g.N = static_cast<int32_t>(N);
   g.n_pad = static_cast<int32_t>(n_pad);
   g.k_tiles = static_cast<int32_t>(k_pad / mr::BK);
-  if (M <= 8) return mr::gemv_launch(a, lda, b, k_pad, M, N, e, static_cast<hipStream_t>(stream));
+  if (M <= 8) return mr::gemv_launch(a, lda, b, k_pad, n_pad, M, N, e, static_cast<hipStream_t>(stream));
   return mr::launch<mr::A_DENSE>(g, e, static_cast<hipStream_t>(stream));
 }
 

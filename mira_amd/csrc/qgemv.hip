@@ -1,5 +1,6 @@
 // Small-M int8 matmul (decode-shaped qmatmul, mira/ops.py:616-620): M <= 8
-// activation rows against packed weights b[n_pad][k_pad].  With so few rows
+// activation rows against packed weights (K-step-major: 64-byte slice kt of
+// row n at (kt * n_pad + n) * 64).  With so few rows
 // the work is reading the weights once (N*K bytes: 16 MiB per 4096x4096
 // layer), so the kernel is a coalesced weight stream rather than MFMA tiles:
 // a group of LPC lanes owns CPW output columns, each lane walks 16-byte
@@ -19,8 +20,9 @@ constexpr int GEMV_CPW = 2;   // output columns per lane group
 struct GemvArgs {
   const int8_t* a;    // [M][lda] int8 activations
   int64_t lda;
-  const int8_t* b;    // [n_pad][k_pad] packed weights
+  const int8_t* b;    // packed weights, [k_pad / 64][n_pad][64]
   int32_t k_pad, N, lpc;   // lpc: lanes per column group (power of two, <= 64)
+  int32_t n_pad;
   int32_t M;
 };
 
@@ -42,11 +44,13 @@ __global__ void __launch_bounds__(256) qgemv_kernel(const GemvArgs g, const EpiD
   if (n0 < g.N) {
     const int8_t* brow[GEMV_CPW];
 #pragma unroll
-    for (int c = 0; c < GEMV_CPW; ++c) brow[c] = g.b + int64_t(min(n0 + c, g.N - 1)) * g.k_pad;
+    for (int c = 0; c < GEMV_CPW; ++c) brow[c] = g.b + int64_t(min(n0 + c, g.N - 1)) * 64;
+    const int64_t kstep = int64_t(g.n_pad) * 64;   // bytes between K steps of one row
     for (int k16 = sub; k16 < chunks; k16 += lpc) {
       v4i w[GEMV_CPW];
 #pragma unroll
-      for (int c = 0; c < GEMV_CPW; ++c) w[c] = *reinterpret_cast<const v4i*>(brow[c] + k16 * 16);
+      for (int c = 0; c < GEMV_CPW; ++c)
+        w[c] = *reinterpret_cast<const v4i*>(brow[c] + (k16 >> 2) * kstep + (k16 & 3) * 16);
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
         if (m >= g.M) break;
@@ -83,14 +87,15 @@ __global__ void __launch_bounds__(256) qgemv_kernel(const GemvArgs g, const EpiD
 }
 
 // M <= 8 rows: returns MR_EUNSUPPORTED for larger M (the caller uses the tiled kernel).
-int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int64_t M, int64_t N,
-                const EpiDev& e, hipStream_t stream) {
+int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int64_t n_pad, int64_t M,
+                int64_t N, const EpiDev& e, hipStream_t stream) {
   if (M > 8) return MR_EUNSUPPORTED;
   GemvArgs g = {};
   g.a = a;
   g.lda = lda;
   g.b = b;
   g.k_pad = static_cast<int32_t>(k_pad);
+  g.n_pad = static_cast<int32_t>(n_pad);
   g.N = static_cast<int32_t>(N);
   g.M = static_cast<int32_t>(M);
   // lanes per column group: enough 16-byte chunks per lane to keep loads in

@@ -42,8 +42,8 @@ __device__ __attribute__((aligned(64))) int32_t g_stem_zero[16];
 
 struct StemArgs {
   const int8_t* x;     // NHWC int8, 4 bytes per pixel
-  const int8_t* b;     // packed weights [>= 64][k_pad]
-  int32_t k_pad;
+  const int8_t* b;     // packed weights, K-step-major [k_pad / 64][n_pad >= 64][64]
+  int32_t k_pad, n_pad;
   int32_t row_bytes;   // packed bytes per kernel row
   int32_t N, H, W, O, OH, OW, KH, KW, SH, SW, PH, PW, DH, DW;
   int32_t ppt, POH, POW;  // pool top pad, pooled size
@@ -79,8 +79,8 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
   for (int s = 0; s < KSUB; ++s)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-      bw[s][j] = *reinterpret_cast<const v4i*>(a.b + int64_t(j * 32 + (lane & 31)) * a.k_pad + s * 32 +
-                                               (lane >> 5) * 16);
+      bw[s][j] = *reinterpret_cast<const v4i*>(a.b + (int64_t(s >> 1) * a.n_pad + j * 32 + (lane & 31)) * 64 +
+                                               (s & 1) * 32 + (lane >> 5) * 16);
 
   // pool-phase role: this lane is output channel `lane`
   const int ch = lane;
@@ -402,6 +402,7 @@ int mr_qconv2d_maxpool(const int8_t* x, const mr_conv_geom* cg, const int8_t* b,
   a.x = x;
   a.b = b;
   a.k_pad = static_cast<int32_t>(k_pad);
+  a.n_pad = static_cast<int32_t>(n_pad);
   a.row_bytes = row_bytes;
   a.N = G.n;
   a.H = G.h;

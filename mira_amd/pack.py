@@ -7,10 +7,13 @@ order changes:
 * activations are NHWC int8 with `c_pad` channels per pixel: a multiple of 16
   so a 16-byte load never straddles two pixels, or exactly 4 for inputs with at
   most 4 channels (the stem layout: one dword per pixel);
-* weights are packed K-contiguous as b[n][k] (`n_pad` rows, `k_pad` bytes
+* weights are packed as a logical matrix b[n][k] (`n_pad` rows, `k_pad` bytes
   each, zero-filled), with k running over (kh, kw, c) -- the order in which the
   implicit-GEMM loader walks an NHWC input.  The stem layout packs each kernel
-  row as 4-tap groups of one dword per tap.
+  row as 4-tap groups of one dword per tap.  The device stores that matrix
+  K-step-major (`device_weights`): [k_pad / 64][n_pad][64], so the 64-byte
+  slices of consecutive rows for one K step are contiguous and a 1 KB load
+  covers whole 128-byte cache lines.
 """
 from __future__ import annotations
 
@@ -63,6 +66,13 @@ def pack_conv(q: np.ndarray, c_pad: int, min_rows: int = 0) -> np.ndarray:
     out = np.zeros((max(roundup(o, N_STEP), min_rows), roundup(body.shape[1], K_STEP)), np.int8)
     out[:o, :body.shape[1]] = body
     return out
+
+
+def device_weights(b: np.ndarray) -> np.ndarray:
+    """Logical packed weights b[n_pad, k_pad] -> the kernels' byte order [k_pad/64][n_pad][64]."""
+    n_pad, k_pad = b.shape
+    assert k_pad % K_STEP == 0, "k_pad must be a multiple of the K step"
+    return np.ascontiguousarray(b.reshape(n_pad, k_pad // K_STEP, K_STEP).transpose(1, 0, 2))
 
 
 def combined_scale(x_scale: float, w_scale: np.ndarray) -> np.ndarray:

@@ -473,7 +473,8 @@ class RocmExecutable:
         K, N = q.shape
         xs = _f32key(a["x_scale"])
         xq, lda = x.i8[xs] if xs in x.i8 else self._quantize_to(x, xs)
-        b = self._upload(pack.pack_matmul(q))
+        bl = pack.pack_matmul(q)
+        b = self._upload(pack.device_weights(bl))
         scale = self._upload(pack.combined_scale(a["x_scale"], a["w_scale"]))
         out = self._new_dv(op.result)
         e, fused = self._epilogue(op, out, False, 1, scale)
@@ -481,7 +482,7 @@ class RocmExecutable:
         if acc is not None:
             e.out_acc, e.ldacc = acc.data_ptr(), N
         M = out.rows
-        lib, kp, npad = self.lib, b.shape[1], b.shape[0]
+        lib, kp, npad = self.lib, bl.shape[1], bl.shape[0]
         self._add("qmatmul", lambda s: L.check(
             lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), kp, npad, M, N, K, C.byref(e), s), "mr_qmatmul"),
             nbytes=M * K + K * N + self._epi_bytes(e, M, N), nops=2 * M * N * K)
@@ -501,7 +502,8 @@ class RocmExecutable:
             xq, cp = x.i8[xs]
         else:
             xq, cp = self._quantize_to(x, xs)
-        b = self._upload(pack.pack_conv(q, cp))
+        bl = pack.pack_conv(q, cp)
+        b = self._upload(pack.device_weights(bl))
         scale = self._upload(pack.combined_scale(a["x_scale"], a["w_scale"]))
         geom = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=cp, o=o, oh=oh, ow=ow, kh=kh, kw=kw, sh=sh, sw=sw, ph=ph,
                           pw=pw, dh=dh, dw=dw)
@@ -511,7 +513,7 @@ class RocmExecutable:
         acc = self._acc_buffer(op, out.rows, o)
         if acc is not None:
             e.out_acc, e.ldacc = acc.data_ptr(), o
-        lib, kp, npad = self.lib, b.shape[1], b.shape[0]
+        lib, kp, npad = self.lib, bl.shape[1], bl.shape[0]
         rows = n * oh * ow
         self._add("qconv2d", lambda s: L.check(
             lib.mr_qconv2d(xq.data_ptr(), C.byref(geom), b.data_ptr(), kp, npad, C.byref(e), s), "mr_qconv2d"),
@@ -550,7 +552,8 @@ class RocmExecutable:
         _, _, oh, ow = conv.result.type.shape
         xs = _f32key(a["x_scale"])
         xq, cp = x.i8[xs] if xs in x.i8 else self._quantize_to(x, xs)
-        b = self._upload(pack.pack_conv(q, cp, min_rows=64))
+        bl = pack.pack_conv(q, cp, min_rows=64)
+        b = self._upload(pack.device_weights(bl))
         scale = self._upload(pack.combined_scale(a["x_scale"], a["w_scale"]))
         geom = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=cp, o=o, oh=oh, ow=ow, kh=kh, kw=kw, sh=sh, sw=sw, ph=ph,
                           pw=pw, dh=dh, dw=dw)
@@ -561,7 +564,7 @@ class RocmExecutable:
         value = float(np.asarray(pad_op.attrs.get("value", 0)).astype(np.float32))
         size, stride = op.attrs["size"], op.attrs["stride"]
         _, _, poh, pw_ = op.result.type.shape
-        lib, kp, npad = self.lib, b.shape[1], b.shape[0]
+        lib, kp, npad = self.lib, bl.shape[1], bl.shape[0]
         pt, pl = pads[2][0], pads[3][0]
         self._add("qconv2d_maxpool", lambda s: L.check(lib.mr_qconv2d_maxpool(
             xq.data_ptr(), C.byref(geom), b.data_ptr(), kp, npad, C.byref(e), size, stride, pt, pl, value, poh, pw_,

@@ -72,7 +72,8 @@ def _run_qmatmul(lib, x, q, ws, xs, steps_np, next_xs=None):
     lda = pack.row_stride_for(K)
     xq = empty((M, lda), torch.int8)
     L.check(lib.mr_quantize_rows(T(x).data_ptr(), M, K, K, xq.data_ptr(), lda, xs, stream()), "q")
-    b = T(pack.pack_matmul(q))
+    bl = pack.pack_matmul(q)
+    b = T(pack.device_weights(bl))
     scale = T(pack.combined_scale(xs, ws))
     keep, steps = [], []
     for fn, mode, arr, sw in steps_np:
@@ -88,7 +89,7 @@ def _run_qmatmul(lib, x, q, ws, xs, steps_np, next_xs=None):
     ldq = pack.row_stride_for(N)
     yq = empty((M, ldq), torch.int8) if next_xs else None
     e = epilogue(steps, scale=scale, out_f32=y, ldo=N, out_i8=yq, ldq=ldq, xs=next_xs or 1.0, out_acc=acc, ldacc=N)
-    L.check(lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), b.shape[1], b.shape[0], M, N, K, C.byref(e), stream()),
+    L.check(lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), bl.shape[1], bl.shape[0], M, N, K, C.byref(e), stream()),
             "mr_qmatmul")
     sync()
     return acc.cpu().numpy(), y.cpu().numpy(), (yq.cpu().numpy()[:, :N] if yq is not None else None)
@@ -194,7 +195,8 @@ def test_qconv2d(lib, n, c, h, w, o, k, s, p, d):
     cp = pack.c_pad_for(c)
     xq = empty((n, h, w, cp), torch.int8)
     L.check(lib.mr_quantize_nchw_nhwc(T(x).data_ptr(), n, c, h, w, xq.data_ptr(), cp, xs, stream()), "q")
-    b = T(pack.pack_conv(q, cp))
+    bl = pack.pack_conv(q, cp)
+    b = T(pack.device_weights(bl))
     scale = T(pack.combined_scale(xs, ws))
     g = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=cp, o=o, oh=oh, ow=ow, kh=k, kw=k, sh=s, sw=s, ph=p, pw=p, dh=d, dw=d)
     M = n * oh * ow
@@ -207,7 +209,7 @@ def test_qconv2d(lib, n, c, h, w, o, k, s, p, d):
     e = epilogue([("add", L.BC_COL, bias_t, 0, False), ("add", L.BC_FULL, res_t, o, False),
                   ("relu", 0, None, 0, False)], scale=scale, out_f32=y, ldo=o, out_i8=yq, ldq=ocp, xs=next_xs,
                  out_acc=acc, ldacc=o)
-    L.check(lib.mr_qconv2d(xq.data_ptr(), C.byref(g), b.data_ptr(), b.shape[1], b.shape[0], C.byref(e), stream()),
+    L.check(lib.mr_qconv2d(xq.data_ptr(), C.byref(g), b.data_ptr(), bl.shape[1], bl.shape[0], C.byref(e), stream()),
             "mr_qconv2d")
     sync()
     to_nhwc = lambda a: a.transpose(0, 2, 3, 1).reshape(M, o)
@@ -259,7 +261,8 @@ def test_qconv2d_epilogue_forms(lib, form, n, c, h, w, o, k, s, p, d):
     cp = pack.c_pad_for(c)
     xq = empty((n, h, w, cp), torch.int8)
     L.check(lib.mr_quantize_nchw_nhwc(T(x).data_ptr(), n, c, h, w, xq.data_ptr(), cp, xs, stream()), "q")
-    b = T(pack.pack_conv(q, cp))
+    bl = pack.pack_conv(q, cp)
+    b = T(pack.device_weights(bl))
     scale = T(pack.combined_scale(xs, ws))
     g = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=cp, o=o, oh=oh, ow=ow, kh=k, kw=k, sh=s, sw=s, ph=p, pw=p, dh=d, dw=d)
     operands = {1: (L.BC_COL, T(bias.reshape(o)), 0), 2: (L.BC_FULL, T(res.transpose(0, 2, 3, 1).reshape(M, o)), o),
@@ -271,7 +274,7 @@ def test_qconv2d_epilogue_forms(lib, form, n, c, h, w, o, k, s, p, d):
     yq = empty((M, ocp), torch.int8) if want_i8 else None
     e = epilogue(dev_steps, scale=scale, out_f32=y, ldo=o if want_f32 else 0, out_i8=yq, ldq=ocp if want_i8 else 0,
                  xs=next_xs)
-    L.check(lib.mr_qconv2d(xq.data_ptr(), C.byref(g), b.data_ptr(), b.shape[1], b.shape[0], C.byref(e), stream()),
+    L.check(lib.mr_qconv2d(xq.data_ptr(), C.byref(g), b.data_ptr(), bl.shape[1], bl.shape[0], C.byref(e), stream()),
             "mr_qconv2d")
     sync()
     to_nhwc = lambda a: a.transpose(0, 2, 3, 1).reshape(M, o)
@@ -299,7 +302,8 @@ def test_qmatmul_epilogue_forms(lib, form, M, K, N):
     lda = pack.row_stride_for(K)
     xq = empty((M, lda), torch.int8)
     L.check(lib.mr_quantize_rows(T(x).data_ptr(), M, K, K, xq.data_ptr(), lda, xs, stream()), "q")
-    b = T(pack.pack_matmul(q))
+    bl = pack.pack_matmul(q)
+    b = T(pack.device_weights(bl))
     bias_t, res_t = T(bias), T(res)
     dev_steps = [(fn, 0, None, 0, sw) if idx is None else
                  ((fn, L.BC_COL, bias_t, 0, sw) if idx == 1 else (fn, L.BC_FULL, res_t, N, sw))
@@ -309,7 +313,7 @@ def test_qmatmul_epilogue_forms(lib, form, M, K, N):
     yq = empty((M, ldq), torch.int8) if want_i8 else None
     e = epilogue(dev_steps, scale=T(pack.combined_scale(xs, ws)), out_f32=y, ldo=N if want_f32 else 0, out_i8=yq,
                  ldq=ldq if want_i8 else 0, xs=next_xs)
-    L.check(lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), b.shape[1], b.shape[0], M, N, K, C.byref(e), stream()),
+    L.check(lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), bl.shape[1], bl.shape[0], M, N, K, C.byref(e), stream()),
             "mr_qmatmul")
     sync()
     if want_f32:
@@ -431,7 +435,8 @@ def test_qconv2d_maxpool(lib, n, c, h, o, k, s, p, pool, pst, ppad, pval, neg):
     cp = 4
     xq = empty((n, h, h, cp), torch.int8)
     L.check(lib.mr_quantize_nchw_nhwc(T(x).data_ptr(), n, c, h, h, xq.data_ptr(), cp, xs, stream()), "q")
-    b = T(pack.pack_conv(q, cp, min_rows=64))
+    bl = pack.pack_conv(q, cp, min_rows=64)
+    b = T(pack.device_weights(bl))
     scale = T(pack.combined_scale(xs, ws))
     g = L.ConvGeom(n=n, h=h, w=h, c=c, c_pad=cp, o=o, oh=oh, ow=oh, kh=k, kw=k, sh=s, sw=s, ph=p, pw=p, dh=1, dw=1)
     M = n * poh * poh
@@ -441,7 +446,7 @@ def test_qconv2d_maxpool(lib, n, c, h, o, k, s, p, pool, pst, ppad, pval, neg):
     bt = T(bias.reshape(o))
     dev_steps = [("add", L.BC_COL, bt, 0, False)] + ([] if neg else [("relu", 0, None, 0, False)])
     e = epilogue(dev_steps, scale=scale, out_f32=y, ldo=o, out_i8=yq, ldq=ocp, xs=next_xs)
-    L.check(lib.mr_qconv2d_maxpool(xq.data_ptr(), C.byref(g), b.data_ptr(), b.shape[1], b.shape[0], C.byref(e),
+    L.check(lib.mr_qconv2d_maxpool(xq.data_ptr(), C.byref(g), b.data_ptr(), bl.shape[1], bl.shape[0], C.byref(e),
                                    pool, pst, ppad, ppad, pval, poh, poh, stream()), "mr_qconv2d_maxpool")
     sync()
     to_rows = lambda a: a.transpose(0, 2, 3, 1).reshape(M, o)

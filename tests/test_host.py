@@ -146,6 +146,10 @@ def test_pack_conv_layouts():
     m = rng.integers(-127, 128, (100, 10)).astype(np.int8)
     bm = pack.pack_matmul(m)
     assert bm.shape == (32, 128) and np.array_equal(bm[:10, :100], m.T)
+    # device byte order: byte k of row n at ((k // 64) * n_pad + n) * 64 + k % 64
+    d = pack.device_weights(b2).reshape(-1)
+    for n, k in ((0, 0), (7, 229), (63, 319), (40, 64), (13, 127)):
+        assert d[((k // 64) * 64 + n) * 64 + k % 64] == b2[n, k]
 
 
 def test_broadcast_modes():
