@@ -199,7 +199,10 @@ __device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, c
   }
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int AMODE, int EF>
+// KB: K bytes per ring stage, 64 or 128 (two 64-byte K steps: each A and B
+// row then moves as one 128-byte run, a whole cache line; dense and
+// c_pad % 128 == 0 conv loaders only).
+template <int BM, int BN, int WM, int WN, int STAGES, int AMODE, int EF, int KB = 64>
 __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, const EpiDev e) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM;
@@ -208,19 +211,22 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
   constexpr int FN = TN / 32;
   constexpr int NB = FM * FN;
   constexpr bool PATCH = AMODE == A_PATCH;
-  constexpr int A_ROWS_PER_OP = AMODE == A_CONV4 ? 4 : 16;   // rows one wave-wide DMA covers
+  static_assert(KB == 64 || (KB == 128 && (AMODE == A_DENSE || AMODE == A_CONV64)), "128-byte stages");
+  constexpr int CPR = KB / 16;                                // 16-byte chunks per LDS row
+  constexpr int NKK = KB / 32;                                // 32-byte MFMA K steps per stage
+  constexpr int A_ROWS_PER_OP = AMODE == A_CONV4 ? 4 : 64 / CPR;   // rows one wave-wide DMA covers
   constexpr int A_OPS = PATCH ? 0 : BM / A_ROWS_PER_OP / NW;   // A DMAs per wave per K step
   constexpr int A_OPS1 = A_OPS > 0 ? A_OPS : 1;
-  constexpr int B_OPS = BN / 16 / NW;
+  constexpr int B_OPS = BN / (64 / CPR) / NW;
   constexpr int OPS = A_OPS + B_OPS;
-  constexpr int A_STAGE = PATCH ? 0 : BM * BK;                  // A bytes in one ring stage
-  constexpr int STAGE_BYTES = A_STAGE + BN * BK;
+  constexpr int A_STAGE = PATCH ? 0 : BM * KB;                  // A bytes in one ring stage
+  constexpr int STAGE_BYTES = A_STAGE + BN * KB;
   constexpr int PATCH_OPS = PATCH ? PATCH_MAX / 16 / (NW * 64) : 0;   // patch DMAs per wave
   constexpr int RING_BYTES = STAGES * STAGE_BYTES;
   constexpr int LDS_BYTES = RING_BYTES + (PATCH ? PATCH_MAX : 0);
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32");
   static_assert(PATCH || (A_OPS * A_ROWS_PER_OP * NW == BM), "loader mapping");
-  static_assert(B_OPS * 16 * NW == BN, "loader mapping");
+  static_assert(B_OPS * (64 / CPR) * NW == BN, "loader mapping");
   static_assert(!PATCH || PATCH_OPS * 16 * NW * 64 == PATCH_MAX, "patch loader mapping");
   static_assert(STAGES >= 3 && (STAGES - 2) * OPS < 64, "stages / vmcnt range");
 
@@ -262,6 +268,9 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
     mvalid = min(g.tr, g.OH - p_oh0) * g.OW;
   }
 
+  // 16-byte chunk c of LDS row r sits at position c ^ row_swz(r)
+  auto row_swz = [](int r) __attribute__((always_inline)) { return KB == 64 ? (r >> 2) & 3 : (r >> 1) & 7; };
+
   // ---- A loader state, one entry per DMA this lane takes part in
   int64_t a_base[A_OPS1];   // dense: m*lda + chunk offset; conv: image pixel base
   int32_t a_ih0[A_OPS1], a_iw0[A_OPS1], a_k[A_OPS1];
@@ -275,8 +284,8 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
       const int p = (slot >> 2) & 3;
       koff = ((p ^ ((row >> 2) & 3)) << 4) + ((slot & 3) << 2);
     } else {
-      row = slot >> 2;
-      koff = ((slot & 3) ^ ((row >> 2) & 3)) << 4;
+      row = slot / CPR;
+      koff = ((slot % CPR) ^ row_swz(row)) << 4;
     }
     a_k[j] = koff;
     const int64_t m = m0 + row;
@@ -296,17 +305,17 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
       a_iw0[j] = ow * g.SW - g.PW;
     }
   }
-  // ---- B loader state
+  // ---- B loader state (weights K-step-major: 64-byte slice kt of row n at (kt * n_pad + n) * 64)
   const int8_t* b_src[B_OPS];
   bool b_ok[B_OPS];
 #pragma unroll
   for (int j = 0; j < B_OPS; ++j) {
     const int slot = (wave * B_OPS + j) * 64 + lane;
-    const int row = slot >> 2;
-    const int koff = ((slot & 3) ^ ((row >> 2) & 3)) << 4;
+    const int row = slot / CPR;
+    const int koff = ((slot % CPR) ^ row_swz(row)) << 4;
     const int n = n0 + row;
     b_ok[j] = n < g.n_pad;
-    b_src[j] = g.b + int64_t(n) * BK + koff;   // K step kt of row n: + kt * n_pad * BK
+    b_src[j] = g.b + (int64_t(koff >> 6) * g.n_pad + n) * 64 + (koff & 63);
   }
 
   // load cursor of A_CONV64: (kernel row, kernel column, 64-channel block) of the next step
@@ -319,13 +328,13 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
     for (int j = 0; j < A_OPS; ++j) {
       const void* src = g_zero_page;
       if constexpr (AMODE == A_DENSE) {
-        const int64_t k = int64_t(kt) * BK + a_k[j];
+        const int64_t k = int64_t(kt) * KB + a_k[j];
         if (a_ok[j] && k < g.lda) src = g.a + a_base[j] + k;
       } else if constexpr (AMODE == A_CONV64) {
         const int32_t ih = a_ih0[j] + l_kh * g.DH;
         const int32_t iw = a_iw0[j] + l_kw * g.DW;
         if (a_ok[j] && l_kh < g.KH && unsigned(ih) < unsigned(g.H) && unsigned(iw) < unsigned(g.W))
-          src = g.a + (a_base[j] + int64_t(ih) * g.W + iw) * g.C_pad + l_cb * BK + a_k[j];
+          src = g.a + (a_base[j] + int64_t(ih) * g.W + iw) * g.C_pad + l_cb * 64 + a_k[j];
       } else if constexpr (AMODE == A_CONV16) {
         const int32_t k = kt * BK + a_k[j];
         if (a_ok[j] && k < g.k_real) {
@@ -348,16 +357,17 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
           src = g.a + (a_base[j] + int64_t(ih) * g.W + iw) * 4;
       }
       if constexpr (AMODE == A_CONV4)
-        dma4(src, As + (wave * A_OPS + j) * (A_ROWS_PER_OP * BK));
+        dma4(src, As + (wave * A_OPS + j) * (A_ROWS_PER_OP * KB));
       else
-        dma16(src, As + (wave * A_OPS + j) * (A_ROWS_PER_OP * BK));
+        dma16(src, As + (wave * A_OPS + j) * (A_ROWS_PER_OP * KB));
     }
 #pragma unroll
     for (int j = 0; j < B_OPS; ++j)
-      dma16(b_ok[j] ? static_cast<const void*>(b_src[j] + int64_t(kt) * g.n_pad * BK) : g_zero_page,
-            Bs + (wave * B_OPS + j) * (16 * BK));
+      dma16(b_ok[j] ? static_cast<const void*>(b_src[j] + int64_t(kt) * (KB / 64) * g.n_pad * 64) : g_zero_page,
+            Bs + (wave * B_OPS + j) * 1024);
     if constexpr (AMODE == A_CONV64) {
-      if (++l_cb == g.cb_per_tap) {
+      l_cb += KB / 64;
+      if (l_cb == g.cb_per_tap) {
         l_cb = 0;
         if (++l_kw == g.KW) {
           l_kw = 0;
@@ -399,7 +409,7 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
     }
   }
 
-  const int KT = g.k_tiles;
+  const int KT = g.k_tiles / (KB / 64);   // ring stages
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < KT) issue(s, s);
@@ -407,7 +417,7 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
   // Fragments of one 32-byte half (kk) of a K step: lane (row r, half h) holds
   // bytes 16h .. 16h+15 of the half for row r of each 32-row block.
   const int frag_row = lane & 31;
-  const int swz = (frag_row >> 2) & 3;
+  const int swz = row_swz(frag_row);
   // A_PATCH: patch pixel of each fragment row at tap (0, 0); rows past the
   // tile's valid pixels read pixel 0 (their results are never stored)
   int p_pix0[PATCH ? FM : 1];
@@ -434,12 +444,12 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
         const int chunk = (cb * 4 + 2 * kk + (lane >> 5)) ^ patch_swz(P);
         af[i] = *reinterpret_cast<const v4i*>(patch + (P * pU + chunk) * 16);
       } else {
-        af[i] = *reinterpret_cast<const v4i*>(As + (wm * TM + i * 32 + frag_row) * BK + pc);
+        af[i] = *reinterpret_cast<const v4i*>(As + (wm * TM + i * 32 + frag_row) * KB + pc);
       }
     }
 #pragma unroll
     for (int j = 0; j < FN; ++j)
-      bf[j] = *reinterpret_cast<const v4i*>(Bs + (wn * TN + j * 32 + frag_row) * BK + pc);
+      bf[j] = *reinterpret_cast<const v4i*>(Bs + (wn * TN + j * 32 + frag_row) * KB + pc);
   };
   auto mfma_all = [&](const v4i (&af)[FM], const v4i (&bf)[FN]) {
 #pragma unroll
@@ -449,17 +459,24 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
         acc[i * FN + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i * FN + j], 0, 0, 0);
   };
 
-  // Software pipeline, one barrier per K step: the MFMAs of each half run
-  // on fragments read during the previous half, and the first half of step
-  // t+1 is read (after the barrier that publishes it) while the second half
-  // of step t multiplies.
+  // Software pipeline, one barrier per stage: the MFMAs of each 32-byte K
+  // step run on fragments read during the previous one, and the first step
+  // of stage t+1 is read (after the barrier that publishes it) while the last
+  // step of stage t multiplies.
   v4i a0[FM], b0[FN], a1[FM], b1[FN];
   if (KT >= STAGES - 1) wait_vmcnt<(STAGES - 2) * OPS>(); else wait_vmcnt<0>();
   block_barrier();
   load_frags(0, 0, q_off, q_cb, a0, b0);
   for (int kt = 0; kt < KT; ++kt) {
     const int cur = kt % STAGES;
-    load_frags(cur, 1, q_off, q_cb, a1, b1);
+#pragma unroll
+    for (int kk = 0; kk + 2 < NKK; kk += 2) {   // 128-byte stages: steps 0..NKK-3
+      load_frags(cur, kk + 1, q_off, q_cb, a1, b1);
+      mfma_all(a0, b0);
+      load_frags(cur, kk + 2, q_off, q_cb, a0, b0);
+      mfma_all(a1, b1);
+    }
+    load_frags(cur, NKK - 1, q_off, q_cb, a1, b1);
     if constexpr (PATCH) {   // advance the cursor to step kt + 1
       if (++q_cb == g.cb_per_tap) {
         q_cb = 0;
@@ -577,13 +594,13 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
 
 // ---------------------------------------------------------------- host dispatch
 
-template <int BM, int BN, int WM, int WN, int STAGES, int AMODE>
+template <int BM, int BN, int WM, int WN, int STAGES, int AMODE, int KB = 64>
 static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
   g.tiles_m = AMODE == A_PATCH ? static_cast<int32_t>(g.M / (int64_t(g.OH) * g.OW)) * g.rg_per_img
                                : static_cast<int32_t>((g.M + BM - 1) / BM);
   g.tiles_n = (g.N + BN - 1) / BN;
   const dim3 grid(static_cast<unsigned>(int64_t(g.tiles_m) * g.tiles_n)), block(WM * WN * 64);
-#define MR_QGEMM_LAUNCH(EFV) hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, STAGES, AMODE, EFV>), grid, block, 0, \
+#define MR_QGEMM_LAUNCH(EFV) hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, STAGES, AMODE, EFV, KB>), grid, block, 0, \
                                                 stream, g, e)
   // compiled forms: the conv modes of the ResNet-style networks and the dense GEMM
   constexpr bool CONV_SPEC = AMODE == A_CONV64 || AMODE == A_PATCH;
@@ -632,6 +649,14 @@ static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
     launch_cfg<128, 128, 2, 2, 3, AMODE>(g, e, stream);
   } else if (mt256 * ((g.N + 255) / 256) >= 4 * cus) {
     launch_cfg<256, 256, 2, 4, 3, AMODE>(g, e, stream);
+  } else if constexpr (AMODE == A_DENSE || AMODE == A_CONV64) {
+    // 128-byte stages (144 KB of LDS: one workgroup per CU) where every row
+    // holds two whole 64-byte K steps and the grid has at most one tile per CU
+    const int64_t tiles = (g.M + 127) / 128 * ((g.N + 255) / 256);
+    if (g.k_tiles % 2 == 0 && (AMODE == A_DENSE || g.C_pad % 128 == 0) && tiles <= cus)
+      launch_cfg<128, 256, 2, 4, 3, AMODE, 128>(g, e, stream);
+    else
+      launch_cfg<128, 256, 2, 4, 3, AMODE>(g, e, stream);
   } else {
     launch_cfg<128, 256, 2, 4, 3, AMODE>(g, e, stream);
   }
