@@ -154,7 +154,8 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* g, const int8_t* b, int64_t 
                int64_t n_pad, const mr_epilogue* epi, void* stream);
 
 /* Fused stem: mr_qconv2d of a <= 4-channel input (c_pad == 4, o <= 64,
- * output width <= 128, weights packed to n_pad >= 64 rows, k_pad <= 256) whose
+ * output width <= 128, pooled width <= 60 for a 3-wide and <= 64 for a
+ * 2-wide pool, weights packed to n_pad >= 64 rows, k_pad <= 256) whose
  * epilogue result feeds a constant pad (pool_pad_* rows/columns of
  * pad_value, mira/ops.py:461-470) and maxpool2d(pool_size, pool_stride)
  * (mira/ops.py:293-296).  Replaces that qconv2d -> pad -> maxpool2d chain;

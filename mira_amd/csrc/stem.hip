@@ -15,13 +15,17 @@
 // pad value joins a window through NumPy's maximum after the epilogue.
 //
 // A workgroup owns BAND pooled rows of one image.  It walks the convolution
-// rows their windows cover, one at a time: 4 waves x one 32-pixel MFMA block
-// row (<= 128 output columns x 64 channels, weights held in registers), the
-// int32 row goes to LDS as [channel][column], and each lane (one channel)
-// max-pools its wave's 16 pooled columns horizontally and folds them into the
+// rows their windows cover, one at a time; each of its 4 waves computes, as
+// one 32-pixel MFMA block row (x 64 channels, weights in LDS), the 32
+// convolution columns that its pooled columns' windows cover (for a 3-wide
+// pool, 15 pooled columns from 32 columns: neighbouring waves overlap by two
+// columns), so the waves never exchange data.  A lane holds 16 columns of
+// one channel per channel block; it trades 8 of them with its partner lane
+// (lane ^ 32) so that each half of the wave holds the consecutive columns of
+// its 8 pooled columns, max-pools them in registers and folds them into the
 // running maxima of the pooled rows whose windows contain the row.  A pooled
-// row is finished (epilogue, f32 and int8 stores, 64 channels per store)
-// when its last convolution row has been folded in.
+// row is finished (epilogue, f32 and int8 stores) when its last convolution
+// row has been folded in.
 #include "mr_common.hpp"
 
 #include <climits>
@@ -32,8 +36,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int BAND = 8;           // pooled rows per workgroup
-constexpr int CRW = 132;          // int32 slots per channel in a staged row: columns -4 .. 127
-constexpr int COL_OFF = 4;        // slot of convolution column 0
 constexpr int BUF_DWORD3 = 0x00020000;   // buffer resource word 3 for raw 32-bit loads on gfx9
 
 // Source of every padding tap: loads are never predicated, their address is
@@ -56,42 +58,49 @@ struct StemArgs {
 template <int KSUB, int RB, int PK, int EF>
 __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const EpiDev e) {
   constexpr int PS = 2;
-  constexpr int PPL = PK == 3 ? 1 : 0;
-  // pooled columns of wave w: 16w .. 16w+15; their windows read staged slots
-  // [RD0 + 32w, + 4*NRD) of the lane's channel
-  constexpr int SPAN_LO = COL_OFF - PPL;                  // slot of the first window column of pooled column 0
-  constexpr int RD0 = SPAN_LO & ~3;                       // aligned start of a wave's reads (wave 0)
-  constexpr int REL = SPAN_LO - RD0;                      // first window slot relative to the read start
-  constexpr int NRD = (REL + 15 * PS + PK + 3) / 4;       // 16-byte reads per lane
-  static_assert(RD0 + 48 * PS + 4 * NRD <= CRW, "pool reads stay inside the staged row");
+  constexpr int PPL = PK == 3 ? 1 : 0;   // window columns/rows left of / above 2p
+  constexpr int PPW = PK == 3 ? 15 : 16; // pooled columns per wave
+  constexpr bool FIXED = EF != EF_GENERIC;
 
-  __shared__ __attribute__((aligned(16))) int32_t crow[2][64 * CRW];
+  __shared__ v4i bw_lds[KSUB][2][64];    // weights, one MFMA B fragment per (K step, channel block, lane)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: keeps per-wave values scalar
+  const int half = lane >> 5;
   const int bands = (a.POH + BAND - 1) / BAND;
   const int img = blockIdx.x / bands;
   const int pr0 = (blockIdx.x - img * bands) * BAND;
   const int pr_end = min(pr0 + BAND, a.POH);
 
-  // weights: lane holds rows (32j + lane%32), K bytes 32s + 16*(lane/32) .. +16
-  v4i bw[KSUB][2];
-#pragma unroll
-  for (int s = 0; s < KSUB; ++s)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      bw[s][j] = *reinterpret_cast<const v4i*>(a.b + (int64_t(s >> 1) * a.n_pad + j * 32 + (lane & 31)) * 64 +
-                                               (s & 1) * 32 + (lane >> 5) * 16);
+  // K step s of channel block j: lane holds row 32j + lane%32, K bytes 32s + 16*(lane/32) .. +16
+  for (int i = threadIdx.x; i < KSUB * 2 * 64; i += 256) {
+    const int s = i >> 7, j = (i >> 6) & 1, l = i & 63;
+    bw_lds[s][j][l] = *reinterpret_cast<const v4i*>(a.b + (int64_t(s >> 1) * a.n_pad + j * 32 + (l & 31)) * 64 +
+                                                    (s & 1) * 32 + (l >> 5) * 16);
+  }
 
-  // pool-phase role: this lane is output channel `lane`
-  const int ch = lane;
-  const int chc = min(ch, a.O - 1);
-  const double scale = e.scale[chc];
-  constexpr bool FIXED = EF != EF_GENERIC;
-  const float colv = FIXED && e.f_col ? e.col_ptr[chc] : 0.0f;
+  // pool-phase role: channels lane%32 and 32 + lane%32, pooled columns
+  // wave*PPW + 8*half + t (t < 8; the upper half of a PK == 3 wave has 7)
+  int chc[2];
+  double scale[2];
+  float colv[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    chc[j] = min(j * 32 + (lane & 31), a.O - 1);
+    scale[j] = e.scale[chc[j]];
+    colv[j] = FIXED && e.f_col ? e.col_ptr[chc[j]] : 0.0f;
+  }
   const float lo = FIXED && e.f_lo && e.lo_ptr ? e.lo_ptr[0] : 0.0f;
   const float hi = FIXED && e.f_hi ? e.hi_ptr[0] : 0.0f;
 
-  const int ow = wave * 32 + (lane & 31);           // this lane's A row (output column)
+  // The wave's 32 convolution columns: cw0 .. cw0 + 31, cw0 = 2 * PPW * wave - PPL,
+  // so its pooled columns' windows lie inside them (neighbouring waves overlap
+  // by two columns for PK == 3).  Lane l is A row (column) cw0 + l % 32,
+  // clamped to [0, OW): a column outside the output recomputes its nearest
+  // output column, which every window that reaches past the edge also
+  // covers (a window starts at 2p - PPL <= OW - 1 and is at most 3 wide), so
+  // the maxima are those over the window's real columns.
+  const int cw0 = 2 * PPW * wave - PPL;
+  const int ow = min(max(cw0 + (lane & 31), 0), a.OW - 1);
   const int iw0 = ow * a.SW - a.PW;
 
   // A fragments of convolution row cr straight from global memory.  A 32-byte
@@ -104,7 +113,7 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
   // past the kernel (kh >= KH, kw >= KW) read whatever is there: their packed
   // weights are zero.
   const int32_t* ximg = reinterpret_cast<const int32_t*>(a.x) + int64_t(img) * a.H * a.W;
-  const int kw0 = RB == 2 ? 4 * (lane >> 5) : 0;
+  const int kw0 = RB == 2 ? 4 * half : 0;
   int cofs[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) cofs[q] = (iw0 + (kw0 + q) * a.DW) * 4;   // negative -> out of range
@@ -120,7 +129,7 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
         for (int q = 0; q < 4; ++q) af[s][q] = __builtin_amdgcn_raw_buffer_load_b32(row, cofs[q], 0, 0);
       } else {
         // lane halves read different kernel rows 2s and 2s+1
-        const int ih = cr * a.SH - a.PH + (2 * s + (lane >> 5)) * a.DH;
+        const int ih = cr * a.SH - a.PH + (2 * s + half) * a.DH;
         const bool ok = unsigned(ih) < unsigned(a.H);
         const int32_t* rp = ximg + int64_t(ok ? ih : 0) * a.W;
 #pragma unroll
@@ -132,144 +141,133 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
     }
   };
 
-  // Columns outside the convolution output read as INT_MIN (max's identity):
-  // the slots of columns -4..-1 and OW4..127 (OW4 = OW rounded down to a
-  // multiple of 4) are set once here and never staged into; a last group
-  // of 1..3 real columns is staged with its tail masked.
-  const int ow4 = a.OW & ~3;
-  for (int i = threadIdx.x; i < 2 * 64 * CRW; i += 256) {
-    const int slot = i % CRW;
-    if (slot < COL_OFF || slot >= COL_OFF + ow4) crow[i / (64 * CRW)][i % (64 * CRW)] = INT_MIN;
-  }
-
-  // Convolution row cr -> h[j]: this lane's channel, max over the window
-  // columns of pooled column 16*wave + j.  The A fragments of row cr are in
-  // afrag on entry; those of row `next` are on their way on return.
+  // Convolution row cr -> h[j][t]: channel 32j + lane%32, max over the window
+  // columns of pooled column wave*PPW + 8*half + t.  The A fragments of row
+  // cr are in afrag on entry; those of row `next` are on their way on return.
   v4i afrag[KSUB];
-  auto conv_row = [&](int cr, int next, int (&h)[16]) {
-    int32_t* buf = crow[cr & 1];
-    {
-      v16i acc[2];
+  __syncthreads();   // weights in LDS
+  auto conv_row = [&](int cr, int next, int (&h)[2][8]) {
+    v16i acc[2];
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[j][r] = 0;
+      for (int r = 0; r < 16; ++r) acc[j][r] = 0;
 #pragma unroll
-      for (int s = 0; s < KSUB; ++s)
+    for (int s = 0; s < KSUB; ++s)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afrag[s], bw[s][j], acc[j], 0, 0, 0);
-      load_row(next, afrag);   // in flight during the staging and pooling of this row
-      // stage as [channel][column]: the lane's 4 consecutive rows (columns) per group
+      for (int j = 0; j < 2; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afrag[s], bw_lds[s][j][lane], acc[j], 0, 0, 0);
+    load_row(next, afrag);   // in flight during the pooling of this row
+    // Register r of a lane holds column 8*(r/4) + 4*half + r%4: the lower
+    // half has columns 0-3, 8-11, 16-19, 24-27, the upper 4-7, ..., 28-31.
+    // v_permlane32_swap(X, Y) exchanges X's upper 32 lanes with Y's lower 32
+    // lanes; applied to (r, 8 + r) for r < 8 it leaves both halves holding
+    // their 16 consecutive columns (16*half + 0..15) in the same registers:
+    // X'[0..3], Y'[0..3], X'[4..7], Y'[4..7].  The lower half's pools also
+    // need column 16, its register 8 before the swap.
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j) {
+      int w[17];
+      w[16] = acc[j][8];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int col = wave * 32 + 8 * g + 4 * (lane >> 5);
-          v4i v = {acc[j][4 * g], acc[j][4 * g + 1], acc[j][4 * g + 2], acc[j][4 * g + 3]};
-          int32_t* dst = buf + (j * 32 + (lane & 31)) * CRW + COL_OFF + col;
-          if (col < ow4) {
-            *reinterpret_cast<v4i*>(dst) = v;
-          } else if (col < a.OW) {
-#pragma unroll
-            for (int b = 0; b < 4; ++b) dst[b] = col + b < a.OW ? v[b] : INT_MIN;
-          }
-        }
-    }
-    __syncthreads();   // the row is staged; the other buffer's readers (row cr-1) are done
-    v4i rd[NRD];
-    const int32_t* src = buf + ch * CRW + RD0 + wave * 16 * PS;
-#pragma unroll
-    for (int q = 0; q < NRD; ++q) rd[q] = *reinterpret_cast<const v4i*>(src + 4 * q);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      int m = INT_MIN;
-#pragma unroll
-      for (int t = 0; t < PK; ++t) {
-        const int slot = REL + j * PS + t;                   // compile-time
-        m = max(m, rd[slot >> 2][slot & 3]);
+      for (int r = 0; r < 8; ++r) {
+        const auto xy = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(acc[j][r]),
+                                                         static_cast<unsigned>(acc[j][8 + r]), false, false);
+        w[(r >> 2) * 8 + (r & 3)] = static_cast<int>(xy[0]);
+        w[(r >> 2) * 8 + 4 + (r & 3)] = static_cast<int>(xy[1]);
       }
-      h[j] = m;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        int m = max(w[2 * t], w[2 * t + 1]);
+        if constexpr (PK == 3) m = max(m, w[2 * t + 2]);
+        h[j][t] = m;
+      }
     }
   };
 
-  // Finish pooled row p from its window maxima v[j]: epilogue on the pooled
-  // accumulators, the pad value where the window covers padding, stores (the
-  // 64 lanes of a wave write one pooled pixel's channels).  Windows reaching
-  // into the left/right padding: bit j of pad_cols.  Stores go through buffer
-  // resources spanning the npx finished pixels of the pooled row; lanes past
-  // the channel count get an offset out of range, so the hardware drops them.
-  const int npx = max(0, min(16, a.POW - wave * 16));   // pooled pixels this wave stores (0 past POW)
-  uint32_t pad_cols = 0;
-  for (int j = 0; j < 16; ++j) {
-    const int left = (wave * 16 + j) * PS - PPL;
-    if (left < 0 || left + PK > a.OW) pad_cols |= 1u << j;
-  }
+  // Finish pooled row p from its window maxima v[j][t]: epilogue on the pooled
+  // accumulators, the pad value where the window covers padding, stores.
+  // Stores go through buffer resources spanning the pooled row; elements
+  // without a pooled column or a channel get an offset out of range, so the
+  // hardware drops them.
   const bool pad_inert = a.pad_value == -INFINITY;   // max with -inf changes nothing
-  const uint32_t vf = ch < a.O ? uint32_t(ch) * 4u : 0x80000000u;
-  const uint32_t vq = ch < a.O ? uint32_t(ch) : 0x80000000u;
+  uint32_t pad_cols = 0, col_ok = 0;
+  for (int t = 0; t < 8; ++t) {
+    const int pc = wave * PPW + 8 * half + t;
+    const int left = pc * PS - PPL;
+    if (left < 0 || left + PK > a.OW) pad_cols |= 1u << t;
+    if (pc < a.POW && 8 * half + t < PPW) col_ok |= 1u << t;
+  }
   // With a finite scale and bias and no NaN bound (the usual case, checked once
   // for the whole wave) the epilogue values are never NaN, NumPy's
   // maximum/minimum reduce to one compare and select, and the int8 clamp to a
   // median.
-  const bool nan_free = FIXED && !__any(!(fabs(scale) < INFINITY) || !(fabsf(colv) < INFINITY) || lo != lo ||
-                                        hi != hi) && !(a.pad_value != a.pad_value);
-  auto finish = [&](int p, const int (&v)[16]) {
+  const bool nan_free = FIXED && !__any(!(fabs(scale[0]) < INFINITY) || !(fabs(scale[1]) < INFINITY) ||
+                                        !(fabsf(colv[0]) < INFINITY) || !(fabsf(colv[1]) < INFINITY) ||
+                                        lo != lo || hi != hi) && !(a.pad_value != a.pad_value);
+  auto finish = [&](int p, const int (&v)[2][8]) {
     const int top = p * PS - PPL;
     const bool pad_rows = top < 0 || top + PK > a.OH;
-    const int64_t row0 = (int64_t(img) * a.POH + p) * a.POW + wave * 16;
+    const int64_t row0 = (int64_t(img) * a.POH + p) * a.POW;
     const __amdgpu_buffer_rsrc_t rf = __builtin_amdgcn_make_buffer_rsrc(
-        e.out_f32 + row0 * e.ldo, 0, e.out_f32 ? npx * int(e.ldo) * 4 : 0, BUF_DWORD3);
+        e.out_f32 + row0 * e.ldo, 0, e.out_f32 ? a.POW * int(e.ldo) * 4 : 0, BUF_DWORD3);
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-        e.out_i8 + row0 * e.ldq, 0, e.out_i8 ? npx * int(e.ldq) : 0, BUF_DWORD3);
-    auto store = [&](int j, float y, int8_t q) {   // pixels j >= npx fall outside the resources
-      if (e.out_f32) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rf, vf + uint32_t(j * e.ldo * 4), 0, 0);
-      if (e.out_i8) __builtin_amdgcn_raw_buffer_store_b8(q, rq, vq + uint32_t(j * e.ldq), 0, 0);
+        e.out_i8 + row0 * e.ldq, 0, e.out_i8 ? a.POW * int(e.ldq) : 0, BUF_DWORD3);
+    auto offs = [&](int j, int t, uint32_t& of, uint32_t& oq) __attribute__((always_inline)) {
+      const int ch = j * 32 + (lane & 31);
+      const int pc = wave * PPW + 8 * half + t;
+      const bool ok = ((col_ok >> t) & 1) && ch < a.O;
+      of = ok ? uint32_t((pc * int(e.ldo) + ch) * 4) : 0x80000000u;
+      oq = ok ? uint32_t(pc * int(e.ldq) + ch) : 0x80000000u;
     };
     if constexpr (EF >= EF_SPEC) {
       if (nan_free && pad_inert) {   // steps and outputs known at compile time: straight-line code
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          float y = dequant(v[j], scale);
-          if constexpr ((EF & SF_COL) != 0) y = __fadd_rn(y, colv);
-          if constexpr ((EF & SF_LO) != 0) y = y > lo ? y : lo;
-          if constexpr ((EF & SF_HI) != 0) y = y < hi ? y : hi;
-          if constexpr ((EF & SF_F32) != 0)
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rf, vf + uint32_t(j * e.ldo * 4), 0, 0);
-          if constexpr ((EF & SF_I8) != 0) {
-            const float t = rintf(static_cast<float>(__dmul_rn(static_cast<double>(y), e.out_rxs)));
-            __builtin_amdgcn_raw_buffer_store_b8(static_cast<int8_t>(static_cast<int>(__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f))),
-                                                 rq, vq + uint32_t(j * e.ldq), 0, 0);
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            uint32_t of, oq;
+            offs(j, t, of, oq);
+            float y = dequant(v[j][t], scale[j]);
+            if constexpr ((EF & SF_COL) != 0) y = __fadd_rn(y, colv[j]);
+            if constexpr ((EF & SF_LO) != 0) y = y > lo ? y : lo;
+            if constexpr ((EF & SF_HI) != 0) y = y < hi ? y : hi;
+            if constexpr ((EF & SF_F32) != 0) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rf, of, 0, 0);
+            if constexpr ((EF & SF_I8) != 0) {
+              const float tq = rintf(static_cast<float>(__dmul_rn(static_cast<double>(y), e.out_rxs)));
+              __builtin_amdgcn_raw_buffer_store_b8(
+                  static_cast<int8_t>(static_cast<int>(__builtin_amdgcn_fmed3f(tq, -127.0f, 127.0f))), rq, oq, 0, 0);
+            }
           }
-        }
         return;
       }
     }
-    if (nan_free) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float y = dequant(v[j], scale);
-        if (e.f_col) y = __fadd_rn(y, colv);
-        if (e.f_lo) y = y > lo ? y : lo;
-        if (e.f_hi) y = y < hi ? y : hi;
-        if (!pad_inert && (pad_rows || ((pad_cols >> j) & 1))) y = y > a.pad_value ? y : a.pad_value;
-        const float t = rintf(static_cast<float>(__dmul_rn(static_cast<double>(y), e.out_rxs)));
-        store(j, y, static_cast<int8_t>(static_cast<int>(__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f))));
-      }
-    } else {
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float y = dequant(v[j], scale);
-        if constexpr (FIXED) {
-          if (e.f_col) y = __fadd_rn(y, colv);
-          if (e.f_lo) y = np_maximum(y, lo);
-          if (e.f_hi) y = np_minimum(y, hi);
+      for (int t = 0; t < 8; ++t) {
+        uint32_t of, oq;
+        offs(j, t, of, oq);
+        float y = dequant(v[j][t], scale[j]);
+        const bool padded = pad_rows || ((pad_cols >> t) & 1);
+        if (nan_free) {
+          if (e.f_col) y = __fadd_rn(y, colv[j]);
+          if (e.f_lo) y = y > lo ? y : lo;
+          if (e.f_hi) y = y < hi ? y : hi;
+          if (!pad_inert && padded) y = y > a.pad_value ? y : a.pad_value;
         } else {
-          y = epi_generic(e, y, row0 + j, chc);
+          if constexpr (FIXED) {
+            if (e.f_col) y = __fadd_rn(y, colv[j]);
+            if (e.f_lo) y = np_maximum(y, lo);
+            if (e.f_hi) y = np_minimum(y, hi);
+          } else {
+            const int pc = wave * PPW + 8 * half + t;
+            y = epi_generic(e, y, row0 + min(pc, a.POW - 1), chc[j]);
+          }
+          if (!pad_inert) y = np_maximum(y, padded ? a.pad_value : -INFINITY);
         }
-        if (!pad_inert) y = np_maximum(y, pad_rows || ((pad_cols >> j) & 1) ? a.pad_value : -INFINITY);
-        store(j, y, quantize_rcp(y, e.out_rxs));
+        if (e.out_f32) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rf, of, 0, 0);
+        if (e.out_i8) __builtin_amdgcn_raw_buffer_store_b8(quantize_rcp(y, e.out_rxs), rq, oq, 0, 0);
       }
-    }
   };
 
   // Pooled row p takes convolution rows 2p-1 (PK == 3), 2p and 2p+1; the host
@@ -277,27 +275,37 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
   // row 2p+1 carrying over into pooled row p+1.
   const int cr_first = max(2 * pr0 - PPL, 0);
   const int cr_last = min(2 * (pr_end - 1) + 1, a.OH - 1);
-  int carry[16];
+  int carry[2][8];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) carry[j] = INT_MIN;
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) carry[j][t] = INT_MIN;
   load_row(cr_first, afrag);
   if (PK == 3 && pr0 > 0) conv_row(2 * pr0 - 1, min(2 * pr0, cr_last), carry);
   for (int p = pr0; p < pr_end; ++p) {
     const int r0 = 2 * p, r1 = 2 * p + 1;
-    int v[16], h[16];
+    int v[2][8], h[2][8];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = PK == 3 ? carry[j] : INT_MIN;
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[j][t] = PK == 3 ? carry[j][t] : INT_MIN;
     if (r0 < a.OH) {
       conv_row(r0, min(r1, cr_last), h);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) v[j] = max(v[j], h[j]);
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[j][t] = max(v[j][t], h[j][t]);
     }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) carry[j] = INT_MIN;
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) carry[j][t] = INT_MIN;
     if (r1 < a.OH) {
       conv_row(r1, min(r1 + 1, cr_last), carry);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) v[j] = max(v[j], carry[j]);
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[j][t] = max(v[j][t], carry[j][t]);
     }
     finish(p, v);
   }
@@ -375,7 +383,7 @@ int mr_qconv2d_maxpool(const int8_t* x, const mr_conv_geom* cg, const int8_t* b,
   MR_REQUIRE(pool_size > 0 && pool_stride > 0 && pool_pad_top >= 0 && pool_pad_left >= 0 &&
                  pool_pad_top < pool_size && pool_pad_left < pool_size,
              "mr_qconv2d_maxpool: bad pool parameters");
-  MR_REQUIRE(poh > 0 && pow_ > 0 && pow_ <= 64 && (poh - 1) * pool_stride - pool_pad_top < oh &&
+  MR_REQUIRE(poh > 0 && pow_ > 0 && pow_ <= (pool_size == 3 ? 60 : 64) && (poh - 1) * pool_stride - pool_pad_top < oh &&
                  (pow_ - 1) * pool_stride - pool_pad_left < ow,
              "mr_qconv2d_maxpool: pooled size %dx%d does not fit the %dx%d convolution output", poh, pow_, oh, ow);
   const bool pool_3_2_1 = pool_size == 3 && pool_stride == 2 && pool_pad_left == 1 && pool_pad_top == 1;

@@ -260,7 +260,8 @@ class RocmExecutable:
         pool_cfg = (pool.attrs["size"], pool.attrs["stride"], pads[2][0], pads[3][0])
         kernel_ok = (5 <= kh <= 8) if kw >= 5 else (kh <= 4)
         return (c <= 4 and o <= 64 and ow <= 128 and kw <= 8 and kernel_ok
-                and pool_cfg in ((3, 2, 1, 1), (2, 2, 0, 0)) and pool.result.type.shape[3] <= 64
+                and pool_cfg in ((3, 2, 1, 1), (2, 2, 0, 0))
+                and pool.result.type.shape[3] <= (60 if pool_cfg[0] == 3 else 64)
                 and self._monotone_epilogue(conv))
 
     def _monotone_epilogue(self, op: ir.Op) -> bool:
