@@ -56,7 +56,8 @@ struct StemArgs {
 // row; PK: pool window (3: rows/columns 2p-1 .. 2p+1, pad 1; 2: 2p .. 2p+1,
 // pad 0), stride 2.
 template <int KSUB, int RB, int PK, int EF>
-__global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const EpiDev e) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) stem_pool_kernel(const StemArgs a,
+                                                                                      const EpiDev e) {
   constexpr int PS = 2;
   constexpr int PPL = PK == 3 ? 1 : 0;   // window columns/rows left of / above 2p
   constexpr int PPW = PK == 3 ? 15 : 16; // pooled columns per wave
@@ -117,6 +118,7 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
   int cofs[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) cofs[q] = (iw0 + (kw0 + q) * a.DW) * 4;   // negative -> out of range
+  const bool left_edge = cofs[0] < 0 || a.DW != 1;   // taps not one contiguous 16-byte run from the row
   auto load_row = [&](int cr, v4i (&af)[KSUB]) {
 #pragma unroll
     for (int s = 0; s < KSUB; ++s) {
@@ -125,8 +127,15 @@ __global__ void __launch_bounds__(256) stem_pool_kernel(const StemArgs a, const 
         const bool ok = unsigned(ih) < unsigned(a.H);
         const __amdgpu_buffer_rsrc_t row = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<int32_t*>(ximg + int64_t(ok ? ih : 0) * a.W), 0, ok ? a.W * 4 : 0, BUF_DWORD3);
+        // the 4 taps are 16 contiguous bytes: one load, range-checked per
+        // dword (taps right of the image read 0); a lane whose first tap is
+        // left of the image (negative offset: the whole load would read 0)
+        // loads its taps one by one
+        af[s] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(row, cofs[0], 0, 0));
+        if (left_edge) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) af[s][q] = __builtin_amdgcn_raw_buffer_load_b32(row, cofs[q], 0, 0);
+          for (int q = 0; q < 4; ++q) af[s][q] = __builtin_amdgcn_raw_buffer_load_b32(row, cofs[q], 0, 0);
+        }
       } else {
         // lane halves read different kernel rows 2s and 2s+1
         const int ih = cr * a.SH - a.PH + (2 * s + half) * a.DH;
