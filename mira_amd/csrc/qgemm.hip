@@ -535,49 +535,64 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
         // rows in flight at once: all of them, or 4 when each also holds a residual
         constexpr int NRC = S_FULL && NR > 4 ? 4 : NR;
         static_assert(NR % NRC == 0, "epilogue row chunks");
+        // residual rows of chunk c (rows past the tile re-read its last row); the
+        // next chunk's are loaded before this chunk's stores, which the compiler
+        // may not move loads across
+        auto load_res = [&](int c0, float4 (&res)[S_FULL ? NRC : 1]) __attribute__((always_inline)) {
+          if constexpr (S_FULL) {
+#pragma unroll
+            for (int k = 0; k < NRC; ++k) {
+              const int rr = threadIdx.x / CG + (c0 + k) * RSTEP;
+              const int lk = (rr >> 5) * TM + pass * 32 + (rr & 31);
+              const int64_t r = mbase + min(lk, mvalid - 1);
+              res[k] = *reinterpret_cast<const float4*>(e.full_ptr + r * e.full_ld + col0);
+            }
+          }
+        };
+        float4 res_cur[S_FULL ? NRC : 1], res_next[S_FULL ? NRC : 1];
+        load_res(0, res_cur);
 #pragma unroll
         for (int k0 = 0; k0 < NR; k0 += NRC) {
         int local[NRC];
         v4i a[NRC];
-        float4 res[S_FULL ? NRC : 1];
 #pragma unroll
         for (int k = 0; k < NRC; ++k) {
           const int rr = threadIdx.x / CG + (k0 + k) * RSTEP;
           local[k] = (rr >> 5) * TM + pass * 32 + (rr & 31);
           a[k] = *reinterpret_cast<const v4i*>(ep + rr * EP_LD + cgi * 4);
         }
-        if constexpr (S_FULL) {
-#pragma unroll
-          for (int k = 0; k < NRC; ++k) {   // rows past the tile re-read its last row
-            const int64_t r = mbase + min(local[k], mvalid - 1);
-            res[k] = *reinterpret_cast<const float4*>(e.full_ptr + r * e.full_ld + col0);
-          }
-        }
+        float y[NRC][4];
 #pragma unroll
         for (int k = 0; k < NRC; ++k) {
-          float y[4];
-          const float o[4] = {res[S_FULL ? k : 0].x, res[S_FULL ? k : 0].y, res[S_FULL ? k : 0].z,
-                              res[S_FULL ? k : 0].w};
+          const float o[4] = {res_cur[S_FULL ? k : 0].x, res_cur[S_FULL ? k : 0].y, res_cur[S_FULL ? k : 0].z,
+                              res_cur[S_FULL ? k : 0].w};
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
-            y[c] = dequant(a[k][c], cols.scale[c]);
-            if constexpr (S_COL) y[c] = __fadd_rn(y[c], cols.colv[c]);
-            if constexpr (S_FULL) y[c] = __fadd_rn(y[c], o[c]);
-            if constexpr (S_LO) y[c] = max_bound(y[c], cols.lo, cols.lo_nan);
-            if constexpr (S_HI) y[c] = min_bound(y[c], cols.hi, cols.hi_nan);
+            float t = dequant(a[k][c], cols.scale[c]);
+            if constexpr (S_COL) t = __fadd_rn(t, cols.colv[c]);
+            if constexpr (S_FULL) t = __fadd_rn(t, o[c]);
+            if constexpr (S_LO) t = max_bound(t, cols.lo, cols.lo_nan);
+            if constexpr (S_HI) t = min_bound(t, cols.hi, cols.hi_nan);
+            y[k][c] = t;
           }
+        }
+        if (k0 + NRC < NR) load_res(k0 + NRC, res_next);
+#pragma unroll
+        for (int k = 0; k < NRC; ++k) {
           if (local[k] < mvalid) {
             const int64_t row = mbase + local[k];
             if constexpr (S_F32)
-              *reinterpret_cast<float4*>(e.out_f32 + row * e.ldo + col0) = make_float4(y[0], y[1], y[2], y[3]);
+              *reinterpret_cast<float4*>(e.out_f32 + row * e.ldo + col0) = make_float4(y[k][0], y[k][1], y[k][2], y[k][3]);
             if constexpr (S_I8) {
               uint32_t packed = 0;
 #pragma unroll
-              for (int c = 0; c < 4; ++c) packed |= uint32_t(quantize_med3(y[c], e.out_rxs) & 0xff) << (8 * c);
+              for (int c = 0; c < 4; ++c) packed |= uint32_t(quantize_med3(y[k][c], e.out_rxs) & 0xff) << (8 * c);
               *reinterpret_cast<uint32_t*>(e.out_i8 + row * e.ldq + col0) = packed;
             }
           }
         }
+#pragma unroll
+        for (int k = 0; k < (S_FULL ? NRC : 1); ++k) res_cur[k] = res_next[k];
         }
         continue;
       }
