@@ -231,6 +231,9 @@ FORMS = {
 }
 FORM_CONV_CASES = [
     (2, 64, 56, 56, 64, 3, 1, 1, 1),      # patch, 128x64 tiles
+    (3, 64, 20, 20, 64, 3, 1, 1, 1),      # patch, last tile of each image 8 of 12 rows
+    (2, 64, 7, 130, 64, 3, 1, 1, 1),      # patch, one 130-pixel row per tile
+    (1, 64, 6, 9, 64, 3, 1, 0, 1),        # patch, no padding
     (2, 128, 28, 28, 128, 3, 1, 1, 1),    # patch, 128x128 tiles
     (1, 256, 7, 7, 96, 3, 1, 1, 1),       # patch, last column tile partial (run-time-flag rows)
     (2, 64, 15, 15, 128, 3, 2, 1, 1),     # stride 2, 64-channel loader
