@@ -271,8 +271,12 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
   // 16-byte chunk c of LDS row r sits at position c ^ row_swz(r)
   auto row_swz = [](int r) __attribute__((always_inline)) { return KB == 64 ? (r >> 2) & 3 : (r >> 1) & 7; };
 
-  // ---- A loader state, one entry per DMA this lane takes part in
-  int64_t a_base[A_OPS1];   // dense: m*lda + chunk offset; conv: image pixel base
+  // ---- A loader state, one entry per DMA this lane takes part in.  The
+  // per-step work of the dense and 64-channel loaders is one uniform offset,
+  // two compares and a select: every per-row product is taken here, once.
+  int64_t a_base[A_OPS1];   // conv16 / conv4: image pixel base
+  int64_t a_off[A_OPS1];    // dense: row chunk at K = 0; conv64: row chunk at tap (0, 0), channel block 0
+  int64_t a_lim[A_OPS1];    // dense: lda for a row inside M, 0 past it
   int32_t a_ih0[A_OPS1], a_iw0[A_OPS1], a_k[A_OPS1];
   bool a_ok[A_OPS1];
 #pragma unroll
@@ -292,6 +296,8 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
     a_ok[j] = m < g.M;
     if constexpr (AMODE == A_DENSE) {
       a_base[j] = m * g.lda;
+      a_off[j] = a_base[j] + koff;
+      a_lim[j] = a_ok[j] ? g.lda : 0;
       a_ih0[j] = a_iw0[j] = 0;
     } else {
       const int32_t mm = a_ok[j] ? static_cast<int32_t>(m) : 0;
@@ -303,19 +309,27 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
       a_base[j] = int64_t(img) * g.H * g.W;
       a_ih0[j] = oh * g.SH - g.PH;
       a_iw0[j] = ow * g.SW - g.PW;
+      a_off[j] = (a_base[j] + int64_t(a_ih0[j]) * g.W + a_iw0[j]) * g.C_pad + koff;
+      a_lim[j] = 0;
+      // rows past M fail every bounds check of the conv64 loader
+      if (AMODE == A_CONV64 && !a_ok[j]) a_ih0[j] = -(1 << 30);
     }
   }
-  // ---- B loader state (weights K-step-major: 64-byte slice kt of row n at (kt * n_pad + n) * 64)
-  const int8_t* b_src[B_OPS];
-  bool b_ok[B_OPS];
+  // ---- B loader state (weights K-step-major: 64-byte slice kt of row n at (kt * n_pad + n) * 64).
+  // Rows past n_pad read the zero page at every step: their step mask is 0.
+  const uintptr_t zero_page = reinterpret_cast<uintptr_t>(g_zero_page);
+  const uintptr_t a_addr = reinterpret_cast<uintptr_t>(g.a);
+  uintptr_t b_src[B_OPS];
+  uint64_t b_mask[B_OPS];
 #pragma unroll
   for (int j = 0; j < B_OPS; ++j) {
     const int slot = (wave * B_OPS + j) * 64 + lane;
     const int row = slot / CPR;
     const int koff = ((slot % CPR) ^ row_swz(row)) << 4;
     const int n = n0 + row;
-    b_ok[j] = n < g.n_pad;
-    b_src[j] = g.b + (int64_t(koff >> 6) * g.n_pad + n) * 64 + (koff & 63);
+    const bool ok = n < g.n_pad;
+    b_src[j] = ok ? reinterpret_cast<uintptr_t>(g.b + (int64_t(koff >> 6) * g.n_pad + n) * 64 + (koff & 63)) : zero_page;
+    b_mask[j] = ok ? ~uint64_t(0) : 0;
   }
 
   // load cursor of A_CONV64: (kernel row, kernel column, 64-channel block) of the next step
@@ -328,13 +342,16 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
     for (int j = 0; j < A_OPS; ++j) {
       const void* src = g_zero_page;
       if constexpr (AMODE == A_DENSE) {
-        const int64_t k = int64_t(kt) * KB + a_k[j];
-        if (a_ok[j] && k < g.lda) src = g.a + a_base[j] + k;
+        const int64_t k0 = int64_t(kt) * KB;   // uniform
+        const bool ok = k0 + a_k[j] < a_lim[j];
+        src = reinterpret_cast<const void*>(ok ? a_addr + a_off[j] + k0 : zero_page);
       } else if constexpr (AMODE == A_CONV64) {
-        const int32_t ih = a_ih0[j] + l_kh * g.DH;
-        const int32_t iw = a_iw0[j] + l_kw * g.DW;
-        if (a_ok[j] && l_kh < g.KH && unsigned(ih) < unsigned(g.H) && unsigned(iw) < unsigned(g.W))
-          src = g.a + (a_base[j] + int64_t(ih) * g.W + iw) * g.C_pad + l_cb * 64 + a_k[j];
+        // uniform offset of the step's tap and channel block (k_pad == k_real:
+        // the cursor never passes the last tap)
+        const int32_t dh = l_kh * g.DH, dw = l_kw * g.DW;
+        const int64_t step_off = (int64_t(dh) * g.W + dw) * g.C_pad + l_cb * 64;
+        const bool ok = unsigned(a_ih0[j] + dh) < unsigned(g.H) && unsigned(a_iw0[j] + dw) < unsigned(g.W);
+        src = reinterpret_cast<const void*>(ok ? a_addr + a_off[j] + step_off : zero_page);
       } else if constexpr (AMODE == A_CONV16) {
         const int32_t k = kt * BK + a_k[j];
         if (a_ok[j] && k < g.k_real) {
@@ -363,7 +380,7 @@ __global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, co
     }
 #pragma unroll
     for (int j = 0; j < B_OPS; ++j)
-      dma16(b_ok[j] ? static_cast<const void*>(b_src[j] + int64_t(kt) * (KB / 64) * g.n_pad * 64) : g_zero_page,
+      dma16(reinterpret_cast<const void*>(b_src[j] + ((uint64_t(kt) * (KB / 64) * g.n_pad * 64) & b_mask[j])),
             Bs + (wave * B_OPS + j) * 1024);
     if constexpr (AMODE == A_CONV64) {
       l_cb += KB / 64;
