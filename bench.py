@@ -1,6 +1,7 @@
 """Benchmark: W8A8 ResNet-18 inference on one MI355X through the rocm target.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 256] [--no-cpu-baseline]
+    python bench.py --workload mlp50m|mobilenetv2 [--batch B] [--steps K] [--warmup W]
 
 A step is one inference of the whole batch (all 20 int8 implicit-GEMM convs,
 pooling, the fc layer) with the input already resident in HBM.  Prints ONE
@@ -13,6 +14,15 @@ roofline   = the qconv2d kernels (the dominant kernel class): their algorithmic
 cpu_baseline = the NumPy golden model (oracle/golden.py, the reference cpu
              target's algorithms) on a 2-image sample with the same attrs,
              timed on this host.
+kernels    = every launch kind of the step: its summed launch durations and its
+             algorithmic rate, int8 TOP/s against 5.0 POPS for the contractions,
+             HBM GB/s against 8 TB/s for the rest.
+
+--workload mlp50m / mobilenetv2 time the other W8A8 networks the same way and
+print one JSON line with their per-kind breakdown (no cpu baseline): the 50M
+MLP at batch 1 runs its four layers on the decode-shaped weight-streaming
+qmatmul kernel, MobileNetV2 its 17 depthwise convolutions on the f32
+depthwise kernel; both are HBM-bound.
 """
 from __future__ import annotations
 
@@ -28,6 +38,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 INT8_PEAK_TOPS = 5000.0          # MI355X dense int8 MFMA peak (5.0 POPS)
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E peak (8 TB/s)
 
 
 def log(*a):
@@ -45,6 +56,96 @@ def build(batch: int, seed: int = 0, peaks=None):
         peaks = calibration_peaks(twin, [{"x": models.image_batch((2, 3, 224, 224), s)} for s in (11, 12)])
     quantize_w8a8(g, peaks=peaks)
     return g, peaks
+
+
+def build_workload(name: str, batch: int):
+    """A W8A8 graph of another configuration, calibrated as the parity tests do it."""
+    from mira_amd import models, passes
+    from mira_amd.quantize import calibration_peaks, quantize_w8a8
+    if name == "mlp50m":
+        builder, cb, seeds, gen = models.mlp_50m, 8, (2, 3), models.normal_batch
+    elif name == "mobilenetv2":
+        builder, cb, seeds, gen = models.mobilenet_v2, 2, (11, 12), models.image_batch
+    else:
+        raise SystemExit(f"unknown workload {name!r}")
+    g = builder(batch=batch, seed=0)
+    passes.optimize(g)
+    twin = builder(batch=cb, seed=0)
+    passes.optimize(twin)
+    shape = twin.inputs[0].type.shape
+    quantize_w8a8(g, peaks=calibration_peaks(twin, [{"x": gen(shape, s)} for s in seeds]))
+    return g, gen(g.inputs[0].type.shape, 7)
+
+
+def time_launches(exe, stream, reps: int = 3) -> dict:
+    """Per-kind device time of one pass: HIP events around every launch on its stream."""
+    import torch
+    handle = stream.cuda_stream
+    per_kind: dict[str, float] = {}
+    for _ in range(reps):
+        evs = []
+        for name, fn in exe.launches:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn(handle)
+            b.record(stream)
+            evs.append((name, a, b))
+        torch.cuda.synchronize()
+        for name, a, b in evs:
+            per_kind[name] = per_kind.get(name, 0.0) + a.elapsed_time(b) / reps
+    return per_kind
+
+
+def kernel_breakdown(exe, per_kind: dict) -> dict:
+    """Each launch kind against both rooflines: its algorithmic int8 ops in TOP/s against
+    the MFMA peak and its algorithmic HBM bytes in GB/s against the HBM peak.  `bound` is
+    the roofline that caps the kind at its arithmetic intensity (ops per byte above or
+    below the ridge point 5.0 POPS / 8 TB/s = 625)."""
+    out = {}
+    for name, ms in sorted(per_kind.items(), key=lambda kv: -kv[1]):
+        cost = [(b, o) for k, b, o in exe.launch_cost if k == name]
+        nbytes, nops = sum(b for b, _ in cost), sum(o for _, o in cost)
+        sec = ms * 1e-3
+        row = {"launches": len(cost), "ms": round(ms, 4)}
+        if nops:
+            row.update(tops=round(nops / sec / 1e12, 1), mfma_frac=round(nops / sec / 1e12 / INT8_PEAK_TOPS, 4))
+        if nbytes:
+            row.update(gbs=round(nbytes / sec / 1e9, 1), hbm_frac=round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4))
+        if nops or nbytes:
+            ridge = INT8_PEAK_TOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+            row["bound"] = "mfma" if nbytes == 0 or nops / nbytes >= ridge else "hbm"
+        out[name] = row
+    return out
+
+
+def bench_workload(args) -> int:
+    import torch
+    from mira_amd.compiler import compile_graph
+    from mira_amd.target import RocmTarget
+    g, x = build_workload(args.workload, args.batch)
+    runner = compile_graph(g, RocmTarget())
+    if len(runner.segments) != 1 or runner.segments[0].device != "rocm":
+        raise SystemExit(f"{args.workload}: expected one rocm segment, got "
+                         f"{[s.device for s in runner.segments]}")
+    exe = runner.segments[0].executable
+    exe.upload({g.inputs[0]: x})
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        exe.launch()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        exe.launch()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / args.steps
+    per_kind = time_launches(exe, stream)
+    log(f"{args.workload} batch {args.batch}: {args.steps} steps, {ms:.4f} ms/step")
+    print(json.dumps({"workload": args.workload, "batch": args.batch, "steps": args.steps, "warmup": args.warmup,
+                      "ms_per_step": round(ms, 4), "dtype": "int8", "data": "synthetic",
+                      "kernels": kernel_breakdown(exe, per_kind)}), flush=True)
+    return 0
 
 
 def cpu_baseline(peaks, macs_per_image: int) -> dict:
@@ -144,7 +245,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--batch", type=int, default=256)
+    ap.add_argument("--batch", type=int, default=None, help="default 256 (resnet18), 1 (mlp50m), 128 (mobilenetv2)")
+    ap.add_argument("--workload", default="resnet18", choices=["resnet18", "mlp50m", "mobilenetv2"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true", help="run the plain copy used to scale counters")
     ap.add_argument("--summarize-counters", metavar="DIR", help="summarize rocprofv3 --pmc CSV output in DIR")
@@ -157,6 +259,10 @@ def main() -> int:
         print("bench.py measures one GPU: this build has no multi-GPU path (the batch would shard by "
               "data parallelism; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
         return 2
+    if args.batch is None:
+        args.batch = {"resnet18": 256, "mlp50m": 1, "mobilenetv2": 128}[args.workload]
+    if args.workload != "resnet18":
+        return bench_workload(args)
 
     import torch
     from mira_amd import models
@@ -188,20 +294,7 @@ def main() -> int:
     log(f"{args.steps} steps: {ms:.3f} ms/step")
 
     # per-launch durations (events around every launch, same stream), 3 instrumented passes
-    handle = stream.cuda_stream
-    per_kind: dict[str, float] = {}
-    reps = 3
-    for _ in range(reps):
-        evs = []
-        for name, fn in exe.launches:
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            fn(handle)
-            b.record(stream)
-            evs.append((name, a, b))
-        torch.cuda.synchronize()
-        for name, a, b in evs:
-            per_kind[name] = per_kind.get(name, 0.0) + a.elapsed_time(b) / reps
+    per_kind = time_launches(exe, stream)
     conv_ms = per_kind.get("qconv2d", 0.0)
     n_conv = exe.kernel_counts.get("qconv2d", 0)
     conv_cost = [(b, o) for name, b, o in exe.launch_cost if name == "qconv2d"]
@@ -245,7 +338,10 @@ def main() -> int:
                      "frac": round(conv_tops / INT8_PEAK_TOPS, 4), "traffic": measured_traffic(args.batch),
                      "algorithmic_bytes_per_launch": int(conv_alg_bytes),
                      "launches_per_step": n_conv, "ms_per_step": round(conv_ms, 4),
-                     "us_per_launch": round(1e3 * conv_ms / max(1, n_conv), 2)},
+                     "us_per_launch": round(1e3 * conv_ms / max(1, n_conv), 2),
+                     "hbm_frac": round(conv_alg_bytes * n_conv / (conv_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "ops_per_byte": round(sum(o for _, o in conv_cost) / max(1, sum(b for b, _ in conv_cost)), 1)},
+        "kernels": kernel_breakdown(exe, per_kind),
     }
     if not args.no_cpu_baseline:
         log("timing the CPU golden model on a 2-image sample ...")

@@ -56,6 +56,121 @@ __global__ void __launch_bounds__(256) dwconv_kernel(const float* __restrict__ x
   }
 }
 
+// 3x3 depthwise convolution, dilation 1, stride SW in both directions,
+// C % 4 == 0: a thread owns 4 channels (one 16-byte run of an NHWC pixel) of
+// OWT adjacent output columns of one output row, loads each input row's
+// (OWT-1)*SW + 3 columns once for all of them, and keeps its 9 weight runs in
+// registers.  Per output element the arithmetic is the one above: +0, then
+// each tap's product added in (i, j) order with separate roundings.
+// EF: EF_GENERIC runs each element's epilogue through epi_steps (any legal
+// epilogue); EF_SPEC | flags is a compiled fixed form -- bias, NumPy maximum /
+// minimum with a wave-uniform bound, f32 and/or int8 out -- run as
+// straight-line code on constants loaded once per thread.
+constexpr int DW_OWT = 4;   // output columns per thread
+template <int SW, int EF>
+__global__ void __launch_bounds__(256) dwconv3x3_kernel(const float* __restrict__ x, mr_conv_geom G,
+                                                        const float* __restrict__ w, const EpiDev e, int cg4,
+                                                        int wtiles, bool vec_out) {
+  constexpr int KH = 3, KW = 3, IWN = (DW_OWT - 1) * SW + KW;
+  const int item = blockIdx.x * 256 + threadIdx.x;
+  if (item >= cg4 * wtiles) return;
+  const int oh = blockIdx.y;
+  const int64_t img = blockIdx.z;
+  const int wt = item / cg4;
+  const int c0 = (item - wt * cg4) * 4;
+  const int ow0 = wt * DW_OWT;
+
+  float4 wv[KH][KW];
+#pragma unroll
+  for (int i = 0; i < KH; ++i)
+#pragma unroll
+    for (int j = 0; j < KW; ++j) wv[i][j] = *reinterpret_cast<const float4*>(w + (i * KW + j) * G.c + c0);
+
+  float acc[DW_OWT][4];
+#pragma unroll
+  for (int k = 0; k < DW_OWT; ++k)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[k][q] = 0.0f;
+
+#pragma unroll
+  for (int i = 0; i < KH; ++i) {
+    const int ih = oh * G.sh - G.ph + i;
+    const bool row_ok = unsigned(ih) < unsigned(G.h);
+    const float* xr = x + ((img * G.h + min(max(ih, 0), G.h - 1)) * G.w) * G.c + c0;
+    float4 xin[IWN];
+#pragma unroll
+    for (int q = 0; q < IWN; ++q) {   // clamped addresses, selected after the load: all in flight at once
+      const int iw = ow0 * SW - G.pw + q;
+      const float4 v = *reinterpret_cast<const float4*>(xr + int64_t(min(max(iw, 0), G.w - 1)) * G.c);
+      xin[q] = row_ok && unsigned(iw) < unsigned(G.w) ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int j = 0; j < KW; ++j)
+#pragma unroll
+      for (int k = 0; k < DW_OWT; ++k) {
+        const float4 xv = xin[k * SW + j];
+        acc[k][0] = __fadd_rn(acc[k][0], __fmul_rn(xv.x, wv[i][j].x));
+        acc[k][1] = __fadd_rn(acc[k][1], __fmul_rn(xv.y, wv[i][j].y));
+        acc[k][2] = __fadd_rn(acc[k][2], __fmul_rn(xv.z, wv[i][j].z));
+        acc[k][3] = __fadd_rn(acc[k][3], __fmul_rn(xv.w, wv[i][j].w));
+      }
+  }
+
+  if constexpr (EF >= EF_SPEC) {
+    constexpr bool S_COL = EF & SF_COL, S_LO = EF & SF_LO, S_HI = EF & SF_HI, S_F32 = EF & SF_F32, S_I8 = EF & SF_I8;
+    static_assert(!(EF & SF_FULL), "no full-size operand in the compiled depthwise forms");
+    const float4 cv = S_COL ? *reinterpret_cast<const float4*>(e.col_ptr + c0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float col[4] = {cv.x, cv.y, cv.z, cv.w};
+    const float lo = S_LO && e.lo_ptr ? e.lo_ptr[0] : 0.0f;
+    const float hi = S_HI ? e.hi_ptr[0] : 0.0f;
+    const bool lo_nan = lo != lo, hi_nan = hi != hi;
+#pragma unroll
+    for (int k = 0; k < DW_OWT; ++k) {
+      const int ow = ow0 + k;
+      if (ow >= G.ow) break;
+      const int64_t pix = (img * G.oh + oh) * G.ow + ow;
+      float y[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float t = acc[k][q];
+        if constexpr (S_COL) t = __fadd_rn(t, col[q]);
+        if constexpr (S_LO) t = max_bound(t, lo, lo_nan);
+        if constexpr (S_HI) t = min_bound(t, hi, hi_nan);
+        y[q] = t;
+      }
+      if constexpr (S_F32) *reinterpret_cast<float4*>(e.out_f32 + pix * e.ldo + c0) = make_float4(y[0], y[1], y[2], y[3]);
+      if constexpr (S_I8) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) packed |= uint32_t(uint8_t(quantize_rcp(y[q], e.out_rxs))) << (8 * q);
+        *reinterpret_cast<uint32_t*>(e.out_i8 + pix * e.ldq + c0) = packed;
+      }
+    }
+    return;
+  }
+#pragma unroll 1
+  for (int k = 0; k < DW_OWT; ++k) {
+    const int ow = ow0 + k;
+    if (ow >= G.ow) break;
+    const int64_t pix = (img * G.oh + oh) * G.ow + ow;
+    float y[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) y[q] = epi_steps(e, acc[k][q], pix, c0 + q);
+    if (vec_out) {   // 16-byte f32 and 4-byte int8 runs (alignment checked on the host)
+      if (e.out_f32) *reinterpret_cast<float4*>(e.out_f32 + pix * e.ldo + c0) = make_float4(y[0], y[1], y[2], y[3]);
+      if (e.out_i8) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) packed |= uint32_t(uint8_t(quantize_rcp(y[q], e.out_rxs))) << (8 * q);
+        *reinterpret_cast<uint32_t*>(e.out_i8 + pix * e.ldq + c0) = packed;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) epi_store(e, y[q], pix, c0 + q);
+    }
+  }
+}
+
 // ---------------------------------------------------------------- maxpool
 
 template <typename Idx>
@@ -241,6 +356,40 @@ int mr_dwconv2d_f32(const float* x, const mr_conv_geom* cg, const float* w, cons
   const int64_t total = int64_t(G.n) * oh * ow * G.c;
   if (total == 0) return MR_OK;
   const int64_t in_total = int64_t(G.n) * G.h * G.w * G.c;
+  // 3x3, dilation 1, equal strides 1 or 2, 16-byte channel runs: the vectorized kernel
+  if (G.kh == 3 && G.kw == 3 && G.dh == 1 && G.dw == 1 && G.sh == G.sw && (G.sh == 1 || G.sh == 2) &&
+      G.c % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
+      G.n <= 65535 && oh <= 65535) {
+    const int cg4 = G.c / 4;
+    const int wtiles = (ow + mr::DW_OWT - 1) / mr::DW_OWT;
+    const bool vec_out = (!e.out_f32 || (e.ldo % 4 == 0 && reinterpret_cast<uintptr_t>(e.out_f32) % 16 == 0)) &&
+                         (!e.out_i8 || (e.ldq % 4 == 0 && reinterpret_cast<uintptr_t>(e.out_i8) % 4 == 0));
+    const dim3 grid(static_cast<unsigned>((int64_t(cg4) * wtiles + 255) / 256), static_cast<unsigned>(oh),
+                    static_cast<unsigned>(G.n));
+    // compiled forms: bias + ReLU6 / ReLU (maximum, minimum with scalars) to f32 and/or int8
+    int form = vec_out && (!e.f_col || reinterpret_cast<uintptr_t>(e.col_ptr) % 16 == 0) ? mr::spec_form(e) : -1;
+    constexpr int R6 = mr::SF_COL | mr::SF_LO | mr::SF_HI, R = mr::SF_COL | mr::SF_LO;
+#define MR_DW_LAUNCH(SWV, EFV) hipLaunchKernelGGL((mr::dwconv3x3_kernel<SWV, EFV>), grid, dim3(256), 0, \
+                                                  static_cast<hipStream_t>(stream), x, G, w, e, cg4, wtiles, vec_out)
+#define MR_DW_FORMS(SWV)                                                              \
+  switch (form) {                                                                   \
+    case R6 | mr::SF_F32 | mr::SF_I8: MR_DW_LAUNCH(SWV, mr::EF_SPEC | R6 | mr::SF_F32 | mr::SF_I8); break; \
+    case R6 | mr::SF_I8: MR_DW_LAUNCH(SWV, mr::EF_SPEC | R6 | mr::SF_I8); break;     \
+    case R6 | mr::SF_F32: MR_DW_LAUNCH(SWV, mr::EF_SPEC | R6 | mr::SF_F32); break;   \
+    case R | mr::SF_F32 | mr::SF_I8: MR_DW_LAUNCH(SWV, mr::EF_SPEC | R | mr::SF_F32 | mr::SF_I8); break; \
+    case R | mr::SF_I8: MR_DW_LAUNCH(SWV, mr::EF_SPEC | R | mr::SF_I8); break;       \
+    default: MR_DW_LAUNCH(SWV, mr::EF_GENERIC); break;                              \
+  }
+    if (G.sh == 1) {
+      MR_DW_FORMS(1)
+    } else {
+      MR_DW_FORMS(2)
+    }
+#undef MR_DW_FORMS
+#undef MR_DW_LAUNCH
+    MR_LAUNCH_CHECK("dwconv2d");
+    return MR_OK;
+  }
   if (total < (int64_t(1) << 32) - 65536 * 256 && in_total < (int64_t(1) << 32))
     hipLaunchKernelGGL(mr::dwconv_kernel<uint32_t>, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), x, G, w, e);

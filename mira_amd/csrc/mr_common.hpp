@@ -149,6 +149,22 @@ struct EpiDev {
   const float* hi_ptr;
 };
 
+// NumPy's maximum(y, b) / minimum(y, b) for a bound b that is the same for the
+// whole wave: an unordered compare and a select.  !(y <= b) holds for y > b
+// and for NaN y, so a NaN y propagates and equality returns b, as NumPy does;
+// a NaN bound is returned as is (it replaces y first, and !(NaN <= NaN)).
+// Every step is a vector instruction: folding b_nan into the compare's
+// condition instead puts a scalar OR between the compare and the select of
+// each element.
+__device__ __forceinline__ float max_bound(float y, float b, bool b_nan) {
+  const float v = b_nan ? b : y;
+  return !(v <= b) ? v : b;
+}
+__device__ __forceinline__ float min_bound(float y, float b, bool b_nan) {
+  const float v = b_nan ? b : y;
+  return !(v >= b) ? v : b;
+}
+
 // The general step interpreter (mira/ops.py:192-199) for one element at
 // (row, col): a rolled loop, so its code stays small; the descriptor is a
 // by-reference kernel argument and is read from the kernel-argument segment.

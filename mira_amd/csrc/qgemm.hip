@@ -109,12 +109,6 @@ struct EpiCols4 {
   bool vec;  // four valid columns and every access 16-byte (f32) / 4-byte (int8) aligned
 };
 
-// NumPy's maximum(y, b) / minimum(y, b) for a bound b that is the same for the
-// whole wave: one unordered compare and a select.  !(y <= b) holds for y > b
-// and for NaN y, so a NaN y propagates and equality returns b, as NumPy does;
-// a NaN bound is returned as is.
-__device__ __forceinline__ float max_bound(float y, float b, bool b_nan) { return !(y <= b) && !b_nan ? y : b; }
-__device__ __forceinline__ float min_bound(float y, float b, bool b_nan) { return !(y >= b) && !b_nan ? y : b; }
 
 // clip(rint(y / xs), -127, 127) with the division done as a multiplication by
 // the double-precision reciprocal (equal to the IEEE quotient; see

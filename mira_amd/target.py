@@ -316,11 +316,12 @@ class RocmExecutable:
             if d.f32 is not None:
                 dst = d.f32
                 self._add("input", lambda s: L.check(lib.mr_nchw_to_nhwc_f32(stage.data_ptr(), n, c, h, w,
-                                                                             dst.data_ptr(), s), "mr_nchw_to_nhwc_f32"))
+                                                                             dst.data_ptr(), s), "mr_nchw_to_nhwc_f32"),
+                          nbytes=8 * n * c * h * w)
             for xs, (q, cp) in d.i8.items():
                 self._add("input", lambda s, q=q, cp=cp, xs=xs: L.check(
                     lib.mr_quantize_nchw_nhwc(stage.data_ptr(), n, c, h, w, q.data_ptr(), cp, xs, s),
-                    "mr_quantize_nchw_nhwc"))
+                    "mr_quantize_nchw_nhwc"), nbytes=4 * n * c * h * w + n * h * w * cp)
         else:
             if d.f32 is not None:
                 d.f32 = stage.reshape(d.f32.shape)       # same layout: the kernels read the input itself
@@ -328,7 +329,7 @@ class RocmExecutable:
             for xs, (q, ld) in d.i8.items():
                 self._add("input", lambda s, q=q, ld=ld, xs=xs: L.check(
                     lib.mr_quantize_rows(stage.data_ptr(), rows, cols, cols, q.data_ptr(), ld, xs, s),
-                    "mr_quantize_rows"))
+                    "mr_quantize_rows"), nbytes=4 * rows * cols + rows * ld)
 
     def _upload(self, arr: np.ndarray, dtype=None):
         torch = _t()
@@ -392,7 +393,8 @@ class RocmExecutable:
         q = torch.empty((d.rows, ld), dtype=torch.int8, device=self.dev)
         lib, src, rows, cols = self.lib, d.f32, d.rows, d.cols
         self._add("quantize", lambda s: L.check(lib.mr_quantize_rows(src.data_ptr(), rows, cols, cols, q.data_ptr(),
-                                                                     ld, xs, s), "mr_quantize_rows"))
+                                                                     ld, xs, s), "mr_quantize_rows"),
+                  nbytes=4 * rows * cols + rows * ld)
         return q, ld
 
     def _finish_i8(self, d: DevValue, fused: Optional[float]) -> None:
@@ -539,7 +541,8 @@ class RocmExecutable:
         e, fused = self._epilogue(op, out, True, 2, None)
         lib, xt = self.lib, x.f32
         self._add("dwconv2d", lambda s: L.check(
-            lib.mr_dwconv2d_f32(xt.data_ptr(), C.byref(geom), wdev.data_ptr(), C.byref(e), s), "mr_dwconv2d_f32"))
+            lib.mr_dwconv2d_f32(xt.data_ptr(), C.byref(geom), wdev.data_ptr(), C.byref(e), s), "mr_dwconv2d_f32"),
+            nbytes=4 * n * c * h * w + 4 * c * kh * kw + self._epi_bytes(e, n * oh * ow, c))
         self._finish_i8(out, fused)
 
     def _emit_fused_stem(self, op: ir.Op) -> None:
@@ -601,7 +604,8 @@ class RocmExecutable:
         xsv = fused if fused is not None else 1.0
         self._add("maxpool2d", lambda s: L.check(lib.mr_maxpool2d_f32(
             xt.data_ptr(), n, h, w, c, k, st, pt, pl, pad_value, oh, ow, _ptr(yt), _ptr(yq), cp, xsv, s),
-            "mr_maxpool2d_f32"))
+            "mr_maxpool2d_f32"), nbytes=4 * n * h * w * c + (4 if yt is not None else 0) * n * oh * ow * c +
+            (n * oh * ow * cp if yq is not None else 0))
         self._finish_i8(out, fused)
 
     def _emit_pad(self, op: ir.Op) -> None:
@@ -615,7 +619,8 @@ class RocmExecutable:
             out.f32 = _t().empty((n, h + t + b, w + l + r, c), dtype=_t().float32, device=self.dev)
         lib, xt, yt = self.lib, x.f32, out.f32
         self._add("pad", lambda s: L.check(lib.mr_pad_hw_f32(xt.data_ptr(), n, h, w, c, t, b, l, r, value,
-                                                             yt.data_ptr(), s), "mr_pad_hw_f32"))
+                                                             yt.data_ptr(), s), "mr_pad_hw_f32"),
+                  nbytes=4 * n * c * (h * w + (h + t + b) * (w + l + r)))
         self._finish_i8(out, None)
 
     def _emit_reduce_mean(self, op: ir.Op) -> None:
@@ -632,7 +637,8 @@ class RocmExecutable:
         lib, xt, yt = self.lib, x.f32, out.f32
         xsv = fused if fused is not None else 1.0
         self._add("mean_hw", lambda s: L.check(lib.mr_mean_hw_f32(
-            xt.data_ptr(), n, h * w, c, _ptr(yt), _ptr(yq), ld, xsv, s), "mr_mean_hw_f32"))
+            xt.data_ptr(), n, h * w, c, _ptr(yt), _ptr(yq), ld, xsv, s), "mr_mean_hw_f32"),
+            nbytes=4 * n * h * w * c + (4 if yt is not None else 0) * n * c + (n * ld if yq is not None else 0))
         self._finish_i8(out, fused)
 
     def _emit_reshape(self, op: ir.Op) -> None:
@@ -659,13 +665,13 @@ class RocmExecutable:
                 canon = torch.empty((n, c, h, w), dtype=torch.float32, device=self.dev)
                 lib, xt, ct = self.lib, x.f32, canon
                 self._add("nhwc_to_nchw", lambda s: L.check(lib.mr_nhwc_to_nchw_f32(
-                    xt.data_ptr(), n, c, h, w, ct.data_ptr(), s), "mr_nhwc_to_nchw_f32"))
+                    xt.data_ptr(), n, c, h, w, ct.data_ptr(), s), "mr_nhwc_to_nchw_f32"), nbytes=8 * n * c * h * w)
             if d.nhwc:
                 n, c, h, w = r.type.shape
                 d.f32 = torch.empty((n, h, w, c), dtype=torch.float32, device=self.dev)
                 lib, ct, yt = self.lib, canon, d.f32
                 self._add("nchw_to_nhwc", lambda s: L.check(lib.mr_nchw_to_nhwc_f32(
-                    ct.data_ptr(), n, c, h, w, yt.data_ptr(), s), "mr_nchw_to_nhwc_f32"))
+                    ct.data_ptr(), n, c, h, w, yt.data_ptr(), s), "mr_nchw_to_nhwc_f32"), nbytes=8 * n * c * h * w)
             else:
                 d.f32 = canon
         else:

@@ -327,32 +327,45 @@ def test_qmatmul_epilogue_forms(lib, form, M, K, N):
 
 # ---------------------------------------------------------------- K4a depthwise, adjuncts
 
-@pytest.mark.parametrize("n,c,h,s", [(2, 32, 16, 1), (2, 144, 15, 2), (1, 960, 7, 1)])
-def test_dwconv_relu6(lib, n, c, h, s):
+@pytest.mark.parametrize("n,c,h,s,k,form,ldo_pad", [
+    (2, 32, 16, 1, 3, "relu6", 0),      # 3x3, 4-channel runs: vectorized kernel
+    (2, 144, 15, 2, 3, "relu6", 0),     # stride 2, last column tile partial
+    (1, 960, 7, 1, 3, "relu6", 0),      # 7 columns: one full and one partial tile
+    (2, 8, 13, 2, 3, "generic", 0),     # step interpreter epilogue (swapped subtract)
+    (2, 16, 9, 1, 3, "relu6", 1),       # f32 rows not 16-byte aligned: element stores
+    (1, 6, 9, 1, 3, "relu6", 0),        # 6 channels: per-element kernel
+    (2, 8, 11, 1, 5, "relu6", 0),       # 5x5: per-element kernel
+])
+def test_dwconv_relu6(lib, n, c, h, s, k, form, ldo_pad):
     torch = _torch()
-    rng = np.random.default_rng(c)
+    rng = np.random.default_rng(c + k)
     x = (rng.standard_normal((n, c, h, h)) * 2).astype(np.float32)
-    wt = rng.standard_normal((c, 1, 3, 3)).astype(np.float32)
+    wt = rng.standard_normal((c, 1, k, k)).astype(np.float32)
     bias = (rng.standard_normal((c, 1, 1)) * 0.1).astype(np.float32)
     zero, six = np.array(0, np.float32), np.array(6, np.float32)
-    attrs = {"stride": (s, s), "padding": (1, 1), "groups": c,
-             "epilogue": (("add", 2, False), ("maximum", 3, False), ("minimum", 4, False))}
+    p = k // 2
+    steps = ((("add", 2, False), ("maximum", 3, False), ("minimum", 4, False)) if form == "relu6" else
+             (("sub", 2, True), ("relu", None, False)))
+    attrs = {"stride": (s, s), "padding": (p, p), "groups": c, "epilogue": steps}
     want = G.conv2d([x, wt, bias, zero, six], attrs)
     oh = want.shape[2]
     xs_next = float(want.max()) / 127 or 1.0
     xd = T(x.transpose(0, 2, 3, 1))
     wd = T(np.ascontiguousarray(wt[:, 0].transpose(1, 2, 0)))
-    g = L.ConvGeom(n=n, h=h, w=h, c=c, c_pad=c, o=c, oh=oh, ow=oh, kh=3, kw=3, sh=s, sw=s, ph=1, pw=1, dh=1, dw=1)
+    g = L.ConvGeom(n=n, h=h, w=h, c=c, c_pad=c, o=c, oh=oh, ow=oh, kh=k, kw=k, sh=s, sw=s, ph=p, pw=p, dh=1, dw=1)
     M = n * oh * oh
-    y = empty((M, c), torch.float32)
+    ldo = c + ldo_pad
+    y = empty((M, ldo), torch.float32)
     cp = pack.c_pad_for(c)
     yq = empty((M, cp), torch.int8)
     bt, zt, st = T(bias.reshape(c)), T(zero.reshape(1)), T(six.reshape(1))
-    e = epilogue([("add", L.BC_COL, bt, 0, False), ("maximum", L.BC_SCALAR, zt, 0, False),
-                  ("minimum", L.BC_SCALAR, st, 0, False)], out_f32=y, ldo=c, out_i8=yq, ldq=cp, xs=xs_next)
+    dev_steps = ([("add", L.BC_COL, bt, 0, False), ("maximum", L.BC_SCALAR, zt, 0, False),
+                  ("minimum", L.BC_SCALAR, st, 0, False)] if form == "relu6" else
+                 [("sub", L.BC_COL, bt, 0, True), ("relu", 0, None, 0, False)])
+    e = epilogue(dev_steps, out_f32=y, ldo=ldo, out_i8=yq, ldq=cp, xs=xs_next)
     L.check(lib.mr_dwconv2d_f32(xd.data_ptr(), C.byref(g), wd.data_ptr(), C.byref(e), stream()), "dw")
     sync()
-    assert bits_equal(y.cpu().numpy(), want.transpose(0, 2, 3, 1).reshape(M, c))
+    assert bits_equal(y.cpu().numpy()[:, :c], want.transpose(0, 2, 3, 1).reshape(M, c))
     assert bits_equal(yq.cpu().numpy()[:, :c],
                       G.quantize_activation(want, xs_next).astype(np.int8).transpose(0, 2, 3, 1).reshape(M, c))
 
