@@ -58,27 +58,27 @@ __global__ void __launch_bounds__(256) dwconv_kernel(const float* __restrict__ x
 
 // 3x3 depthwise convolution, dilation 1, stride SW in both directions,
 // C % 4 == 0: a thread owns 4 channels (one 16-byte run of an NHWC pixel) of
-// OWT adjacent output columns of one output row, loads each input row's
-// (OWT-1)*SW + 3 columns once for all of them, and keeps its 9 weight runs in
-// registers.  Per output element the arithmetic is the one above: +0, then
+// OWT adjacent output columns of one output row (4 for stride-1 maps wider
+// than 28 columns, else 2: measured on the MobileNetV2 layers), loads each
+// input row's (OWT-1)*SW + 3 columns once for all of them, and keeps its 9
+// weight runs in registers.  Per output element the arithmetic is the one above: +0, then
 // each tap's product added in (i, j) order with separate roundings.
 // EF: EF_GENERIC runs each element's epilogue through epi_steps (any legal
 // epilogue); EF_SPEC | flags is a compiled fixed form -- bias, NumPy maximum /
 // minimum with a wave-uniform bound, f32 and/or int8 out -- run as
 // straight-line code on constants loaded once per thread.
-constexpr int DW_OWT = 4;   // output columns per thread
-template <int SW, int EF>
+template <int SW, int OWT, int EF>
 __global__ void __launch_bounds__(256) dwconv3x3_kernel(const float* __restrict__ x, mr_conv_geom G,
                                                         const float* __restrict__ w, const EpiDev e, int cg4,
                                                         int wtiles, bool vec_out) {
-  constexpr int KH = 3, KW = 3, IWN = (DW_OWT - 1) * SW + KW;
+  constexpr int KH = 3, KW = 3, IWN = (OWT - 1) * SW + KW;
   const int item = blockIdx.x * 256 + threadIdx.x;
   if (item >= cg4 * wtiles) return;
   const int oh = blockIdx.y;
   const int64_t img = blockIdx.z;
   const int wt = item / cg4;
   const int c0 = (item - wt * cg4) * 4;
-  const int ow0 = wt * DW_OWT;
+  const int ow0 = wt * OWT;
 
   float4 wv[KH][KW];
 #pragma unroll
@@ -86,9 +86,9 @@ __global__ void __launch_bounds__(256) dwconv3x3_kernel(const float* __restrict_
 #pragma unroll
     for (int j = 0; j < KW; ++j) wv[i][j] = *reinterpret_cast<const float4*>(w + (i * KW + j) * G.c + c0);
 
-  float acc[DW_OWT][4];
+  float acc[OWT][4];
 #pragma unroll
-  for (int k = 0; k < DW_OWT; ++k)
+  for (int k = 0; k < OWT; ++k)
 #pragma unroll
     for (int q = 0; q < 4; ++q) acc[k][q] = 0.0f;
 
@@ -107,7 +107,7 @@ __global__ void __launch_bounds__(256) dwconv3x3_kernel(const float* __restrict_
 #pragma unroll
     for (int j = 0; j < KW; ++j)
 #pragma unroll
-      for (int k = 0; k < DW_OWT; ++k) {
+      for (int k = 0; k < OWT; ++k) {
         const float4 xv = xin[k * SW + j];
         acc[k][0] = __fadd_rn(acc[k][0], __fmul_rn(xv.x, wv[i][j].x));
         acc[k][1] = __fadd_rn(acc[k][1], __fmul_rn(xv.y, wv[i][j].y));
@@ -125,7 +125,7 @@ __global__ void __launch_bounds__(256) dwconv3x3_kernel(const float* __restrict_
     const float hi = S_HI ? e.hi_ptr[0] : 0.0f;
     const bool lo_nan = lo != lo, hi_nan = hi != hi;
 #pragma unroll
-    for (int k = 0; k < DW_OWT; ++k) {
+    for (int k = 0; k < OWT; ++k) {
       const int ow = ow0 + k;
       if (ow >= G.ow) break;
       const int64_t pix = (img * G.oh + oh) * G.ow + ow;
@@ -149,7 +149,7 @@ __global__ void __launch_bounds__(256) dwconv3x3_kernel(const float* __restrict_
     return;
   }
 #pragma unroll 1
-  for (int k = 0; k < DW_OWT; ++k) {
+  for (int k = 0; k < OWT; ++k) {
     const int ow = ow0 + k;
     if (ow >= G.ow) break;
     const int64_t pix = (img * G.oh + oh) * G.ow + ow;
@@ -361,7 +361,8 @@ int mr_dwconv2d_f32(const float* x, const mr_conv_geom* cg, const float* w, cons
       G.c % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
       G.n <= 65535 && oh <= 65535) {
     const int cg4 = G.c / 4;
-    const int wtiles = (ow + mr::DW_OWT - 1) / mr::DW_OWT;
+    const int owt = G.sh == 1 && ow > 28 ? 4 : 2;
+    const int wtiles = (ow + owt - 1) / owt;
     const bool vec_out = (!e.out_f32 || (e.ldo % 4 == 0 && reinterpret_cast<uintptr_t>(e.out_f32) % 16 == 0)) &&
                          (!e.out_i8 || (e.ldq % 4 == 0 && reinterpret_cast<uintptr_t>(e.out_i8) % 4 == 0));
     const dim3 grid(static_cast<unsigned>((int64_t(cg4) * wtiles + 255) / 256), static_cast<unsigned>(oh),
@@ -369,21 +370,24 @@ int mr_dwconv2d_f32(const float* x, const mr_conv_geom* cg, const float* w, cons
     // compiled forms: bias + ReLU6 / ReLU (maximum, minimum with scalars) to f32 and/or int8
     int form = vec_out && (!e.f_col || reinterpret_cast<uintptr_t>(e.col_ptr) % 16 == 0) ? mr::spec_form(e) : -1;
     constexpr int R6 = mr::SF_COL | mr::SF_LO | mr::SF_HI, R = mr::SF_COL | mr::SF_LO;
-#define MR_DW_LAUNCH(SWV, EFV) hipLaunchKernelGGL((mr::dwconv3x3_kernel<SWV, EFV>), grid, dim3(256), 0, \
-                                                  static_cast<hipStream_t>(stream), x, G, w, e, cg4, wtiles, vec_out)
-#define MR_DW_FORMS(SWV)                                                              \
-  switch (form) {                                                                   \
-    case R6 | mr::SF_F32 | mr::SF_I8: MR_DW_LAUNCH(SWV, mr::EF_SPEC | R6 | mr::SF_F32 | mr::SF_I8); break; \
-    case R6 | mr::SF_I8: MR_DW_LAUNCH(SWV, mr::EF_SPEC | R6 | mr::SF_I8); break;     \
-    case R6 | mr::SF_F32: MR_DW_LAUNCH(SWV, mr::EF_SPEC | R6 | mr::SF_F32); break;   \
-    case R | mr::SF_F32 | mr::SF_I8: MR_DW_LAUNCH(SWV, mr::EF_SPEC | R | mr::SF_F32 | mr::SF_I8); break; \
-    case R | mr::SF_I8: MR_DW_LAUNCH(SWV, mr::EF_SPEC | R | mr::SF_I8); break;       \
-    default: MR_DW_LAUNCH(SWV, mr::EF_GENERIC); break;                              \
+#define MR_DW_LAUNCH(SWV, OWTV, EFV)                                                                  \
+  hipLaunchKernelGGL((mr::dwconv3x3_kernel<SWV, OWTV, EFV>), grid, dim3(256), 0, static_cast<hipStream_t>(stream), \
+                     x, G, w, e, cg4, wtiles, vec_out)
+#define MR_DW_FORMS(SWV, OWTV)                                                                             \
+  switch (form) {                                                                                          \
+    case R6 | mr::SF_F32 | mr::SF_I8: MR_DW_LAUNCH(SWV, OWTV, mr::EF_SPEC | R6 | mr::SF_F32 | mr::SF_I8); break; \
+    case R6 | mr::SF_I8: MR_DW_LAUNCH(SWV, OWTV, mr::EF_SPEC | R6 | mr::SF_I8); break;                     \
+    case R6 | mr::SF_F32: MR_DW_LAUNCH(SWV, OWTV, mr::EF_SPEC | R6 | mr::SF_F32); break;                   \
+    case R | mr::SF_F32 | mr::SF_I8: MR_DW_LAUNCH(SWV, OWTV, mr::EF_SPEC | R | mr::SF_F32 | mr::SF_I8); break; \
+    case R | mr::SF_I8: MR_DW_LAUNCH(SWV, OWTV, mr::EF_SPEC | R | mr::SF_I8); break;                       \
+    default: MR_DW_LAUNCH(SWV, OWTV, mr::EF_GENERIC); break;                                              \
   }
-    if (G.sh == 1) {
-      MR_DW_FORMS(1)
+    if (G.sh == 2) {
+      MR_DW_FORMS(2, 2)
+    } else if (owt == 4) {
+      MR_DW_FORMS(1, 4)
     } else {
-      MR_DW_FORMS(2)
+      MR_DW_FORMS(1, 2)
     }
 #undef MR_DW_FORMS
 #undef MR_DW_LAUNCH

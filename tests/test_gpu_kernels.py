@@ -328,7 +328,8 @@ def test_qmatmul_epilogue_forms(lib, form, M, K, N):
 # ---------------------------------------------------------------- K4a depthwise, adjuncts
 
 @pytest.mark.parametrize("n,c,h,s,k,form,ldo_pad", [
-    (2, 32, 16, 1, 3, "relu6", 0),      # 3x3, 4-channel runs: vectorized kernel
+    (2, 32, 16, 1, 3, "relu6", 0),      # 3x3, 4-channel runs: vectorized kernel, 2 columns per thread
+    (1, 8, 30, 1, 3, "relu6", 0),       # 4 columns per thread, last tile 2 of 4
     (2, 144, 15, 2, 3, "relu6", 0),     # stride 2, last column tile partial
     (1, 960, 7, 1, 3, "relu6", 0),      # 7 columns: one full and one partial tile
     (2, 8, 13, 2, 3, "generic", 0),     # step interpreter epilogue (swapped subtract)
