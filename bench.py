@@ -240,6 +240,39 @@ def summarize_counters(d: str) -> int:
     return 0
 
 
+def summarize_mfma(d: str) -> int:
+    """MFMA utilisation per kernel from `rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE
+    --output-format csv -d d/mfma -o run -- python3 bench.py ...`.
+
+    SQ_VALU_MFMA_BUSY_CYCLES sums the cycles each of the 1024 SIMDs (256 CUs x 4) spent on
+    MFMA work; GRBM_GUI_ACTIVE sums the busy cycles of the 8 XCDs.  Utilisation =
+    (MFMA busy cycles per SIMD) / (kernel cycles) = MFMA_BUSY / (GUI_ACTIVE * 1024 / 8)."""
+    import csv
+    import collections
+    rows = list(csv.DictReader(open(os.path.join(d, "mfma", "run_counter_collection.csv"))))
+    per = collections.defaultdict(lambda: collections.defaultdict(float))
+    disp = collections.defaultdict(set)
+    for r in rows:
+        k = r["Kernel_Name"]
+        per[k][r["Counter_Name"]] += float(r["Counter_Value"])
+        disp[k].add(r["Dispatch_Id"])
+    print(f"{'kernel':72s} {'launches':>8s} {'MFMA busy':>10s}")
+    conv_busy = conv_active = 0.0
+    for k, c in sorted(per.items(), key=lambda kv: -kv[1].get("GRBM_GUI_ACTIVE", 0.0)):
+        act = c.get("GRBM_GUI_ACTIVE", 0.0)
+        if "rocclr" in k or act <= 0:
+            continue
+        util = c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (act * 1024 / 8)
+        print(f"{k[:72]:72s} {len(disp[k]):8d} {100 * util:9.2f}%")
+        targs = k[k.find("<") + 1:k.find(">")].split(",") if "qgemm_kernel<" in k else []
+        if len(targs) >= 6 and int(targs[5]) != 0:
+            conv_busy += c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0)
+            conv_active += act
+    if conv_active:
+        print(f"qconv2d_mfma_busy_fraction: {conv_busy / (conv_active * 1024 / 8):.4f}")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -250,9 +283,12 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true", help="run the plain copy used to scale counters")
     ap.add_argument("--summarize-counters", metavar="DIR", help="summarize rocprofv3 --pmc CSV output in DIR")
+    ap.add_argument("--summarize-mfma", metavar="DIR", help="MFMA utilisation from rocprofv3 --pmc CSV output in DIR/mfma")
     args = ap.parse_args()
     if args.summarize_counters:
         return summarize_counters(args.summarize_counters)
+    if args.summarize_mfma:
+        return summarize_mfma(args.summarize_mfma)
     if args.copy_calibration:
         return copy_calibration()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
