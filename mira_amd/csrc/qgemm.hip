@@ -196,8 +196,14 @@ __device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, c
 // KB: K bytes per ring stage, 64 or 128 (two 64-byte K steps: each A and B
 // row then moves as one 128-byte run, a whole cache line; dense and
 // c_pad % 128 == 0 conv loaders only).
+//
+// The 64-column patch tiles (ResNet layer 1) are held to 128 VGPRs, 4 waves per
+// SIMD: their residual epilogues stream 0.5 GB per launch, and the fourth
+// workgroup per CU hides more of that latency than the registers it costs.
 template <int BM, int BN, int WM, int WN, int STAGES, int AMODE, int EF, int KB = 64>
-__global__ void __launch_bounds__(WM* WN * 64) qgemm_kernel(const GemmArgs g, const EpiDev e) {
+__global__ void __launch_bounds__(WM* WN * 64)
+    __attribute__((amdgpu_waves_per_eu((AMODE == A_PATCH && BN == 64) ? 4 : 1)))
+    qgemm_kernel(const GemmArgs g, const EpiDev e) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM;
   constexpr int TN = BN / WN;
