@@ -634,7 +634,7 @@ static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(int64_t(g.tiles_m) * g.tiles_n)), block(WM * WN * 64);
 #define MR_QGEMM_LAUNCH(EFV) hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, STAGES, AMODE, EFV, KB>), grid, block, 0, \
                                                 stream, g, e)
-  // compiled forms: the conv modes of the ResNet-style networks and the dense GEMM
+  // compiled forms: the conv modes of the ResNet- and MobileNet-style networks and the dense GEMM
   constexpr bool CONV_SPEC = AMODE == A_CONV64 || AMODE == A_PATCH;
   if constexpr (CONV_SPEC || AMODE == A_DENSE) {
     switch (spec_form(e)) {
@@ -648,6 +648,14 @@ static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
       case SPEC_RES_F32_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_F32_I8); return;
       case SPEC_RES_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_I8); return;
       case SPEC_RES_F32: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_F32); return;
+      default: break;
+    }
+  }
+  if constexpr (AMODE == A_CONV16 || AMODE == A_CONV64 || AMODE == A_CONV4) {
+    switch (spec_form(e)) {
+      case SPEC_RELU6_F32: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RELU6_F32); return;
+      case SPEC_BIAS_F32_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_F32_I8); return;
+      case SPEC_BIAS_RES_F32_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_RES_F32_I8); return;
       default: break;
     }
   }

@@ -228,6 +228,8 @@ FORMS = {
     "res_f32": ((("add", 1, False), ("add", 2, False), ("relu", None, False)), True, False),
     "bias_f32": ((("add", 1, False),), True, False),
     "bias_relu6_f32": ((("add", 1, False), ("maximum", 3, False), ("minimum", 4, False)), True, False),
+    "bias_f32_i8": ((("add", 1, False),), True, True),
+    "bias_res_f32_i8": ((("add", 1, False), ("add", 2, False)), True, True),
 }
 FORM_CONV_CASES = [
     (2, 64, 56, 56, 64, 3, 1, 1, 1),      # patch, 128x64 tiles
@@ -239,6 +241,8 @@ FORM_CONV_CASES = [
     (2, 64, 15, 15, 128, 3, 2, 1, 1),     # stride 2, 64-channel loader
     (1, 256, 7, 7, 512, 3, 1, 1, 1),      # 128x256 tiles
     (2, 64, 14, 14, 128, 1, 2, 0, 1),     # downsample
+    (2, 24, 14, 14, 144, 1, 1, 0, 1),     # 1x1 expansion, 16-byte chunk loader (c_pad 32)
+    (2, 3, 17, 17, 32, 3, 2, 1, 1),       # 3-channel stem, 4-channel loader
 ]
 
 
