@@ -681,7 +681,9 @@ static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
       launch_cfg<PATCH_BM64, 64, 4, 1, 3, AMODE>(g, e, stream);
     else
       launch_cfg<PATCH_BM128, 128, 2, 2, 3, AMODE>(g, e, stream);
-  } else if (g.N <= 32) {
+  } else if (g.N <= 32 || (g.M + 63) / 64 * ((g.N + 31) / 32) <= 2 * cus) {
+    // N <= 32, or a grid so small (the fc layer of a CNN: M = batch) that even
+    // 64x32 tiles give at most two per CU: the most workgroups wins
     launch_cfg<64, 32, 2, 1, 4, AMODE>(g, e, stream);
   } else if (g.N <= 64) {
     launch_cfg<128, 64, 4, 1, 3, AMODE>(g, e, stream);
