@@ -334,6 +334,8 @@ class RocmExecutable:
     def _upload(self, arr: np.ndarray, dtype=None):
         torch = _t()
         a = np.ascontiguousarray(arr if dtype is None else arr.astype(dtype))
+        if not a.flags.writeable:        # torch wraps only writable arrays (a read-only const attr)
+            a = a.copy()
         t = torch.from_numpy(a).to(self.dev)
         self.const_bytes += a.nbytes
         self.keep.append(t)
