@@ -228,12 +228,17 @@ class RocmExecutable:
                 for v in op.inputs:
                     if v not in self.consts or op.kind != "conv2d" or v is op.inputs[0]:
                         self.need_f32.add(v)
-        # reshapes: the input must provide what the output's consumers read
+        # reshapes: the input must provide what the output's consumers read; a reshape
+        # that keeps the int8 layout (same rows, columns and row stride) passes its
+        # int8 copies through, so the producer writes them in its epilogue
         for op in reversed(g.ops):
             if op.kind == "reshape":
                 r = op.result
                 if r in self.need_f32 or r in self.need_i8:
                     self.need_f32.add(op.inputs[0])
+                if r in self.need_i8 and self._i8_view(op.inputs[0], r):
+                    lst = self.need_i8.setdefault(op.inputs[0], [])
+                    lst += [s for s in self.need_i8[r] if s not in lst]
         self.staging: dict[ir.Value, object] = {}
         for v in g.inputs:
             self._emit_input(v)
@@ -244,6 +249,17 @@ class RocmExecutable:
         for v in g.outputs:
             if v in self.consts and v not in self.dv:
                 self._const_dv(v)
+
+    @staticmethod
+    def _i8_view(src: ir.Value, r: ir.Value) -> bool:
+        """Is the int8 copy of `r` (a reshape of `src`) the same bytes as src's? Only for
+        [n, c, 1, 1] <-> [n, c] (global average pooling into an fc layer): NHWC with 1x1
+        pixels is row-major [n, c], and both strides round c up to 16."""
+        a, b = tuple(src.type.shape), tuple(r.type.shape)
+        if len(a) == 4 and len(b) == 2:
+            a, b = b, a
+        return len(a) == 2 and len(b) == 4 and b[2] == b[3] == 1 and a == (b[0], b[1]) and \
+            pack.c_pad_for(b[1]) == pack.row_stride_for(b[1])
 
     def _stem_fusable(self, conv: Optional[ir.Op], pad_op: ir.Op, pool: ir.Op) -> bool:
         """Can qconv2d -> pad -> maxpool2d run as mr_qconv2d_maxpool (the convolution is never stored)?
@@ -402,7 +418,7 @@ class RocmExecutable:
     def _finish_i8(self, d: DevValue, fused: Optional[float]) -> None:
         """int8 copies the producer did not write itself come from its f32 copy."""
         for xs in self.need_i8.get(d.value, []):
-            if xs != fused:
+            if xs != fused and xs not in d.i8:
                 d.i8[xs] = self._quantize_to(d, xs)
 
     # ---------------------------------------------------------------- epilogue descriptors
@@ -678,6 +694,10 @@ class RocmExecutable:
                 d.f32 = canon
         else:
             raise L.RocmError("reshape input has no f32 copy")
+        if self._i8_view(src_v, r):
+            for xs in self.need_i8.get(r, []):
+                if xs in x.i8:
+                    d.i8[xs] = x.i8[xs]
         self._finish_i8(d, None)
 
     # ---------------------------------------------------------------- run
