@@ -292,8 +292,8 @@ def main() -> int:
     if args.copy_calibration:
         return copy_calibration()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the batch would shard by "
-              "data parallelism; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: the rocm target has no multi-GPU path (the batch would shard "
+              "by data parallelism, one share per GPU). Run with --gpus 1.", file=sys.stderr)
         return 2
     if args.batch is None:
         args.batch = {"resnet18": 256, "mlp50m": 1, "mobilenetv2": 128}[args.workload]

@@ -36,7 +36,7 @@ enum mr_status {
   MR_OK = 0,
   MR_EINVAL = 1,      /* bad argument (shape, pointer, alignment) */
   MR_EHIP = 2,        /* a HIP runtime call failed */
-  MR_EUNSUPPORTED = 3 /* valid request this build has no kernel for */
+  MR_EUNSUPPORTED = 3 /* valid request the library has no kernel for */
 };
 
 /* Epilogue step functions: the fusable ops of mira/passes.py:151-152 that

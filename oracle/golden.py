@@ -1,8 +1,8 @@
 """NumPy restatement of MIRA's `cpu` golden model for the W8A8 inference path.
 
 TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py may import this module, and only as the checker
-(or, in bench.py, as the timed CPU baseline).  The rocm target never calls it:
+cpu_baseline leg of bench.py may import this module, and only to check GPU results
+against (or, in bench.py, as the timed CPU baseline).  The rocm target never calls it:
 its run path is the HIP library, and it fails loudly without it.
 
 Every function restates one reference function; the docstring names the

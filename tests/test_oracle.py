@@ -1,4 +1,4 @@
-"""Pin the oracle (oracle/golden.py) before trusting it as the checker.
+"""Pin the oracle (oracle/golden.py) before the GPU parity tests compare against it.
 
 The reference ships no golden vectors or known-answer tests for W8A8
 (its only W8A8 tests are tolerance tests, tests/test_control_dynamic_quant.py:
