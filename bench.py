@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 256] [--no-cpu-baseline]
     python bench.py --workload mlp50m|mobilenetv2 [--batch B] [--steps K] [--warmup W]
+    python bench.py --per-launch [--workload W] [--batch B]
 
 A step is one inference of the whole batch (all 20 int8 implicit-GEMM convs,
 pooling, the fc layer) with the input already resident in HBM.  Prints ONE
@@ -116,6 +117,53 @@ def kernel_breakdown(exe, per_kind: dict) -> dict:
             row["bound"] = "mfma" if nbytes == 0 or nops / nbytes >= ridge else "hbm"
         out[name] = row
     return out
+
+
+def per_launch(args) -> int:
+    """One row per launch of a step: its device time (HIP events around it, mean of 5 passes),
+    algorithmic ops and bytes, and the fraction of its roofline time it reaches --
+    roofline time = max(ops / 5.0 POPS, bytes / 8 TB/s)."""
+    import torch
+    from mira_amd import models
+    from mira_amd.compiler import compile_graph
+    from mira_amd.target import RocmTarget
+    if args.workload == "resnet18":
+        g, _ = build(args.batch)
+        x = models.image_batch((args.batch, 3, 224, 224), 7)
+    else:
+        g, x = build_workload(args.workload, args.batch)
+    runner = compile_graph(g, RocmTarget())
+    exe = runner.segments[0].executable
+    exe.upload({g.inputs[0]: x})
+    stream = torch.cuda.current_stream()
+    handle = stream.cuda_stream
+    for _ in range(3):
+        exe.launch()
+    torch.cuda.synchronize()
+    reps = 5
+    t = np.zeros(len(exe.launches))
+    for _ in range(reps):
+        evs = []
+        for _name, fn in exe.launches:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn(handle)
+            b.record(stream)
+            evs.append((a, b))
+        torch.cuda.synchronize()
+        t += np.array([a.elapsed_time(b) for a, b in evs]) * 1e3 / reps
+    print(f"{'#':>3s} {'kind':16s} {'us':>8s} {'GOP':>8s} {'MB':>8s} {'TOP/s':>7s} {'TB/s':>6s} "
+          f"{'ops/B':>6s} {'bound':>5s} {'roof us':>8s} {'frac':>6s}")
+    for i, ((name, _fn), (_, nb, no)) in enumerate(zip(exe.launches, exe.launch_cost)):
+        us = t[i]
+        roof_mfma, roof_hbm = no / (INT8_PEAK_TOPS * 1e12) * 1e6, nb / (HBM_PEAK_GBS * 1e9) * 1e6
+        roof = max(roof_mfma, roof_hbm)
+        bound = "-" if roof == 0 else ("mfma" if roof_mfma >= roof_hbm else "hbm")
+        print(f"{i:3d} {name:16s} {us:8.1f} {no / 1e9:8.2f} {nb / 1e6:8.1f} {no / us / 1e6 if us else 0:7.1f} "
+              f"{nb / us / 1e6 if us else 0:6.2f} {no / nb if nb else 0:6.0f} {bound:>5s} {roof:8.1f} "
+              f"{roof / us if us else 0:6.3f}")
+    print(f"total {t.sum():.1f} us of launches; roofline {sum(max(o / 5e15, b / 8e12) for _, b, o in exe.launch_cost) * 1e6:.1f} us")
+    return 0
 
 
 def bench_workload(args) -> int:
@@ -280,6 +328,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=None, help="default 256 (resnet18), 1 (mlp50m), 128 (mobilenetv2)")
     ap.add_argument("--workload", default="resnet18", choices=["resnet18", "mlp50m", "mobilenetv2"])
+    ap.add_argument("--per-launch", action="store_true", help="per-launch time against each launch's roofline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true", help="run the plain copy used to scale counters")
     ap.add_argument("--summarize-counters", metavar="DIR", help="summarize rocprofv3 --pmc CSV output in DIR")
@@ -297,6 +346,8 @@ def main() -> int:
         return 2
     if args.batch is None:
         args.batch = {"resnet18": 256, "mlp50m": 1, "mobilenetv2": 128}[args.workload]
+    if args.per_launch:
+        return per_launch(args)
     if args.workload != "resnet18":
         return bench_workload(args)
 
