@@ -157,7 +157,8 @@ def compile_ir(graph: ir.Graph, target: Union[str, object] = "rocm", *, optimize
             calibration = default_calibration(graph)
         quantize_w8a8(graph, calibration, log=log, peaks=peaks)
     elif quantize:
-        raise ValueError(f"quantize={quantize!r}: the rocm target implements W8A8 only")
+        from .quantize import quantize_weights
+        quantize_weights(graph, quantize, log=log)
     tgt = get_target(target, **target_options) if isinstance(target, str) else target
     runner = compile_graph(graph, tgt, cost_model, fallback=fallback)
     return CompiledProgram(tgt.name, runner, log, time.perf_counter() - t0)

@@ -86,6 +86,95 @@ __global__ void __launch_bounds__(256) qgemv_kernel(const GemvArgs g, const EpiD
     }
 }
 
+// Weight-only int8 (mira/quantize.py:45-68): y[M,N] = x[M,K] (f32) @ W, W the
+// dequantized constant fl32(q[k][n] * scale[n]) (mira/ops.py:581-589), then
+// the epilogue (mira/ops.py:217-219).  Same weight stream as qgemv_kernel
+// (16-byte chunks of packed int8 columns, LPC lanes per column pair); each
+// weight byte is dequantized into f32 exactly as the reference does, then
+// multiply-added into f32 accumulators.  blockIdx.y picks a block of MR rows
+// (the weights are streamed once per block: meant for decode shapes).  The summation order is not
+// NumPy's BLAS order, so results agree to f32 rounding, not bit for bit.
+template <int MR>
+__global__ void __launch_bounds__(256) w8gemv_kernel(const float* __restrict__ x, const int64_t ldx,
+                                                      const float* __restrict__ wscale, const GemvArgs g,
+                                                      const EpiDev e) {
+  const int lane = threadIdx.x & 63;
+  const int lpc = g.lpc;
+  const int sub = lane & (lpc - 1);
+  const int64_t group = (int64_t(blockIdx.x) * 256 + threadIdx.x) / lpc;
+  const int n0 = static_cast<int>(group * GEMV_CPW);
+  const int chunks = g.k_pad / 16;
+  const bool x_vec = (ldx & 3) == 0;   // rows 16-byte aligned: float4 activation loads
+  const int r0 = blockIdx.y * MR;      // first row of this block
+  const int rows = min(MR, g.M - r0);
+
+  float acc[MR][GEMV_CPW];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int c = 0; c < GEMV_CPW; ++c) acc[m][c] = 0.0f;
+
+  if (n0 < g.N) {
+    const int8_t* brow[GEMV_CPW];
+    float s[GEMV_CPW];
+#pragma unroll
+    for (int c = 0; c < GEMV_CPW; ++c) {
+      const int n = min(n0 + c, g.N - 1);
+      brow[c] = g.b + int64_t(n) * 64;
+      s[c] = wscale[n];
+    }
+    const int64_t kstep = int64_t(g.n_pad) * 64;
+    for (int k16 = sub; k16 < chunks; k16 += lpc) {
+      if (k16 * 16 >= g.lda) break;   // past K: zero weights and no activation columns
+      v4i wq[GEMV_CPW];
+#pragma unroll
+      for (int c = 0; c < GEMV_CPW; ++c)
+        wq[c] = *reinterpret_cast<const v4i*>(brow[c] + (k16 >> 2) * kstep + (k16 & 3) * 16);
+      float w[GEMV_CPW][16];
+#pragma unroll
+      for (int c = 0; c < GEMV_CPW; ++c)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          w[c][i] = __fmul_rn(static_cast<float>(static_cast<int8_t>(wq[c][i >> 2] >> (8 * (i & 3)))), s[c]);
+      const int kv = min(16, static_cast<int>(g.lda) - k16 * 16);   // activation columns in this chunk
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        if (m >= rows) break;
+        const float* xr = x + (r0 + m) * ldx + k16 * 16;
+        float xv[16];
+        if (kv == 16 && x_vec) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float4 t = *reinterpret_cast<const float4*>(xr + 4 * q);
+            xv[4 * q] = t.x; xv[4 * q + 1] = t.y; xv[4 * q + 2] = t.z; xv[4 * q + 3] = t.w;
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) xv[i] = i < kv ? xr[i] : 0.0f;
+        }
+#pragma unroll
+        for (int c = 0; c < GEMV_CPW; ++c)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[m][c] = __fmaf_rn(xv[i], w[c][i], acc[m][c]);
+      }
+    }
+  }
+  for (int off = lpc >> 1; off > 0; off >>= 1)
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int c = 0; c < GEMV_CPW; ++c) acc[m][c] += __shfl_xor(acc[m][c], off, 64);
+
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int c = 0; c < GEMV_CPW; ++c) {
+      if (sub != m * GEMV_CPW + c || m >= rows || n0 + c >= g.N) continue;
+      const int n = n0 + c;
+      epi_store(e, epi_steps(e, acc[m][c], r0 + m, n), r0 + m, n);
+    }
+}
+
 // M <= 8 rows: returns MR_EUNSUPPORTED for larger M (the caller uses the tiled kernel).
 int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int64_t n_pad, int64_t M,
                 int64_t N, const EpiDev& e, hipStream_t stream) {
@@ -121,3 +210,49 @@ int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, in
 }
 
 }  // namespace mr
+
+extern "C" int mr_w8_matmul_f32(const float* x, int64_t ldx, const int8_t* b, const float* w_scale, int64_t k_pad,
+                                int64_t n_pad, int64_t M, int64_t N, int64_t K, const mr_epilogue* epi,
+                                void* stream) {
+  MR_REQUIRE(x && b && w_scale, "mr_w8_matmul_f32: NULL operand");
+  MR_REQUIRE(M >= 0 && M <= 8 * 65535 && N > 0 && K > 0, "mr_w8_matmul_f32: M=%lld, N=%lld, K=%lld",
+             (long long)M, (long long)N, (long long)K);
+  MR_REQUIRE(ldx >= K, "mr_w8_matmul_f32: ldx %lld < K %lld", (long long)ldx, (long long)K);
+  MR_REQUIRE(k_pad >= K && k_pad % 64 == 0, "mr_w8_matmul_f32: k_pad %lld must be >= K and a multiple of 64",
+             (long long)k_pad);
+  MR_REQUIRE(n_pad >= N && n_pad % 32 == 0, "mr_w8_matmul_f32: n_pad %lld must be >= N and a multiple of 32",
+             (long long)n_pad);
+  MR_REQUIRE(N < (int64_t(1) << 30) && k_pad < (int64_t(1) << 30), "mr_w8_matmul_f32: problem too large");
+  MR_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0,
+             "mr_w8_matmul_f32: operands must be 16-byte aligned");
+  mr::EpiDev e;
+  const int rc = mr::make_epi(epi, N, false, &e);
+  if (rc != MR_OK) return rc;
+  if (M == 0) return MR_OK;
+  mr::GemvArgs g = {};
+  g.b = b;
+  g.lda = K;   // activation columns (the kernel stops at K)
+  g.k_pad = static_cast<int32_t>(k_pad);
+  g.n_pad = static_cast<int32_t>(n_pad);
+  g.N = static_cast<int32_t>(N);
+  g.M = static_cast<int32_t>(M);
+  const int mr_rows = static_cast<int>(M < 8 ? M : 8);   // rows per block
+  int lpc = 64;
+  while (lpc > 4 && k_pad / 16 < 4 * lpc) lpc >>= 1;
+  while (lpc < mr_rows * mr::GEMV_CPW) lpc <<= 1;
+  g.lpc = lpc;
+  const int64_t groups = (N + mr::GEMV_CPW - 1) / mr::GEMV_CPW;
+  const int mr_blk = mr_rows == 1 ? 1 : mr_rows == 2 ? 2 : mr_rows <= 4 ? 4 : 8;
+  const dim3 grid(static_cast<unsigned>((groups * lpc + 255) / 256), static_cast<unsigned>((M + mr_blk - 1) / mr_blk));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (mr_blk == 1)
+    hipLaunchKernelGGL(mr::w8gemv_kernel<1>, grid, dim3(256), 0, s, x, ldx, w_scale, g, e);
+  else if (mr_blk == 2)
+    hipLaunchKernelGGL(mr::w8gemv_kernel<2>, grid, dim3(256), 0, s, x, ldx, w_scale, g, e);
+  else if (mr_blk == 4)
+    hipLaunchKernelGGL(mr::w8gemv_kernel<4>, grid, dim3(256), 0, s, x, ldx, w_scale, g, e);
+  else
+    hipLaunchKernelGGL(mr::w8gemv_kernel<8>, grid, dim3(256), 0, s, x, ldx, w_scale, g, e);
+  MR_LAUNCH_CHECK("w8gemv");
+  return MR_OK;
+}

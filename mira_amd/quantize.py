@@ -1,5 +1,10 @@
-"""W8A8 rewriting: matmuls and ungrouped convs with constant weights become
-`qmatmul` / `qconv2d` whose attrs the rocm kernels consume.
+"""Quantization rewrites whose results the rocm kernels consume.
+
+Weight-only int8 (mira/quantize.py:21-68): large matmul/conv weight constants
+become `dequantize` constants (int8 + per-output-channel scale).
+
+W8A8: matmuls and ungrouped convs with constant weights become `qmatmul` /
+`qconv2d`.
 
 Follows mira/quantize.py:24-31 (weights) and :95-143 (calibration + rewrite):
   q, w_scale = per-output-channel symmetric int8 weights
@@ -27,6 +32,51 @@ def quantize_array(w: np.ndarray, axis: int) -> tuple[np.ndarray, np.ndarray]:
     bshape[axis] = -1
     q = np.clip(np.round(w.astype(np.float32) / scale.reshape(bshape)), -127, 127).astype(np.int8)
     return q, scale
+
+
+MIN_ELEMS = 1024   # mira/quantize.py:21: smaller constants (biases, norms) stay f32
+
+
+def _weight_axis(v: ir.Value, users: list) -> Optional[int]:
+    """mira/quantize.py:34-43: the output-channel axis when every use of `v` is as a
+    matmul weight ([K, N] -> 1) or a conv weight ([O, C, KH, KW] -> 0), else None."""
+    if not users:
+        return None
+    if v.type.rank == 2 and all(u.kind == "matmul" and u.inputs[1] is v and u.inputs[0] is not v for u in users):
+        return 1
+    if v.type.rank == 4 and all(u.kind == "conv2d" and u.inputs[1] is v for u in users):
+        return 0
+    return None
+
+
+def quantize_weights(g: ir.Graph, mode: str = "int8", log: Optional[list] = None) -> tuple[int, int]:
+    """mira/quantize.py:46-68, the weight-only mode: each constant of at least
+    MIN_ELEMS elements used only as matmul/conv weights becomes a `dequantize`
+    constant (int8 q + one f32 scale per output channel).  Returns the weight
+    bytes before and after."""
+    if mode != "int8":
+        raise ValueError(f"unknown quantization mode '{mode}' (supported: int8)")
+    before = after = 0
+    users = g.users()
+    for op in g.ops:
+        for _, sub in op.subgraphs():
+            b, a = quantize_weights(sub, mode)
+            before, after = before + b, after + a
+        if not op.is_const or op.result.type.numel < MIN_ELEMS:
+            continue
+        axis = _weight_axis(op.result, users.get(op.result, []))
+        if axis is None:
+            continue
+        w = op.attrs["value"]
+        q, scale = quantize_array(w, axis)
+        before += w.nbytes
+        after += q.nbytes + scale.nbytes
+        op.kind = "dequantize"
+        op.attrs = {"q": q, "scale": scale, "axis": axis, "dtype": op.result.type.dtype}
+    g.verify()
+    if log is not None and before:
+        log.append(("quantize-int8", f"// weights: {before / 2**20:.2f} MiB -> {after / 2**20:.2f} MiB\n{g}"))
+    return before, after
 
 
 def w8a8_weight(op: ir.Op) -> Optional[tuple[np.ndarray, np.ndarray]]:

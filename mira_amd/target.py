@@ -78,6 +78,9 @@ class DevValue:
         return pack.c_pad_for(self.cols) if self.nhwc else pack.row_stride_for(self.cols)
 
 
+W8_MAX_ROWS = 64     # mr_w8_matmul_f32 streams the weights once per 8 rows: decode shapes only
+
+
 def _ptr(t) -> int:
     return 0 if t is None else t.data_ptr()
 
@@ -127,8 +130,26 @@ class RocmTarget:
         if k == "reshape":
             return None
         if k == "matmul":
-            return "f32 matmul stays on the CPU (its summation order is BLAS's, not reproducible bit for bit)"
+            return self._check_w8_matmul(op)
         return f"'{k}' has no rocm kernel"
+
+    def _check_w8_matmul(self, op: ir.Op) -> Optional[str]:
+        """Decode-shaped matmuls of the weight-only int8 mode (mira/quantize.py:45-68): an f32
+        activation of at most W8_MAX_ROWS rows against a `dequantize` [K, N] weight.  These
+        compute in f32 in another summation order than BLAS's, so they match the reference
+        to f32 rounding (relative 1e-5), not bit for bit; every other f32 matmul stays on the
+        CPU."""
+        x, w = op.inputs[0], op.inputs[1]
+        p = w.producer
+        if p is None or p.kind != "dequantize" or p.attrs["axis"] != 1 or w.type.rank != 2:
+            return ("f32 matmul stays on the CPU (its summation order is BLAS's, not reproducible bit for bit) "
+                    "unless its weight is an int8 weight-only constant")
+        if x.type.rank not in (2, 3) or x.type.dtype != "f32":
+            return "weight-only int8 matmul runs on rocm for rank-2/3 f32 activations"
+        rows = int(np.prod(x.type.shape[:-1], dtype=np.int64))
+        if rows > W8_MAX_ROWS:
+            return f"weight-only int8 matmul runs on rocm for decode shapes (<= {W8_MAX_ROWS} rows), not {rows}"
+        return self._check_epilogue(op, op.result.type.shape, False)
 
     def _check_epilogue(self, op: ir.Op, shape: tuple, is_conv: bool, first_operand: int = 1) -> Optional[str]:
         for fn, idx, _sw in op.attrs.get("epilogue", ()):
@@ -226,7 +247,7 @@ class RocmExecutable:
                     self.need_f32.add(pad_op.inputs[0])
             else:
                 for v in op.inputs:
-                    if v not in self.consts or op.kind != "conv2d" or v is op.inputs[0]:
+                    if v not in self.consts or op.kind not in ("conv2d", "matmul") or v is op.inputs[0]:
                         self.need_f32.add(v)
         # reshapes: the input must provide what the output's consumers read; a reshape
         # that keeps the int8 layout (same rows, columns and row stride) passes its
@@ -507,6 +528,26 @@ class RocmExecutable:
         self._add("qmatmul", lambda s: L.check(
             lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), kp, npad, M, N, K, C.byref(e), s), "mr_qmatmul"),
             nbytes=M * K + K * N + self._epi_bytes(e, M, N), nops=2 * M * N * K)
+        self._finish_i8(out, fused)
+
+    def _emit_matmul(self, op: ir.Op) -> None:
+        """Weight-only int8 matmul (checked by _check_w8_matmul): the int8 weights are packed
+        and uploaded once with their f32 scales; each run streams them through the
+        mr_w8_matmul_f32 kernel."""
+        x = self._src(op.inputs[0])
+        w = self.consts[op.inputs[1]].attrs
+        q = np.asarray(w["q"], np.int8)
+        K, N = q.shape
+        bl = pack.pack_matmul(q)
+        b = self._upload(pack.device_weights(bl))
+        ws = self._upload(np.asarray(w["scale"], np.float32).reshape(-1))
+        out = self._new_dv(op.result)
+        e, fused = self._epilogue(op, out, False, 2, None)
+        M = out.rows
+        lib, kp, npad, xf = self.lib, bl.shape[1], bl.shape[0], x.f32
+        self._add("w8matmul", lambda s: L.check(
+            lib.mr_w8_matmul_f32(xf.data_ptr(), K, b.data_ptr(), ws.data_ptr(), kp, npad, M, N, K, C.byref(e), s),
+            "mr_w8_matmul_f32"), nbytes=4 * M * K + K * N + 4 * N + self._epi_bytes(e, M, N))
         self._finish_i8(out, fused)
 
     def _emit_qconv2d(self, op: ir.Op) -> None:

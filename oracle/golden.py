@@ -340,6 +340,36 @@ def calibrate(g, feeds: list, watch: set) -> dict:
     return peak
 
 
+WEIGHT_ONLY_MIN_ELEMS = 1024     # mira/quantize.py:21
+
+
+def weight_only_attrs(g) -> dict:
+    """The `dequantize` attrs mira/quantize.py:46-68 (weight-only int8) would give each
+    constant of g, keyed by const op (g itself is left untouched): constants of at least
+    1024 elements whose every use is as a matmul [K, N] weight (axis 1; the same value
+    not also the activation) or a conv [O, C, KH, KW] weight (axis 0), mira/quantize.py:34-43."""
+    users: dict = {}
+    for op in g.ops:
+        for v in op.inputs:
+            users.setdefault(v, []).append(op)
+    out = {}
+    for op in g.ops:
+        if op.kind != "const" or int(np.prod(op.result.type.shape, dtype=np.int64)) < WEIGHT_ONLY_MIN_ELEMS:
+            continue
+        v, us = op.result, users.get(op.result, [])
+        axis = None
+        if us and v.type.rank == 2 and all(u.kind == "matmul" and u.inputs[1] is v and u.inputs[0] is not v
+                                           for u in us):
+            axis = 1
+        elif us and v.type.rank == 4 and all(u.kind == "conv2d" and u.inputs[1] is v for u in us):
+            axis = 0
+        if axis is None:
+            continue
+        q, scale = quantize_array(op.attrs["value"], axis)
+        out[op] = {"q": q, "scale": scale, "axis": axis, "dtype": v.type.dtype}
+    return out
+
+
 def w8a8_weight(op) -> Optional[tuple[np.ndarray, np.ndarray]]:
     """mira/quantize.py:95-115."""
     w = op.inputs[1].producer

@@ -150,6 +150,88 @@ def test_qmatmul_rejects_bad_shapes(lib):
     assert lib.mr_qmatmul(a.data_ptr(), 16, b.data_ptr(), 60, 32, 4, 8, 16, C.byref(e), stream()) == 1
 
 
+# ---------------------------------------------------------------- weight-only int8 matmul (f32 activations)
+
+# The f32 sums run in another order than NumPy's BLAS, so parity is a tolerance:
+# |got - want| <= W8_TOL * (|x| @ |W| + |epilogue operands|), want = the oracle's f32 matmul
+# over the dequantized weight (mira/ops.py:217-219, 581-589).
+W8_TOL = 1e-5
+
+
+def _run_w8(lib, x, K, q, s, steps_np, next_xs=None):
+    """x: [M, ldx] f32 (columns >= K are ignored). Returns (y f32, y int8 or None)."""
+    torch = _torch()
+    M, ldx = x.shape
+    N = q.shape[1]
+    bl = pack.pack_matmul(q)
+    b, ws, xd = T(pack.device_weights(bl)), T(s.astype(np.float32)), T(x)
+    keep, steps = [], []
+    for fn, mode, arr, sw in steps_np:
+        if arr is None:
+            steps.append((fn, mode, None, 0, sw))
+            continue
+        t = T(np.ascontiguousarray(arr, np.float32))
+        keep.append(t)
+        steps.append((fn, mode, t, N if mode == L.BC_FULL else (1 if mode == L.BC_ROW else 0), sw))
+    y = empty((M, N), torch.float32)
+    ldq = pack.row_stride_for(N)
+    yq = empty((M, ldq), torch.int8) if next_xs else None
+    e = epilogue(steps, out_f32=y, ldo=N, out_i8=yq, ldq=ldq, xs=next_xs or 1.0)
+    L.check(lib.mr_w8_matmul_f32(xd.data_ptr(), ldx, b.data_ptr(), ws.data_ptr(), bl.shape[1], bl.shape[0], M, N, K,
+                                 C.byref(e), stream()), "mr_w8_matmul_f32")
+    sync()
+    return y.cpu().numpy(), (yq.cpu().numpy()[:, :N] if yq is not None else None)
+
+
+@pytest.mark.parametrize("M,K,N,ldx", [(1, 4096, 4096, 4096), (1, 4096, 1000, 4096), (2, 784, 512, 784),
+                                       (3, 100, 65, 100), (8, 512, 256, 520), (13, 256, 10, 257),
+                                       (64, 784, 512, 784), (5, 33, 1, 33)])
+def test_w8_matmul_bias_relu(lib, M, K, N, ldx):
+    rng = np.random.default_rng(M * 31 + K + N)
+    x = rng.standard_normal((M, ldx)).astype(np.float32)      # columns >= K are never read as data
+    w = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    q, s = G.quantize_array(w, 1)
+    deq = G.dequantize({"q": q, "scale": s, "axis": 1, "dtype": "f32"})
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    want = G.matmul([x[:, :K], deq, bias], {"epilogue": (("add", 2, False), ("relu", None, False))})
+    y, yq = _run_w8(lib, x, K, q, s, [("add", L.BC_COL, bias, False), ("relu", 0, None, False)], next_xs=0.02)
+    bound = np.abs(x[:, :K]).astype(np.float64) @ np.abs(deq).astype(np.float64) + np.abs(bias)
+    assert np.all(np.abs(y.astype(np.float64) - want) <= W8_TOL * bound)
+    assert (y >= 0).all()
+    # the requantized copy is the reference's quantize_activation of the kernel's own f32 result
+    assert bits_equal(yq, G.quantize_activation(y, 0.02).astype(np.int8))
+
+
+def test_w8_matmul_row_blocks_and_operands(lib):
+    """Row-indexed epilogue operands across several 8-row blocks (M = 21)."""
+    rng = np.random.default_rng(5)
+    M, K, N = 21, 192, 48
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    q = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    s = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    deq = G.dequantize({"q": q, "scale": s, "axis": 1, "dtype": "f32"})
+    full = rng.standard_normal((M, N)).astype(np.float32)
+    row = rng.uniform(0.5, 2, (M, 1)).astype(np.float32)
+    want = G.matmul([x, deq, full, row], {"epilogue": (("sub", 2, True), ("mul", 3, False))})
+    y, _ = _run_w8(lib, x, K, q, s, [("sub", L.BC_FULL, full, True), ("mul", L.BC_ROW, row, False)])
+    bound = (np.abs(x).astype(np.float64) @ np.abs(deq) + np.abs(full)) * row
+    assert np.all(np.abs(y.astype(np.float64) - want) <= W8_TOL * bound)
+
+
+def test_w8_matmul_rejects_bad_arguments(lib):
+    torch = _torch()
+    x = empty((4, 16), torch.float32)
+    b = empty((32, 64), torch.int8)
+    s = empty((8,), torch.float32)
+    e = epilogue(out_f32=empty((4, 8), torch.float32), ldo=8)
+    assert lib.mr_w8_matmul_f32(x.data_ptr(), 15, b.data_ptr(), s.data_ptr(), 64, 32, 4, 8, 16, C.byref(e),
+                                stream()) == 1
+    assert b"ldx" in lib.mr_last_error()
+    e2 = epilogue(out_f32=empty((4, 8), torch.float32), ldo=8, scale=s)
+    assert lib.mr_w8_matmul_f32(x.data_ptr(), 16, b.data_ptr(), s.data_ptr(), 64, 32, 4, 8, 16, C.byref(e2),
+                                stream()) == 1
+
+
 # ---------------------------------------------------------------- K2c qconv2d
 
 CONV_CASES = [

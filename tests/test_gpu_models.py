@@ -15,7 +15,7 @@ import pytest
 
 from mira_amd import models, passes
 from mira_amd.compiler import compile_graph
-from mira_amd.quantize import calibration_peaks, quantize_w8a8
+from mira_amd.quantize import calibration_peaks, quantize_w8a8, quantize_weights
 from mira_amd.target import RocmTarget
 from oracle import golden as G
 
@@ -212,3 +212,70 @@ def test_gpt_decode_step_batch512_rows():
     want = G.run_graph(g3, small)
     for a, b in zip(got, want):
         assert bits_equal(a[rows], b)
+
+
+# ---------------------------------------------------------------- weight-only int8 (decode-shaped f32 matmuls)
+#
+# quantize="int8" keeps activations in f32; the dequantized weights feed f32 matmuls that
+# the rocm target runs as weight streams for up to 64 rows.  Their sums run in another
+# order than BLAS's, so outputs match the oracle on the same quantized graph to within
+# W8_MODEL_TOL of the output's peak magnitude (about ten f32 roundings of a K = 4096 dot
+# product compounded over the layers), not bit for bit.
+
+W8_MODEL_TOL = 1e-4
+
+
+def _weight_only(g):
+    passes.optimize(g)
+    want = G.weight_only_attrs(g)
+    quantize_weights(g)
+    for op, a in want.items():
+        assert op.kind == "dequantize" and np.array_equal(op.attrs["q"], a["q"])
+    return g
+
+
+def _run_weight_only(g, feeds):
+    runner = compile_graph(g, RocmTarget(), fallback=G.CPUTarget())
+    got = runner.run_list([feeds[v.name] for v in g.inputs])
+    env = oracle_env(g, feeds)
+    return runner, got, [env[v] for v in g.outputs]
+
+
+def _w8_launches(runner) -> int:
+    return sum(seg.executable.kernel_counts.get("w8matmul", 0) for seg in runner.segments if seg.device == "rocm")
+
+
+def test_weight_only_mlp50m_batch1():
+    g = _weight_only(models.mlp_50m(batch=1))
+    runner, (got,), (want,) = _run_weight_only(g, {"x": models.normal_batch((1, 4096), 3)})
+    assert [s.device for s in runner.segments] == ["rocm"] and _w8_launches(runner) == 4
+    assert np.abs(got - want).max() <= W8_MODEL_TOL * np.abs(want).max()
+
+
+def test_weight_only_mlp_mira_batch64():
+    """The reference's own int8 check (its tests/test_control_dynamic_quant.py:178-189) with
+    the three matmuls on rocm: within 0.05 of the f32 model, argmax agreement above 0.9."""
+    x = np.random.default_rng(0).standard_normal((64, 784)).astype(np.float32)
+    f32g = models.mlp_mira(batch=64)
+    passes.optimize(f32g)
+    (ref,) = G.run_graph(f32g, {"x": x})
+    g = _weight_only(models.mlp_mira(batch=64))
+    runner, (got,), (want,) = _run_weight_only(g, {"x": x})
+    assert [s.device for s in runner.segments] == ["rocm", "cpu"] and _w8_launches(runner) == 3
+    assert np.abs(got - want).max() <= 1e-5            # softmax probabilities
+    assert np.abs(got - ref).max() < 0.05 and (got.argmax(1) == ref.argmax(1)).mean() > 0.9
+
+
+def test_weight_only_gpt_decode_step_batch2():
+    cfg = models.GPTConfig()
+    params = models.gpt_params(cfg, 0)
+    g = _weight_only(models.gpt_decode_step(cfg, 2, params))
+    r = np.random.default_rng(9)
+    toks = r.integers(0, cfg.V, (2, cfg.T)).astype(np.int32)
+    caches = [(r.standard_normal((2, cfg.T, cfg.D)).astype(np.float32),
+               r.standard_normal((2, cfg.T, cfg.D)).astype(np.float32)) for _ in range(cfg.L)]
+    feeds = models.gpt_step_feeds(cfg, params, toks, 20, caches)
+    runner, got, want = _run_weight_only(g, feeds)
+    assert _w8_launches(runner) > 0
+    for a, b in zip(got, want):
+        assert np.abs(a - b).max() <= W8_MODEL_TOL * max(np.abs(b).max(), 1.0)

@@ -10,7 +10,7 @@ from mira_amd import models, pack, passes
 from mira_amd.compiler import compile_graph
 from mira_amd.ir import Graph
 from mira_amd.partition import partition
-from mira_amd.quantize import quantize_array, quantize_w8a8
+from mira_amd.quantize import quantize_array, quantize_w8a8, quantize_weights
 from mira_amd.target import RocmTarget, _bcast_mode
 from oracle import golden as G
 
@@ -79,6 +79,68 @@ def test_quantize_array_matches_oracle():
         q1, s1 = quantize_array(w.reshape(64, -1) if axis == 1 else w, axis)
         q2, s2 = G.quantize_array(w.reshape(64, -1) if axis == 1 else w, axis)
         assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
+
+
+def test_weight_only_rewrite_matches_oracle():
+    """mira/quantize.py:46-68 on examples/mlp.mira: the reference's own test expects three
+    dequantize constants (its tests/test_control_dynamic_quant.py:178-189); the biases stay
+    f32; q, scale and axis equal the oracle's restatement; the byte counts are the weights'."""
+    g = models.mlp_mira(batch=4)
+    passes.optimize(g)
+    want = G.weight_only_attrs(g)
+    log = []
+    before, after = quantize_weights(g, log=log)
+    deq = [op for op in g.ops if op.kind == "dequantize"]
+    assert len(deq) == 3 and set(deq) == set(want)
+    for op in deq:
+        a = want[op]
+        assert np.array_equal(op.attrs["q"], a["q"]) and np.array_equal(op.attrs["scale"], a["scale"])
+        assert op.attrs["axis"] == a["axis"] == 1 and op.attrs["dtype"] == "f32"
+    shapes = [(784, 512), (512, 256), (256, 10)]
+    assert before == sum(4 * k * n for k, n in shapes)
+    assert after == sum(k * n + 4 * n for k, n in shapes)
+    assert log[0][0] == "quantize-int8" and log[0][1].startswith("// weights: ")
+    with pytest.raises(ValueError, match="int8"):
+        quantize_weights(g, "int4")
+
+
+def test_weight_only_rules():
+    """mira/quantize.py:34-43: conv weights get axis 0; a constant that is also an
+    activation, feeds an elementwise op, or has fewer than 1024 elements stays f32."""
+    rng = np.random.default_rng(0)
+    conv = {"stride": (1, 1), "padding": (1, 1)}
+    g = Graph("t", [], [], [])
+    x = g.input("x", (2, 8, 6, 6))
+    wc = g.const(rng.standard_normal((16, 8, 3, 3)).astype(np.float32))          # 1152 elements
+    small = g.const(rng.standard_normal((8, 8, 3, 3)).astype(np.float32))       # 576 elements
+    h = g.add("conv2d", [x, wc], conv)
+    h = g.add("conv2d", [h, g.const(rng.standard_normal((8, 16, 3, 3)).astype(np.float32))], conv)
+    y = g.input("y", (40, 40))
+    sq = g.const(rng.standard_normal((40, 40)).astype(np.float32))
+    m = g.add("matmul", [sq, sq])                                                # also the activation
+    shared = g.const(rng.standard_normal((40, 40)).astype(np.float32))
+    m2 = g.add("add", [g.add("matmul", [y, shared]), shared])                  # also an add operand
+    g.outputs = [h, m, m2, g.add("conv2d", [x, small], conv)]
+    want = G.weight_only_attrs(g)
+    quantize_weights(g)
+    deq = {op for op in g.ops if op.kind == "dequantize"}
+    assert deq == set(want)
+    assert [op.attrs["axis"] for op in g.ops if op.kind == "dequantize"] == [0, 0]
+    assert sq.producer.kind == shared.producer.kind == small.producer.kind == "const"
+
+
+def test_check_decisions_weight_only():
+    """Weight-only int8 matmuls run on rocm for decode shapes (up to 64 rows); larger
+    batches, and matmuls whose weight is not a dequantize constant, stay on the CPU."""
+    t = RocmTarget()
+    for batch, placed in ((4, True), (64, True), (65, False)):
+        g = models.mlp_mira(batch=batch)
+        passes.optimize(g)
+        quantize_weights(g)
+        mm = [op for op in g.compute_ops() if op.kind == "matmul"]
+        assert len(mm) == 3
+        reasons = [t.check(op) for op in mm]
+        assert all(r is None for r in reasons) if placed else all("decode shapes" in r for r in reasons)
 
 
 def test_check_decisions():
