@@ -1,7 +1,7 @@
 """Benchmark: W8A8 ResNet-18 inference on one MI355X through the rocm target.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 256] [--no-cpu-baseline]
-    python bench.py --workload mlp50m|mobilenetv2 [--batch B] [--steps K] [--warmup W]
+    python bench.py --workload mlp50m|mlp50m-int8|mobilenetv2 [--batch B] [--steps K] [--warmup W]
     python bench.py --per-launch [--workload W] [--batch B]
 
 A step is one inference of the whole batch (all 20 int8 implicit-GEMM convs,
@@ -23,7 +23,11 @@ kernels    = every launch kind of the step: its summed launch durations and its
 print one JSON line with their per-kind breakdown (no cpu baseline): the 50M
 MLP at batch 1 runs its four layers on the decode-shaped weight-streaming
 qmatmul kernel, MobileNetV2 its 17 depthwise convolutions on the f32
-depthwise kernel; both are HBM-bound.
+depthwise kernel; both are HBM-bound.  mlp50m-int8 is the same MLP in the
+int8 weight-only mode (f32 activations, int8 weights dequantized in
+registers), batch 1: four weight-streaming f32 matmul launches.
+resnet18-onnx is ResNet-18 laid out as MIRA's ONNX importer emits it (BN as a
+per-channel mul + add in each conv epilogue instead of folded weights).
 """
 from __future__ import annotations
 
@@ -60,13 +64,23 @@ def build(batch: int, seed: int = 0, peaks=None):
 
 
 def build_workload(name: str, batch: int):
-    """A W8A8 graph of another configuration, calibrated as the parity tests do it."""
+    """A W8A8 graph of another configuration, calibrated as the parity tests do it (or,
+    for mlp50m-int8, the weight-only rewrite, which needs no calibration)."""
     from mira_amd import models, passes
-    from mira_amd.quantize import calibration_peaks, quantize_w8a8
+    from mira_amd.quantize import calibration_peaks, quantize_w8a8, quantize_weights
+    if name == "mlp50m-int8":
+        g = models.mlp_50m(batch=batch, seed=0)
+        passes.optimize(g)
+        quantize_weights(g)
+        return g, models.normal_batch(g.inputs[0].type.shape, 7)
     if name == "mlp50m":
         builder, cb, seeds, gen = models.mlp_50m, 8, (2, 3), models.normal_batch
     elif name == "mobilenetv2":
         builder, cb, seeds, gen = models.mobilenet_v2, 2, (11, 12), models.image_batch
+    elif name == "resnet18-onnx":
+        def builder(batch, seed):
+            return models.resnet18(batch=batch, seed=seed, bn_epilogue=True)
+        cb, seeds, gen = 2, (11, 12), models.image_batch
     else:
         raise SystemExit(f"unknown workload {name!r}")
     g = builder(batch=batch, seed=0)
@@ -191,7 +205,8 @@ def bench_workload(args) -> int:
     per_kind = time_launches(exe, stream)
     log(f"{args.workload} batch {args.batch}: {args.steps} steps, {ms:.4f} ms/step")
     print(json.dumps({"workload": args.workload, "batch": args.batch, "steps": args.steps, "warmup": args.warmup,
-                      "ms_per_step": round(ms, 4), "dtype": "int8", "data": "synthetic",
+                      "ms_per_step": round(ms, 4), "dtype": "f32" if args.workload.endswith("-int8") else "int8",
+                      "data": "synthetic",
                       "kernels": kernel_breakdown(exe, per_kind)}), flush=True)
     return 0
 
@@ -326,8 +341,10 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--batch", type=int, default=None, help="default 256 (resnet18), 1 (mlp50m), 128 (mobilenetv2)")
-    ap.add_argument("--workload", default="resnet18", choices=["resnet18", "mlp50m", "mobilenetv2"])
+    ap.add_argument("--batch", type=int, default=None,
+                    help="default 256 (resnet18), 1 (mlp50m, mlp50m-int8), 128 (mobilenetv2)")
+    ap.add_argument("--workload", default="resnet18",
+                    choices=["resnet18", "resnet18-onnx", "mlp50m", "mlp50m-int8", "mobilenetv2"])
     ap.add_argument("--per-launch", action="store_true", help="per-launch time against each launch's roofline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true", help="run the plain copy used to scale counters")
@@ -345,7 +362,8 @@ def main() -> int:
               "by data parallelism, one share per GPU). Run with --gpus 1.", file=sys.stderr)
         return 2
     if args.batch is None:
-        args.batch = {"resnet18": 256, "mlp50m": 1, "mobilenetv2": 128}[args.workload]
+        args.batch = {"resnet18": 256, "resnet18-onnx": 256, "mlp50m": 1, "mlp50m-int8": 1,
+                      "mobilenetv2": 128}[args.workload]
     if args.per_launch:
         return per_launch(args)
     if args.workload != "resnet18":

@@ -176,7 +176,10 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* g, const int8_t* b, int64_t 
  * the convolution result is never stored.  `epi` carries the convolution's
  * scale and epilogue steps, while its outputs (out_f32/ldo, out_i8/ldq/out_xs)
  * receive the pooled [n, poh, pow_, o] result in NHWC rows; out_acc must be
- * NULL. */
+ * NULL.  The pool runs on the accumulators, so every epilogue step must be
+ * non-decreasing with a scalar or per-channel operand: add, sub (not
+ * swapped), maximum, minimum, relu, and mul whose operand the caller
+ * guarantees to be positive and finite (it is not read on the host). */
 int mr_qconv2d_maxpool(const int8_t* x, const mr_conv_geom* g, const int8_t* b, int64_t k_pad, int64_t n_pad,
                        const mr_epilogue* epi, int32_t pool_size, int32_t pool_stride, int32_t pool_pad_top,
                        int32_t pool_pad_left, float pad_value, int32_t poh, int32_t pow_, void* stream);

@@ -65,43 +65,47 @@ int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out)
   out->out_acc = epi->out_acc;
   out->ldacc = epi->ldacc;
   out->out_rxs = epi->out_i8 ? 1.0 / static_cast<double>(epi->out_xs) : 0.0;
-  // recognise the fixed form  add(col)? add(full)? max(scalar)|relu? min(scalar)?
+  // recognise the fixed form  mul(col)? add(col)? add(full)? max(scalar)|relu? min(scalar)?
   int stage = 0;
   bool fixed = true;
   for (int s = 0; s < epi->n_steps && fixed; ++s) {
     const mr_epi_step& st = epi->steps[s];
     if (st.fn == MR_EPI_RELU) {
-      if (stage > 2) fixed = false;
+      if (stage > 3) fixed = false;
       out->f_lo = 1;
       out->lo_ptr = nullptr;
-      stage = 3;
+      stage = 4;
       continue;
     }
     if (st.swapped) {
       fixed = false;
-    } else if (st.fn == MR_EPI_ADD && st.mode == MR_BC_COL && stage < 1) {
+    } else if (st.fn == MR_EPI_MUL && st.mode == MR_BC_COL && stage < 1) {
+      out->f_mul = 1;
+      out->mul_ptr = st.ptr;
+      stage = 1;
+    } else if (st.fn == MR_EPI_ADD && st.mode == MR_BC_COL && stage < 2) {
       out->f_col = 1;
       out->col_ptr = st.ptr;
-      stage = 1;
-    } else if (st.fn == MR_EPI_ADD && st.mode == MR_BC_FULL && stage < 2) {
+      stage = 2;
+    } else if (st.fn == MR_EPI_ADD && st.mode == MR_BC_FULL && stage < 3) {
       out->f_full = 1;
       out->full_ptr = st.ptr;
       out->full_ld = st.ld;
-      stage = 2;
-    } else if (st.fn == MR_EPI_MAX && st.mode == MR_BC_SCALAR && stage < 3) {
+      stage = 3;
+    } else if (st.fn == MR_EPI_MAX && st.mode == MR_BC_SCALAR && stage < 4) {
       out->f_lo = 1;
       out->lo_ptr = st.ptr;
-      stage = 3;
-    } else if (st.fn == MR_EPI_MIN && st.mode == MR_BC_SCALAR && stage < 4) {
+      stage = 4;
+    } else if (st.fn == MR_EPI_MIN && st.mode == MR_BC_SCALAR && stage < 5) {
       out->f_hi = 1;
       out->hi_ptr = st.ptr;
-      stage = 4;
+      stage = 5;
     } else {
       fixed = false;
     }
   }
   out->fixed = fixed;
-  if (!fixed) out->f_col = out->f_full = out->f_lo = out->f_hi = 0;
+  if (!fixed) out->f_mul = out->f_col = out->f_full = out->f_lo = out->f_hi = 0;
   return MR_OK;
 }
 

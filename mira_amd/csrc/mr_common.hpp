@@ -136,12 +136,15 @@ struct EpiDev {
   int64_t ldacc;
   double out_rxs;  // fl64(1 / out_xs), computed on the host
   // Fixed form recognised on the host (make_epi): the steps are, in this order
-  // and each optional, add(per-column) -> add(full) -> maximum(scalar) or relu
-  // -> minimum(scalar), none swapped.  Every bias/residual/ReLU/ReLU6 epilogue
-  // has this form; kernels then run it without the general step interpreter.
+  // and each optional, mul(per-column) -> add(per-column) -> add(full) ->
+  // maximum(scalar) or relu -> minimum(scalar), none swapped.  Every
+  // bias/residual/ReLU/ReLU6 epilogue has this form, with or without a
+  // per-channel BatchNorm multiply in front; kernels then run it without the
+  // general step interpreter.
   int32_t fixed;
-  int32_t f_col, f_full, f_lo, f_hi;
+  int32_t f_mul, f_col, f_full, f_lo, f_hi;
   int32_t reserved2;
+  const float* mul_ptr;
   const float* col_ptr;
   const float* full_ptr;
   int64_t full_ld;
@@ -188,8 +191,9 @@ __device__ __forceinline__ float epi_generic(const EpiDev& e, float y, int64_t r
   return y;
 }
 
-// The fixed form (see EpiDev): add(col)? add(full)? maximum(lo)? minimum(hi)?
+// The fixed form (see EpiDev): mul(col)? add(col)? add(full)? maximum(lo)? minimum(hi)?
 __device__ __forceinline__ float epi_fixed(const EpiDev& e, float y, int64_t row, int64_t col) {
+  if (e.f_mul) y = __fmul_rn(y, e.mul_ptr[col]);
   if (e.f_col) y = __fadd_rn(y, e.col_ptr[col]);
   if (e.f_full) y = __fadd_rn(y, e.full_ptr[row * e.full_ld + col]);
   if (e.f_lo) y = np_maximum(y, e.lo_ptr ? e.lo_ptr[0] : 0.0f);
@@ -230,6 +234,7 @@ int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, in
 // the stores), so the rows' latencies overlap.
 constexpr int EF_GENERIC = 0, EF_FIXED = 1, EF_SPEC = 0x100;
 constexpr int SF_COL = 1, SF_FULL = 2, SF_LO = 4, SF_HI = 8, SF_F32 = 16, SF_I8 = 32;
+constexpr int SF_MUL = 64;   // no compiled form has it: a leading mul runs the EF_FIXED path
 // the forms with compiled kernels: bias+ReLU -> int8; bias+residual+ReLU -> f32
 // and/or int8; bias -> f32 (ResNet blocks, downsample and fc layers, MLPs)
 constexpr int SPEC_RELU_I8 = SF_COL | SF_LO | SF_I8;
@@ -254,6 +259,7 @@ inline int spec_form(const EpiDev& e) {
     return reinterpret_cast<uintptr_t>(p) % bytes == 0 && ld % 4 == 0;
   };
   int f = 0;
+  if (e.f_mul) f |= SF_MUL;
   if (e.f_col) f |= SF_COL;
   if (e.f_full) {
     if (!al(e.full_ptr, e.full_ld, 16)) return -1;

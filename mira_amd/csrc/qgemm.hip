@@ -103,6 +103,7 @@ __device__ __forceinline__ void dma4(const void* src, int8_t* lds_dst) {
 // operand and the scalar bounds.
 struct EpiCols4 {
   double scale[4];
+  float mulv[4];
   float colv[4];
   float lo, hi;
   bool lo_nan, hi_nan;
@@ -125,6 +126,7 @@ __device__ __forceinline__ void load_cols4(const EpiDev& e, int col0, int N, Epi
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     c.scale[k] = col0 + k < N ? e.scale[col0 + k] : 0.0;
+    c.mulv[k] = (e.f_mul && col0 + k < N) ? e.mul_ptr[col0 + k] : 0.0f;
     c.colv[k] = (e.f_col && col0 + k < N) ? e.col_ptr[col0 + k] : 0.0f;
   }
   c.lo = e.f_lo && e.lo_ptr ? e.lo_ptr[0] : 0.0f;
@@ -144,6 +146,10 @@ __device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, c
 #pragma unroll
   for (int k = 0; k < 4; ++k) y[k] = dequant(acc[k], c.scale[k]);
   if constexpr (FIXED) {
+    if (e.f_mul) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) y[k] = __fmul_rn(y[k], c.mulv[k]);
+    }
     if (e.f_col) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) y[k] = __fadd_rn(y[k], c.colv[k]);

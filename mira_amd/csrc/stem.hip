@@ -7,9 +7,9 @@
 // for ResNet-18 at batch 256) only for the pool to read it back.  Here the
 // pool runs on the int32 accumulators and the epilogue only on the pooled
 // values: for a fixed output channel the epilogue is a non-decreasing
-// function of the accumulator (dequant by a positive scale, then adds,
-// subtractions of a constant, maximum/minimum with constants: the host only
-// fuses such epilogues), so the maximum over a window commutes with it, and
+// function of the accumulator (dequant by a positive scale, then products
+// with positive constants, adds, subtractions of a constant, maximum/minimum
+// with constants: the host only fuses such epilogues), so the maximum over a window commutes with it, and
 // max(f(a1), .., f(ak)) == f(max(a1, .., ak)) bit for bit (the values are never
 // NaN unless an epilogue operand is, in which case both sides are NaN).  The
 // pad value joins a window through NumPy's maximum after the epilogue.
@@ -83,11 +83,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
   // wave*PPW + 8*half + t (t < 8; the upper half of a PK == 3 wave has 7)
   int chc[2];
   double scale[2];
-  float colv[2];
+  float mulv[2], colv[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     chc[j] = min(j * 32 + (lane & 31), a.O - 1);
     scale[j] = e.scale[chc[j]];
+    mulv[j] = FIXED && e.f_mul ? e.mul_ptr[chc[j]] : 1.0f;
     colv[j] = FIXED && e.f_col ? e.col_ptr[chc[j]] : 0.0f;
   }
   const float lo = FIXED && e.f_lo && e.lo_ptr ? e.lo_ptr[0] : 0.0f;
@@ -212,6 +213,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
   // median.
   const bool nan_free = FIXED && !__any(!(fabs(scale[0]) < INFINITY) || !(fabs(scale[1]) < INFINITY) ||
                                         !(fabsf(colv[0]) < INFINITY) || !(fabsf(colv[1]) < INFINITY) ||
+                                        !(fabsf(mulv[0]) < INFINITY) || !(fabsf(mulv[1]) < INFINITY) ||
                                         lo != lo || hi != hi) && !(a.pad_value != a.pad_value);
   auto finish = [&](int p, const int (&v)[2][8]) {
     const int top = p * PS - PPL;
@@ -259,12 +261,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
         float y = dequant(v[j][t], scale[j]);
         const bool padded = pad_rows || ((pad_cols >> t) & 1);
         if (nan_free) {
+          if (e.f_mul) y = __fmul_rn(y, mulv[j]);
           if (e.f_col) y = __fadd_rn(y, colv[j]);
           if (e.f_lo) y = y > lo ? y : lo;
           if (e.f_hi) y = y < hi ? y : hi;
           if (!pad_inert && padded) y = y > a.pad_value ? y : a.pad_value;
         } else {
           if constexpr (FIXED) {
+            if (e.f_mul) y = __fmul_rn(y, mulv[j]);
             if (e.f_col) y = __fadd_rn(y, colv[j]);
             if (e.f_lo) y = np_maximum(y, lo);
             if (e.f_hi) y = np_minimum(y, hi);
@@ -350,14 +354,15 @@ static bool launch_stem_pool(int ksub, bool rb2, dim3 grid, hipStream_t s, const
 
 // The pool commutes with the epilogue only if every step is a non-decreasing
 // function of the value with an operand that is the same across a window
-// (a scalar or a per-channel vector).
+// (a scalar or a per-channel vector).  A mul step is non-decreasing only for a
+// positive operand, which lives in device memory: the caller guarantees it.
 static bool monotone_epilogue(const mr_epilogue* epi) {
   for (int i = 0; i < epi->n_steps; ++i) {
     const mr_epi_step& st = epi->steps[i];
     if (st.fn == MR_EPI_RELU) continue;
     if (st.mode != MR_BC_SCALAR && st.mode != MR_BC_COL) return false;
     switch (st.fn) {
-      case MR_EPI_ADD: case MR_EPI_MAX: case MR_EPI_MIN: break;
+      case MR_EPI_ADD: case MR_EPI_MUL: case MR_EPI_MAX: case MR_EPI_MIN: break;
       case MR_EPI_SUB: if (st.swapped) return false; break;
       default: return false;
     }
@@ -405,7 +410,7 @@ int mr_qconv2d_maxpool(const int8_t* x, const mr_conv_geom* cg, const int8_t* b,
   MR_REQUIRE(epi != nullptr, "mr_qconv2d_maxpool: NULL epilogue");
   if (!mr::monotone_epilogue(epi)) {
     mr::set_error("mr_qconv2d_maxpool: the epilogue must be non-decreasing with scalar or per-channel operands "
-                  "(add, sub, maximum, minimum, relu)");
+                  "(add, sub, positive mul, maximum, minimum, relu)");
     return MR_EUNSUPPORTED;
   }
   MR_REQUIRE(reinterpret_cast<uintptr_t>(x) % 4 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0,

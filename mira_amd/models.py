@@ -86,11 +86,15 @@ def mlp_50m(batch: int = 4096, seed: int = 0) -> Graph:
 # ---------------------------------------------------------------- CNNs
 
 class _ConvNet:
-    """Helper that draws folded conv+BN parameters in a fixed order."""
+    """Helper that draws conv+BN parameters in a fixed order.  bn_epilogue=False folds BN
+    into the weights and a bias; bn_epilogue=True keeps it as the `mul` + `add` of
+    per-channel constants that MIRA's ONNX importer emits for BatchNormalization
+    (mira/frontends/onnx_import.py:423-431), after a bias-free conv."""
 
-    def __init__(self, g: Graph, seed: int):
+    def __init__(self, g: Graph, seed: int, bn_epilogue: bool = False):
         self.g = g
         self.rng = np.random.default_rng(seed)
+        self.bn_epilogue = bn_epilogue
 
     def conv(self, x, o: int, k: int, stride: int = 1, pad: int = 0, groups: int = 1, bn: bool = True):
         """conv2d + folded BatchNorm: Kaiming-normal (fan_out) weights scaled by gamma/sqrt(var+eps),
@@ -107,6 +111,10 @@ class _ConvNet:
             mean = rng.normal(0.0, 0.1, o)
             var = rng.uniform(0.5, 1.5, o)
             s = gamma / np.sqrt(var + 1e-5)
+            if self.bn_epilogue:
+                y = self.g.add("conv2d", [x, self.g.const(w)], attrs)
+                y = self.g.add("mul", [y, self.g.const(s.reshape(o, 1, 1).astype(np.float32))])
+                return self.g.add("add", [y, self.g.const((beta - mean * s).reshape(o, 1, 1).astype(np.float32))])
             w = (w * s.reshape(-1, 1, 1, 1)).astype(np.float32)
             bias = (beta - mean * s).astype(np.float32)
         else:
@@ -133,11 +141,12 @@ class _ConvNet:
         return g.add("add", [g.add("matmul", [flat, g.const(w)]), g.const(b)])
 
 
-def resnet18(batch: int = 256, seed: int = 0, classes: int = 1000) -> Graph:
-    """torchvision ResNet-18 with BN folded: 7x7/2 stem, 3x3/2 max pool, 4 stages of two basic
-    blocks (64, 128, 256, 512 channels; stride-2 1x1 downsample convs), GAP, fc."""
+def resnet18(batch: int = 256, seed: int = 0, classes: int = 1000, bn_epilogue: bool = False) -> Graph:
+    """torchvision ResNet-18: 7x7/2 stem, 3x3/2 max pool, 4 stages of two basic blocks (64, 128,
+    256, 512 channels; stride-2 1x1 downsample convs), GAP, fc.  BN folded, or (bn_epilogue)
+    as the ONNX importer's per-channel mul + add."""
     g = Graph("resnet18", [], [], [])
-    net = _ConvNet(g, seed)
+    net = _ConvNet(g, seed, bn_epilogue)
     x = g.input("x", (batch, 3, 224, 224))
     h = net.relu(net.conv(x, 64, 7, 2, 3))
     h = g.add("pad", [h], {"pads": ((0, 0), (0, 0), (1, 1), (1, 1)), "value": -np.inf})
@@ -155,12 +164,12 @@ def resnet18(batch: int = 256, seed: int = 0, classes: int = 1000) -> Graph:
     return g
 
 
-def mobilenet_v2(batch: int = 128, seed: int = 0, classes: int = 1000) -> Graph:
-    """torchvision MobileNetV2 with BN folded: 3x3/2 stem, 17 inverted residual blocks
-    (1x1 expand + ReLU6, 3x3 depthwise + ReLU6, 1x1 linear projection, residual when
-    shapes allow), 1x1 conv to 1280 + ReLU6, GAP, fc."""
+def mobilenet_v2(batch: int = 128, seed: int = 0, classes: int = 1000, bn_epilogue: bool = False) -> Graph:
+    """torchvision MobileNetV2: 3x3/2 stem, 17 inverted residual blocks (1x1 expand + ReLU6,
+    3x3 depthwise + ReLU6, 1x1 linear projection, residual when shapes allow), 1x1 conv to
+    1280 + ReLU6, GAP, fc.  BN folded, or (bn_epilogue) as the ONNX importer's mul + add."""
     g = Graph("mobilenet_v2", [], [], [])
-    net = _ConvNet(g, seed)
+    net = _ConvNet(g, seed, bn_epilogue)
     x = g.input("x", (batch, 3, 224, 224))
     h = net.relu6(net.conv(x, 32, 3, 2, 1))
     c_in = 32

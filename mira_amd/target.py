@@ -303,14 +303,21 @@ class RocmExecutable:
 
     def _monotone_epilogue(self, op: ir.Op) -> bool:
         """Every step non-decreasing in the value, with an operand that is the same across a
-        pooling window (scalar or per-channel)."""
+        pooling window (scalar or per-channel).  A mul qualifies when its operand is a
+        constant that is finite and positive everywhere (a BatchNorm scale)."""
         rshape = op.result.type.shape
         for fn, idx, swapped in op.attrs.get("epilogue", ()):
             if fn == "relu":
                 continue
-            if fn not in ("add", "sub", "maximum", "minimum") or (fn == "sub" and swapped):
-                return False
             v = op.inputs[idx]
+            if fn == "mul":
+                if v not in self.consts:
+                    return False
+                m = np.asarray(self._const_value(v), np.float32)
+                if not (np.isfinite(m).all() and (m > 0).all()):
+                    return False
+            elif fn not in ("add", "sub", "maximum", "minimum") or (fn == "sub" and swapped):
+                return False
             shape = np.shape(self._const_value(v)) if v in self.consts else v.type.shape
             if _bcast_mode(shape, rshape, True) not in (L.BC_SCALAR, L.BC_COL):
                 return False

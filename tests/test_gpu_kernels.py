@@ -312,6 +312,11 @@ FORMS = {
     "bias_relu6_f32": ((("add", 1, False), ("maximum", 3, False), ("minimum", 4, False)), True, False),
     "bias_f32_i8": ((("add", 1, False),), True, True),
     "bias_res_f32_i8": ((("add", 1, False), ("add", 2, False)), True, True),
+    # BatchNorm as MIRA's ONNX importer leaves it: a per-channel mul ahead of the bias
+    "bn_relu_i8": ((("mul", 5, False), ("add", 1, False), ("relu", None, False)), False, True),
+    "bn_res_f32_i8": ((("mul", 5, False), ("add", 1, False), ("add", 2, False), ("relu", None, False)), True, True),
+    "bn_relu6_f32": ((("mul", 5, False), ("add", 1, False), ("maximum", 3, False), ("minimum", 4, False)), True,
+                     False),
 }
 FORM_CONV_CASES = [
     (2, 64, 56, 56, 64, 3, 1, 1, 1),      # patch, 128x64 tiles
@@ -343,9 +348,10 @@ def test_qconv2d_epilogue_forms(lib, form, n, c, h, w, o, k, s, p, d):
     bias = (rng.standard_normal((o, 1, 1)) * 0.1).astype(np.float32)
     res = rng.standard_normal((n, o, oh, ow)).astype(np.float32)
     zero, six = np.array(0, np.float32), np.array(6, np.float32)
+    bn = rng.uniform(-1.5, 1.5, (o, 1, 1)).astype(np.float32)
     attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "stride": (s, s), "padding": (p, p),
              "dilation": (d, d), "epilogue": steps}
-    want = G.qconv2d([x, bias, res, zero, six], attrs)
+    want = G.qconv2d([x, bias, res, zero, six, bn], attrs)
     next_xs = float(np.abs(want[np.isfinite(want)]).max()) / 127 or 1.0
     cp = pack.c_pad_for(c)
     xq = empty((n, h, w, cp), torch.int8)
@@ -355,7 +361,8 @@ def test_qconv2d_epilogue_forms(lib, form, n, c, h, w, o, k, s, p, d):
     scale = T(pack.combined_scale(xs, ws))
     g = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=cp, o=o, oh=oh, ow=ow, kh=k, kw=k, sh=s, sw=s, ph=p, pw=p, dh=d, dw=d)
     operands = {1: (L.BC_COL, T(bias.reshape(o)), 0), 2: (L.BC_FULL, T(res.transpose(0, 2, 3, 1).reshape(M, o)), o),
-                3: (L.BC_SCALAR, T(zero.reshape(1)), 0), 4: (L.BC_SCALAR, T(six.reshape(1)), 0)}
+                3: (L.BC_SCALAR, T(zero.reshape(1)), 0), 4: (L.BC_SCALAR, T(six.reshape(1)), 0),
+                5: (L.BC_COL, T(bn.reshape(o)), 0)}
     dev_steps = [(fn, 0, None, 0, sw) if idx is None else (fn, operands[idx][0], operands[idx][1], operands[idx][2], sw)
                  for fn, idx, sw in steps]
     y = empty((M, o), torch.float32) if want_f32 else None

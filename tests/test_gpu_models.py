@@ -102,6 +102,18 @@ def test_mobilenet_v2_batch2():
     assert [s.device for s in runner.segments] == ["rocm"]
 
 
+@pytest.mark.parametrize("builder", [models.resnet18, models.mobilenet_v2])
+def test_onnx_layout_batch2(builder):
+    """The CNNs as MIRA's ONNX importer lays them out: BatchNormalization as a per-channel mul +
+    add after a bias-free conv (mira/frontends/onnx_import.py:423-431), fused into the conv
+    epilogue.  Every op on rocm; accumulators and outputs bit-exact."""
+    g, _ = _quantized(lambda batch, seed: builder(batch=batch, seed=seed, bn_epilogue=True), 2, 0, (11, 12),
+                      dist="uniform")
+    assert any(op.attrs.get("epilogue", ())[:1] == (("mul", 1, False),) for op in g.compute_ops())
+    runner = _compare(g, {"x": models.image_batch((2, 3, 224, 224), 5)}, fallback=False)
+    assert [s.device for s in runner.segments] == ["rocm"]
+
+
 def test_mlp50m_batch8():
     g, _ = _quantized(models.mlp_50m, 8, 0, (2, 3))
     _compare(g, {"x": models.normal_batch((8, 4096), 1)}, fallback=False)
@@ -128,9 +140,13 @@ def test_mlp50m_batch4096_rows():
     _rows_match_small_run(models.mlp_50m, 4096, [0, 1234, 4095], 0, (2, 3), "normal", (4096,))
 
 
-def test_resnet18_batch2_fused_stem():
-    """Without debug accumulators the stem conv, pad and max pool run as one kernel."""
-    g, _ = _quantized(models.resnet18, 2, 0, (11, 12), dist="uniform")
+@pytest.mark.parametrize("bn_epilogue", [False, True])
+def test_resnet18_batch2_fused_stem(bn_epilogue):
+    """Without debug accumulators the stem conv, pad and max pool run as one kernel, also with
+    the ONNX importer's BatchNorm mul (a positive per-channel constant keeps the epilogue
+    monotone, so pooling the accumulators first is exact)."""
+    g, _ = _quantized(lambda batch, seed: models.resnet18(batch=batch, seed=seed, bn_epilogue=bn_epilogue), 2, 0,
+                      (11, 12), dist="uniform")
     runner = compile_graph(g, RocmTarget())
     exe = runner.segments[0].executable
     assert exe.kernel_counts.get("qconv2d_maxpool") == 1 and "maxpool2d" not in exe.kernel_counts
