@@ -28,6 +28,8 @@ int8 weight-only mode (f32 activations, int8 weights dequantized in
 registers), batch 1: four weight-streaming f32 matmul launches.
 resnet18-onnx is ResNet-18 laid out as MIRA's ONNX importer emits it (BN as a
 per-channel mul + add in each conv epilogue instead of folded weights).
+gpt-decode times the device part of one character-level GPT decode step
+(default batch 1; the host-side attention and normalisations are excluded).
 """
 from __future__ import annotations
 
@@ -211,6 +213,75 @@ def bench_workload(args) -> int:
     return 0
 
 
+def bench_gpt(args) -> int:
+    """The character-level GPT decode step (L=2, d=64, vocab 65, context 128), W8A8 on the
+    QKV/out/MLP/vocab projections.  Attention, softmax, layernorm and the gelu projection
+    run on the host (MIRA's cpu target), which this package does not ship, so the timed
+    work is the device part of one decode step: every rocm segment's launch list, inputs
+    already in HBM.  Reported per step and per token (step / batch)."""
+    import torch
+    from mira_amd import models, passes
+    from mira_amd.partition import partition
+    from mira_amd.quantize import calibration_peaks, quantize_w8a8
+    from mira_amd.target import RocmTarget
+    cfg = models.GPTConfig()
+    params = models.gpt_params(cfg, 0)
+
+    def graph(batch):
+        g = models.gpt_decode_step(cfg, batch, params)
+        passes.optimize(g)
+        return g
+    twin = graph(2)
+    calib = []
+    for s in (2, 3):
+        r = np.random.default_rng(s)
+        toks = r.integers(0, cfg.V, (2, cfg.T)).astype(np.int32)
+        caches = [(r.standard_normal((2, cfg.T, cfg.D)).astype(np.float32),
+                   r.standard_normal((2, cfg.T, cfg.D)).astype(np.float32)) for _ in range(cfg.L)]
+        calib.append(models.gpt_step_feeds(cfg, params, toks, 16, caches))
+    peaks = calibration_peaks(twin, calib)
+    g = graph(args.batch)
+    quantize_w8a8(g, peaks=peaks)
+    tgt = RocmTarget()
+    segs, _ = partition(g, tgt)
+    exes = [tgt.compile(s.graph) for s in segs if s.device == "rocm"]
+    for i, exe in enumerate(exes):
+        exe.upload({v: models.normal_batch(v.type.shape, 100 + i).astype(np.float32) for v in exe.g.inputs})
+    stream = torch.cuda.current_stream()
+
+    def step():
+        for exe in exes:
+            exe.launch()
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / args.steps
+    kernels = {}
+    for exe in exes:
+        for kind, row in kernel_breakdown(exe, time_launches(exe, stream)).items():
+            k = kernels.setdefault(kind, {"launches": 0, "ms": 0.0})
+            k["launches"] += row["launches"]
+            k["ms"] = round(k["ms"] + row["ms"], 4)
+    launches = sum(len(exe.launches) for exe in exes)
+    weight_bytes = sum(exe.const_bytes for exe in exes)
+    log(f"gpt decode batch {args.batch}: {len(exes)} rocm segments, {launches} launches, {ms * 1e3:.1f} us/step")
+    print(json.dumps({"workload": "gpt-decode", "batch": args.batch, "steps": args.steps, "warmup": args.warmup,
+                      "ms_per_step": round(ms, 4), "us_per_token": round(ms * 1e3 / args.batch, 3),
+                      "tokens_per_s": round(args.batch / (ms * 1e-3), 1), "rocm_segments": len(exes),
+                      "launches_per_step": launches, "device_constant_bytes": weight_bytes,
+                      "dtype": "int8", "data": "synthetic",
+                      "timed": "device part of one decode step (the host-side attention, softmax, layernorm "
+                               "and gelu projection are not included)",
+                      "kernels": kernels}), flush=True)
+    return 0
+
+
 def cpu_baseline(peaks, macs_per_image: int) -> dict:
     """The golden model on a bounded 2-image sample: 1 warm-up + 3 timed runs, median."""
     from oracle import golden as G
@@ -344,7 +415,7 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=None,
                     help="default 256 (resnet18), 1 (mlp50m, mlp50m-int8), 128 (mobilenetv2)")
     ap.add_argument("--workload", default="resnet18",
-                    choices=["resnet18", "resnet18-onnx", "mlp50m", "mlp50m-int8", "mobilenetv2"])
+                    choices=["resnet18", "resnet18-onnx", "mlp50m", "mlp50m-int8", "mobilenetv2", "gpt-decode"])
     ap.add_argument("--per-launch", action="store_true", help="per-launch time against each launch's roofline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true", help="run the plain copy used to scale counters")
@@ -363,7 +434,9 @@ def main() -> int:
         return 2
     if args.batch is None:
         args.batch = {"resnet18": 256, "resnet18-onnx": 256, "mlp50m": 1, "mlp50m-int8": 1,
-                      "mobilenetv2": 128}[args.workload]
+                      "mobilenetv2": 128, "gpt-decode": 1}[args.workload]
+    if args.workload == "gpt-decode":
+        return bench_gpt(args)
     if args.per_launch:
         return per_launch(args)
     if args.workload != "resnet18":
