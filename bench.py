@@ -27,7 +27,9 @@ depthwise kernel; both are HBM-bound.  mlp50m-int8 is the same MLP in the
 int8 weight-only mode (f32 activations, int8 weights dequantized in
 registers), batch 1: four weight-streaming f32 matmul launches.
 resnet18-onnx is ResNet-18 laid out as MIRA's ONNX importer emits it (BN as a
-per-channel mul + add in each conv epilogue instead of folded weights).
+per-channel mul + add in each conv epilogue instead of folded weights);
+resnet18-f16 is the f16 graph (MIRA's default precision for accelerator
+targets), every result rounded to f16 and stored as f32.
 gpt-decode times the device part of one character-level GPT decode step
 (default batch 1; the host-side attention and normalisations are excluded).
 """
@@ -83,12 +85,15 @@ def build_workload(name: str, batch: int):
         def builder(batch, seed):
             return models.resnet18(batch=batch, seed=seed, bn_epilogue=True)
         cb, seeds, gen = 2, (11, 12), models.image_batch
+    elif name == "resnet18-f16":
+        builder, cb, seeds, gen = models.resnet18, 2, (11, 12), models.image_batch
     else:
         raise SystemExit(f"unknown workload {name!r}")
+    precision = "f16" if name.endswith("-f16") else None
     g = builder(batch=batch, seed=0)
-    passes.optimize(g)
+    passes.optimize(g, precision=precision)
     twin = builder(batch=cb, seed=0)
-    passes.optimize(twin)
+    passes.optimize(twin, precision=precision)
     shape = twin.inputs[0].type.shape
     quantize_w8a8(g, peaks=calibration_peaks(twin, [{"x": gen(shape, s)} for s in seeds]))
     return g, gen(g.inputs[0].type.shape, 7)
@@ -415,7 +420,8 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=None,
                     help="default 256 (resnet18), 1 (mlp50m, mlp50m-int8), 128 (mobilenetv2)")
     ap.add_argument("--workload", default="resnet18",
-                    choices=["resnet18", "resnet18-onnx", "mlp50m", "mlp50m-int8", "mobilenetv2", "gpt-decode"])
+                    choices=["resnet18", "resnet18-onnx", "resnet18-f16", "mlp50m", "mlp50m-int8", "mobilenetv2",
+                             "gpt-decode"])
     ap.add_argument("--per-launch", action="store_true", help="per-launch time against each launch's roofline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true", help="run the plain copy used to scale counters")
@@ -433,7 +439,7 @@ def main() -> int:
               "by data parallelism, one share per GPU). Run with --gpus 1.", file=sys.stderr)
         return 2
     if args.batch is None:
-        args.batch = {"resnet18": 256, "resnet18-onnx": 256, "mlp50m": 1, "mlp50m-int8": 1,
+        args.batch = {"resnet18": 256, "resnet18-onnx": 256, "resnet18-f16": 256, "mlp50m": 1, "mlp50m-int8": 1,
                       "mobilenetv2": 128, "gpt-decode": 1}[args.workload]
     if args.workload == "gpt-decode":
         return bench_gpt(args)

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MR_ABI_VERSION 2
+#define MR_ABI_VERSION 3
 
 enum mr_status {
   MR_OK = 0,
@@ -77,13 +77,19 @@ typedef struct mr_epi_step {
 /* What happens to each result element after the contraction:
  *   y = f32(f64(acc) * scale[col])          (mira/ops.py:618,633; skipped when scale == NULL)
  *   y = steps[0..n_steps)(y)                (mira/ops.py:192-199)
+ *   y = f32(f16(y))                         (flags & MR_EPI_OUT_F16: the op's result is
+ *                                            f16, mira/ops.py:620,634 .astype(float16);
+ *                                            round to nearest even, overflow to inf; the
+ *                                            value is still stored as f32)
  *   out_f32[row*ldo+col] = y                (if out_f32)
  *   out_i8[row*ldq+col]  = clip(rint(y / out_xs), +-127)
  *                                           (mira/ops.py:602-603, the next q-op's input)
  *   out_acc[row*ldacc+col] = acc            (int32 accumulator, if out_acc) */
+#define MR_EPI_OUT_F16 1
+
 typedef struct mr_epilogue {
   int32_t n_steps;
-  int32_t reserved0;
+  int32_t flags;      /* MR_EPI_OUT_F16 or 0 */
   mr_epi_step steps[MR_MAX_EPI];
   const double* scale;
   float* out_f32;
@@ -202,6 +208,12 @@ int mr_maxpool2d_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c,
                      int32_t size, int32_t stride, int32_t pad_top, int32_t pad_left,
                      float pad_value, int32_t oh, int32_t ow, float* y,
                      int8_t* yq, int32_t c_pad, float xs, void* stream);
+
+/* Replaces mira/ops.py:405-406 cast of an f32 tensor to f16, and the final
+ * .astype(float16) of an f16 op that takes no epilogue descriptor (e.g.
+ * reduce_mean): y[i] = f32(f16(x[i])), round to nearest even, over n floats
+ * (y == x allowed).  f16 tensors stay stored as f32 on the device. */
+int mr_round_f16_f32(const float* x, int64_t n, float* y, void* stream);
 
 /* mira/ops.py:318-343 reduce_mean over H,W (NumPy order: pairwise f32 sum,
  * then f32(f64(sum) / count)).  NHWC f32 [n,hw,c] -> [n,c]; optional int8. */

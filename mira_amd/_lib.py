@@ -10,11 +10,12 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "libmira_rocm.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 MAX_EPI = 8
 
 # enum mr_epi_fn
 EPI_FN = {"add": 1, "sub": 2, "mul": 3, "div": 4, "maximum": 5, "minimum": 6, "relu": 7}
+EPI_OUT_F16 = 1     # mr_epilogue.flags: round results to f16 (the op's dtype is f16)
 # enum mr_bcast
 BC_SCALAR, BC_COL, BC_ROW, BC_FULL = 0, 1, 2, 3
 
@@ -22,7 +23,7 @@ EXPORTS = [
     "mr_abi_version", "mr_last_error", "mr_sizeof", "mr_init",
     "mr_quantize_rows", "mr_quantize_nchw_nhwc",
     "mr_qmatmul", "mr_w8_matmul_f32", "mr_qconv2d", "mr_qconv2d_maxpool", "mr_dwconv2d_f32",
-    "mr_maxpool2d_f32", "mr_mean_hw_f32", "mr_pad_hw_f32",
+    "mr_maxpool2d_f32", "mr_mean_hw_f32", "mr_pad_hw_f32", "mr_round_f16_f32",
     "mr_nchw_to_nhwc_f32", "mr_nhwc_to_nchw_f32",
 ]
 
@@ -33,7 +34,7 @@ class EpiStep(C.Structure):
 
 
 class Epilogue(C.Structure):
-    _fields_ = [("n_steps", C.c_int32), ("reserved0", C.c_int32), ("steps", EpiStep * MAX_EPI),
+    _fields_ = [("n_steps", C.c_int32), ("flags", C.c_int32), ("steps", EpiStep * MAX_EPI),
                 ("scale", C.c_void_p), ("out_f32", C.c_void_p), ("ldo", C.c_int64),
                 ("out_i8", C.c_void_p), ("ldq", C.c_int64), ("out_xs", C.c_float), ("reserved1", C.c_int32),
                 ("out_acc", C.c_void_p), ("ldacc", C.c_int64)]
@@ -68,6 +69,7 @@ _SIGS = {
                           _p], C.c_int),
     "mr_mean_hw_f32": ([_p, _i32, _i32, _i32, _p, _p, _i32, _f32, _p], C.c_int),
     "mr_pad_hw_f32": ([_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p], C.c_int),
+    "mr_round_f16_f32": ([_p, _i64, _p, _p], C.c_int),
     "mr_nchw_to_nhwc_f32": ([_p, _i32, _i32, _i32, _i32, _p, _p], C.c_int),
     "mr_nhwc_to_nchw_f32": ([_p, _i32, _i32, _i32, _i32, _p, _p], C.c_int),
 }

@@ -143,14 +143,19 @@ def default_calibration(graph: ir.Graph) -> list[dict]:
 
 
 def compile_ir(graph: ir.Graph, target: Union[str, object] = "rocm", *, optimize: bool = True, fuse: bool = True,
-               cost_model: bool = True, quantize: Optional[str] = None, calibration: Optional[list] = None,
-               peaks: Optional[Sequence[float]] = None, fallback=None, **target_options) -> CompiledProgram:
-    """mira/compiler.py:287-311 with precision fixed to the f32 graph (the rocm target
-    computes f32 epilogues; the reference's "auto" would lower non-cpu targets to f16)."""
+               precision: Optional[str] = None, cost_model: bool = True, quantize: Optional[str] = None,
+               calibration: Optional[list] = None, peaks: Optional[Sequence[float]] = None, fallback=None,
+               **target_options) -> CompiledProgram:
+    """mira/compiler.py:287-311.  precision None keeps the f32 graph (bit-exact against the
+    cpu target's f32 results); "f16" lowers it as the reference does for accelerator
+    targets under its default "auto", and the rocm target then rounds every result to
+    f16 exactly as the reference's ops do."""
     t0 = time.perf_counter()
     log = [("input", str(graph))]
     if optimize:
-        passes.optimize(graph, fuse=fuse, log=log)
+        passes.optimize(graph, fuse=fuse, log=log, precision=precision)
+    elif precision == "f16":
+        passes.to_f16(graph)
     if quantize == "w8a8":
         from .quantize import quantize_w8a8
         if calibration is None and peaks is None:

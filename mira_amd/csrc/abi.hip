@@ -29,6 +29,7 @@ int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out)
     MR_REQUIRE(epi->scale == nullptr, "this kernel has no int32 accumulator to dequantize");
   }
   MR_REQUIRE(epi->out_f32 || epi->out_i8 || epi->out_acc, "epilogue writes no output");
+  MR_REQUIRE((epi->flags & ~MR_EPI_OUT_F16) == 0, "unknown epilogue flags 0x%x", epi->flags);
   if (epi->out_f32) MR_REQUIRE(epi->ldo >= cols, "ldo %lld < cols %lld", (long long)epi->ldo, (long long)cols);
   if (epi->out_i8) {
     MR_REQUIRE(epi->ldq >= cols, "ldq %lld < cols %lld", (long long)epi->ldq, (long long)cols);
@@ -62,6 +63,7 @@ int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out)
   out->out_i8 = epi->out_i8;
   out->ldq = epi->ldq;
   out->out_xs = epi->out_xs;
+  out->f16 = (epi->flags & MR_EPI_OUT_F16) != 0;
   out->out_acc = epi->out_acc;
   out->ldacc = epi->ldacc;
   out->out_rxs = epi->out_i8 ? 1.0 / static_cast<double>(epi->out_xs) : 0.0;

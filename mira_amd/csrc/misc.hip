@@ -171,6 +171,15 @@ __global__ void __launch_bounds__(256) dwconv3x3_kernel(const float* __restrict_
   }
 }
 
+// ---------------------------------------------------------------- f16 rounding
+
+// y[i] = f32(f16(x[i])): a cast to f16 (mira/ops.py:405-406) or the final
+// .astype(float16) of an op without an epilogue descriptor, on f32 storage.
+__global__ void __launch_bounds__(256) round_f16_kernel(const float* __restrict__ x, int64_t n, float* y) {
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) y[i] = round_f16(x[i]);
+}
+
 // ---------------------------------------------------------------- maxpool
 
 template <typename Idx>
@@ -463,6 +472,16 @@ int mr_pad_hw_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, in
     hipLaunchKernelGGL(mr::pad_kernel<uint64_t>, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), x, n, h, w, c, top, left, oh, ow, value, y);
   MR_LAUNCH_CHECK("pad_hw");
+  return MR_OK;
+}
+
+int mr_round_f16_f32(const float* x, int64_t n, float* y, void* stream) {
+  MR_REQUIRE(x && y, "mr_round_f16_f32: NULL argument");
+  MR_REQUIRE(n >= 0, "mr_round_f16_f32: bad size");
+  if (n == 0) return MR_OK;
+  hipLaunchKernelGGL(mr::round_f16_kernel, dim3(mr::grid_1d(n, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     x, n, y);
+  MR_LAUNCH_CHECK("round_f16");
   return MR_OK;
 }
 

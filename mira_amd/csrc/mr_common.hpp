@@ -10,6 +10,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
 
 #include <cstdint>
 #include <cstdarg>
@@ -131,7 +132,7 @@ struct EpiDev {
   int8_t* out_i8;
   int64_t ldq;
   float out_xs;
-  int32_t reserved;
+  int32_t f16;     // round results to f16 after the steps (MR_EPI_OUT_F16)
   int32_t* out_acc;
   int64_t ldacc;
   double out_rxs;  // fl64(1 / out_xs), computed on the host
@@ -201,12 +202,19 @@ __device__ __forceinline__ float epi_fixed(const EpiDev& e, float y, int64_t row
   return y;
 }
 
+// NumPy's astype(float16) of an f32 value, back in f32: round to nearest even
+// (overflow to inf, f16 subnormals kept), for ops whose result dtype is f16
+// (mira/ops.py:620, 634 and every other op's final .astype).  Idempotent.
+__device__ __forceinline__ float round_f16(float y) { return __half2float(__float2half_rn(y)); }
+
 __device__ __forceinline__ float epi_steps(const EpiDev& e, float y, int64_t row, int64_t col) {
-  return e.fixed ? epi_fixed(e, y, row, col) : epi_generic(e, y, row, col);
+  y = e.fixed ? epi_fixed(e, y, row, col) : epi_generic(e, y, row, col);
+  return e.f16 ? round_f16(y) : y;
 }
 
 // Write the outputs for one finished result element.
 __device__ __forceinline__ void epi_store(const EpiDev& e, float y, int64_t row, int64_t col) {
+  if (e.f16) y = round_f16(y);
   if (e.out_f32) e.out_f32[row * e.ldo + col] = y;
   if (e.out_i8) e.out_i8[row * e.ldq + col] = quantize_rcp(y, e.out_rxs);
 }
@@ -254,7 +262,7 @@ constexpr int SPEC_BIAS_RES_F32_I8 = SF_COL | SF_FULL | SF_F32 | SF_I8;
 // form without an int32 accumulator output, every output and operand row
 // 16-byte (f32) / 4-byte (int8) aligned.
 inline int spec_form(const EpiDev& e) {
-  if (!e.fixed || e.out_acc) return -1;
+  if (!e.fixed || e.out_acc || e.f16) return -1;
   auto al = [](const void* p, int64_t ld, int bytes) {
     return reinterpret_cast<uintptr_t>(p) % bytes == 0 && ld % 4 == 0;
   };

@@ -180,6 +180,10 @@ __device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, c
     for (int k = 0; k < 4; ++k)
       if (col0 + k < N) y[k] = epi_generic(e, y[k], row, col0 + k);
   }
+  if (e.f16) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) y[k] = round_f16(y[k]);
+  }
   if (c.vec) {
     if (e.out_acc) *reinterpret_cast<v4i*>(e.out_acc + row * e.ldacc + col0) = acc;
     if (e.out_f32) *reinterpret_cast<float4*>(e.out_f32 + row * e.ldo + col0) = make_float4(y[0], y[1], y[2], y[3]);

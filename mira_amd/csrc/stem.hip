@@ -265,6 +265,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
           if (e.f_col) y = __fadd_rn(y, colv[j]);
           if (e.f_lo) y = y > lo ? y : lo;
           if (e.f_hi) y = y < hi ? y : hi;
+          if (e.f16) y = round_f16(y);
           if (!pad_inert && padded) y = y > a.pad_value ? y : a.pad_value;
         } else {
           if constexpr (FIXED) {
@@ -276,6 +277,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
             const int pc = wave * PPW + 8 * half + t;
             y = epi_generic(e, y, row0 + min(pc, a.POW - 1), chc[j]);
           }
+          if (e.f16) y = round_f16(y);
           if (!pad_inert) y = np_maximum(y, padded ? a.pad_value : -INFINITY);
         }
         if (e.out_f32) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rf, of, 0, 0);

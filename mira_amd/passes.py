@@ -190,14 +190,56 @@ PIPELINE: list[tuple[str, Callable[[ir.Graph], bool]]] = [
 ]
 
 
-def optimize(g: ir.Graph, fuse: bool = True, log: Optional[list] = None) -> ir.Graph:
-    """mira/passes.py:266-286 without f16 lowering (the rocm target computes the f32 graph)."""
+def to_f16(g: ir.Graph) -> bool:
+    """mira/passes.py:206-253 for graphs without control flow: every f32 value becomes f16
+    (f32 constants are rounded to f16), a cast to f16 follows each f32 graph input and a
+    cast back to f32 precedes each f32 graph output, and float<->float casts inside the
+    graph disappear (casts to or from integers stay, aimed at f16)."""
+    if all(op.result.type.dtype != "f32" for op in g.ops if op.results) and \
+            all(v.type.dtype != "f32" for v in g.inputs):
+        return False
+    if any(op.is_control for op in g.ops):
+        raise NotImplementedError("to_f16: graphs with control flow are not supported here")
+    old_ops = g.ops
+    g.ops = []
+    remap: dict = {}
+    for v in g.inputs:
+        remap[v] = g.add("cast", [v], {"dtype": "f16"}) if v.type.dtype == "f32" else v
+    for op in old_ops:
+        if op.is_const:
+            value = op.attrs["value"]
+            remap[op.result] = g.const(value.astype(np.float16) if value.dtype.kind == "f" else value)
+        elif op.kind == "cast":
+            src = remap[op.inputs[0]]
+            target = "f16" if op.attrs["dtype"] in ("f16", "f32") else op.attrs["dtype"]
+            remap[op.result] = src if src.type.dtype == target else g.add("cast", [src], {"dtype": target})
+        else:
+            remap[op.result] = g.add(op.kind, [remap[v] for v in op.inputs], dict(op.attrs))
+    outs = []
+    for v in g.outputs:
+        nv = remap[v]
+        if v.type.dtype == "f32" and nv.type.dtype != "f32":
+            nv = g.add("cast", [nv], {"dtype": "f32"})
+        outs.append(nv)
+    g.outputs = outs
+    return True
+
+
+def optimize(g: ir.Graph, fuse: bool = True, log: Optional[list] = None,
+             precision: Optional[str] = None) -> ir.Graph:
+    """mira/passes.py:266-286: optional f16 lowering, fold/simplify/CSE/DCE to a fixed
+    point, then epilogue fusion."""
     def run(name: str, fn) -> bool:
         changed = fn(g)
         g.verify()
         if changed and log is not None:
             log.append((name, str(g)))
         return changed
+
+    if precision == "f16":
+        run("to-f16", to_f16)
+    elif precision is not None:
+        raise ValueError(f"precision={precision!r}: expected None (f32) or 'f16'")
 
     for _ in range(10):
         if not any([run(n, f) for n, f in PIPELINE]):

@@ -78,6 +78,12 @@ class DevValue:
         return pack.c_pad_for(self.cols) if self.nhwc else pack.row_stride_for(self.cols)
 
 
+# Result dtypes the kernels produce.  f16 values (the reference's default precision for
+# accelerator targets, mira/passes.py:206-253) stay stored as f32 on the device: every op
+# computes in f32 as the reference's ops do (mira/ops.py:43-44) and rounds its result to
+# f16 where the reference casts it (.astype(float16)), so f16 results are bit-exact too.
+FLOAT_DTYPES = ("f32", "f16")
+
 W8_MAX_ROWS = 64     # mr_w8_matmul_f32 streams the weights once per 8 rows: decode shapes only
 
 
@@ -100,9 +106,13 @@ class RocmTarget:
         """None if the rocm kernels run `op` with the golden model's exact arithmetic."""
         if op.is_control:
             return "control flow runs on the host"
-        if any(r.type.dtype != "f32" for r in op.results):
-            return "the rocm target computes the f32 graph (W8A8 parity needs f32 epilogues)"
+        if any(r.type.dtype not in FLOAT_DTYPES for r in op.results):
+            return "the rocm target computes f32 and f16 graphs only"
         k = op.kind
+        if k == "cast":
+            if op.inputs[0].type.dtype not in FLOAT_DTYPES:
+                return "casts from integer types run on the host"
+            return None
         if k in ("qmatmul", "qconv2d"):
             if k == "qconv2d" and op.attrs.get("groups", 1) != 1:
                 return "grouped int8 convolution has no kernel"
@@ -144,8 +154,8 @@ class RocmTarget:
         if p is None or p.kind != "dequantize" or p.attrs["axis"] != 1 or w.type.rank != 2:
             return ("f32 matmul stays on the CPU (its summation order is BLAS's, not reproducible bit for bit) "
                     "unless its weight is an int8 weight-only constant")
-        if x.type.rank not in (2, 3) or x.type.dtype != "f32":
-            return "weight-only int8 matmul runs on rocm for rank-2/3 f32 activations"
+        if x.type.rank not in (2, 3) or x.type.dtype not in FLOAT_DTYPES:
+            return "weight-only int8 matmul runs on rocm for rank-2/3 float activations"
         rows = int(np.prod(x.type.shape[:-1], dtype=np.int64))
         if rows > W8_MAX_ROWS:
             return f"weight-only int8 matmul runs on rocm for decode shapes (<= {W8_MAX_ROWS} rows), not {rows}"
@@ -158,8 +168,8 @@ class RocmTarget:
             if idx is None:
                 continue
             v = op.inputs[idx]
-            if v.type.dtype != "f32":
-                return "epilogue operands must be f32"
+            if v.type.dtype not in FLOAT_DTYPES:
+                return "epilogue operands must be f32 or f16"
             if v.producer is not None and v.producer.is_constant_like:
                 continue
             if _bcast_mode(v.type.shape, shape, is_conv) is None:
@@ -260,6 +270,19 @@ class RocmExecutable:
                 if r in self.need_i8 and self._i8_view(op.inputs[0], r):
                     lst = self.need_i8.setdefault(op.inputs[0], [])
                     lst += [s for s in self.need_i8[r] if s not in lst]
+        # a cast to f16 that is a graph input's only use rounds the input buffer in place
+        # before anything reads it; its result then shares the input's device copies
+        self.input_casts: set = set()
+        for op in g.ops:
+            v = op.inputs[0] if op.kind == "cast" and op.inputs else None
+            if v is not None and v in g.inputs and v not in g.outputs and len(users.get(v, [])) == 1 and \
+                    v.type.dtype == "f32" and op.result.type.dtype == "f16":
+                self.input_casts.add(op)
+                r = op.result
+                if r not in self.need_f32:
+                    self.need_f32.discard(v)
+                lst = self.need_i8.setdefault(v, [])
+                lst += [s for s in self.need_i8.get(r, []) if s not in lst]
         self.staging: dict[ir.Value, object] = {}
         for v in g.inputs:
             self._emit_input(v)
@@ -354,6 +377,8 @@ class RocmExecutable:
         lib = self.lib
         stage = torch.empty(v.type.shape, dtype=torch.float32, device=self.dev)
         self.staging[v] = stage
+        if any(op.inputs[0] is v for op in self.input_casts):
+            self._round_f16(stage, stage)
         d = self._new_dv(v, with_i8=True)
         if d.nhwc:
             n, c, h, w = v.type.shape
@@ -459,6 +484,7 @@ class RocmExecutable:
             raise L.RocmError(f"epilogue has {len(steps)} steps; the kernels take at most {L.MAX_EPI}")
         rshape = op.result.type.shape
         e.n_steps = len(steps)
+        e.flags = L.EPI_OUT_F16 if op.result.type.dtype == "f16" else 0
         for i, (fn, idx, sw) in enumerate(steps):
             st = e.steps[i]
             st.fn = L.EPI_FN[fn]
@@ -693,8 +719,11 @@ class RocmExecutable:
         x = self._src(op.inputs[0])
         n, c, h, w = op.inputs[0].type.shape
         out = self._new_dv(op.result)
+        f16 = op.result.type.dtype == "f16"
+        if f16 and out.f32 is None:
+            out.f32 = _t().empty((out.rows, out.cols), dtype=_t().float32, device=self.dev)
         wants = self.need_i8.get(op.result, [])
-        fused = wants[0] if wants else None
+        fused = wants[0] if wants and not f16 else None     # f16: quantize the rounded mean
         yq, ld = None, 0
         if fused is not None:
             ld = out.i8_ld()
@@ -705,7 +734,31 @@ class RocmExecutable:
         self._add("mean_hw", lambda s: L.check(lib.mr_mean_hw_f32(
             xt.data_ptr(), n, h * w, c, _ptr(yt), _ptr(yq), ld, xsv, s), "mr_mean_hw_f32"),
             nbytes=4 * n * h * w * c + (4 if yt is not None else 0) * n * c + (n * ld if yq is not None else 0))
+        if f16:
+            self._round_f16(yt, yt)
         self._finish_i8(out, fused)
+
+    def _round_f16(self, src, dst) -> None:
+        """dst = f32(f16(src)) on the device (the reference's .astype(float16))."""
+        lib, numel = self.lib, src.numel()
+        self._add("round_f16", lambda s: L.check(lib.mr_round_f16_f32(src.data_ptr(), numel, dst.data_ptr(), s),
+                                                 "mr_round_f16_f32"), nbytes=8 * numel)
+
+    def _emit_cast(self, op: ir.Op) -> None:
+        """mira/ops.py:405-406 between f32 and f16.  To f16: round (in place on the input
+        buffer when the cast is a graph input's only use, see _plan); to f32: the f16
+        values are already stored as f32, so the result shares the input's buffers."""
+        x = self._src(op.inputs[0])
+        r = op.result
+        if op in self.input_casts or r.type.dtype == "f32" or op.inputs[0].type.dtype == "f16":
+            self.dv[r] = DevValue(r, nhwc=x.nhwc, f32=x.f32, i8=x.i8)
+            self._finish_i8(self.dv[r], None)
+            return
+        out = self._new_dv(r)
+        if out.f32 is None:
+            out.f32 = _t().empty_like(x.f32)
+        self._round_f16(x.f32, out.f32)
+        self._finish_i8(out, None)
 
     def _emit_reshape(self, op: ir.Op) -> None:
         torch = _t()

@@ -48,7 +48,9 @@ def test_invalid_arguments_are_rejected_before_any_launch():
 
 def test_fused_stem_declines_what_it_cannot_fuse():
     """mr_qconv2d_maxpool answers MR_EUNSUPPORTED (3) for pool shapes without a kernel and
-    for epilogues the pool does not commute with; the caller then runs conv and pool apart."""
+    for epilogues the pool does not commute with (a mul is accepted only per channel or
+    scalar: the caller guarantees its operand positive); the caller then runs conv and pool
+    apart."""
     lib = L.load()
     g = L.ConvGeom(n=1, h=224, w=224, c=3, c_pad=4, o=64, oh=112, ow=112, kh=7, kw=7, sh=2, sw=2, ph=3, pw=3,
                    dh=1, dw=1)
@@ -60,7 +62,7 @@ def test_fused_stem_declines_what_it_cannot_fuse():
     inf = float("-inf")
     assert lib.mr_qconv2d_maxpool(x, C.byref(g), b, 256, 64, C.byref(e), 3, 3, 1, 1, inf, 38, 38, None) == 3
     assert b"no kernel" in lib.mr_last_error()
-    for fn, mode, swapped in (("mul", L.BC_COL, 0), ("add", L.BC_FULL, 0), ("add", L.BC_ROW, 0),
+    for fn, mode, swapped in (("mul", L.BC_ROW, 0), ("add", L.BC_FULL, 0), ("add", L.BC_ROW, 0),
                               ("sub", L.BC_SCALAR, 1), ("div", L.BC_SCALAR, 0)):
         e.steps[0].fn, e.steps[0].mode, e.steps[0].swapped = L.EPI_FN[fn], mode, swapped
         assert lib.mr_qconv2d_maxpool(x, C.byref(g), b, 256, 64, C.byref(e), 3, 2, 1, 1, inf, 56, 56, None) == 3

@@ -150,6 +150,59 @@ def test_qmatmul_rejects_bad_shapes(lib):
     assert lib.mr_qmatmul(a.data_ptr(), 16, b.data_ptr(), 60, 32, 4, 8, 16, C.byref(e), stream()) == 1
 
 
+# ---------------------------------------------------------------- f16 results (values stored as f32)
+
+def test_round_f16_matches_numpy(lib):
+    """mr_round_f16_f32 == NumPy's astype(float16) back to f32: ties to even, f16
+    subnormals, overflow to inf, signed zeros, inf and NaN."""
+    torch = _torch()
+    tiny = np.float32(2.0 ** -24)                  # smallest f16 subnormal
+    special = np.array([0.0, -0.0, 1.0, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 65504.0, 65519.99, 65520.0, 7e4,
+                        -7e4, tiny, tiny / 2, tiny * 0.5001, tiny * 1.5, 3.1e-5, 6.1e-5, np.inf, -np.inf, np.nan,
+                        1e-30, -1e-30, 2049.0, 2051.0], np.float32)
+    rng = np.random.default_rng(0)
+    x = np.concatenate([special, rng.standard_normal(100_003).astype(np.float32) * 100,
+                        rng.standard_normal(1000).astype(np.float32) * 1e-5])
+    xd, y = T(x), empty(x.shape, torch.float32)
+    L.check(lib.mr_round_f16_f32(xd.data_ptr(), x.size, y.data_ptr(), stream()), "round")
+    L.check(lib.mr_round_f16_f32(xd.data_ptr(), x.size, xd.data_ptr(), stream()), "round in place")
+    sync()
+    want = x.astype(np.float16).astype(np.float32)
+    assert bits_equal(y.cpu().numpy(), want) and bits_equal(xd.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("M,K,N", [(300, 512, 1000), (4, 256, 96)])     # tiled and weight-stream kernels
+def test_qmatmul_f16_result(lib, M, K, N):
+    """A q-op of dtype f16 (mira/ops.py:620): the f32 epilogue result rounded to f16, and the
+    int8 copy quantized from the rounded value; large outputs overflow to inf as in NumPy."""
+    torch = _torch()
+    rng = np.random.default_rng(M + N)
+    x = (rng.standard_normal((M, K)) * 30).astype(np.float16).astype(np.float32)
+    w = rng.standard_normal((K, N)).astype(np.float32)
+    q, ws = G.quantize_array(w, 1)
+    ws = ws * np.float32(40.0)                    # push some results past the f16 range
+    xs = float(np.abs(x).max()) / 127
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float16)
+    attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f16", "epilogue": (("add", 1, False),)}
+    want = G.qmatmul([x.astype(np.float16), bias], attrs)
+    assert want.dtype == np.float16 and np.isinf(want).any()
+    lda = pack.row_stride_for(K)
+    xq = empty((M, lda), torch.int8)
+    L.check(lib.mr_quantize_rows(T(x).data_ptr(), M, K, K, xq.data_ptr(), lda, xs, stream()), "q")
+    bl = pack.pack_matmul(q)
+    b, scale, bt = T(pack.device_weights(bl)), T(pack.combined_scale(xs, ws)), T(bias.astype(np.float32))
+    y = empty((M, N), torch.float32)
+    ldq = pack.row_stride_for(N)
+    yq = empty((M, ldq), torch.int8)
+    e = epilogue([("add", L.BC_COL, bt, 0, False)], scale=scale, out_f32=y, ldo=N, out_i8=yq, ldq=ldq, xs=3.0)
+    e.flags = L.EPI_OUT_F16
+    L.check(lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), bl.shape[1], bl.shape[0], M, N, K, C.byref(e), stream()),
+            "mr_qmatmul")
+    sync()
+    assert bits_equal(y.cpu().numpy(), want.astype(np.float32))
+    assert bits_equal(yq.cpu().numpy()[:, :N], G.quantize_activation(want, 3.0).astype(np.int8))
+
+
 # ---------------------------------------------------------------- weight-only int8 matmul (f32 activations)
 
 # The f32 sums run in another order than NumPy's BLAS, so parity is a tolerance:

@@ -114,6 +114,32 @@ def test_onnx_layout_batch2(builder):
     assert [s.device for s in runner.segments] == ["rocm"]
 
 
+@pytest.mark.parametrize("builder,shape,dist", [(models.resnet18, (2, 3, 224, 224), "uniform"),
+                                                (models.mobilenet_v2, (2, 3, 224, 224), "uniform"),
+                                                (models.mlp_50m, (8, 4096), "normal")])
+def test_f16_graph(builder, shape, dist):
+    """The reference's default precision for accelerator targets ("auto" -> f16,
+    mira/compiler.py:293-294; lowering mira/passes.py:206-253): every op computes in f32 and
+    rounds its result to f16 as the reference's ops do.  Every op on rocm (the interface
+    casts included); accumulators and outputs bit-exact against the oracle on the same
+    f16 graph."""
+    gen = models.image_batch if dist == "uniform" else models.normal_batch
+    g = builder(batch=shape[0], seed=0)
+    passes.optimize(g, precision="f16")
+    quantize_w8a8(g, peaks=calibration_peaks(g, [{"x": gen(shape, s)} for s in (11, 12)]))
+    assert sum(op.result.type.dtype == "f16" for op in g.compute_ops()) > 3
+    runner = _compare(g, {"x": gen(shape, 5)}, fallback=False)
+    assert [s.device for s in runner.segments] == ["rocm"]
+
+
+def test_f16_mlp_mira_with_softmax_fallback():
+    g = models.mlp_mira(batch=64)
+    passes.optimize(g, precision="f16")
+    quantize_w8a8(g, [{"x": models.normal_batch((64, 784), s)} for s in (2, 3)])
+    runner = _compare(g, {"x": models.normal_batch((64, 784), 1)})
+    assert "rocm" in [s.device for s in runner.segments]
+
+
 def test_mlp50m_batch8():
     g, _ = _quantized(models.mlp_50m, 8, 0, (2, 3))
     _compare(g, {"x": models.normal_batch((8, 4096), 1)}, fallback=False)
@@ -140,13 +166,15 @@ def test_mlp50m_batch4096_rows():
     _rows_match_small_run(models.mlp_50m, 4096, [0, 1234, 4095], 0, (2, 3), "normal", (4096,))
 
 
-@pytest.mark.parametrize("bn_epilogue", [False, True])
-def test_resnet18_batch2_fused_stem(bn_epilogue):
+@pytest.mark.parametrize("bn_epilogue,precision", [(False, None), (True, None), (False, "f16")])
+def test_resnet18_batch2_fused_stem(bn_epilogue, precision):
     """Without debug accumulators the stem conv, pad and max pool run as one kernel, also with
     the ONNX importer's BatchNorm mul (a positive per-channel constant keeps the epilogue
-    monotone, so pooling the accumulators first is exact)."""
-    g, _ = _quantized(lambda batch, seed: models.resnet18(batch=batch, seed=seed, bn_epilogue=bn_epilogue), 2, 0,
-                      (11, 12), dist="uniform")
+    monotone, so pooling the accumulators first is exact) and in the f16 graph (rounding to
+    f16 is monotone too)."""
+    g = models.resnet18(batch=2, seed=0, bn_epilogue=bn_epilogue)
+    passes.optimize(g, precision=precision)
+    quantize_w8a8(g, peaks=calibration_peaks(g, [{"x": models.image_batch((2, 3, 224, 224), s)} for s in (11, 12)]))
     runner = compile_graph(g, RocmTarget())
     exe = runner.segments[0].executable
     assert exe.kernel_counts.get("qconv2d_maxpool") == 1 and "maxpool2d" not in exe.kernel_counts
