@@ -129,6 +129,25 @@ def test_weight_only_rules():
     assert sq.producer.kind == shared.producer.kind == small.producer.kind == "const"
 
 
+def test_to_f16_lowering():
+    """mira/passes.py:206-253: a cast to f16 after each f32 input, f16 constants and results,
+    a cast back to f32 before each f32 output; float casts inside the graph disappear."""
+    g = Graph("t", [], [], [])
+    x = g.input("x", (4, 16))
+    w = g.const(np.full((16, 8), 0.1, np.float32))
+    h = g.add("cast", [g.add("relu", [g.add("matmul", [x, w])])], {"dtype": "f32"})
+    g.outputs = [g.add("add", [h, g.const(np.float32(1e-4))])]
+    passes.optimize(g, precision="f16", fuse=False)
+    ops = g.compute_ops()
+    assert ops[0].kind == "cast" and ops[0].inputs[0] is x and ops[0].result.type.dtype == "f16"
+    assert [op.kind for op in ops] == ["cast", "matmul", "relu", "add", "cast"]
+    assert all(op.result.type.dtype == "f16" for op in ops[:-1])
+    assert g.outputs[0].producer is ops[-1] and g.outputs[0].type.dtype == "f32"
+    consts = [op.attrs["value"] for op in g.ops if op.is_const]
+    assert all(c.dtype == np.float16 for c in consts)
+    assert any(c.size == 1 and c.item() == np.float16(1e-4) for c in consts)
+
+
 def test_check_decisions_weight_only():
     """Weight-only int8 matmuls run on rocm for decode shapes (up to 64 rows); larger
     batches, and matmuls whose weight is not a dequantize constant, stay on the CPU."""
