@@ -243,6 +243,7 @@ int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, in
 constexpr int EF_GENERIC = 0, EF_FIXED = 1, EF_SPEC = 0x100;
 constexpr int SF_COL = 1, SF_FULL = 2, SF_LO = 4, SF_HI = 8, SF_F32 = 16, SF_I8 = 32;
 constexpr int SF_MUL = 64;   // no compiled form has it: a leading mul runs the EF_FIXED path
+constexpr int SF_F16 = 128;  // results rounded to f16 (compiled for the ResNet-style forms only)
 // the forms with compiled kernels: bias+ReLU -> int8; bias+residual+ReLU -> f32
 // and/or int8; bias -> f32 (ResNet blocks, downsample and fc layers, MLPs)
 constexpr int SPEC_RELU_I8 = SF_COL | SF_LO | SF_I8;
@@ -262,11 +263,12 @@ constexpr int SPEC_BIAS_RES_F32_I8 = SF_COL | SF_FULL | SF_F32 | SF_I8;
 // form without an int32 accumulator output, every output and operand row
 // 16-byte (f32) / 4-byte (int8) aligned.
 inline int spec_form(const EpiDev& e) {
-  if (!e.fixed || e.out_acc || e.f16) return -1;
+  if (!e.fixed || e.out_acc) return -1;
   auto al = [](const void* p, int64_t ld, int bytes) {
     return reinterpret_cast<uintptr_t>(p) % bytes == 0 && ld % 4 == 0;
   };
   int f = 0;
+  if (e.f16) f |= SF_F16;
   if (e.f_mul) f |= SF_MUL;
   if (e.f_col) f |= SF_COL;
   if (e.f_full) {

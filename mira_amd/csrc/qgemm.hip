@@ -556,7 +556,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
     if constexpr (EF >= EF_SPEC) {
       if (n0 + BN <= g.N) {
         constexpr bool S_COL = EF & SF_COL, S_FULL = EF & SF_FULL, S_LO = EF & SF_LO, S_HI = EF & SF_HI;
-        constexpr bool S_F32 = EF & SF_F32, S_I8 = EF & SF_I8;
+        constexpr bool S_F32 = EF & SF_F32, S_I8 = EF & SF_I8, S_F16 = EF & SF_F16;
         constexpr int NR = EP_ROWS / RSTEP;
         static_assert(EP_ROWS % RSTEP == 0, "epilogue rows per thread");
         // rows in flight at once: all of them, or 4 when each also holds a residual
@@ -600,6 +600,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
             if constexpr (S_FULL) t = __fadd_rn(t, o[c]);
             if constexpr (S_LO) t = max_bound(t, cols.lo, cols.lo_nan);
             if constexpr (S_HI) t = min_bound(t, cols.hi, cols.hi_nan);
+            if constexpr (S_F16) t = round_f16(t);
             y[k][c] = t;
           }
         }
@@ -658,6 +659,10 @@ static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
       case SPEC_RES_F32_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_F32_I8); return;
       case SPEC_RES_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_I8); return;
       case SPEC_RES_F32: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_F32); return;
+      // the same ResNet block forms in f16 graphs
+      case SPEC_RELU_I8 | SF_F16: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RELU_I8 | SF_F16); return;
+      case SPEC_RES_F32_I8 | SF_F16: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_F32_I8 | SF_F16); return;
+      case SPEC_BIAS_F32 | SF_F16: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_F32 | SF_F16); return;
       default: break;
     }
   }

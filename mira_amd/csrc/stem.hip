@@ -242,6 +242,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
             if constexpr ((EF & SF_COL) != 0) y = __fadd_rn(y, colv[j]);
             if constexpr ((EF & SF_LO) != 0) y = y > lo ? y : lo;
             if constexpr ((EF & SF_HI) != 0) y = y < hi ? y : hi;
+            if constexpr ((EF & SF_F16) != 0) y = round_f16(y);
             if constexpr ((EF & SF_F32) != 0) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rf, of, 0, 0);
             if constexpr ((EF & SF_I8) != 0) {
               const float tq = rintf(static_cast<float>(__dmul_rn(static_cast<double>(y), e.out_rxs)));
@@ -330,6 +331,9 @@ template <int KS, int RBV, int PK>
 static void launch_stem(dim3 grid, hipStream_t s, const StemArgs& a, const EpiDev& e) {
   if (spec_form(e) == SPEC_RELU_F32_I8)
     hipLaunchKernelGGL((stem_pool_kernel<KS, RBV, PK, EF_SPEC | SPEC_RELU_F32_I8>), grid, dim3(256), 0, s, a, e);
+  else if (spec_form(e) == (SPEC_RELU_F32_I8 | SF_F16))
+    hipLaunchKernelGGL((stem_pool_kernel<KS, RBV, PK, EF_SPEC | SPEC_RELU_F32_I8 | SF_F16>), grid, dim3(256), 0, s, a,
+                       e);
   else if (e.fixed)
     hipLaunchKernelGGL((stem_pool_kernel<KS, RBV, PK, EF_FIXED>), grid, dim3(256), 0, s, a, e);
   else

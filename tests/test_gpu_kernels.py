@@ -386,11 +386,16 @@ FORM_CONV_CASES = [
 ]
 
 
-@pytest.mark.parametrize("form", list(FORMS))
+# forms of an f16 graph (results rounded to f16; operands are f16 values)
+F16_FORMS = ["relu_i8_f16", "res_f32_i8_f16", "bias_f32_f16", "bias_relu6_f32_f16"]
+
+
+@pytest.mark.parametrize("form", list(FORMS) + F16_FORMS)
 @pytest.mark.parametrize("n,c,h,w,o,k,s,p,d", FORM_CONV_CASES)
 def test_qconv2d_epilogue_forms(lib, form, n, c, h, w, o, k, s, p, d):
     torch = _torch()
-    steps, want_f32, want_i8 = FORMS[form]
+    f16 = form.endswith("_f16")
+    steps, want_f32, want_i8 = FORMS[form[:-4] if f16 else form]
     rng = np.random.default_rng(n * 1000 + c * 10 + k + 7)
     x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
     wt = rng.standard_normal((o, c, k, k)).astype(np.float32)
@@ -402,8 +407,10 @@ def test_qconv2d_epilogue_forms(lib, form, n, c, h, w, o, k, s, p, d):
     res = rng.standard_normal((n, o, oh, ow)).astype(np.float32)
     zero, six = np.array(0, np.float32), np.array(6, np.float32)
     bn = rng.uniform(-1.5, 1.5, (o, 1, 1)).astype(np.float32)
-    attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "stride": (s, s), "padding": (p, p),
-             "dilation": (d, d), "epilogue": steps}
+    if f16:     # an f16 graph's tensors hold f16 values
+        x, bias, res, bn = (a.astype(np.float16).astype(np.float32) for a in (x, bias, res, bn))
+    attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f16" if f16 else "f32", "stride": (s, s),
+             "padding": (p, p), "dilation": (d, d), "epilogue": steps}
     want = G.qconv2d([x, bias, res, zero, six, bn], attrs)
     next_xs = float(np.abs(want[np.isfinite(want)]).max()) / 127 or 1.0
     cp = pack.c_pad_for(c)
@@ -423,12 +430,13 @@ def test_qconv2d_epilogue_forms(lib, form, n, c, h, w, o, k, s, p, d):
     yq = empty((M, ocp), torch.int8) if want_i8 else None
     e = epilogue(dev_steps, scale=scale, out_f32=y, ldo=o if want_f32 else 0, out_i8=yq, ldq=ocp if want_i8 else 0,
                  xs=next_xs)
+    e.flags = L.EPI_OUT_F16 if f16 else 0
     L.check(lib.mr_qconv2d(xq.data_ptr(), C.byref(g), b.data_ptr(), bl.shape[1], bl.shape[0], C.byref(e), stream()),
             "mr_qconv2d")
     sync()
     to_nhwc = lambda a: a.transpose(0, 2, 3, 1).reshape(M, o)
     if want_f32:
-        assert bits_equal(y.cpu().numpy(), to_nhwc(want))
+        assert bits_equal(y.cpu().numpy(), to_nhwc(want).astype(np.float32))
     if want_i8:
         assert bits_equal(yq.cpu().numpy()[:, :o], to_nhwc(G.quantize_activation(want, next_xs)).astype(np.int8))
 
