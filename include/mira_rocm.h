@@ -138,6 +138,12 @@ int mr_quantize_rows(const float* x, int64_t rows, int64_t cols, int64_t ldx,
 int mr_quantize_nchw_nhwc(const float* x, int32_t n, int32_t c, int32_t h, int32_t w,
                           int8_t* q, int32_t c_pad, float xs, void* stream);
 
+/* The same after the f32 -> f16 cast that MIRA's f16 lowering puts on each
+ * graph input (mira/passes.py:220-223, mira/ops.py:405-406): quantizes
+ * f32(f16(x)), for an input whose only use is that cast. */
+int mr_quantize_f16_nchw_nhwc(const float* x, int32_t n, int32_t c, int32_t h, int32_t w,
+                              int8_t* q, int32_t c_pad, float xs, void* stream);
+
 /* ---- K2/K3: int8 GEMM with fused dequant/epilogue/requant -------------- */
 
 /* Replaces mira/ops.py:616-620 _qmatmul_ref (after quantize_activation):

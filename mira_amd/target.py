@@ -377,9 +377,13 @@ class RocmExecutable:
         lib = self.lib
         stage = torch.empty(v.type.shape, dtype=torch.float32, device=self.dev)
         self.staging[v] = stage
-        if any(op.inputs[0] is v for op in self.input_casts):
-            self._round_f16(stage, stage)
         d = self._new_dv(v, with_i8=True)
+        cast16 = any(op.inputs[0] is v for op in self.input_casts)
+        # an image that only feeds q-ops is quantized straight from its f16 rounding
+        fused16 = cast16 and d.nhwc and d.f32 is None
+        if cast16 and not fused16:
+            self._round_f16(stage, stage)
+        quant_nchw = lib.mr_quantize_f16_nchw_nhwc if fused16 else lib.mr_quantize_nchw_nhwc
         if d.nhwc:
             n, c, h, w = v.type.shape
             if d.f32 is not None:
@@ -389,7 +393,7 @@ class RocmExecutable:
                           nbytes=8 * n * c * h * w)
             for xs, (q, cp) in d.i8.items():
                 self._add("input", lambda s, q=q, cp=cp, xs=xs: L.check(
-                    lib.mr_quantize_nchw_nhwc(stage.data_ptr(), n, c, h, w, q.data_ptr(), cp, xs, s),
+                    quant_nchw(stage.data_ptr(), n, c, h, w, q.data_ptr(), cp, xs, s),
                     "mr_quantize_nchw_nhwc"), nbytes=4 * n * c * h * w + n * h * w * cp)
         else:
             if d.f32 is not None:

@@ -41,10 +41,12 @@ def test_quantize_rows(lib, rows, cols, xs):
     assert not got[:, cols:].any()
 
 
+@pytest.mark.parametrize("f16", [False, True])
 @pytest.mark.parametrize("n,c,h,w,ties", [(3, 3, 21, 19, False), (2, 20, 5, 6, False), (1, 1, 28, 28, False),
                                            (2, 3, 8, 12, True), (2, 20, 6, 6, True), (3, 4, 7, 4, False)])
-def test_quantize_nchw_nhwc(lib, n, c, h, w, ties):
-    """Both kernels: any pixel count, and four pixels per thread when h*w % 4 == 0."""
+def test_quantize_nchw_nhwc(lib, n, c, h, w, ties, f16):
+    """Both kernels: any pixel count, and four pixels per thread when h*w % 4 == 0; with f16,
+    the input's f32 -> f16 cast fused in front (mr_quantize_f16_nchw_nhwc)."""
     torch = _torch()
     rng = np.random.default_rng(c + h)
     x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
@@ -55,10 +57,11 @@ def test_quantize_nchw_nhwc(lib, n, c, h, w, ties):
     cp = pack.c_pad_for(c)
     q = empty((n, h, w, cp), torch.int8)
     xs = float(np.float32(1 / 127))
-    L.check(lib.mr_quantize_nchw_nhwc(T(x).data_ptr(), n, c, h, w, q.data_ptr(), cp, xs, stream()), "q")
+    fn = lib.mr_quantize_f16_nchw_nhwc if f16 else lib.mr_quantize_nchw_nhwc
+    L.check(fn(T(x).data_ptr(), n, c, h, w, q.data_ptr(), cp, xs, stream()), "q")
     sync()
     got = q.cpu().numpy()
-    want = G.quantize_activation(x, xs).astype(np.int8).transpose(0, 2, 3, 1)
+    want = G.quantize_activation(x.astype(np.float16) if f16 else x, xs).astype(np.int8).transpose(0, 2, 3, 1)
     assert bits_equal(got[..., :c], want) and not got[..., c:].any()
 
 
