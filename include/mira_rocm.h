@@ -160,15 +160,17 @@ int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int
  * (mira/quantize.py:45-68), mira/ops.py:217-219 _matmul_ref fed by the
  * dequantize constant of mira/ops.py:581-589:
  * y[M,N] = x[M,K] (f32, row stride ldx) @ W, W[k][n] = fl32(q[k][n] *
- * w_scale[n]) with q packed as B[n_pad][k_pad] (B[n][k] = q[k][n], stored
+ * w_scale[n]) (rounded on to f16 when w_f16 != 0: a dequantize of dtype
+ * f16) with q packed as B[n_pad][k_pad] (B[n][k] = q[k][n], stored
  * K-step-major as for mr_qmatmul), f32 multiply-adds, then the epilogue (its
  * scale must be NULL and it writes no int32 accumulators).  The weights are
  * streamed once per block of 8 rows, so it is meant for decode shapes
  * (M <= 524280).  ldx >= K, x and b 16-byte aligned.  The sums run in another order than
  * NumPy's, so the result matches to f32 rounding (relative 1e-5), not bit
  * for bit. */
-int mr_w8_matmul_f32(const float* x, int64_t ldx, const int8_t* b, const float* w_scale, int64_t k_pad,
-                     int64_t n_pad, int64_t M, int64_t N, int64_t K, const mr_epilogue* epi, void* stream);
+int mr_w8_matmul_f32(const float* x, int64_t ldx, const int8_t* b, const float* w_scale, int32_t w_f16,
+                     int64_t k_pad, int64_t n_pad, int64_t M, int64_t N, int64_t K, const mr_epilogue* epi,
+                     void* stream);
 
 /* Replaces mira/ops.py:630-634 _qconv2d_ref (after quantize_activation):
  * implicit-GEMM convolution of NHWC int8 x with packed weights

@@ -61,7 +61,7 @@ _SIGS = {
     "mr_quantize_nchw_nhwc": ([_p, _i32, _i32, _i32, _i32, _p, _i32, _f32, _p], C.c_int),
     "mr_quantize_f16_nchw_nhwc": ([_p, _i32, _i32, _i32, _i32, _p, _i32, _f32, _p], C.c_int),
     "mr_qmatmul": ([_p, _i64, _p, _i64, _i64, _i64, _i64, _i64, C.POINTER(Epilogue), _p], C.c_int),
-    "mr_w8_matmul_f32": ([_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, C.POINTER(Epilogue), _p], C.c_int),
+    "mr_w8_matmul_f32": ([_p, _i64, _p, _p, _i32, _i64, _i64, _i64, _i64, _i64, C.POINTER(Epilogue), _p], C.c_int),
     "mr_qconv2d": ([_p, C.POINTER(ConvGeom), _p, _i64, _i64, C.POINTER(Epilogue), _p], C.c_int),
     "mr_qconv2d_maxpool": ([_p, C.POINTER(ConvGeom), _p, _i64, _i64, C.POINTER(Epilogue), _i32, _i32, _i32, _i32,
                             _f32, _i32, _i32, _p], C.c_int),

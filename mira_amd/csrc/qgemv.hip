@@ -96,8 +96,8 @@ __global__ void __launch_bounds__(256) qgemv_kernel(const GemvArgs g, const EpiD
 // NumPy's BLAS order, so results agree to f32 rounding, not bit for bit.
 template <int MR>
 __global__ void __launch_bounds__(256) w8gemv_kernel(const float* __restrict__ x, const int64_t ldx,
-                                                      const float* __restrict__ wscale, const GemvArgs g,
-                                                      const EpiDev e) {
+                                                      const float* __restrict__ wscale, const int w_f16,
+                                                      const GemvArgs g, const EpiDev e) {
   const int lane = threadIdx.x & 63;
   const int lpc = g.lpc;
   const int sub = lane & (lpc - 1);
@@ -136,6 +136,12 @@ __global__ void __launch_bounds__(256) w8gemv_kernel(const float* __restrict__ x
 #pragma unroll
         for (int i = 0; i < 16; ++i)
           w[c][i] = __fmul_rn(static_cast<float>(static_cast<int8_t>(wq[c][i >> 2] >> (8 * (i & 3)))), s[c]);
+      if (w_f16) {   // f16 weights (a dequantize of dtype f16): the product rounded once more
+#pragma unroll
+        for (int c = 0; c < GEMV_CPW; ++c)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) w[c][i] = round_f16(w[c][i]);
+      }
       const int kv = min(16, static_cast<int>(g.lda) - k16 * 16);   // activation columns in this chunk
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
@@ -211,9 +217,9 @@ int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, in
 
 }  // namespace mr
 
-extern "C" int mr_w8_matmul_f32(const float* x, int64_t ldx, const int8_t* b, const float* w_scale, int64_t k_pad,
-                                int64_t n_pad, int64_t M, int64_t N, int64_t K, const mr_epilogue* epi,
-                                void* stream) {
+extern "C" int mr_w8_matmul_f32(const float* x, int64_t ldx, const int8_t* b, const float* w_scale, int32_t w_f16,
+                                int64_t k_pad, int64_t n_pad, int64_t M, int64_t N, int64_t K,
+                                const mr_epilogue* epi, void* stream) {
   MR_REQUIRE(x && b && w_scale, "mr_w8_matmul_f32: NULL operand");
   MR_REQUIRE(M >= 0 && M <= 8 * 65535 && N > 0 && K > 0, "mr_w8_matmul_f32: M=%lld, N=%lld, K=%lld",
              (long long)M, (long long)N, (long long)K);
@@ -246,13 +252,13 @@ extern "C" int mr_w8_matmul_f32(const float* x, int64_t ldx, const int8_t* b, co
   const dim3 grid(static_cast<unsigned>((groups * lpc + 255) / 256), static_cast<unsigned>((M + mr_blk - 1) / mr_blk));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (mr_blk == 1)
-    hipLaunchKernelGGL(mr::w8gemv_kernel<1>, grid, dim3(256), 0, s, x, ldx, w_scale, g, e);
+    hipLaunchKernelGGL(mr::w8gemv_kernel<1>, grid, dim3(256), 0, s, x, ldx, w_scale, w_f16, g, e);
   else if (mr_blk == 2)
-    hipLaunchKernelGGL(mr::w8gemv_kernel<2>, grid, dim3(256), 0, s, x, ldx, w_scale, g, e);
+    hipLaunchKernelGGL(mr::w8gemv_kernel<2>, grid, dim3(256), 0, s, x, ldx, w_scale, w_f16, g, e);
   else if (mr_blk == 4)
-    hipLaunchKernelGGL(mr::w8gemv_kernel<4>, grid, dim3(256), 0, s, x, ldx, w_scale, g, e);
+    hipLaunchKernelGGL(mr::w8gemv_kernel<4>, grid, dim3(256), 0, s, x, ldx, w_scale, w_f16, g, e);
   else
-    hipLaunchKernelGGL(mr::w8gemv_kernel<8>, grid, dim3(256), 0, s, x, ldx, w_scale, g, e);
+    hipLaunchKernelGGL(mr::w8gemv_kernel<8>, grid, dim3(256), 0, s, x, ldx, w_scale, w_f16, g, e);
   MR_LAUNCH_CHECK("w8gemv");
   return MR_OK;
 }

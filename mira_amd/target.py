@@ -578,12 +578,14 @@ class RocmExecutable:
         bl = pack.pack_matmul(q)
         b = self._upload(pack.device_weights(bl))
         ws = self._upload(np.asarray(w["scale"], np.float32).reshape(-1))
+        w16 = int(w["dtype"] == "f16")        # mira/ops.py:584 casts the dequantized weight to its dtype
         out = self._new_dv(op.result)
         e, fused = self._epilogue(op, out, False, 2, None)
         M = out.rows
         lib, kp, npad, xf = self.lib, bl.shape[1], bl.shape[0], x.f32
         self._add("w8matmul", lambda s: L.check(
-            lib.mr_w8_matmul_f32(xf.data_ptr(), K, b.data_ptr(), ws.data_ptr(), kp, npad, M, N, K, C.byref(e), s),
+            lib.mr_w8_matmul_f32(xf.data_ptr(), K, b.data_ptr(), ws.data_ptr(), w16, kp, npad, M, N, K, C.byref(e),
+                                 s),
             "mr_w8_matmul_f32"), nbytes=4 * M * K + K * N + 4 * N + self._epi_bytes(e, M, N))
         self._finish_i8(out, fused)
 

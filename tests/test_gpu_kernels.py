@@ -214,7 +214,7 @@ def test_qmatmul_f16_result(lib, M, K, N):
 W8_TOL = 1e-5
 
 
-def _run_w8(lib, x, K, q, s, steps_np, next_xs=None):
+def _run_w8(lib, x, K, q, s, steps_np, next_xs=None, w16=False):
     """x: [M, ldx] f32 (columns >= K are ignored). Returns (y f32, y int8 or None)."""
     torch = _torch()
     M, ldx = x.shape
@@ -233,8 +233,8 @@ def _run_w8(lib, x, K, q, s, steps_np, next_xs=None):
     ldq = pack.row_stride_for(N)
     yq = empty((M, ldq), torch.int8) if next_xs else None
     e = epilogue(steps, out_f32=y, ldo=N, out_i8=yq, ldq=ldq, xs=next_xs or 1.0)
-    L.check(lib.mr_w8_matmul_f32(xd.data_ptr(), ldx, b.data_ptr(), ws.data_ptr(), bl.shape[1], bl.shape[0], M, N, K,
-                                 C.byref(e), stream()), "mr_w8_matmul_f32")
+    L.check(lib.mr_w8_matmul_f32(xd.data_ptr(), ldx, b.data_ptr(), ws.data_ptr(), int(w16), bl.shape[1], bl.shape[0],
+                                 M, N, K, C.byref(e), stream()), "mr_w8_matmul_f32")
     sync()
     return y.cpu().numpy(), (yq.cpu().numpy()[:, :N] if yq is not None else None)
 
@@ -256,6 +256,37 @@ def test_w8_matmul_bias_relu(lib, M, K, N, ldx):
     assert (y >= 0).all()
     # the requantized copy is the reference's quantize_activation of the kernel's own f32 result
     assert bits_equal(yq, G.quantize_activation(y, 0.02).astype(np.int8))
+
+
+def test_w8_matmul_f16_weights(lib):
+    """A dequantize of dtype f16 (mira/ops.py:584): the weights are fl16(fl32(q * scale)); with
+    f16 activations and an f16 result rounded after the epilogue."""
+    rng = np.random.default_rng(8)
+    M, K, N = 3, 512, 200
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    q = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    s = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    deq = G.dequantize({"q": q, "scale": s, "axis": 1, "dtype": "f16"})
+    assert deq.dtype == np.float16
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float16)
+    want = G.matmul([x, deq, bias], {"epilogue": (("add", 2, False),)})
+    torch = _torch()
+    bl = pack.pack_matmul(q)
+    y = empty((M, N), torch.float32)
+    bt = T(bias.astype(np.float32))
+    e = epilogue([("add", L.BC_COL, bt, 0, False)], out_f32=y, ldo=N)
+    e.flags = L.EPI_OUT_F16
+    xd, bd, sd = T(x.astype(np.float32)), T(pack.device_weights(bl)), T(s)     # alive until the kernel ran
+    L.check(lib.mr_w8_matmul_f32(xd.data_ptr(), K, bd.data_ptr(), sd.data_ptr(), 1, bl.shape[1], bl.shape[0], M, N, K,
+                                 C.byref(e), stream()), "w8")
+    sync()
+    got = y.cpu().numpy()
+    assert bits_equal(got, got.astype(np.float16).astype(np.float32))           # f16 values
+    bound = np.abs(x.astype(np.float64)) @ np.abs(deq.astype(np.float64)) + np.abs(bias)
+    # f32 summation order differences, then the f16 roundings may land one f16 ulp apart
+    # (2^-10 relative, 2^-24 absolute for subnormals)
+    assert np.all(np.abs(got - want.astype(np.float64)) <=
+                  W8_TOL * bound + 2.0 ** -10 * np.abs(want.astype(np.float64)) + 2.0 ** -24)
 
 
 def test_w8_matmul_row_blocks_and_operands(lib):
@@ -280,11 +311,11 @@ def test_w8_matmul_rejects_bad_arguments(lib):
     b = empty((32, 64), torch.int8)
     s = empty((8,), torch.float32)
     e = epilogue(out_f32=empty((4, 8), torch.float32), ldo=8)
-    assert lib.mr_w8_matmul_f32(x.data_ptr(), 15, b.data_ptr(), s.data_ptr(), 64, 32, 4, 8, 16, C.byref(e),
+    assert lib.mr_w8_matmul_f32(x.data_ptr(), 15, b.data_ptr(), s.data_ptr(), 0, 64, 32, 4, 8, 16, C.byref(e),
                                 stream()) == 1
     assert b"ldx" in lib.mr_last_error()
     e2 = epilogue(out_f32=empty((4, 8), torch.float32), ldo=8, scale=s)
-    assert lib.mr_w8_matmul_f32(x.data_ptr(), 16, b.data_ptr(), s.data_ptr(), 64, 32, 4, 8, 16, C.byref(e2),
+    assert lib.mr_w8_matmul_f32(x.data_ptr(), 16, b.data_ptr(), s.data_ptr(), 0, 64, 32, 4, 8, 16, C.byref(e2),
                                 stream()) == 1
 
 
