@@ -91,6 +91,17 @@ __device__ __forceinline__ void block_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// Barrier after LDS stores that other waves read next.  s_barrier does not
+// wait for the wave's own outstanding LDS operations, so the stores are first
+// drained (lgkmcnt 0; vmcnt and expcnt untouched): without this a wave can
+// read a row another wave has issued but not yet written.
+__device__ __forceinline__ void lds_store_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // vmcnt 63, expcnt 7, lgkmcnt 0
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 __device__ __forceinline__ void dma16(const void* src, int8_t* lds_dst) {
   __builtin_amdgcn_global_load_lds(src, (lds_void*)lds_dst, 16, 0, 0);
 }
@@ -552,7 +563,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
       for (int r = 0; r < 16; ++r)
         ep[(wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * EP_LD + wn * TN + j * 32 + (lane & 31)] =
             acc[pass * FN + j][r];
-    block_barrier();
+    lds_store_barrier();
     if constexpr (EF >= EF_SPEC) {
       if (n0 + BN <= g.N) {
         constexpr bool S_COL = EF & SF_COL, S_FULL = EF & SF_FULL, S_LO = EF & SF_LO, S_HI = EF & SF_HI;

@@ -84,6 +84,9 @@ class DevValue:
 # f16 where the reference casts it (.astype(float16)), so f16 results are bit-exact too.
 FLOAT_DTYPES = ("f32", "f16")
 
+# ops whose rank-4 operands and results are images, stored NHWC
+IMAGE_OPS = ("qconv2d", "conv2d", "maxpool2d", "pad", "reduce_mean")
+
 W8_MAX_ROWS = 64     # mr_w8_matmul_f32 streams the weights once per 8 rows: decode shapes only
 
 
@@ -230,6 +233,16 @@ class RocmExecutable:
         users = g.users()
         self.users = users
         self.consts = {op.result: op for op in g.ops if op.is_constant_like}
+        # rank-4 values that an image op reads or writes live NHWC on the device; other
+        # rank-4 values (attention heads [b, s, h, d], say) keep the graph's C order
+        self.images: set = set()
+        for op in g.ops:
+            if op.kind in IMAGE_OPS:
+                self.images.update(v for v in [*op.inputs, op.result] if v.type.rank == 4)
+        for _ in range(2):      # a cast's result shares its input's buffers, so their layouts agree
+            for op in g.ops:
+                if op.kind == "cast" and (op.result in self.images or op.inputs[0] in self.images):
+                    self.images.update((op.inputs[0], op.result))
         # which forms each value needs
         self.need_f32: set = set(g.outputs)
         self.need_i8: dict[ir.Value, list[float]] = {}
@@ -294,11 +307,12 @@ class RocmExecutable:
             if v in self.consts and v not in self.dv:
                 self._const_dv(v)
 
-    @staticmethod
-    def _i8_view(src: ir.Value, r: ir.Value) -> bool:
-        """Is the int8 copy of `r` (a reshape of `src`) the same bytes as src's? Only for
-        [n, c, 1, 1] <-> [n, c] (global average pooling into an fc layer): NHWC with 1x1
-        pixels is row-major [n, c], and both strides round c up to 16."""
+    def _i8_view(self, src: ir.Value, r: ir.Value) -> bool:
+        """Is the int8 copy of `r` (a reshape of `src`) the same bytes as src's? Only for an
+        [n, c, 1, 1] image <-> [n, c] (global average pooling into an fc layer): NHWC with
+        1x1 pixels is row-major [n, c], and both strides round c up to 16."""
+        if not ({src, r} & self.images):
+            return False
         a, b = tuple(src.type.shape), tuple(r.type.shape)
         if len(a) == 4 and len(b) == 2:
             a, b = b, a
@@ -357,7 +371,7 @@ class RocmExecutable:
         """Allocate v's f32 copy if anything reads it; int8 copies only for segment inputs
         (producers allocate the ones they write)."""
         torch = _t()
-        d = DevValue(v, nhwc=v.type.rank == 4)
+        d = DevValue(v, nhwc=v in self.images)
         if v in self.need_f32:
             s = v.type.shape
             shape = (s[0], s[2], s[3], s[1]) if d.nhwc else s
@@ -426,7 +440,7 @@ class RocmExecutable:
         if v in self.dv:
             return self.dv[v]
         a = self._const_value(v).astype(np.float32)
-        d = DevValue(v, nhwc=v.type.rank == 4)
+        d = DevValue(v, nhwc=v in self.images)
         d.f32 = self._upload(a.transpose(0, 2, 3, 1) if d.nhwc else a)
         self.dv[v] = d
         for xs in self.need_i8.get(v, []):
@@ -770,7 +784,7 @@ class RocmExecutable:
         torch = _t()
         src_v, r = op.inputs[0], op.result
         x = self._src(src_v)
-        d = DevValue(r, nhwc=r.type.rank == 4)
+        d = DevValue(r, nhwc=r in self.images)
         self.dv[r] = d
         if r not in self.need_f32 and r not in self.need_i8:
             return
