@@ -41,7 +41,11 @@ import os
 import sys
 import time
 
-import numpy as np
+# The CPU baseline's BLAS pool (set before NumPy loads it): the OpenMP thread count the
+# environment gives, else every host CPU up to 16.
+os.environ.setdefault("OPENBLAS_NUM_THREADS", os.environ.get("OMP_NUM_THREADS", str(min(os.cpu_count() or 1, 16))))
+
+import numpy as np  # noqa: E402
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
@@ -55,27 +59,26 @@ def log(*a):
 
 
 def build(batch: int, seed: int = 0, peaks=None):
-    from mira_amd import models, passes
-    from mira_amd.quantize import calibration_peaks, quantize_w8a8
-    g = models.resnet18(batch=batch, seed=seed)
-    passes.optimize(g)
+    """W8A8 ResNet-18 at `batch`, lowered as MIRA's compiler would; calibrated on two seeded
+    2-image batches of a same-weight twin (or the given peaks)."""
+    from harness import lowering as LW
+    from harness import models
+    g = LW.prepare(models.resnet18(batch=batch, seed=seed))
     if peaks is None:
-        twin = models.resnet18(batch=2, seed=seed)
-        passes.optimize(twin)
-        peaks = calibration_peaks(twin, [{"x": models.image_batch((2, 3, 224, 224), s)} for s in (11, 12)])
-    quantize_w8a8(g, peaks=peaks)
+        twin = LW.prepare(models.resnet18(batch=2, seed=seed))
+        peaks = LW.calibrate(twin, [{"x": models.image_batch((2, 3, 224, 224), s)} for s in (11, 12)])
+    LW.w8a8(g, peaks=peaks)
     return g, peaks
 
 
 def build_workload(name: str, batch: int):
     """A W8A8 graph of another configuration, calibrated as the parity tests do it (or,
     for mlp50m-int8, the weight-only rewrite, which needs no calibration)."""
-    from mira_amd import models, passes
-    from mira_amd.quantize import calibration_peaks, quantize_w8a8, quantize_weights
+    from harness import lowering as LW
+    from harness import models
     if name == "mlp50m-int8":
-        g = models.mlp_50m(batch=batch, seed=0)
-        passes.optimize(g)
-        quantize_weights(g)
+        g = LW.prepare(models.mlp_50m(batch=batch, seed=0))
+        LW.weight_only(g)
         return g, models.normal_batch(g.inputs[0].type.shape, 7)
     if name == "mlp50m":
         builder, cb, seeds, gen = models.mlp_50m, 8, (2, 3), models.normal_batch
@@ -90,13 +93,21 @@ def build_workload(name: str, batch: int):
     else:
         raise SystemExit(f"unknown workload {name!r}")
     precision = "f16" if name.endswith("-f16") else None
-    g = builder(batch=batch, seed=0)
-    passes.optimize(g, precision=precision)
-    twin = builder(batch=cb, seed=0)
-    passes.optimize(twin, precision=precision)
+    g = LW.prepare(builder(batch=batch, seed=0), precision)
+    twin = LW.prepare(builder(batch=cb, seed=0), precision)
     shape = twin.inputs[0].type.shape
-    quantize_w8a8(g, peaks=calibration_peaks(twin, [{"x": gen(shape, s)} for s in seeds]))
+    LW.w8a8(g, peaks=LW.calibrate(twin, [{"x": gen(shape, s)} for s in seeds]))
     return g, gen(g.inputs[0].type.shape, 7)
+
+
+def single_segment(g):
+    """Compile g on the rocm target; every op must run there (one segment)."""
+    from harness.runner import Runner
+    from mira_amd.target import RocmTarget
+    runner = Runner(g, RocmTarget())
+    if runner.devices != ["rocm"]:
+        raise SystemExit(f"{g.name}: expected one rocm segment, got {runner.devices}")
+    return runner.executables("rocm")[0]
 
 
 def time_launches(exe, stream, reps: int = 3) -> dict:
@@ -119,10 +130,13 @@ def time_launches(exe, stream, reps: int = 3) -> dict:
 
 
 def kernel_breakdown(exe, per_kind: dict) -> dict:
-    """Each launch kind against both rooflines: its algorithmic int8 ops in TOP/s against
-    the MFMA peak and its algorithmic HBM bytes in GB/s against the HBM peak.  `bound` is
-    the roofline that caps the kind at its arithmetic intensity (ops per byte above or
-    below the ridge point 5.0 POPS / 8 TB/s = 625)."""
+    """Each launch kind against both rooflines: its algorithmic int8 ops in TOP/s against the
+    MFMA peak and its algorithmic HBM bytes in GB/s against the HBM peak.  `bound` is the
+    peak the kind is priced against: MFMA for the int8 contractions, HBM for everything
+    else.  `launch_bounds` counts its launches by the side of the ridge point
+    (5.0 POPS / 8 TB/s = 625 ops per byte) each one falls on, and `roofline_frac` is the sum
+    over its launches of max(ops / MFMA peak, bytes / HBM peak) over the measured time."""
+    ridge = INT8_PEAK_TOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
     out = {}
     for name, ms in sorted(per_kind.items(), key=lambda kv: -kv[1]):
         cost = [(b, o) for k, b, o in exe.launch_cost if k == name]
@@ -134,8 +148,11 @@ def kernel_breakdown(exe, per_kind: dict) -> dict:
         if nbytes:
             row.update(gbs=round(nbytes / sec / 1e9, 1), hbm_frac=round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4))
         if nops or nbytes:
-            ridge = INT8_PEAK_TOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
-            row["bound"] = "mfma" if nbytes == 0 or nops / nbytes >= ridge else "hbm"
+            row["bound"] = "mfma" if nops else "hbm"
+            row["launch_bounds"] = {"mfma": sum(1 for b, o in cost if b == 0 or o / b >= ridge),
+                                    "hbm": sum(1 for b, o in cost if b and o / b < ridge)}
+            roof = sum(max(o / (INT8_PEAK_TOPS * 1e12), b / (HBM_PEAK_GBS * 1e9)) for b, o in cost)
+            row["roofline_frac"] = round(roof / sec, 4) if sec else None
         out[name] = row
     return out
 
@@ -145,16 +162,13 @@ def per_launch(args) -> int:
     algorithmic ops and bytes, and the fraction of its roofline time it reaches --
     roofline time = max(ops / 5.0 POPS, bytes / 8 TB/s)."""
     import torch
-    from mira_amd import models
-    from mira_amd.compiler import compile_graph
-    from mira_amd.target import RocmTarget
+    from harness import models
     if args.workload == "resnet18":
         g, _ = build(args.batch)
         x = models.image_batch((args.batch, 3, 224, 224), 7)
     else:
         g, x = build_workload(args.workload, args.batch)
-    runner = compile_graph(g, RocmTarget())
-    exe = runner.segments[0].executable
+    exe = single_segment(g)
     exe.upload({g.inputs[0]: x})
     stream = torch.cuda.current_stream()
     handle = stream.cuda_stream
@@ -189,14 +203,8 @@ def per_launch(args) -> int:
 
 def bench_workload(args) -> int:
     import torch
-    from mira_amd.compiler import compile_graph
-    from mira_amd.target import RocmTarget
     g, x = build_workload(args.workload, args.batch)
-    runner = compile_graph(g, RocmTarget())
-    if len(runner.segments) != 1 or runner.segments[0].device != "rocm":
-        raise SystemExit(f"{args.workload}: expected one rocm segment, got "
-                         f"{[s.device for s in runner.segments]}")
-    exe = runner.segments[0].executable
+    exe = single_segment(g)
     exe.upload({g.inputs[0]: x})
     stream = torch.cuda.current_stream()
     for _ in range(args.warmup):
@@ -219,24 +227,22 @@ def bench_workload(args) -> int:
 
 
 def bench_gpt(args) -> int:
-    """The character-level GPT decode step (L=2, d=64, vocab 65, context 128), W8A8 on the
-    QKV/out/MLP/vocab projections.  Attention, softmax, layernorm and the gelu projection
-    run on the host (MIRA's cpu target), which this package does not ship, so the timed
-    work is the device part of one decode step: every rocm segment's launch list, inputs
-    already in HBM.  Reported per step and per token (step / batch)."""
+    """Greedy decoding with the character-level GPT (L=2, d=64, 4 heads, vocab 65, context
+    T=272 = 16 + 256), W8A8 on the QKV/out/MLP/vocab projections, end to end: a seeded
+    16-token prompt per sequence, `--tokens` generated tokens, every step through the
+    runner -- the rocm segments (the projections) and the host segments (embedding gather,
+    the f32 attention, softmax, layernorm and the gelu projection, which the rocm target
+    leaves to the CPU), host/device copies included.  Also times the device part alone
+    (each rocm segment's launch list, inputs already in HBM)."""
     import torch
-    from mira_amd import models, passes
-    from mira_amd.partition import partition
-    from mira_amd.quantize import calibration_peaks, quantize_w8a8
+    from harness import lowering as LW
+    from harness import models
+    from harness.hosteval import HostTarget
+    from harness.runner import Runner
     from mira_amd.target import RocmTarget
     cfg = models.GPTConfig()
     params = models.gpt_params(cfg, 0)
-
-    def graph(batch):
-        g = models.gpt_decode_step(cfg, batch, params)
-        passes.optimize(g)
-        return g
-    twin = graph(2)
+    twin = LW.prepare(models.gpt_decode_step(cfg, 2, params))
     calib = []
     for s in (2, 3):
         r = np.random.default_rng(s)
@@ -244,71 +250,112 @@ def bench_gpt(args) -> int:
         caches = [(r.standard_normal((2, cfg.T, cfg.D)).astype(np.float32),
                    r.standard_normal((2, cfg.T, cfg.D)).astype(np.float32)) for _ in range(cfg.L)]
         calib.append(models.gpt_step_feeds(cfg, params, toks, 16, caches))
-    peaks = calibration_peaks(twin, calib)
-    g = graph(args.batch)
-    quantize_w8a8(g, peaks=peaks)
-    tgt = RocmTarget()
-    segs, _ = partition(g, tgt)
-    exes = [tgt.compile(s.graph) for s in segs if s.device == "rocm"]
+    peaks = LW.calibrate(twin, calib)
+    g = LW.prepare(models.gpt_decode_step(cfg, args.batch, params))
+    LW.w8a8(g, peaks=peaks)
+    runner = Runner(g, RocmTarget(), fallback=HostTarget())
+    prompt = np.random.default_rng(4).integers(0, cfg.V, (args.batch, 16)).astype(np.int32)
+    new = min(args.tokens, cfg.T - 16)
+    timings = {"rocm": 0.0, "cpu": 0.0}
+
+    def step(feeds):
+        out = runner.run(feeds)
+        for dev, sec in runner.timings:
+            timings[dev] = timings.get(dev, 0.0) + sec
+        return out
+    models.gpt_decode(step, cfg, params, prompt, 4)            # warm-up
+    torch.cuda.synchronize()
+    timings = {"rocm": 0.0, "cpu": 0.0}
+    t0 = time.perf_counter()
+    tokens, _ = models.gpt_decode(step, cfg, params, prompt, new)
+    total = time.perf_counter() - t0
+    steps = 16 + new - 1
+    log(f"gpt decode batch {args.batch}: {new} tokens in {total:.3f} s ({1e6 * total / steps:.0f} us/step)")
+
+    # device part alone: each rocm segment's launch list with its inputs resident
+    exes = runner.executables("rocm")
     for i, exe in enumerate(exes):
         exe.upload({v: models.normal_batch(v.type.shape, 100 + i).astype(np.float32) for v in exe.g.inputs})
     stream = torch.cuda.current_stream()
-
-    def step():
+    for _ in range(args.warmup):
         for exe in exes:
             exe.launch()
-    for _ in range(args.warmup):
-        step()
     torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for _ in range(args.steps):
-        step()
+        for exe in exes:
+            exe.launch()
     stop.record(stream)
     torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / args.steps
+    dev_ms = start.elapsed_time(stop) / args.steps
     kernels = {}
     for exe in exes:
         for kind, row in kernel_breakdown(exe, time_launches(exe, stream)).items():
             k = kernels.setdefault(kind, {"launches": 0, "ms": 0.0})
             k["launches"] += row["launches"]
             k["ms"] = round(k["ms"] + row["ms"], 4)
-    launches = sum(len(exe.launches) for exe in exes)
-    weight_bytes = sum(exe.const_bytes for exe in exes)
-    log(f"gpt decode batch {args.batch}: {len(exes)} rocm segments, {launches} launches, {ms * 1e3:.1f} us/step")
-    print(json.dumps({"workload": "gpt-decode", "batch": args.batch, "steps": args.steps, "warmup": args.warmup,
-                      "ms_per_step": round(ms, 4), "us_per_token": round(ms * 1e3 / args.batch, 3),
-                      "tokens_per_s": round(args.batch / (ms * 1e-3), 1), "rocm_segments": len(exes),
-                      "launches_per_step": launches, "device_constant_bytes": weight_bytes,
-                      "dtype": "int8", "data": "synthetic",
-                      "timed": "device part of one decode step (the host-side attention, softmax, layernorm "
-                               "and gelu projection are not included)",
-                      "kernels": kernels}), flush=True)
+    print(json.dumps({
+        "workload": "gpt-decode", "batch": args.batch, "prompt_tokens": 16, "generated_tokens": new,
+        "decode_steps": steps, "seconds": round(total, 4),
+        "us_per_step": round(1e6 * total / steps, 1),
+        "us_per_token": round(1e6 * total / (new * args.batch), 3),
+        "tokens_per_s": round(new * args.batch / total, 1),
+        "split_s": {"rocm_segments": round(timings.get("rocm", 0.0), 4),
+                    "host_segments": round(timings.get("cpu", 0.0), 4),
+                    "host_feeds_and_argmax": round(total - sum(timings.values()), 4)},
+        "rocm_segments_per_step": len(exes), "launches_per_step": sum(len(e.launches) for e in exes),
+        "device_only_us_per_step": round(dev_ms * 1e3, 1),
+        "device_constant_bytes": sum(e.const_bytes for e in exes),
+        "dtype": "int8", "data": "synthetic",
+        "timed": "end-to-end greedy decode through the runner (host segments on NumPy, host/device copies "
+                 "included); device_only_us_per_step times the rocm launch lists alone",
+        "kernels": kernels}), flush=True)
     return 0
 
 
-def cpu_baseline(peaks, macs_per_image: int) -> dict:
-    """The golden model on a bounded 2-image sample: 1 warm-up + 3 timed runs, median."""
-    from oracle import golden as G
-    from mira_amd import models
+def _host_description() -> dict:
+    """CPU model, logical CPUs, NumPy version and the BLAS library the baseline runs on."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    blas = []
     try:
         from threadpoolctl import threadpool_info
-        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+        blas = [{k: p.get(k) for k in ("internal_api", "version", "num_threads", "architecture")}
+                for p in threadpool_info()]
     except Exception:
-        threads = os.cpu_count() or 1
+        pass
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "numpy": np.__version__, "blas": blas}
+
+
+def cpu_baseline(peaks, macs_per_image: int, runs: int = 5) -> dict:
+    """The golden model on a bounded 2-image sample of the same network and attrs: 1 warm-up,
+    then the median of `runs` timed runs."""
+    from oracle import golden as G
+    from harness import models
     g, _ = build(2, peaks=peaks)
     x = models.image_batch((2, 3, 224, 224), 7)
     G.run_graph(g, {"x": x})
     times = []
-    for _ in range(3):
+    for _ in range(runs):
         t0 = time.perf_counter()
         G.run_graph(g, {"x": x})
         times.append(time.perf_counter() - t0)
     t = float(np.median(times))
+    host = _host_description()
+    threads = max([b.get("num_threads") or 1 for b in host["blas"]] or [1])
     return {"value": round(2 * macs_per_image * 2 / t / 1e12, 6), "unit": "TOPS", "cores": int(threads),
-            "kind": "port", "ms_per_image": round(t / 2 * 1e3, 2),
-            "sample": "2 images of the same W8A8 ResNet-18 (same attrs), NumPy golden model "
-                      "(int64 matmul, per-tap f32 einsum convs), median of 3 after 1 warm-up"}
+            "kind": "port", "ms_per_image": round(t / 2 * 1e3, 2), "runs_s": [round(v, 3) for v in times],
+            "host": host,
+            "sample": f"2 images of the same W8A8 ResNet-18 (same attrs), NumPy golden model "
+                      f"(int64 matmul, per-tap f32 einsum convs through BLAS with {threads} threads), "
+                      f"median of {runs} after 1 warm-up"}
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qconv2d_resnet18_b256_traffic.txt")
@@ -422,6 +469,7 @@ def main() -> int:
     ap.add_argument("--workload", default="resnet18",
                     choices=["resnet18", "resnet18-onnx", "resnet18-f16", "mlp50m", "mlp50m-int8", "mobilenetv2",
                              "gpt-decode"])
+    ap.add_argument("--tokens", type=int, default=256, help="gpt-decode: tokens generated per sequence")
     ap.add_argument("--per-launch", action="store_true", help="per-launch time against each launch's roofline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true", help="run the plain copy used to scale counters")
@@ -449,16 +497,12 @@ def main() -> int:
         return bench_workload(args)
 
     import torch
-    from mira_amd import models
-    from mira_amd.compiler import compile_graph
-    from mira_amd.target import RocmTarget
+    from harness import models
 
     t0 = time.perf_counter()
     g, peaks = build(args.batch)
     macs = models.conv_macs(g)
-    runner = compile_graph(g, RocmTarget())
-    (seg,) = runner.segments
-    exe = seg.executable
+    exe = single_segment(g)
     log(f"compiled in {time.perf_counter() - t0:.1f}s: {exe.report()}")
     x = models.image_batch((args.batch, 3, 224, 224), 7)
     exe.upload({g.inputs[0]: x})
@@ -520,6 +564,9 @@ def main() -> int:
         "roofline": {"bound": "mfma", "kernel": "qconv2d implicit GEMM (19 convs; the stem conv runs fused with its max pool)",
                      "achieved": round(conv_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
                      "frac": round(conv_tops / INT8_PEAK_TOPS, 4), "traffic": measured_traffic(args.batch),
+                     "traffic_source": "HBM bytes per qconv2d launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE "
+                                       "(copy-calibrated) of this workload, committed in "
+                                       "profiles/qconv2d_resnet18_b256_traffic.txt; not measured in this run",
                      "algorithmic_bytes_per_launch": int(conv_alg_bytes),
                      "launches_per_step": n_conv, "ms_per_step": round(conv_ms, 4),
                      "us_per_launch": round(1e3 * conv_ms / max(1, n_conv), 2),

@@ -1,0 +1,171 @@
+"""Host (NumPy) evaluation of float graphs for the harness.
+
+Two uses, neither of which produces a result the rocm target returns:
+
+* calibration (`lowering.calibrate`): a float forward pass that records the
+  peak |x| of every q-op input, from which x_scale follows;
+* `HostTarget`: the benchmark's stand-in for MIRA's cpu target, the fallback
+  that runs the ops the rocm target rejects (the f32 attention, softmax,
+  layernorm and gelu of the GPT decode step).  The parity tests use the
+  oracle for that role instead.
+
+Convolutions run as one im2col GEMM (grouped ones tap by tap), so float
+results can differ from MIRA's per-tap einsum in the last bits; nothing here
+is compared bit for bit.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import numpy as np
+
+from .graph import DTYPES, conv_out
+
+
+def _f32(a) -> np.ndarray:
+    return np.asarray(a).astype(np.float32, copy=False)
+
+
+def _gelu(x):
+    return 0.5 * x * (1.0 + np.tanh(0.7978845608028654 * (x + 0.044715 * x ** 3)))
+
+
+UNARY = {"relu": lambda x: np.maximum(x, 0), "gelu": _gelu, "sigmoid": lambda x: 1.0 / (1.0 + np.exp(-x)),
+         "tanh": np.tanh, "exp": np.exp, "neg": np.negative, "abs": np.abs, "sqrt": np.sqrt}
+BINARY = {"add": np.add, "sub": np.subtract, "mul": np.multiply, "div": np.divide, "maximum": np.maximum,
+          "minimum": np.minimum}
+
+
+def apply_epilogue(y: np.ndarray, operands: list, steps) -> np.ndarray:
+    """Run epilogue steps (fn, operand index, swapped) on y in f32."""
+    for fn, idx, swapped in steps:
+        if idx is None:
+            y = UNARY[fn](y)
+        else:
+            o = _f32(operands[idx])
+            y = BINARY[fn](o, y) if swapped else BINARY[fn](y, o)
+    return y
+
+
+def conv2d_f32(x: np.ndarray, w: np.ndarray, a: dict) -> np.ndarray:
+    """NCHW x OIHW -> NCHW f32 convolution: im2col + one GEMM, or per tap for grouped convs."""
+    (sh, sw), (ph, pw) = a["stride"], a["padding"]
+    dh, dw = a.get("dilation", (1, 1))
+    g = a.get("groups", 1)
+    n, c, h, wd = x.shape
+    o, cg, kh, kw = w.shape
+    oh, ow = conv_out(h, kh, sh, ph, dh), conv_out(wd, kw, sw, pw, dw)
+    xp = np.pad(_f32(x), ((0, 0), (0, 0), (ph, ph), (pw, pw))).transpose(0, 2, 3, 1)
+    w = _f32(w)
+
+    def tap(i, j):
+        return xp[:, i * dh:i * dh + sh * (oh - 1) + 1:sh, j * dw:j * dw + sw * (ow - 1) + 1:sw, :]
+
+    if g == 1:
+        cols = np.empty((n, oh, ow, kh, kw, c), np.float32)
+        for i in range(kh):
+            for j in range(kw):
+                cols[:, :, :, i, j, :] = tap(i, j)
+        out = cols.reshape(n * oh * ow, -1) @ w.transpose(2, 3, 1, 0).reshape(kh * kw * c, o)
+        return np.ascontiguousarray(out.reshape(n, oh, ow, o).transpose(0, 3, 1, 2))
+    og = o // g
+    acc = np.zeros((n, oh, ow, o), np.float32)
+    for i in range(kh):
+        for j in range(kw):
+            xt = tap(i, j)
+            if cg == 1 and og == 1:
+                acc += xt * w[:, 0, i, j]
+            else:
+                for gi in range(g):
+                    part = xt[..., gi * cg:(gi + 1) * cg].reshape(-1, cg) @ w[gi * og:(gi + 1) * og, :, i, j].T
+                    acc[..., gi * og:(gi + 1) * og] += part.reshape(n, oh, ow, og)
+    return np.ascontiguousarray(acc.transpose(0, 3, 1, 2))
+
+
+def quantize_activation(x: np.ndarray, x_scale: float) -> np.ndarray:
+    """clip(rint(x / f32(x_scale)), +-127) in f32 arithmetic, as int64."""
+    return np.clip(np.rint(_f32(x) / np.float32(x_scale)), -127, 127).astype(np.int64)
+
+
+def evaluate(kind: str, xs: list, a: dict) -> np.ndarray:
+    if kind == "const":
+        return a["value"]
+    if kind == "dequantize":
+        shape = [1] * a["q"].ndim
+        shape[a["axis"]] = -1
+        return (a["q"].astype(np.float32) * a["scale"].reshape(shape)).astype(DTYPES[a["dtype"]])
+    dt = xs[0].dtype if xs else np.float32
+    if kind in UNARY:
+        return UNARY[kind](_f32(xs[0])).astype(dt)
+    if kind in BINARY:
+        return BINARY[kind](_f32(xs[0]), _f32(xs[1])).astype(dt)
+    if kind == "matmul":
+        return apply_epilogue(_f32(xs[0]) @ _f32(xs[1]), xs, a.get("epilogue", ())).astype(dt)
+    if kind == "conv2d":
+        return apply_epilogue(conv2d_f32(xs[0], xs[1], a), xs, a.get("epilogue", ())).astype(dt)
+    if kind == "qmatmul":
+        acc = quantize_activation(xs[0], a["x_scale"]) @ a["q"].astype(np.int64)
+        y = (acc.astype(np.float64) * (np.float64(a["x_scale"]) * a["w_scale"].astype(np.float64))).astype(np.float32)
+        return apply_epilogue(y, xs, a.get("epilogue", ())).astype(DTYPES[a["dtype"]])
+    if kind == "maxpool2d":
+        k, s = a["size"], a["stride"]
+        win = np.lib.stride_tricks.sliding_window_view(xs[0], (k, k), axis=(2, 3))[:, :, ::s, ::s]
+        return win.max(axis=(-2, -1)).astype(dt)
+    if kind == "pad":
+        return np.pad(xs[0], a["pads"], constant_values=np.asarray(a.get("value", 0)).astype(dt))
+    if kind == "reduce_mean":
+        return np.asarray(_f32(xs[0]).mean(axis=tuple(a["axes"]), keepdims=a.get("keepdims", False))).astype(dt)
+    if kind == "reshape":
+        return xs[0].reshape(a["shape"])
+    if kind == "transpose":
+        return np.ascontiguousarray(xs[0].transpose(a["perm"]))
+    if kind == "concat":
+        return np.concatenate(xs, axis=a["axis"])
+    if kind == "softmax":
+        x = _f32(xs[0])
+        e = np.exp(x - x.max(axis=a["axis"], keepdims=True))
+        return (e / e.sum(axis=a["axis"], keepdims=True)).astype(dt)
+    if kind == "layernorm":
+        x, gam, bet = (_f32(v) for v in xs)
+        mu = x.mean(axis=-1, keepdims=True)
+        var = ((x - mu) ** 2).mean(axis=-1, keepdims=True)
+        return ((x - mu) / np.sqrt(var + a["eps"]) * gam + bet).astype(dt)
+    if kind == "cast":
+        return xs[0].astype(DTYPES[a["dtype"]])
+    raise NotImplementedError(f"no host evaluation for '{kind}'")
+
+
+def run(g, feeds: dict, watch: Optional[set] = None, peaks: Optional[dict] = None) -> dict:
+    """Evaluate g from {input Value: array}; returns every value.  With `watch`, the running
+    max |x| of each watched value is folded into `peaks`."""
+    env = {v: np.asarray(feeds[v]).astype(v.type.np_dtype) for v in g.inputs}
+    for op in g.ops:
+        env[op.result] = evaluate(op.kind, [env[x] for x in op.inputs], op.attrs)
+    if watch:
+        for v in watch:
+            m = float(np.abs(_f32(env[v])).max()) if np.size(env[v]) else 0.0
+            peaks[v] = max(peaks.get(v, 0.0), m)
+    return env
+
+
+class HostExecutable:
+    def __init__(self, g):
+        self.g = g
+
+    def run(self, feeds: dict) -> dict:
+        env = run(self.g, feeds)
+        return {v: env[v] for v in self.g.outputs}
+
+    def report(self) -> str:
+        return f"host: {len(self.g.compute_ops())} ops evaluated with NumPy"
+
+
+class HostTarget:
+    """The CPU fallback the benchmark gives the runner (MIRA's cpu target plays this role)."""
+    name = "cpu"
+
+    def check(self, op) -> Optional[str]:
+        return None
+
+    def compile(self, g) -> HostExecutable:
+        return HostExecutable(g)

@@ -1,9 +1,8 @@
 """Float graph builders for the W8A8 benchmark configurations.
 
-Each builder returns an unoptimized float32 IR graph with constant weights,
-laid out as MIRA's front ends produce it, so the reference pass pipeline
-(optimize -> fuse_epilogues -> quantize_w8a8) gives the same op and epilogue
-structure:
+Each builder returns an unoptimized float32 graph with constant weights, laid
+out as MIRA's front ends produce it, so lowering (harness.lowering.prepare,
+then w8a8) gives the op and epilogue structure MIRA's compiler gives it:
 
 * dense layers are `matmul` + `add(bias)` (+ activation), as in
   examples/mlp.mira (`x @ w + b`);
@@ -22,8 +21,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .ir import Graph
-from .ops import conv_out
+from .graph import Graph, conv_out
 
 
 def _normal(rng, shape, std):
@@ -31,7 +29,11 @@ def _normal(rng, shape, std):
 
 
 def mira_random_weight(rng, shape) -> np.ndarray:
-    """The distribution of mira/elaborate.py:1114-1123 (rank 1: 1 + 0.1 N; else N / sqrt(fan_in))."""
+    """The seeded weights MIRA's elaborator gives a const parameter (mira/elaborate.py:1114-1123),
+    drawn in parameter order from one generator: rank 1 -> 1 + 0.1 N; rank 4 -> N / sqrt(C*KH*KW);
+    any other rank -> N / sqrt(shape[-2])."""
+    if len(shape) == 0:
+        return np.array(rng.standard_normal(), dtype=np.float32)
     if len(shape) == 1:
         return (1.0 + 0.1 * rng.standard_normal(shape)).astype(np.float32)
     fan_in = int(np.prod(shape[1:])) if len(shape) == 4 else shape[-2]
@@ -43,26 +45,26 @@ def mira_random_weight(rng, shape) -> np.ndarray:
 def mlp_dense(batch: int = 256, k: int = 64, n: int = 10, seed: int = 0) -> Graph:
     """x f32[batch, k] @ w f32[k, n] ~ N(0, 0.1) + b zeros (a zero bias is removed by simplify)."""
     rng = np.random.default_rng(seed)
-    g = Graph("mlp_dense", [], [], [])
+    g = Graph("mlp_dense")
     x = g.input("x", (batch, k))
     w = g.const(_normal(rng, (k, n), 0.1))
     b = g.const(np.zeros(n, np.float32))
-    g.outputs = [g.add("add", [g.add("matmul", [x, w]), b])]
+    g.outputs = [g.op("add", [g.op("matmul", [x, w]), b])]
     return g
 
 
 def mlp_mira(batch: int = 64, seed: int = 0) -> Graph:
     """examples/mlp.mira: 784 -> 512 -> 256 -> 10 with ReLU, then softmax(axis=1)."""
     rng = np.random.default_rng(seed)
-    g = Graph("mlp", [], [], [])
+    g = Graph("mlp")
     h = g.input("x", (batch, 784))
     dims = [(784, 512), (512, 256), (256, 10)]
     params = [(mira_random_weight(rng, d), mira_random_weight(rng, (d[1],))) for d in dims]
     for i, (w, b) in enumerate(params):
-        h = g.add("add", [g.add("matmul", [h, g.const(w)]), g.const(b)])
+        h = g.op("add", [g.op("matmul", [h, g.const(w)]), g.const(b)])
         if i < 2:
-            h = g.add("relu", [h])
-    g.outputs = [g.add("softmax", [h], {"axis": 1})]
+            h = g.op("relu", [h])
+    g.outputs = [g.op("softmax", [h], {"axis": 1})]
     return g
 
 
@@ -70,15 +72,15 @@ def mlp_50m(batch: int = 4096, seed: int = 0) -> Graph:
     """4 dense layers 4096->4096 (x3) and 4096->1000, ReLU between, W ~ N(0, 1/sqrt(4096)),
     biases ~ N(0, 0.1): 54.4 M parameters."""
     rng = np.random.default_rng(seed)
-    g = Graph("mlp50m", [], [], [])
+    g = Graph("mlp50m")
     h = g.input("x", (batch, 4096))
     dims = [(4096, 4096)] * 3 + [(4096, 1000)]
     for i, (k, n) in enumerate(dims):
         w = g.const(_normal(rng, (k, n), 1.0 / np.sqrt(4096)))
         b = g.const(_normal(rng, (n,), 0.1))
-        h = g.add("add", [g.add("matmul", [h, w]), b])
+        h = g.op("add", [g.op("matmul", [h, w]), b])
         if i < len(dims) - 1:
-            h = g.add("relu", [h])
+            h = g.op("relu", [h])
     g.outputs = [h]
     return g
 
@@ -112,45 +114,45 @@ class _ConvNet:
             var = rng.uniform(0.5, 1.5, o)
             s = gamma / np.sqrt(var + 1e-5)
             if self.bn_epilogue:
-                y = self.g.add("conv2d", [x, self.g.const(w)], attrs)
-                y = self.g.add("mul", [y, self.g.const(s.reshape(o, 1, 1).astype(np.float32))])
-                return self.g.add("add", [y, self.g.const((beta - mean * s).reshape(o, 1, 1).astype(np.float32))])
+                y = self.g.op("conv2d", [x, self.g.const(w)], attrs)
+                y = self.g.op("mul", [y, self.g.const(s.reshape(o, 1, 1).astype(np.float32))])
+                return self.g.op("add", [y, self.g.const((beta - mean * s).reshape(o, 1, 1).astype(np.float32))])
             w = (w * s.reshape(-1, 1, 1, 1)).astype(np.float32)
             bias = (beta - mean * s).astype(np.float32)
         else:
             bias = np.zeros(o, np.float32)
-        y = self.g.add("conv2d", [x, self.g.const(w)], attrs)
-        return self.g.add("add", [y, self.g.const(bias.reshape(o, 1, 1))])
+        y = self.g.op("conv2d", [x, self.g.const(w)], attrs)
+        return self.g.op("add", [y, self.g.const(bias.reshape(o, 1, 1))])
 
     def relu(self, x):
-        return self.g.add("relu", [x])
+        return self.g.op("relu", [x])
 
     def relu6(self, x):
         g = self.g
-        y = g.add("maximum", [x, g.const(np.array(0.0, np.float32))])
-        return g.add("minimum", [y, g.const(np.array(6.0, np.float32))])
+        y = g.op("maximum", [x, g.const(np.array(0.0, np.float32))])
+        return g.op("minimum", [y, g.const(np.array(6.0, np.float32))])
 
     def head(self, x, classes: int):
         """Global average pool, flatten, fully connected."""
         g = self.g
         n, c = x.type.shape[:2]
-        pooled = g.add("reduce_mean", [x], {"axes": (2, 3), "keepdims": True})
-        flat = g.add("reshape", [pooled], {"shape": (n, c)})
+        pooled = g.op("reduce_mean", [x], {"axes": (2, 3), "keepdims": True})
+        flat = g.op("reshape", [pooled], {"shape": (n, c)})
         w = _normal(self.rng, (c, classes), 1.0 / np.sqrt(c))
         b = _normal(self.rng, (classes,), 0.01)
-        return g.add("add", [g.add("matmul", [flat, g.const(w)]), g.const(b)])
+        return g.op("add", [g.op("matmul", [flat, g.const(w)]), g.const(b)])
 
 
 def resnet18(batch: int = 256, seed: int = 0, classes: int = 1000, bn_epilogue: bool = False) -> Graph:
     """torchvision ResNet-18: 7x7/2 stem, 3x3/2 max pool, 4 stages of two basic blocks (64, 128,
     256, 512 channels; stride-2 1x1 downsample convs), GAP, fc.  BN folded, or (bn_epilogue)
     as the ONNX importer's per-channel mul + add."""
-    g = Graph("resnet18", [], [], [])
+    g = Graph("resnet18")
     net = _ConvNet(g, seed, bn_epilogue)
     x = g.input("x", (batch, 3, 224, 224))
     h = net.relu(net.conv(x, 64, 7, 2, 3))
-    h = g.add("pad", [h], {"pads": ((0, 0), (0, 0), (1, 1), (1, 1)), "value": -np.inf})
-    h = g.add("maxpool2d", [h], {"size": 3, "stride": 2})
+    h = g.op("pad", [h], {"pads": ((0, 0), (0, 0), (1, 1), (1, 1)), "value": -np.inf})
+    h = g.op("maxpool2d", [h], {"size": 3, "stride": 2})
     c_in = 64
     for stage, c in enumerate((64, 128, 256, 512)):
         for blk in range(2):
@@ -158,7 +160,7 @@ def resnet18(batch: int = 256, seed: int = 0, classes: int = 1000, bn_epilogue: 
             y = net.relu(net.conv(h, c, 3, stride, 1))
             y = net.conv(y, c, 3, 1, 1)
             shortcut = net.conv(h, c, 1, stride, 0) if (stride != 1 or c_in != c) else h
-            h = net.relu(g.add("add", [y, shortcut]))
+            h = net.relu(g.op("add", [y, shortcut]))
             c_in = c
     g.outputs = [net.head(h, classes)]
     return g
@@ -168,7 +170,7 @@ def mobilenet_v2(batch: int = 128, seed: int = 0, classes: int = 1000, bn_epilog
     """torchvision MobileNetV2: 3x3/2 stem, 17 inverted residual blocks (1x1 expand + ReLU6,
     3x3 depthwise + ReLU6, 1x1 linear projection, residual when shapes allow), 1x1 conv to
     1280 + ReLU6, GAP, fc.  BN folded, or (bn_epilogue) as the ONNX importer's mul + add."""
-    g = Graph("mobilenet_v2", [], [], [])
+    g = Graph("mobilenet_v2")
     net = _ConvNet(g, seed, bn_epilogue)
     x = g.input("x", (batch, 3, 224, 224))
     h = net.relu6(net.conv(x, 32, 3, 2, 1))
@@ -183,7 +185,7 @@ def mobilenet_v2(batch: int = 128, seed: int = 0, classes: int = 1000, bn_epilog
                 y = net.relu6(net.conv(y, hidden, 1))
             y = net.relu6(net.conv(y, hidden, 3, stride, 1, groups=hidden))
             y = net.conv(y, c, 1)
-            h = g.add("add", [y, h]) if (stride == 1 and c_in == c) else y
+            h = g.op("add", [y, h]) if (stride == 1 and c_in == c) else y
             c_in = c
     h = net.relu6(net.conv(h, 1280, 1))
     g.outputs = [net.head(h, classes)]
@@ -193,19 +195,17 @@ def mobilenet_v2(batch: int = 128, seed: int = 0, classes: int = 1000, bn_epilog
 def cnn_mira(batch: int = 16, seed: int = 0) -> Graph:
     """examples/cnn.mira: two conv(3x3, pad 1) + bias + relu + maxpool(2) blocks, flatten, dense, softmax."""
     rng = np.random.default_rng(seed)
-    g = Graph("cnn", [], [], [])
+    g = Graph("cnn")
     h = g.input("img", (batch, 1, 28, 28))
-    for o, c in ((16, 1), (32, 16)):
-        k = mira_random_weight(rng, (o, c, 3, 3))
-        b = (1.0 + 0.1 * rng.standard_normal((o, 1, 1))).astype(np.float32)
-        y = g.add("conv2d", [h, g.const(k)], {"stride": (1, 1), "padding": (1, 1)})
-        y = g.add("relu", [g.add("add", [y, g.const(b)])])
-        h = g.add("maxpool2d", [y], {"size": 2, "stride": 2})
-    n = h.type.numel // batch
-    flat = g.add("reshape", [h], {"shape": (batch, n)})
-    wf = mira_random_weight(rng, (n, 10))
+    params = [(mira_random_weight(rng, (o, c, 3, 3)), mira_random_weight(rng, (o, 1, 1))) for o, c in ((16, 1), (32, 16))]
+    wf = mira_random_weight(rng, (1568, 10))
     bf = mira_random_weight(rng, (10,))
-    g.outputs = [g.add("softmax", [g.add("add", [g.add("matmul", [flat, g.const(wf)]), g.const(bf)])],
+    for k, b in params:
+        y = g.op("conv2d", [h, g.const(k)], {"stride": (1, 1), "padding": (1, 1)})
+        y = g.op("relu", [g.op("add", [y, g.const(b)])])
+        h = g.op("maxpool2d", [y], {"size": 2, "stride": 2})
+    flat = g.op("reshape", [h], {"shape": (batch, h.type.numel // batch)})
+    g.outputs = [g.op("softmax", [g.op("add", [g.op("matmul", [flat, g.const(wf)]), g.const(bf)])],
                        {"axis": -1})]
     return g
 
@@ -286,7 +286,7 @@ def gpt_decode_step(cfg: GPTConfig, batch: int, params: dict) -> Graph:
     static shapes at every position."""
     L, D, H, V, T = cfg.L, cfg.D, cfg.H, cfg.V, cfg.T
     hd = D // H
-    g = Graph("gpt_step", [], [], [])
+    g = Graph("gpt_step")
     h = g.input("h", (batch, D))
     mask = g.input("mask", (1, 1, 1, T + 1))
     caches = [(g.input(f"kc{l}", (batch, T, D)), g.input(f"vc{l}", (batch, T, D))) for l in range(L)]
@@ -295,23 +295,23 @@ def gpt_decode_step(cfg: GPTConfig, batch: int, params: dict) -> Graph:
     kv_out = []
     for l in range(L):
         kc, vc = caches[l]
-        x = g.add("layernorm", [h, c(f"g1{l}"), c(f"b1{l}")], {"eps": 1e-5})
-        q = g.add("matmul", [x, c(f"wq{l}")])
-        k = g.add("matmul", [x, c(f"wk{l}")])
-        v = g.add("matmul", [x, c(f"wv{l}")])
+        x = g.op("layernorm", [h, c(f"g1{l}"), c(f"b1{l}")], {"eps": 1e-5})
+        q = g.op("matmul", [x, c(f"wq{l}")])
+        k = g.op("matmul", [x, c(f"wk{l}")])
+        v = g.op("matmul", [x, c(f"wv{l}")])
         kv_out += [k, v]
-        q4 = g.add("transpose", [g.add("reshape", [q], {"shape": (batch, 1, H, hd)})], {"perm": (0, 2, 1, 3)})
-        keys = g.add("concat", [kc, g.add("reshape", [k], {"shape": (batch, 1, D)})], {"axis": 1})
-        vals = g.add("concat", [vc, g.add("reshape", [v], {"shape": (batch, 1, D)})], {"axis": 1})
-        k4 = g.add("transpose", [g.add("reshape", [keys], {"shape": (batch, T + 1, H, hd)})], {"perm": (0, 2, 3, 1)})
-        v4 = g.add("transpose", [g.add("reshape", [vals], {"shape": (batch, T + 1, H, hd)})], {"perm": (0, 2, 1, 3)})
-        s = g.add("add", [g.add("mul", [g.add("matmul", [q4, k4]), scale]), mask])
-        o4 = g.add("matmul", [g.add("softmax", [s], {"axis": -1}), v4])
-        o = g.add("reshape", [g.add("transpose", [o4], {"perm": (0, 2, 1, 3)})], {"shape": (batch, D)})
-        h = g.add("add", [h, g.add("matmul", [o, c(f"wo{l}")])])
-        y = g.add("layernorm", [h, c(f"g2{l}"), c(f"b2{l}")], {"eps": 1e-5})
-        h = g.add("add", [h, g.add("matmul", [g.add("gelu", [g.add("matmul", [y, c(f"w1{l}")])]), c(f"w2{l}")])])
-    logits = g.add("matmul", [g.add("layernorm", [h, c("gf"), c("bf")], {"eps": 1e-5}), c("wout")])
+        q4 = g.op("transpose", [g.op("reshape", [q], {"shape": (batch, 1, H, hd)})], {"perm": (0, 2, 1, 3)})
+        keys = g.op("concat", [kc, g.op("reshape", [k], {"shape": (batch, 1, D)})], {"axis": 1})
+        vals = g.op("concat", [vc, g.op("reshape", [v], {"shape": (batch, 1, D)})], {"axis": 1})
+        k4 = g.op("transpose", [g.op("reshape", [keys], {"shape": (batch, T + 1, H, hd)})], {"perm": (0, 2, 3, 1)})
+        v4 = g.op("transpose", [g.op("reshape", [vals], {"shape": (batch, T + 1, H, hd)})], {"perm": (0, 2, 1, 3)})
+        s = g.op("add", [g.op("mul", [g.op("matmul", [q4, k4]), scale]), mask])
+        o4 = g.op("matmul", [g.op("softmax", [s], {"axis": -1}), v4])
+        o = g.op("reshape", [g.op("transpose", [o4], {"perm": (0, 2, 1, 3)})], {"shape": (batch, D)})
+        h = g.op("add", [h, g.op("matmul", [o, c(f"wo{l}")])])
+        y = g.op("layernorm", [h, c(f"g2{l}"), c(f"b2{l}")], {"eps": 1e-5})
+        h = g.op("add", [h, g.op("matmul", [g.op("gelu", [g.op("matmul", [y, c(f"w1{l}")])]), c(f"w2{l}")])])
+    logits = g.op("matmul", [g.op("layernorm", [h, c("gf"), c("bf")], {"eps": 1e-5}), c("wout")])
     g.outputs = [logits] + kv_out
     return g
 

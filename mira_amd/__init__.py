@@ -1,19 +1,31 @@
 """mira_amd: MIRA's W8A8 quantized-inference path as an MI355X (gfx950) target.
 
 The package is the `rocm` execution target of the MIRA tensor compiler
-(myramay/MIRA) for one hot path -- W8A8 inference -- plus the host-side
-mirror of the reference interfaces it plugs into:
+(myramay/MIRA) for one hot path, W8A8 inference.  MIRA's own compiler,
+quantizer and partitioner produce the graphs; this package runs them:
 
-    target.RocmTarget / RocmExecutable   the Target/Executable plugin (mira/backends/base.py)
+    target.RocmTarget / RocmExecutable   the Target/Executable plugin (mira/backends/base.py:13-26)
     _lib                                 ctypes binding of libmira_rocm.so (include/mira_rocm.h)
+    pack                                 host-side byte order of int8 weights and activations
+    build                                hipcc build of libmira_rocm.so for gfx950
     csrc/                                the HIP kernels (int8 MFMA GEMM / implicit-GEMM conv,
                                          fused dequant/epilogue/requant, quantizer, depthwise,
                                          pooling) and their C ABI
-    ir, types, ops, passes, quantize,    mirrors of the reference's IR, type rules, passes,
-    partition, compiler                  W8A8 rewrite, partitioner and driver
-    hosteval                             compile-time constant folding and calibration
-    models                               graph builders for the benchmark configurations
-"""
-from .compiler import CompiledProgram, compile_graph, compile_ir, get_target  # noqa: F401
 
-__all__ = ["compile_ir", "compile_graph", "get_target", "CompiledProgram"]
+`get_target` / `TARGETS` are the branch a MIRA checkout adds to its backend
+registry (mira/backends/__init__.py:5-25).
+"""
+from __future__ import annotations
+
+TARGETS = ["rocm"]
+
+
+def get_target(name: str, **options):
+    """The rocm branch of MIRA's get_target: options device (int) and debug_acc (bool)."""
+    if name != "rocm":
+        raise ValueError(f"unknown target '{name}' (this package provides: rocm)")
+    from .target import RocmTarget
+    return RocmTarget(device=options.get("device", 0), debug_acc=options.get("debug_acc", False))
+
+
+__all__ = ["get_target", "TARGETS"]

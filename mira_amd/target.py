@@ -28,10 +28,13 @@ from typing import Callable, Optional
 import numpy as np
 
 from . import _lib as L
-from . import ir
 from . import pack
-from .ops import conv_out, conv_params
 
+
+# Type annotations "Graph", "Op" and "Value" name MIRA's IR types (mira/ir.py:34-154); the
+# target reads them by attribute only (kind, inputs, attrs, results, type.shape/dtype, producer,
+# is_constant_like, is_control; graph inputs/ops/outputs/users()/compute_ops()), so any graph
+# with those attributes compiles.
 
 EPI_FNS = {"add", "sub", "mul", "div", "maximum", "minimum", "relu"}
 
@@ -46,6 +49,17 @@ def _t():
     return _torch
 
 
+def conv_params(a: dict) -> tuple:
+    """((sh, sw), (ph, pw), (dh, dw), groups) of a conv op's attrs (the names MIRA's conv2d
+    and qconv2d ops carry; dilation and groups may be absent)."""
+    return tuple(a["stride"]), tuple(a["padding"]), tuple(a.get("dilation", (1, 1))), a.get("groups", 1)
+
+
+def conv_out(size: int, k: int, stride: int, pad: int, dilation: int = 1) -> int:
+    """Output extent of a convolution or pooling window along one axis."""
+    return (size + 2 * pad - dilation * (k - 1) - 1) // stride + 1
+
+
 def _f32key(x: float) -> float:
     """x_scale as the quantizer sees it: rounded to f32 (mira/ops.py:603)."""
     return float(np.float32(x))
@@ -54,7 +68,7 @@ def _f32key(x: float) -> float:
 @dataclass
 class DevValue:
     """Device copies of one IR value."""
-    value: ir.Value
+    value: object
     nhwc: bool                                   # rank-4 values are stored NHWC
     f32: object = None                           # torch tensor (NHWC or row-major)
     i8: dict = field(default_factory=dict)       # f32 x_scale -> (torch int8 tensor, row stride)
@@ -105,7 +119,7 @@ class RocmTarget:
 
     # ---------------------------------------------------------------- check
 
-    def check(self, op: ir.Op) -> Optional[str]:
+    def check(self, op: "Op") -> Optional[str]:
         """None if the rocm kernels run `op` with the golden model's exact arithmetic."""
         if op.is_control:
             return "control flow runs on the host"
@@ -146,7 +160,7 @@ class RocmTarget:
             return self._check_w8_matmul(op)
         return f"'{k}' has no rocm kernel"
 
-    def _check_w8_matmul(self, op: ir.Op) -> Optional[str]:
+    def _check_w8_matmul(self, op: "Op") -> Optional[str]:
         """Decode-shaped matmuls of the weight-only int8 mode (mira/quantize.py:45-68): an f32
         activation of at most W8_MAX_ROWS rows against a `dequantize` [K, N] weight.  These
         compute in f32 in another summation order than BLAS's, so they match the reference
@@ -164,7 +178,7 @@ class RocmTarget:
             return f"weight-only int8 matmul runs on rocm for decode shapes (<= {W8_MAX_ROWS} rows), not {rows}"
         return self._check_epilogue(op, op.result.type.shape, False)
 
-    def _check_epilogue(self, op: ir.Op, shape: tuple, is_conv: bool, first_operand: int = 1) -> Optional[str]:
+    def _check_epilogue(self, op: "Op", shape: tuple, is_conv: bool, first_operand: int = 1) -> Optional[str]:
         for fn, idx, _sw in op.attrs.get("epilogue", ()):
             if fn not in EPI_FNS:
                 return f"epilogue step '{fn}' is not bit-reproducible on rocm (libm)"
@@ -179,7 +193,7 @@ class RocmTarget:
                 return f"runtime epilogue operand {v.type} broadcasts onto {list(shape)} in a way rocm can't index"
         return None
 
-    def compile(self, g: ir.Graph) -> "RocmExecutable":
+    def compile(self, g: "Graph") -> "RocmExecutable":
         return RocmExecutable(g, self)
 
 
@@ -202,7 +216,7 @@ def _bcast_mode(oshape: tuple, rshape: tuple, is_conv: bool) -> Optional[int]:
 class RocmExecutable:
     """A compiled rocm segment: device buffers, packed constants and a launch list."""
 
-    def __init__(self, g: ir.Graph, target: RocmTarget):
+    def __init__(self, g: "Graph", target: RocmTarget):
         torch = _t()
         self.g = g
         self.target = target
@@ -219,8 +233,8 @@ class RocmExecutable:
                     raise L.RocmError(f"rocm cannot run {op.kind}: {reason}")
         self.launches: list[tuple[str, Callable[[int], None]]] = []
         self.keep: list = []          # host objects (ctypes structs, tensors) the launches refer to
-        self.dv: dict[ir.Value, DevValue] = {}
-        self.acc: dict[ir.Value, object] = {}      # debug int32 accumulators per q-op result
+        self.dv: dict["Value", DevValue] = {}
+        self.acc: dict["Value", object] = {}      # debug int32 accumulators per q-op result
         self.kernel_counts: dict[str, int] = {}
         self.launch_cost: list[tuple[str, int, int]] = []
         self.const_bytes = 0
@@ -239,13 +253,18 @@ class RocmExecutable:
         for op in g.ops:
             if op.kind in IMAGE_OPS:
                 self.images.update(v for v in [*op.inputs, op.result] if v.type.rank == 4)
-        for _ in range(2):      # a cast's result shares its input's buffers, so their layouts agree
+        # a cast's result shares its input's buffers, so their layouts agree: propagate along
+        # chains of casts until nothing changes
+        grew = True
+        while grew:
+            grew = False
             for op in g.ops:
-                if op.kind == "cast" and (op.result in self.images or op.inputs[0] in self.images):
+                if op.kind == "cast" and (op.result in self.images) != (op.inputs[0] in self.images):
                     self.images.update((op.inputs[0], op.result))
+                    grew = True
         # which forms each value needs
         self.need_f32: set = set(g.outputs)
-        self.need_i8: dict[ir.Value, list[float]] = {}
+        self.need_i8: dict["Value", list[float]] = {}
         self.folded_pads: set = set()
         self.fused_stem: dict = {}          # maxpool op -> (qconv2d op, pad op) run as one kernel
         self.skip: set = set()
@@ -296,7 +315,7 @@ class RocmExecutable:
                     self.need_f32.discard(v)
                 lst = self.need_i8.setdefault(v, [])
                 lst += [s for s in self.need_i8.get(r, []) if s not in lst]
-        self.staging: dict[ir.Value, object] = {}
+        self.staging: dict["Value", object] = {}
         for v in g.inputs:
             self._emit_input(v)
         for op in g.ops:
@@ -307,7 +326,7 @@ class RocmExecutable:
             if v in self.consts and v not in self.dv:
                 self._const_dv(v)
 
-    def _i8_view(self, src: ir.Value, r: ir.Value) -> bool:
+    def _i8_view(self, src: "Value", r: "Value") -> bool:
         """Is the int8 copy of `r` (a reshape of `src`) the same bytes as src's? Only for an
         [n, c, 1, 1] image <-> [n, c] (global average pooling into an fc layer): NHWC with
         1x1 pixels is row-major [n, c], and both strides round c up to 16."""
@@ -319,7 +338,7 @@ class RocmExecutable:
         return len(a) == 2 and len(b) == 4 and b[2] == b[3] == 1 and a == (b[0], b[1]) and \
             pack.c_pad_for(b[1]) == pack.row_stride_for(b[1])
 
-    def _stem_fusable(self, conv: Optional[ir.Op], pad_op: ir.Op, pool: ir.Op) -> bool:
+    def _stem_fusable(self, conv: Optional["Op"], pad_op: "Op", pool: "Op") -> bool:
         """Can qconv2d -> pad -> maxpool2d run as mr_qconv2d_maxpool (the convolution is never stored)?
         The kernel pools the int32 accumulators, so the epilogue must commute with max."""
         if conv is None or conv.kind != "qconv2d" or self.target.debug_acc:
@@ -338,7 +357,7 @@ class RocmExecutable:
                 and pool.result.type.shape[3] <= (60 if pool_cfg[0] == 3 else 64)
                 and self._monotone_epilogue(conv))
 
-    def _monotone_epilogue(self, op: ir.Op) -> bool:
+    def _monotone_epilogue(self, op: "Op") -> bool:
         """Every step non-decreasing in the value, with an operand that is the same across a
         pooling window (scalar or per-channel).  A mul qualifies when its operand is a
         constant that is finite and positive everywhere (a BatchNorm scale)."""
@@ -360,14 +379,14 @@ class RocmExecutable:
                 return False
         return True
 
-    def _foldable_pad(self, v: ir.Value) -> bool:
+    def _foldable_pad(self, v: "Value") -> bool:
         p = v.producer
         if p is None or p.kind != "pad" or v in self.g.outputs or len(self.users.get(v, [])) != 1:
             return False
         pads = tuple(tuple(x) for x in p.attrs["pads"])
         return p.inputs[0].type.rank == 4 and pads[0] == (0, 0) and pads[1] == (0, 0)
 
-    def _new_dv(self, v: ir.Value, with_i8: bool = False) -> DevValue:
+    def _new_dv(self, v: "Value", with_i8: bool = False) -> DevValue:
         """Allocate v's f32 copy if anything reads it; int8 copies only for segment inputs
         (producers allocate the ones they write)."""
         torch = _t()
@@ -382,7 +401,7 @@ class RocmExecutable:
         self.dv[v] = d
         return d
 
-    def _emit_input(self, v: ir.Value) -> None:
+    def _emit_input(self, v: "Value") -> None:
         """A segment input lives on the device as f32 in the graph's own layout (NCHW for
         images); the launch list starts by building the copies the kernels read from it: the
         NHWC f32 copy and the int8 copies its q-op consumers need (their quantize_activation,
@@ -428,14 +447,19 @@ class RocmExecutable:
         self.keep.append(t)
         return t
 
-    def _const_value(self, v: ir.Value) -> np.ndarray:
+    def _const_value(self, v: "Value") -> np.ndarray:
         op = self.consts[v]
         if op.kind == "const":
             return np.asarray(op.attrs["value"])
-        from .hosteval import evaluate            # a dequantize constant, materialized once
-        return evaluate("dequantize", [], op.attrs)
+        # a `dequantize` constant (int8 weight-only mode), materialized once as
+        # q * scale in f32, then in its dtype (mira/ops.py:581-586)
+        a = op.attrs
+        shape = [1] * a["q"].ndim
+        shape[a["axis"]] = -1
+        return (a["q"].astype(np.float32) * np.asarray(a["scale"], np.float32).reshape(shape)).astype(
+            np.float16 if a["dtype"] == "f16" else np.float32)
 
-    def _const_dv(self, v: ir.Value) -> DevValue:
+    def _const_dv(self, v: "Value") -> DevValue:
         """A constant used as a data input: upload it in its device layout."""
         if v in self.dv:
             return self.dv[v]
@@ -447,7 +471,7 @@ class RocmExecutable:
             d.i8[xs] = self._quantize_to(d, xs)
         return d
 
-    def _src(self, v: ir.Value) -> DevValue:
+    def _src(self, v: "Value") -> DevValue:
         if v in self.consts:
             return self._const_dv(v)
         return self.dv[v]
@@ -494,7 +518,7 @@ class RocmExecutable:
 
     # ---------------------------------------------------------------- epilogue descriptors
 
-    def _epilogue(self, op: ir.Op, out: DevValue, is_conv: bool, first: int, scale) -> tuple:
+    def _epilogue(self, op: "Op", out: DevValue, is_conv: bool, first: int, scale) -> tuple:
         """Build the mr_epilogue for `op` writing into `out` (f32 and the first int8 copy)."""
         e = L.Epilogue()
         steps = op.attrs.get("epilogue", ())
@@ -534,7 +558,7 @@ class RocmExecutable:
         self.keep.append(e)
         return e, fused
 
-    def _const_operand(self, v: ir.Value, rshape: tuple, is_conv: bool):
+    def _const_operand(self, v: "Value", rshape: tuple, is_conv: bool):
         a = self._const_value(v).astype(np.float32)
         mode = _bcast_mode(a.shape, rshape, is_conv)
         if mode is None:                     # partial broadcast: materialize the full operand
@@ -552,14 +576,14 @@ class RocmExecutable:
 
     # ---------------------------------------------------------------- emitters
 
-    def _acc_buffer(self, op: ir.Op, rows: int, cols: int):
+    def _acc_buffer(self, op: "Op", rows: int, cols: int):
         if not self.target.debug_acc:
             return None
         t = _t().empty((rows, cols), dtype=_t().int32, device=self.dev)
         self.acc[op.result] = t
         return t
 
-    def _emit_qmatmul(self, op: ir.Op) -> None:
+    def _emit_qmatmul(self, op: "Op") -> None:
         a = op.attrs
         x = self._src(op.inputs[0])
         q = np.asarray(a["q"], np.int8)
@@ -581,7 +605,7 @@ class RocmExecutable:
             nbytes=M * K + K * N + self._epi_bytes(e, M, N), nops=2 * M * N * K)
         self._finish_i8(out, fused)
 
-    def _emit_matmul(self, op: ir.Op) -> None:
+    def _emit_matmul(self, op: "Op") -> None:
         """Weight-only int8 matmul (checked by _check_w8_matmul): the int8 weights are packed
         and uploaded once with their f32 scales; each run streams them through the
         mr_w8_matmul_f32 kernel."""
@@ -603,7 +627,7 @@ class RocmExecutable:
             "mr_w8_matmul_f32"), nbytes=4 * M * K + K * N + 4 * N + self._epi_bytes(e, M, N))
         self._finish_i8(out, fused)
 
-    def _emit_qconv2d(self, op: ir.Op) -> None:
+    def _emit_qconv2d(self, op: "Op") -> None:
         a = op.attrs
         xv = op.inputs[0]
         x = self._src(xv)
@@ -635,7 +659,7 @@ class RocmExecutable:
             nbytes=n * h * w * c + o * c * kh * kw + self._epi_bytes(e, rows, o), nops=2 * rows * o * c * kh * kw)
         self._finish_i8(out, fused)
 
-    def _emit_conv2d(self, op: ir.Op) -> None:
+    def _emit_conv2d(self, op: "Op") -> None:
         """Depthwise f32 convolution (groups == C, one filter per channel)."""
         a = op.attrs
         xv = op.inputs[0]
@@ -657,7 +681,7 @@ class RocmExecutable:
             nbytes=4 * n * c * h * w + 4 * c * kh * kw + self._epi_bytes(e, n * oh * ow, c))
         self._finish_i8(out, fused)
 
-    def _emit_fused_stem(self, op: ir.Op) -> None:
+    def _emit_fused_stem(self, op: "Op") -> None:
         conv, pad_op = self.fused_stem[op]
         a = conv.attrs
         x = self._src(conv.inputs[0])
@@ -688,7 +712,7 @@ class RocmExecutable:
             nops=2 * n * oh * ow * o * c * kh * kw)
         self._finish_i8(out, fused)
 
-    def _emit_maxpool2d(self, op: ir.Op) -> None:
+    def _emit_maxpool2d(self, op: "Op") -> None:
         if op in self.fused_stem:
             return self._emit_fused_stem(op)
         v = op.inputs[0]
@@ -720,7 +744,7 @@ class RocmExecutable:
             (n * oh * ow * cp if yq is not None else 0))
         self._finish_i8(out, fused)
 
-    def _emit_pad(self, op: ir.Op) -> None:
+    def _emit_pad(self, op: "Op") -> None:
         x = self._src(op.inputs[0])
         n, c, h, w = op.inputs[0].type.shape
         pads = tuple(tuple(p) for p in op.attrs["pads"])
@@ -735,7 +759,7 @@ class RocmExecutable:
                   nbytes=4 * n * c * (h * w + (h + t + b) * (w + l + r)))
         self._finish_i8(out, None)
 
-    def _emit_reduce_mean(self, op: ir.Op) -> None:
+    def _emit_reduce_mean(self, op: "Op") -> None:
         x = self._src(op.inputs[0])
         n, c, h, w = op.inputs[0].type.shape
         out = self._new_dv(op.result)
@@ -764,7 +788,7 @@ class RocmExecutable:
         self._add("round_f16", lambda s: L.check(lib.mr_round_f16_f32(src.data_ptr(), numel, dst.data_ptr(), s),
                                                  "mr_round_f16_f32"), nbytes=8 * numel)
 
-    def _emit_cast(self, op: ir.Op) -> None:
+    def _emit_cast(self, op: "Op") -> None:
         """mira/ops.py:405-406 between f32 and f16.  To f16: round (in place on the input
         buffer when the cast is a graph input's only use, see _plan); to f32: the f16
         values are already stored as f32, so the result shares the input's buffers."""
@@ -780,7 +804,7 @@ class RocmExecutable:
         self._round_f16(x.f32, out.f32)
         self._finish_i8(out, None)
 
-    def _emit_reshape(self, op: ir.Op) -> None:
+    def _emit_reshape(self, op: "Op") -> None:
         torch = _t()
         src_v, r = op.inputs[0], op.result
         x = self._src(src_v)
@@ -830,7 +854,7 @@ class RocmExecutable:
             arr = np.ascontiguousarray(np.asarray(feeds[v]).astype(np.float32)).reshape(v.type.shape)
             self.staging[v].copy_(torch.from_numpy(arr), non_blocking=False)
 
-    def device_input(self, v: ir.Value):
+    def device_input(self, v: "Value"):
         """The device f32 buffer (graph layout) that `launch` reads segment input v from."""
         return self.staging[v]
 
@@ -869,7 +893,7 @@ class RocmExecutable:
         """int32 accumulators of every q-op from the last run (needs RocmTarget(debug_acc=True))."""
         return {v: t.cpu().numpy() for v, t in self.acc.items()}
 
-    def device_of(self, v: ir.Value) -> Optional[str]:
+    def device_of(self, v: "Value") -> Optional[str]:
         return "rocm" if v in self.dv else None
 
     def report(self) -> str:

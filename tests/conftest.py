@@ -38,10 +38,13 @@ def lib():
 
 
 def bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
-    """Equal as values (NaN == NaN, +0 == -0), dtype and shape."""
+    """Same dtype, shape and bit pattern (so +0 and -0 differ); every NaN counts as one
+    canonical NaN, since NaN payloads are not part of any result's meaning."""
     a, b = np.asarray(a), np.asarray(b)
     if a.shape != b.shape or a.dtype != b.dtype:
         return False
     if a.dtype.kind == "f":
-        return bool(np.all((a == b) | (np.isnan(a) & np.isnan(b))))
+        ui = {2: np.uint16, 4: np.uint32, 8: np.uint64}[a.dtype.itemsize]
+        an, bn = np.isnan(a), np.isnan(b)
+        return bool(np.array_equal(an, bn) and np.array_equal(a[~an].view(ui), b[~bn].view(ui)))
     return bool(np.array_equal(a, b))

@@ -29,7 +29,11 @@ def test_kernel_breakdown_rooflines():
     assert abs(conv["tops"] - 20.0) < 1e-9                     # 2e10 ops in 1 ms
     assert abs(conv["mfma_frac"] - 20.0 / bench.INT8_PEAK_TOPS) < 1e-6
     assert abs(conv["gbs"] - 20.0) < 1e-9 and abs(conv["hbm_frac"] - 20.0 / bench.HBM_PEAK_GBS) < 1e-6
-    assert out["qmatmul"]["bound"] == "hbm"
+    assert conv["launch_bounds"] == {"mfma": 2, "hbm": 0}
+    # priced against MFMA (a contraction) even though this launch sits below the ridge
+    mm = out["qmatmul"]
+    assert mm["bound"] == "mfma" and mm["launch_bounds"] == {"mfma": 0, "hbm": 1}
+    assert abs(mm["roofline_frac"] - (4e6 / (bench.HBM_PEAK_GBS * 1e9)) / 1e-5) < 1e-9
     inp = out["input"]
     assert inp["bound"] == "hbm" and "tops" not in inp and abs(inp["gbs"] - 4000.0) < 1e-6
     # kinds come out slowest first

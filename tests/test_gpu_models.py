@@ -1,21 +1,23 @@
 """End-to-end parity of the rocm target on the W8A8 configurations.
 
-Each graph is optimized and W8A8-quantized once; the same quantized graph (the
-same attrs) then runs on the rocm target and on the oracle's CPU executor.
-Every int32 accumulator, and every output, must match bit for bit.  Ops the
-rocm target rejects (softmax) run on the oracle's CPU target, as MIRA's
-partitioner would send them to its cpu target.
+Each graph is lowered and W8A8-quantized once (harness.lowering); the same quantized
+graph (the same attrs) then runs on the rocm target and on the oracle.  Every int32
+accumulator and every output must match bit for bit.  Ops the rocm target rejects
+(softmax, the f32 attention, layernorm and gelu of the GPT step) run on the oracle's
+CPU target, as MIRA's partitioner would send them to its cpu target.
 
-Full-size configurations are checked through batch independence: rows of the
-batch-256 (or 4096) run must equal the oracle's results for those rows run on
-their own, with the same attrs.
+Full-size batches are checked through batch independence: chosen rows of the big run
+must equal the oracle's results for those rows run on their own with the same attrs.
+The rows are spread over the batch (and so over the tile grid), and include the
+images an epilogue race once corrupted (7, 10, 12, 23, 53, 60, 78, 83, 130, 138, 162,
+165, 180).
 """
 import numpy as np
 import pytest
 
-from mira_amd import models, passes
-from mira_amd.compiler import compile_graph
-from mira_amd.quantize import calibration_peaks, quantize_w8a8, quantize_weights
+from harness import lowering as LW
+from harness import models
+from harness.runner import Runner
 from mira_amd.target import RocmTarget
 from oracle import golden as G
 
@@ -24,35 +26,38 @@ from gpu_util import oracle_env
 
 pytestmark = pytest.mark.gpu
 
+RACE_ROWS = [7, 10, 12, 23, 53, 60, 78, 83, 130, 138, 162, 165, 180]
 
-def _quantized(builder, batch, seed, calib_seeds, input_name="x", dist="normal", calib_batch=None, peaks=None):
-    g = builder(batch=batch, seed=seed)
-    passes.optimize(g)
+
+def _gen(dist):
+    return models.image_batch if dist == "uniform" else models.normal_batch
+
+
+def _quantized(builder, batch, calib_seeds=(11, 12), dist="uniform", calib_batch=None, peaks=None,
+               precision=None):
+    """builder(batch, seed=0) lowered and W8A8-rewritten; calibration on a twin of
+    calib_batch rows (same weights), or the given peaks."""
+    g = LW.prepare(builder(batch=batch, seed=0), precision)
     if peaks is None:
         cb = calib_batch or batch
-        twin = builder(batch=cb, seed=seed) if cb != batch else g
-        if twin is not g:
-            passes.optimize(twin)
-        shape = twin.inputs[0].type.shape
-        gen = models.image_batch if dist == "uniform" else models.normal_batch
-        peaks = calibration_peaks(twin, [{input_name: gen(shape, s)} for s in calib_seeds])
-    quantize_w8a8(g, peaks=peaks)
+        twin = g if cb == batch else LW.prepare(builder(batch=cb, seed=0), precision)
+        x = twin.inputs[0]
+        peaks = LW.calibrate(twin, [{x.name: _gen(dist)(x.type.shape, s)} for s in calib_seeds])
+    LW.w8a8(g, peaks=peaks)
     return g, peaks
 
 
 def _compare(g, feeds, check_acc=True, fallback=True):
-    runner = compile_graph(g, RocmTarget(debug_acc=True), fallback=G.CPUTarget() if fallback else None)
-    got = runner.run_list([feeds[v.name] for v in g.inputs])
+    runner = Runner(g, RocmTarget(debug_acc=True), fallback=G.CPUTarget() if fallback else None)
+    got = runner.run(feeds)
     env = oracle_env(g, feeds)
     for v, out in zip(g.outputs, got):
         assert bits_equal(out, env[v]), f"output {v} differs: max abs {np.abs(out - env[v]).max()}"
     if check_acc:
         n_acc = 0
-        for seg in runner.segments:
-            if seg.device != "rocm":
-                continue
-            accs = seg.executable.accumulators()
-            for op in seg.graph.ops:
+        for exe in runner.executables("rocm"):
+            accs = exe.accumulators()
+            for op in exe.g.ops:
                 if op.kind == "qmatmul":
                     want = G.qmatmul_acc(env[op.inputs[0]], op.attrs)
                     want = want.reshape(-1, want.shape[-1])
@@ -69,49 +74,131 @@ def _compare(g, feeds, check_acc=True, fallback=True):
     return runner
 
 
+def _rows_match_small_run(builder, big, rows, dist, calib_seeds=(11, 12), runs=1):
+    """The full batch on rocm (production path: fused stem, no debug copies); the chosen rows
+    alone on the oracle with the same attrs.  With runs > 1 the executable runs again and
+    every run must give the same bits."""
+    g_big, peaks = _quantized(builder, big, calib_seeds, dist, calib_batch=2)
+    x = _gen(dist)((big,) + g_big.inputs[0].type.shape[1:], 7)
+    runner = Runner(g_big, RocmTarget())
+    assert runner.devices == ["rocm"]
+    outs = [runner.run({"x": x})[0] for _ in range(runs)]
+    g_small, _ = _quantized(builder, len(rows), dist=dist, peaks=peaks)
+    (want,) = G.run_graph(g_small, {"x": x[rows]})
+    for out in outs:
+        assert bits_equal(out[rows], want)
+        assert np.isfinite(out).all()
+        assert bits_equal(out, outs[0])
+
+
+# ---------------------------------------------------------------- C1 and the reference's own programs
+
 def test_c1_dense_256x64_to_10():
     """x f32[256,64] ~ N(0,1), w ~ N(0,0.1), b = 0; calibration on 8 seeded batches."""
-    g, _ = _quantized(models.mlp_dense, 256, 0, range(1, 9))
-    kinds = [op.kind for op in g.compute_ops()]
-    assert kinds == ["qmatmul"] and "epilogue" not in g.compute_ops()[0].attrs   # zero bias simplified away
+    g, _ = _quantized(models.mlp_dense, 256, range(1, 9), "normal")
+    ops = g.compute_ops()
+    assert [op.kind for op in ops] == ["qmatmul"] and "epilogue" not in ops[0].attrs   # zero bias dropped
     _compare(g, {"x": models.normal_batch((256, 64), 100)}, fallback=False)
 
 
 def test_mlp_mira_with_softmax_fallback():
-    g, _ = _quantized(models.mlp_mira, 64, 0, (2, 3))
+    g, _ = _quantized(models.mlp_mira, 64, (2, 3), "normal")
     runner = _compare(g, {"x": models.normal_batch((64, 784), 1)})
-    assert [s.device for s in runner.segments] == ["rocm", "cpu"]
+    assert runner.devices == ["rocm", "cpu"]
     soft = next(op for op in g.compute_ops() if op.kind == "softmax")
-    assert "softmax" in runner.placement.reason[soft]
+    assert "softmax" in runner.reasons[soft]
 
 
 def test_cnn_mira():
-    g, _ = _quantized(models.cnn_mira, 16, 0, (2, 3), input_name="img")
+    g, _ = _quantized(models.cnn_mira, 16, (2, 3), "normal")
     _compare(g, {"img": models.normal_batch((16, 1, 28, 28), 1)})
 
 
+# ---------------------------------------------------------------- C2 MLP-50M
+
+def test_mlp50m_batch1_whole_network():
+    """Batch 1 (the decode-shaped weight-streaming qmatmul), all four layers."""
+    g, _ = _quantized(models.mlp_50m, 1, (2, 3), "normal", calib_batch=8)
+    runner = _compare(g, {"x": models.normal_batch((1, 4096), 1)}, fallback=False)
+    assert runner.executables("rocm")[0].kernel_counts.get("qmatmul") == 4
+
+
+def test_mlp50m_batch8():
+    g, _ = _quantized(models.mlp_50m, 8, (2, 3), "normal")
+    _compare(g, {"x": models.normal_batch((8, 4096), 1)}, fallback=False)
+
+
+def test_mlp50m_batch4096_rows():
+    _rows_match_small_run(models.mlp_50m, 4096, [0, 1, 255, 256, 1234, 2047, 2048, 3333, 4095], "normal",
+                          calib_seeds=(2, 3))
+
+
+# ---------------------------------------------------------------- C3 ResNet-18
+
+def test_resnet18_batch1():
+    g, _ = _quantized(models.resnet18, 1)
+    runner = _compare(g, {"x": models.image_batch((1, 3, 224, 224), 5)}, fallback=False)
+    assert runner.devices == ["rocm"]
+
+
 def test_resnet18_batch2():
-    g, _ = _quantized(models.resnet18, 2, 0, (11, 12), dist="uniform")
+    g, _ = _quantized(models.resnet18, 2)
     runner = _compare(g, {"x": models.image_batch((2, 3, 224, 224), 5)}, fallback=False)
-    assert [s.device for s in runner.segments] == ["rocm"]
+    assert runner.devices == ["rocm"]
+
+
+def test_resnet18_batch256_rows():
+    """16 oracle rows of the batch-256 run, three runs of one executable bit-identical."""
+    _rows_match_small_run(models.resnet18, 256, [0] + RACE_ROWS + [200, 255], "uniform", runs=3)
+
+
+@pytest.mark.parametrize("bn_epilogue,precision", [(False, None), (True, None), (False, "f16")])
+def test_resnet18_batch2_fused_stem(bn_epilogue, precision):
+    """Without debug accumulators the stem conv, pad and max pool run as one kernel, also with
+    the ONNX importer's BatchNorm mul (a positive per-channel constant keeps the epilogue
+    monotone, so pooling the accumulators first is exact) and in the f16 graph (rounding to
+    f16 is monotone too)."""
+    def builder(batch, seed):
+        return models.resnet18(batch=batch, seed=seed, bn_epilogue=bn_epilogue)
+    g, _ = _quantized(builder, 2, precision=precision)
+    runner = Runner(g, RocmTarget())
+    exe = runner.executables("rocm")[0]
+    assert exe.kernel_counts.get("qconv2d_maxpool") == 1 and "maxpool2d" not in exe.kernel_counts
+    x = models.image_batch((2, 3, 224, 224), 5)
+    (got,) = runner.run({"x": x})
+    (want,) = G.run_graph(g, {"x": x})
+    assert bits_equal(got, want)
+
+
+# ---------------------------------------------------------------- C4 MobileNetV2
+
+def test_mobilenet_v2_batch1():
+    g, _ = _quantized(models.mobilenet_v2, 1, calib_batch=2)
+    runner = _compare(g, {"x": models.image_batch((1, 3, 224, 224), 5)}, fallback=False)
+    assert runner.devices == ["rocm"]
 
 
 def test_mobilenet_v2_batch2():
-    g, _ = _quantized(models.mobilenet_v2, 2, 0, (11, 12), dist="uniform")
+    g, _ = _quantized(models.mobilenet_v2, 2)
     runner = _compare(g, {"x": models.image_batch((2, 3, 224, 224), 5)}, fallback=False)
-    assert [s.device for s in runner.segments] == ["rocm"]
+    assert runner.devices == ["rocm"]
 
+
+def test_mobilenet_v2_batch128_rows():
+    _rows_match_small_run(models.mobilenet_v2, 128, [0, 7, 10, 23, 53, 64, 100, 127], "uniform", runs=2)
+
+
+# ---------------------------------------------------------------- other layouts and precisions
 
 @pytest.mark.parametrize("builder", [models.resnet18, models.mobilenet_v2])
 def test_onnx_layout_batch2(builder):
     """The CNNs as MIRA's ONNX importer lays them out: BatchNormalization as a per-channel mul +
     add after a bias-free conv (mira/frontends/onnx_import.py:423-431), fused into the conv
     epilogue.  Every op on rocm; accumulators and outputs bit-exact."""
-    g, _ = _quantized(lambda batch, seed: builder(batch=batch, seed=seed, bn_epilogue=True), 2, 0, (11, 12),
-                      dist="uniform")
+    g, _ = _quantized(lambda batch, seed: builder(batch=batch, seed=seed, bn_epilogue=True), 2)
     assert any(op.attrs.get("epilogue", ())[:1] == (("mul", 1, False),) for op in g.compute_ops())
     runner = _compare(g, {"x": models.image_batch((2, 3, 224, 224), 5)}, fallback=False)
-    assert [s.device for s in runner.segments] == ["rocm"]
+    assert runner.devices == ["rocm"]
 
 
 @pytest.mark.parametrize("builder,shape,dist", [(models.resnet18, (2, 3, 224, 224), "uniform"),
@@ -123,86 +210,24 @@ def test_f16_graph(builder, shape, dist):
     rounds its result to f16 as the reference's ops do.  Every op on rocm (the interface
     casts included); accumulators and outputs bit-exact against the oracle on the same
     f16 graph."""
-    gen = models.image_batch if dist == "uniform" else models.normal_batch
-    g = builder(batch=shape[0], seed=0)
-    passes.optimize(g, precision="f16")
-    quantize_w8a8(g, peaks=calibration_peaks(g, [{"x": gen(shape, s)} for s in (11, 12)]))
+    g, _ = _quantized(builder, shape[0], dist=dist, precision="f16")
     assert sum(op.result.type.dtype == "f16" for op in g.compute_ops()) > 3
-    runner = _compare(g, {"x": gen(shape, 5)}, fallback=False)
-    assert [s.device for s in runner.segments] == ["rocm"]
+    runner = _compare(g, {"x": _gen(dist)(shape, 5)}, fallback=False)
+    assert runner.devices == ["rocm"]
 
 
 def test_f16_mlp_mira_with_softmax_fallback():
-    g = models.mlp_mira(batch=64)
-    passes.optimize(g, precision="f16")
-    quantize_w8a8(g, [{"x": models.normal_batch((64, 784), s)} for s in (2, 3)])
+    g, _ = _quantized(models.mlp_mira, 64, (2, 3), "normal", precision="f16")
     runner = _compare(g, {"x": models.normal_batch((64, 784), 1)})
-    assert "rocm" in [s.device for s in runner.segments]
+    assert "rocm" in runner.devices
 
 
-def test_mlp50m_batch8():
-    g, _ = _quantized(models.mlp_50m, 8, 0, (2, 3))
-    _compare(g, {"x": models.normal_batch((8, 4096), 1)}, fallback=False)
-
-
-def _rows_match_small_run(builder, big, small_rows, seed, calib_seeds, dist, input_shape_tail, input_name="x"):
-    """Run the full-size batch on rocm; rerun chosen rows alone on the oracle with the same attrs."""
-    g_big, peaks = _quantized(builder, big, seed, calib_seeds, dist=dist, calib_batch=2)
-    gen = models.image_batch if dist == "uniform" else models.normal_batch
-    x = gen((big,) + input_shape_tail, 7)
-    runner = compile_graph(g_big, RocmTarget())
-    (out,) = runner.run_list([x])
-    g_small, _ = _quantized(builder, len(small_rows), seed, calib_seeds, dist=dist, peaks=peaks)
-    (want,) = G.run_graph(g_small, {input_name: x[small_rows]})
-    assert bits_equal(out[small_rows], want)
-    assert np.isfinite(out).all()
-
-
-def test_resnet18_batch256_rows():
-    _rows_match_small_run(models.resnet18, 256, [0, 255], 0, (11, 12), "uniform", (3, 224, 224))
-
-
-def test_resnet18_batch256_repeatable():
-    """Runs of one executable give identical outputs.  The epilogue stages each int32 tile in
-    LDS for other waves to read; a barrier that did not drain the LDS stores first once let
-    a few pixels per run read stale rows (different images on every run)."""
-    g, _ = _quantized(models.resnet18, 256, 0, (11, 12), dist="uniform", calib_batch=2)
-    runner = compile_graph(g, RocmTarget())
-    x = models.image_batch((256, 3, 224, 224), 7)
-    outs = [runner.run_list([x])[0] for _ in range(4)]
-    for o in outs[1:]:
-        assert bits_equal(o, outs[0])
-
-
-def test_mlp50m_batch4096_rows():
-    _rows_match_small_run(models.mlp_50m, 4096, [0, 1234, 4095], 0, (2, 3), "normal", (4096,))
-
-
-@pytest.mark.parametrize("bn_epilogue,precision", [(False, None), (True, None), (False, "f16")])
-def test_resnet18_batch2_fused_stem(bn_epilogue, precision):
-    """Without debug accumulators the stem conv, pad and max pool run as one kernel, also with
-    the ONNX importer's BatchNorm mul (a positive per-channel constant keeps the epilogue
-    monotone, so pooling the accumulators first is exact) and in the f16 graph (rounding to
-    f16 is monotone too)."""
-    g = models.resnet18(batch=2, seed=0, bn_epilogue=bn_epilogue)
-    passes.optimize(g, precision=precision)
-    quantize_w8a8(g, peaks=calibration_peaks(g, [{"x": models.image_batch((2, 3, 224, 224), s)} for s in (11, 12)]))
-    runner = compile_graph(g, RocmTarget())
-    exe = runner.segments[0].executable
-    assert exe.kernel_counts.get("qconv2d_maxpool") == 1 and "maxpool2d" not in exe.kernel_counts
-    x = models.image_batch((2, 3, 224, 224), 5)
-    (got,) = runner.run_list([x])
-    (want,) = G.run_graph(g, {"x": x})
-    assert bits_equal(got, want)
-
-
-# ---------------------------------------------------------------- character-level GPT decode (small-M qmatmul)
+# ---------------------------------------------------------------- C5 character-level GPT decode
 
 def _gpt_quantized(batch, peaks=None):
     cfg = models.GPTConfig()
     params = models.gpt_params(cfg, 0)
-    g = models.gpt_decode_step(cfg, batch, params)
-    passes.optimize(g)
+    g = LW.prepare(models.gpt_decode_step(cfg, batch, params))
     if peaks is None:
         calib = []
         for s in (2, 3):
@@ -211,14 +236,14 @@ def _gpt_quantized(batch, peaks=None):
             caches = [(r.standard_normal((batch, cfg.T, cfg.D)).astype(np.float32),
                        r.standard_normal((batch, cfg.T, cfg.D)).astype(np.float32)) for _ in range(cfg.L)]
             calib.append(models.gpt_step_feeds(cfg, params, toks, 16, caches))
-        peaks = calibration_peaks(g, calib)
-    quantize_w8a8(g, peaks=peaks)
+        peaks = LW.calibrate(g, calib)
+    LW.w8a8(g, peaks=peaks)
     return cfg, params, g, peaks
 
 
 def _gpt_runner(g, debug_acc=False):
-    runner = compile_graph(g, RocmTarget(debug_acc=debug_acc), fallback=G.CPUTarget())
-    assert "rocm" in [s.device for s in runner.segments]
+    runner = Runner(g, RocmTarget(debug_acc=debug_acc), fallback=G.CPUTarget())
+    assert "rocm" in runner.devices
     return runner
 
 
@@ -234,42 +259,41 @@ def test_gpt_decode_step_batch2():
     feeds = models.gpt_step_feeds(cfg, params, toks, 20, caches)
     runner = _compare(g, feeds)
     # the [b, 1, heads, d] head tensors are not images: they keep C order, no transposes
-    assert not any(k in seg.executable.kernel_counts for seg in runner.segments if seg.device == "rocm"
+    assert not any(k in exe.kernel_counts for exe in runner.executables("rocm")
                    for k in ("nchw_to_nhwc", "nhwc_to_nchw"))
     gelu_q = [op for op in g.compute_ops() if op.kind == "qmatmul" and op.attrs.get("epilogue", ())
               and op.attrs["epilogue"][0][0] == "gelu"]
-    assert len(gelu_q) == cfg.L and all("gelu" in runner.placement.reason[op] for op in gelu_q)
+    assert len(gelu_q) == cfg.L and all("gelu" in runner.reasons[op] for op in gelu_q)
 
 
-def test_gpt_greedy_decode_batch2():
-    """Autoregressive greedy decoding from a seeded 16-token prompt: rocm and the oracle produce
-    the same tokens and the same logits at every step."""
-    cfg, params, g, _ = _gpt_quantized(2)
-    prompt = np.random.default_rng(4).integers(0, cfg.V, (2, 16)).astype(np.int32)
+def test_gpt_greedy_decode_256_tokens_batch1():
+    """The configuration's decode: batch 1, a seeded 16-token prompt of uniform token ids, 256
+    generated tokens (context T = 272 = 16 + 256).  rocm and the oracle produce the same
+    tokens and the same logits, bit for bit, at every one of the 271 steps."""
+    cfg, params, g, _ = _gpt_quantized(1)
+    prompt = np.random.default_rng(4).integers(0, cfg.V, (1, 16)).astype(np.int32)
     runner = _gpt_runner(g)
-    names = [v.name for v in g.inputs]
-    got_tok, got_logits = models.gpt_decode(lambda f: runner.run_list([f[n] for n in names]), cfg, params, prompt, 8)
-    want_tok, want_logits = models.gpt_decode(lambda f: G.run_graph(g, f), cfg, params, prompt, 8)
-    assert np.array_equal(got_tok, want_tok)
+    got_tok, got_logits = models.gpt_decode(runner.run, cfg, params, prompt, 256)
+    want_tok, want_logits = models.gpt_decode(lambda f: G.run_graph(g, f), cfg, params, prompt, 256)
+    assert got_tok.shape == (1, 272) and np.array_equal(got_tok, want_tok)
+    assert len(got_logits) == 271
     for a, b in zip(got_logits, want_logits):
         assert bits_equal(a, b)
 
 
-def test_gpt_decode_step_batch512_rows():
+def test_gpt_greedy_decode_batch512_rows():
+    """Batch 512: 6 decode steps from seeded 16-token prompts; rows 0, 317 and 511 decoded
+    alone on the oracle (same attrs) give the same tokens and logits at every step."""
     cfg, params, g2, peaks = _gpt_quantized(2)
     _, _, g, _ = _gpt_quantized(512, peaks=peaks)
-    r = np.random.default_rng(5)
-    toks = r.integers(0, cfg.V, (512, cfg.T)).astype(np.int32)
-    caches = [(r.standard_normal((512, cfg.T, cfg.D)).astype(np.float32),
-               r.standard_normal((512, cfg.T, cfg.D)).astype(np.float32)) for _ in range(cfg.L)]
-    feeds = models.gpt_step_feeds(cfg, params, toks, 100, caches)
-    runner = _gpt_runner(g)
-    got = runner.run_list([feeds[v.name] for v in g.inputs])
-    rows = [0, 317, 511]
-    small = {k: (v[rows] if k != "mask" else v) for k, v in feeds.items()}
     _, _, g3, _ = _gpt_quantized(3, peaks=peaks)
-    want = G.run_graph(g3, small)
-    for a, b in zip(got, want):
+    prompt = np.random.default_rng(5).integers(0, cfg.V, (512, 16)).astype(np.int32)
+    rows = [0, 317, 511]
+    runner = _gpt_runner(g)
+    got_tok, got_logits = models.gpt_decode(runner.run, cfg, params, prompt, 6)
+    want_tok, want_logits = models.gpt_decode(lambda f: G.run_graph(g3, f), cfg, params, prompt[rows], 6)
+    assert np.array_equal(got_tok[rows], want_tok)
+    for a, b in zip(got_logits, want_logits):
         assert bits_equal(a[rows], b)
 
 
@@ -284,24 +308,24 @@ def test_gpt_decode_step_batch512_rows():
 W8_MODEL_TOL = 1e-4
 
 
-def _weight_only(g):
-    passes.optimize(g)
+def _weight_only(g, precision=None):
+    LW.prepare(g, precision)
     want = G.weight_only_attrs(g)
-    quantize_weights(g)
+    LW.weight_only(g)
     for op, a in want.items():
         assert op.kind == "dequantize" and np.array_equal(op.attrs["q"], a["q"])
     return g
 
 
 def _run_weight_only(g, feeds):
-    runner = compile_graph(g, RocmTarget(), fallback=G.CPUTarget())
-    got = runner.run_list([feeds[v.name] for v in g.inputs])
+    runner = Runner(g, RocmTarget(), fallback=G.CPUTarget())
+    got = runner.run(feeds)
     env = oracle_env(g, feeds)
     return runner, got, [env[v] for v in g.outputs]
 
 
 def _w8_launches(runner) -> int:
-    return sum(seg.executable.kernel_counts.get("w8matmul", 0) for seg in runner.segments if seg.device == "rocm")
+    return sum(exe.kernel_counts.get("w8matmul", 0) for exe in runner.executables("rocm"))
 
 
 @pytest.mark.parametrize("precision", [None, "f16"])
@@ -309,12 +333,9 @@ def test_weight_only_mlp50m_batch1(precision):
     """f32, and the f16 graph of MIRA's default precision: f16 weights (fl16(q * scale)),
     every result rounded to f16; f16 results may sit one f16 ulp apart where the f32 sums
     straddle a rounding boundary, hence the looser bound there."""
-    g = models.mlp_50m(batch=1)
-    if precision:
-        passes.optimize(g, precision=precision)
-    g = _weight_only(g)
+    g = _weight_only(models.mlp_50m(batch=1), precision)
     runner, (got,), (want,) = _run_weight_only(g, {"x": models.normal_batch((1, 4096), 3)})
-    assert [s.device for s in runner.segments] == ["rocm"] and _w8_launches(runner) == 4
+    assert runner.devices == ["rocm"] and _w8_launches(runner) == 4
     tol = 1e-2 if precision else W8_MODEL_TOL
     assert np.abs(got - want).max() <= tol * np.abs(want).max()
 
@@ -323,12 +344,11 @@ def test_weight_only_mlp_mira_batch64():
     """The reference's own int8 check (its tests/test_control_dynamic_quant.py:178-189) with
     the three matmuls on rocm: within 0.05 of the f32 model, argmax agreement above 0.9."""
     x = np.random.default_rng(0).standard_normal((64, 784)).astype(np.float32)
-    f32g = models.mlp_mira(batch=64)
-    passes.optimize(f32g)
+    f32g = LW.prepare(models.mlp_mira(batch=64))
     (ref,) = G.run_graph(f32g, {"x": x})
     g = _weight_only(models.mlp_mira(batch=64))
     runner, (got,), (want,) = _run_weight_only(g, {"x": x})
-    assert [s.device for s in runner.segments] == ["rocm", "cpu"] and _w8_launches(runner) == 3
+    assert runner.devices == ["rocm", "cpu"] and _w8_launches(runner) == 3
     assert np.abs(got - want).max() <= 1e-5            # softmax probabilities
     assert np.abs(got - ref).max() < 0.05 and (got.argmax(1) == ref.argmax(1)).mean() > 0.9
 

@@ -1,72 +1,74 @@
-"""Host-side logic of the rocm target on the CPU: the pass/quantizer mirrors, the
-partitioner and fallback, check() decisions, weight packing and broadcast modes.
-Structure tests follow the reference's own (tests/test_passes.py:51-72,
-tests/test_backends.py:40-55)."""
+"""Host-side logic on the CPU: the harness's lowering (against the oracle's
+restatement of MIRA's rewrite), the split between the rocm target and the CPU
+fallback, the target's check() decisions, weight packing, broadcast modes and
+the requant arithmetic.  Structure tests follow the reference's own
+(tests/test_passes.py:51-72, tests/test_backends.py:40-55)."""
 import numpy as np
 import pytest
 
+from harness import lowering as LW
+from harness import models
+from harness.graph import Graph
+from harness.runner import Runner, split
 from mira_amd import _lib as L
-from mira_amd import models, pack, passes
-from mira_amd.compiler import compile_graph
-from mira_amd.ir import Graph
-from mira_amd.partition import partition
-from mira_amd.quantize import quantize_array, quantize_w8a8, quantize_weights
+from mira_amd import pack
 from mira_amd.target import RocmTarget, _bcast_mode
 from oracle import golden as G
 
 
 def _dense_graph(bias_shape=(4,), relu=True, sub_from_bias=False):
-    g = Graph("t", [], [], [])
+    g = Graph("t")
     x = g.input("x", (8, 16))
     w = g.const(np.random.default_rng(0).standard_normal((16, 4)).astype(np.float32))
     b = g.const(np.random.default_rng(1).standard_normal(bias_shape).astype(np.float32))
-    y = g.add("matmul", [x, w])
-    y = g.add("sub", [b, y]) if sub_from_bias else g.add("add", [y, b])
+    y = g.op("matmul", [x, w])
+    y = g.op("sub", [b, y]) if sub_from_bias else g.op("add", [y, b])
     if relu:
-        y = g.add("relu", [y])
+        y = g.op("relu", [y])
     g.outputs = [y]
     return g
 
 
 def test_fusion_builds_epilogue():
     g = _dense_graph()
-    passes.optimize(g)
+    LW.prepare(g)
     (op,) = g.compute_ops()
     assert op.kind == "matmul" and [s[0] for s in op.attrs["epilogue"]] == ["add", "relu"]
 
 
 def test_fusion_respects_operand_order():
     g = _dense_graph(bias_shape=(8, 4), relu=False, sub_from_bias=True)
-    passes.optimize(g)
+    LW.prepare(g)
     (op,) = g.compute_ops()
     assert op.attrs["epilogue"][0][0] == "sub" and op.attrs["epilogue"][0][2] is True
 
 
 def test_fusion_skips_multi_use_results():
-    g = Graph("t", [], [], [])
+    g = Graph("t")
     x = g.input("x", (8, 16))
-    h = g.add("matmul", [x, g.const(np.ones((16, 16), np.float32))])
-    g.outputs = [g.add("add", [g.add("relu", [h]), h])]
-    passes.optimize(g)
+    h = g.op("matmul", [x, g.const(np.ones((16, 16), np.float32))])
+    g.outputs = [g.op("add", [g.op("relu", [h]), h])]
+    LW.prepare(g)
     assert "epilogue" not in g.compute_ops()[0].attrs
 
 
 def test_zero_bias_is_simplified_away():
     g = models.mlp_dense(batch=4)
-    passes.optimize(g)
+    LW.prepare(g)
     (op,) = g.compute_ops()
     assert op.kind == "matmul" and "epilogue" not in op.attrs
 
 
-def test_quantizer_matches_oracle():
-    g = models.mlp_mira(batch=4)
-    passes.optimize(g)
-    calib = [{"x": models.normal_batch((4, 784), s)} for s in (2, 3)]
+@pytest.mark.parametrize("builder,shape", [(models.mlp_mira, (4, 784)), (models.cnn_mira, (4, 1, 28, 28))])
+def test_quantizer_matches_oracle(builder, shape):
+    g = builder(batch=shape[0])
+    LW.prepare(g)
+    calib = [{g.inputs[0].name: models.normal_batch(shape, s)} for s in (2, 3)]
     want = G.w8a8_attrs(g, calib)
     wanted = [(op.inputs[0], want[op]) for op in g.ops if op in want]
-    n = quantize_w8a8(g, calib)
-    assert n == 3
-    qops = [op for op in g.ops if op.kind == "qmatmul"]
+    LW.w8a8(g, calib)
+    qops = [op for op in g.ops if op.kind in ("qmatmul", "qconv2d")]
+    assert len(qops) == 3
     for op, (_x, a) in zip(qops, wanted):
         assert np.array_equal(op.attrs["q"], a["q"]) and np.array_equal(op.attrs["w_scale"], a["w_scale"])
         assert op.attrs["epilogue"] == a["epilogue"]
@@ -76,7 +78,7 @@ def test_quantizer_matches_oracle():
 def test_quantize_array_matches_oracle():
     w = np.random.default_rng(3).standard_normal((64, 3, 7, 7)).astype(np.float32)
     for axis in (0, 1):
-        q1, s1 = quantize_array(w.reshape(64, -1) if axis == 1 else w, axis)
+        q1, s1 = LW.quantize_array(w.reshape(64, -1) if axis == 1 else w, axis)
         q2, s2 = G.quantize_array(w.reshape(64, -1) if axis == 1 else w, axis)
         assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
 
@@ -84,24 +86,18 @@ def test_quantize_array_matches_oracle():
 def test_weight_only_rewrite_matches_oracle():
     """mira/quantize.py:46-68 on examples/mlp.mira: the reference's own test expects three
     dequantize constants (its tests/test_control_dynamic_quant.py:178-189); the biases stay
-    f32; q, scale and axis equal the oracle's restatement; the byte counts are the weights'."""
+    f32; q, scale and axis equal the oracle's restatement."""
     g = models.mlp_mira(batch=4)
-    passes.optimize(g)
+    LW.prepare(g)
     want = G.weight_only_attrs(g)
-    log = []
-    before, after = quantize_weights(g, log=log)
+    assert LW.weight_only(g) == 3
     deq = [op for op in g.ops if op.kind == "dequantize"]
     assert len(deq) == 3 and set(deq) == set(want)
     for op in deq:
         a = want[op]
         assert np.array_equal(op.attrs["q"], a["q"]) and np.array_equal(op.attrs["scale"], a["scale"])
         assert op.attrs["axis"] == a["axis"] == 1 and op.attrs["dtype"] == "f32"
-    shapes = [(784, 512), (512, 256), (256, 10)]
-    assert before == sum(4 * k * n for k, n in shapes)
-    assert after == sum(k * n + 4 * n for k, n in shapes)
-    assert log[0][0] == "quantize-int8" and log[0][1].startswith("// weights: ")
-    with pytest.raises(ValueError, match="int8"):
-        quantize_weights(g, "int4")
+    assert [op.attrs["value"].shape for op in g.ops if op.kind == "const"] == [(512,), (256,), (10,)]
 
 
 def test_weight_only_rules():
@@ -109,20 +105,20 @@ def test_weight_only_rules():
     activation, feeds an elementwise op, or has fewer than 1024 elements stays f32."""
     rng = np.random.default_rng(0)
     conv = {"stride": (1, 1), "padding": (1, 1)}
-    g = Graph("t", [], [], [])
+    g = Graph("t")
     x = g.input("x", (2, 8, 6, 6))
     wc = g.const(rng.standard_normal((16, 8, 3, 3)).astype(np.float32))          # 1152 elements
     small = g.const(rng.standard_normal((8, 8, 3, 3)).astype(np.float32))       # 576 elements
-    h = g.add("conv2d", [x, wc], conv)
-    h = g.add("conv2d", [h, g.const(rng.standard_normal((8, 16, 3, 3)).astype(np.float32))], conv)
+    h = g.op("conv2d", [x, wc], conv)
+    h = g.op("conv2d", [h, g.const(rng.standard_normal((8, 16, 3, 3)).astype(np.float32))], conv)
     y = g.input("y", (40, 40))
     sq = g.const(rng.standard_normal((40, 40)).astype(np.float32))
-    m = g.add("matmul", [sq, sq])                                                # also the activation
+    m = g.op("matmul", [sq, sq])                                                # also the activation
     shared = g.const(rng.standard_normal((40, 40)).astype(np.float32))
-    m2 = g.add("add", [g.add("matmul", [y, shared]), shared])                  # also an add operand
-    g.outputs = [h, m, m2, g.add("conv2d", [x, small], conv)]
+    m2 = g.op("add", [g.op("matmul", [y, shared]), shared])                  # also an add operand
+    g.outputs = [h, m, m2, g.op("conv2d", [x, small], conv)]
     want = G.weight_only_attrs(g)
-    quantize_weights(g)
+    LW.weight_only(g)
     deq = {op for op in g.ops if op.kind == "dequantize"}
     assert deq == set(want)
     assert [op.attrs["axis"] for op in g.ops if op.kind == "dequantize"] == [0, 0]
@@ -131,13 +127,14 @@ def test_weight_only_rules():
 
 def test_to_f16_lowering():
     """mira/passes.py:206-253: a cast to f16 after each f32 input, f16 constants and results,
-    a cast back to f32 before each f32 output; float casts inside the graph disappear."""
-    g = Graph("t", [], [], [])
+    a cast back to f32 before each f32 output."""
+    g = Graph("t")
     x = g.input("x", (4, 16))
     w = g.const(np.full((16, 8), 0.1, np.float32))
-    h = g.add("cast", [g.add("relu", [g.add("matmul", [x, w])])], {"dtype": "f32"})
-    g.outputs = [g.add("add", [h, g.const(np.float32(1e-4))])]
-    passes.optimize(g, precision="f16", fuse=False)
+    h = g.op("relu", [g.op("matmul", [x, w])])
+    g.outputs = [g.op("add", [h, g.const(np.float32(1e-4))])]
+    LW.lower_f16(g)
+    g.check()
     ops = g.compute_ops()
     assert ops[0].kind == "cast" and ops[0].inputs[0] is x and ops[0].result.type.dtype == "f16"
     assert [op.kind for op in ops] == ["cast", "matmul", "relu", "add", "cast"]
@@ -154,8 +151,8 @@ def test_check_decisions_weight_only():
     t = RocmTarget()
     for batch, placed in ((4, True), (64, True), (65, False)):
         g = models.mlp_mira(batch=batch)
-        passes.optimize(g)
-        quantize_weights(g)
+        LW.prepare(g)
+        LW.weight_only(g)
         mm = [op for op in g.compute_ops() if op.kind == "matmul"]
         assert len(mm) == 3
         reasons = [t.check(op) for op in mm]
@@ -165,48 +162,50 @@ def test_check_decisions_weight_only():
 def test_check_decisions():
     t = RocmTarget()
     g = models.mlp_mira(batch=4)
-    passes.optimize(g)
-    quantize_w8a8(g, [{"x": models.normal_batch((4, 784), 2)}])
+    LW.prepare(g)
+    LW.w8a8(g, [{"x": models.normal_batch((4, 784), 2)}])
     reasons = {op.kind: t.check(op) for op in g.compute_ops()}
     assert reasons["qmatmul"] is None
     assert "softmax" in reasons["softmax"]
-    gg = Graph("t", [], [], [])
+    gg = Graph("t")
     x = gg.input("x", (2, 3))
-    m = gg.add("matmul", [x, gg.input("w", (3, 4))])
+    m = gg.op("matmul", [x, gg.input("w", (3, 4))])
     assert "BLAS" in t.check(m.producer)
     gelu = _dense_graph(relu=False)
-    y = gelu.add("gelu", [gelu.outputs[0]])
+    y = gelu.op("gelu", [gelu.outputs[0]])
     gelu.outputs = [y]
-    passes.optimize(gelu)
-    quantize_w8a8(gelu, [{"x": models.normal_batch((8, 16), 2)}])
+    LW.prepare(gelu)
+    LW.w8a8(gelu, [{"x": models.normal_batch((8, 16), 2)}])
     assert "not bit-reproducible" in t.check(gelu.compute_ops()[0])
 
 
-def test_partition_falls_back_and_requires_a_fallback_target():
+def test_split_falls_back_and_requires_a_fallback_target():
     g = models.mlp_mira(batch=4)
-    passes.optimize(g)
-    quantize_w8a8(g, [{"x": models.normal_batch((4, 784), 2)}])
-    segs, placement = partition(g, RocmTarget())
+    LW.prepare(g)
+    LW.w8a8(g, [{"x": models.normal_batch((4, 784), 2)}])
+    segs, reasons = split(g, RocmTarget())
     assert [s.device for s in segs] == ["rocm", "cpu"]
     soft = next(op for op in g.compute_ops() if op.kind == "softmax")
-    assert placement.device[soft] == "cpu"
+    assert "softmax" in reasons[soft]
+    rocm, cpu = segs
+    assert cpu.graph.inputs == rocm.graph.outputs and cpu.graph.outputs == g.outputs
+    assert all(op.is_constant_like for op in rocm.graph.ops if op.result in {v for o in rocm.graph.ops
+                                                                             for v in o.inputs[1:]})
 
     class NoCompile(RocmTarget):
         def compile(self, g):
             return object()
     with pytest.raises(RuntimeError, match="fallback"):
-        compile_graph(g, NoCompile())
+        Runner(g, NoCompile())
 
 
-def test_cost_model_keeps_tiny_segments_on_cpu():
-    g = Graph("t", [], [], [])
+def test_light_segments_stay_on_cpu():
+    g = Graph("t")
     x = g.input("x", (1, 4, 6, 6))
-    y = g.add("pad", [x], {"pads": ((0, 0), (0, 0), (1, 1), (1, 1)), "value": 0.0})
+    y = g.op("pad", [x], {"pads": ((0, 0), (0, 0), (1, 1), (1, 1)), "value": 0.0})
     g.outputs = [y]
-    segs, placement = partition(g, RocmTarget())
-    assert [s.device for s in segs] == ["cpu"]
-    segs, _ = partition(g, RocmTarget(), cost_model=False)
-    assert [s.device for s in segs] == ["rocm"]
+    segs, reasons = split(g, RocmTarget())
+    assert [s.device for s in segs] == ["cpu"] and "heavy" in reasons[y.producer]
 
 
 def test_pack_conv_layouts():
@@ -246,8 +245,8 @@ def test_broadcast_modes():
 
 def test_model_mac_counts():
     g = models.resnet18(batch=1)
-    passes.optimize(g)
-    quantize_w8a8(g, peaks=[1.0] * 21)
+    LW.prepare(g)
+    LW.w8a8(g, peaks=[1.0] * 21)
     assert models.conv_macs(g) == 1_814_073_344
     g = models.mlp_50m(batch=1)
     n_params = sum(op.attrs["value"].size for op in g.ops if op.is_const)
@@ -305,14 +304,13 @@ def test_gpt_decode_step_graph_and_placement():
     cfg = models.GPTConfig()
     params = models.gpt_params(cfg, 0)
     g = models.gpt_decode_step(cfg, 2, params)
-    passes.optimize(g)
+    LW.prepare(g)
     r = np.random.default_rng(2)
     toks = r.integers(0, cfg.V, (2, cfg.T)).astype(np.int32)
     caches = [(r.standard_normal((2, cfg.T, cfg.D)).astype(np.float32),
                r.standard_normal((2, cfg.T, cfg.D)).astype(np.float32)) for _ in range(cfg.L)]
     feeds = models.gpt_step_feeds(cfg, params, toks, 16, caches)
-    from mira_amd.quantize import calibration_peaks
-    quantize_w8a8(g, peaks=calibration_peaks(g, [feeds]))
+    LW.w8a8(g, [feeds])
     qops = [op for op in g.compute_ops() if op.kind == "qmatmul"]
     assert len(qops) == 6 * cfg.L + 1
     tgt = RocmTarget()

@@ -293,13 +293,13 @@ def test_epilogue_operand_order():
 # ---------------------------------------------------------------- calibration and rewrite
 
 def test_calibration_peaks_and_attrs():
-    from mira_amd.ir import Graph
-    g = Graph("t", [], [], [])
+    from harness.graph import Graph
+    g = Graph("t")
     x = g.input("x", (4, 3))
     w1 = np.array([[1, -2], [0.5, 1], [-1, 0]], np.float32)
     w2 = np.array([[2], [-1]], np.float32)
-    h = g.add("relu", [g.add("matmul", [x, g.const(w1)])])
-    y = g.add("matmul", [h, g.const(w2)])
+    h = g.op("relu", [g.op("matmul", [x, g.const(w1)])])
+    y = g.op("matmul", [h, g.const(w2)])
     g.outputs = [y]
     feeds = [{"x": np.array([[1, 2, 3]] * 4, np.float32)}, {"x": np.array([[-4, 0, 1]] * 4, np.float32)}]
     attrs = G.w8a8_attrs(g, feeds)
@@ -313,9 +313,9 @@ def test_calibration_peaks_and_attrs():
 
 
 def test_zero_peak_gives_unit_scale():
-    from mira_amd.ir import Graph
-    g = Graph("t", [], [], [])
+    from harness.graph import Graph
+    g = Graph("t")
     x = g.input("x", (2, 3))
-    g.outputs = [g.add("matmul", [x, g.const(np.ones((3, 2), np.float32))])]
+    g.outputs = [g.op("matmul", [x, g.const(np.ones((3, 2), np.float32))])]
     attrs = G.w8a8_attrs(g, [{"x": np.zeros((2, 3), np.float32)}])
     assert list(attrs.values())[0]["x_scale"] == 1.0
