@@ -657,3 +657,72 @@ def test_qconv2d_maxpool(lib, n, c, h, o, k, s, p, pool, pst, ppad, pval, neg):
     to_rows = lambda a: a.transpose(0, 2, 3, 1).reshape(M, o)
     assert bits_equal(y.cpu().numpy(), to_rows(want))
     assert bits_equal(yq.cpu().numpy()[:, :o], to_rows(G.quantize_activation(want, next_xs)).astype(np.int8))
+
+
+@pytest.mark.parametrize("kind,shape", [("matmul", (300, 512, 256)), ("matmul", (4096, 1152, 128)),
+                                        ("conv", (2, 64, 56, 56, 64, 3, 1, 1)),      # patch tiles
+                                        ("conv", (2, 256, 14, 14, 512, 3, 1, 1)),    # 128x256 tiles
+                                        ("conv", (4, 128, 28, 28, 256, 3, 2, 1))])   # stride 2
+def test_int8_epilogue_ties(lib, kind, shape):
+    """bias + ReLU -> int8 where every odd accumulator lands exactly on a rounding midpoint:
+    power-of-two scales make y / next_xs = acc / 2 + integer, so the requant must round each
+    of these exact ties half to even, as NumPy's rint does."""
+    torch = _torch()
+    rng = np.random.default_rng(sum(shape))
+    xs, wsv, next_xs = 2.0 ** -5, np.float32(2.0 ** -7), 2.0 ** -11
+    if kind == "matmul":
+        M, K, N = shape
+        xi = rng.integers(-1, 2, (M, K))
+        q = rng.integers(-3, 4, (K, N)).astype(np.int8)
+        o = N
+    else:
+        n, c, h, w, o, k, s, p = shape
+        xi = rng.integers(-1, 2, (n, c, h, w))
+        q = rng.integers(-3, 4, (o, c, k, k)).astype(np.int8)
+    x = (xi * xs).astype(np.float32)
+    ws = np.full(o, wsv, np.float32)
+    bias = (rng.integers(-20, 20, o) * next_xs).astype(np.float32)
+    steps = (("add", 1, False), ("relu", None, False))
+    scale = T(pack.combined_scale(xs, ws))
+    if kind == "matmul":
+        attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "epilogue": steps}
+        want = G.qmatmul([x, bias], attrs)
+        acc = G.qmatmul_acc(x, attrs)
+        lda = pack.row_stride_for(K)
+        xq = empty((M, lda), torch.int8)
+        L.check(lib.mr_quantize_rows(T(x).data_ptr(), M, K, K, xq.data_ptr(), lda, xs, stream()), "q")
+        bl = pack.pack_matmul(q)
+        b = T(pack.device_weights(bl))
+        ocp = pack.row_stride_for(o)
+        rows = M
+    else:
+        attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "stride": (s, s), "padding": (p, p),
+                 "epilogue": steps}
+        want = G.qconv2d([x, bias.reshape(o, 1, 1)], attrs)
+        acc = G.qconv2d_acc(x, attrs)
+        oh = ow = G.conv_out(h, k, s, p)
+        rows = n * oh * ow
+        want = want.transpose(0, 2, 3, 1).reshape(rows, o)
+        acc = acc.transpose(0, 2, 3, 1).reshape(rows, o)
+        cp = pack.c_pad_for(c)
+        xq = empty((n, h, w, cp), torch.int8)
+        L.check(lib.mr_quantize_nchw_nhwc(T(x).data_ptr(), n, c, h, w, xq.data_ptr(), cp, xs, stream()), "q")
+        bl = pack.pack_conv(q, cp)
+        b = T(pack.device_weights(bl))
+        ocp = pack.c_pad_for(o)
+    assert (np.abs(acc) < 2 ** 24).all()
+    odd = (acc.astype(np.int64) % 2 != 0) & (want > 0) & (want < 127 * next_xs)
+    assert odd.mean() > 0.15                      # plenty of exact ties in range
+    yq = empty((rows, ocp), torch.int8)
+    e = epilogue([("add", L.BC_COL, T(bias), 0, False), ("relu", 0, None, 0, False)], scale=scale, out_i8=yq,
+                 ldq=ocp, xs=next_xs)
+    if kind == "matmul":
+        L.check(lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), bl.shape[1], bl.shape[0], M, N, K, C.byref(e),
+                               stream()), "mr_qmatmul")
+    else:
+        g = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=cp, o=o, oh=oh, ow=ow, kh=k, kw=k, sh=s, sw=s, ph=p, pw=p, dh=1,
+                       dw=1)
+        L.check(lib.mr_qconv2d(xq.data_ptr(), C.byref(g), b.data_ptr(), bl.shape[1], bl.shape[0], C.byref(e),
+                               stream()), "mr_qconv2d")
+    sync()
+    assert bits_equal(yq.cpu().numpy()[:, :o], G.quantize_activation(want, next_xs).astype(np.int8))
