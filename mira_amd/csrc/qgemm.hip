@@ -71,7 +71,19 @@ struct GemmArgs {
   // A_PATCH: a tile is `tr` output rows of one image (tr * OW <= BM pixels);
   // its patch is pr x pc input pixels (rows oh0-PH .. oh0-PH+pr-1, columns -PW .. pc-PW-1)
   int32_t tr, rg_per_img, pr, pc, patch_slots;
+  // A_PATCH divisions by launch constants: C_pad / 16 = 1 << pu_shift, and
+  // n / pc == umulhi(n, pc_magic), n / OW == umulhi(n, ow_magic) with
+  // magic = ceil(2^32 / d), exact for the n the kernel divides (n * d < 2^32,
+  // checked on the host)
+  int32_t pu_shift;
+  uint32_t pc_magic, ow_magic;
 };
+
+// ceil(2^32 / d) for d >= 2: n / d == __umulhi(n, magic) whenever n * d < 2^32.  With
+// magic = (2^32 + e) / d, 0 <= e < d, n * magic / 2^32 = n / d + n * e / (d * 2^32), and
+// n * e < 2^32 keeps the added term under 1/d, the least distance from n / d up to the
+// next integer, so the floor is unchanged.
+static uint32_t div_magic(uint32_t d) { return static_cast<uint32_t>(((uint64_t(1) << 32) + d - 1) / d); }
 
 constexpr int BK = 64;
 
@@ -435,9 +447,9 @@ __global__ void __launch_bounds__(WM* WN * 64)
       const int slot = (wave * PATCH_OPS + j) * 64 + lane;
       const void* src = g_zero_page;
       if (slot < g.patch_slots) {
-        const int P = slot / pU;
-        const int chunk = (slot - P * pU) ^ patch_swz(P);
-        const int r = P / g.pc;
+        const int P = slot >> g.pu_shift;
+        const int chunk = (slot & (pU - 1)) ^ patch_swz(P);
+        const int r = static_cast<int>(__umulhi(static_cast<uint32_t>(P), g.pc_magic));
         const int ih = p_oh0 - g.PH + r;
         const int iw = P - r * g.pc - g.PW;
         if (unsigned(ih) < unsigned(g.H) && unsigned(iw) < unsigned(g.W))
@@ -464,7 +476,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
     for (int i = 0; i < FM; ++i) {
       int p = wm * TM + i * 32 + frag_row;
       if (p >= mvalid) p = 0;
-      const int orow = p / g.OW;
+      const int orow = static_cast<int>(__umulhi(static_cast<uint32_t>(p), g.ow_magic));
       p_pix0[i] = orow * g.pc + (p - orow * g.OW);
     }
   }
@@ -842,7 +854,14 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
     const int32_t tr = std::min(mr::patch_bm(G.o) / ow, oh);
     const int32_t pr = tr + G.kh - 1, pc = ow + G.kw - 1;
     const int64_t slots = int64_t(pr) * pc * (G.c_pad / 16);
-    if (slots * 16 <= mr::PATCH_MAX) {
+    // the kernel divides patch pixel indices (< pr * pc) by pc and tile rows (< patch_bm)
+    // by ow through multiplier magics, exact while n * d < 2^32
+    const bool magic_ok = pc >= 2 && ow >= 2 && uint64_t(pr) * pc * pc < (uint64_t(1) << 32) &&
+                          uint64_t(mr::patch_bm(G.o)) * ow < (uint64_t(1) << 32);
+    if (slots * 16 <= mr::PATCH_MAX && magic_ok) {
+      g.pu_shift = G.c_pad == 64 ? 2 : G.c_pad == 128 ? 3 : 4;
+      g.pc_magic = mr::div_magic(static_cast<uint32_t>(pc));
+      g.ow_magic = mr::div_magic(static_cast<uint32_t>(ow));
       g.tr = tr;
       g.rg_per_img = (oh + tr - 1) / tr;
       g.pr = pr;

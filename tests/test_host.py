@@ -318,3 +318,15 @@ def test_gpt_decode_step_graph_and_placement():
     assert len(rejected) == cfg.L and all(op.attrs["epilogue"][0][0] == "gelu" for op in rejected)
     logits, *kv = G.run_graph(g, feeds)
     assert logits.shape == (2, cfg.V) and np.isfinite(logits).all() and len(kv) == 2 * cfg.L
+
+
+def test_division_magic_is_exact():
+    """The patch loader divides by launch constants d as umulhi(n, ceil(2^32 / d)), which the
+    host allows only while n * d < 2^32: checked here for every d < 600 and n up to that
+    bound's edge (all n below 4096, a sample above)."""
+    rng = np.random.default_rng(0)
+    for d in range(2, 600):
+        m = ((1 << 32) + d - 1) // d
+        nmax = (1 << 32) // d - 1
+        n = np.concatenate([np.arange(min(nmax, 4096)), rng.integers(0, nmax, 4096), [nmax]]).astype(np.uint64)
+        assert np.array_equal((n * np.uint64(m)) >> np.uint64(32), n // np.uint64(d))
