@@ -459,6 +459,50 @@ def summarize_mfma(d: str) -> int:
     return 0
 
 
+SQ_PASS1 = ("SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_INST_LDS SQ_WAIT_ANY SQ_ACTIVE_INST_LDS SQ_INSTS_LDS "
+            "SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE")
+SQ_PASS2 = ("SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU SQ_INSTS_SALU SQ_INSTS_MFMA SQ_WAIT_INST_ANY "
+            "SQ_ACTIVE_INST_VALU SQ_LDS_DATA_FIFO_FULL SQ_INSTS_VMEM GRBM_GUI_ACTIVE")
+
+
+def summarize_sq(d: str) -> int:
+    """Per-kernel issue and wait counters from two rocprofv3 --pmc passes over the same command:
+    d/sq1 = SQ_PASS1, d/sq2 = SQ_PASS2 (`--output-format csv -d d/sqN -o run`).
+
+    mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * 1024 / 8) (the 1024 SIMDs' MFMA-busy
+    cycles over the 8 XCDs' active cycles); valu/salu/lds/vmem per mfma = instruction counts per
+    MFMA instruction; wait_any, wait_lds, lds_active = fractions of SQ_WAVE_CYCLES (summed over
+    resident waves); bank_conflict = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE."""
+    import csv
+    import collections
+    per = collections.defaultdict(lambda: collections.defaultdict(float))
+    launches = collections.defaultdict(set)
+    for sub in ("sq1", "sq2"):
+        for r in csv.DictReader(open(os.path.join(d, sub, "run_counter_collection.csv"))):
+            k = r["Kernel_Name"]
+            per[k][r["Counter_Name"]] += float(r["Counter_Value"])
+            launches[k].add((sub, r["Dispatch_Id"]))
+    print(f"{'kernel':60s} {'n':>3s} {'mfma_busy':>9s} {'valu/mf':>7s} {'salu/mf':>7s} {'lds/mf':>6s} "
+          f"{'vmem/mf':>7s} {'wait_any':>8s} {'wait_lds':>8s} {'lds_act':>7s} {'bankconf':>8s}")
+    rows = sorted(per.items(), key=lambda kv: -kv[1].get("GRBM_GUI_ACTIVE", 0.0))
+    for k, c in rows:
+        if "rocclr" in k or c.get("GRBM_GUI_ACTIVE", 0) <= 0:
+            continue
+        n = len([x for x in launches[k] if x[0] == "sq2"])
+        mf = c.get("SQ_INSTS_MFMA", 0.0)
+        wc = c.get("SQ_WAVE_CYCLES", 0.0) or 1.0
+        busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (c["GRBM_GUI_ACTIVE"] * 1024 / 8)
+
+        def per_mf(key):
+            return f"{c.get(key, 0.0) / mf:7.2f}" if mf else "      -"
+        name = k.replace("void ", "").replace("mr::", "")[:60]
+        print(f"{name:60s} {n:3d} {busy:9.3f} {per_mf('SQ_INSTS_VALU')} {per_mf('SQ_INSTS_SALU')} "
+              f"{per_mf('SQ_INSTS_LDS')[1:]} {per_mf('SQ_INSTS_VMEM')} {c.get('SQ_WAIT_ANY', 0) / wc:8.3f} "
+              f"{c.get('SQ_WAIT_INST_LDS', 0) / wc:8.3f} {c.get('SQ_ACTIVE_INST_LDS', 0) / wc:7.3f} "
+              f"{c.get('SQ_LDS_BANK_CONFLICT', 0) / max(1.0, c.get('SQ_LDS_IDX_ACTIVE', 0)):8.3f}")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -475,11 +519,15 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true", help="run the plain copy used to scale counters")
     ap.add_argument("--summarize-counters", metavar="DIR", help="summarize rocprofv3 --pmc CSV output in DIR")
     ap.add_argument("--summarize-mfma", metavar="DIR", help="MFMA utilisation from rocprofv3 --pmc CSV output in DIR/mfma")
+    ap.add_argument("--summarize-sq", metavar="DIR", help="issue/wait/LDS counters from rocprofv3 --pmc output in "
+                                                         "DIR/sq1 and DIR/sq2 (see SQ_PASS1, SQ_PASS2)")
     args = ap.parse_args()
     if args.summarize_counters:
         return summarize_counters(args.summarize_counters)
     if args.summarize_mfma:
         return summarize_mfma(args.summarize_mfma)
+    if args.summarize_sq:
+        return summarize_sq(args.summarize_sq)
     if args.copy_calibration:
         return copy_calibration()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
