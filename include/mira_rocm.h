@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MR_ABI_VERSION 3
+#define MR_ABI_VERSION 4
 
 enum mr_status {
   MR_OK = 0,
@@ -39,9 +39,12 @@ enum mr_status {
   MR_EUNSUPPORTED = 3 /* valid request the library has no kernel for */
 };
 
-/* Epilogue step functions: the fusable ops of mira/passes.py:151-152 that
- * have exact IEEE-754 single-precision semantics (UNARY/BINARY tables,
- * mira/ops.py:99-139).  relu == np.maximum(x, 0). */
+/* Epilogue step functions: the fusable ops of mira/passes.py:151-152
+ * (UNARY/BINARY tables, mira/ops.py:99-139).  ADD..RELU have exact IEEE-754
+ * single-precision semantics (relu == np.maximum(x, 0)).  GELU (the tanh form
+ * of mira/ops.py:94-96), SIGMOID (1 / (1 + exp(-x)), :102) and TANH (:103)
+ * call the device's expf/tanhf, whose results differ from NumPy's in the last
+ * bits: a caller that needs bit-exact results does not use them. */
 enum mr_epi_fn {
   MR_EPI_ADD = 1,
   MR_EPI_SUB = 2,
@@ -49,7 +52,10 @@ enum mr_epi_fn {
   MR_EPI_DIV = 4,
   MR_EPI_MAX = 5,
   MR_EPI_MIN = 6,
-  MR_EPI_RELU = 7
+  MR_EPI_RELU = 7,
+  MR_EPI_GELU = 8,
+  MR_EPI_SIGMOID = 9,
+  MR_EPI_TANH = 10
 };
 
 /* How an epilogue operand broadcasts onto the [rows, cols] result
@@ -64,7 +70,8 @@ enum mr_bcast {
 #define MR_MAX_EPI 8
 
 /* One step of mira/ops.py:192-199 epilogue_ref: acc = fn(acc, other), or
- * fn(other, acc) when swapped; `ptr` is unused for MR_EPI_RELU. */
+ * fn(other, acc) when swapped; `ptr` is unused for the unary steps
+ * (MR_EPI_RELU, MR_EPI_GELU, MR_EPI_SIGMOID, MR_EPI_TANH). */
 typedef struct mr_epi_step {
   int32_t fn;
   int32_t swapped;
@@ -238,6 +245,46 @@ int mr_nchw_to_nhwc_f32(const float* x, int32_t n, int32_t c, int32_t h, int32_t
                         float* y, void* stream);
 int mr_nhwc_to_nchw_f32(const float* x, int32_t n, int32_t c, int32_t h, int32_t w,
                         float* y, void* stream);
+
+/* ---- the float ops of a transformer decode step --------------------------
+ * Row-major (C order) f32 tensors; f16 results are rounded and stored as f32
+ * when out_f16 is set, as for every other op. */
+
+/* Replaces mira/ops.py:356-360 layernorm over the last axis of x [rows, d],
+ * bit for bit: NumPy's pairwise f32 sums for both means, each divided by the
+ * count in double precision, var + f32(eps), IEEE sqrt and division.  Writes
+ * y [rows, d] (if y) and the int8 copy yq [rows, ldq] = clip(rint(y / xs),
+ * +-127) of a following q-op's input (if yq, mira/ops.py:602-603). */
+int mr_layernorm_f32(const float* x, int64_t rows, int32_t d, const float* gamma,
+                     const float* beta, float eps, int32_t out_f16, float* y,
+                     int8_t* yq, int64_t ldq, float xs, void* stream);
+
+/* Replaces mira/ops.py:310-313 softmax over the last axis of x [rows, n]:
+ * exp(x - max) / sum.  Approximate: expf and the summation order are not
+ * NumPy's (relative error ~1e-6 per element). */
+int mr_softmax_f32(const float* x, int64_t rows, int32_t n, int32_t out_f16,
+                   float* y, void* stream);
+
+/* Replaces mira/ops.py:217-219 matmul of two float tensors with NumPy's
+ * batch broadcasting: for each batch index (nb <= 4 dimensions of extents
+ * bdim, element strides sa and sw in a and w, 0 where an operand
+ * broadcasts), [M, K] @ [K, N] in f32, then the epilogue over the
+ * [batches * M, N] result (scale must be NULL).  Approximate: the summation
+ * order is k-ascending with fused multiply-adds, not BLAS's. */
+int mr_bmm_f32(const float* a, const float* w, int32_t nb, const int64_t* bdim,
+               const int64_t* sa, const int64_t* sw, int64_t M, int64_t N,
+               int64_t K, const mr_epilogue* epi, void* stream);
+
+/* Replaces mira/ops.py:375 transpose (np.ascontiguousarray(np.transpose(x,
+ * perm))) for rank 1..4; exact (a copy). */
+int mr_transpose_f32(const float* x, int32_t rank, const int64_t* shape,
+                     const int32_t* perm, float* y, void* stream);
+
+/* One operand of mira/ops.py:403 concat: x viewed as [outer, inner] is copied
+ * into columns [at, at + inner) of y viewed as [outer, ld]; exact.  An empty
+ * operand (outer * inner == 0) is a no-op and its pointers may be NULL. */
+int mr_copy_rows_f32(const float* x, int64_t outer, int64_t inner, float* y,
+                     int64_t ld, int64_t at, void* stream);
 
 #ifdef __cplusplus
 }

@@ -10,11 +10,14 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "libmira_rocm.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 MAX_EPI = 8
 
 # enum mr_epi_fn
-EPI_FN = {"add": 1, "sub": 2, "mul": 3, "div": 4, "maximum": 5, "minimum": 6, "relu": 7}
+EPI_FN = {"add": 1, "sub": 2, "mul": 3, "div": 4, "maximum": 5, "minimum": 6, "relu": 7,
+          "gelu": 8, "sigmoid": 9, "tanh": 10}
+EPI_UNARY = ("relu", "gelu", "sigmoid", "tanh")
+EPI_APPROX = ("gelu", "sigmoid", "tanh")     # libm steps: not bit-identical to NumPy
 EPI_OUT_F16 = 1     # mr_epilogue.flags: round results to f16 (the op's dtype is f16)
 # enum mr_bcast
 BC_SCALAR, BC_COL, BC_ROW, BC_FULL = 0, 1, 2, 3
@@ -25,6 +28,7 @@ EXPORTS = [
     "mr_qmatmul", "mr_w8_matmul_f32", "mr_qconv2d", "mr_qconv2d_maxpool", "mr_dwconv2d_f32",
     "mr_maxpool2d_f32", "mr_mean_hw_f32", "mr_pad_hw_f32", "mr_round_f16_f32",
     "mr_nchw_to_nhwc_f32", "mr_nhwc_to_nchw_f32",
+    "mr_layernorm_f32", "mr_softmax_f32", "mr_bmm_f32", "mr_transpose_f32", "mr_copy_rows_f32",
 ]
 
 
@@ -73,6 +77,11 @@ _SIGS = {
     "mr_round_f16_f32": ([_p, _i64, _p, _p], C.c_int),
     "mr_nchw_to_nhwc_f32": ([_p, _i32, _i32, _i32, _i32, _p, _p], C.c_int),
     "mr_nhwc_to_nchw_f32": ([_p, _i32, _i32, _i32, _i32, _p, _p], C.c_int),
+    "mr_layernorm_f32": ([_p, _i64, _i32, _p, _p, _f32, _i32, _p, _p, _i64, _f32, _p], C.c_int),
+    "mr_softmax_f32": ([_p, _i64, _i32, _i32, _p, _p], C.c_int),
+    "mr_bmm_f32": ([_p, _p, _i32, _p, _p, _p, _i64, _i64, _i64, C.POINTER(Epilogue), _p], C.c_int),
+    "mr_transpose_f32": ([_p, _i32, _p, _p, _p, _p], C.c_int),
+    "mr_copy_rows_f32": ([_p, _i64, _i64, _p, _i64, _i64, _p], C.c_int),
 }
 
 

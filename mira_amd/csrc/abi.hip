@@ -44,8 +44,9 @@ int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out)
   out->has_scale = epi->scale != nullptr;
   for (int s = 0; s < epi->n_steps; ++s) {
     const mr_epi_step& st = epi->steps[s];
-    MR_REQUIRE(st.fn >= MR_EPI_ADD && st.fn <= MR_EPI_RELU, "epilogue step %d: unknown fn %d", s, st.fn);
-    if (st.fn != MR_EPI_RELU) {
+    MR_REQUIRE(st.fn >= MR_EPI_ADD && st.fn <= MR_EPI_TANH, "epilogue step %d: unknown fn %d", s, st.fn);
+    const bool unary = st.fn == MR_EPI_RELU || st.fn >= MR_EPI_GELU;
+    if (!unary) {
       MR_REQUIRE(st.ptr != nullptr, "epilogue step %d: operand pointer is NULL", s);
       MR_REQUIRE(st.mode >= MR_BC_SCALAR && st.mode <= MR_BC_FULL, "epilogue step %d: bad mode %d", s,
                  st.mode);

@@ -1,0 +1,290 @@
+// The float ops of a transformer decode step around its W8A8 projections
+// (examples/gpt_text.mira's `generate` body): layer normalisation, the f32
+// attention matmuls, softmax, and the transposes and concatenations that
+// reshape the key/value cache.  All operate on C-order (row-major) tensors.
+//
+// layernorm, transpose and concat reproduce mira/ops.py bit for bit: layernorm
+// is NumPy's pairwise f32 sums and single IEEE operations.  softmax and the f32
+// batched matmul do not: exp (libm) and BLAS's summation order cannot be
+// matched, so the rocm target runs them only when asked for approximate f32
+// ops, and their results agree with NumPy's to f32 rounding.
+#include "mr_common.hpp"
+#include "np_sum.hpp"
+
+namespace mr {
+
+// ---------------------------------------------------------------- layernorm
+
+// Correctly rounded f32 square root (NumPy's np.sqrt), whatever the compiler lowers sqrtf to
+// (clang's __fsqrt_rn is the hardware approximation, within 1 ulp).  Rounding to nearest
+// picks s when the true root lies between the midpoints m- and m+ to s's neighbours; a
+// midpoint has at most 25 significant bits, so m*m is exact in double and the comparison
+// with v is exact (never equal: m*m has more bits than a float).  A faithful first guess
+// is off by at most one ulp, so one correction suffices.
+__device__ inline float sqrt_rn(float v) {
+  float s = sqrtf(v);
+  if (!(v > 0.0f) || !(v < __builtin_inff())) return s;     // +-0, negative, NaN, inf: exact cases
+  const float dn = nextafterf(s, 0.0f), up = nextafterf(s, __builtin_inff());
+  const double x = static_cast<double>(v);
+  const double lo = 0.5 * (static_cast<double>(s) + static_cast<double>(dn));
+  const double hi = 0.5 * (static_cast<double>(s) + static_cast<double>(up));
+  if (__dmul_rn(lo, lo) > x) return dn;
+  if (__dmul_rn(hi, hi) < x) return up;
+  return s;
+}
+
+__device__ inline float mean_of_sum(float s, int d) {
+  return static_cast<float>(__ddiv_rn(static_cast<double>(__fadd_rn(0.0f, s)), static_cast<double>(d)));
+}
+
+// mira/ops.py:356-360 on [rows, d]: mu = mean(x), var = mean((x - mu)^2),
+// y = (x - mu) / sqrt(var + eps) * g + b, rounded to f16 when out_f16, and the
+// optional int8 copy clip(rint(y / xs), +-127) of the next q-op's input.
+// NumPy's mean is an add-reduce seeded with +0 over the pairwise f32 sum, then
+// the division of that f32 sum by the count in double precision, rounded back
+// to f32; eps is added in f32; the square root and the division are IEEE.  The
+// squared deviations are recomputed inside the sum, so no workspace is needed.
+// One wave per row: rows of at most 128 elements split the pairwise
+// accumulators over lanes, longer rows run the pairwise recursion on lane 0.
+__global__ void __launch_bounds__(64) layernorm_kernel(const float* __restrict__ x, int32_t d,
+                                                       const float* __restrict__ g, const float* __restrict__ b,
+                                                       float eps, int out_f16, float* __restrict__ y,
+                                                       int8_t* __restrict__ yq, int64_t ldq, float xs) {
+  const int64_t r = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* xr = x + r * d;
+  auto elem = [=](int64_t i) { return xr[i]; };
+  float mu;
+  if (d <= 128) {
+    mu = mean_of_sum(wave_pairwise_block(elem, d, lane), d);
+  } else {
+    float s = 0.0f;
+    if (lane == 0) s = pairwise_sum_of(elem, d);
+    mu = mean_of_sum(__shfl(s, 0), d);
+  }
+  auto sq = [=](int64_t i) {
+    const float t = __fsub_rn(xr[i], mu);
+    return __fmul_rn(t, t);
+  };
+  float var;
+  if (d <= 128) {
+    var = mean_of_sum(wave_pairwise_block(sq, d, lane), d);
+  } else {
+    float s = 0.0f;
+    if (lane == 0) s = pairwise_sum_of(sq, d);
+    var = mean_of_sum(__shfl(s, 0), d);
+  }
+  const float sd = sqrt_rn(__fadd_rn(var, eps));
+  for (int i = lane; i < d; i += 64) {
+    float v = __fadd_rn(__fmul_rn(__fdiv_rn(__fsub_rn(xr[i], mu), sd), g[i]), b[i]);
+    if (out_f16) v = round_f16(v);
+    if (y) y[r * d + i] = v;
+    if (yq) yq[r * ldq + i] = quantize_one(v, xs);
+  }
+}
+
+// ---------------------------------------------------------------- softmax (approximate)
+
+// mira/ops.py:308-311 over the last axis of [rows, n]: e = exp(x - max), e / sum(e).
+// One wave per row; the maximum is exact, exp and the sum's order are not NumPy's.
+__global__ void __launch_bounds__(256) softmax_kernel(const float* __restrict__ x, int64_t rows, int32_t n,
+                                                     int out_f16, float* __restrict__ y) {
+  const int64_t r = blockIdx.x * int64_t(blockDim.x / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const float* xr = x + r * n;
+  float* yr = y + r * n;
+  float m = -__builtin_inff();
+  for (int i = lane; i < n; i += 64) m = np_maximum(m, xr[i]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = np_maximum(m, __shfl_xor(m, o));
+  float s = 0.0f;
+  for (int i = lane; i < n; i += 64) {
+    const float e = expf(__fsub_rn(xr[i], m));
+    yr[i] = e;
+    s = __fadd_rn(s, e);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s = __fadd_rn(s, __shfl_xor(s, o));
+  for (int i = lane; i < n; i += 64) {
+    const float v = __fdiv_rn(yr[i], s);
+    yr[i] = out_f16 ? round_f16(v) : v;
+  }
+}
+
+// ---------------------------------------------------------------- batched f32 matmul (approximate)
+
+// mira/ops.py:217-219 for runtime operands: c[bt] = a[bt] @ w[bt] with the batch
+// index bt broadcast onto each operand through its own batch strides (sa, sw;
+// 0 for a broadcast dimension), then the epilogue on the [batches * M, N] result.
+// One thread per output element; f32 multiply-adds in k order.
+struct BmmArgs {
+  const float* a;
+  const float* w;
+  int64_t batches, M, N, K;
+  int32_t nb;                 // batch dimensions (<= 4)
+  int64_t bdim[4];            // batch extents, outermost first
+  int64_t sa[4], sw[4];       // element strides of each batch dimension in a and w
+};
+
+__global__ void __launch_bounds__(256) bmm_f32_kernel(const BmmArgs p, const EpiDev e) {
+  const int64_t total = p.batches * p.M * p.N;
+  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < total; t += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t n = t % p.N;
+    const int64_t row = t / p.N;          // bt * M + m
+    const int64_t m = row % p.M;
+    int64_t bt = row / p.M;
+    int64_t oa = 0, ow = 0;
+    for (int i = p.nb - 1; i >= 0; --i) {
+      const int64_t q = bt % p.bdim[i];
+      bt /= p.bdim[i];
+      oa += q * p.sa[i];
+      ow += q * p.sw[i];
+    }
+    const float* ar = p.a + oa + m * p.K;
+    const float* wc = p.w + ow + n;
+    float acc = 0.0f;
+    for (int64_t k = 0; k < p.K; ++k) acc = fmaf(ar[k], wc[k * p.N], acc);
+    const float y = epi_steps(e, acc, row, n);
+    if (e.out_f32) e.out_f32[row * e.ldo + n] = y;
+    if (e.out_i8) e.out_i8[row * e.ldq + n] = quantize_rcp(y, e.out_rxs);
+  }
+}
+
+// ---------------------------------------------------------------- transpose / concat
+
+// mira/ops.py:375: y = ascontiguousarray(transpose(x, perm)) for rank <= 4
+// (shapes padded with leading 1s to rank 4; perm over the padded axes).
+struct PermArgs {
+  int64_t oshape[4];    // output extents
+  int64_t istride[4];   // input element stride of the axis each output axis reads
+};
+
+__global__ void __launch_bounds__(256) transpose4_kernel(const float* __restrict__ x, const PermArgs p,
+                                                         float* __restrict__ y) {
+  const int64_t total = p.oshape[0] * p.oshape[1] * p.oshape[2] * p.oshape[3];
+  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < total; t += int64_t(gridDim.x) * blockDim.x) {
+    int64_t rest = t, off = 0;
+#pragma unroll
+    for (int i = 3; i >= 0; --i) {
+      off += (rest % p.oshape[i]) * p.istride[i];
+      rest /= p.oshape[i];
+    }
+    y[t] = x[off];
+  }
+}
+
+// One operand of mira/ops.py:402 concatenate: x viewed as [outer, inner] rows
+// lands in y's [outer, ld] rows at column offset `at`.
+__global__ void __launch_bounds__(256) copy_rows_kernel(const float* __restrict__ x, int64_t outer, int64_t inner,
+                                                        float* __restrict__ y, int64_t ld, int64_t at) {
+  const int64_t total = outer * inner;
+  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < total; t += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t r = t / inner;
+    y[r * ld + at + (t - r * inner)] = x[t];
+  }
+}
+
+static unsigned grid_1d(int64_t total, int block) {
+  int64_t g = (total + block - 1) / block;
+  const int64_t cap = int64_t(device_cu_count()) * 32;
+  return static_cast<unsigned>(g < 1 ? 1 : (g > cap ? cap : g));
+}
+
+}  // namespace mr
+
+extern "C" {
+
+int mr_layernorm_f32(const float* x, int64_t rows, int32_t d, const float* gamma, const float* beta, float eps,
+                     int32_t out_f16, float* y, int8_t* yq, int64_t ldq, float xs, void* stream) {
+  MR_REQUIRE(x && gamma && beta, "mr_layernorm_f32: NULL operand");
+  MR_REQUIRE(y || yq, "mr_layernorm_f32: no output");
+  MR_REQUIRE(rows >= 0 && d > 0, "mr_layernorm_f32: bad shape [%lld, %d]", (long long)rows, d);
+  if (yq) MR_REQUIRE(ldq >= d && xs > 0.0f, "mr_layernorm_f32: int8 output needs ldq >= d and xs > 0");
+  if (rows == 0) return MR_OK;
+  MR_REQUIRE(rows < (int64_t(1) << 31), "mr_layernorm_f32: too many rows");
+  hipLaunchKernelGGL(mr::layernorm_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), 0,
+                     static_cast<hipStream_t>(stream), x, d, gamma, beta, eps, out_f16, y, yq, ldq, xs);
+  MR_LAUNCH_CHECK("layernorm");
+  return MR_OK;
+}
+
+int mr_softmax_f32(const float* x, int64_t rows, int32_t n, int32_t out_f16, float* y, void* stream) {
+  MR_REQUIRE(x && y, "mr_softmax_f32: NULL pointer");
+  MR_REQUIRE(rows >= 0 && n > 0, "mr_softmax_f32: bad shape");
+  if (rows == 0) return MR_OK;
+  const int64_t blocks = (rows + 3) / 4;
+  MR_REQUIRE(blocks < (int64_t(1) << 31), "mr_softmax_f32: too many rows");
+  hipLaunchKernelGGL(mr::softmax_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, rows, n, out_f16, y);
+  MR_LAUNCH_CHECK("softmax");
+  return MR_OK;
+}
+
+int mr_bmm_f32(const float* a, const float* w, int32_t nb, const int64_t* bdim, const int64_t* sa, const int64_t* sw,
+               int64_t M, int64_t N, int64_t K, const mr_epilogue* epi, void* stream) {
+  MR_REQUIRE(a && w, "mr_bmm_f32: NULL operand");
+  MR_REQUIRE(nb >= 0 && nb <= 4 && (nb == 0 || (bdim && sa && sw)), "mr_bmm_f32: 0..4 batch dimensions");
+  MR_REQUIRE(M > 0 && N > 0 && K > 0, "mr_bmm_f32: bad sizes");
+  mr::BmmArgs p = {};
+  p.a = a;
+  p.w = w;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.nb = nb;
+  p.batches = 1;
+  for (int i = 0; i < nb; ++i) {
+    MR_REQUIRE(bdim[i] > 0 && sa[i] >= 0 && sw[i] >= 0, "mr_bmm_f32: bad batch dimension %d", i);
+    p.bdim[i] = bdim[i];
+    p.sa[i] = sa[i];
+    p.sw[i] = sw[i];
+    p.batches *= bdim[i];
+  }
+  mr::EpiDev e;
+  const int rc = mr::make_epi(epi, N, false, &e);
+  if (rc != MR_OK) return rc;
+  MR_REQUIRE(!e.out_acc, "mr_bmm_f32: no int32 accumulators");
+  hipLaunchKernelGGL(mr::bmm_f32_kernel, dim3(mr::grid_1d(p.batches * M * N, 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), p, e);
+  MR_LAUNCH_CHECK("bmm_f32");
+  return MR_OK;
+}
+
+int mr_transpose_f32(const float* x, int32_t rank, const int64_t* shape, const int32_t* perm, float* y, void* stream) {
+  MR_REQUIRE(x && y && shape && perm, "mr_transpose_f32: NULL argument");
+  MR_REQUIRE(rank >= 1 && rank <= 4, "mr_transpose_f32: rank %d not in 1..4", rank);
+  MR_REQUIRE(x != y, "mr_transpose_f32: in place is not supported");
+  int64_t s4[4], st4[4];
+  const int pad = 4 - rank;
+  for (int i = 0; i < 4; ++i) s4[i] = i < pad ? 1 : shape[i - pad];
+  st4[3] = 1;
+  for (int i = 2; i >= 0; --i) st4[i] = st4[i + 1] * s4[i + 1];
+  mr::PermArgs p = {};
+  bool seen[4] = {false, false, false, false};
+  for (int i = 0; i < 4; ++i) {
+    const int src = i < pad ? i : pad + perm[i - pad];
+    MR_REQUIRE(src >= 0 && src < 4 && !seen[src] && (i < pad) == (src < pad), "mr_transpose_f32: bad perm");
+    seen[src] = true;
+    p.oshape[i] = s4[src];
+    p.istride[i] = st4[src];
+  }
+  const int64_t total = s4[0] * s4[1] * s4[2] * s4[3];
+  if (total == 0) return MR_OK;
+  hipLaunchKernelGGL(mr::transpose4_kernel, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, p, y);
+  MR_LAUNCH_CHECK("transpose");
+  return MR_OK;
+}
+
+int mr_copy_rows_f32(const float* x, int64_t outer, int64_t inner, float* y, int64_t ld, int64_t at, void* stream) {
+  MR_REQUIRE(outer >= 0 && inner >= 0 && at >= 0 && at + inner <= ld, "mr_copy_rows_f32: bad extents");
+  if (outer * inner == 0) return MR_OK;      // an empty operand (its pointer may be NULL)
+  MR_REQUIRE(x && y, "mr_copy_rows_f32: NULL pointer");
+  hipLaunchKernelGGL(mr::copy_rows_kernel, dim3(mr::grid_1d(outer * inner, 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, outer, inner, y, ld, at);
+  MR_LAUNCH_CHECK("copy_rows");
+  return MR_OK;
+}
+
+}  // extern "C"

@@ -6,6 +6,7 @@
 // All tensors are NHWC inside a segment; threads run along channels so
 // every global access coalesces.
 #include "mr_common.hpp"
+#include "np_sum.hpp"
 
 namespace mr {
 
@@ -213,73 +214,6 @@ __global__ void __launch_bounds__(256) maxpool_kernel(const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------- mean over H*W
-
-// NumPy's float32 pairwise summation (numpy/_core/src/umath/loops_utils.h.src,
-// @TYPE@_pairwise_sum, PW_BLOCKSIZE 128) over n values spaced `stride` apart.
-__device__ float pairwise_block(const float* a, int64_t n, int64_t stride) {
-  if (n < 8) {
-    float res = -0.0f;
-    for (int64_t i = 0; i < n; ++i) res = __fadd_rn(res, a[i * stride]);
-    return res;
-  }
-  float r[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) r[j] = a[j * stride];
-  int64_t i = 8;
-  for (; i < n - (n % 8); i += 8) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = __fadd_rn(r[j], a[(i + j) * stride]);
-  }
-  float res = __fadd_rn(__fadd_rn(__fadd_rn(r[0], r[1]), __fadd_rn(r[2], r[3])),
-                        __fadd_rn(__fadd_rn(r[4], r[5]), __fadd_rn(r[6], r[7])));
-  for (; i < n; ++i) res = __fadd_rn(res, a[i * stride]);
-  return res;
-}
-
-// The recursion (split at n/2 rounded down to a multiple of 8, sum the two
-// halves) run with an explicit stack: depth <= 40 covers any int64 count.
-__device__ float pairwise_sum(const float* a, int64_t n, int64_t stride) {
-  if (n <= 128) return pairwise_block(a, n, stride);
-  int64_t off[40], cnt[40];
-  float left[40];
-  int state[40];
-  int sp = 0;
-  off[0] = 0;
-  cnt[0] = n;
-  state[0] = 0;
-  float ret = 0.0f;
-  while (true) {
-    if (cnt[sp] <= 128) {
-      ret = pairwise_block(a + off[sp] * stride, cnt[sp], stride);
-      --sp;
-      // unwind: finished children return into their parents
-      while (sp >= 0) {
-        if (state[sp] == 0) {
-          left[sp] = ret;
-          state[sp] = 1;
-          int64_t n2 = cnt[sp] / 2;
-          n2 -= n2 % 8;
-          off[sp + 1] = off[sp] + n2;
-          cnt[sp + 1] = cnt[sp] - n2;
-          state[sp + 1] = 0;
-          ++sp;
-          break;
-        }
-        ret = __fadd_rn(left[sp], ret);
-        --sp;
-      }
-      if (sp < 0) return ret;
-      continue;
-    }
-    int64_t n2 = cnt[sp] / 2;
-    n2 -= n2 % 8;
-    state[sp] = 0;
-    off[sp + 1] = off[sp];
-    cnt[sp + 1] = n2;
-    state[sp + 1] = 0;
-    ++sp;
-  }
-}
 
 // y[img, ch] = f32(f64(pairwise_sum) / f64(hw)): NumPy's mean divides the f32
 // sum by the intp count in a double-precision loop and casts back.

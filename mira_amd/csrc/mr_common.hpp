@@ -112,6 +112,23 @@ __device__ __forceinline__ float epi_binary(int fn, float a, float b) {
   }
 }
 
+// The unary steps with a libm call (mira/ops.py:94-103), each operation in
+// NumPy's order: gelu = (0.5 * x) * (1 + tanh(c * (x + 0.044715 * x^3))),
+// sigmoid = 1 / (1 + exp(-x)), tanh.  expf/tanhf and x*x*x for NumPy's powf
+// differ from NumPy's results in the last bits, so these steps are approximate.
+__device__ __noinline__ float epi_unary_approx(int fn, float x) {
+  switch (fn) {
+    case MR_EPI_GELU: {
+      const float x3 = __fmul_rn(__fmul_rn(x, x), x);
+      const float u = __fmul_rn(0.7978845608028654f, __fadd_rn(x, __fmul_rn(0.044715f, x3)));
+      return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(u)));
+    }
+    case MR_EPI_SIGMOID: return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-x)));
+    case MR_EPI_TANH: return tanhf(x);
+    default: return x;
+  }
+}
+
 // Device copy of mr_epilogue (passed by value as a kernel argument).
 struct EpiStepDev {
   int32_t fn;
@@ -178,6 +195,10 @@ __device__ __forceinline__ float epi_generic(const EpiDev& e, float y, int64_t r
     const int fn = e.steps[s].fn;
     if (fn == MR_EPI_RELU) {
       y = np_maximum(y, 0.0f);
+      continue;
+    }
+    if (fn >= MR_EPI_GELU) {
+      y = epi_unary_approx(fn, y);
       continue;
     }
     const float* p = e.steps[s].ptr;

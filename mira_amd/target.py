@@ -104,6 +104,9 @@ IMAGE_OPS = ("qconv2d", "conv2d", "maxpool2d", "pad", "reduce_mean")
 W8_MAX_ROWS = 64     # mr_w8_matmul_f32 streams the weights once per 8 rows: decode shapes only
 
 
+_UNARY_CODES = {L.EPI_FN[f] for f in L.EPI_UNARY}
+
+
 def _ptr(t) -> int:
     return 0 if t is None else t.data_ptr()
 
@@ -113,9 +116,14 @@ class RocmTarget:
     name = "rocm"
     supports_control_flow = False
 
-    def __init__(self, device: int = 0, debug_acc: bool = False):
+    def __init__(self, device: int = 0, debug_acc: bool = False, approx_f32: bool = False):
+        """approx_f32: also run the float ops whose NumPy results depend on libm or on BLAS's
+        summation order (softmax, f32 matmul of two float tensors, and gelu/sigmoid/tanh
+        epilogue steps).  Their results then agree with the reference's to f32 rounding
+        (relative ~1e-6), not bit for bit; every other op stays bit-exact."""
         self.device = device
         self.debug_acc = debug_acc
+        self.approx_f32 = approx_f32
 
     # ---------------------------------------------------------------- check
 
@@ -154,11 +162,40 @@ class RocmTarget:
             if op.inputs[0].type.rank != 4 or axes != [2, 3]:
                 return "reduce_mean runs on rocm only over H and W (global average pooling)"
             return None
-        if k == "reshape":
+        if k in ("reshape", "concat"):
+            return None
+        if k == "transpose":
+            if not 1 <= op.inputs[0].type.rank <= 4:
+                return "transpose runs on rocm for rank 1..4"
+            return None
+        if k == "layernorm":
+            return None
+        if k == "softmax":
+            if not self.approx_f32:
+                return "softmax calls exp (libm): not bit-reproducible on rocm (approx_f32 runs it)"
+            r = op.inputs[0].type.rank
+            if r == 0 or op.attrs["axis"] % r != r - 1:
+                return "softmax runs on rocm over the last axis"
             return None
         if k == "matmul":
-            return self._check_w8_matmul(op)
+            w = op.inputs[1]
+            if w.producer is not None and w.producer.kind == "dequantize":
+                return self._check_w8_matmul(op)
+            return self._check_f32_matmul(op)
         return f"'{k}' has no rocm kernel"
+
+    def _check_f32_matmul(self, op: "Op") -> Optional[str]:
+        """matmul of two float tensors (attention scores and context): mr_bmm_f32 in the
+        approximate mode only (BLAS's summation order is not reproducible)."""
+        if not self.approx_f32:
+            return ("f32 matmul stays on the CPU (its summation order is BLAS's, not reproducible bit for bit) "
+                    "unless its weight is an int8 weight-only constant or approx_f32 is set")
+        x, w = op.inputs[0], op.inputs[1]
+        if x.type.dtype not in FLOAT_DTYPES or w.type.dtype not in FLOAT_DTYPES:
+            return "f32 matmul needs float operands"
+        if len(op.result.type.shape) - 2 > 4:
+            return "f32 matmul runs on rocm for at most 4 batch dimensions"
+        return self._check_epilogue(op, op.result.type.shape, False, first_operand=2)
 
     def _check_w8_matmul(self, op: "Op") -> Optional[str]:
         """Decode-shaped matmuls of the weight-only int8 mode (mira/quantize.py:45-68): an f32
@@ -180,8 +217,10 @@ class RocmTarget:
 
     def _check_epilogue(self, op: "Op", shape: tuple, is_conv: bool, first_operand: int = 1) -> Optional[str]:
         for fn, idx, _sw in op.attrs.get("epilogue", ()):
-            if fn not in EPI_FNS:
-                return f"epilogue step '{fn}' is not bit-reproducible on rocm (libm)"
+            if fn in L.EPI_APPROX and not self.approx_f32:
+                return f"epilogue step '{fn}' calls libm: not bit-reproducible on rocm (approx_f32 runs it)"
+            if fn not in EPI_FNS and fn not in L.EPI_APPROX:
+                return f"epilogue step '{fn}' has no rocm implementation"
             if idx is None:
                 continue
             v = op.inputs[idx]
@@ -316,6 +355,7 @@ class RocmExecutable:
                 lst = self.need_i8.setdefault(v, [])
                 lst += [s for s in self.need_i8.get(r, []) if s not in lst]
         self.staging: dict["Value", object] = {}
+        self.canon: dict["Value", object] = {}     # C-order copies of NHWC values (_c_order)
         for v in g.inputs:
             self._emit_input(v)
         for op in g.ops:
@@ -489,7 +529,7 @@ class RocmExecutable:
         n = 8 * cols if e.scale else 0
         for i in range(e.n_steps):
             st = e.steps[i]
-            if st.fn != L.EPI_FN["relu"]:
+            if st.fn not in _UNARY_CODES:
                 n += {L.BC_SCALAR: 4, L.BC_COL: 4 * cols, L.BC_ROW: 4 * rows, L.BC_FULL: 4 * rows * cols}[st.mode]
         if e.out_f32:
             n += 4 * rows * cols
@@ -606,6 +646,12 @@ class RocmExecutable:
         self._finish_i8(out, fused)
 
     def _emit_matmul(self, op: "Op") -> None:
+        w = op.inputs[1]
+        if w.producer is not None and w.producer.kind == "dequantize":
+            return self._emit_w8_matmul(op)
+        return self._emit_bmm(op)
+
+    def _emit_w8_matmul(self, op: "Op") -> None:
         """Weight-only int8 matmul (checked by _check_w8_matmul): the int8 weights are packed
         and uploaded once with their f32 scales; each run streams them through the
         mr_w8_matmul_f32 kernel."""
@@ -844,6 +890,166 @@ class RocmExecutable:
                 if xs in x.i8:
                     d.i8[xs] = x.i8[xs]
         self._finish_i8(d, None)
+
+    # ---------------------------------------------------------------- float ops of a decode step
+
+    def _c_order(self, v: "Value"):
+        """v's f32 values in the graph's C order (an NHWC image is converted once)."""
+        torch = _t()
+        d = self._src(v)
+        if d.f32 is None:
+            raise L.RocmError(f"{v} has no f32 copy on the device")
+        if not d.nhwc:
+            return d.f32
+        if v not in self.canon:
+            n, c, h, w = v.type.shape
+            t = torch.empty((n, c, h, w), dtype=torch.float32, device=self.dev)
+            lib, xt = self.lib, d.f32
+            self._add("nhwc_to_nchw", lambda s: L.check(lib.mr_nhwc_to_nchw_f32(
+                xt.data_ptr(), n, c, h, w, t.data_ptr(), s), "mr_nhwc_to_nchw_f32"), nbytes=8 * n * c * h * w)
+            self.canon[v] = t
+        return self.canon[v]
+
+    def _c_order_out(self, op: "Op"):
+        """Allocate op's result and return the buffer its kernel writes in C order: the f32
+        copy itself, or a temporary that _publish converts when the result is stored NHWC."""
+        torch = _t()
+        out = self._new_dv(op.result)
+        shape = op.result.type.shape
+        if out.nhwc:
+            return out, torch.empty(shape, dtype=torch.float32, device=self.dev)
+        if out.f32 is None:
+            out.f32 = torch.empty(shape, dtype=torch.float32, device=self.dev)
+        return out, out.f32
+
+    def _publish(self, out: DevValue, t) -> None:
+        """Finish a result written in C order: the NHWC copy of an image, then the int8 copies."""
+        if out.nhwc:
+            torch = _t()
+            n, c, h, w = out.value.type.shape
+            if out.f32 is None:
+                out.f32 = torch.empty((n, h, w, c), dtype=torch.float32, device=self.dev)
+            lib, yt = self.lib, out.f32
+            self._add("nchw_to_nhwc", lambda s: L.check(lib.mr_nchw_to_nhwc_f32(
+                t.data_ptr(), n, c, h, w, yt.data_ptr(), s), "mr_nchw_to_nhwc_f32"), nbytes=8 * n * c * h * w)
+        self._finish_i8(out, None)
+
+    def _emit_layernorm(self, op: "Op") -> None:
+        """mira/ops.py:356-360, bit-exact; the first int8 copy a q-op consumer needs is written
+        by the same kernel."""
+        torch = _t()
+        xv = op.inputs[0]
+        x = self._c_order(xv)
+        gm, bt = self._c_order(op.inputs[1]), self._c_order(op.inputs[2])
+        d = xv.type.shape[-1]
+        rows = xv.type.numel // d
+        out = self._new_dv(op.result)
+        wants = self.need_i8.get(op.result, [])
+        fused = wants[0] if wants and not out.nhwc else None
+        yq, ld = None, 0
+        if fused is not None:
+            ld = out.i8_ld()
+            yq = torch.empty((out.rows, ld), dtype=torch.int8, device=self.dev)
+            out.i8[fused] = (yq, ld)
+        if out.nhwc:
+            y = torch.empty(op.result.type.shape, dtype=torch.float32, device=self.dev)
+        else:
+            if out.f32 is None and yq is None:
+                out.f32 = torch.empty(op.result.type.shape, dtype=torch.float32, device=self.dev)
+            y = out.f32
+        eps, f16 = float(op.attrs["eps"]), int(op.result.type.dtype == "f16")
+        lib, xs = self.lib, (fused if fused is not None else 1.0)
+        self._add("layernorm", lambda s: L.check(lib.mr_layernorm_f32(
+            x.data_ptr(), rows, d, gm.data_ptr(), bt.data_ptr(), eps, f16, _ptr(y), _ptr(yq), ld, xs, s),
+            "mr_layernorm_f32"),
+            nbytes=4 * rows * d + 8 * d + (4 * rows * d if y is not None else 0) + rows * ld)
+        if out.nhwc:
+            self._publish(out, y)
+        else:
+            self._finish_i8(out, fused)
+
+    def _emit_softmax(self, op: "Op") -> None:
+        """mira/ops.py:310-313 over the last axis (approx_f32 only)."""
+        xv = op.inputs[0]
+        x = self._c_order(xv)
+        n = xv.type.shape[-1]
+        rows = xv.type.numel // n
+        out, y = self._c_order_out(op)
+        lib, f16 = self.lib, int(op.result.type.dtype == "f16")
+        self._add("softmax", lambda s: L.check(lib.mr_softmax_f32(x.data_ptr(), rows, n, f16, y.data_ptr(), s),
+                                               "mr_softmax_f32"), nbytes=8 * rows * n)
+        self._publish(out, y)
+
+    def _emit_transpose(self, op: "Op") -> None:
+        """mira/ops.py:375.  A permutation that keeps the order of the axes longer than 1 moves
+        no data: the result shares the input's f32 buffer."""
+        xv, r = op.inputs[0], op.result
+        x = self._c_order(xv)
+        shape, perm = tuple(xv.type.shape), tuple(op.attrs["perm"])
+        moved = [p for p in perm if shape[p] != 1]
+        if moved == sorted(moved) and r not in self.images:
+            d = DevValue(r, nhwc=False, f32=x.view(r.type.shape))
+            self.dv[r] = d
+            self._finish_i8(d, None)
+            return
+        rank = len(shape)
+        cs = (C.c_int64 * rank)(*shape)
+        cp = (C.c_int32 * rank)(*perm)
+        self.keep += [cs, cp]
+        out, y = self._c_order_out(op)
+        lib = self.lib
+        self._add("transpose", lambda s: L.check(lib.mr_transpose_f32(x.data_ptr(), rank, cs, cp, y.data_ptr(), s),
+                                                 "mr_transpose_f32"), nbytes=8 * xv.type.numel)
+        self._publish(out, y)
+
+    def _emit_concat(self, op: "Op") -> None:
+        """mira/ops.py:403: each operand's [outer, inner] rows land at their column offset."""
+        r = op.result
+        rank = r.type.rank
+        axis = op.attrs["axis"] % rank
+        out, y = self._c_order_out(op)
+        outer = int(np.prod(r.type.shape[:axis], dtype=np.int64))
+        ld = int(np.prod(r.type.shape[axis:], dtype=np.int64))
+        at = 0
+        lib = self.lib
+        for v in op.inputs:
+            x = self._c_order(v)
+            inner = int(np.prod(v.type.shape[axis:], dtype=np.int64))
+            if outer * inner == 0:
+                continue
+            self._add("concat", lambda s, x=x, inner=inner, at=at: L.check(lib.mr_copy_rows_f32(
+                x.data_ptr(), outer, inner, y.data_ptr(), ld, at, s), "mr_copy_rows_f32"), nbytes=8 * outer * inner)
+            at += inner
+        self._publish(out, y)
+
+    def _emit_bmm(self, op: "Op") -> None:
+        """f32 matmul of two float tensors with NumPy's batch broadcasting (mira/ops.py:217-219;
+        approx_f32 only), the epilogue fused."""
+        av, wv = op.inputs[0], op.inputs[1]
+        a, w = self._c_order(av), self._c_order(wv)
+        rs = tuple(op.result.type.shape)
+        nb = len(rs) - 2
+        M, N, K = rs[-2], rs[-1], av.type.shape[-1]
+
+        def batch_strides(shape):
+            full = (1,) * (len(rs) - len(shape)) + tuple(shape)
+            return [0 if full[i] == 1 else int(np.prod(full[i + 1:], dtype=np.int64)) for i in range(nb)]
+
+        bdim = (C.c_int64 * max(nb, 1))(*rs[:nb])
+        sa = (C.c_int64 * max(nb, 1))(*batch_strides(av.type.shape))
+        sw = (C.c_int64 * max(nb, 1))(*batch_strides(wv.type.shape))
+        self.keep += [bdim, sa, sw]
+        out = self._new_dv(op.result)
+        if out.nhwc:
+            raise L.RocmError("an f32 matmul result read as an image has no rocm layout")
+        e, fused = self._epilogue(op, out, False, 2, None)
+        batches = int(np.prod(rs[:nb], dtype=np.int64))
+        lib = self.lib
+        self._add("bmm_f32", lambda s: L.check(lib.mr_bmm_f32(
+            a.data_ptr(), w.data_ptr(), nb, bdim, sa, sw, M, N, K, C.byref(e), s), "mr_bmm_f32"),
+            nbytes=4 * (av.type.numel + wv.type.numel) + self._epi_bytes(e, batches * M, N),
+            nops=2 * batches * M * N * K)
+        self._finish_i8(out, fused)
 
     # ---------------------------------------------------------------- run
 

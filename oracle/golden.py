@@ -37,7 +37,9 @@ def _native_or_f32(x: np.ndarray) -> np.ndarray:
 # ---------------------------------------------------------------- elementwise (mira/ops.py:94-172)
 
 def _gelu(x):
-    """mira/ops.py:94-96 (tanh approximation).  Parity unpinned on device (libm tanh)."""
+    """mira/ops.py:94-96 (tanh approximation).  Pinned by float64 closed forms (gelu(1) =
+    0.8411920 for the tanh form); its last bits are libm's tanh, so device results are
+    compared within a tolerance."""
     return 0.5 * x * (1.0 + np.tanh(0.7978845608028654 * (x + 0.044715 * x ** 3)))
 
 
@@ -156,14 +158,18 @@ def reduce(kind: str, xs: list, a: dict) -> np.ndarray:
 
 
 def softmax(xs: list, a: dict) -> np.ndarray:
-    """mira/ops.py:304-308.  libm exp: parity unpinned beyond tolerance."""
+    """mira/ops.py:310-313.  Pinned by closed forms (equal logits give fl32(1/n), a two-logit
+    row its exact probabilities, no overflow for large logits); the last bits of exp are
+    libm's, so device results are compared within a tolerance."""
     x = f32(xs[0])
     e = np.exp(x - x.max(axis=a["axis"], keepdims=True))
     return (e / e.sum(axis=a["axis"], keepdims=True)).astype(xs[0].dtype)
 
 
 def layernorm(xs: list, a: dict) -> np.ndarray:
-    """mira/ops.py:356-360.  Parity unpinned beyond tolerance."""
+    """mira/ops.py:356-360.  Pinned bit for bit by a scalar restatement (pairwise means seeded
+    with +0, float64 division by the count, one float32 operation per step) and by closed forms
+    (constant rows give b, [a, -a] gives +-g + b, unit mean square with eps = 0)."""
     x, g, b = (f32(v) for v in xs)
     mu = x.mean(axis=-1, keepdims=True)
     var = ((x - mu) ** 2).mean(axis=-1, keepdims=True)

@@ -1,0 +1,323 @@
+"""The float ops of a transformer decode step on rocm, through the C ABI and through the target.
+
+layernorm, transpose and concat are bit-exact against the oracle (they are single IEEE
+operations and copies).  softmax, the f32 batched matmul and the gelu/sigmoid/tanh epilogue
+steps call libm or sum in another order than NumPy/BLAS; they run only in the target's
+approx_f32 mode and are checked within the tolerances stated in each test.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from harness import lowering as LW
+from harness import models
+from harness.runner import Runner
+from mira_amd import _lib as L
+from mira_amd import pack
+from mira_amd.target import RocmTarget
+from oracle import golden as G
+
+from conftest import bits_equal
+from gpu_util import T, empty, epilogue, oracle_env, stream, sync
+
+pytestmark = pytest.mark.gpu
+
+# f32 results of the approximate ops: |got - want| <= RTOL * |want| + ATOL * scale, where
+# scale is the magnitude the result is computed from (see each test)
+RTOL = 1e-5
+ATOL = 1e-6
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _close(got, want, scale=1.0, rtol=RTOL, atol=ATOL):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    assert got.shape == want.shape
+    err = np.abs(got - want) - (rtol * np.abs(want) + atol * np.asarray(scale, np.float64))
+    assert err.max() <= 0, f"max excess {err.max():.3g}"
+
+
+# ---------------------------------------------------------------- layernorm (bit-exact)
+
+@pytest.mark.parametrize("rows,d", [(1, 64), (3, 1), (5, 7), (2, 8), (300, 100), (7, 128), (4, 129), (2, 768),
+                                    (3, 1029), (1, 4096)])
+@pytest.mark.parametrize("f16", [False, True])
+def test_layernorm_bit_exact(lib, rows, d, f16):
+    torch = _torch()
+    rng = np.random.default_rng(rows * 1000 + d)
+    x = (rng.standard_normal((rows, d)) * rng.uniform(0.05, 40) + rng.uniform(-10, 10)).astype(np.float32)
+    if rows >= 3:
+        x[1] = 2.5                              # constant row: variance 0
+        x[2, : d // 2] *= 100 if f16 else 1e6   # wide dynamic range (f16 stays finite)
+    g = rng.standard_normal(d).astype(np.float32)
+    b = rng.standard_normal(d).astype(np.float32)
+    if f16:
+        x, g, b = (a.astype(np.float16).astype(np.float32) for a in (x, g, b))
+    want = G.layernorm([x.astype(np.float16), g.astype(np.float16), b.astype(np.float16)] if f16 else [x, g, b],
+                       {"eps": 1e-5}).astype(np.float32)
+    xs = np.float32(0.0173)
+    ld = pack.row_stride_for(d)
+    y = empty((rows, d), torch.float32)
+    yq = empty((rows, ld), torch.int8)
+    xd, gd, bd = T(x), T(g), T(b)          # named: a temporary's memory could be reused before the kernel runs
+    L.check(lib.mr_layernorm_f32(xd.data_ptr(), rows, d, gd.data_ptr(), bd.data_ptr(), 1e-5, int(f16),
+                                 y.data_ptr(), yq.data_ptr(), ld, float(xs), stream()), "layernorm")
+    sync()
+    assert bits_equal(y.cpu().numpy(), want)
+    assert bits_equal(yq.cpu().numpy()[:, :d], G.quantize_activation(want, xs).astype(np.int8))
+
+
+def test_layernorm_int8_only_and_errors(lib):
+    torch = _torch()
+    x = np.random.default_rng(3).standard_normal((6, 48)).astype(np.float32)
+    g, b = np.ones(48, np.float32), np.zeros(48, np.float32)
+    yq = empty((6, 64), torch.int8)
+    xd, gd, bd = T(x), T(g), T(b)
+    L.check(lib.mr_layernorm_f32(xd.data_ptr(), 6, 48, gd.data_ptr(), bd.data_ptr(), 1e-5, 0, None, yq.data_ptr(), 64,
+                                 0.05, stream()), "layernorm")
+    sync()
+    want = G.quantize_activation(G.layernorm([x, g, b], {"eps": 1e-5}), np.float32(0.05)).astype(np.int8)
+    assert bits_equal(yq.cpu().numpy()[:, :48], want)
+    assert lib.mr_layernorm_f32(xd.data_ptr(), 6, 48, gd.data_ptr(), bd.data_ptr(), 1e-5, 0, None, None, 0, 1.0,
+                                stream()) == 1
+    assert lib.mr_layernorm_f32(xd.data_ptr(), 6, 48, gd.data_ptr(), bd.data_ptr(), 1e-5, 0, None, yq.data_ptr(), 40,
+                                0.05, stream()) == 1
+
+
+# ---------------------------------------------------------------- transpose / concat (bit-exact)
+
+@pytest.mark.parametrize("shape,perm", [((7,), (0,)), ((5, 9), (1, 0)), ((2, 273, 4, 16), (0, 2, 3, 1)),
+                                        ((2, 273, 4, 16), (0, 2, 1, 3)), ((3, 1, 4, 5), (3, 0, 2, 1)),
+                                        ((6, 5, 4), (2, 0, 1))])
+def test_transpose_exact(lib, shape, perm):
+    torch = _torch()
+    x = np.random.default_rng(len(shape)).standard_normal(shape).astype(np.float32)
+    want = G.evaluate("transpose", [x], {"perm": perm})
+    y = empty(want.shape, torch.float32)
+    r = len(shape)
+    xd = T(x)
+    L.check(lib.mr_transpose_f32(xd.data_ptr(), r, (C.c_int64 * r)(*shape), (C.c_int32 * r)(*perm), y.data_ptr(),
+                                 stream()), "transpose")
+    sync()
+    assert bits_equal(y.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("shapes,axis", [([(2, 272, 64), (2, 1, 64)], 1), ([(3, 4), (5, 4), (1, 4)], 0),
+                                         ([(2, 3, 1), (2, 3, 6)], 2), ([(1, 0, 8), (1, 2, 8)], 1)])
+def test_concat_exact(lib, shapes, axis):
+    torch = _torch()
+    rng = np.random.default_rng(11)
+    xs = [rng.standard_normal(s).astype(np.float32) for s in shapes]
+    want = G.evaluate("concat", xs, {"axis": axis})
+    y = empty(want.shape, torch.float32)
+    outer = int(np.prod(want.shape[:axis], dtype=np.int64))
+    ld = int(np.prod(want.shape[axis:], dtype=np.int64))
+    at = 0
+    xd = [T(a) for a in xs]
+    for a, t in zip(xs, xd):
+        inner = int(np.prod(a.shape[axis:], dtype=np.int64))
+        L.check(lib.mr_copy_rows_f32(t.data_ptr(), outer, inner, y.data_ptr(), ld, at, stream()), "concat")
+        at += inner
+    sync()
+    assert bits_equal(y.cpu().numpy(), want)
+
+
+# ---------------------------------------------------------------- softmax / bmm (approximate)
+
+@pytest.mark.parametrize("rows,n", [(8, 273), (1, 1), (300, 65), (3, 1000), (2, 4097)])
+def test_softmax_within_tolerance(lib, rows, n):
+    """Probabilities within 1e-5 relative + 1e-6 absolute of NumPy's; rows sum to 1."""
+    torch = _torch()
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((rows, n)) * 4).astype(np.float32)
+    x[0, :: 3] = -10000.0                       # masked positions, as the decode mask writes them
+    want = G.softmax([x], {"axis": -1})
+    y = empty((rows, n), torch.float32)
+    xd = T(x)
+    L.check(lib.mr_softmax_f32(xd.data_ptr(), rows, n, 0, y.data_ptr(), stream()), "softmax")
+    sync()
+    got = y.cpu().numpy()
+    _close(got, want)
+    assert np.abs(got.astype(np.float64).sum(axis=1) - 1).max() < 1e-5
+
+
+def _bstrides(shape, rs):
+    nb = len(rs) - 2
+    full = (1,) * (len(rs) - len(shape)) + tuple(shape)
+    return [0 if full[i] == 1 else int(np.prod(full[i + 1:], dtype=np.int64)) for i in range(nb)]
+
+
+@pytest.mark.parametrize("ashape,wshape", [((1, 4, 1, 16), (1, 4, 16, 273)), ((1, 4, 1, 273), (1, 4, 273, 16)),
+                                           ((2, 3, 5, 7), (7, 9)), ((4, 1, 8, 32), (1, 3, 32, 16)),
+                                           ((64, 128), (128, 96)), ((2, 1, 3, 2, 5, 6), (2, 2, 1, 2, 6, 4)),
+                                           ((2, 1, 2, 3, 2, 5, 6), (2, 2, 1, 3, 2, 6, 4))])
+def test_bmm_f32_within_tolerance(lib, ashape, wshape):
+    """a @ w with NumPy batch broadcasting and a scale+mask epilogue: every element within
+    1e-5 of the float64 product's magnitude sum (|a| @ |w|), the bound for any f32 order."""
+    torch = _torch()
+    rng = np.random.default_rng(len(ashape) * 10 + len(wshape))
+    a = rng.standard_normal(ashape).astype(np.float32)
+    w = rng.standard_normal(wshape).astype(np.float32)
+    prod = np.matmul(a, w)
+    rs = prod.shape
+    nb = len(rs) - 2
+    M, N, K = rs[-2], rs[-1], ashape[-1]
+    scale = np.float32(0.25)
+    mask = np.where(rng.random(N) < 0.3, -10000.0, 0.0).astype(np.float32)
+    want = G.epilogue_ref(prod, [None, None, scale, mask], (("mul", 2, False), ("add", 3, False)))
+    mag = np.matmul(np.abs(a).astype(np.float64), np.abs(w).astype(np.float64)) * 0.25
+    y = empty((int(np.prod(rs[:-1])), N), torch.float32)
+    st, mk = T(scale.reshape(1)), T(mask)
+    e = epilogue([("mul", L.BC_SCALAR, st, 0, False), ("add", L.BC_COL, mk, 1, False)], out_f32=y, ldo=N)
+    ad, wd = T(a), T(w)
+    if nb > 4:
+        with pytest.raises(L.RocmError):
+            L.check(lib.mr_bmm_f32(ad.data_ptr(), wd.data_ptr(), nb, None, None, None, M, N, K, C.byref(e),
+                                   stream()), "bmm")
+        return
+    arr = lambda v: (C.c_int64 * max(nb, 1))(*v)
+    L.check(lib.mr_bmm_f32(ad.data_ptr(), wd.data_ptr(), nb, arr(rs[:nb]), arr(_bstrides(ashape, rs)),
+                           arr(_bstrides(wshape, rs)), M, N, K, C.byref(e), stream()), "bmm")
+    sync()
+    _close(y.cpu().numpy().reshape(rs), want, scale=mag, rtol=0, atol=1e-5)
+
+
+# ---------------------------------------------------------------- libm epilogue steps (approximate)
+
+@pytest.mark.parametrize("fn", ["gelu", "sigmoid", "tanh"])
+@pytest.mark.parametrize("M,K,N", [(1, 256, 96), (300, 512, 256)])        # weight-stream and tiled kernels
+def test_qmatmul_libm_epilogue(lib, fn, M, K, N):
+    """The step after bias: within 1e-5 relative + 1e-6 absolute of NumPy's (gelu's absolute
+    term scales with |x|, where 1 + tanh cancels)."""
+    torch = _torch()
+    rng = np.random.default_rng(M + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = rng.standard_normal((K, N)).astype(np.float32)
+    q, ws = G.quantize_array(w, 1)
+    bias = rng.standard_normal(N).astype(np.float32)
+    xs = np.float32(np.abs(x).max() / 127)
+    attrs = {"q": q, "w_scale": ws, "x_scale": float(xs), "dtype": "f32",
+             "epilogue": (("add", 1, False), (fn, None, False))}
+    want = G.qmatmul([x, bias], attrs)
+    pre = G.qmatmul([x, bias], dict(attrs, epilogue=(("add", 1, False),)))
+    xq = G.quantize_activation(x, xs).astype(np.int8)
+    lda = pack.row_stride_for(K)
+    xpad = np.zeros((M, lda), np.int8)
+    xpad[:, :K] = xq
+    bl = pack.pack_matmul(q)
+    y = empty((M, N), torch.float32)
+    sc, bd = T(pack.combined_scale(float(xs), ws)), T(bias)
+    e = epilogue([("add", L.BC_COL, bd, 1, False), (fn, 0, None, 0, False)], scale=sc, out_f32=y, ldo=N)
+    xd, bw = T(xpad), T(pack.device_weights(bl))
+    L.check(lib.mr_qmatmul(xd.data_ptr(), lda, bw.data_ptr(), bl.shape[1], bl.shape[0], M, N, K, C.byref(e),
+                           stream()), "qmatmul")
+    sync()
+    _close(y.cpu().numpy(), want, scale=np.maximum(np.abs(pre), 1.0))
+
+
+# ---------------------------------------------------------------- the GPT decode step through the target
+
+def _gpt(batch):
+    cfg = models.GPTConfig()
+    params = models.gpt_params(cfg, 0)
+    g = LW.prepare(models.gpt_decode_step(cfg, batch, params))
+    calib = []
+    for s in (2, 3):
+        r = np.random.default_rng(s)
+        toks = r.integers(0, cfg.V, (batch, cfg.T)).astype(np.int32)
+        caches = [(r.standard_normal((batch, cfg.T, cfg.D)).astype(np.float32),
+                   r.standard_normal((batch, cfg.T, cfg.D)).astype(np.float32)) for _ in range(cfg.L)]
+        calib.append(models.gpt_step_feeds(cfg, params, toks, 16, caches))
+    LW.w8a8(g, peaks=LW.calibrate(g, calib))
+    return cfg, params, g
+
+
+def _step_feeds(cfg, params, batch, t, seed=9):
+    r = np.random.default_rng(seed)
+    toks = r.integers(0, cfg.V, (batch, cfg.T)).astype(np.int32)
+    caches = [(r.standard_normal((batch, cfg.T, cfg.D)).astype(np.float32),
+               r.standard_normal((batch, cfg.T, cfg.D)).astype(np.float32)) for _ in range(cfg.L)]
+    return models.gpt_step_feeds(cfg, params, toks, t, caches)
+
+
+def test_gpt_step_exact_mode_device_ops():
+    """Default mode: layernorm, the head transposes and the cache concats join the W8A8
+    projections on rocm; the attention matmuls, softmax and the gelu projection stay on the
+    CPU; every output bit-exact."""
+    cfg, params, g = _gpt(2)
+    feeds = _step_feeds(cfg, params, 2, 20)
+    runner = Runner(g, RocmTarget(), fallback=G.CPUTarget())
+    on_cpu = {op.kind for seg in runner.segments if seg.device == "cpu" for op in seg.graph.compute_ops()}
+    assert on_cpu <= {"matmul", "softmax", "qmatmul", "transpose", "reshape", "concat"}, on_cpu
+    kinds = {k for exe in runner.executables("rocm") for k in exe.kernel_counts}
+    assert {"layernorm", "concat"} <= kinds
+    got = runner.run(feeds)
+    want = G.run_graph(g, feeds)
+    for a, b in zip(got, want):
+        assert bits_equal(a, b)
+
+
+def _flips(exe, g, env) -> int:
+    """int32 accumulators of the rocm run that differ from the oracle's for the same graph
+    inputs: each is an int8 activation that the two runs rounded to different steps."""
+    acc = exe.accumulators()
+    n = 0
+    for op in g.compute_ops():
+        if op.kind == "qmatmul":
+            want = G.qmatmul_acc(env[op.inputs[0]], op.attrs).astype(np.int32)
+            n += int((acc[op.result].reshape(want.shape) != want).sum())
+    return n
+
+
+@pytest.mark.parametrize("batch", [1, 2])
+def test_gpt_step_approx_mode_one_segment(batch):
+    """approx_f32: the whole step is one rocm segment.  Every approximate result (attention,
+    softmax, gelu) is requantized to int8 before anything reads it, so the logits and the new
+    key/value rows are bit-exact unless a requantization flipped (an accumulator differs);
+    with no flip here they must be bit-exact."""
+    cfg, params, g = _gpt(batch)
+    feeds = _step_feeds(cfg, params, batch, 20)
+    runner = Runner(g, RocmTarget(approx_f32=True, debug_acc=True), fallback=G.CPUTarget())
+    assert runner.devices == ["rocm"]
+    got = runner.run(feeds)
+    env = oracle_env(g, feeds)
+    flips = _flips(runner.executables("rocm")[0], g, env)
+    for a, v in zip(got, g.outputs):
+        assert bits_equal(a, env[v]) or flips > 0
+    assert flips <= 2
+
+
+def test_gpt_greedy_decode_256_tokens_approx_mode():
+    """The configuration's decode (batch 1, seeded 16-token prompt, 256 new tokens, T = 272)
+    with the whole step on rocm, teacher-forced: each step runs on the oracle's own feeds
+    (its tokens and cache).  Every step's logits and key/value rows are bit-exact unless an
+    int8 requantization flipped at that step; flips are rare (at most 1 step in 10), a flip
+    step's logits stay within 5% of the largest logit, and the greedy tokens are the oracle's."""
+    cfg, params, g = _gpt(1)
+    prompt = np.random.default_rng(4).integers(0, cfg.V, (1, 16)).astype(np.int32)
+    runner = Runner(g, RocmTarget(approx_f32=True, debug_acc=True), fallback=G.CPUTarget())
+    assert runner.devices == ["rocm"]
+    exe = runner.executables("rocm")[0]
+    steps = []
+
+    def run(feeds):
+        got = runner.run(feeds)
+        env = oracle_env(g, feeds)
+        want = [env[v] for v in g.outputs]
+        flips = _flips(exe, g, env)
+        exact = all(bits_equal(a, b) for a, b in zip(got, want))
+        err = float(np.abs(got[0] - want[0]).max() / max(np.abs(want[0]).max(), 1.0))
+        steps.append((exact, flips, err, int(got[0].argmax()) == int(want[0].argmax())))
+        return want
+
+    models.gpt_decode(run, cfg, params, prompt, 256)
+    assert len(steps) == 271
+    print(f"steps with flips: {sum(f > 0 for _, f, _, _ in steps)}, max rel err {max(e for *_, e, _ in steps):.3g}")
+    assert all(exact or flips > 0 for exact, flips, _, _ in steps)
+    assert sum(flips > 0 for _, flips, _, _ in steps) <= 27
+    assert max(err for _, _, err, _ in steps) <= 0.05
+    assert all(same for *_, same in steps)

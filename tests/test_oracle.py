@@ -13,6 +13,10 @@ tiny inputs, or by exact arithmetic:
   depthwise conv2d     scalar float32 tap loop in (i, j) order
   maxpool2d / pad      window brute force / closed form
   reduce_mean          NumPy's pairwise summation restated in scalar float32
+  layernorm            scalar restatement (pairwise means, f64 divide, f32 steps); closed forms
+  softmax              equal logits -> fl32(1/n), [0, ln 3] -> [1/4, 3/4], no overflow
+  gelu/sigmoid/tanh    float64 closed forms, tanh-form gelu(1) = 0.8411920
+  transpose / concat   index brute force
   epilogue_ref         operand order of every binary step, including swapped
   calibrate / attrs    hand-computed peaks on a two-layer graph
 """
@@ -278,6 +282,83 @@ def test_reduce_mean_is_pairwise_then_f64_divide(hw):
         for c in range(3):
             s = pairwise_f32(x[b, c].ravel().tolist())
             assert y[b, c, 0, 0] == np.float32(np.float64(s) / np.float64(n))
+
+
+def _layernorm_scalar(x, g, b, eps) -> np.ndarray:
+    """mira/ops.py:356-360 restated element by element: each mean is the pairwise sum seeded
+    with +0, divided by the count in float64 (NumPy's mean divides by an intp count), and every
+    other step is one float32 operation."""
+    n = len(x)
+    mu = np.float32(np.float64(np.float32(np.float32(0) + pairwise_f32(x))) / np.float64(n))
+    sq = [np.float32(np.float32(v - mu) * np.float32(v - mu)) for v in x]
+    var = np.float32(np.float64(np.float32(np.float32(0) + pairwise_f32(sq))) / np.float64(n))
+    sd = np.sqrt(np.float32(var + np.float32(eps)))
+    return np.array([np.float32(np.float32(np.float32(np.float32(v - mu) / sd) * gi) + bi)
+                     for v, gi, bi in zip(x, g, b)], np.float32)
+
+
+@pytest.mark.parametrize("d", [1, 3, 7, 8, 9, 64, 100, 128, 129, 300, 1029])
+def test_layernorm_is_pairwise_mean_and_f32_steps(d):
+    rng = np.random.default_rng(d)
+    x = (rng.standard_normal((3, d)) * rng.uniform(0.1, 50) + rng.uniform(-20, 20)).astype(np.float32)
+    g = rng.standard_normal(d).astype(np.float32)
+    b = rng.standard_normal(d).astype(np.float32)
+    y = G.layernorm([x, g, b], {"eps": 1e-5})
+    for r in range(3):
+        assert np.array_equal(y[r].view(np.uint32), _layernorm_scalar(x[r].tolist(), g, b, 1e-5).view(np.uint32))
+
+
+def test_layernorm_closed_forms():
+    g = np.float32([1.5, -2.0])
+    b = np.float32([0.25, 3.0])
+    # constant rows: x - mu == 0, so y == 0 * g + b == b exactly
+    assert np.array_equal(G.layernorm([np.full((2, 2), 7.25, np.float32), g, b], {"eps": 1e-5}), np.stack([b, b]))
+    # [a, -a]: mu = 0, var = a^2, y = +-a / sqrt(a^2 + eps) * g + b, which is +-g + b for large a
+    y = G.layernorm([np.float32([[1000.0, -1000.0]]), g, b], {"eps": 1e-5})
+    assert np.array_equal(y, np.float32([[1.75, 5.0]]))
+    # biased variance (ddof 0): with g = 1, b = 0, eps = 0 the rows have mean 0 and mean square 1
+    x = np.random.default_rng(1).standard_normal((4, 8)).astype(np.float32)
+    y = G.layernorm([x, np.ones(8, np.float32), np.zeros(8, np.float32)], {"eps": 0.0}).astype(np.float64)
+    assert np.abs(y.mean(axis=1)).max() < 1e-6 and np.abs((y ** 2).mean(axis=1) - 1).max() < 1e-5
+
+
+def test_softmax_closed_forms():
+    # equal logits: exp(0) = 1 each, so every probability is fl32(1 / n)
+    for n in (1, 3, 273):
+        assert np.array_equal(G.softmax([np.full((2, n), -4.5, np.float32)], {"axis": -1}),
+                              np.full((2, n), np.float32(1) / np.float32(n), np.float32))
+    # [0, d] -> [1, e^d] / (1 + e^d); the max is subtracted first, so large logits do not
+    # overflow (d = 1.0986328125 ~ ln 3 is a multiple of 2^-10, so 1000 + d is exact in f32)
+    d = 1.0986328125
+    y = G.softmax([np.float32([[0.0, d], [1000.0, 1000.0 + d]])], {"axis": -1})
+    assert np.abs(y - np.array([1.0, np.exp(d)]) / (1 + np.exp(d))).max() < 1e-6
+    # the axis attribute selects the reduced axis
+    x = np.random.default_rng(2).standard_normal((3, 5)).astype(np.float32)
+    assert np.abs(G.softmax([x], {"axis": 0}).sum(axis=0) - 1).max() < 1e-6
+
+
+def test_libm_unary_closed_forms():
+    """gelu is the tanh form 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) (mira/ops.py:94-96)."""
+    x = np.float32([0.0, 1.0, -1.0, 6.0, -6.0])
+    gelu = G.unary("gelu", x).astype(np.float64)
+    want = [0.5 * v * (1 + np.tanh(np.sqrt(2 / np.pi) * (v + 0.044715 * v ** 3))) for v in x.astype(np.float64)]
+    assert np.abs(gelu - want).max() < 1e-6
+    assert abs(gelu[1] - 0.8411920) < 1e-6                  # the tanh form at 1 (the erf form gives 0.8413447)
+    assert np.array_equal(G.unary("sigmoid", np.float32([0.0])), np.float32([0.5]))
+    assert np.array_equal(G.unary("tanh", np.float32([0.0, 20.0])), np.float32([0.0, 1.0]))
+
+
+def test_transpose_and_concat_brute_force():
+    x = np.arange(2 * 3 * 4 * 5, dtype=np.float32).reshape(2, 3, 4, 5)
+    y = G.evaluate("transpose", [x], {"perm": (0, 2, 3, 1)})
+    assert y.shape == (2, 4, 5, 3) and y.flags.c_contiguous
+    for a, b_, c, d in np.ndindex(*y.shape):
+        assert y[a, b_, c, d] == x[a, d, b_, c]
+    p, q = x[:, :2], x[:, 2:] * -1
+    z = G.evaluate("concat", [p, q], {"axis": 1})
+    assert z.shape == x.shape
+    for a, b_, c, d in np.ndindex(*z.shape):
+        assert z[a, b_, c, d] == (x[a, b_, c, d] if b_ < 2 else -x[a, b_, c, d])
 
 
 def test_epilogue_operand_order():
