@@ -30,8 +30,10 @@ resnet18-onnx is ResNet-18 laid out as MIRA's ONNX importer emits it (BN as a
 per-channel mul + add in each conv epilogue instead of folded weights);
 resnet18-f16 is the f16 graph (MIRA's default precision for accelerator
 targets), every result rounded to f16 and stored as f32.
-gpt-decode times the device part of one character-level GPT decode step
-(default batch 1; the host-side attention and normalisations are excluded).
+gpt-decode times greedy decoding with the character-level GPT (default batch 1;
+16-token prompt, --tokens generated): the whole loop resident on the GPU, one
+HIP graph replay per step, in microseconds per token, beside the eager launch
+loop and the bit-exact mode driven from the host.
 """
 from __future__ import annotations
 
@@ -228,15 +230,20 @@ def bench_workload(args) -> int:
 
 def bench_gpt(args) -> int:
     """Greedy decoding with the character-level GPT (L=2, d=64, 4 heads, vocab 65, context
-    T=272 = 16 + 256), W8A8 on the QKV/out/MLP/vocab projections, end to end: a seeded
-    16-token prompt per sequence, `--tokens` generated tokens, every step through the
-    runner -- the rocm segments (the projections) and the host segments (embedding gather,
-    the f32 attention, softmax, layernorm and the gelu projection, which the rocm target
-    leaves to the CPU), host/device copies included.  Also times the device part alone
-    (each rocm segment's launch list, inputs already in HBM)."""
+    T=272 = 16 + 256), W8A8 on the QKV/out/MLP/vocab projections: a seeded 16-token prompt per
+    sequence, then `--tokens` generated tokens (16 + tokens - 1 decode steps).
+
+    Timed (`us_per_token`): the whole decode resident on the GPU -- the step graph as one rocm
+    executable in approx_f32 mode (softmax, the attention matmuls and gelu on the device) and
+    the loop state (embedding row, mask, cache writes, argmax) in device memory
+    (harness.decode.DeviceDecoder), each step replayed as one HIP graph; HIP events around
+    all the steps, no host synchronisation inside.  Beside it: the same loop launched eagerly,
+    and the bit-exact default mode driven from the host through the runner (softmax, the f32
+    attention and the gelu projection on NumPy, host/device copies included)."""
     import torch
     from harness import lowering as LW
     from harness import models
+    from harness.decode import DeviceDecoder
     from harness.hosteval import HostTarget
     from harness.runner import Runner
     from mira_amd.target import RocmTarget
@@ -253,63 +260,68 @@ def bench_gpt(args) -> int:
     peaks = LW.calibrate(twin, calib)
     g = LW.prepare(models.gpt_decode_step(cfg, args.batch, params))
     LW.w8a8(g, peaks=peaks)
-    runner = Runner(g, RocmTarget(), fallback=HostTarget())
     prompt = np.random.default_rng(4).integers(0, cfg.V, (args.batch, 16)).astype(np.int32)
     new = min(args.tokens, cfg.T - 16)
-    timings = {"rocm": 0.0, "cpu": 0.0}
-
-    def step(feeds):
-        out = runner.run(feeds)
-        for dev, sec in runner.timings:
-            timings[dev] = timings.get(dev, 0.0) + sec
-        return out
-    models.gpt_decode(step, cfg, params, prompt, 4)            # warm-up
-    torch.cuda.synchronize()
-    timings = {"rocm": 0.0, "cpu": 0.0}
-    t0 = time.perf_counter()
-    tokens, _ = models.gpt_decode(step, cfg, params, prompt, new)
-    total = time.perf_counter() - t0
     steps = 16 + new - 1
-    log(f"gpt decode batch {args.batch}: {new} tokens in {total:.3f} s ({1e6 * total / steps:.0f} us/step)")
-
-    # device part alone: each rocm segment's launch list with its inputs resident
-    exes = runner.executables("rocm")
-    for i, exe in enumerate(exes):
-        exe.upload({v: models.normal_batch(v.type.shape, 100 + i).astype(np.float32) for v in exe.g.inputs})
     stream = torch.cuda.current_stream()
-    for _ in range(args.warmup):
-        for exe in exes:
-            exe.launch()
-    torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(args.steps):
-        for exe in exes:
-            exe.launch()
-    stop.record(stream)
-    torch.cuda.synchronize()
-    dev_ms = start.elapsed_time(stop) / args.steps
+
+    # the decode resident on the device: one executable, one graph replay per step
+    dev_runner = Runner(g, RocmTarget(approx_f32=True))
+    (exe,) = dev_runner.executables("rocm")
+    dec = DeviceDecoder(dev_runner, cfg, params, args.batch)
+    dec.capture()
+
+    def timed_decode(use_graph: bool) -> tuple:
+        dec.reset(prompt)
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record(stream)
+        dec.run_steps(steps, use_graph)
+        stop.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) * 1e-3, time.perf_counter() - t0, dec.tokens[:, :16 + new].cpu().numpy()
+
+    for _ in range(max(args.warmup, 1)):
+        timed_decode(True)
+        timed_decode(False)
+    graph_s, graph_wall, tok_graph = timed_decode(True)
+    eager_s, eager_wall, tok_eager = timed_decode(False)
+    assert np.array_equal(tok_graph, tok_eager), "graph and eager device decodes disagree"
+    log(f"gpt decode batch {args.batch} on the device: {new} tokens, {1e6 * graph_s / steps:.1f} us/step "
+        f"(graph), {1e6 * eager_s / steps:.1f} us/step (eager launches)")
     kernels = {}
-    for exe in exes:
-        for kind, row in kernel_breakdown(exe, time_launches(exe, stream)).items():
-            k = kernels.setdefault(kind, {"launches": 0, "ms": 0.0})
-            k["launches"] += row["launches"]
-            k["ms"] = round(k["ms"] + row["ms"], 4)
+    for kind, row in kernel_breakdown(exe, time_launches(exe, stream)).items():
+        kernels[kind] = {"launches": row["launches"], "ms": round(row["ms"], 4)}
+
+    # the bit-exact default mode, driven from the host through the runner
+    host_runner = Runner(g, RocmTarget(), fallback=HostTarget())
+    models.gpt_decode(host_runner.run, cfg, params, prompt, 4)            # warm-up
+    torch.cuda.synchronize()
+    host_steps = min(steps, 16 + min(new, 64) - 1)
+    t0 = time.perf_counter()
+    tok_host, _ = models.gpt_decode(host_runner.run, cfg, params, prompt, host_steps - 15)
+    host_s = time.perf_counter() - t0
+    log(f"gpt decode batch {args.batch}, exact mode through the host: {1e6 * host_s / host_steps:.0f} us/step")
+
     print(json.dumps({
         "workload": "gpt-decode", "batch": args.batch, "prompt_tokens": 16, "generated_tokens": new,
-        "decode_steps": steps, "seconds": round(total, 4),
-        "us_per_step": round(1e6 * total / steps, 1),
-        "us_per_token": round(1e6 * total / (new * args.batch), 3),
-        "tokens_per_s": round(new * args.batch / total, 1),
-        "split_s": {"rocm_segments": round(timings.get("rocm", 0.0), 4),
-                    "host_segments": round(timings.get("cpu", 0.0), 4),
-                    "host_feeds_and_argmax": round(total - sum(timings.values()), 4)},
-        "rocm_segments_per_step": len(exes), "launches_per_step": sum(len(e.launches) for e in exes),
-        "device_only_us_per_step": round(dev_ms * 1e3, 1),
-        "device_constant_bytes": sum(e.const_bytes for e in exes),
+        "decode_steps": steps, "seconds": round(graph_s, 6),
+        "us_per_step": round(1e6 * graph_s / steps, 2),
+        "us_per_token": round(1e6 * graph_s / (new * args.batch), 4),
+        "tokens_per_s": round(new * args.batch / graph_s, 1),
+        "mode": "approx_f32 (softmax, attention matmuls and gelu on the device; W8A8 projections, layernorm, "
+                "transposes and concats bit-exact)",
+        "eager_us_per_step": round(1e6 * eager_s / steps, 2),
+        "graph_wall_us_per_step": round(1e6 * graph_wall / steps, 2),
+        "exact_mode_host_loop_us_per_step": round(1e6 * host_s / host_steps, 1),
+        "exact_mode_host_loop_steps": host_steps,
+        "exact_mode_segments": host_runner.devices,
+        "launches_per_step": len(exe.launches),
+        "device_constant_bytes": exe.const_bytes,
         "dtype": "int8", "data": "synthetic",
-        "timed": "end-to-end greedy decode through the runner (host segments on NumPy, host/device copies "
-                 "included); device_only_us_per_step times the rocm launch lists alone",
+        "timed": "HIP events around every decode step of the prompt and the generated tokens, the step "
+                 "graph replayed once per step with the loop state on the device; inputs resident",
         "kernels": kernels}), flush=True)
     return 0
 

@@ -1064,6 +1064,14 @@ class RocmExecutable:
         """The device f32 buffer (graph layout) that `launch` reads segment input v from."""
         return self.staging[v]
 
+    def device_output(self, v: "Value"):
+        """The device f32 buffer (graph layout) that `launch` leaves output v in; it is rewritten
+        by the next launch.  Only for values stored in C order (not NHWC images)."""
+        d = self._src(v)
+        if d.nhwc or d.f32 is None:
+            raise L.RocmError(f"{v} has no C-order f32 copy on the device")
+        return d.f32.reshape(v.type.shape)
+
     def launch(self) -> None:
         """Queue every kernel of the segment on the current stream, starting from the f32 inputs
         already on the device (quantizing them is part of the work)."""

@@ -321,3 +321,35 @@ def test_gpt_greedy_decode_256_tokens_approx_mode():
     assert sum(flips > 0 for _, flips, _, _ in steps) <= 27
     assert max(err for _, _, err, _ in steps) <= 0.05
     assert all(same for *_, same in steps)
+
+
+# ---------------------------------------------------------------- the decode loop resident on the device
+
+@pytest.mark.parametrize("batch,new", [(1, 256), (2, 40)])
+def test_device_decoder_matches_host_loop(batch, new):
+    """harness.decode.DeviceDecoder (embedding, mask, cache writes and argmax on the device, no
+    host synchronisation per token) gives the tokens and last logits of models.gpt_decode driven
+    through the same executable, bit for bit; so does its HIP graph, replayed once per step with
+    synchronisations and eager work between some replays."""
+    import torch
+    from harness.decode import DeviceDecoder
+    cfg, params, g = _gpt(batch)
+    prompt = np.random.default_rng(4).integers(0, cfg.V, (batch, 16)).astype(np.int32)
+    runner = Runner(g, RocmTarget(approx_f32=True))
+    want_tok, want_logits = models.gpt_decode(runner.run, cfg, params, prompt, new)
+    dec = DeviceDecoder(runner, cfg, params, batch)
+    got_tok = dec.decode(prompt, new)
+    assert np.array_equal(got_tok, want_tok)
+    assert bits_equal(dec.logits.cpu().numpy(), want_logits[-1])
+    dec.capture()
+    dec.reset(prompt)
+    steps = 16 + new - 1
+    for i in range(steps):
+        dec.run_steps(1, use_graph=True)
+        if i % 37 == 0:
+            torch.cuda.synchronize()
+            assert int(dec.t.item()) == i + 1
+            _ = (dec.logits * 2).sum().item()          # eager work between replays
+    graph_tok = dec.tokens[:, :16 + new].cpu().numpy()
+    assert np.array_equal(graph_tok, want_tok)
+    assert bits_equal(dec.logits.cpu().numpy(), want_logits[-1])

@@ -320,6 +320,73 @@ def test_gpt_decode_step_graph_and_placement():
     assert logits.shape == (2, cfg.V) and np.isfinite(logits).all() and len(kv) == 2 * cfg.L
 
 
+def test_gpt_placement_by_mode():
+    """Default mode: layernorm, the head transposes and the cache concats join the projections
+    on rocm and the step splits into 9 segments; approx_f32: the whole step is one segment."""
+    cfg = models.GPTConfig()
+    params = models.gpt_params(cfg, 0)
+    g = LW.prepare(models.gpt_decode_step(cfg, 1, params))
+    r = np.random.default_rng(2)
+    caches = [(r.standard_normal((1, cfg.T, cfg.D)).astype(np.float32),
+               r.standard_normal((1, cfg.T, cfg.D)).astype(np.float32)) for _ in range(cfg.L)]
+    LW.w8a8(g, [models.gpt_step_feeds(cfg, params, np.zeros((1, cfg.T), np.int32), 16, caches)])
+    segs, reasons = split(g, RocmTarget())
+    assert len(segs) == 9 and {op.kind for op in reasons} == {"matmul", "softmax", "qmatmul"}
+    segs, reasons = split(g, RocmTarget(approx_f32=True))
+    assert [s.device for s in segs] == ["rocm"] and not reasons
+
+
+class _OracleStepExecutable:
+    """Stands in for the rocm executable of the decode step on the CPU: the same device_input /
+    device_output / launch surface over CPU tensors, launch() evaluating the step with the oracle."""
+
+    def __init__(self, g):
+        import torch
+        self.g, self.dev = g, torch.device("cpu")
+        self.inputs = {v: torch.zeros(v.type.shape, dtype=torch.float32) for v in g.inputs}
+        self.outputs = {v: torch.zeros(v.type.shape, dtype=torch.float32) for v in g.outputs}
+
+    def device_input(self, v):
+        return self.inputs[v]
+
+    def device_output(self, v):
+        return self.outputs[v]
+
+    def launch(self):
+        import torch
+        feeds = {v.name: t.numpy().copy() for v, t in self.inputs.items()}
+        for v, arr in zip(self.g.outputs, G.run_graph(self.g, feeds)):
+            self.outputs[v].copy_(torch.from_numpy(np.asarray(arr, np.float32)))
+
+
+def test_device_decoder_loop_on_cpu():
+    """harness.decode.DeviceDecoder's loop (embedding/position rows, mask rows, cache writes,
+    argmax, the prompt guard, the step counter) run on CPU tensors around the oracle's step
+    gives the tokens of models.gpt_decode; a step past the context raises instead of indexing
+    out of range."""
+    from harness.decode import DeviceDecoder
+
+    class FakeRunner:
+        def __init__(self, g):
+            self.graph, self.devices = g, ["rocm"]
+            self.exe = _OracleStepExecutable(g)
+
+        def executables(self, device=None):
+            return [self.exe]
+
+    cfg = models.GPTConfig()
+    params = models.gpt_params(cfg, 0)
+    g = LW.prepare(models.gpt_decode_step(cfg, 2, params))
+    prompt = np.random.default_rng(4).integers(0, cfg.V, (2, 16)).astype(np.int32)
+    want, _ = models.gpt_decode(lambda f: G.run_graph(g, f), cfg, params, prompt, 12)
+    dec = DeviceDecoder(FakeRunner(g), cfg, params, 2)
+    assert np.array_equal(dec.decode(prompt, 12), want)
+    dec.reset(prompt)
+    dec.steps_done = cfg.T - 1            # as after a full-context decode
+    with pytest.raises(RuntimeError):
+        dec.step()
+
+
 def test_division_magic_is_exact():
     """The patch loader divides by launch constants d as umulhi(n, ceil(2^32 / d)), which the
     host allows only while n * d < 2^32: checked here for every d < 600 and n up to that
