@@ -6,6 +6,6 @@ epilogue fusion, the W8A8 and weight-only int8 rewrites, calibration), and
 runs them split between the rocm target and a CPU fallback (`runner`).  Its
 small IR (`graph`) carries the attribute names of MIRA's IR, which is all the
 target reads.  In a MIRA deployment MIRA itself does every one of these
-steps; tests/test_harness.py checks the harness against MIRA's own output for
+steps; tests/test_mira_golden.py checks the harness against MIRA's own output for
 MIRA's programs (tests/golden).
 """
