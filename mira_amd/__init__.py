@@ -10,7 +10,8 @@ quantizer and partitioner produce the graphs; this package runs them:
     build                                hipcc build of libmira_rocm.so for gfx950
     csrc/                                the HIP kernels (int8 MFMA GEMM / implicit-GEMM conv,
                                          fused dequant/epilogue/requant, quantizer, depthwise,
-                                         pooling) and their C ABI
+                                         pooling, the float ops of a transformer decode step)
+                                         and their C ABI
 
 `get_target` / `TARGETS` are the branch a MIRA checkout adds to its backend
 registry (mira/backends/__init__.py:5-25).
@@ -21,11 +22,17 @@ TARGETS = ["rocm"]
 
 
 def get_target(name: str, **options):
-    """The rocm branch of MIRA's get_target: options device (int) and debug_acc (bool)."""
+    """The rocm branch of MIRA's get_target: options device (int), debug_acc (bool) and
+    approx_f32 (bool: also run softmax, f32 matmuls of two tensors and libm epilogue steps,
+    to f32 rounding instead of bit for bit)."""
     if name != "rocm":
         raise ValueError(f"unknown target '{name}' (this package provides: rocm)")
     from .target import RocmTarget
-    return RocmTarget(device=options.get("device", 0), debug_acc=options.get("debug_acc", False))
+    unknown = set(options) - {"device", "debug_acc", "approx_f32"}
+    if unknown:
+        raise ValueError(f"unknown rocm target options: {sorted(unknown)}")
+    return RocmTarget(device=options.get("device", 0), debug_acc=options.get("debug_acc", False),
+                      approx_f32=options.get("approx_f32", False))
 
 
 __all__ = ["get_target", "TARGETS"]
