@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MR_ABI_VERSION 4
+#define MR_ABI_VERSION 5
 
 enum mr_status {
   MR_OK = 0,
@@ -268,12 +268,16 @@ int mr_softmax_f32(const float* x, int64_t rows, int32_t n, int32_t out_f16,
 /* Replaces mira/ops.py:217-219 matmul of two float tensors with NumPy's
  * batch broadcasting: for each batch index (nb <= 4 dimensions of extents
  * bdim, element strides sa and sw in a and w, 0 where an operand
- * broadcasts), [M, K] @ [K, N] in f32, then the epilogue over the
- * [batches * M, N] result (scale must be NULL).  Approximate: the summation
- * order is k-ascending with fused multiply-adds, not BLAS's. */
+ * broadcasts), [M, K] @ [K, N] in f32, then the epilogue over the C-order
+ * [batches * M, N] result (scale must be NULL).  Both operands are strided
+ * views: mk_strides = {a's M stride, a's K stride, w's K stride, w's N
+ * stride} in elements, so transposed operands are read in place.
+ * Approximate: fused multiply-adds over interleaved k-groups added by a lane
+ * butterfly, not BLAS's summation order. */
 int mr_bmm_f32(const float* a, const float* w, int32_t nb, const int64_t* bdim,
-               const int64_t* sa, const int64_t* sw, int64_t M, int64_t N,
-               int64_t K, const mr_epilogue* epi, void* stream);
+               const int64_t* sa, const int64_t* sw, const int64_t* mk_strides,
+               int64_t M, int64_t N, int64_t K, const mr_epilogue* epi,
+               void* stream);
 
 /* Replaces mira/ops.py:375 transpose (np.ascontiguousarray(np.transpose(x,
  * perm))) for rank 1..4; exact (a copy). */

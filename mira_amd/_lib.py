@@ -10,7 +10,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "libmira_rocm.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 MAX_EPI = 8
 
 # enum mr_epi_fn
@@ -79,7 +79,7 @@ _SIGS = {
     "mr_nhwc_to_nchw_f32": ([_p, _i32, _i32, _i32, _i32, _p, _p], C.c_int),
     "mr_layernorm_f32": ([_p, _i64, _i32, _p, _p, _f32, _i32, _p, _p, _i64, _f32, _p], C.c_int),
     "mr_softmax_f32": ([_p, _i64, _i32, _i32, _p, _p], C.c_int),
-    "mr_bmm_f32": ([_p, _p, _i32, _p, _p, _p, _i64, _i64, _i64, C.POINTER(Epilogue), _p], C.c_int),
+    "mr_bmm_f32": ([_p, _p, _i32, _p, _p, _p, _p, _i64, _i64, _i64, C.POINTER(Epilogue), _p], C.c_int),
     "mr_transpose_f32": ([_p, _i32, _p, _p, _p, _p], C.c_int),
     "mr_copy_rows_f32": ([_p, _i64, _i64, _p, _i64, _i64, _p], C.c_int),
 }

@@ -114,10 +114,13 @@ __global__ void __launch_bounds__(256) softmax_kernel(const float* __restrict__ 
 
 // ---------------------------------------------------------------- batched f32 matmul (approximate)
 
-// mira/ops.py:217-219 for runtime operands: c[bt] = a[bt] @ w[bt] with the batch
+// mira/ops.py:217-219 for float operands: c[bt] = a[bt] @ w[bt] with the batch
 // index bt broadcast onto each operand through its own batch strides (sa, sw;
-// 0 for a broadcast dimension), then the epilogue on the [batches * M, N] result.
-// One thread per output element; f32 multiply-adds in k order.
+// 0 for a broadcast dimension), then the epilogue on the [batches * M, N] result
+// (C order).  Each operand is a strided view: a[bt][m][k] sits at
+// a + oa(bt) + m * sam + k * sak and w[bt][k][n] at w + ow(bt) + k * swk + n * swn,
+// so transposed operands are read in place.  f32 multiply-adds in k order per
+// partial sum: the result is not NumPy/BLAS's to the last bit.
 struct BmmArgs {
   const float* a;
   const float* w;
@@ -125,29 +128,66 @@ struct BmmArgs {
   int32_t nb;                 // batch dimensions (<= 4)
   int64_t bdim[4];            // batch extents, outermost first
   int64_t sa[4], sw[4];       // element strides of each batch dimension in a and w
+  int64_t sam, sak, swk, swn; // element strides of a's M and K axes and of w's K and N axes
 };
 
-__global__ void __launch_bounds__(256) bmm_f32_kernel(const BmmArgs p, const EpiDev e) {
-  const int64_t total = p.batches * p.M * p.N;
-  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < total; t += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t n = t % p.N;
-    const int64_t row = t / p.N;          // bt * M + m
+__device__ inline void bmm_offsets(const BmmArgs& p, int64_t bt, int64_t& oa, int64_t& ow) {
+  oa = 0;
+  ow = 0;
+  for (int i = p.nb - 1; i >= 0; --i) {
+    const int64_t q = bt % p.bdim[i];
+    bt /= p.bdim[i];
+    oa += q * p.sa[i];
+    ow += q * p.sw[i];
+  }
+}
+
+// One wave per (output row, block of NB = 2^nb_log2 columns): lane = kg * NB + j
+// computes column j of the block over k = kg, kg + KG, ... (KG = 64 / NB k-groups),
+// and log2(KG) butterfly steps add the k-groups.  The host picks NB so that
+// consecutive lanes read consecutive floats of w: along n when w's n axis is
+// contiguous, along k when its k axis is (the scores of attention read the key
+// cache that way).  Columns past N and lanes past K contribute nothing.
+__global__ void __launch_bounds__(256) bmm_f32_kernel(const BmmArgs p, const EpiDev e, int nb_log2,
+                                                      int64_t jobs) {
+  const int lane = threadIdx.x & 63;
+  const int NB = 1 << nb_log2;
+  const int KG = 64 >> nb_log2;
+  const int j = lane & (NB - 1);
+  const int kg = lane >> nb_log2;
+  const int64_t nblocks = (p.N + NB - 1) / NB;
+  for (int64_t job = blockIdx.x * int64_t(blockDim.x / 64) + (threadIdx.x >> 6); job < jobs;
+       job += int64_t(gridDim.x) * (blockDim.x / 64)) {
+    const int64_t row = job / nblocks;
+    const int64_t n = (job - row * nblocks) * NB + j;
+    const bool valid = n < p.N;
     const int64_t m = row % p.M;
-    int64_t bt = row / p.M;
-    int64_t oa = 0, ow = 0;
-    for (int i = p.nb - 1; i >= 0; --i) {
-      const int64_t q = bt % p.bdim[i];
-      bt /= p.bdim[i];
-      oa += q * p.sa[i];
-      ow += q * p.sw[i];
-    }
-    const float* ar = p.a + oa + m * p.K;
-    const float* wc = p.w + ow + n;
+    int64_t oa, ow;
+    bmm_offsets(p, row / p.M, oa, ow);
+    const float* ar = p.a + oa + m * p.sam;
+    const float* wc = p.w + ow + (valid ? n : 0) * p.swn;
     float acc = 0.0f;
-    for (int64_t k = 0; k < p.K; ++k) acc = fmaf(ar[k], wc[k * p.N], acc);
-    const float y = epi_steps(e, acc, row, n);
-    if (e.out_f32) e.out_f32[row * e.ldo + n] = y;
-    if (e.out_i8) e.out_i8[row * e.ldq + n] = quantize_rcp(y, e.out_rxs);
+    if (valid) {
+      // eight loads in flight before their multiply-adds, which stay in k order
+      int64_t k = kg;
+      for (; k + 7 * KG < p.K; k += 8 * KG) {
+        float av[8], wv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          av[u] = ar[(k + u * KG) * p.sak];
+          wv[u] = wc[(k + u * KG) * p.swk];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = fmaf(av[u], wv[u], acc);
+      }
+      for (; k < p.K; k += KG) acc = fmaf(ar[k * p.sak], wc[k * p.swk], acc);
+    }
+    for (int o = NB; o < 64; o <<= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o));
+    if (kg == 0 && valid) {
+      const float y = epi_steps(e, acc, row, n);
+      if (e.out_f32) e.out_f32[row * e.ldo + n] = y;
+      if (e.out_i8) e.out_i8[row * e.ldq + n] = quantize_rcp(y, e.out_rxs);
+    }
   }
 }
 
@@ -222,8 +262,8 @@ int mr_softmax_f32(const float* x, int64_t rows, int32_t n, int32_t out_f16, flo
 }
 
 int mr_bmm_f32(const float* a, const float* w, int32_t nb, const int64_t* bdim, const int64_t* sa, const int64_t* sw,
-               int64_t M, int64_t N, int64_t K, const mr_epilogue* epi, void* stream) {
-  MR_REQUIRE(a && w, "mr_bmm_f32: NULL operand");
+               const int64_t* mk_strides, int64_t M, int64_t N, int64_t K, const mr_epilogue* epi, void* stream) {
+  MR_REQUIRE(a && w && mk_strides, "mr_bmm_f32: NULL operand");
   MR_REQUIRE(nb >= 0 && nb <= 4 && (nb == 0 || (bdim && sa && sw)), "mr_bmm_f32: 0..4 batch dimensions");
   MR_REQUIRE(M > 0 && N > 0 && K > 0, "mr_bmm_f32: bad sizes");
   mr::BmmArgs p = {};
@@ -233,6 +273,11 @@ int mr_bmm_f32(const float* a, const float* w, int32_t nb, const int64_t* bdim, 
   p.N = N;
   p.K = K;
   p.nb = nb;
+  p.sam = mk_strides[0];
+  p.sak = mk_strides[1];
+  p.swk = mk_strides[2];
+  p.swn = mk_strides[3];
+  MR_REQUIRE(p.sam >= 0 && p.sak >= 0 && p.swk >= 0 && p.swn >= 0, "mr_bmm_f32: negative stride");
   p.batches = 1;
   for (int i = 0; i < nb; ++i) {
     MR_REQUIRE(bdim[i] > 0 && sa[i] >= 0 && sw[i] >= 0, "mr_bmm_f32: bad batch dimension %d", i);
@@ -245,8 +290,13 @@ int mr_bmm_f32(const float* a, const float* w, int32_t nb, const int64_t* bdim, 
   const int rc = mr::make_epi(epi, N, false, &e);
   if (rc != MR_OK) return rc;
   MR_REQUIRE(!e.out_acc, "mr_bmm_f32: no int32 accumulators");
-  hipLaunchKernelGGL(mr::bmm_f32_kernel, dim3(mr::grid_1d(p.batches * M * N, 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), p, e);
+  // lanes along k when w's k axis is the contiguous one and long enough to give every
+  // lane work, else along n
+  auto log2_ceil = [](int64_t v) { int l = 0; while ((int64_t(1) << l) < v && l < 6) ++l; return l; };
+  const int nb_log2 = (p.swk == 1 && p.swn != 1 && K >= 64) ? 6 - log2_ceil(K) : log2_ceil(N);
+  const int64_t jobs = p.batches * M * ((N + (int64_t(1) << nb_log2) - 1) >> nb_log2);
+  hipLaunchKernelGGL(mr::bmm_f32_kernel, dim3(mr::grid_1d(jobs * 64, 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), p, e, nb_log2, jobs);
   MR_LAUNCH_CHECK("bmm_f32");
   return MR_OK;
 }

@@ -107,6 +107,27 @@ W8_MAX_ROWS = 64     # mr_w8_matmul_f32 streams the weights once per 8 rows: dec
 _UNARY_CODES = {L.EPI_FN[f] for f in L.EPI_UNARY}
 
 
+def _contig(shape) -> tuple:
+    """Element strides of a C-order tensor of this shape."""
+    st, acc = [], 1
+    for d in reversed(tuple(shape)):
+        st.append(acc)
+        acc *= int(d)
+    return tuple(reversed(st))
+
+
+def _is_contig(shape, strides) -> bool:
+    """Does the strided view hold its elements in C order with no gaps (axes of extent 1,
+    whose stride is never used, aside)?"""
+    want = 1
+    for d, s in zip(reversed(tuple(shape)), reversed(tuple(strides))):
+        if d != 1:
+            if s != want:
+                return False
+            want *= int(d)
+    return True
+
+
 def _ptr(t) -> int:
     return 0 if t is None else t.data_ptr()
 
@@ -356,15 +377,89 @@ class RocmExecutable:
                 lst += [s for s in self.need_i8.get(r, []) if s not in lst]
         self.staging: dict["Value", object] = {}
         self.canon: dict["Value", object] = {}     # C-order copies of NHWC values (_c_order)
+        self._plan_views()
         for v in g.inputs:
             self._emit_input(v)
         for op in g.ops:
-            if op.is_constant_like or op in self.folded_pads or op in self.skip:
+            if not self._device_op(op) or op in self.virtual:
                 continue
             getattr(self, f"_emit_{op.kind}")(op)
         for v in g.outputs:
             if v in self.consts and v not in self.dv:
                 self._const_dv(v)
+
+    def _is_bmm(self, op: "Op") -> bool:
+        w = op.inputs[1] if op.kind == "matmul" else None
+        return w is not None and not (w.producer is not None and w.producer.kind == "dequantize")
+
+    def _view_chain(self, v: "Value") -> tuple:
+        """(base, shape, strides, chain): v as a strided view of `base`, the first value up its
+        chain of reshapes and transposes that has its own C-order buffer; `chain` lists the
+        values passed on the way (v first).  A reshape of a view that is not contiguous stops
+        the walk (that value is then the base)."""
+        p = v.producer
+        shape = tuple(v.type.shape)
+        if p is not None and v not in self.images and p.kind in ("transpose", "reshape") and \
+                p.inputs[0] not in self.images and p.inputs[0] not in self.consts:
+            base, s, st, chain = self._view_chain(p.inputs[0])
+            if p.kind == "transpose":
+                perm = tuple(p.attrs["perm"])
+                return base, shape, tuple(st[i] for i in perm), [v] + chain
+            if _is_contig(s, st):
+                return base, shape, _contig(shape), [v] + chain
+        return v, shape, _contig(shape), []
+
+    def _plan_views(self) -> None:
+        """Two ways of not copying, decided before any buffer exists:
+        * a transpose whose result is read only as a matmul operand (directly or through
+          reshapes and transposes) is not run: the matmul reads its input as a strided view;
+        * a segment input read only by one concat becomes a slice of the concat's result
+          buffer, so the concat copies only its other operands (a key/value cache joined by
+          the current step's row)."""
+        torch = _t()
+        g, users = self.g, self.users
+        self.virtual: set = set()
+        if self.target.approx_f32:
+            through: dict = {}          # value -> number of matmul operand chains passing it
+            for op in g.ops:
+                if op.kind == "matmul" and self._is_bmm(op):
+                    for v in op.inputs[:2]:
+                        for c in self._view_chain(v)[3]:
+                            through[c] = through.get(c, 0) + 1
+            def only_views(r) -> bool:
+                """Is every read of r, and of whatever reshapes/transposes make of it, a matmul
+                operand chain?"""
+                if r not in through or r in g.outputs:
+                    return False
+                return all((u.kind == "matmul" and self._is_bmm(u) and r in u.inputs[:2]) or
+                           (u.kind in ("reshape", "transpose") and only_views(u.result))
+                           for u in users.get(r, []))
+
+            # a chain op is not run when nothing but the chains reads its result
+            for op in g.ops:
+                if op.kind in ("transpose", "reshape") and only_views(op.result):
+                    self.virtual.add(op)
+        self.concat_out: dict = {}     # concat op -> its preallocated C-order result buffer
+        self.prealias: dict = {}       # segment input -> its slice of a concat result
+        for op in g.ops:
+            if op.kind != "concat" or op.result in self.images or not self._device_op(op):
+                continue
+            r = op.result
+            axis = op.attrs["axis"] % r.type.rank
+            buf, at = None, 0
+            for v in op.inputs:
+                n = v.type.shape[axis]
+                if v in g.inputs and v not in g.outputs and v not in self.images and v not in self.prealias and \
+                        op.inputs.count(v) == 1 and len(users.get(v, [])) == 1 and not self.need_i8.get(v):
+                    if buf is None:
+                        buf = torch.empty(r.type.shape, dtype=torch.float32, device=self.dev)
+                    self.prealias[v] = buf.narrow(axis, at, n)
+                at += n
+            if buf is not None:
+                self.concat_out[op] = buf
+
+    def _device_op(self, op: "Op") -> bool:
+        return not (op.is_constant_like or op in self.folded_pads or op in self.skip)
 
     def _i8_view(self, src: "Value", r: "Value") -> bool:
         """Is the int8 copy of `r` (a reshape of `src`) the same bytes as src's? Only for an
@@ -448,7 +543,9 @@ class RocmExecutable:
         mira/ops.py:602-603)."""
         torch = _t()
         lib = self.lib
-        stage = torch.empty(v.type.shape, dtype=torch.float32, device=self.dev)
+        stage = self.prealias.get(v)
+        if stage is None:
+            stage = torch.empty(v.type.shape, dtype=torch.float32, device=self.dev)
         self.staging[v] = stage
         d = self._new_dv(v, with_i8=True)
         cast16 = any(op.inputs[0] is v for op in self.input_casts)
@@ -1007,16 +1104,21 @@ class RocmExecutable:
         r = op.result
         rank = r.type.rank
         axis = op.attrs["axis"] % rank
-        out, y = self._c_order_out(op)
+        if op in self.concat_out:
+            out = self._new_dv(r)
+            out.f32 = y = self.concat_out[op]
+        else:
+            out, y = self._c_order_out(op)
         outer = int(np.prod(r.type.shape[:axis], dtype=np.int64))
         ld = int(np.prod(r.type.shape[axis:], dtype=np.int64))
         at = 0
         lib = self.lib
         for v in op.inputs:
-            x = self._c_order(v)
             inner = int(np.prod(v.type.shape[axis:], dtype=np.int64))
-            if outer * inner == 0:
+            if outer * inner == 0 or v in self.prealias:      # empty, or already in place
+                at += inner
                 continue
+            x = self._c_order(v)
             self._add("concat", lambda s, x=x, inner=inner, at=at: L.check(lib.mr_copy_rows_f32(
                 x.data_ptr(), outer, inner, y.data_ptr(), ld, at, s), "mr_copy_rows_f32"), nbytes=8 * outer * inner)
             at += inner
@@ -1026,19 +1128,25 @@ class RocmExecutable:
         """f32 matmul of two float tensors with NumPy's batch broadcasting (mira/ops.py:217-219;
         approx_f32 only), the epilogue fused."""
         av, wv = op.inputs[0], op.inputs[1]
-        a, w = self._c_order(av), self._c_order(wv)
         rs = tuple(op.result.type.shape)
         nb = len(rs) - 2
         M, N, K = rs[-2], rs[-1], av.type.shape[-1]
 
-        def batch_strides(shape):
-            full = (1,) * (len(rs) - len(shape)) + tuple(shape)
-            return [0 if full[i] == 1 else int(np.prod(full[i + 1:], dtype=np.int64)) for i in range(nb)]
+        def operand(v):
+            """(C-order base buffer, batch strides broadcast onto the result, last two strides)"""
+            base, shape, st, _ = self._view_chain(v)
+            t = self._c_order(base)
+            pad = len(rs) - len(shape)
+            full, fst = (1,) * pad + shape, (0,) * pad + st
+            return t, [0 if full[i] == 1 else fst[i] for i in range(nb)], fst[-2], fst[-1]
 
+        a, sa_, sam, sak = operand(av)
+        w, sw_, swk, swn = operand(wv)
         bdim = (C.c_int64 * max(nb, 1))(*rs[:nb])
-        sa = (C.c_int64 * max(nb, 1))(*batch_strides(av.type.shape))
-        sw = (C.c_int64 * max(nb, 1))(*batch_strides(wv.type.shape))
-        self.keep += [bdim, sa, sw]
+        sa = (C.c_int64 * max(nb, 1))(*sa_)
+        sw = (C.c_int64 * max(nb, 1))(*sw_)
+        mk = (C.c_int64 * 4)(sam, sak, swk, swn)
+        self.keep += [bdim, sa, sw, mk]
         out = self._new_dv(op.result)
         if out.nhwc:
             raise L.RocmError("an f32 matmul result read as an image has no rocm layout")
@@ -1046,7 +1154,7 @@ class RocmExecutable:
         batches = int(np.prod(rs[:nb], dtype=np.int64))
         lib = self.lib
         self._add("bmm_f32", lambda s: L.check(lib.mr_bmm_f32(
-            a.data_ptr(), w.data_ptr(), nb, bdim, sa, sw, M, N, K, C.byref(e), s), "mr_bmm_f32"),
+            a.data_ptr(), w.data_ptr(), nb, bdim, sa, sw, mk, M, N, K, C.byref(e), s), "mr_bmm_f32"),
             nbytes=4 * (av.type.numel + wv.type.numel) + self._epi_bytes(e, batches * M, N),
             nops=2 * batches * M * N * K)
         self._finish_i8(out, fused)

@@ -21,6 +21,8 @@ from oracle import golden as G
 from conftest import bits_equal
 from gpu_util import T, empty, epilogue, oracle_env, stream, sync
 
+T_ = T      # for tests whose parameters shadow T
+
 pytestmark = pytest.mark.gpu
 
 # f32 results of the approximate ops: |got - want| <= RTOL * |want| + ATOL * scale, where
@@ -157,7 +159,8 @@ def _bstrides(shape, rs):
                                            ((2, 1, 2, 3, 2, 5, 6), (2, 2, 1, 3, 2, 6, 4))])
 def test_bmm_f32_within_tolerance(lib, ashape, wshape):
     """a @ w with NumPy batch broadcasting and a scale+mask epilogue: every element within
-    1e-5 of the float64 product's magnitude sum (|a| @ |w|), the bound for any f32 order."""
+    1e-5 of the float64 product's magnitude sum (|a| @ |w|), the bound for any f32 order, plus
+    one f32 ulp of the result (masked entries are x - 10000, rounded at 10000's ulp)."""
     torch = _torch()
     rng = np.random.default_rng(len(ashape) * 10 + len(wshape))
     a = rng.standard_normal(ashape).astype(np.float32)
@@ -174,16 +177,47 @@ def test_bmm_f32_within_tolerance(lib, ashape, wshape):
     st, mk = T(scale.reshape(1)), T(mask)
     e = epilogue([("mul", L.BC_SCALAR, st, 0, False), ("add", L.BC_COL, mk, 1, False)], out_f32=y, ldo=N)
     ad, wd = T(a), T(w)
+    mk = (C.c_int64 * 4)(K, 1, N, 1)
     if nb > 4:
         with pytest.raises(L.RocmError):
-            L.check(lib.mr_bmm_f32(ad.data_ptr(), wd.data_ptr(), nb, None, None, None, M, N, K, C.byref(e),
+            L.check(lib.mr_bmm_f32(ad.data_ptr(), wd.data_ptr(), nb, None, None, None, mk, M, N, K, C.byref(e),
                                    stream()), "bmm")
         return
     arr = lambda v: (C.c_int64 * max(nb, 1))(*v)
     L.check(lib.mr_bmm_f32(ad.data_ptr(), wd.data_ptr(), nb, arr(rs[:nb]), arr(_bstrides(ashape, rs)),
-                           arr(_bstrides(wshape, rs)), M, N, K, C.byref(e), stream()), "bmm")
+                           arr(_bstrides(wshape, rs)), mk, M, N, K, C.byref(e), stream()), "bmm")
     sync()
-    _close(y.cpu().numpy().reshape(rs), want, scale=mag, rtol=0, atol=1e-5)
+    _close(y.cpu().numpy().reshape(rs), want, scale=mag, rtol=2.0 ** -23, atol=1e-5)
+
+
+@pytest.mark.parametrize("B,H,T,hd", [(1, 4, 273, 16), (3, 2, 40, 8), (2, 4, 300, 64)])
+def test_bmm_f32_reads_transposed_operands_in_place(lib, B, H, T, hd):
+    """The decode attention products with the cache read in place: scores = q @ keys^T and
+    context = p @ values, where keys/values are [B, T, H*hd] rows and the matmul takes their
+    transposed views through strides (short-K and long-K kernels)."""
+    torch = _torch()
+    rng = np.random.default_rng(T)
+    D = H * hd
+    q = rng.standard_normal((B, D)).astype(np.float32)
+    keys = rng.standard_normal((B, T, D)).astype(np.float32)
+    p = rng.random((B, H, 1, T)).astype(np.float32)
+    q4 = q.reshape(B, 1, H, hd).transpose(0, 2, 1, 3)                   # [B, H, 1, hd]
+    k4 = keys.reshape(B, T, H, hd).transpose(0, 2, 3, 1)                # [B, H, hd, T]
+    v4 = keys.reshape(B, T, H, hd).transpose(0, 2, 1, 3)                # [B, H, T, hd]
+    qd, kd, pd = T_(q), T_(keys), T_(p)
+    arr = lambda v: (C.c_int64 * 2)(*v)
+    for a_dev, a_np, sa, sam_sak, w_np, sw, swk_swn, (M, N, K) in [
+            (qd, q4, (D, hd), (D, 1), k4, (T * D, hd), (1, D), (1, T, hd)),
+            (pd, p, (H * T, T), (T, 1), v4, (T * D, hd), (D, 1), (1, hd, T))]:
+        want = np.matmul(a_np.astype(np.float64), w_np.astype(np.float64))
+        mag = np.matmul(np.abs(a_np).astype(np.float64), np.abs(w_np).astype(np.float64))
+        y = empty((B * H, N), torch.float32)
+        e = epilogue([], out_f32=y, ldo=N)
+        mk = (C.c_int64 * 4)(*sam_sak, *swk_swn)
+        L.check(lib.mr_bmm_f32(a_dev.data_ptr(), kd.data_ptr(), 2, arr((B, H)), arr(sa), arr(sw), mk, M, N, K,
+                               C.byref(e), stream()), "bmm")
+        sync()
+        _close(y.cpu().numpy().reshape(want.shape), want, scale=mag, rtol=0, atol=1e-5)
 
 
 # ---------------------------------------------------------------- libm epilogue steps (approximate)
