@@ -247,6 +247,10 @@ __device__ __forceinline__ float dequant(int32_t acc, double scale) {
   return static_cast<float>(__dmul_rn(static_cast<double>(acc), scale));
 }
 
+// Word 3 of a raw buffer resource (32-bit elements) on gfx9: loads past num_records
+// return 0 and stores past it are dropped, which the kernels use for bounds.
+constexpr int BUF_DWORD3 = 0x00020000;
+
 // ---------------------------------------------------------------- host-side epilogue validation
 
 int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out);

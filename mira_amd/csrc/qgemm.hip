@@ -142,6 +142,26 @@ __device__ __forceinline__ int quantize_med3(float y, double rxs) {
   return static_cast<int>(__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f));
 }
 
+// The same quantizer for four results, packed little-endian into one word.  The
+// quotient is clamped first (rounding commutes with a clamp to integer bounds) and
+// then rounded by adding 1.5 * 2^23: every sum lies in [2^23, 2^24), where the
+// spacing of floats is 1, so the addition rounds to the nearest integer with ties
+// to even (as rintf) and leaves q + 2^22 in the low mantissa bits; the low byte of
+// the bit pattern is q's two's-complement byte.  v_med3_f32 maps a NaN to -127, as
+// quantize_med3 does.  Three byte permutes gather the four low bytes.
+__device__ __forceinline__ uint32_t quantize4_med3(const float (&y)[4], double rxs) {
+  uint32_t b[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const float t = __builtin_amdgcn_fmed3f(static_cast<float>(__dmul_rn(static_cast<double>(y[c]), rxs)),
+                                            -127.0f, 127.0f);
+    b[c] = __float_as_uint(__fadd_rn(t, 12582912.0f));
+  }
+  const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u);   // bytes 0, 1: b0, b1
+  const uint32_t hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);   // bytes 0, 1: b2, b3
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
 __device__ __forceinline__ void load_cols4(const EpiDev& e, int col0, int N, EpiCols4& c) {
   bool vec = col0 + 3 < N && (e.ldo % 4 == 0) && (e.ldq % 4 == 0) && (e.ldacc % 4 == 0) &&
              (reinterpret_cast<uintptr_t>(e.out_f32) % 16 == 0) && (reinterpret_cast<uintptr_t>(e.out_i8) % 4 == 0) &&
@@ -599,6 +619,12 @@ __global__ void __launch_bounds__(WM* WN * 64)
             }
           }
         };
+        // the tile's result rows as raw buffers: a row past mvalid lies past num_records,
+        // so its store is dropped by the hardware, and offsets are 32-bit
+        const __amdgpu_buffer_rsrc_t rf = __builtin_amdgcn_make_buffer_rsrc(
+            e.out_f32 + mbase * e.ldo, 0, S_F32 ? mvalid * int(e.ldo) * 4 : 0, BUF_DWORD3);
+        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+            e.out_i8 + mbase * e.ldq, 0, S_I8 ? mvalid * int(e.ldq) : 0, BUF_DWORD3);
         float4 res_cur[S_FULL ? NRC : 1], res_next[S_FULL ? NRC : 1];
         load_res(0, res_cur);
 #pragma unroll
@@ -630,17 +656,14 @@ __global__ void __launch_bounds__(WM* WN * 64)
         if (k0 + NRC < NR) load_res(k0 + NRC, res_next);
 #pragma unroll
         for (int k = 0; k < NRC; ++k) {
-          if (local[k] < mvalid) {
-            const int64_t row = mbase + local[k];
-            if constexpr (S_F32)
-              *reinterpret_cast<float4*>(e.out_f32 + row * e.ldo + col0) = make_float4(y[k][0], y[k][1], y[k][2], y[k][3]);
-            if constexpr (S_I8) {
-              uint32_t packed = 0;
-#pragma unroll
-              for (int c = 0; c < 4; ++c) packed |= uint32_t(quantize_med3(y[k][c], e.out_rxs) & 0xff) << (8 * c);
-              *reinterpret_cast<uint32_t*>(e.out_i8 + row * e.ldq + col0) = packed;
-            }
+          const int lr = local[k];       // rows past mvalid: dropped by the resource's bound
+          if constexpr (S_F32) {
+            const v4i v = {int(__float_as_uint(y[k][0])), int(__float_as_uint(y[k][1])),
+                           int(__float_as_uint(y[k][2])), int(__float_as_uint(y[k][3]))};
+            __builtin_amdgcn_raw_buffer_store_b128(v, rf, (lr * int(e.ldo) + col0) * 4, 0, 0);
           }
+          if constexpr (S_I8)
+            __builtin_amdgcn_raw_buffer_store_b32(quantize4_med3(y[k], e.out_rxs), rq, lr * int(e.ldq) + col0, 0, 0);
         }
 #pragma unroll
         for (int k = 0; k < (S_FULL ? NRC : 1); ++k) res_cur[k] = res_next[k];

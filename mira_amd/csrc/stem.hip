@@ -36,7 +36,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int BAND = 8;           // pooled rows per workgroup
-constexpr int BUF_DWORD3 = 0x00020000;   // buffer resource word 3 for raw 32-bit loads on gfx9
 
 // Source of every padding tap: loads are never predicated, their address is
 // (a select before the load keeps all of a row's loads in flight at once).
