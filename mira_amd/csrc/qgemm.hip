@@ -46,8 +46,10 @@ enum AMode {
                  // per-tile input patch (tile rows plus the kernel's halo) held in LDS
 };
 
-// A_PATCH: LDS bytes reserved for one tile's input patch, and the tile height.
-constexpr int PATCH_MAX = 24576;
+// A_PATCH: LDS bytes reserved for one tile's input patch (ResNet layer 1: 6 x 58
+// pixels x 5 slots = 27 840 bytes), and the tile height.  With the 256x64 tile's
+// 12 KB ring, four workgroups fill a CU's 160 KB.
+constexpr int PATCH_MAX = 28672;
 // tile rows (pixels) of the A_PATCH configurations: N <= 64 and N <= 128
 constexpr int PATCH_BM64 = 256, PATCH_BM128 = 128;
 static int patch_bm(int n) { return n <= 64 ? PATCH_BM64 : PATCH_BM128; }
@@ -71,12 +73,11 @@ struct GemmArgs {
   // A_PATCH: a tile is `tr` output rows of one image (tr * OW <= BM pixels);
   // its patch is pr x pc input pixels (rows oh0-PH .. oh0-PH+pr-1, columns -PW .. pc-PW-1)
   int32_t tr, rg_per_img, pr, pc, patch_slots;
-  // A_PATCH divisions by launch constants: C_pad / 16 = 1 << pu_shift, and
+  // A_PATCH divisions by launch constants: n / (C_pad / 16 + 1) == umulhi(n, ps_magic),
   // n / pc == umulhi(n, pc_magic), n / OW == umulhi(n, ow_magic) with
   // magic = ceil(2^32 / d), exact for the n the kernel divides (n * d < 2^32,
   // checked on the host)
-  int32_t pu_shift;
-  uint32_t pc_magic, ow_magic;
+  uint32_t ps_magic, pc_magic, ow_magic;
 };
 
 // ceil(2^32 / d) for d >= 2: n / d == __umulhi(n, magic) whenever n * d < 2^32.  With
@@ -454,25 +455,23 @@ __global__ void __launch_bounds__(WM* WN * 64)
     for (int r = 0; r < 16; ++r) acc[b][r] = 0;
 
   // A_PATCH: 16-byte chunk j of patch pixel P (P = r * pc + c) sits at slot
-  // P * U + (j ^ patch_swz(P)), U = C_pad / 16 in {4, 8, 16}: 16 consecutive
-  // pixels of one chunk then fall on 16 distinct 16-byte bank groups, as in
-  // the ring.
-  const int pU = g.C_pad >> 4;
-  auto patch_swz = [&](int P) __attribute__((always_inline)) {
-    return ((P * pU) >> 4) & (pU - 1);
-  };
+  // P * S + j, S = C_pad / 16 + 1 in {5, 9, 17}: each pixel is followed by one
+  // unused slot, so 16 consecutive pixels' chunk j lie an odd number S of
+  // 16-byte groups apart and fall on 16 distinct bank groups.  A fragment's
+  // address is then a per-lane constant plus a per-step uniform offset.
+  const int pS = (g.C_pad >> 4) + 1;
   if constexpr (PATCH) {
 #pragma unroll
     for (int j = 0; j < PATCH_OPS; ++j) {
       const int slot = (wave * PATCH_OPS + j) * 64 + lane;
       const void* src = g_zero_page;
       if (slot < g.patch_slots) {
-        const int P = slot >> g.pu_shift;
-        const int chunk = (slot & (pU - 1)) ^ patch_swz(P);
+        const int P = static_cast<int>(__umulhi(static_cast<uint32_t>(slot), g.ps_magic));
+        const int chunk = slot - P * pS;            // pS - 1: the padding slot
         const int r = static_cast<int>(__umulhi(static_cast<uint32_t>(P), g.pc_magic));
         const int ih = p_oh0 - g.PH + r;
         const int iw = P - r * g.pc - g.PW;
-        if (unsigned(ih) < unsigned(g.H) && unsigned(iw) < unsigned(g.W))
+        if (chunk < pS - 1 && unsigned(ih) < unsigned(g.H) && unsigned(iw) < unsigned(g.W))
           src = g.a + ((int64_t(p_img) * g.H + ih) * g.W + iw) * g.C_pad + chunk * 16;
       }
       dma16(src, patch + (wave * PATCH_OPS + j) * 1024);
@@ -488,20 +487,22 @@ __global__ void __launch_bounds__(WM* WN * 64)
   // bytes 16h .. 16h+15 of the half for row r of each 32-row block.
   const int frag_row = lane & 31;
   const int swz = row_swz(frag_row);
-  // A_PATCH: patch pixel of each fragment row at tap (0, 0); rows past the
-  // tile's valid pixels read pixel 0 (their results are never stored)
-  int p_pix0[PATCH ? FM : 1];
+  // A_PATCH: LDS byte address of each fragment row's bytes at tap (0, 0), channel
+  // block 0 (its patch pixel times the pixel stride, plus the lane's 16-byte half);
+  // rows past the tile's valid pixels read pixel 0 (their results are never stored)
+  int p_addr0[PATCH ? FM : 1];
   if constexpr (PATCH) {
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       int p = wm * TM + i * 32 + frag_row;
       if (p >= mvalid) p = 0;
       const int orow = static_cast<int>(__umulhi(static_cast<uint32_t>(p), g.ow_magic));
-      p_pix0[i] = orow * g.pc + (p - orow * g.OW);
+      p_addr0[i] = ((orow * g.pc + (p - orow * g.OW)) * pS + (lane >> 5)) * 16;
     }
   }
-  // read cursor of A_PATCH for the step being read: patch offset kh * pc + kw
-  // of its tap, that tap's kw, and its channel block (scalars in registers)
+  // read cursor of A_PATCH for the step being read: the byte offset of its tap and
+  // channel block in the patch ((kh * pc + kw) * pixel stride + cb * 64), that tap's
+  // kw, and its channel block (scalars in registers)
   int q_off = 0, q_kw = 0, q_cb = 0;
   auto load_frags = [&](int stage, int kk, int off, int cb, v4i (&af)[FM], v4i (&bf)[FN]) {
     const int8_t* As = lds + stage * STAGE_BYTES;
@@ -510,9 +511,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       if constexpr (PATCH) {
-        const int P = p_pix0[i] + off;
-        const int chunk = (cb * 4 + 2 * kk + (lane >> 5)) ^ patch_swz(P);
-        af[i] = *reinterpret_cast<const v4i*>(patch + (P * pU + chunk) * 16);
+        af[i] = *reinterpret_cast<const v4i*>(patch + p_addr0[i] + off + kk * 32);
       } else {
         af[i] = *reinterpret_cast<const v4i*>(As + (wm * TM + i * 32 + frag_row) * KB + pc);
       }
@@ -548,12 +547,13 @@ __global__ void __launch_bounds__(WM* WN * 64)
     }
     load_frags(cur, NKK - 1, q_off, q_cb, a1, b1);
     if constexpr (PATCH) {   // advance the cursor to step kt + 1
+      q_off += 64;
       if (++q_cb == g.cb_per_tap) {
         q_cb = 0;
-        ++q_off;
+        q_off += pS * 16 - g.cb_per_tap * 64;        // next tap: one pixel on
         if (++q_kw == g.KW) {
           q_kw = 0;
-          q_off += g.pc - g.KW;
+          q_off += (g.pc - g.KW) * pS * 16;         // next kernel row: pc - KW pixels on
         }
       }
     }
@@ -876,13 +876,13 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
       G.dh == 1 && G.dw == 1 && G.kh * G.kw > 1 && G.o <= 128 && ow <= mr::patch_bm(G.o)) {
     const int32_t tr = std::min(mr::patch_bm(G.o) / ow, oh);
     const int32_t pr = tr + G.kh - 1, pc = ow + G.kw - 1;
-    const int64_t slots = int64_t(pr) * pc * (G.c_pad / 16);
+    const int64_t slots = int64_t(pr) * pc * (G.c_pad / 16 + 1);   // one padding slot per pixel
     // the kernel divides patch pixel indices (< pr * pc) by pc and tile rows (< patch_bm)
     // by ow through multiplier magics, exact while n * d < 2^32
     const bool magic_ok = pc >= 2 && ow >= 2 && uint64_t(pr) * pc * pc < (uint64_t(1) << 32) &&
                           uint64_t(mr::patch_bm(G.o)) * ow < (uint64_t(1) << 32);
     if (slots * 16 <= mr::PATCH_MAX && magic_ok) {
-      g.pu_shift = G.c_pad == 64 ? 2 : G.c_pad == 128 ? 3 : 4;
+      g.ps_magic = mr::div_magic(static_cast<uint32_t>(G.c_pad / 16 + 1));
       g.pc_magic = mr::div_magic(static_cast<uint32_t>(pc));
       g.ow_magic = mr::div_magic(static_cast<uint32_t>(ow));
       g.tr = tr;
