@@ -712,7 +712,8 @@ static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
       default: break;
     }
   }
-  if constexpr (AMODE == A_CONV16 || AMODE == A_CONV64 || AMODE == A_CONV4) {
+  // the MobileNet-style forms (also for dense mode: 1x1 convolutions run as GEMMs)
+  if constexpr (AMODE == A_CONV16 || AMODE == A_CONV64 || AMODE == A_CONV4 || AMODE == A_DENSE) {
     switch (spec_form(e)) {
       case SPEC_RELU6_F32: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RELU6_F32); return;
       case SPEC_BIAS_F32_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_F32_I8); return;
@@ -869,6 +870,12 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
   g.row_bytes = row_bytes;
   g.k_real = k_real;
   g.cb_per_tap = G.c_pad / 64;
+  // a 1x1 stride-1 unpadded convolution reads each output pixel's own input row: it is the
+  // dense GEMM [n*h*w, c_pad] x [c_pad, o] over the NHWC rows (K past c_pad reads zeros)
+  if (mode != mr::A_CONV4 && G.kh == 1 && G.kw == 1 && G.sh == 1 && G.sw == 1 && G.ph == 0 && G.pw == 0) {
+    g.lda = G.c_pad;
+    mode = mr::A_DENSE;
+  }
   // stride-1 convolutions with a halo (3x3 and the like) read A from a
   // per-tile input patch: each input pixel crosses L2 -> LDS about
   // (tr + kh - 1) / tr times instead of kh * kw times
@@ -899,6 +906,7 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
     case mr::A_PATCH: return mr::launch<mr::A_PATCH>(g, e, s);
     case mr::A_CONV4: return mr::launch<mr::A_CONV4>(g, e, s);
     case mr::A_CONV64: return mr::launch<mr::A_CONV64>(g, e, s);
+    case mr::A_DENSE: return mr::launch<mr::A_DENSE>(g, e, s);
     default: return mr::launch<mr::A_CONV16>(g, e, s);
   }
 }

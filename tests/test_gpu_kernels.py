@@ -329,7 +329,9 @@ CONV_CASES = [
     (2, 64, 15, 15, 128, 3, 2, 1, 1),
     (2, 64, 14, 14, 128, 1, 2, 0, 1),     # downsample
     (1, 256, 7, 7, 512, 3, 1, 1, 1),
-    (3, 24, 9, 9, 144, 1, 1, 0, 1),       # c_pad 32
+    (3, 24, 9, 9, 144, 1, 1, 0, 1),       # 1x1 as a dense GEMM, c_pad 32
+    (2, 144, 28, 28, 24, 1, 1, 0, 1),     # 1x1 as a dense GEMM, c_pad 144: K tail past the row
+    (2, 64, 14, 14, 384, 1, 1, 0, 1),     # 1x1 as a dense GEMM, 128x256 tiles
     (2, 16, 11, 11, 24, 3, 1, 2, 2),      # dilation 2
     (2, 1, 28, 28, 16, 3, 1, 1, 1),       # single channel (cnn.mira)
     # stride-1 convolutions read through the per-tile input patch
@@ -415,7 +417,9 @@ FORM_CONV_CASES = [
     (2, 64, 15, 15, 128, 3, 2, 1, 1),     # stride 2, 64-channel loader
     (1, 256, 7, 7, 512, 3, 1, 1, 1),      # 128x256 tiles
     (2, 64, 14, 14, 128, 1, 2, 0, 1),     # downsample
-    (2, 24, 14, 14, 144, 1, 1, 0, 1),     # 1x1 expansion, 16-byte chunk loader (c_pad 32)
+    (2, 24, 14, 14, 144, 1, 1, 0, 1),     # 1x1 expansion as a dense GEMM (c_pad 32)
+    (2, 96, 14, 14, 576, 1, 1, 0, 1),     # 1x1 expansion as a dense GEMM (c_pad 96)
+    (2, 160, 7, 7, 960, 1, 1, 0, 1),      # 1x1 expansion as a dense GEMM, partial column tile
     (2, 3, 17, 17, 32, 3, 2, 1, 1),       # 3-channel stem, 4-channel loader
 ]
 
