@@ -157,7 +157,9 @@ int mr_quantize_f16_nchw_nhwc(const float* x, int32_t n, int32_t c, int32_t h, i
  * acc[M,N] = a[M,K] (int8, row stride lda) x B[N,k_pad]^T (packed int8
  * weights, zero for k >= K and n >= N, N rounded up to n_pad rows),
  * exact int32, then the epilogue.  lda % 16 == 0, k_pad % 64 == 0,
- * n_pad % 32 == 0.  Every packed weight argument of this library stores the
+ * n_pad % 32 == 0; a holds M whole rows of lda bytes, and for M > 8 both
+ * a (M * lda bytes) and the packed weights are under 2 GiB (MR_EINVAL
+ * otherwise).  Every packed weight argument of this library stores the
  * logical B[n_pad][k_pad] K-step-major: byte k of row n at
  * ((k / 64) * n_pad + n) * 64 + k % 64. */
 int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int64_t n_pad,
@@ -184,7 +186,8 @@ int mr_w8_matmul_f32(const float* x, int64_t ldx, const int8_t* b, const float* 
  * B[n_pad][k_pad] (stored K-step-major as for mr_qmatmul) whose k index is
  * (kh, kw, c) with c fastest over c_pad
  * (or the stem row layout when c_pad == 4).  Result rows are NHWC pixels
- * (n, oh, ow), columns output channels. */
+ * (n, oh, ow), columns output channels.  x (n * h * w * c_pad bytes) and the
+ * packed weights are each under 2 GiB (MR_EINVAL otherwise). */
 int mr_qconv2d(const int8_t* x, const mr_conv_geom* g, const int8_t* b, int64_t k_pad,
                int64_t n_pad, const mr_epilogue* epi, void* stream);
 

@@ -8,12 +8,16 @@
 // Pipeline.  A workgroup owns a BM x BN tile of the result and walks K in
 // 64-byte steps.  Each step's A slice (BM x 64 bytes) and B slice (weights,
 // BN x 64 bytes, contiguous: weights are stored K-step-major,
-// [k_pad / 64][n_pad][64]) travel global -> LDS by direct-to-LDS loads
-// (global_load_lds_dwordx4: no VGPR staging), STAGES-1 steps ahead of the
-// MFMAs, through a ring of STAGES LDS buffers.  One s_barrier per step; the
-// only wait is a counted vmcnt for the step about to be consumed.  Padding
-// taps and rows/columns past the end load from a 256-byte zero page, so the
-// LDS copy is always complete and no lane needs a masked write.
+// [k_pad / 64][n_pad][64]) travel global -> LDS by direct-to-LDS loads (no
+// VGPR staging), STAGES-1 steps ahead of the MFMAs, through a ring of STAGES
+// LDS buffers.  The weights and the dense / 64-channel activation loaders use
+// buffer loads: a lane's offset is fixed for a tap (or for the whole loop) and
+// the step's advance is a scalar offset, so a step costs almost no vector
+// instructions; padding taps and rows/columns past the end carry an offset
+// past the buffer's range and read zeros.  The other activation loaders read
+// such chunks from a 256-byte zero page.  One s_barrier per step; the only
+// wait is a counted vmcnt for the step about to be consumed, so the LDS copy
+// is always complete and no lane needs a masked write.
 //
 // LDS layout.  Each row of a slice is 64 bytes = four 16-byte chunks; chunk c
 // of row r sits at position c ^ ((r >> 2) & 3).  gfx950's LDS serves 256 bytes
@@ -78,7 +82,15 @@ struct GemmArgs {
   // magic = ceil(2^32 / d), exact for the n the kernel divides (n * d < 2^32,
   // checked on the host)
   uint32_t ps_magic, pc_magic, ow_magic;
+  // dense / 64-channel conv loaders: bytes of A and of the packed weights, the ranges of
+  // their buffer resources (each < 2^31: offsets are 32-bit)
+  uint32_t a_bytes, b_bytes;
 };
+
+// A buffer-load offset past every resource's range: the load returns zeros.  The range
+// check compares the lane's offset (not the scalar offset) with the resource's size, so
+// a lane with this offset reads zeros whatever scalar offset the step adds.
+constexpr uint32_t OOB_OFF = 0x80000000u;
 
 // ceil(2^32 / d) for d >= 2: n / d == __umulhi(n, magic) whenever n * d < 2^32.  With
 // magic = (2^32 + e) / d, 0 <= e < d, n * magic / 2^32 = n / d + n * e / (d * 2^32), and
@@ -120,6 +132,11 @@ __device__ __forceinline__ void dma16(const void* src, int8_t* lds_dst) {
 }
 __device__ __forceinline__ void dma4(const void* src, int8_t* lds_dst) {
   __builtin_amdgcn_global_load_lds(src, (lds_void*)lds_dst, 4, 0, 0);
+}
+// 16 bytes per lane from a buffer resource at (lane offset + scalar offset) into LDS; the
+// 64 lanes' chunks land contiguously at lds_dst (the LDS address is a wave-uniform M0)
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, int8_t* lds_dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_dst, 16, voff, soff, 0, 0);
 }
 
 // Per-thread constants of the 4 result columns col0 .. col0+3 a thread owns
@@ -325,12 +342,19 @@ __global__ void __launch_bounds__(WM* WN * 64)
   // 16-byte chunk c of LDS row r sits at position c ^ row_swz(r)
   auto row_swz = [](int r) __attribute__((always_inline)) { return KB == 64 ? (r >> 2) & 3 : (r >> 1) & 7; };
 
-  // ---- A loader state, one entry per DMA this lane takes part in.  The
-  // per-step work of the dense and 64-channel loaders is one uniform offset,
-  // two compares and a select: every per-row product is taken here, once.
+  // ---- A loader state, one entry per DMA this lane takes part in.
+  // Dense and 64-channel conv loaders read through buffer resources: per step a lane's
+  // offset is fixed (dense: plus the step's K offset; conv: refreshed once per tap) and the
+  // rest of the step's offset is a scalar, so a step costs almost no vector instructions.
+  constexpr bool BUF_A = AMODE == A_DENSE || AMODE == A_CONV64;
+  const __amdgpu_buffer_rsrc_t rsrc_a =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(g.a), 0, BUF_A ? g.a_bytes : 0, BUF_DWORD3);
+  const __amdgpu_buffer_rsrc_t rsrc_b =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(g.b), 0, g.b_bytes, BUF_DWORD3);
+  uint32_t a_vo[A_OPS1];    // dense: offset of the lane's chunk at K = 0; conv64: at the current tap
+  int32_t a_px[A_OPS1];     // conv64: offset of the lane's chunk at tap (0, 0) (negative above/left of the image)
+  uint32_t a_tm[A_OPS1];    // conv64: bit kh * KW + kw set where that tap reads inside the image
   int64_t a_base[A_OPS1];   // conv16 / conv4: image pixel base
-  int64_t a_off[A_OPS1];    // dense: row chunk at K = 0; conv64: row chunk at tap (0, 0), channel block 0
-  int64_t a_lim[A_OPS1];    // dense: lda for a row inside M, 0 past it
   int32_t a_ih0[A_OPS1], a_iw0[A_OPS1], a_k[A_OPS1];
   bool a_ok[A_OPS1];
 #pragma unroll
@@ -348,10 +372,12 @@ __global__ void __launch_bounds__(WM* WN * 64)
     a_k[j] = koff;
     const int64_t m = m0 + row;
     a_ok[j] = m < g.M;
+    a_vo[j] = OOB_OFF;
+    a_px[j] = 0;
+    a_tm[j] = 0;
     if constexpr (AMODE == A_DENSE) {
-      a_base[j] = m * g.lda;
-      a_off[j] = a_base[j] + koff;
-      a_lim[j] = a_ok[j] ? g.lda : 0;
+      if (a_ok[j]) a_vo[j] = static_cast<uint32_t>(m * g.lda + koff);
+      a_base[j] = 0;
       a_ih0[j] = a_iw0[j] = 0;
     } else {
       const int32_t mm = a_ok[j] ? static_cast<int32_t>(m) : 0;
@@ -363,50 +389,55 @@ __global__ void __launch_bounds__(WM* WN * 64)
       a_base[j] = int64_t(img) * g.H * g.W;
       a_ih0[j] = oh * g.SH - g.PH;
       a_iw0[j] = ow * g.SW - g.PW;
-      a_off[j] = (a_base[j] + int64_t(a_ih0[j]) * g.W + a_iw0[j]) * g.C_pad + koff;
-      a_lim[j] = 0;
-      // rows past M fail every bounds check of the conv64 loader
-      if (AMODE == A_CONV64 && !a_ok[j]) a_ih0[j] = -(1 << 30);
+      if constexpr (AMODE == A_CONV64) {
+        a_px[j] = ((img * g.H + a_ih0[j]) * g.W + a_iw0[j]) * g.C_pad + koff;
+        uint32_t tm = 0;
+        if (a_ok[j]) {
+          for (int i = 0, t = 0; i < g.KH; ++i) {
+            const bool rok = unsigned(a_ih0[j] + i * g.DH) < unsigned(g.H);
+            for (int jj = 0; jj < g.KW; ++jj, ++t)
+              if (rok && unsigned(a_iw0[j] + jj * g.DW) < unsigned(g.W)) tm |= 1u << t;
+          }
+        }
+        a_tm[j] = tm;
+      }
     }
   }
   // ---- B loader state (weights K-step-major: 64-byte slice kt of row n at (kt * n_pad + n) * 64).
-  // Rows past n_pad read the zero page at every step: their step mask is 0.
-  const uintptr_t zero_page = reinterpret_cast<uintptr_t>(g_zero_page);
-  const uintptr_t a_addr = reinterpret_cast<uintptr_t>(g.a);
-  uintptr_t b_src[B_OPS];
-  uint64_t b_mask[B_OPS];
+  // Rows past n_pad read zeros at every step.
+  uint32_t b_vo[B_OPS];
 #pragma unroll
   for (int j = 0; j < B_OPS; ++j) {
     const int slot = (wave * B_OPS + j) * 64 + lane;
     const int row = slot / CPR;
     const int koff = ((slot % CPR) ^ row_swz(row)) << 4;
     const int n = n0 + row;
-    const bool ok = n < g.n_pad;
-    b_src[j] = ok ? reinterpret_cast<uintptr_t>(g.b + (int64_t(koff >> 6) * g.n_pad + n) * 64 + (koff & 63)) : zero_page;
-    b_mask[j] = ok ? ~uint64_t(0) : 0;
+    b_vo[j] = n < g.n_pad ? static_cast<uint32_t>(((koff >> 6) * g.n_pad + n) * 64 + (koff & 63)) : OOB_OFF;
   }
 
-  // load cursor of A_CONV64: (kernel row, kernel column, 64-channel block) of the next step
-  int l_kh = 0, l_kw = 0, l_cb = 0;
+  // load cursor of A_CONV64: (kernel row, kernel column, 64-channel block) of the next
+  // step, its tap index and the tap's offset in the input
+  int l_kh = 0, l_kw = 0, l_cb = 0, l_t = 0, l_off = 0;
 
   auto issue = [&](int kt, int stage) {
     int8_t* As = lds + stage * STAGE_BYTES;
     int8_t* Bs = As + A_STAGE;
+    if constexpr (AMODE == A_CONV64) {
+      if (l_cb == 0) {   // a new tap: the lanes whose row reads outside the image for it read zeros
+#pragma unroll
+        for (int j = 0; j < A_OPS; ++j)
+          a_vo[j] = (a_tm[j] >> l_t) & 1 ? static_cast<uint32_t>(a_px[j] + l_off) : OOB_OFF;
+      }
+    }
 #pragma unroll
     for (int j = 0; j < A_OPS; ++j) {
-      const void* src = g_zero_page;
+      int8_t* dst = As + (wave * A_OPS + j) * (A_ROWS_PER_OP * KB);
       if constexpr (AMODE == A_DENSE) {
-        const int64_t k0 = int64_t(kt) * KB;   // uniform
-        const bool ok = k0 + a_k[j] < a_lim[j];
-        src = reinterpret_cast<const void*>(ok ? a_addr + a_off[j] + k0 : zero_page);
+        dma16_buf(rsrc_a, dst, a_vo[j] + static_cast<uint32_t>(kt * KB), 0);
       } else if constexpr (AMODE == A_CONV64) {
-        // uniform offset of the step's tap and channel block (k_pad == k_real:
-        // the cursor never passes the last tap)
-        const int32_t dh = l_kh * g.DH, dw = l_kw * g.DW;
-        const int64_t step_off = (int64_t(dh) * g.W + dw) * g.C_pad + l_cb * 64;
-        const bool ok = unsigned(a_ih0[j] + dh) < unsigned(g.H) && unsigned(a_iw0[j] + dw) < unsigned(g.W);
-        src = reinterpret_cast<const void*>(ok ? a_addr + a_off[j] + step_off : zero_page);
+        dma16_buf(rsrc_a, dst, a_vo[j], static_cast<uint32_t>(l_cb * 64));
       } else if constexpr (AMODE == A_CONV16) {
+        const void* src = g_zero_page;
         const int32_t k = kt * BK + a_k[j];
         if (a_ok[j] && k < g.k_real) {
           const int32_t tap = k / g.C_pad;
@@ -418,7 +449,9 @@ __global__ void __launch_bounds__(WM* WN * 64)
           if (unsigned(ih) < unsigned(g.H) && unsigned(iw) < unsigned(g.W))
             src = g.a + (a_base[j] + int64_t(ih) * g.W + iw) * g.C_pad + c0;
         }
+        dma16(src, dst);
       } else {  // A_CONV4: one dword = one tap (4 channels) of kernel row kh
+        const void* src = g_zero_page;
         const int32_t k = kt * BK + a_k[j];
         const int32_t kh = k / g.row_bytes;
         const int32_t kw = (k - kh * g.row_bytes) >> 2;
@@ -426,24 +459,22 @@ __global__ void __launch_bounds__(WM* WN * 64)
         const int32_t iw = a_iw0[j] + kw * g.DW;
         if (a_ok[j] && kh < g.KH && kw < g.KW && unsigned(ih) < unsigned(g.H) && unsigned(iw) < unsigned(g.W))
           src = g.a + (a_base[j] + int64_t(ih) * g.W + iw) * 4;
+        dma4(src, dst);
       }
-      if constexpr (AMODE == A_CONV4)
-        dma4(src, As + (wave * A_OPS + j) * (A_ROWS_PER_OP * KB));
-      else
-        dma16(src, As + (wave * A_OPS + j) * (A_ROWS_PER_OP * KB));
     }
+    const uint32_t b_soff = static_cast<uint32_t>(kt * (KB / 64) * g.n_pad * 64);
 #pragma unroll
-    for (int j = 0; j < B_OPS; ++j)
-      dma16(reinterpret_cast<const void*>(b_src[j] + ((uint64_t(kt) * (KB / 64) * g.n_pad * 64) & b_mask[j])),
-            Bs + (wave * B_OPS + j) * 1024);
+    for (int j = 0; j < B_OPS; ++j) dma16_buf(rsrc_b, Bs + (wave * B_OPS + j) * 1024, b_vo[j], b_soff);
     if constexpr (AMODE == A_CONV64) {
       l_cb += KB / 64;
       if (l_cb == g.cb_per_tap) {
         l_cb = 0;
+        ++l_t;
         if (++l_kw == g.KW) {
           l_kw = 0;
           ++l_kh;
         }
+        l_off = (l_kh * g.DH * g.W + l_kw * g.DW) * g.C_pad;
       }
     }
   };
@@ -803,6 +834,10 @@ int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int
   g.n_pad = static_cast<int32_t>(n_pad);
   g.k_tiles = static_cast<int32_t>(k_pad / mr::BK);
   if (M <= 8) return mr::gemv_launch(a, lda, b, k_pad, n_pad, M, N, e, static_cast<hipStream_t>(stream));
+  MR_REQUIRE(M * lda < (int64_t(1) << 31) && k_pad * n_pad < (int64_t(1) << 31),
+             "mr_qmatmul: operands of 2 GiB or more are not supported (32-bit buffer offsets)");
+  g.a_bytes = static_cast<uint32_t>(M * lda);
+  g.b_bytes = static_cast<uint32_t>(k_pad * n_pad);
   return mr::launch<mr::A_DENSE>(g, e, static_cast<hipStream_t>(stream));
 }
 
@@ -827,7 +862,8 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
   } else {
     MR_REQUIRE(G.c_pad % 16 == 0 && G.c_pad >= G.c, "mr_qconv2d: c_pad %d must be 4 or a multiple of 16 >= c",
                G.c_pad);
-    mode = G.c_pad % 64 == 0 ? mr::A_CONV64 : mr::A_CONV16;
+    // the 64-channel loader keeps one bit per kernel tap (at most 32 taps)
+    mode = G.c_pad % 64 == 0 && G.kh * G.kw <= 32 ? mr::A_CONV64 : mr::A_CONV16;
     k_real = G.kh * G.kw * G.c_pad;
   }
   MR_REQUIRE(k_pad >= k_real && k_pad % 64 == 0, "mr_qconv2d: k_pad %lld must be >= %d and a multiple of 64",
@@ -870,6 +906,10 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
   g.row_bytes = row_bytes;
   g.k_real = k_real;
   g.cb_per_tap = G.c_pad / 64;
+  MR_REQUIRE(int64_t(G.n) * G.h * G.w * G.c_pad < (int64_t(1) << 31) && k_pad * n_pad < (int64_t(1) << 31),
+             "mr_qconv2d: operands of 2 GiB or more are not supported (32-bit buffer offsets)");
+  g.a_bytes = static_cast<uint32_t>(int64_t(G.n) * G.h * G.w * G.c_pad);
+  g.b_bytes = static_cast<uint32_t>(k_pad * n_pad);
   // a 1x1 stride-1 unpadded convolution reads each output pixel's own input row: it is the
   // dense GEMM [n*h*w, c_pad] x [c_pad, o] over the NHWC rows (K past c_pad reads zeros)
   if (mode != mr::A_CONV4 && G.kh == 1 && G.kw == 1 && G.sh == 1 && G.sw == 1 && G.ph == 0 && G.pw == 0) {
