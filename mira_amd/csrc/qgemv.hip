@@ -16,6 +16,7 @@ namespace mr {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int GEMV_CPW = 2;   // output columns per lane group
+constexpr int GEMV_UNR = 4;   // 16-byte weight chunks per column a lane has in flight
 
 struct GemvArgs {
   const int8_t* a;    // [M][lda] int8 activations
@@ -46,23 +47,34 @@ __global__ void __launch_bounds__(256) qgemv_kernel(const GemvArgs g, const EpiD
 #pragma unroll
     for (int c = 0; c < GEMV_CPW; ++c) brow[c] = g.b + int64_t(min(n0 + c, g.N - 1)) * 64;
     const int64_t kstep = int64_t(g.n_pad) * 64;   // bytes between K steps of one row
-    for (int k16 = sub; k16 < chunks; k16 += lpc) {
-      v4i w[GEMV_CPW];
+    // GEMV_UNR chunks per column in flight per lane: the weights are read once, so the
+    // stream's rate is the bytes in flight over the memory latency
+    for (int kb = sub; kb < chunks; kb += GEMV_UNR * lpc) {
+      v4i w[GEMV_UNR][GEMV_CPW];
 #pragma unroll
-      for (int c = 0; c < GEMV_CPW; ++c)
-        w[c] = *reinterpret_cast<const v4i*>(brow[c] + (k16 >> 2) * kstep + (k16 & 3) * 16);
-#pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        if (m >= g.M) break;
-        // activation bytes past K read the zero-padded row stride or, beyond
-        // lda, contribute against zero weights; lda >= K and the weights are
-        // zero for k >= K, so only bytes < lda are ever nonzero products
-        v4i x = {0, 0, 0, 0};
-        if (k16 * 16 < g.lda) x = *reinterpret_cast<const v4i*>(g.a + m * g.lda + k16 * 16);
+      for (int u = 0; u < GEMV_UNR; ++u) {
+        const int k16 = min(kb + u * lpc, chunks - 1);   // past the end: reread the last chunk, unused
 #pragma unroll
         for (int c = 0; c < GEMV_CPW; ++c)
+          w[u][c] = *reinterpret_cast<const v4i*>(brow[c] + (k16 >> 2) * kstep + (k16 & 3) * 16);
+      }
 #pragma unroll
-          for (int q = 0; q < 4; ++q) acc[m][c] = __builtin_amdgcn_sdot4(x[q], w[c][q], acc[m][c], false);
+      for (int u = 0; u < GEMV_UNR; ++u) {
+        const int k16 = kb + u * lpc;
+        if (k16 >= chunks) break;
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          if (m >= g.M) break;
+          // activation bytes past K read the zero-padded row stride or, beyond
+          // lda, contribute against zero weights; lda >= K and the weights are
+          // zero for k >= K, so only bytes < lda are ever nonzero products
+          v4i x = {0, 0, 0, 0};
+          if (k16 * 16 < g.lda) x = *reinterpret_cast<const v4i*>(g.a + m * g.lda + k16 * 16);
+#pragma unroll
+          for (int c = 0; c < GEMV_CPW; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[m][c] = __builtin_amdgcn_sdot4(x[q], w[u][c][q], acc[m][c], false);
+        }
       }
     }
   }

@@ -29,6 +29,7 @@
 #include "mr_common.hpp"
 
 #include <climits>
+#include <type_traits>
 
 namespace mr {
 
@@ -70,6 +71,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
   const int img = blockIdx.x / bands;
   const int pr0 = (blockIdx.x - img * bands) * BAND;
   const int pr_end = min(pr0 + BAND, a.POH);
+  // the convolution rows this band walks
+  const int cr_first = max(2 * pr0 - PPL, 0);
+  const int cr_last = min(2 * (pr_end - 1) + 1, a.OH - 1);
 
   // K step s of channel block j: lane holds row 32j + lane%32, K bytes 32s + 16*(lane/32) .. +16
   for (int i = threadIdx.x; i < KSUB * 2 * 64; i += 256) {
@@ -151,11 +155,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
   };
 
   // Convolution row cr -> h[j][t]: channel 32j + lane%32, max over the window
-  // columns of pooled column wave*PPW + 8*half + t.  The A fragments of row
-  // cr are in afrag on entry; those of row `next` are on their way on return.
-  v4i afrag[KSUB];
+  // columns of pooled column wave*PPW + 8*half + t.  The A fragments of rows
+  // cr and cr + 1 are in afr[cr & 1] and afr[(cr + 1) & 1] on entry (two rows
+  // in flight hide the input's latency); those of row cr + 2 replace row cr's.
+  v4i afr[2][KSUB];
   __syncthreads();   // weights in LDS
-  auto conv_row = [&](int cr, int next, int (&h)[2][8]) {
+  auto conv_row = [&](auto par, int cr, int (&h)[2][8]) {
+    constexpr int P = decltype(par)::value;
     v16i acc[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -164,8 +170,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
 #pragma unroll
     for (int s = 0; s < KSUB; ++s)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afrag[s], bw_lds[s][j][lane], acc[j], 0, 0, 0);
-    load_row(next, afrag);   // in flight during the pooling of this row
+      for (int j = 0; j < 2; ++j)
+        acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[P][s], bw_lds[s][j][lane], acc[j], 0, 0, 0);
+    if (cr + 2 <= cr_last) load_row(cr + 2, afr[P]);   // in flight during the next rows
     // Register r of a lane holds column 8*(r/4) + 4*half + r%4: the lower
     // half has columns 0-3, 8-11, 16-19, 24-27, the upper 4-7, ..., 28-31.
     // v_permlane32_swap(X, Y) exchanges X's upper 32 lanes with Y's lower 32
@@ -288,15 +295,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
   // Pooled row p takes convolution rows 2p-1 (PK == 3), 2p and 2p+1; the host
   // guarantees 2p - PPL < OH for every pooled row.  Rows are walked in order,
   // row 2p+1 carrying over into pooled row p+1.
-  const int cr_first = max(2 * pr0 - PPL, 0);
-  const int cr_last = min(2 * (pr_end - 1) + 1, a.OH - 1);
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
   int carry[2][8];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int t = 0; t < 8; ++t) carry[j][t] = INT_MIN;
-  load_row(cr_first, afrag);
-  if (PK == 3 && pr0 > 0) conv_row(2 * pr0 - 1, min(2 * pr0, cr_last), carry);
+  if (cr_first & 1) load_row(cr_first, afr[1]); else load_row(cr_first, afr[0]);
+  if (cr_first + 1 <= cr_last) {
+    if (cr_first & 1) load_row(cr_first + 1, afr[0]); else load_row(cr_first + 1, afr[1]);
+  }
+  if (PK == 3 && pr0 > 0) conv_row(P1{}, 2 * pr0 - 1, carry);   // 2 * pr0 - 1 is odd
   for (int p = pr0; p < pr_end; ++p) {
     const int r0 = 2 * p, r1 = 2 * p + 1;
     int v[2][8], h[2][8];
@@ -305,7 +315,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
 #pragma unroll
       for (int t = 0; t < 8; ++t) v[j][t] = PK == 3 ? carry[j][t] : INT_MIN;
     if (r0 < a.OH) {
-      conv_row(r0, min(r1, cr_last), h);
+      conv_row(P0{}, r0, h);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -316,7 +326,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
 #pragma unroll
       for (int t = 0; t < 8; ++t) carry[j][t] = INT_MIN;
     if (r1 < a.OH) {
-      conv_row(r1, min(r1 + 1, cr_last), carry);
+      conv_row(P1{}, r1, carry);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
