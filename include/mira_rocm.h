@@ -172,11 +172,12 @@ int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int
  * w_scale[n]) (rounded on to f16 when w_f16 != 0: a dequantize of dtype
  * f16) with q packed as B[n_pad][k_pad] (B[n][k] = q[k][n], stored
  * K-step-major as for mr_qmatmul), f32 multiply-adds, then the epilogue (its
- * scale must be NULL and it writes no int32 accumulators).  The weights are
- * streamed once per block of 8 rows, so it is meant for decode shapes
- * (M <= 524280).  ldx >= K, x and b 16-byte aligned.  The sums run in another order than
- * NumPy's, so the result matches to f32 rounding (relative 1e-5), not bit
- * for bit. */
+ * scale must be NULL and it writes no int32 accumulators).  Up to 16 rows the
+ * weights are streamed once per block of 8 rows (decode shapes); more rows run
+ * as 128 x 128 tiles on f32 MFMAs when K and ldx are multiples of 4 and x is
+ * under 2 GiB, else as 8-row blocks (M <= 524280).  ldx >= K, x and b 16-byte
+ * aligned.  The sums run in another order than NumPy's, so the result matches
+ * to f32 rounding (relative 1e-5), not bit for bit. */
 int mr_w8_matmul_f32(const float* x, int64_t ldx, const int8_t* b, const float* w_scale, int32_t w_f16,
                      int64_t k_pad, int64_t n_pad, int64_t M, int64_t N, int64_t K, const mr_epilogue* epi,
                      void* stream);

@@ -233,8 +233,8 @@ extern "C" int mr_w8_matmul_f32(const float* x, int64_t ldx, const int8_t* b, co
                                 int64_t k_pad, int64_t n_pad, int64_t M, int64_t N, int64_t K,
                                 const mr_epilogue* epi, void* stream) {
   MR_REQUIRE(x && b && w_scale, "mr_w8_matmul_f32: NULL operand");
-  MR_REQUIRE(M >= 0 && M <= 8 * 65535 && N > 0 && K > 0, "mr_w8_matmul_f32: M=%lld, N=%lld, K=%lld",
-             (long long)M, (long long)N, (long long)K);
+  MR_REQUIRE(M >= 0 && N > 0 && K > 0, "mr_w8_matmul_f32: M=%lld, N=%lld, K=%lld", (long long)M, (long long)N,
+             (long long)K);
   MR_REQUIRE(ldx >= K, "mr_w8_matmul_f32: ldx %lld < K %lld", (long long)ldx, (long long)K);
   MR_REQUIRE(k_pad >= K && k_pad % 64 == 0, "mr_w8_matmul_f32: k_pad %lld must be >= K and a multiple of 64",
              (long long)k_pad);
@@ -247,6 +247,13 @@ extern "C" int mr_w8_matmul_f32(const float* x, int64_t ldx, const int8_t* b, co
   const int rc = mr::make_epi(epi, N, false, &e);
   if (rc != MR_OK) return rc;
   if (M == 0) return MR_OK;
+  // more than 16 rows: tiles on f32 MFMAs (the weights cross HBM once per 128 rows)
+  if (M > 16) {
+    const int rt = mr::w8gemm_launch(x, ldx, b, w_scale, w_f16, k_pad, n_pad, M, N, K, e, static_cast<hipStream_t>(stream));
+    if (rt != MR_EUNSUPPORTED) return rt;
+  }
+  MR_REQUIRE(M <= 8 * 65535, "mr_w8_matmul_f32: M=%lld rows need K and ldx multiples of 4 (tiled kernel)",
+             (long long)M);
   mr::GemvArgs g = {};
   g.b = b;
   g.lda = K;   // activation columns (the kernel stops at K)

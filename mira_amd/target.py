@@ -101,7 +101,7 @@ FLOAT_DTYPES = ("f32", "f16")
 # ops whose rank-4 operands and results are images, stored NHWC
 IMAGE_OPS = ("qconv2d", "conv2d", "maxpool2d", "pad", "reduce_mean")
 
-W8_MAX_ROWS = 64     # mr_w8_matmul_f32 streams the weights once per 8 rows: decode shapes only
+W8_STREAM_ROWS = 64   # mr_w8_matmul_f32 streams the weights once per 8 rows when K % 4 != 0
 
 
 _UNARY_CODES = {L.EPI_FN[f] for f in L.EPI_UNARY}
@@ -219,11 +219,12 @@ class RocmTarget:
         return self._check_epilogue(op, op.result.type.shape, False, first_operand=2)
 
     def _check_w8_matmul(self, op: "Op") -> Optional[str]:
-        """Decode-shaped matmuls of the weight-only int8 mode (mira/quantize.py:45-68): an f32
-        activation of at most W8_MAX_ROWS rows against a `dequantize` [K, N] weight.  These
-        compute in f32 in another summation order than BLAS's, so they match the reference
-        to f32 rounding (relative 1e-5), not bit for bit; every other f32 matmul stays on the
-        CPU."""
+        """Matmuls of the weight-only int8 mode (mira/quantize.py:45-68): an f32 activation
+        against a `dequantize` [K, N] weight.  Decode shapes stream the weights once per 8
+        rows; more rows run as f32-MFMA tiles when K % 4 == 0 (else at most W8_STREAM_ROWS
+        rows).  These compute in f32 in another summation order than BLAS's, so they match
+        the reference to f32 rounding (relative 1e-5), not bit for bit; every other f32
+        matmul stays on the CPU."""
         x, w = op.inputs[0], op.inputs[1]
         p = w.producer
         if p is None or p.kind != "dequantize" or p.attrs["axis"] != 1 or w.type.rank != 2:
@@ -232,8 +233,12 @@ class RocmTarget:
         if x.type.rank not in (2, 3) or x.type.dtype not in FLOAT_DTYPES:
             return "weight-only int8 matmul runs on rocm for rank-2/3 float activations"
         rows = int(np.prod(x.type.shape[:-1], dtype=np.int64))
-        if rows > W8_MAX_ROWS:
-            return f"weight-only int8 matmul runs on rocm for decode shapes (<= {W8_MAX_ROWS} rows), not {rows}"
+        K = int(x.type.shape[-1])
+        if K % 4 != 0 and rows > W8_STREAM_ROWS:
+            return (f"weight-only int8 matmul of {rows} rows runs on rocm only for K % 4 == 0 "
+                    f"(or <= {W8_STREAM_ROWS} rows), K is {K}")
+        if rows * K * 4 >= 2 ** 31:
+            return "weight-only int8 matmul: an activation of 2 GiB or more"
         return self._check_epilogue(op, op.result.type.shape, False)
 
     def _check_epilogue(self, op: "Op", shape: tuple, is_conv: bool, first_operand: int = 1) -> Optional[str]:

@@ -258,6 +258,40 @@ def test_w8_matmul_bias_relu(lib, M, K, N, ldx):
     assert bits_equal(yq, G.quantize_activation(y, 0.02).astype(np.int8))
 
 
+@pytest.mark.parametrize("M,K,N,ldx", [(17, 64, 33, 64), (128, 784, 512, 784), (300, 1024, 1000, 1028),
+                                       (1000, 256, 130, 256), (40, 33, 20, 36)])
+def test_w8_matmul_tiled(lib, M, K, N, ldx):
+    """More than 16 rows: 128 x 128 f32-MFMA tiles (ragged M, N and K tails; the last case,
+    K % 4 != 0, takes the 8-row weight stream instead)."""
+    rng = np.random.default_rng(M * 7 + K + N)
+    x = rng.standard_normal((M, ldx)).astype(np.float32)
+    x[:, K:] = np.inf                      # columns >= K must never be read as data
+    w = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    q, s = G.quantize_array(w, 1)
+    deq = G.dequantize({"q": q, "scale": s, "axis": 1, "dtype": "f32"})
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    want = G.matmul([x[:, :K], deq, bias], {"epilogue": (("add", 2, False), ("relu", None, False))})
+    y, yq = _run_w8(lib, x, K, q, s, [("add", L.BC_COL, bias, False), ("relu", 0, None, False)], next_xs=0.02)
+    bound = np.abs(x[:, :K]).astype(np.float64) @ np.abs(deq).astype(np.float64) + np.abs(bias)
+    assert np.all(np.abs(y.astype(np.float64) - want) <= W8_TOL * bound)
+    assert (y >= 0).all()
+    assert bits_equal(yq, G.quantize_activation(y, 0.02).astype(np.int8))
+
+
+def test_w8_matmul_tiled_f16_weights(lib):
+    """The tiled kernel with an f16 dequantize: weights fl16(fl32(q * scale))."""
+    rng = np.random.default_rng(81)
+    M, K, N = 200, 512, 200
+    x = rng.standard_normal((M, K)).astype(np.float16).astype(np.float32)
+    q = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    s = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    deq = G.dequantize({"q": q, "scale": s, "axis": 1, "dtype": "f16"})
+    want = G.matmul([x, deq.astype(np.float32)], {})
+    y, _ = _run_w8(lib, x, K, q, s, [], w16=True)
+    bound = np.abs(x).astype(np.float64) @ np.abs(deq.astype(np.float64))
+    assert np.all(np.abs(y.astype(np.float64) - want) <= W8_TOL * bound)
+
+
 def test_w8_matmul_f16_weights(lib):
     """A dequantize of dtype f16 (mira/ops.py:584): the weights are fl16(fl32(q * scale)); with
     f16 activations and an f16 result rounded after the epilogue."""

@@ -340,6 +340,14 @@ def test_weight_only_mlp50m_batch1(precision):
     assert np.abs(got - want).max() <= tol * np.abs(want).max()
 
 
+def test_weight_only_mlp50m_batch4096():
+    """The 4096-row weight-only MLP-50M on the f32-MFMA tiles, every row against the oracle."""
+    g = _weight_only(models.mlp_50m(batch=4096))
+    runner, (got,), (want,) = _run_weight_only(g, {"x": models.normal_batch((4096, 4096), 4)})
+    assert runner.devices == ["rocm"] and _w8_launches(runner) == 4
+    assert np.abs(got - want).max() <= W8_MODEL_TOL * np.abs(want).max()
+
+
 def test_weight_only_mlp_mira_batch64():
     """The reference's own int8 check (its tests/test_control_dynamic_quant.py:178-189) with
     the three matmuls on rocm: within 0.05 of the f32 model, argmax agreement above 0.9."""

@@ -146,17 +146,28 @@ def test_to_f16_lowering():
 
 
 def test_check_decisions_weight_only():
-    """Weight-only int8 matmuls run on rocm for decode shapes (up to 64 rows); larger
-    batches, and matmuls whose weight is not a dequantize constant, stay on the CPU."""
+    """Weight-only int8 matmuls run on rocm at any batch whose K is a multiple of 4 (f32-MFMA
+    tiles above 16 rows); with K % 4 != 0 only up to 64 rows (the 8-row weight stream); matmuls
+    whose weight is not a dequantize constant stay on the CPU."""
     t = RocmTarget()
-    for batch, placed in ((4, True), (64, True), (65, False)):
-        g = models.mlp_mira(batch=batch)
+    for batch in (4, 64, 65, 4096):
+        g = models.mlp_mira(batch=batch)      # K = 784, 512, 256
         LW.prepare(g)
         LW.weight_only(g)
         mm = [op for op in g.compute_ops() if op.kind == "matmul"]
         assert len(mm) == 3
-        reasons = [t.check(op) for op in mm]
-        assert all(r is None for r in reasons) if placed else all("decode shapes" in r for r in reasons)
+        assert all(t.check(op) is None for op in mm)
+    from harness.graph import Graph
+    for rows, ok in ((64, True), (65, False)):
+        g = Graph("k33")
+        x = g.input("x", (rows, 33))
+        w = g.const(np.ones((33, 8), np.float32))
+        y = g.op("matmul", [x, w])
+        g.outputs = [y]
+        w.producer.kind = "dequantize"
+        w.producer.attrs = {"q": np.ones((33, 8), np.int8), "scale": np.ones(8, np.float32), "axis": 1, "dtype": "f32"}
+        r = t.check(y.producer)
+        assert (r is None) if ok else ("K % 4 == 0" in r)
 
 
 def test_check_decisions():
