@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MR_ABI_VERSION 5
+#define MR_ABI_VERSION 6
 
 enum mr_status {
   MR_OK = 0,
@@ -181,6 +181,19 @@ int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int
 int mr_w8_matmul_f32(const float* x, int64_t ldx, const int8_t* b, const float* w_scale, int32_t w_f16,
                      int64_t k_pad, int64_t n_pad, int64_t M, int64_t N, int64_t K, const mr_epilogue* epi,
                      void* stream);
+
+/* Replaces, for convolutions of the int8 weight-only mode (mira/quantize.py:45-68),
+ * mira/ops.py:265-276 _conv2d_ref (groups 1) over the dequantize constant of
+ * mira/ops.py:581-589: y[n,oh,ow,o] (NHWC rows = output pixels) = the convolution of
+ * the NHWC f32 image x (g->c channels per pixel, c % 4 == 0) with
+ * W[o][c][kh][kw] = fl32(q * w_scale[o]) (rounded on to f16 when w_f16 != 0), q packed
+ * as B[n_pad][k_pad] with k = (kh * kw_count + kw) * g->c_pad + c (c_pad % 4 == 0,
+ * channels c..c_pad-1 zero), K-step-major as for mr_qmatmul; then the epilogue (scale
+ * NULL, no int32 accumulators).  f32 multiply-adds on MFMAs in another order than
+ * NumPy's, so the result matches to f32 rounding (relative 1e-5), not bit for bit.
+ * x and the weights each under 2 GiB. */
+int mr_w8_conv2d_f32(const float* x, const mr_conv_geom* g, const int8_t* b, const float* w_scale, int32_t w_f16,
+                     int64_t k_pad, int64_t n_pad, const mr_epilogue* epi, void* stream);
 
 /* Replaces mira/ops.py:630-634 _qconv2d_ref (after quantize_activation):
  * implicit-GEMM convolution of NHWC int8 x with packed weights

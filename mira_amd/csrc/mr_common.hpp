@@ -261,8 +261,10 @@ int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, in
 
 // Weight-only int8 matmul of many rows on f32 MFMAs (w8gemm.hip); MR_EUNSUPPORTED when K
 // or ldx is not a multiple of 4 or an operand reaches 2 GiB.
+// With a conv geometry, the implicit-GEMM convolution of an NHWC f32 image (C % 4 == 0).
 int w8gemm_launch(const float* x, int64_t ldx, const int8_t* b, const float* w_scale, int32_t w_f16, int64_t k_pad,
-                  int64_t n_pad, int64_t M, int64_t N, int64_t K, const EpiDev& e, hipStream_t stream);
+                  int64_t n_pad, int64_t M, int64_t N, int64_t K, const EpiDev& e, hipStream_t stream,
+                  const mr_conv_geom* cg = nullptr);
 
 // Epilogue forms a kernel is compiled for: EF_GENERIC runs the step
 // interpreter, EF_FIXED the fixed form (see EpiDev) with its flags read at run

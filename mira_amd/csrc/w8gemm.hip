@@ -20,6 +20,13 @@
 // take K elements 32h .. 32h + 31, one per MFMA step, so each lane reads its
 // x values as 16-byte runs and its weights as 16-byte runs.
 //
+// CONV: the same product as an implicit-GEMM convolution (the weight-only mode's f32
+// conv2d over a dequantize weight, mira/ops.py:265-276): x is an NHWC f32 image with C
+// channels per pixel (C % 4 == 0), row m of the product is output pixel (n, oh, ow), and
+// K element k is (tap (kh, kw), channel c) with k = (kh * KW + kw) * c_pad + c, the
+// packed weights' order.  Each lane's 16-byte run keeps its (kh, kw, c) and steps it 64
+// elements per stage; taps outside the image and channels >= C read zeros.
+//
 // LDS layout.  x rows are 256 bytes (16 chunks of 16 bytes; chunk c of row r
 // sits at position c ^ (r & 15)), weight rows 64 bytes (chunk c of row n at
 // c ^ ((n >> 2) & 3)): 16 consecutive rows of one chunk land on 16 distinct
@@ -46,8 +53,11 @@ struct W8GemmArgs {
   int32_t ldx, k_pad, n_pad, M, N, K, w16;
   int32_t tiles_m;
   uint32_t x_bytes, b_bytes;
+  // CONV geometry (x NHWC with C channels per pixel; k = (kh * KW + kw) * c_pad + c)
+  int32_t H, W, C, c_pad, OH, OW, KH, KW, SH, SW, PH, PW, DH, DW;
 };
 
+template <bool CONV>
 __global__ void __launch_bounds__(256) w8gemm_f32_kernel(const W8GemmArgs g, const EpiDev e) {
   __shared__ __attribute__((aligned(1024))) int8_t lds[2 * W8_STAGE];
   const int lane = threadIdx.x & 63;
@@ -68,6 +78,9 @@ __global__ void __launch_bounds__(256) w8gemm_f32_kernel(const W8GemmArgs g, con
   // chunk position l % 16 of row 4o + l / 16, i.e. global chunk (l % 16) ^ (row & 15)
   uint32_t x_row[8];
   int32_t x_k[8];
+  // CONV: the row's top-left input pixel and the run's tap and channel at the next stage
+  int32_t cv_img[CONV ? 8 : 1], cv_ih[CONV ? 8 : 1], cv_iw[CONV ? 8 : 1];
+  int32_t cv_kh[CONV ? 8 : 1], cv_kw[CONV ? 8 : 1], cv_c[CONV ? 8 : 1];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int o = wave * 8 + j;
@@ -75,6 +88,20 @@ __global__ void __launch_bounds__(256) w8gemm_f32_kernel(const W8GemmArgs g, con
     const int c = (lane & 15) ^ (r & 15);
     x_k[j] = c * 4;
     x_row[j] = m0 + r < g.M ? static_cast<uint32_t>((m0 + r) * g.ldx * 4) : W8_OOB;
+    if constexpr (CONV) {
+      const int m = min(m0 + r, g.M - 1);
+      const int img = m / (g.OH * g.OW);
+      const int rem = m - img * g.OH * g.OW;
+      const int oh = rem / g.OW;
+      cv_img[j] = m0 + r < g.M ? img : -1;
+      cv_ih[j] = oh * g.SH - g.PH;
+      cv_iw[j] = (rem - oh * g.OW) * g.SW - g.PW;
+      // k = c * 4 at stage 0: tap and channel of that K element
+      const int tap = (c * 4) / g.c_pad;
+      cv_c[j] = c * 4 - tap * g.c_pad;
+      cv_kh[j] = tap / g.KW;
+      cv_kw[j] = tap - cv_kh[j] * g.KW;
+    }
   }
   // weight loader: 8 DMAs of 1 KB (16 rows) per stage, 2 per wave
   uint32_t b_vo[2];
@@ -90,9 +117,26 @@ __global__ void __launch_bounds__(256) w8gemm_f32_kernel(const W8GemmArgs g, con
     const int k0 = kt * W8K;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int k = k0 + x_k[j];
-      // K % 4 == 0 (checked on the host): a 16-byte chunk is all below K or all past it
-      const uint32_t off = (k < g.K && x_row[j] != W8_OOB) ? x_row[j] + static_cast<uint32_t>(k * 4) : W8_OOB;
+      uint32_t off;
+      if constexpr (CONV) {
+        const int ih = cv_ih[j] + cv_kh[j] * g.DH, iw = cv_iw[j] + cv_kw[j] * g.DW;
+        const bool ok = cv_img[j] >= 0 && cv_kh[j] < g.KH && cv_c[j] < g.C && unsigned(ih) < unsigned(g.H) &&
+                        unsigned(iw) < unsigned(g.W);
+        off = ok ? static_cast<uint32_t>((((cv_img[j] * g.H + ih) * g.W + iw) * g.C + cv_c[j]) * 4) : W8_OOB;
+        // on to the next stage's element of this run: 64 channels later, across taps
+        cv_c[j] += W8K;
+        while (cv_c[j] >= g.c_pad) {
+          cv_c[j] -= g.c_pad;
+          if (++cv_kw[j] == g.KW) {
+            cv_kw[j] = 0;
+            ++cv_kh[j];
+          }
+        }
+      } else {
+        const int k = k0 + x_k[j];
+        // K % 4 == 0 (checked on the host): a 16-byte chunk is all below K or all past it
+        off = (k < g.K && x_row[j] != W8_OOB) ? x_row[j] + static_cast<uint32_t>(k * 4) : W8_OOB;
+      }
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (w8_lds_void*)(As + (wave * 8 + j) * 1024), 16, off, 0, 0, 0);
     }
     const uint32_t soff = static_cast<uint32_t>(kt * g.n_pad * 64);
@@ -185,8 +229,10 @@ __global__ void __launch_bounds__(256) w8gemm_f32_kernel(const W8GemmArgs g, con
 }
 
 int w8gemm_launch(const float* x, int64_t ldx, const int8_t* b, const float* w_scale, int32_t w_f16, int64_t k_pad,
-                  int64_t n_pad, int64_t M, int64_t N, int64_t K, const EpiDev& e, hipStream_t stream) {
-  if (K % 4 != 0 || ldx % 4 != 0 || M * ldx * 4 >= (int64_t(1) << 31) || k_pad * n_pad >= (int64_t(1) << 31))
+                  int64_t n_pad, int64_t M, int64_t N, int64_t K, const EpiDev& e, hipStream_t stream,
+                  const mr_conv_geom* cg) {
+  const int64_t x_elems = cg ? int64_t(cg->n) * cg->h * cg->w * cg->c : M * ldx;
+  if (K % 4 != 0 || ldx % 4 != 0 || x_elems * 4 >= (int64_t(1) << 31) || k_pad * n_pad >= (int64_t(1) << 31))
     return MR_EUNSUPPORTED;
   W8GemmArgs g = {};
   g.x = x;
@@ -200,13 +246,52 @@ int w8gemm_launch(const float* x, int64_t ldx, const int8_t* b, const float* w_s
   g.K = static_cast<int32_t>(K);
   g.w16 = w_f16;
   g.tiles_m = static_cast<int32_t>((M + W8T - 1) / W8T);
-  g.x_bytes = static_cast<uint32_t>(M * ldx * 4);
+  g.x_bytes = static_cast<uint32_t>(x_elems * 4);
+  if (cg) {
+    g.H = cg->h; g.W = cg->w; g.C = cg->c; g.c_pad = cg->c_pad; g.OH = cg->oh; g.OW = cg->ow;
+    g.KH = cg->kh; g.KW = cg->kw; g.SH = cg->sh; g.SW = cg->sw; g.PH = cg->ph; g.PW = cg->pw; g.DH = cg->dh; g.DW = cg->dw;
+  }
   g.b_bytes = static_cast<uint32_t>(k_pad * n_pad);
   const int64_t tiles = int64_t(g.tiles_m) * ((N + W8T - 1) / W8T);
   MR_REQUIRE(tiles < (int64_t(1) << 31), "w8gemm: too many tiles");
-  hipLaunchKernelGGL(w8gemm_f32_kernel, dim3(static_cast<unsigned>(tiles)), dim3(256), 0, stream, g, e);
+  if (cg)
+    hipLaunchKernelGGL(w8gemm_f32_kernel<true>, dim3(static_cast<unsigned>(tiles)), dim3(256), 0, stream, g, e);
+  else
+    hipLaunchKernelGGL(w8gemm_f32_kernel<false>, dim3(static_cast<unsigned>(tiles)), dim3(256), 0, stream, g, e);
   MR_LAUNCH_CHECK("w8gemm");
   return MR_OK;
 }
 
 }  // namespace mr
+
+extern "C" int mr_w8_conv2d_f32(const float* x, const mr_conv_geom* cg, const int8_t* b, const float* w_scale,
+                                int32_t w_f16, int64_t k_pad, int64_t n_pad, const mr_epilogue* epi, void* stream) {
+  MR_REQUIRE(x && cg && b && w_scale, "mr_w8_conv2d_f32: NULL argument");
+  const mr_conv_geom& G = *cg;
+  MR_REQUIRE(G.n >= 0 && G.h > 0 && G.w > 0 && G.c > 0 && G.o > 0 && G.c % 4 == 0,
+             "mr_w8_conv2d_f32: bad shape (the input's channel count must be a multiple of 4)");
+  MR_REQUIRE(G.kh > 0 && G.kw > 0 && G.sh > 0 && G.sw > 0 && G.dh > 0 && G.dw > 0 && G.ph >= 0 && G.pw >= 0,
+             "mr_w8_conv2d_f32: bad kernel/stride/padding/dilation");
+  const int32_t oh = (G.h + 2 * G.ph - G.dh * (G.kh - 1) - 1) / G.sh + 1;
+  const int32_t ow = (G.w + 2 * G.pw - G.dw * (G.kw - 1) - 1) / G.sw + 1;
+  MR_REQUIRE(oh == G.oh && ow == G.ow && oh > 0 && ow > 0, "mr_w8_conv2d_f32: output %dx%d does not match (%dx%d)",
+             G.oh, G.ow, oh, ow);
+  MR_REQUIRE(G.c_pad >= G.c && G.c_pad % 4 == 0, "mr_w8_conv2d_f32: c_pad %d must be >= c and a multiple of 4",
+             G.c_pad);
+  MR_REQUIRE(k_pad >= int64_t(G.kh) * G.kw * G.c_pad && k_pad % 64 == 0,
+             "mr_w8_conv2d_f32: k_pad %lld must cover kh*kw*c_pad and be a multiple of 64", (long long)k_pad);
+  MR_REQUIRE(n_pad >= G.o && n_pad % 32 == 0, "mr_w8_conv2d_f32: n_pad %lld must be >= o and a multiple of 32",
+             (long long)n_pad);
+  MR_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0,
+             "mr_w8_conv2d_f32: operands must be 16-byte aligned");
+  mr::EpiDev e;
+  const int rc = mr::make_epi(epi, G.o, false, &e);
+  if (rc != MR_OK) return rc;
+  const int64_t M = int64_t(G.n) * oh * ow;
+  if (M == 0) return MR_OK;
+  MR_REQUIRE(M < (int64_t(1) << 31), "mr_w8_conv2d_f32: too many pixels");
+  const int r = mr::w8gemm_launch(x, 0, b, w_scale, w_f16, k_pad, n_pad, M, G.o, k_pad, e,
+                                  static_cast<hipStream_t>(stream), cg);
+  if (r == MR_EUNSUPPORTED) mr::set_error("mr_w8_conv2d_f32: the input or the weights reach 2 GiB");
+  return r;
+}

@@ -166,6 +166,10 @@ class RocmTarget:
         if k == "conv2d":
             x, w = op.inputs[0], op.inputs[1]
             (_, _, _, g) = conv_params(op.attrs)
+            if w.producer is not None and w.producer.kind == "dequantize" and g == 1:
+                return self._check_w8_conv2d(op)
+            # depthwise (a dequantize weight of the weight-only mode is materialized in f32 at
+            # compile time, exactly as mira/ops.py:581-586 does, so these stay bit-exact)
             if not (g == x.type.shape[1] == w.type.shape[0] and w.type.shape[1] == 1):
                 return "only depthwise f32 convolution runs on rocm (dense f32 conv is not on the W8A8 path)"
             if w.producer is None or not w.producer.is_constant_like:
@@ -240,6 +244,26 @@ class RocmTarget:
         if rows * K * 4 >= 2 ** 31:
             return "weight-only int8 matmul: an activation of 2 GiB or more"
         return self._check_epilogue(op, op.result.type.shape, False)
+
+    def _check_w8_conv2d(self, op: "Op") -> Optional[str]:
+        """Convolutions of the weight-only int8 mode: an f32 conv2d (groups 1) over a
+        `dequantize` [O, C, KH, KW] weight, as an implicit GEMM on f32 MFMAs.  The kernel
+        reads the NHWC image 4 channels at a time, so C must be a multiple of 4 (a 3-channel
+        stem stays on the CPU).  Like the weight-only matmul it matches the reference to f32
+        rounding, not bit for bit."""
+        x, w = op.inputs[0], op.inputs[1]
+        p = w.producer
+        (_, _, _, g) = conv_params(op.attrs)
+        if p.attrs["axis"] != 0 or w.type.rank != 4 or g != 1:
+            return "weight-only int8 convolution runs on rocm for dense (groups 1) convolutions"
+        if x.type.rank != 4 or x.type.dtype not in FLOAT_DTYPES:
+            return "weight-only int8 convolution needs an NCHW float input"
+        n, c, h, wd = x.type.shape
+        if c % 4 != 0:
+            return f"weight-only int8 convolution runs on rocm for channel counts divisible by 4, not {c}"
+        if n * h * wd * c * 4 >= 2 ** 31:
+            return "weight-only int8 convolution: an input of 2 GiB or more"
+        return self._check_epilogue(op, op.result.type.shape, True, first_operand=2)
 
     def _check_epilogue(self, op: "Op", shape: tuple, is_conv: bool, first_operand: int = 1) -> Optional[str]:
         for fn, idx, _sw in op.attrs.get("epilogue", ()):
@@ -807,8 +831,44 @@ class RocmExecutable:
             nbytes=n * h * w * c + o * c * kh * kw + self._epi_bytes(e, rows, o), nops=2 * rows * o * c * kh * kw)
         self._finish_i8(out, fused)
 
+    def _emit_w8_conv2d(self, op: "Op") -> None:
+        """Weight-only int8 convolution (checked by _check_w8_conv2d): the int8 weights are
+        packed with a 16-channel-multiple tap stride and uploaded once with their f32 scales;
+        each run is one mr_w8_conv2d_f32 implicit GEMM over the NHWC f32 image."""
+        a = op.attrs
+        xv = op.inputs[0]
+        x = self._src(xv)
+        n, c, h, w = xv.type.shape
+        wa = self.consts[op.inputs[1]].attrs
+        q = np.asarray(wa["q"], np.int8)
+        o, _, kh, kw = q.shape
+        (sh, sw), (ph, pw), (dh, dw), _ = conv_params(a)
+        _, _, oh, ow = op.result.type.shape
+        cp = pack.roundup(c, 16)                   # the packed taps' channel stride
+        bl = pack.pack_conv(q, cp)
+        b = self._upload(pack.device_weights(bl))
+        ws = self._upload(np.asarray(wa["scale"], np.float32).reshape(-1))
+        w16 = int(wa["dtype"] == "f16")
+        geom = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=cp, o=o, oh=oh, ow=ow, kh=kh, kw=kw, sh=sh, sw=sw, ph=ph, pw=pw,
+                          dh=dh, dw=dw)
+        self.keep.append(geom)
+        out = self._new_dv(op.result)
+        e, fused = self._epilogue(op, out, True, 2, None)
+        lib, xt, kp, npad = self.lib, x.f32, bl.shape[1], bl.shape[0]
+        rows = n * oh * ow
+        self._add("w8conv2d", lambda s: L.check(
+            lib.mr_w8_conv2d_f32(xt.data_ptr(), C.byref(geom), b.data_ptr(), ws.data_ptr(), w16, kp, npad, C.byref(e),
+                                 s), "mr_w8_conv2d_f32"),
+            nbytes=4 * n * c * h * w + o * c * kh * kw + 4 * o + self._epi_bytes(e, rows, o),
+            nops=2 * rows * o * c * kh * kw)
+        self._finish_i8(out, fused)
+
     def _emit_conv2d(self, op: "Op") -> None:
-        """Depthwise f32 convolution (groups == C, one filter per channel)."""
+        """Depthwise f32 convolution (groups == C, one filter per channel); a weight-only
+        int8 convolution goes to _emit_w8_conv2d."""
+        wp = op.inputs[1].producer
+        if wp is not None and wp.kind == "dequantize" and conv_params(op.attrs)[3] == 1:
+            return self._emit_w8_conv2d(op)
         a = op.attrs
         xv = op.inputs[0]
         x = self._src(xv)

@@ -292,6 +292,54 @@ def test_w8_matmul_tiled_f16_weights(lib):
     assert np.all(np.abs(y.astype(np.float64) - want) <= W8_TOL * bound)
 
 
+@pytest.mark.parametrize("n,c,h,o,k,s,p,d,w16", [(2, 64, 14, 128, 3, 1, 1, 1, False), (2, 64, 15, 130, 3, 2, 1, 1, False),
+                                                (3, 20, 9, 24, 1, 1, 0, 1, False), (2, 4, 17, 32, 3, 2, 1, 1, False),
+                                                (2, 16, 11, 40, 3, 1, 2, 2, False), (1, 96, 7, 200, 1, 2, 0, 1, True)])
+def test_w8_conv2d(lib, n, c, h, o, k, s, p, d, w16):
+    """Weight-only int8 convolution (f32 conv2d over a dequantize weight, mira/ops.py:265-276,
+    581-589) as an implicit GEMM on f32 MFMAs: within the f32-rounding bound of the matmul
+    tests, every tap/stride/padding/dilation case and ragged pixel / channel counts."""
+    torch = _torch()
+    rng = np.random.default_rng(n * 100 + c + o + k)
+    x = rng.standard_normal((n, c, h, h)).astype(np.float32)
+    q = rng.integers(-127, 128, (o, c, k, k)).astype(np.int8)
+    sc = rng.uniform(0.001, 0.01, o).astype(np.float32)
+    deq = G.dequantize({"q": q, "scale": sc, "axis": 0, "dtype": "f16" if w16 else "f32"}).astype(np.float32)
+    bias = (rng.standard_normal((o, 1, 1)) * 0.1).astype(np.float32)
+    attrs = {"stride": (s, s), "padding": (p, p), "dilation": (d, d),
+             "epilogue": (("add", 2, False), ("relu", None, False))}
+    want = G.conv2d([x, deq, bias], attrs)
+    oh = want.shape[2]
+    M = n * oh * oh
+    cp = pack.roundup(c, 16)
+    bl = pack.pack_conv(q, cp)
+    xd, b, ws, bt = T(x.transpose(0, 2, 3, 1)), T(pack.device_weights(bl)), T(sc), T(bias.reshape(o))
+    y = empty((M, o), torch.float32)
+    e = epilogue([("add", L.BC_COL, bt, 0, False), ("relu", 0, None, 0, False)], out_f32=y, ldo=o)
+    g = L.ConvGeom(n=n, h=h, w=h, c=c, c_pad=cp, o=o, oh=oh, ow=oh, kh=k, kw=k, sh=s, sw=s, ph=p, pw=p, dh=d, dw=d)
+    L.check(lib.mr_w8_conv2d_f32(xd.data_ptr(), C.byref(g), b.data_ptr(), ws.data_ptr(), int(w16), bl.shape[1],
+                                 bl.shape[0], C.byref(e), stream()), "mr_w8_conv2d_f32")
+    sync()
+    got = y.cpu().numpy()
+    to_nhwc = lambda a: a.transpose(0, 2, 3, 1).reshape(M, o)
+    bound = to_nhwc(G.conv2d([np.abs(x).astype(np.float64), np.abs(deq).astype(np.float64)],
+                             {"stride": (s, s), "padding": (p, p), "dilation": (d, d)})) + np.abs(bias.reshape(o))
+    assert np.all(np.abs(got.astype(np.float64) - to_nhwc(want)) <= W8_TOL * bound)
+    assert (got >= 0).all()
+
+
+def test_w8_conv2d_rejects_bad_arguments(lib):
+    torch = _torch()
+    x = empty((1, 5, 5, 3), torch.float32)
+    b = empty((64, 64), torch.int8)
+    s = empty((8,), torch.float32)
+    e = epilogue(out_f32=empty((25, 8), torch.float32), ldo=8)
+    g = L.ConvGeom(n=1, h=5, w=5, c=3, c_pad=16, o=8, oh=5, ow=5, kh=1, kw=1, sh=1, sw=1, ph=0, pw=0, dh=1, dw=1)
+    assert lib.mr_w8_conv2d_f32(x.data_ptr(), C.byref(g), b.data_ptr(), s.data_ptr(), 0, 64, 64, C.byref(e),
+                                stream()) == 1
+    assert b"multiple of 4" in lib.mr_last_error()
+
+
 def test_w8_matmul_f16_weights(lib):
     """A dequantize of dtype f16 (mira/ops.py:584): the weights are fl16(fl32(q * scale)); with
     f16 activations and an f16 result rounded after the epilogue."""

@@ -348,6 +348,20 @@ def test_weight_only_mlp50m_batch4096():
     assert np.abs(got - want).max() <= W8_MODEL_TOL * np.abs(want).max()
 
 
+@pytest.mark.parametrize("builder,convs", [(models.resnet18, 19), (models.mobilenet_v2, 33)])
+def test_weight_only_cnn_batch2(builder, convs):
+    """Weight-only ResNet-18 and MobileNetV2: every dense convolution over a dequantize weight
+    whose input has a channel count divisible by 4 on rocm (the 3-channel stems, and the two
+    MobileNetV2 convolutions whose weights are under 1024 elements and stay f32, run on the
+    CPU; depthwise weights are materialized in f32 and stay bit-exact), within f32 rounding
+    of the oracle compounded over the network."""
+    g = _weight_only(builder(batch=2, seed=0))
+    runner, (got,), (want,) = _run_weight_only(g, {"x": models.image_batch((2, 3, 224, 224), 7)})
+    n = sum(exe.kernel_counts.get("w8conv2d", 0) for exe in runner.executables("rocm"))
+    assert n == convs, n
+    assert np.abs(got - want).max() <= W8_MODEL_TOL * np.abs(want).max()
+
+
 def test_weight_only_mlp_mira_batch64():
     """The reference's own int8 check (its tests/test_control_dynamic_quant.py:178-189) with
     the three matmuls on rocm: within 0.05 of the f32 model, argmax agreement above 0.9."""
