@@ -606,6 +606,8 @@ def test_qmatmul_epilogue_forms(lib, form, M, K, N):
     (1, 8, 30, 1, 3, "relu6", 0),       # 4 columns per thread, last tile 2 of 4
     (2, 144, 15, 2, 3, "relu6", 0),     # stride 2, last column tile partial
     (1, 960, 7, 1, 3, "relu6", 0),      # 7 columns: one full and one partial tile
+    (3, 24, 11, 1, 3, "relu6", 0),      # 11 output rows: the last row pair of a thread half past the map
+    (1, 16, 17, 2, 3, "relu6", 0),      # stride 2, 9 output rows: the same at stride 2
     (2, 8, 13, 2, 3, "generic", 0),     # step interpreter epilogue (swapped subtract)
     (2, 16, 9, 1, 3, "relu6", 1),       # f32 rows not 16-byte aligned: element stores
     (1, 6, 9, 1, 3, "relu6", 0),        # 6 channels: per-element kernel
