@@ -100,7 +100,10 @@ def _run_qmatmul(lib, x, q, ws, xs, steps_np, next_xs=None):
 
 @pytest.mark.parametrize("M,K,N", [(256, 64, 10), (64, 784, 512), (300, 512, 1000), (1, 4096, 4096),
                                    (4096, 4096, 1000), (33, 128, 65), (70000, 64, 128),
-                                   (49920, 160, 272),     # 256x256 tiles, ragged K and N
+                                   (49920, 160, 272),     # short K: 128x64 tiles, ragged K and N
+                                   (6272, 960, 320),      # short K, under one 128x64 tile per CU: 64x32
+                                   (25088, 384, 96),      # short K, under one 128x128 tile per CU: 64x32
+                                   (25088, 64, 384),      # short K, N > 128: 128x64
                                    (3, 4096, 1000), (8, 512, 65), (2, 64, 64), (5, 192, 130)])   # weight stream
 def test_qmatmul_bias_relu_requant(lib, M, K, N):
     rng = np.random.default_rng(M * 7 + N)
@@ -413,7 +416,7 @@ CONV_CASES = [
     (1, 256, 7, 7, 512, 3, 1, 1, 1),
     (3, 24, 9, 9, 144, 1, 1, 0, 1),       # 1x1 as a dense GEMM, c_pad 32
     (2, 144, 28, 28, 24, 1, 1, 0, 1),     # 1x1 as a dense GEMM, c_pad 144: K tail past the row
-    (2, 64, 14, 14, 384, 1, 1, 0, 1),     # 1x1 as a dense GEMM, 128x256 tiles
+    (2, 64, 14, 14, 384, 1, 1, 0, 1),     # 1x1 as a dense GEMM (a small grid: 64x32 tiles)
     (2, 16, 11, 11, 24, 3, 1, 2, 2),      # dilation 2
     (2, 1, 28, 28, 16, 3, 1, 1, 1),       # single channel (cnn.mira)
     # stride-1 convolutions read through the per-tile input patch
