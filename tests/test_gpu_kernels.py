@@ -104,7 +104,8 @@ def _run_qmatmul(lib, x, q, ws, xs, steps_np, next_xs=None):
                                    (6272, 960, 320),      # short K, under one 128x64 tile per CU: 64x32
                                    (25088, 384, 96),      # short K, under one 128x128 tile per CU: 64x32
                                    (25088, 64, 384),      # short K, N > 128: 128x64
-                                   (3, 4096, 1000), (8, 512, 65), (2, 64, 64), (5, 192, 130)])   # weight stream
+                                   (3, 4096, 1000), (8, 512, 65), (2, 64, 64), (5, 192, 130),   # weight stream
+                                   (2, 5000, 96), (1, 8192, 40)])   # k_pad > 4096: lane groups per column pair
 def test_qmatmul_bias_relu_requant(lib, M, K, N):
     rng = np.random.default_rng(M * 7 + N)
     x = rng.standard_normal((M, K)).astype(np.float32)
