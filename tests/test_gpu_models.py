@@ -201,6 +201,37 @@ def test_onnx_layout_batch2(builder):
     assert runner.devices == ["rocm"]
 
 
+def _imported(data: bytes, shape, seeds=(11, 12)):
+    """An ONNX model read by harness/onnx_import.py, lowered and W8A8-rewritten with
+    calibration on seeded uniform batches of its input shape."""
+    from harness import onnx_import as OI
+    g = LW.prepare(OI.import_model(data))
+    LW.w8a8(g, peaks=LW.calibrate(g, [{"x": models.image_batch(shape, s)} for s in seeds]))
+    return g
+
+
+def test_onnx_import_resnet18_batch2():
+    """A torchvision-layout ResNet-18 (torch modules, random weights) written as ONNX and read by
+    this repository's importer: every op on rocm; accumulators and outputs bit-exact."""
+    import torch_onnx_nets as N
+    _, data = N.resnet18(2, seed=3)
+    g = _imported(data, (2, 3, 224, 224))
+    runner = _compare(g, {"x": models.image_batch((2, 3, 224, 224), 6)}, fallback=False)
+    assert runner.devices == ["rocm"]
+
+
+@pytest.mark.parametrize("opset", [10, 13])
+def test_onnx_import_edge_net(opset):
+    """The importer's less common forms on rocm: an asymmetric pad before a 4-channel conv, a
+    dilated depthwise conv, ReLU6 as Clip, a ceil-mode max pool, the Shape-Gather-Concat flatten,
+    Gemm alpha/beta as epilogue steps."""
+    import torch_onnx_nets as N
+    _, data = N.edge_net(4, opset)
+    g = _imported(data, (4, 3, 9, 9))
+    runner = _compare(g, {"x": models.image_batch((4, 3, 9, 9), 6)}, fallback=False)
+    assert runner.devices == ["rocm"]
+
+
 @pytest.mark.parametrize("builder,shape,dist", [(models.resnet18, (2, 3, 224, 224), "uniform"),
                                                 (models.mobilenet_v2, (2, 3, 224, 224), "uniform"),
                                                 (models.mlp_50m, (8, 4096), "normal")])
