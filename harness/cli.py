@@ -1,0 +1,374 @@
+"""Command-line driver for .mira programs and .onnx models: the counterpart of mira/cli.py's
+run / emit / bench / check for the rocm target and its cpu reference.
+
+    python -m harness.cli run   prog.mira -t rocm --quantize w8a8 --check
+    python -m harness.cli emit  prog.mira --stage opt
+    python -m harness.cli bench prog.mira --targets rocm,cpu
+    python -m harness.cli check prog.mira
+
+The compile steps follow mira/compiler.py:252-312: elaborate (or import the ONNX model),
+precision "auto" -> f16 for every target but cpu, the optimizer's lowering, then W8A8
+(calibrated on four batches of default_rng(0) normal inputs unless a calibration is given)
+or int8 weight-only, then the split between the target and the cpu fallback.  Random
+inputs are default_rng(seed + 1) normal (mira/cli.py:76-80); `run --check` compares every
+output with the unquantized cpu run of the same program:
+max|out - ref| / max|ref| < tol, tol 2e-2 by default (mira/cli.py:101-111).
+
+The cpu target is the harness's NumPy evaluator (harness.hosteval.HostTarget).
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import sys
+import time
+from typing import Optional
+
+import numpy as np
+
+from harness import hosteval
+from harness import lowering as LW
+from harness import mira_lang
+from harness import onnx_import
+from harness.graph import Graph
+from harness.runner import Runner
+
+TARGETS = ["rocm", "cpu"]
+STAGES = ["tokens", "ast", "ir", "opt", "partition"]
+
+
+class CompileError(Exception):
+    """A user-facing error: bad program text, shapes, flags."""
+
+
+def _target(name: str):
+    if name == "cpu":
+        return hosteval.HostTarget()
+    if name == "rocm":
+        from mira_amd.target import RocmTarget
+        return RocmTarget()
+    raise CompileError(f"unknown target '{name}' (choose from {', '.join(TARGETS)})")
+
+
+class Program:
+    """A compiled program: the graph as lowered, its segments, timings of the last run."""
+
+    def __init__(self, target: str, graph: Graph, ir_text: str, runner: Runner, seconds: float):
+        self.target = target
+        self.graph = graph
+        self.ir_text = ir_text
+        self.runner = runner
+        self.compile_seconds = seconds
+
+    @property
+    def segments(self):
+        return self.runner.segments
+
+    @property
+    def last_timings(self) -> list:
+        return self.runner.timings
+
+    def run(self, feeds: dict) -> list:
+        return self.runner.run(feeds)
+
+    def summary(self) -> str:
+        lines = [f"target {self.target}: {len(self.segments)} segment(s), compiled in {self.compile_seconds:.2f}s"]
+        for i, seg in enumerate(self.segments):
+            ins = ", ".join(f"{v!r}:{v.type}" for v in seg.graph.inputs)
+            lines.append(f"  [{i}] {seg.device:<8} {len(seg.graph.compute_ops()):3d} ops   inputs: {ins}")
+            lines.append("      " + seg.executable.report().replace("\n", "\n      "))
+        return "\n".join(lines)
+
+    def placement_report(self) -> str:
+        lines = []
+        for op in self.graph.compute_ops():
+            why = self.runner.reasons.get(op)
+            dev = "cpu" if why is not None else self.target
+            lines.append(f"{op.kind:<12} {str(op.result.type):<24} {dev}" + (f"   ({why})" if why else ""))
+        return "\n".join(lines)
+
+
+def load_graph(path: str, entry: str = "main", weights: Optional[dict] = None, dims: Optional[dict] = None,
+               seed: Optional[int] = 0, input_shapes: Optional[dict] = None) -> Graph:
+    """The float graph of a .mira program or a .onnx model."""
+    if path.endswith(".onnx"):
+        try:
+            return onnx_import.load(path, input_shapes)
+        except onnx_import.OnnxImportError as err:
+            raise CompileError(str(err)) from None
+    with open(path) as f:
+        src = f.read()
+    try:
+        return mira_lang.elaborate(src, entry, weights, dims, seed, name=os.path.splitext(os.path.basename(path))[0])
+    except mira_lang.MiraSyntaxError as err:
+        raise CompileError(f"{path}: {err}") from None
+
+
+def compile_graph(g: Graph, target: str, precision: Optional[str] = "auto", quantize: Optional[str] = None,
+                  calibration: Optional[list] = None, started: Optional[float] = None) -> Program:
+    """Lower a float graph for `target` (mira/compiler.py:287-312) and compile its segments."""
+    t0 = started if started is not None else time.perf_counter()
+    if precision == "auto":
+        precision = None if target == "cpu" else "f16"
+    ir_text = str(g)
+    LW.prepare(g, precision=precision)
+    if quantize == "w8a8":
+        if calibration is None:
+            rng = np.random.default_rng(0)
+            calibration = [{v.name: rng.standard_normal(v.type.shape).astype(v.type.np_dtype) for v in g.inputs}
+                           for _ in range(4)]
+        LW.w8a8(g, calibration)
+    elif quantize == "int8":
+        LW.weight_only(g)
+    elif quantize is not None:
+        raise CompileError(f"unknown quantization '{quantize}' (int8, w8a8)")
+    tgt = _target(target)
+    runner = Runner(g, tgt, fallback=None if target == "cpu" else hosteval.HostTarget())
+    return Program(target, g, ir_text, runner, time.perf_counter() - t0)
+
+
+def compile_file(path: str, target: str = "cpu", *, entry: str = "main", weights: Optional[dict] = None,
+                 dims: Optional[dict] = None, seed: Optional[int] = 0, precision: Optional[str] = "auto",
+                 quantize: Optional[str] = None, calibration: Optional[list] = None,
+                 input_shapes: Optional[dict] = None) -> Program:
+    t0 = time.perf_counter()
+    g = load_graph(path, entry, weights, dims, seed, input_shapes)
+    return compile_graph(g, target, precision, quantize, calibration, started=t0)
+
+
+# ---------------------------------------------------------------- argument helpers
+
+def _dims(items) -> dict:
+    out = {}
+    for it in items or []:
+        k, _, v = it.partition("=")
+        if not v:
+            raise CompileError(f"--dim expects NAME=VALUE, got {it!r}")
+        out[k] = int(v)
+    return out
+
+
+def _shapes(items) -> dict:
+    out = {}
+    for it in items or []:
+        name, _, dims = it.rpartition("=")
+        if not name:
+            raise CompileError(f"--shape expects NAME=D0,D1,..., got {it!r}")
+        out[name] = tuple(int(d) for d in dims.split(",") if d)
+    return out
+
+
+def _load_npz(path) -> dict:
+    if not path:
+        return {}
+    with np.load(path) as z:
+        return {k: z[k] for k in z.files}
+
+
+def _compile(args, target: str) -> Program:
+    return compile_file(args.file, target, entry=args.entry, weights=_load_npz(args.weights), dims=_dims(args.dim),
+                        seed=args.seed, precision=args.precision, quantize=args.quantize,
+                        input_shapes=_shapes(args.shape))
+
+
+def _reference(args) -> Program:
+    """The unquantized cpu run of the same program (what --check compares with)."""
+    return compile_file(args.file, "cpu", entry=args.entry, weights=_load_npz(args.weights), dims=_dims(args.dim),
+                        seed=args.seed, input_shapes=_shapes(args.shape))
+
+
+def _inputs(prog: Program, path, seed: int) -> dict:
+    given = _load_npz(path)
+    rng = np.random.default_rng(seed + 1)
+    return {v.name: given[v.name] if v.name in given else rng.standard_normal(v.type.shape).astype(v.type.np_dtype)
+            for v in prog.graph.inputs}
+
+
+def _rel_err(out, ref) -> tuple:
+    err = float(np.abs(np.asarray(out, np.float32) - np.asarray(ref, np.float32)).max()) if np.size(ref) else 0.0
+    return err, err / (float(np.abs(ref).max()) + 1e-12 if np.size(ref) else 1.0)
+
+
+# ---------------------------------------------------------------- commands
+
+def cmd_run(args) -> int:
+    prog = _compile(args, args.target)
+    feeds = _inputs(prog, args.inputs, args.seed)
+    outs = prog.run(feeds)
+    print(prog.summary())
+    print(f"wall time {sum(t for _, t in prog.last_timings) * 1e3:.2f} ms")
+    for i, out in enumerate(outs):
+        print(f"output {i}: {list(out.shape)} {out.dtype}")
+        with np.printoptions(precision=4, suppress=True, threshold=12, edgeitems=3):
+            print(out)
+    if args.save:
+        if len(outs) > 1:
+            np.savez(args.save, *outs)
+        else:
+            np.save(args.save, outs[0])
+        print(f"saved to {args.save}")
+    if args.check and args.target != "cpu":
+        ok, lines = check_outputs(outs, _reference(args).run(feeds), args.tol)
+        print("\n".join(lines))
+        return 0 if ok else 1
+    return 0
+
+
+def check_outputs(outs: list, refs: list, tol: float) -> tuple:
+    """(all within tol, report lines): max|out - ref| / max|ref| per output."""
+    ok, lines = True, []
+    for i, (out, ref) in enumerate(zip(outs, refs)):
+        err, rel = _rel_err(out, ref)
+        ok &= rel < tol
+        lines.append(f"check output {i} vs cpu reference: max abs err {err:.3e}, relative {rel:.3e}  ->  "
+                     f"{'PASS' if rel < tol else 'FAIL'}")
+    return ok, lines
+
+
+def _format_dim(d) -> str:
+    return f"({_format_dim(d[1])} {d[0]} {_format_dim(d[2])})" if isinstance(d, tuple) else str(d)
+
+
+def _format_type(t) -> str:
+    return f"{t.dtype}[{', '.join(_format_dim(d) for d in t.dims)}]" if t.dims else t.dtype
+
+
+def _format_expr(e) -> str:
+    kind = e[0]
+    if kind == "num":
+        return repr(e[1])
+    if kind == "bool":
+        return "true" if e[1] else "false"
+    if kind == "name":
+        return e[1]
+    if kind == "list":
+        return "[" + ", ".join(_format_expr(x) for x in e[1]) + "]"
+    if kind == "neg":
+        return f"-{_format_expr(e[1])}"
+    if kind == "bin":
+        return f"({_format_expr(e[2])} {e[1]} {_format_expr(e[3])})"
+    _, name, args, kwargs, _ = e
+    return f"{name}(" + ", ".join([_format_expr(a) for a in args] +
+                                  [f"{k}={_format_expr(v)}" for k, v in kwargs.items()]) + ")"
+
+
+def format_module(fns: dict) -> str:
+    """The parse tree of a program as fully parenthesized source."""
+    out = []
+    for fn in fns.values():
+        params = ", ".join(("const " if p.const else "") + f"{p.name}: {_format_type(p.type)}" for p in fn.params)
+        out.append(f"fn {fn.name}({params}) -> {_format_type(fn.ret)} {{")
+        for st in fn.body:
+            out.append(f"  let {st[1]} = {_format_expr(st[2])}" if st[0] == "let" else f"  return {_format_expr(st[1])}")
+        out.append("}")
+    return "\n".join(out)
+
+
+def cmd_emit(args) -> int:
+    if args.stage in ("tokens", "ast"):
+        if args.file.endswith(".onnx"):
+            raise CompileError(f"'{args.stage}' is a .mira source stage; ONNX models start at the 'ir' stage")
+        with open(args.file) as f:
+            src = f.read()
+        try:
+            if args.stage == "tokens":
+                for t in mira_lang.tokenize(src):
+                    print(f"{t.line:4d} {t.kind:<5} {t.text}")
+            else:
+                print(format_module(mira_lang.parse(src)))
+        except mira_lang.MiraSyntaxError as err:
+            raise CompileError(f"{args.file}: {err}") from None
+        return 0
+    prog = _compile(args, args.target)
+    if args.stage == "ir":
+        print(prog.ir_text)
+    elif args.stage == "opt":
+        print(prog.graph)
+    else:
+        print(prog.placement_report())
+        print()
+        print(prog.summary())
+    return 0
+
+
+def cmd_bench(args) -> int:
+    feeds, ref = None, None
+    print(f"{'target':<10} {'compile':>9} {'median':>10} {'min':>10}   {'rel err':>9}  segments")
+    for t in args.targets.split(","):
+        prog = _compile(args, t)
+        if feeds is None:
+            feeds = _inputs(prog, args.inputs, args.seed)
+        out = prog.run(feeds)[0]                  # warm-up, and the output checked
+        if ref is None:
+            ref = _reference(args).run(feeds)[0]
+        times = []
+        for _ in range(args.iters):
+            t0 = time.perf_counter()
+            prog.run(feeds)
+            times.append(time.perf_counter() - t0)
+        _, rel = _rel_err(out, ref)
+        segs = "+".join(s.device for s in prog.segments)
+        print(f"{t:<10} {prog.compile_seconds:8.2f}s {np.median(times) * 1e3:8.3f}ms {min(times) * 1e3:8.3f}ms"
+              f"   {rel:9.2e}  {segs}")
+    return 0
+
+
+def cmd_check(args) -> int:
+    g = _compile(args, "cpu").graph
+    ins = ", ".join(f"{v.name}: {v.type}" for v in g.inputs)
+    print(f"ok: {args.file}  inputs ({ins}) -> {g.outputs[0].type}, {len(g.compute_ops())} ops")
+    return 0
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(prog="harness.cli", description="run .mira programs and .onnx models on rocm")
+    sub = ap.add_subparsers(dest="cmd", required=True)
+
+    def common(p):
+        p.add_argument("file")
+        p.add_argument("--target", "-t", default="cpu", choices=TARGETS)
+        p.add_argument("--entry", default="main")
+        p.add_argument("--weights", help=".npz with values for const parameters (default: random)")
+        p.add_argument("--inputs", help=".npz with runtime inputs (default: random)")
+        p.add_argument("--dim", action="append", help="bind a shape symbol of the entry function, e.g. --dim B=32")
+        p.add_argument("--shape", action="append", metavar="NAME=D0,D1,...",
+                       help="ONNX models: the shape of an input with symbolic dims")
+        p.add_argument("--seed", type=int, default=0)
+        p.add_argument("--precision", default="auto", choices=["auto", "f16", "none"])
+        p.add_argument("--quantize", choices=["int8", "w8a8"],
+                       help="int8: store large weights as int8; w8a8: also do the multiplies in int8")
+
+    p = sub.add_parser("run", help="compile and run")
+    common(p)
+    p.add_argument("--check", action="store_true", help="compare against the cpu reference")
+    p.add_argument("--tol", type=float, default=2e-2)
+    p.add_argument("--save")
+    p.set_defaults(fn=cmd_run)
+
+    p = sub.add_parser("emit", help="print a compiler stage")
+    common(p)
+    p.add_argument("--stage", "-s", default="opt", choices=STAGES)
+    p.set_defaults(fn=cmd_emit)
+
+    p = sub.add_parser("bench", help="time targets")
+    common(p)
+    p.add_argument("--targets", default="rocm,cpu")
+    p.add_argument("--iters", type=int, default=20)
+    p.set_defaults(fn=cmd_bench)
+
+    p = sub.add_parser("check", help="parse and type-check only")
+    common(p)
+    p.set_defaults(fn=cmd_check)
+
+    args = ap.parse_args(argv)
+    if getattr(args, "precision", None) == "none":
+        args.precision = None
+    try:
+        return args.fn(args)
+    except CompileError as err:
+        print(f"error: {err}", file=sys.stderr)
+        return 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -4,9 +4,10 @@ Two uses, neither of which produces a result the rocm target returns:
 
 * calibration (`lowering.calibrate`): a float forward pass that records the
   peak |x| of every q-op input, from which x_scale follows;
-* `HostTarget`: the benchmark's stand-in for MIRA's cpu target, the fallback
-  that runs the ops the rocm target rejects (the f32 attention, softmax,
-  layernorm and gelu of the GPT decode step).  The parity tests use the
+* `HostTarget`: the stand-in for MIRA's cpu target in the benchmark and the
+  command-line driver: the fallback that runs the ops the rocm target rejects
+  (the f32 attention, softmax, layernorm and gelu of the GPT decode step), and
+  the `cpu` target that `run --check` compares with.  The parity tests use the
   oracle for that role instead.
 
 Convolutions run as one im2col GEMM (grouped ones tap by tap), so float
@@ -47,29 +48,30 @@ def apply_epilogue(y: np.ndarray, operands: list, steps) -> np.ndarray:
     return y
 
 
-def conv2d_f32(x: np.ndarray, w: np.ndarray, a: dict) -> np.ndarray:
-    """NCHW x OIHW -> NCHW f32 convolution: im2col + one GEMM, or per tap for grouped convs."""
+def conv2d_f32(x: np.ndarray, w: np.ndarray, a: dict, dt=np.float32) -> np.ndarray:
+    """NCHW x OIHW -> NCHW convolution in `dt` (f32; f64 makes integer operands exact):
+    im2col + one GEMM, or per tap for grouped convs."""
     (sh, sw), (ph, pw) = a["stride"], a["padding"]
     dh, dw = a.get("dilation", (1, 1))
     g = a.get("groups", 1)
     n, c, h, wd = x.shape
     o, cg, kh, kw = w.shape
     oh, ow = conv_out(h, kh, sh, ph, dh), conv_out(wd, kw, sw, pw, dw)
-    xp = np.pad(_f32(x), ((0, 0), (0, 0), (ph, ph), (pw, pw))).transpose(0, 2, 3, 1)
-    w = _f32(w)
+    xp = np.pad(np.asarray(x, dt), ((0, 0), (0, 0), (ph, ph), (pw, pw))).transpose(0, 2, 3, 1)
+    w = np.asarray(w, dt)
 
     def tap(i, j):
         return xp[:, i * dh:i * dh + sh * (oh - 1) + 1:sh, j * dw:j * dw + sw * (ow - 1) + 1:sw, :]
 
     if g == 1:
-        cols = np.empty((n, oh, ow, kh, kw, c), np.float32)
+        cols = np.empty((n, oh, ow, kh, kw, c), dt)
         for i in range(kh):
             for j in range(kw):
                 cols[:, :, :, i, j, :] = tap(i, j)
         out = cols.reshape(n * oh * ow, -1) @ w.transpose(2, 3, 1, 0).reshape(kh * kw * c, o)
         return np.ascontiguousarray(out.reshape(n, oh, ow, o).transpose(0, 3, 1, 2))
     og = o // g
-    acc = np.zeros((n, oh, ow, o), np.float32)
+    acc = np.zeros((n, oh, ow, o), dt)
     for i in range(kh):
         for j in range(kw):
             xt = tap(i, j)
@@ -106,6 +108,12 @@ def evaluate(kind: str, xs: list, a: dict) -> np.ndarray:
     if kind == "qmatmul":
         acc = quantize_activation(xs[0], a["x_scale"]) @ a["q"].astype(np.int64)
         y = (acc.astype(np.float64) * (np.float64(a["x_scale"]) * a["w_scale"].astype(np.float64))).astype(np.float32)
+        return apply_epilogue(y, xs, a.get("epilogue", ())).astype(DTYPES[a["dtype"]])
+    if kind == "qconv2d":
+        # integer products summed in f64: exact while |sum| < 2^53 (127 * 127 * K is far below)
+        acc = conv2d_f32(quantize_activation(xs[0], a["x_scale"]), a["q"], a, np.float64)
+        scale = np.float64(a["x_scale"]) * a["w_scale"].astype(np.float64).reshape(1, -1, 1, 1)
+        y = (acc * scale).astype(np.float32)
         return apply_epilogue(y, xs, a.get("epilogue", ())).astype(DTYPES[a["dtype"]])
     if kind == "maxpool2d":
         k, s = a["size"], a["stride"]

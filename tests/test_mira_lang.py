@@ -1,0 +1,275 @@
+"""The .mira front end (harness/mira_lang.py) and the command-line driver (harness/cli.py).
+
+The programs under tests/programs are this repository's own.  Two of them are written to
+compute what MIRA's W8A8 example programs compute, so their elaborated graphs are checked
+op for op -- kinds, wiring, shapes, attributes and the bytes of every seeded weight --
+against the elaborated graphs MIRA itself wrote into the golden fixtures.  The third one
+uses every builtin and operator form and is checked against the same computation written
+in NumPy."""
+import hashlib
+import os
+import re
+
+import numpy as np
+import pytest
+
+from harness import cli
+from harness import lowering as LW
+from harness import mira_lang as ML
+from harness import models
+from oracle import golden as G
+
+from conftest import bits_equal
+from mira_fixtures import Fixture
+
+PROGRAMS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "programs")
+MLP = os.path.join(PROGRAMS, "affine_mlp.mira")
+CNN = os.path.join(PROGRAMS, "conv_stages.mira")
+BUILTINS = os.path.join(PROGRAMS, "builtins.mira")
+# program, its dims, the builder that draws MIRA's example weights, input name and shape
+CASES = {"mlp": (MLP, {"B": 64}, models.mlp_mira, "x", (64, 784)),
+         "cnn": (CNN, {"N": 16}, models.cnn_mira, "img", (16, 1, 28, 28))}
+
+
+def _read(path: str) -> str:
+    with open(path) as f:
+        return f.read()
+
+
+def _sha(a) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def _ours(g) -> tuple:
+    ids = {v: ("input", v.name, tuple(v.type.shape)) for v in g.inputs}
+    ops = []
+    for i, op in enumerate(g.ops):
+        ids[op.result] = i
+        attrs = {k: _sha(v) if k == "value" else v for k, v in op.attrs.items()}
+        ops.append((op.kind, tuple(ids[x] for x in op.inputs), tuple(op.result.type.shape), op.result.type.dtype,
+                    attrs))
+    return ops, [ids[v] for v in g.outputs]
+
+
+def _mira(doc) -> tuple:
+    def norm(v):
+        if isinstance(v, dict) and "tuple" in v:
+            return tuple(norm(x) for x in v["tuple"])
+        return v["sha256"] if isinstance(v, dict) and "sha256" in v else v
+    ids = {i["id"]: ("input", i["name"], tuple(i["shape"])) for i in doc["inputs"]}
+    ops = []
+    for i, op in enumerate(doc["ops"]):
+        ids[op["result"]["id"]] = i
+        ops.append((op["kind"], tuple(ids[x] for x in op["inputs"]), tuple(op["result"]["shape"]),
+                    op["result"]["dtype"], {k: norm(v) for k, v in op["attrs"].items()}))
+    return ops, [ids[v] for v in doc["outputs"]]
+
+
+# ---------------------------------------------------------------- against MIRA's own elaboration
+
+@pytest.mark.parametrize("case", ["mlp", "cnn"])
+def test_elaborates_like_mira(case):
+    """Generic helpers inlined with their shape symbols bound, `H / 2`-style return dims,
+    the entry's const parameters drawn in declaration order from default_rng(0): the same
+    graph MIRA's elaborator built for its example program, weights byte for byte."""
+    path, dims, _, _, _ = CASES[case]
+    g = ML.elaborate(_read(path), dims=dims)
+    assert _ours(g) == _mira(Fixture(f"{case}_f32").float_graph("elaborated"))
+
+
+@pytest.mark.parametrize("precision", [None, "f16"])
+@pytest.mark.parametrize("case", ["mlp", "cnn"])
+def test_driver_lowers_like_the_builders(case, precision):
+    """compile_graph's lowering and W8A8 rewrite of the elaborated program give the same ops
+    and attrs (q, w_scale, x_scale, epilogues) as the builders' graphs, which
+    test_mira_golden pins against MIRA's quantized graphs; calibration rng(2), rng(3)."""
+    path, dims, builder, name, shape = CASES[case]
+    calib = [{name: np.random.default_rng(s).standard_normal(shape).astype(np.float32)} for s in (2, 3)]
+    prog = cli.compile_graph(ML.elaborate(_read(path), dims=dims), "cpu", precision=precision, quantize="w8a8",
+                             calibration=calib)
+    built = LW.prepare(builder(batch=shape[0], seed=0), precision)
+    LW.w8a8(built, calib)
+
+    def key(g):
+        """Compute ops in order; operands named by what they are (input, constant bytes, or
+        the index of the compute op producing them), since constants may sit anywhere."""
+        index = {op.result: i for i, op in enumerate(g.compute_ops())}
+
+        def operand(v):
+            if v in index:
+                return index[v]
+            return ("const", _sha(v.producer.attrs["value"])) if v.producer is not None else ("input", v.name)
+        return [(op.kind, op.result.type.shape, op.result.type.dtype, [operand(v) for v in op.inputs],
+                 sorted((k, _sha(v) if isinstance(v, np.ndarray) else v) for k, v in op.attrs.items()))
+                for op in g.compute_ops()]
+    assert key(prog.graph) == key(built)
+    assert {op.kind for op in prog.graph.ops} >= ({"qmatmul"} if case == "mlp" else {"qmatmul", "qconv2d"})
+
+
+# ---------------------------------------------------------------- builtins against NumPy
+
+def _numpy_builtins(img, dk, w, s):
+    n, c, h, wd = img.shape
+    xp = np.pad(img, ((0, 0), (0, 0), (2, 2), (2, 2)))
+    conv = np.zeros_like(img)
+    for i in range(3):
+        for j in range(3):
+            conv += xp[:, :, 2 * i:2 * i + h, 2 * j:2 * j + wd] * dk[:, 0, i, j][None, :, None, None]
+    d = img + conv
+    p = d.reshape(n, c, h // 2, 2, wd // 2, 2).mean(axis=(3, 5))
+    dp = np.pad(d, ((0, 0), (0, 0), (1, 1), (1, 1)), constant_values=-np.inf)
+    q = np.empty_like(p)
+    for a in range(h // 2):
+        for b in range(wd // 2):
+            q[:, :, a, b] = dp[:, :, 2 * a:2 * a + 3, 2 * b:2 * b + 3].max(axis=(2, 3))
+    f = (p + q).reshape(n, -1)
+    h0 = np.maximum(f @ w, 0.25) * s + 1.5
+    hh = h0 - h0.mean(axis=1, keepdims=True)
+    t = (1 / (1 + np.exp(-hh)) + np.tanh(hh) * 2 / 4).T
+    u = np.minimum(np.abs(t), np.sqrt(np.exp(-t) + 1))
+    e = np.exp(u - u.max(axis=0, keepdims=True))
+    sm = e / e.sum(axis=0, keepdims=True)
+    return np.maximum(u - u.mean(), 0) + sm.mean()
+
+
+def test_builtins_match_numpy():
+    """Dilated depthwise conv, avg / padded max pooling, reshape with symbol arithmetic,
+    flatten, matmul, scalar operands on either side, unary minus, keepdims means,
+    transpose's default perm, softmax over axis 0: the host evaluator and the oracle on
+    the elaborated graph both agree with NumPy in f64 to f32 rounding."""
+    rng = np.random.default_rng(4)
+    weights = {"dk": rng.standard_normal((3, 1, 3, 3)).astype(np.float32),
+               "w": (rng.standard_normal((48, 5)) / 7).astype(np.float32),
+               "s": rng.uniform(0.5, 1.5, 5).astype(np.float32)}
+    img = rng.standard_normal((2, 3, 8, 8)).astype(np.float32)
+    want = _numpy_builtins(img.astype(np.float64), *(weights[k].astype(np.float64) for k in ("dk", "w", "s")))
+    g = ML.elaborate(_read(BUILTINS), weights=weights, seed=None)
+    (oracle_out,) = G.run_graph(g, {"img": img})
+    np.testing.assert_allclose(oracle_out, want, rtol=2e-5, atol=1e-6)
+    prog = cli.compile_graph(ML.elaborate(_read(BUILTINS), weights=weights, seed=None), "cpu")
+    (host_out,) = prog.run({"img": img})
+    np.testing.assert_allclose(host_out, want, rtol=2e-5, atol=1e-6)
+
+
+def test_weights_given_seeded_and_f16():
+    """Given weights replace the seeded draw for those parameters and take nothing from the
+    generator, so the next parameter gets the draw the given one would have had
+    (mira/elaborate.py:204-210); f16 parameters hold f16 constants."""
+    src = ("fn main(x: f32[2, 3], const a: f32[3, 4], const b: f32[4], const c: f16[4]) -> f32[2, 4] {\n"
+           "  return x @ a + b\n}\n")
+    rng = np.random.default_rng(0)
+    drawn = [models.mira_random_weight(rng, s) for s in ((3, 4), (4,), (4,))]
+    g = ML.elaborate(src)
+    consts = [op.attrs["value"] for op in g.ops if op.kind == "const"]
+    assert all(np.array_equal(x, y.astype(x.dtype)) for x, y in zip(consts, drawn))
+    assert consts[2].dtype == np.float16
+    given = np.full((4,), 3.0, np.float32)
+    consts2 = [op.attrs["value"] for op in ML.elaborate(src, weights={"b": given}).ops if op.kind == "const"]
+    assert np.array_equal(consts2[1], given) and np.array_equal(consts2[0], consts[0])
+    assert np.array_equal(consts2[2], drawn[1].astype(np.float16))
+
+
+# ---------------------------------------------------------------- errors
+
+ERRORS = [
+    ("fn main(x: f32[2]) -> f32[2] {\n  return x +\n}\n", {}, "line 3"),
+    ("fn main(x: f32[2]) -> f32[2] { return x $ x }", {}, "unexpected character"),
+    ("fn main(x: f32[B, 3]) -> f32[B, 3] { return x }", {}, "'B' of the entry function needs a value"),
+    ("fn f(a: f32[N], b: f32[N]) -> f32[N] { return a + b }\n"
+     "fn main(x: f32[3], y: f32[4]) -> f32[3] { return f(x, y) }", {}, "N is already 3, got 4"),
+    ("fn main(x: f32[4]) -> f32[5] { return x }", {}, "the result of 'main'"),
+    ("fn half(v: f32[N]) -> f32[N / 2] { return v }\n"
+     "fn main(x: f32[3]) -> f32[1] { return half(x) }", {}, "3 / 2 is not a whole number"),
+    ("fn main(x: f32[2]) -> f32[2] { return frobnicate(x) }", {}, "unknown function 'frobnicate'"),
+    ("fn f(v: f32[2]) -> f32[2] { return f(v) }\nfn main(x: f32[2]) -> f32[2] { return f(x) }", {},
+     "recursive call to 'f'"),
+    ("fn f(const v: f32[2]) -> f32[2] { return v }\nfn main(x: f32[2]) -> f32[2] { return f(x) }", {},
+     "'const' is only allowed"),
+    ("fn main(x: f32[2]) -> f32[2] { return y }", {}, "'y' is undefined"),
+    ("fn main(x: f32[2]) -> f32[2] { return relu }", {}, "'relu' is a function"),
+    ("fn main(x: f32[2, 2]) -> f32[2, 2] { return softmax(axis=0, x) }", {}, "positional argument after"),
+    ("fn main(x: f32[2, 2]) -> f32[2, 2] { return softmax(x, dim=0) }", {}, "no argument 'dim'"),
+    ("fn main(x: f32[2, 2]) -> f32[2, 1] { return mean(x, axis=1, keepdims=1) }", {}, "keepdims must be"),
+    ("fn main(x: f32[2, 3]) -> f32[2, 3] { return x @ x }", {}, "matmul"),
+    ("fn f(v: f32[2]) -> f32[2] { return v }\nfn main(x: f16[2]) -> f32[2] { return f(x) }", {}, "f16 != f32"),
+    ("fn main(x: f32[2], const w: f32[2]) -> f32[2] { return x + w }", {"seed": None}, "no value for const"),
+    ("fn main(x: f32[2], const w: f32[2]) -> f32[2] { return x + w }", {"weights": {"v": np.ones(2)}},
+     "unknown const parameters: v"),
+    ("fn main(x: f32[2], const w: f32[2]) -> f32[2] { return x + w }", {"weights": {"w": np.ones(3)}},
+     "weight 'w' has shape [3]"),
+    ("fn main(x: f32[6]) -> f32[4] { return reshape(x, [-1, 4]) }", {}, "cannot infer -1"),
+    ("fn main(x: f32[2]) -> f32[2] { return x }\nfn main(x: f32[2]) -> f32[2] { return x }", {}, "defined twice"),
+]
+
+
+@pytest.mark.parametrize("src,kw,match", ERRORS, ids=[e[2] for e in ERRORS])
+def test_errors(src, kw, match):
+    with pytest.raises(ML.MiraSyntaxError, match=re.escape(match)):
+        ML.elaborate(src, **kw)
+
+
+# ---------------------------------------------------------------- the driver
+
+def test_cli_check_and_emit(capsys):
+    assert cli.main(["check", MLP, "--dim", "B=64"]) == 0
+    assert "ok: " in capsys.readouterr().out
+    for stage in ("tokens", "ir", "opt", "partition"):
+        assert cli.main(["emit", CNN, "--dim", "N=2", "--stage", stage]) == 0
+        assert capsys.readouterr().out.strip()
+    # the parse tree printed as source parses back to the same tree (line numbers aside)
+    assert cli.main(["emit", BUILTINS, "--stage", "ast"]) == 0
+    printed = capsys.readouterr().out
+    assert cli.format_module(ML.parse(printed)) == printed.strip()
+    assert "(C * (H / 2)) * (W / 2)" in printed and "keepdims=true" in printed
+
+
+def test_cli_run_save_weights_inputs(tmp_path, capsys):
+    """--weights / --inputs from .npz, --save; the cpu target's W8A8 run of the CNN (host
+    qconv2d / qmatmul) equals the oracle's evaluation of the same quantized graph."""
+    rng = np.random.default_rng(9)
+    wpath, xpath, out = tmp_path / "w.npz", tmp_path / "x.npz", tmp_path / "y.npy"
+    np.savez(wpath, hb=np.linspace(-1, 1, 10).astype(np.float32))
+    img = rng.standard_normal((4, 1, 28, 28)).astype(np.float32)
+    np.savez(xpath, img=img)
+    args = [CNN, "--dim", "N=4", "--weights", str(wpath), "--inputs", str(xpath), "--quantize", "w8a8"]
+    assert cli.main(["run", *args, "--save", str(out)]) == 0
+    assert "saved to" in capsys.readouterr().out
+    got = np.load(out)
+    prog = cli.compile_file(CNN, "cpu", dims={"N": 4}, weights={"hb": np.linspace(-1, 1, 10).astype(np.float32)},
+                            quantize="w8a8")
+    assert bits_equal(got, prog.run({"img": img})[0])
+    assert bits_equal(got, G.run_graph(prog.graph, {"img": img})[0])
+    assert {op.kind for op in prog.graph.ops} >= {"qconv2d", "qmatmul"}
+
+
+def test_check_outputs():
+    ref = np.array([[0.5, -2.0], [1.0, 0.0]], np.float32)
+    ok, lines = cli.check_outputs([ref + 0.039], [ref], 2e-2)
+    assert ok and "PASS" in lines[0]
+    ok, lines = cli.check_outputs([ref, ref + np.float32(0.041)], [ref, ref], 2e-2)
+    assert not ok and "PASS" in lines[0] and "FAIL" in lines[1] and "relative 2.05" in lines[1]
+
+
+def test_cli_bench_and_errors(tmp_path, capsys):
+    assert cli.main(["bench", MLP, "--dim", "B=8", "--targets", "cpu", "--iters", "2"]) == 0
+    assert "cpu" in capsys.readouterr().out
+    bad = tmp_path / "bad.mira"
+    bad.write_text("fn main(x: f32[2]) -> f32[2] {\n  return x @\n}\n")
+    assert cli.main(["run", str(bad)]) == 1
+    assert "line 3" in capsys.readouterr().err
+    assert cli.main(["check", MLP]) == 1
+    assert "'B' of the entry function needs a value" in capsys.readouterr().err
+
+
+def test_cli_onnx_model(tmp_path, capsys):
+    """.onnx files go through the importer; a symbolic batch is pinned with --shape."""
+    import onnx_writer as W
+    m = W.Model(13)
+    x = m.input("x", ("n", 6))
+    m.output(m.node("Relu", [m.node("Gemm", [x, m.init(np.eye(6, 3, dtype=np.float32))])]), ("n", 3))
+    path = tmp_path / "tiny.onnx"
+    path.write_bytes(m.bytes())
+    assert cli.main(["check", str(path)]) == 1
+    assert "symbolic" in capsys.readouterr().err
+    assert cli.main(["check", str(path), "--shape", "x=5,6"]) == 0
+    assert "x: f32[5, 6]" in capsys.readouterr().out
