@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MR_ABI_VERSION 6
+#define MR_ABI_VERSION 7
 
 enum mr_status {
   MR_OK = 0,
@@ -221,6 +221,22 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* g, const int8_t* b, int64_t 
 int mr_qconv2d_maxpool(const int8_t* x, const mr_conv_geom* g, const int8_t* b, int64_t k_pad, int64_t n_pad,
                        const mr_epilogue* epi, int32_t pool_size, int32_t pool_stride, int32_t pool_pad_top,
                        int32_t pool_pad_left, float pad_value, int32_t poh, int32_t pow_, void* stream);
+
+/* The same fused stem reading the f32 NCHW image [n, c, h, w] itself: the
+ * activation quantizer of mira/ops.py:602-603 (round(x / x_scale) clipped to
+ * +-127, of the f16 rounding of x when round_f16 is set: the f32 -> f16 cast
+ * of mira/ops.py:405-406 in an f16 graph) followed by mr_qconv2d_maxpool, as
+ * one kernel.  Replaces mr_quantize_nchw_nhwc / mr_quantize_f16_nchw_nhwc +
+ * mr_qconv2d_maxpool when the stem is the only reader of the image's int8
+ * copy, which is then never written.  Same geometry rules (c_pad == 4
+ * describes the packed weights), plus: 7 kernel rows of 5 to 8 taps, no
+ * dilation, an even column stride, a row stride of at most 2, and input rows
+ * of (ow - 1) * sw + 8 pixels forming at most 64 four-pixel groups (ResNet's
+ * 224 x 224 stem: 230 pixels, 58 groups); MR_EUNSUPPORTED otherwise. */
+int mr_qconv2d_maxpool_f32in(const float* x, float x_scale, int32_t round_f16, const mr_conv_geom* g,
+                             const int8_t* b, int64_t k_pad, int64_t n_pad, const mr_epilogue* epi,
+                             int32_t pool_size, int32_t pool_stride, int32_t pool_pad_top, int32_t pool_pad_left,
+                             float pad_value, int32_t poh, int32_t pow_, void* stream);
 
 /* ---- K4a: f32 depthwise conv ------------------------------------------ */
 

@@ -404,6 +404,17 @@ class RocmExecutable:
                     self.need_f32.discard(v)
                 lst = self.need_i8.setdefault(v, [])
                 lst += [s for s in self.need_i8.get(r, []) if s not in lst]
+        # a fused stem that is its image input's only reader quantizes the rows it needs
+        # from the f32 input itself: no int8 copy of the image is made
+        self.stem_f32in: dict = {}          # maxpool op -> (graph input, quantize its f16 rounding)
+        for pool, (conv, _) in self.fused_stem.items():
+            src = self._stem_f32_source(conv)
+            if src is None:
+                continue
+            self.stem_f32in[pool] = src
+            xs = _f32key(conv.attrs["x_scale"])
+            for v in {src[0], conv.inputs[0]}:
+                self.need_i8[v] = [s for s in self.need_i8.get(v, []) if s != xs]
         self.staging: dict["Value", object] = {}
         self.canon: dict["Value", object] = {}     # C-order copies of NHWC values (_c_order)
         self._plan_views()
@@ -520,6 +531,30 @@ class RocmExecutable:
                 and pool_cfg in ((3, 2, 1, 1), (2, 2, 0, 0))
                 and pool.result.type.shape[3] <= (60 if pool_cfg[0] == 3 else 64)
                 and self._monotone_epilogue(conv))
+
+    def _stem_f32_source(self, conv: "Op") -> Optional[tuple]:
+        """(graph input, round to f16 first) when a fused stem can read its image straight from
+        the f32 NCHW input with mr_qconv2d_maxpool_f32in: the convolution is the input's only
+        reader (directly, or through the f16 cast of an f16 graph), the kernel has 7 rows of
+        5-8 taps, no dilation, an even column stride, a row stride of at most 2, and input rows
+        of at most 64 four-pixel groups."""
+        x = conv.inputs[0]
+        p = x.producer
+        f16 = p is not None and p in self.input_casts
+        v = p.inputs[0] if f16 else x
+        if v not in self.g.inputs or v in self.g.outputs or x in self.g.outputs:
+            return None
+        if len(self.users.get(v, [])) != 1 or len(self.users.get(x, [])) != 1:
+            return None
+        if v in self.need_f32 or x in self.need_f32 or v.type.dtype != "f32":
+            return None
+        _, c, kh, kw = conv.attrs["q"].shape
+        (sh, sw), (_, pw), (dh, dw), _ = conv_params(conv.attrs)
+        ow = conv.result.type.shape[3]
+        groups = ((ow - 1) * sw + 8 - pw + (pw + 3) // 4 * 4 + 3) // 4     # 4-pixel column groups per input row
+        if c > 4 or kh != 7 or not 5 <= kw <= 8 or (dh, dw) != (1, 1) or sw % 2 or sh > 2 or groups > 64:
+            return None
+        return v, f16
 
     def _monotone_epilogue(self, op: "Op") -> bool:
         """Every step non-decreasing in the value, with an operand that is the same across a
@@ -892,14 +927,15 @@ class RocmExecutable:
     def _emit_fused_stem(self, op: "Op") -> None:
         conv, pad_op = self.fused_stem[op]
         a = conv.attrs
-        x = self._src(conv.inputs[0])
+        f32in = self.stem_f32in.get(op)
+        x = None if f32in else self._src(conv.inputs[0])
         q = np.asarray(a["q"], np.int8)
         n, c, h, w = conv.inputs[0].type.shape
         o, _, kh, kw = q.shape
         (sh, sw), (ph, pw), (dh, dw), _ = conv_params(a)
         _, _, oh, ow = conv.result.type.shape
         xs = _f32key(a["x_scale"])
-        xq, cp = x.i8[xs] if xs in x.i8 else self._quantize_to(x, xs)
+        xq, cp = (None, 4) if f32in else x.i8[xs] if xs in x.i8 else self._quantize_to(x, xs)
         bl = pack.pack_conv(q, cp, min_rows=64)
         b = self._upload(pack.device_weights(bl))
         scale = self._upload(pack.combined_scale(a["x_scale"], a["w_scale"]))
@@ -914,10 +950,17 @@ class RocmExecutable:
         _, _, poh, pw_ = op.result.type.shape
         lib, kp, npad = self.lib, bl.shape[1], bl.shape[0]
         pt, pl = pads[2][0], pads[3][0]
-        self._add("qconv2d_maxpool", lambda s: L.check(lib.mr_qconv2d_maxpool(
-            xq.data_ptr(), C.byref(geom), b.data_ptr(), kp, npad, C.byref(e), size, stride, pt, pl, value, poh, pw_,
-            s), "mr_qconv2d_maxpool"), nbytes=n * h * w * c + o * c * kh * kw + self._epi_bytes(e, n * poh * pw_, o),
-            nops=2 * n * oh * ow * o * c * kh * kw)
+        out_bytes = o * c * kh * kw + self._epi_bytes(e, n * poh * pw_, o)
+        if f32in:
+            stage, rf16 = self.staging[f32in[0]], int(f32in[1])
+            self._add("qconv2d_maxpool", lambda s: L.check(lib.mr_qconv2d_maxpool_f32in(
+                stage.data_ptr(), xs, rf16, C.byref(geom), b.data_ptr(), kp, npad, C.byref(e), size, stride, pt, pl,
+                value, poh, pw_, s), "mr_qconv2d_maxpool_f32in"), nbytes=4 * n * h * w * c + out_bytes,
+                nops=2 * n * oh * ow * o * c * kh * kw)
+        else:
+            self._add("qconv2d_maxpool", lambda s: L.check(lib.mr_qconv2d_maxpool(
+                xq.data_ptr(), C.byref(geom), b.data_ptr(), kp, npad, C.byref(e), size, stride, pt, pl, value, poh,
+                pw_, s), "mr_qconv2d_maxpool"), nbytes=n * h * w * c + out_bytes, nops=2 * n * oh * ow * o * c * kh * kw)
         self._finish_i8(out, fused)
 
     def _emit_maxpool2d(self, op: "Op") -> None:

@@ -751,6 +751,88 @@ def test_qconv2d_maxpool(lib, n, c, h, o, k, s, p, pool, pst, ppad, pval, neg):
     assert bits_equal(yq.cpu().numpy()[:, :o], to_rows(G.quantize_activation(want, next_xs)).astype(np.int8))
 
 
+@pytest.mark.parametrize("n,c,h,w,o,kw,sh,sw,pool,pval,f16,neg", [
+    (2, 3, 224, 224, 64, 7, 2, 2, 3, float("-inf"), False, False),   # ResNet-18 stem from the f32 image
+    (2, 3, 224, 224, 64, 7, 2, 2, 3, float("-inf"), True, False),    # f16 graph: quantize the f16 rounding
+    (3, 1, 61, 45, 32, 7, 2, 2, 3, 0.25, False, True),               # odd sizes, finite pad, negative maxima
+    (2, 4, 40, 38, 16, 6, 2, 2, 2, 0.0, False, False),               # 4 channels, 6 taps, 2x2 pool
+    (2, 2, 23, 50, 64, 5, 1, 2, 3, float("-inf"), True, False),      # row stride 1, 5 taps
+])
+def test_qconv2d_maxpool_f32in(lib, n, c, h, w, o, kw, sh, sw, pool, pval, f16, neg):
+    """The stem reading the f32 NCHW image (quantized per band into LDS) against the unfused
+    quantize + mr_qconv2d_maxpool and against the oracle, bit for bit.  The image holds
+    exact quantization ties, values far past the clip range and infinities."""
+    torch = _torch()
+    rng = np.random.default_rng(h * w + o)
+    kh, ph, pw = 7, 3, kw // 2
+    xs = 2.0 ** -6
+    x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    flat = x.reshape(-1)
+    picks = rng.choice(flat.size, 64, replace=False)
+    flat[picks[:32]] = (rng.integers(-100, 100, 32) + 0.5) * xs       # ties: half to even
+    flat[picks[32:48]] = rng.choice([-3.0, 5.0, np.inf, -np.inf], 16)  # clipped to +-127
+    wt = rng.standard_normal((o, c, kh, kw)).astype(np.float32)
+    if neg:
+        x, wt = np.abs(x) + 0.01, -np.abs(wt)
+    q, ws = G.quantize_array(wt, 0)
+    bias = (rng.standard_normal((o, 1, 1)) * 0.3).astype(np.float32)
+    steps = (("add", 1, False),) if neg else (("add", 1, False), ("relu", None, False))
+    attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "stride": (sh, sw), "padding": (ph, pw),
+             "epilogue": steps}
+    x_in = x.astype(np.float16).astype(np.float32) if f16 else x
+    conv = G.qconv2d([x_in, bias], attrs)
+    ppad = 1 if pool == 3 else 0
+    padded = G.pad([conv], {"pads": ((0, 0), (0, 0), (ppad, ppad), (ppad, ppad)), "value": pval})
+    want = G.maxpool2d([padded], {"size": pool, "stride": 2})
+    oh, ow = conv.shape[2:]
+    poh, pw_ = want.shape[2:]
+    next_xs = float(np.abs(want[np.isfinite(want)]).max()) / 127
+    cp = 4
+    bl = pack.pack_conv(q, cp, min_rows=64)
+    b = T(pack.device_weights(bl))
+    scale = T(pack.combined_scale(xs, ws))
+    g = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=cp, o=o, oh=oh, ow=ow, kh=kh, kw=kw, sh=sh, sw=sw, ph=ph, pw=pw, dh=1,
+                   dw=1)
+    M = n * poh * pw_
+    ocp = pack.c_pad_for(o)
+    bt = T(bias.reshape(o))
+    dev_steps = [("add", L.BC_COL, bt, 0, False)] + ([] if neg else [("relu", 0, None, 0, False)])
+    xd = T(x)
+    outs = []
+    for fused in (True, False):
+        y, yq = empty((M, o), torch.float32), empty((M, ocp), torch.int8)
+        e = epilogue(dev_steps, scale=scale, out_f32=y, ldo=o, out_i8=yq, ldq=ocp, xs=next_xs)
+        print(f"f32in n={n} c={c} {h}x{w} o={o} kw={kw} stride=({sh},{sw}) pool={pool} f16={f16} fused={fused}",
+              flush=True)
+        if fused:
+            L.check(lib.mr_qconv2d_maxpool_f32in(xd.data_ptr(), xs, int(f16), C.byref(g), b.data_ptr(), bl.shape[1],
+                                                 bl.shape[0], C.byref(e), pool, 2, ppad, ppad, pval, poh, pw_,
+                                                 stream()), "mr_qconv2d_maxpool_f32in")
+        else:
+            xq = empty((n, h, w, cp), torch.int8)
+            quant = lib.mr_quantize_f16_nchw_nhwc if f16 else lib.mr_quantize_nchw_nhwc
+            L.check(quant(xd.data_ptr(), n, c, h, w, xq.data_ptr(), cp, xs, stream()), "quantize")
+            L.check(lib.mr_qconv2d_maxpool(xq.data_ptr(), C.byref(g), b.data_ptr(), bl.shape[1], bl.shape[0],
+                                           C.byref(e), pool, 2, ppad, ppad, pval, poh, pw_, stream()),
+                    "mr_qconv2d_maxpool")
+        sync()
+        outs.append((y.cpu().numpy(), yq.cpu().numpy()[:, :o]))
+    to_rows = lambda a: a.transpose(0, 2, 3, 1).reshape(M, o)
+    assert bits_equal(outs[0][0], outs[1][0]) and bits_equal(outs[0][1], outs[1][1])
+    assert bits_equal(outs[0][0], to_rows(want))
+    assert bits_equal(outs[0][1], to_rows(G.quantize_activation(want, next_xs)).astype(np.int8))
+
+
+def test_qconv2d_maxpool_f32in_rejects(lib):
+    """Shapes the f32-input stem has no kernel for answer MR_EUNSUPPORTED (3) before any launch."""
+    g = L.ConvGeom(n=1, h=64, w=64, c=3, c_pad=4, o=64, oh=32, ow=32, kh=5, kw=5, sh=2, sw=2, ph=2, pw=2, dh=1, dw=1)
+    e = epilogue(scale=T(np.ones(64)), out_f32=empty((16 * 16, 64), _torch().float32), ldo=64)
+    x, b = T(np.zeros((1, 3, 64, 64), np.float32)), T(np.zeros((64, 192), np.int8))
+    assert lib.mr_qconv2d_maxpool_f32in(x.data_ptr(), 0.1, 0, C.byref(g), b.data_ptr(), 192, 64, C.byref(e), 3, 2, 1,
+                                        1, float("-inf"), 16, 16, stream()) == 3
+    assert "7-row kernel" in lib.mr_last_error().decode()
+
+
 @pytest.mark.parametrize("kind,shape", [("matmul", (300, 512, 256)), ("matmul", (4096, 1152, 128)),
                                         ("conv", (2, 64, 56, 56, 64, 3, 1, 1)),      # patch tiles
                                         ("conv", (2, 256, 14, 14, 512, 3, 1, 1)),    # 128x256 tiles
