@@ -286,10 +286,13 @@ constexpr int SPEC_BIAS_F32 = SF_COL | SF_F32;
 // the fused stem's usual form: bias + ReLU, pooled, to f32 and int8
 constexpr int SPEC_RELU_F32_I8 = SF_COL | SF_LO | SF_F32 | SF_I8;
 // MobileNet-style blocks: 1x1 expansion + ReLU6 -> f32 (read by the depthwise
-// conv); linear projection -> f32 + int8, with or without the residual add
+// conv); linear projection -> f32 + int8, with or without the residual add, or
+// int8 only when no later residual reads the block's output
 constexpr int SPEC_RELU6_F32 = SF_COL | SF_LO | SF_HI | SF_F32;
 constexpr int SPEC_BIAS_F32_I8 = SF_COL | SF_F32 | SF_I8;
 constexpr int SPEC_BIAS_RES_F32_I8 = SF_COL | SF_FULL | SF_F32 | SF_I8;
+constexpr int SPEC_BIAS_I8 = SF_COL | SF_I8;
+constexpr int SPEC_BIAS_RES_I8 = SF_COL | SF_FULL | SF_I8;
 
 // The compile-time form of an epilogue, or -1 when it has none: the fixed
 // form without an int32 accumulator output, every output and operand row

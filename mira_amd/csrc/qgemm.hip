@@ -749,6 +749,8 @@ static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
       case SPEC_RELU6_F32: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RELU6_F32); return;
       case SPEC_BIAS_F32_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_F32_I8); return;
       case SPEC_BIAS_RES_F32_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_RES_F32_I8); return;
+      case SPEC_BIAS_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_I8); return;
+      case SPEC_BIAS_RES_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_RES_I8); return;
       default: break;
     }
   }

@@ -487,6 +487,9 @@ FORMS = {
     "bias_relu6_f32": ((("add", 1, False), ("maximum", 3, False), ("minimum", 4, False)), True, False),
     "bias_f32_i8": ((("add", 1, False),), True, True),
     "bias_res_f32_i8": ((("add", 1, False), ("add", 2, False)), True, True),
+    # MobileNet projections whose output no later residual reads: int8 only
+    "bias_i8": ((("add", 1, False),), False, True),
+    "bias_res_i8": ((("add", 1, False), ("add", 2, False)), False, True),
     # BatchNorm as MIRA's ONNX importer leaves it: a per-channel mul ahead of the bias
     "bn_relu_i8": ((("mul", 5, False), ("add", 1, False), ("relu", None, False)), False, True),
     "bn_res_f32_i8": ((("mul", 5, False), ("add", 1, False), ("add", 2, False), ("relu", None, False)), True, True),
@@ -507,6 +510,8 @@ FORM_CONV_CASES = [
     (2, 96, 14, 14, 576, 1, 1, 0, 1),     # 1x1 expansion as a dense GEMM (c_pad 96)
     (2, 160, 7, 7, 960, 1, 1, 0, 1),      # 1x1 expansion as a dense GEMM, partial column tile
     (2, 3, 17, 17, 32, 3, 2, 1, 1),       # 3-channel stem, 4-channel loader
+    (2, 32, 28, 28, 16, 1, 1, 0, 1),      # 1x1 projection to 16 channels (64x32 tiles)
+    (2, 144, 14, 14, 24, 1, 1, 0, 1),     # 1x1 projection to 24 channels, K past one stage
 ]
 
 
