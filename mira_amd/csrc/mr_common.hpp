@@ -269,7 +269,7 @@ int w8gemm_launch(const float* x, int64_t ldx, const int8_t* b, const float* w_s
 // Epilogue forms a kernel is compiled for: EF_GENERIC runs the step
 // interpreter, EF_FIXED the fixed form (see EpiDev) with its flags read at run
 // time, and EF_SPEC | SF_* the fixed form with its steps and outputs known at
-// compile time: a tile whose columns are all in range then runs its rows as
+// compile time: a tile whose columns are all in range (any tile when N % 4 == 0) then runs its rows as
 // straight-line code (all LDS reads, then all operand loads, then the math and
 // the stores), so the rows' latencies overlap.
 constexpr int EF_GENERIC = 0, EF_FIXED = 1, EF_SPEC = 0x100;

@@ -294,12 +294,20 @@ __global__ void __launch_bounds__(WM* WN * 64)
   constexpr int STAGE_BYTES = A_STAGE + BN * KB;
   constexpr int PATCH_OPS = PATCH ? PATCH_MAX / 16 / (NW * 64) : 0;   // patch DMAs per wave
   constexpr int RING_BYTES = STAGES * STAGE_BYTES;
-  constexpr int LDS_BYTES = RING_BYTES + (PATCH ? PATCH_MAX : 0);
+  // the epilogue stages the int32 tile one 32-row block row per wave at a time
+  constexpr int EP_ROWS = WM * 32;
+  constexpr int EP_LD = BN + 4;                     // int32 row stride (16-byte pad)
+  constexpr int EP_BYTES = EP_ROWS * EP_LD * 4;
+  constexpr int LDS_BYTES = RING_BYTES + (PATCH ? PATCH_MAX : 0) > EP_BYTES ? RING_BYTES + (PATCH ? PATCH_MAX : 0)
+                                                                            : EP_BYTES;
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32");
   static_assert(PATCH || (A_OPS * A_ROWS_PER_OP * NW == BM), "loader mapping");
   static_assert(B_OPS * (64 / CPR) * NW == BN, "loader mapping");
   static_assert(!PATCH || PATCH_OPS * 16 * NW * 64 == PATCH_MAX, "patch loader mapping");
-  static_assert(STAGES >= 3 && (STAGES - 2) * OPS < 64, "stages / vmcnt range");
+  // STAGES == 1: a single 64-byte K step (launched only for k_tiles == 1), no ring, so the
+  // workgroup holds only its epilogue staging and many more fit on a CU
+  static_assert((STAGES == 1 && KB == 64 && !PATCH) || (STAGES >= 3 && (STAGES - 2) * OPS < 64),
+                "stages / vmcnt range");
 
   __shared__ __attribute__((aligned(1024))) int8_t lds[LDS_BYTES];
   int8_t* const patch = lds + RING_BYTES;
@@ -564,6 +572,15 @@ __global__ void __launch_bounds__(WM* WN * 64)
   // of stage t+1 is read (after the barrier that publishes it) while the last
   // step of stage t multiplies.
   v4i a0[FM], b0[FN], a1[FM], b1[FN];
+  if constexpr (STAGES == 1) {
+    issue(0, 0);
+    wait_vmcnt<0>();
+    block_barrier();
+    load_frags(0, 0, q_off, q_cb, a0, b0);
+    load_frags(0, 1, q_off, q_cb, a1, b1);
+    mfma_all(a0, b0);
+    mfma_all(a1, b1);
+  } else {
   if (KT >= STAGES - 1) wait_vmcnt<(STAGES - 2) * OPS>(); else wait_vmcnt<0>();
   block_barrier();
   load_frags(0, 0, q_off, q_cb, a0, b0);
@@ -600,16 +617,14 @@ __global__ void __launch_bounds__(WM* WN * 64)
     }
     mfma_all(a1, b1);
   }
+  }  // STAGES >= 3
 
   // ---- fused epilogue.  The int32 tile goes through LDS one 32-row block row
   // per wave at a time; the whole workgroup then walks those rows with each
   // thread owning 4 adjacent columns: per-column constants are read once,
   // operands and results move as 16-byte (f32) / 4-byte (int8) accesses.
-  constexpr int EP_ROWS = WM * 32;
-  constexpr int EP_LD = BN + 4;                     // int32 row stride (16-byte pad)
   constexpr int CG = BN / 4;                        // 4-column groups per row
   constexpr int RSTEP = (WM * WN * 64) / CG;        // rows walked concurrently
-  static_assert(EP_ROWS * EP_LD * 4 <= LDS_BYTES, "epilogue staging exceeds LDS");
   static_assert((WM * WN * 64) % CG == 0, "epilogue thread mapping");
   int32_t* ep = reinterpret_cast<int32_t*>(lds);
   const int cgi = threadIdx.x % CG;
@@ -628,7 +643,12 @@ __global__ void __launch_bounds__(WM* WN * 64)
             acc[pass * FN + j][r];
     lds_store_barrier();
     if constexpr (EF >= EF_SPEC) {
-      if (n0 + BN <= g.N) {
+      // a partial last column tile runs here too when N % 4 == 0: a thread's 4 columns are
+      // then all in range or all past N, and a thread past N computes but stores nothing
+      // (its residual loads read column 0 of the row instead)
+      if (n0 + BN <= g.N || (g.N & 3) == 0) {
+        const bool cok = col0 < g.N;
+        const int rcol = cok ? col0 : 0;
         constexpr bool S_COL = EF & SF_COL, S_FULL = EF & SF_FULL, S_LO = EF & SF_LO, S_HI = EF & SF_HI;
         constexpr bool S_F32 = EF & SF_F32, S_I8 = EF & SF_I8, S_F16 = EF & SF_F16;
         constexpr int NR = EP_ROWS / RSTEP;
@@ -646,7 +666,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
               const int rr = threadIdx.x / CG + (c0 + k) * RSTEP;
               const int lk = (rr >> 5) * TM + pass * 32 + (rr & 31);
               const int64_t r = mbase + min(lk, mvalid - 1);
-              res[k] = *reinterpret_cast<const float4*>(e.full_ptr + r * e.full_ld + col0);
+              res[k] = *reinterpret_cast<const float4*>(e.full_ptr + r * e.full_ld + rcol);
             }
           }
         };
@@ -688,6 +708,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
 #pragma unroll
         for (int k = 0; k < NRC; ++k) {
           const int lr = local[k];       // rows past mvalid: dropped by the resource's bound
+          if (!cok) continue;
           if constexpr (S_F32) {
             const v4i v = {int(__float_as_uint(y[k][0])), int(__float_as_uint(y[k][1])),
                            int(__float_as_uint(y[k][2])), int(__float_as_uint(y[k][3]))};
@@ -778,8 +799,14 @@ static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
       launch_cfg<PATCH_BM128, 128, 2, 2, 3, AMODE>(g, e, stream);
   } else if (g.N <= 32 || (g.M + 63) / 64 * ((g.N + 31) / 32) <= 2 * cus) {
     // N <= 32, or a grid so small (the fc layer of a CNN: M = batch) that even
-    // 64x32 tiles give at most two per CU: the most workgroups wins
-    launch_cfg<64, 32, 2, 1, 4, AMODE>(g, e, stream);
+    // 64x32 tiles give at most two per CU: the most workgroups wins.  The ring is
+    // what limits how many share a CU (LDS), so it is 3 stages, or none when K is
+    // one 64-byte step (MobileNetV2 B=128: 3-channel stem 100 -> 90 us with 3
+    // stages instead of 4, 32 -> 16 projection 53 -> 45 us)
+    if (g.k_tiles == 1)
+      launch_cfg<64, 32, 2, 1, 1, AMODE>(g, e, stream);
+    else
+      launch_cfg<64, 32, 2, 1, 3, AMODE>(g, e, stream);
   } else if (AMODE == A_DENSE && g.k_pad <= 1024) {
     // short K (the 1x1 convolutions of a MobileNet): the launch is bound by its
     // result stores, and small tiles -- more workgroups, shorter epilogues --

@@ -512,6 +512,8 @@ FORM_CONV_CASES = [
     (2, 3, 17, 17, 32, 3, 2, 1, 1),       # 3-channel stem, 4-channel loader
     (2, 32, 28, 28, 16, 1, 1, 0, 1),      # 1x1 projection to 16 channels (64x32 tiles)
     (2, 144, 14, 14, 24, 1, 1, 0, 1),     # 1x1 projection to 24 channels, K past one stage
+    (2, 16, 28, 28, 96, 1, 1, 0, 1),      # 1x1 expansion 16 -> 96 as a dense GEMM: 96 of 128 tile columns
+    (2, 64, 15, 15, 160, 3, 2, 1, 1),     # stride 2, 64-channel loader, 160 columns: last tile partial
 ]
 
 
