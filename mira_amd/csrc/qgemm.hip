@@ -815,7 +815,14 @@ static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
     const int64_t mt128 = (g.M + 127) / 128;
     const bool n128 = g.N > 64 && g.N <= 128;   // one 128-column tile (else 64-column ones)
     if (n128 ? mt128 < cus : mt128 * ((g.N + 63) / 64) < cus)
-      launch_cfg<64, 32, 2, 1, 4, AMODE>(g, e, stream);
+      launch_cfg<64, 32, 2, 1, 3, AMODE>(g, e, stream);
+    else if (g.k_tiles == 1 && n128)
+      // K in one 64-byte step: no ring, so more workgroups share a CU (MobileNetV2
+      // B=128 112x112 16->96: 161 -> 152 us)
+      launch_cfg<128, 128, 2, 2, 1, AMODE>(g, e, stream);
+    else if (g.k_tiles == 1)
+      // and 64x64 tiles of 2 waves (56x56 24->144: 53 -> 45 us; 14x14 64->384: 16 -> 14 us)
+      launch_cfg<64, 64, 1, 2, 1, AMODE>(g, e, stream);
     else if (n128)
       launch_cfg<128, 128, 2, 2, 3, AMODE>(g, e, stream);
     else

@@ -514,6 +514,8 @@ FORM_CONV_CASES = [
     (2, 144, 14, 14, 24, 1, 1, 0, 1),     # 1x1 projection to 24 channels, K past one stage
     (2, 16, 28, 28, 96, 1, 1, 0, 1),      # 1x1 expansion 16 -> 96 as a dense GEMM: 96 of 128 tile columns
     (2, 64, 15, 15, 160, 3, 2, 1, 1),     # stride 2, 64-channel loader, 160 columns: last tile partial
+    (4, 24, 56, 56, 144, 1, 1, 0, 1),     # 1x1 expansion, K in one step, large grid: 64x64 tiles, no ring
+    (2, 16, 128, 128, 96, 1, 1, 0, 1),    # 1x1 expansion 16 -> 96, large grid: 128x128 tiles, no ring
 ]
 
 
