@@ -161,7 +161,7 @@ struct EpiDev {
   // general step interpreter.
   int32_t fixed;
   int32_t f_mul, f_col, f_full, f_lo, f_hi;
-  int32_t reserved2;
+  int32_t nt_f32;  // f32 results of 256 MiB or more: stored with the non-temporal hint (set by the launcher)
   const float* mul_ptr;
   const float* col_ptr;
   const float* full_ptr;

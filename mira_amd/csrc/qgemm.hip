@@ -712,7 +712,11 @@ __global__ void __launch_bounds__(WM* WN * 64)
           if constexpr (S_F32) {
             const v4i v = {int(__float_as_uint(y[k][0])), int(__float_as_uint(y[k][1])),
                            int(__float_as_uint(y[k][2])), int(__float_as_uint(y[k][3]))};
-            __builtin_amdgcn_raw_buffer_store_b128(v, rf, (lr * int(e.ldo) + col0) * 4, 0, 0);
+            const int off = (lr * int(e.ldo) + col0) * 4;
+            if (e.nt_f32)
+              __builtin_amdgcn_raw_buffer_store_b128(v, rf, off, 0, 2);   // nt
+            else
+              __builtin_amdgcn_raw_buffer_store_b128(v, rf, off, 0, 0);
           }
           if constexpr (S_I8)
             __builtin_amdgcn_raw_buffer_store_b32(quantize4_med3(y[k], e.out_rxs), rq, lr * int(e.ldq) + col0, 0, 0);
@@ -873,6 +877,10 @@ int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int
   int rc = mr::make_epi(epi, N, true, &e);
   if (rc != MR_OK) return rc;
   if (M == 0) return MR_OK;
+  // f32 results larger than the 256 MB Infinity Cache are stored with the
+  // non-temporal hint (MobileNetV2 B=128 112x112 16->96: 152 -> 112 us, and its
+  // depthwise reader 160 -> 128 us); smaller ones stay cached for their reader
+  e.nt_f32 = e.out_f32 != nullptr && M * e.ldo * 4 >= (int64_t(256) << 20);
   mr::GemmArgs g = {};
   g.a = a;
   g.lda = lda;
@@ -930,6 +938,10 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
   if (rc != MR_OK) return rc;
   const int64_t M = int64_t(G.n) * oh * ow;
   if (M == 0) return MR_OK;
+  // f32 results larger than the 256 MB Infinity Cache are stored with the
+  // non-temporal hint (MobileNetV2 B=128 112x112 16->96: 152 -> 112 us, and its
+  // depthwise reader 160 -> 128 us); smaller ones stay cached for their reader
+  e.nt_f32 = e.out_f32 != nullptr && M * e.ldo * 4 >= (int64_t(256) << 20);
   mr::GemmArgs g = {};
   g.a = x;
   g.lda = 0;
