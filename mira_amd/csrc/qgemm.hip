@@ -854,6 +854,19 @@ static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
 
 static bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+// Whether an f32 result goes out with the non-temporal hint.  Results larger than the
+// 256 MB Infinity Cache do (MobileNetV2 B=128 112x112 16->96 expansion: 152 -> 112 us, and
+// the depthwise conv reading it 160 -> 128 us).  So do those of 96 MiB or more whose
+// epilogue adds a residual: a residual block's output, whose f32 copy is next read as the
+// residual two launches later (ResNet-18 B=256 layer 1/2 blocks: the two writers and their
+// residual readers 2-5 us faster each).  Smaller results, and those read by the very next
+// launch (MobileNetV2's 231 MB expansions feeding their depthwise convs), stay cached.
+static bool stream_f32(const EpiDev& e, int64_t M) {
+  if (!e.out_f32) return false;
+  const int64_t bytes = M * e.ldo * 4;
+  return bytes >= (int64_t(256) << 20) || (e.fixed && e.f_full && bytes >= (int64_t(96) << 20));
+}
+
 }  // namespace mr
 
 extern "C" {
@@ -877,10 +890,7 @@ int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int
   int rc = mr::make_epi(epi, N, true, &e);
   if (rc != MR_OK) return rc;
   if (M == 0) return MR_OK;
-  // f32 results larger than the 256 MB Infinity Cache are stored with the
-  // non-temporal hint (MobileNetV2 B=128 112x112 16->96: 152 -> 112 us, and its
-  // depthwise reader 160 -> 128 us); smaller ones stay cached for their reader
-  e.nt_f32 = e.out_f32 != nullptr && M * e.ldo * 4 >= (int64_t(256) << 20);
+  e.nt_f32 = mr::stream_f32(e, M);
   mr::GemmArgs g = {};
   g.a = a;
   g.lda = lda;
@@ -938,10 +948,7 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
   if (rc != MR_OK) return rc;
   const int64_t M = int64_t(G.n) * oh * ow;
   if (M == 0) return MR_OK;
-  // f32 results larger than the 256 MB Infinity Cache are stored with the
-  // non-temporal hint (MobileNetV2 B=128 112x112 16->96: 152 -> 112 us, and its
-  // depthwise reader 160 -> 128 us); smaller ones stay cached for their reader
-  e.nt_f32 = e.out_f32 != nullptr && M * e.ldo * 4 >= (int64_t(256) << 20);
+  e.nt_f32 = mr::stream_f32(e, M);
   mr::GemmArgs g = {};
   g.a = x;
   g.lda = 0;
