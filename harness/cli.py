@@ -136,93 +136,131 @@ def compile_file(path: str, target: str = "cpu", *, entry: str = "main", weights
     return compile_graph(g, target, precision, quantize, calibration, started=t0)
 
 
-# ---------------------------------------------------------------- argument helpers
+# ---------------------------------------------------------------- what a command line asks for
 
-def _dims(items) -> dict:
-    out = {}
-    for it in items or []:
-        k, _, v = it.partition("=")
-        if not v:
-            raise CompileError(f"--dim expects NAME=VALUE, got {it!r}")
-        out[k] = int(v)
-    return out
-
-
-def _shapes(items) -> dict:
-    out = {}
-    for it in items or []:
-        name, _, dims = it.rpartition("=")
-        if not name:
-            raise CompileError(f"--shape expects NAME=D0,D1,..., got {it!r}")
-        out[name] = tuple(int(d) for d in dims.split(",") if d)
-    return out
+def parse_bindings(items, flag: str, value) -> dict:
+    """NAME=VALUE items of a repeatable flag (--dim B=32, --shape x=1,3,224,224) as a dict,
+    each VALUE passed through `value`."""
+    bound = {}
+    for item in items or []:
+        name, sep, text = item.partition("=")
+        if not (name and sep and text):
+            raise CompileError(f"{flag} takes NAME=VALUE items, not {item!r}")
+        bound[name] = value(text)
+    return bound
 
 
-def _load_npz(path) -> dict:
+def _dims_tuple(text: str) -> tuple:
+    return tuple(int(d) for d in text.split(",") if d.strip())
+
+
+def read_arrays(path: Optional[str]) -> dict:
+    """The arrays of an .npz file by name (no file: none)."""
     if not path:
         return {}
-    with np.load(path) as z:
-        return {k: z[k] for k in z.files}
+    with np.load(path, allow_pickle=False) as z:
+        return dict(z.items())
 
 
-def _compile(args, target: str) -> Program:
-    return compile_file(args.file, target, entry=args.entry, weights=_load_npz(args.weights), dims=_dims(args.dim),
-                        seed=args.seed, precision=args.precision, quantize=args.quantize,
-                        input_shapes=_shapes(args.shape))
+def random_feeds(graph: Graph, given: dict, seed: int) -> dict:
+    """Values for the graph inputs: the given ones, and standard-normal draws from one
+    default_rng(seed + 1) stream for the others, in input order -- the inputs MIRA's driver
+    makes up for a run (mira/cli.py:76-80), so the same flags feed the same values."""
+    stream = np.random.default_rng(seed + 1)
+    feeds = {}
+    for v in graph.inputs:
+        feeds[v.name] = given[v.name] if v.name in given else \
+            stream.standard_normal(v.type.shape).astype(v.type.np_dtype)
+    return feeds
 
 
-def _reference(args) -> Program:
-    """The unquantized cpu run of the same program (what --check compares with)."""
-    return compile_file(args.file, "cpu", entry=args.entry, weights=_load_npz(args.weights), dims=_dims(args.dim),
-                        seed=args.seed, input_shapes=_shapes(args.shape))
+def relative_error(out, ref) -> tuple:
+    """(max|out - ref|, max|ref|, their ratio) with MIRA's 1e-12 guard on the peak."""
+    a, b = np.asarray(out, np.float32), np.asarray(ref, np.float32)
+    worst = float(np.abs(a - b).max()) if b.size else 0.0
+    peak = float(np.abs(b).max()) if b.size else 0.0
+    return worst, peak, worst / (peak + 1e-12)
 
 
-def _inputs(prog: Program, path, seed: int) -> dict:
-    given = _load_npz(path)
-    rng = np.random.default_rng(seed + 1)
-    return {v.name: given[v.name] if v.name in given else rng.standard_normal(v.type.shape).astype(v.type.np_dtype)
-            for v in prog.graph.inputs}
+def compare(outs: list, refs: list, tol: float) -> tuple:
+    """Each output against its reference as max|out - ref| / max|ref| (the accuracy check of
+    `run --check`, mira/cli.py:101-111): (every output under tol, one report line each)."""
+    verdicts, lines = [], []
+    for i, (out, ref) in enumerate(zip(outs, refs)):
+        worst, peak, rel = relative_error(out, ref)
+        verdicts.append(rel < tol)
+        lines.append(f"output {i} vs the unquantized cpu run: |err| <= {worst:.3e}, {rel:.3e} of the peak "
+                     f"{peak:.3e} (tol {tol:g})  {'PASS' if verdicts[-1] else 'FAIL'}")
+    return all(verdicts), lines
 
 
-def _rel_err(out, ref) -> tuple:
-    err = float(np.abs(np.asarray(out, np.float32) - np.asarray(ref, np.float32)).max()) if np.size(ref) else 0.0
-    return err, err / (float(np.abs(ref).max()) + 1e-12 if np.size(ref) else 1.0)
+class Invocation:
+    """One command line resolved: the program file and the flags that shape its graph.
+    Builds the program for a target, its unquantized cpu reference (once) and its feeds."""
+
+    def __init__(self, args):
+        self.path = args.file
+        self.entry = args.entry
+        self.seed = args.seed
+        self.weights = read_arrays(args.weights)
+        self.given = read_arrays(getattr(args, "inputs", None))
+        self.dims = parse_bindings(args.dim, "--dim", int)
+        self.shapes = parse_bindings(args.shape, "--shape", _dims_tuple)
+        self.precision = args.precision
+        self.quantize = args.quantize
+        self._ref: Optional[Program] = None
+
+    def program(self, target: str) -> Program:
+        return compile_file(self.path, target, entry=self.entry, weights=self.weights, dims=self.dims,
+                            seed=self.seed, precision=self.precision, quantize=self.quantize,
+                            input_shapes=self.shapes)
+
+    def reference(self) -> Program:
+        """The same program on the cpu target in f32 without quantization."""
+        if self._ref is None:
+            self._ref = compile_file(self.path, "cpu", entry=self.entry, weights=self.weights, dims=self.dims,
+                                     seed=self.seed, input_shapes=self.shapes)
+        return self._ref
+
+    def feeds(self, prog: Program) -> dict:
+        return random_feeds(prog.graph, self.given, self.seed)
+
+
+def _describe(i: int, out: np.ndarray) -> str:
+    head = f"output {i}: {out.dtype}{list(out.shape)}"
+    if out.size:
+        head += f"  min {float(out.min()):.4g}  max {float(out.max()):.4g}  mean {float(out.mean()):.4g}"
+    with np.printoptions(precision=4, suppress=True, threshold=12, edgeitems=3):
+        return head + "\n" + np.array2string(out)
+
+
+def _save(path: str, outs: list) -> None:
+    if len(outs) == 1:
+        np.save(path, outs[0])
+    else:
+        np.savez(path, **{f"output{i}": o for i, o in enumerate(outs)})
 
 
 # ---------------------------------------------------------------- commands
 
 def cmd_run(args) -> int:
-    prog = _compile(args, args.target)
-    feeds = _inputs(prog, args.inputs, args.seed)
+    job = Invocation(args)
+    prog = job.program(args.target)
+    feeds = job.feeds(prog)
     outs = prog.run(feeds)
     print(prog.summary())
-    print(f"wall time {sum(t for _, t in prog.last_timings) * 1e3:.2f} ms")
+    seconds = [t for _, t in prog.last_timings]
+    print(f"ran {len(seconds)} segment(s) in {sum(seconds) * 1e3:.2f} ms")
     for i, out in enumerate(outs):
-        print(f"output {i}: {list(out.shape)} {out.dtype}")
-        with np.printoptions(precision=4, suppress=True, threshold=12, edgeitems=3):
-            print(out)
+        print(_describe(i, out))
     if args.save:
-        if len(outs) > 1:
-            np.savez(args.save, *outs)
-        else:
-            np.save(args.save, outs[0])
+        _save(args.save, outs)
         print(f"saved to {args.save}")
-    if args.check and args.target != "cpu":
-        ok, lines = check_outputs(outs, _reference(args).run(feeds), args.tol)
-        print("\n".join(lines))
-        return 0 if ok else 1
-    return 0
-
-
-def check_outputs(outs: list, refs: list, tol: float) -> tuple:
-    """(all within tol, report lines): max|out - ref| / max|ref| per output."""
-    ok, lines = True, []
-    for i, (out, ref) in enumerate(zip(outs, refs)):
-        err, rel = _rel_err(out, ref)
-        ok &= rel < tol
-        lines.append(f"check output {i} vs cpu reference: max abs err {err:.3e}, relative {rel:.3e}  ->  "
-                     f"{'PASS' if rel < tol else 'FAIL'}")
-    return ok, lines
+    if not args.check or args.target == "cpu":
+        return 0
+    ok, lines = compare(outs, job.reference().run(feeds), args.tol)
+    print("\n".join(lines))
+    return 0 if ok else 1
 
 
 def _format_dim(d) -> str:
@@ -279,7 +317,7 @@ def cmd_emit(args) -> int:
         except mira_lang.MiraSyntaxError as err:
             raise CompileError(f"{args.file}: {err}") from None
         return 0
-    prog = _compile(args, args.target)
+    prog = Invocation(args).program(args.target)
     if args.stage == "ir":
         print(prog.ir_text)
     elif args.stage == "opt":
@@ -291,32 +329,40 @@ def cmd_emit(args) -> int:
     return 0
 
 
+def _timed_runs(prog: Program, feeds: dict, n: int) -> np.ndarray:
+    seconds = np.empty(n)
+    for i in range(n):
+        t0 = time.perf_counter()
+        prog.run(feeds)
+        seconds[i] = time.perf_counter() - t0
+    return seconds
+
+
 def cmd_bench(args) -> int:
-    feeds, ref = None, None
-    print(f"{'target':<10} {'compile':>9} {'median':>10} {'min':>10}   {'rel err':>9}  segments")
-    for t in args.targets.split(","):
-        prog = _compile(args, t)
-        if feeds is None:
-            feeds = _inputs(prog, args.inputs, args.seed)
-        out = prog.run(feeds)[0]                  # warm-up, and the output checked
-        if ref is None:
-            ref = _reference(args).run(feeds)[0]
-        times = []
-        for _ in range(args.iters):
-            t0 = time.perf_counter()
-            prog.run(feeds)
-            times.append(time.perf_counter() - t0)
-        _, rel = _rel_err(out, ref)
-        segs = "+".join(s.device for s in prog.segments)
-        print(f"{t:<10} {prog.compile_seconds:8.2f}s {np.median(times) * 1e3:8.3f}ms {min(times) * 1e3:8.3f}ms"
-              f"   {rel:9.2e}  {segs}")
+    """Each target in turn: compile, one checked warm-up run, then `--iters` timed runs on the
+    same feeds; the first output's error is against the unquantized cpu run."""
+    job = Invocation(args)
+    rows, feeds, ref = [], None, None
+    for target in [t for t in args.targets.split(",") if t]:
+        prog = job.program(target)
+        feeds = feeds if feeds is not None else job.feeds(prog)
+        first = prog.run(feeds)[0]
+        ref = ref if ref is not None else job.reference().run(feeds)[0]
+        rel = relative_error(first, ref)[2]
+        t = _timed_runs(prog, feeds, args.iters) * 1e3
+        rows.append((target, prog.compile_seconds, float(np.median(t)), float(t.min()), rel,
+                     "+".join(s.device for s in prog.segments)))
+    head = ("target", "compile s", "median ms", "best ms", "rel err", "segments")
+    print("  ".join(f"{h:>10}" for h in head))
+    for target, comp, med, best, rel, segs in rows:
+        print(f"{target:>10}  {comp:>10.2f}  {med:>10.3f}  {best:>10.3f}  {rel:>10.2e}  {segs:>10}")
     return 0
 
 
 def cmd_check(args) -> int:
-    g = _compile(args, "cpu").graph
-    ins = ", ".join(f"{v.name}: {v.type}" for v in g.inputs)
-    print(f"ok: {args.file}  inputs ({ins}) -> {g.outputs[0].type}, {len(g.compute_ops())} ops")
+    g = Invocation(args).program("cpu").graph
+    sig = ", ".join(f"{v.name}: {v.type}" for v in g.inputs)
+    print(f"ok: {args.file}  inputs ({sig}) -> {g.outputs[0].type}, {len(g.compute_ops())} ops")
     return 0
 
 

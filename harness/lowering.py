@@ -6,7 +6,7 @@ epilogue fusion, then the W8A8 (or weight-only int8) rewrite.  The tests and
 the benchmark need the same graphs without MIRA, so this module produces
 them.  What it must agree with MIRA on is the *result* -- which ops exist,
 the epilogue step tuples, the q-op attrs -- and that is checked against
-MIRA's own output for its programs (tests/golden, tests/test_harness.py).
+MIRA's own output for its programs (tests/golden, tests/test_mira_golden.py).
 The attr names and the step tuple format are MIRA's interface:
 
     qmatmul / qconv2d attrs: q (int8), w_scale (f32 per output channel),

@@ -161,7 +161,8 @@ struct EpiDev {
   // general step interpreter.
   int32_t fixed;
   int32_t f_mul, f_col, f_full, f_lo, f_hi;
-  int32_t nt_f32;  // f32 results of 256 MiB or more: stored with the non-temporal hint (set by the launcher)
+  int32_t nt_f32;  // f32 results stored with the non-temporal hint (set by the launcher: results of 256 MiB
+                  // or more, and fixed-form results with a residual of 96 MiB or more; qgemm.hip stream_f32)
   const float* mul_ptr;
   const float* col_ptr;
   const float* full_ptr;

@@ -974,12 +974,15 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
   g.row_bytes = row_bytes;
   g.k_real = k_real;
   g.cb_per_tap = G.c_pad / 64;
-  MR_REQUIRE(int64_t(G.n) * G.h * G.w * G.c_pad < (int64_t(1) << 31) && k_pad * n_pad < (int64_t(1) << 31),
-             "mr_qconv2d: operands of 2 GiB or more are not supported (32-bit buffer offsets)");
-  g.a_bytes = static_cast<uint32_t>(int64_t(G.n) * G.h * G.w * G.c_pad);
+  MR_REQUIRE(k_pad * n_pad < (int64_t(1) << 31),
+             "mr_qconv2d: packed weights of 2 GiB or more are not supported (32-bit buffer offsets)");
+  const int64_t a_bytes = int64_t(G.n) * G.h * G.w * G.c_pad;
+  g.a_bytes = static_cast<uint32_t>(std::min(a_bytes, int64_t(0x7fffffff)));
   g.b_bytes = static_cast<uint32_t>(k_pad * n_pad);
   // a 1x1 stride-1 unpadded convolution reads each output pixel's own input row: it is the
-  // dense GEMM [n*h*w, c_pad] x [c_pad, o] over the NHWC rows (K past c_pad reads zeros)
+  // dense GEMM [n*h*w, c_pad] x [c_pad, o] over the NHWC rows.  Its K runs to k_pad, past
+  // c_pad when c_pad % 64 != 0: those bytes belong to the next pixel's row, and the
+  // products vanish only because packed weights are zero for k >= kh*kw*c_pad
   if (mode != mr::A_CONV4 && G.kh == 1 && G.kw == 1 && G.sh == 1 && G.sw == 1 && G.ph == 0 && G.pw == 0) {
     g.lda = G.c_pad;
     mode = mr::A_DENSE;
@@ -1009,6 +1012,10 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
       mode = mr::A_PATCH;
     }
   }
+  // the dense and 64-channel loaders read A through a buffer resource (32-bit offsets); the
+  // others form 64-bit addresses
+  MR_REQUIRE((mode != mr::A_DENSE && mode != mr::A_CONV64) || a_bytes < (int64_t(1) << 31),
+             "mr_qconv2d: an int8 input of 2 GiB or more is not supported by this loader (32-bit buffer offsets)");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (mode) {
     case mr::A_PATCH: return mr::launch<mr::A_PATCH>(g, e, s);

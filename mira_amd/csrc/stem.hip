@@ -115,7 +115,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
   // thread; each writes its plane's 4 bytes, so the ring is zeroed once and
   // channel bytes past C stay 0.  Loads and stores are issued without branches
   // (a store with nothing to write goes to a sink byte), so every load of a
-  // batch is in flight at once.  The image is under 2 GiB (host).
+  // batch is in flight at once.  One image is under 2 GiB (checked on the host).
   extern __shared__ int32_t xin[];
   __shared__ int32_t sink[64];
   const int ih_first = cr_first * a.SH - a.PH;
@@ -654,6 +654,9 @@ int mr_qconv2d_maxpool_f32in(const float* x, float x_scale, int32_t round_f16, c
   const int rc = mr::stem_setup("mr_qconv2d_maxpool_f32in", cg, b, k_pad, n_pad, epi, pool_size, pool_stride,
                                 pool_pad_top, pool_pad_left, pad_value, poh, pow_, &a, &e, &pool3);
   if (rc != MR_OK) return rc;
+  // one image's f32 planes are read through a buffer resource with 32-bit byte offsets
+  MR_REQUIRE(int64_t(a.C) * a.H * a.W * 4 < (int64_t(1) << 31),
+             "mr_qconv2d_maxpool_f32in: an f32 image of 2 GiB or more is not supported");
   if (a.KH != 7 || a.KW < 5 || a.DH != 1 || a.DW != 1 || a.SW % 2 != 0) {
     mr::set_error("mr_qconv2d_maxpool_f32in: needs a 7-row kernel of 5 to 8 taps, no dilation and an even column "
                   "stride (got %dx%d, stride %d, dilation %dx%d)", a.KH, a.KW, a.SW, a.DH, a.DW);

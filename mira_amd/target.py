@@ -132,6 +132,11 @@ def _ptr(t) -> int:
     return 0 if t is None else t.data_ptr()
 
 
+# Longest contraction whose int32 accumulator cannot overflow: K * 127 * 127 < 2^31
+# (the library rejects longer ones).
+MAX_EXACT_K = 133144
+
+
 class RocmTarget:
     """MIRA Target for one MI355X (gfx950)."""
     name = "rocm"
@@ -162,6 +167,9 @@ class RocmTarget:
         if k in ("qmatmul", "qconv2d"):
             if k == "qconv2d" and op.attrs.get("groups", 1) != 1:
                 return "grouped int8 convolution has no kernel"
+            why = self._check_q_sizes(op)
+            if why is not None:
+                return why
             return self._check_epilogue(op, op.result.type.shape, k == "qconv2d")
         if k == "conv2d":
             x, w = op.inputs[0], op.inputs[1]
@@ -208,6 +216,36 @@ class RocmTarget:
                 return self._check_w8_matmul(op)
             return self._check_f32_matmul(op)
         return f"'{k}' has no rocm kernel"
+
+    @staticmethod
+    def _check_q_sizes(op: "Op") -> Optional[str]:
+        """The limits of the int8 contraction kernels, so an op past them stays on the CPU
+        instead of failing at launch: their buffer loads take 32-bit byte offsets (int8
+        activations and packed weights under 2 GiB) and they index pixels with int32."""
+        q = op.attrs["q"]
+        k_real = int(np.prod(q.shape, dtype=np.int64)) // q.shape[1 if op.kind == "qmatmul" else 0]
+        if k_real > MAX_EXACT_K:
+            return f"contraction length {k_real} > {MAX_EXACT_K}: the int32 accumulator could overflow"
+        if op.kind == "qmatmul":
+            K, N = q.shape
+            rows = int(np.prod(op.inputs[0].type.shape[:-1], dtype=np.int64))
+            if rows > 8 and rows * pack.row_stride_for(K) >= 2 ** 31:
+                return "int8 matmul: an activation of 2 GiB or more"
+            k_pad, n_pad = pack.roundup(K, pack.K_STEP), pack.roundup(N, pack.N_STEP)
+        else:
+            o, c, kh, kw = q.shape
+            n, _, h, w = op.inputs[0].type.shape
+            _, oh, ow = op.result.type.shape[1:]
+            cp = pack.c_pad_for(c)
+            if n * h * w >= 2 ** 31 or n * oh * ow >= 2 ** 31:
+                return "int8 convolution: 2^31 pixels or more"
+            if n * h * w * cp >= 2 ** 31:
+                return "int8 convolution: an int8 input of 2 GiB or more"
+            k = kh * (pack.conv_row_bytes(kw) if cp == 4 else kw * cp)
+            k_pad, n_pad = pack.roundup(k, pack.K_STEP), pack.roundup(o, pack.N_STEP)
+        if k_pad * n_pad >= 2 ** 31:
+            return "int8 weights of 2 GiB or more"
+        return None
 
     def _check_f32_matmul(self, op: "Op") -> Optional[str]:
         """matmul of two float tensors (attention scores and context): mr_bmm_f32 in the

@@ -29,7 +29,7 @@ def test_program_bit_exact(name, dims, precision):
     assert "qmatmul" in on_rocm and ("qconv2d" in on_rocm) == name.startswith("conv")
     f16 = [op for op in prog.graph.compute_ops() if op.result.type.dtype == "f16"]
     assert bool(f16) == (precision == "auto")
-    feeds = cli._inputs(prog, None, 0)
+    feeds = cli.random_feeds(prog.graph, {}, 0)
     print(f"{name} precision={precision}", flush=True)
     (got,) = prog.run(feeds)
     want = oracle_env(prog.graph, feeds)[prog.graph.outputs[0]]

@@ -147,6 +147,34 @@ def test_qmatmul_every_epilogue_step(lib, M):
     assert bits_equal(y, want)
 
 
+@pytest.mark.parametrize("M,K", [(300, 80), (5, 80), (300, 16)])
+def test_qmatmul_row_tail_past_k_is_not_read_as_data(lib, M, K):
+    """lda < k_pad: the dense loader's K runs to k_pad, past each row's K bytes into the
+    next row.  Those bytes are nonzero here; the packed weights are zero for k >= K (the
+    packing contract), so the accumulators still equal the oracle's."""
+    torch = _torch()
+    rng = np.random.default_rng(M + K)
+    N = 40
+    xq = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    q = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    lda = pack.row_stride_for(K)
+    bl = pack.pack_matmul(q)
+    assert lda < bl.shape[1]
+    rows = rng.integers(-127, 128, (M, lda)).astype(np.int8)      # bytes K..lda-1 nonzero
+    rows[:, :K] = xq
+    ws = np.full(N, 0.01, np.float32)
+    attrs = {"q": q, "w_scale": ws, "x_scale": 1.0, "dtype": "f32", "epilogue": ()}
+    want = G.qmatmul_acc(xq.astype(np.float32), attrs).astype(np.int32)
+    acc = empty((M, N), torch.int32)
+    y = empty((M, N), torch.float32)
+    xd, bd, sc = T(rows), T(pack.device_weights(bl)), T(pack.combined_scale(1.0, ws))
+    e = epilogue([], scale=sc, out_f32=y, ldo=N, out_acc=acc, ldacc=N)
+    L.check(lib.mr_qmatmul(xd.data_ptr(), lda, bd.data_ptr(), bl.shape[1], bl.shape[0], M, N, K, C.byref(e),
+                           stream()), "mr_qmatmul")
+    sync()
+    assert np.array_equal(acc.cpu().numpy(), want)
+
+
 def test_qmatmul_rejects_bad_shapes(lib):
     torch = _torch()
     a = empty((4, 16), torch.int8)

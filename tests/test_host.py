@@ -408,3 +408,36 @@ def test_division_magic_is_exact():
         nmax = (1 << 32) // d - 1
         n = np.concatenate([np.arange(min(nmax, 4096)), rng.integers(0, nmax, 4096), [nmax]]).astype(np.uint64)
         assert np.array_equal((n * np.uint64(m)) >> np.uint64(32), n // np.uint64(d))
+
+
+def test_check_rejects_int8_operands_past_the_kernel_limits():
+    """An int8 activation or packed weight of 2 GiB or more, or 2^31 pixels, stays on the CPU
+    (the contraction kernels use 32-bit buffer offsets and int32 pixel indices) instead of
+    failing at launch; the same shapes one size down run on rocm."""
+    t = RocmTarget()
+
+    from harness.graph import Op, TensorType, Value
+
+    def q_op(kind, xshape, yshape, q, **conv):
+        attrs = {"q": q, "w_scale": np.ones(q.shape[0 if conv else 1], np.float32), "x_scale": 1.0,
+                 "dtype": "f32", "epilogue": (), **conv}
+        return Op(kind, [Value(TensorType("f32", xshape))], attrs, [Value(TensorType("f32", yshape))])
+
+    def qmm(rows, K, N):
+        # the shapes only: an int8 weight of the right shape, with strides of 0 (no memory)
+        q = np.lib.stride_tricks.as_strided(np.zeros(1, np.int8), (K, N), (0, 0))
+        return q_op("qmatmul", (rows, K), (rows, N), q)
+
+    def qconv(n, c, hw, o=8):
+        return q_op("qconv2d", (n, c, hw, hw), (n, o, hw, hw), np.zeros((o, c, 3, 3), np.int8),
+                    stride=(1, 1), padding=(1, 1), dilation=(1, 1), groups=1)
+
+    assert t.check(qmm(2 ** 31 // 64 - 1, 64, 16)) is None
+    assert "2 GiB" in t.check(qmm(2 ** 31 // 64, 64, 16))
+    assert t.check(qmm(8, 133144, 16)) is None
+    assert "overflow" in t.check(qmm(8, 133145, 16))        # K * 127^2 reaches 2^31
+    assert t.check(qmm(16, 2 ** 17, 2 ** 14 - 32)) is None
+    assert "weights of 2 GiB" in t.check(qmm(16, 2 ** 17, 2 ** 14))
+    assert t.check(qconv(1024, 64, 180)) is None            # 2.12e9 bytes, under 2^31
+    assert "2 GiB" in t.check(qconv(1024, 64, 200))
+    assert "pixels" in t.check(qconv(2 ** 16, 4, 256))

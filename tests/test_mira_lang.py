@@ -242,12 +242,29 @@ def test_cli_run_save_weights_inputs(tmp_path, capsys):
     assert {op.kind for op in prog.graph.ops} >= {"qconv2d", "qmatmul"}
 
 
-def test_check_outputs():
+def test_compare_outputs():
+    """--check's measure: max|out - ref| / max|ref| against the tolerance, per output."""
     ref = np.array([[0.5, -2.0], [1.0, 0.0]], np.float32)
-    ok, lines = cli.check_outputs([ref + 0.039], [ref], 2e-2)
+    ok, lines = cli.compare([ref + 0.039], [ref], 2e-2)
     assert ok and "PASS" in lines[0]
-    ok, lines = cli.check_outputs([ref, ref + np.float32(0.041)], [ref, ref], 2e-2)
-    assert not ok and "PASS" in lines[0] and "FAIL" in lines[1] and "relative 2.05" in lines[1]
+    ok, lines = cli.compare([ref, ref + np.float32(0.041)], [ref, ref], 2e-2)
+    assert not ok and "PASS" in lines[0] and "FAIL" in lines[1] and "2.050e-02 of the peak" in lines[1]
+    assert cli.relative_error(ref + 0.5, ref)[2] == pytest.approx(0.25)
+    assert cli.relative_error(np.zeros(0), np.zeros(0)) == (0.0, 0.0, 0.0)
+
+
+def test_random_feeds_follow_the_seed_rule():
+    """Inputs not given are standard-normal draws of one default_rng(seed + 1) stream in input
+    order; a given input takes no draw."""
+    g = ML.elaborate(_read(MLP), dims={"B": 3})
+    (x,) = g.inputs
+    feeds = cli.random_feeds(g, {}, 4)
+    assert np.array_equal(feeds[x.name], np.random.default_rng(5).standard_normal(x.type.shape).astype(np.float32))
+    given = np.ones(x.type.shape, np.float32)
+    assert cli.random_feeds(g, {x.name: given}, 4)[x.name] is given
+    assert cli.parse_bindings(["B=3", "x=1,2"], "--dim", str) == {"B": "3", "x": "1,2"}
+    with pytest.raises(cli.CompileError, match="NAME=VALUE"):
+        cli.parse_bindings(["B"], "--dim", int)
 
 
 def test_cli_bench_and_errors(tmp_path, capsys):
