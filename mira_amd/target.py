@@ -461,6 +461,8 @@ class RocmExecutable:
             for v in {src[0], conv.inputs[0]}:
                 self.need_i8[v] = [s for s in self.need_i8.get(v, []) if s != xs]
         self.staging: dict["Value", object] = {}
+        self._pinned: dict["Value", object] = {}     # pinned host buffers of upload()
+        self._upload_done = None                     # event after upload()'s last DMA
         self.canon: dict["Value", object] = {}     # C-order copies of NHWC values (_c_order)
         self._plan_views()
         for v in g.inputs:
@@ -1350,12 +1352,40 @@ class RocmExecutable:
 
     # ---------------------------------------------------------------- run
 
+    # bytes per host -> device chunk: the next chunk's copy into pinned memory overlaps the
+    # previous chunk's DMA
+    UPLOAD_CHUNK = 32 << 20
+
     def upload(self, feeds: dict) -> None:
-        """Copy the segment inputs (host arrays, the graph's layout) into their device buffers."""
+        """Copy the segment inputs (host arrays, the graph's layout) into their device buffers,
+        through pinned host buffers allocated on first use and kept with the executable: the
+        arrays are copied into them in chunks by torch's multi-threaded CPU copy, and each
+        chunk's DMA is queued on the current stream as soon as it is there."""
         torch = _t()
+        stream = torch.cuda.current_stream(self.dev)
+        if self._upload_done is not None:
+            self._upload_done.synchronize()       # the pinned buffers are free again
         for v in self.g.inputs:
-            arr = np.ascontiguousarray(np.asarray(feeds[v]).astype(np.float32)).reshape(v.type.shape)
-            self.staging[v].copy_(torch.from_numpy(arr), non_blocking=False)
+            arr = np.ascontiguousarray(np.asarray(feeds[v], dtype=np.float32)).reshape(-1)
+            if arr.size != v.type.numel:
+                raise ValueError(f"input {v}: {arr.size} elements for {v.type}")
+            pin = self._pinned.get(v)
+            if pin is None:
+                pin = self._pinned[v] = torch.empty(v.type.numel, dtype=torch.float32, pin_memory=True)
+            src = torch.from_numpy(arr)
+            stage = self.staging[v]
+            if not stage.is_contiguous():     # a slice of a concat's buffer: one strided copy
+                pin.copy_(src)
+                stage.copy_(pin.view(v.type.shape), non_blocking=True)
+                continue
+            dst = stage.view(-1)
+            step = max(self.UPLOAD_CHUNK // 4, 1)
+            for a in range(0, arr.size, step):
+                b = min(a + step, arr.size)
+                pin[a:b].copy_(src[a:b])
+                dst[a:b].copy_(pin[a:b], non_blocking=True)
+        self._upload_done = torch.cuda.Event()
+        self._upload_done.record(stream)
 
     def device_input(self, v: "Value"):
         """The device f32 buffer (graph layout) that `launch` reads segment input v from."""

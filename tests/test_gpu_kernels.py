@@ -720,7 +720,8 @@ def test_qmatmul_epilogue_forms(lib, form, M, K, N):
     y = empty((M, N), torch.float32) if want_f32 else None
     ldq = pack.row_stride_for(N)
     yq = empty((M, ldq), torch.int8) if want_i8 else None
-    e = epilogue(dev_steps, scale=T(pack.combined_scale(xs, ws)), out_f32=y, ldo=N if want_f32 else 0, out_i8=yq,
+    sc = T(pack.combined_scale(xs, ws))        # named: kept alive until the kernel has run
+    e = epilogue(dev_steps, scale=sc, out_f32=y, ldo=N if want_f32 else 0, out_i8=yq,
                  ldq=ldq if want_i8 else 0, xs=next_xs)
     L.check(lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), bl.shape[1], bl.shape[0], M, N, K, C.byref(e), stream()),
             "mr_qmatmul")
@@ -1017,7 +1018,8 @@ def test_int8_epilogue_ties(lib, kind, shape, lines_kind):
     odd = (acc.astype(np.int64) % 2 != 0) & (want > 0) & (want < 127 * next_xs)
     assert odd.mean() > 0.15                      # plenty of exact ties in range
     yq = empty((rows, ocp), torch.int8)
-    e = epilogue([("add", L.BC_COL, T(bias), 0, False), ("relu", 0, None, 0, False)], scale=scale, out_i8=yq,
+    bd = T(bias)        # named: a temporary's memory could be reused (by the lines) before the kernel runs
+    e = epilogue([("add", L.BC_COL, bd, 0, False), ("relu", 0, None, 0, False)], scale=scale, out_i8=yq,
                  ldq=ocp, xs=next_xs)
     if lines_kind:
         k_real = K if kind == "matmul" else c * k * k

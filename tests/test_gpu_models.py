@@ -175,7 +175,7 @@ def test_resnet18_batch2_fused_stem(bn_epilogue, precision):
 
 # ---------------------------------------------------------------- C4 MobileNetV2
 
-@pytest.mark.parametrize("builder,min_lines", [(models.resnet18, 8), (models.mobilenet_v2, 4)])
+@pytest.mark.parametrize("builder,min_lines", [(models.resnet18, 8), (models.mobilenet_v2, 2)])
 def test_requant_lines_in_the_networks(builder, min_lines):
     """The production target gives the int8-only conv epilogues (ResNet-18's first conv of
     each block and its downsamples, MobileNetV2's projections) integer requantization
