@@ -102,15 +102,11 @@ def build_workload(name: str, batch: int):
     return g, gen(g.inputs[0].type.shape, 7)
 
 
-# RocmTarget options of the timed executables (--no-lines: int8 epilogues on the float chain)
-TARGET_OPTIONS: dict = {}
-
-
 def single_segment(g):
     """Compile g on the rocm target; every op must run there (one segment)."""
     from harness.runner import Runner
     from mira_amd.target import RocmTarget
-    runner = Runner(g, RocmTarget(**TARGET_OPTIONS))
+    runner = Runner(g, RocmTarget())
     if runner.devices != ["rocm"]:
         raise SystemExit(f"{g.name}: expected one rocm segment, got {runner.devices}")
     return runner.executables("rocm")[0]
@@ -564,8 +560,6 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=256, help="gpt-decode: tokens generated per sequence")
     ap.add_argument("--per-launch", action="store_true", help="per-launch time against each launch's roofline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-lines", action="store_true",
-                    help="int8-only epilogues evaluate the float chain instead of requantization lines")
     ap.add_argument("--copy-calibration", action="store_true", help="run the plain copy used to scale counters")
     ap.add_argument("--summarize-counters", metavar="DIR", help="summarize rocprofv3 --pmc CSV output in DIR")
     ap.add_argument("--summarize-mfma", metavar="DIR", help="MFMA utilisation from rocprofv3 --pmc CSV output in DIR/mfma")
@@ -584,8 +578,6 @@ def main() -> int:
         print("bench.py measures one GPU: the rocm target has no multi-GPU path (the batch would shard "
               "by data parallelism, one share per GPU). Run with --gpus 1.", file=sys.stderr)
         return 2
-    if args.no_lines:
-        TARGET_OPTIONS["requant_lines"] = False
     if args.batch is None:
         args.batch = {"resnet18": 256, "resnet18-onnx": 256, "resnet18-f16": 256, "mlp50m": 1, "mlp50m-int8": 1,
                       "mobilenetv2": 128, "gpt-decode": 1}[args.workload]

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MR_ABI_VERSION 8
+#define MR_ABI_VERSION 7
 
 enum mr_status {
   MR_OK = 0,
@@ -94,24 +94,6 @@ typedef struct mr_epi_step {
  *   out_acc[row*ldacc+col] = acc            (int32 accumulator, if out_acc) */
 #define MR_EPI_OUT_F16 1
 
-/* Integer requantization line of one output column, for an epilogue whose only
- * output is out_i8 (mr_epilogue.lines).  The int8 result is then
- *   r = acc * m + c                          (int64)
- *   q = clamp(r >> 32, lo, hi)               unless (uint32)r < w,
- * where the kernel evaluates the epilogue above instead.  The caller computes the
- * lines so that this equals the epilogue for every accumulator the contraction
- * can produce (|acc| <= K * 127^2): the int8 result of a per-column epilogue of
- * non-decreasing steps is a non-decreasing step function of acc, the line matches
- * its thresholds, and the window w covers every accumulator where it does not
- * (those lie next to a crossing of the line).  m >= 0, |c| < 2^62. */
-typedef struct mr_requant_line {
-  int64_t c;
-  int32_t m;
-  uint32_t w;
-  int32_t lo, hi;
-  int64_t reserved;
-} mr_requant_line;
-
 typedef struct mr_epilogue {
   int32_t n_steps;
   int32_t flags;      /* MR_EPI_OUT_F16 or 0 */
@@ -125,10 +107,6 @@ typedef struct mr_epilogue {
   int32_t reserved1;
   int32_t* out_acc;
   int64_t ldacc;
-  /* NULL, or one line per column (see mr_requant_line): allowed only with out_i8
-   * and without out_f32 / out_acc; kernels without a line form ignore it and
-   * evaluate the epilogue, with the same result */
-  const mr_requant_line* lines;
 } mr_epilogue;
 
 /* Geometry of an NHWC convolution (mira/ops.py:225-276 conv_params/_conv2d_infer).

@@ -10,7 +10,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "libmira_rocm.so"
-ABI_VERSION = 8
+ABI_VERSION = 7
 MAX_EPI = 8
 
 # enum mr_epi_fn
@@ -42,13 +42,7 @@ class Epilogue(C.Structure):
     _fields_ = [("n_steps", C.c_int32), ("flags", C.c_int32), ("steps", EpiStep * MAX_EPI),
                 ("scale", C.c_void_p), ("out_f32", C.c_void_p), ("ldo", C.c_int64),
                 ("out_i8", C.c_void_p), ("ldq", C.c_int64), ("out_xs", C.c_float), ("reserved1", C.c_int32),
-                ("out_acc", C.c_void_p), ("ldacc", C.c_int64), ("lines", C.c_void_p)]
-
-
-class RequantLine(C.Structure):
-    """mr_requant_line; mira_amd.requant.LINE_DTYPE has the same layout."""
-    _fields_ = [("c", C.c_int64), ("m", C.c_int32), ("w", C.c_uint32), ("lo", C.c_int32), ("hi", C.c_int32),
-                ("reserved", C.c_int64)]
+                ("out_acc", C.c_void_p), ("ldacc", C.c_int64)]
 
 
 class ConvGeom(C.Structure):
@@ -118,8 +112,7 @@ def load(path: Optional[Path] = None) -> C.CDLL:
         fn.restype = res
     if lib.mr_abi_version() != ABI_VERSION:
         raise RocmError(f"{p}: ABI version {lib.mr_abi_version()} != {ABI_VERSION}")
-    for name, cls in (("mr_epi_step", EpiStep), ("mr_epilogue", Epilogue), ("mr_conv_geom", ConvGeom),
-                      ("mr_requant_line", RequantLine)):
+    for name, cls in (("mr_epi_step", EpiStep), ("mr_epilogue", Epilogue), ("mr_conv_geom", ConvGeom)):
         if lib.mr_sizeof(name.encode()) != C.sizeof(cls):
             raise RocmError(f"{p}: sizeof({name}) {lib.mr_sizeof(name.encode())} != binding {C.sizeof(cls)}")
     _lib = lib

@@ -39,11 +39,6 @@ int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out)
     MR_REQUIRE(need_scale, "int32 accumulators exist only for int8 contractions");
     MR_REQUIRE(epi->ldacc >= cols, "ldacc < cols");
   }
-  if (epi->lines) {
-    MR_REQUIRE(need_scale && epi->out_i8 && !epi->out_f32 && !epi->out_acc,
-               "requantization lines need an int8-only epilogue of an int8 contraction");
-    MR_REQUIRE(reinterpret_cast<uintptr_t>(epi->lines) % 16 == 0, "requantization lines must be 16-byte aligned");
-  }
   std::memset(out, 0, sizeof(*out));
   out->n_steps = epi->n_steps;
   out->has_scale = epi->scale != nullptr;
@@ -73,7 +68,6 @@ int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out)
   out->out_acc = epi->out_acc;
   out->ldacc = epi->ldacc;
   out->out_rxs = epi->out_i8 ? 1.0 / static_cast<double>(epi->out_xs) : 0.0;
-  out->lines = epi->lines;
   // recognise the fixed form  mul(col)? add(col)? add(full)? max(scalar)|relu? min(scalar)?
   int stage = 0;
   bool fixed = true;
@@ -131,7 +125,6 @@ int64_t mr_sizeof(const char* name) {
   if (!std::strcmp(name, "mr_epi_step")) return sizeof(mr_epi_step);
   if (!std::strcmp(name, "mr_epilogue")) return sizeof(mr_epilogue);
   if (!std::strcmp(name, "mr_conv_geom")) return sizeof(mr_conv_geom);
-  if (!std::strcmp(name, "mr_requant_line")) return sizeof(mr_requant_line);
   return -1;
 }
 

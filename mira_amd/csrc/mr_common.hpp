@@ -169,7 +169,6 @@ struct EpiDev {
   int64_t full_ld;
   const float* lo_ptr;  // NULL with f_lo set: relu (maximum with +0)
   const float* hi_ptr;
-  const mr_requant_line* lines;  // int8-only epilogues: per-column integer requantization lines
 };
 
 // NumPy's maximum(y, b) / minimum(y, b) for a bound b that is the same for the
@@ -278,9 +277,6 @@ constexpr int EF_GENERIC = 0, EF_FIXED = 1, EF_SPEC = 0x100;
 constexpr int SF_COL = 1, SF_FULL = 2, SF_LO = 4, SF_HI = 8, SF_F32 = 16, SF_I8 = 32;
 constexpr int SF_MUL = 64;   // no compiled form has it: a leading mul runs the EF_FIXED path
 constexpr int SF_F16 = 128;  // results rounded to f16 (compiled for the ResNet-style forms only)
-// int8 result from the per-column integer lines (mr_requant_line), the epilogue's float
-// chain only for the accumulators in a line's flag window; int8-only forms
-constexpr int SF_LINE = 512;
 // the forms with compiled kernels: bias+ReLU -> int8; bias+residual+ReLU -> f32
 // and/or int8; bias -> f32 (ResNet blocks, downsample and fc layers, MLPs)
 constexpr int SPEC_RELU_I8 = SF_COL | SF_LO | SF_I8;
@@ -325,7 +321,6 @@ inline int spec_form(const EpiDev& e) {
     if (!al(e.out_i8, e.ldq, 4)) return -1;
     f |= SF_I8;
   }
-  if (e.lines) f |= SF_LINE;
   return f;
 }
 

@@ -631,24 +631,6 @@ __global__ void __launch_bounds__(WM* WN * 64)
   const int col0 = n0 + cgi * 4;
   EpiCols4 cols;
   load_cols4(e, col0, g.N, cols);
-  // int8-only compiled forms with requantization lines: the lines of the thread's 4 columns
-  constexpr bool S_LINE = (EF & SF_LINE) != 0;
-  int64_t ln_c[4] = {0, 0, 0, 0};
-  int32_t ln_m[4] = {0, 0, 0, 0}, ln_lo[4] = {0, 0, 0, 0}, ln_hi[4] = {0, 0, 0, 0};
-  uint32_t ln_w[4] = {0, 0, 0, 0};
-  if constexpr (S_LINE) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (col0 + c < g.N) {
-        const mr_requant_line& ln = e.lines[col0 + c];
-        ln_c[c] = ln.c;
-        ln_m[c] = ln.m;
-        ln_w[c] = ln.w;
-        ln_lo[c] = ln.lo;
-        ln_hi[c] = ln.hi;
-      }
-    }
-  }
 
 #pragma unroll
   for (int pass = 0; pass < FM; ++pass) {
@@ -705,36 +687,6 @@ __global__ void __launch_bounds__(WM* WN * 64)
           const int rr = threadIdx.x / CG + (k0 + k) * RSTEP;
           local[k] = (rr >> 5) * TM + pass * 32 + (rr & 31);
           a[k] = *reinterpret_cast<const v4i*>(ep + rr * EP_LD + cgi * 4);
-        }
-        if constexpr (S_LINE) {
-          static_assert(S_I8 && !S_F32 && !S_FULL, "requantization lines: int8-only forms");
-          // the float chain of one output, for the accumulators in a line's window (rare):
-          // its per-column constants are read here rather than held in registers
-          auto chain_q = [&](int32_t acc, int col) __attribute__((always_inline)) {
-            float t = dequant(acc, e.scale[col]);
-            if constexpr (S_COL) t = __fadd_rn(t, e.col_ptr[col]);
-            if constexpr (S_LO) t = max_bound(t, cols.lo, cols.lo_nan);
-            if constexpr (S_HI) t = min_bound(t, cols.hi, cols.hi_nan);
-            if constexpr (S_F16) t = round_f16(t);
-            return quantize_med3(t, e.out_rxs);
-          };
-#pragma unroll
-          for (int k = 0; k < NRC; ++k) {
-            uint32_t b[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              const int64_t r = int64_t(a[k][c]) * ln_m[c] + ln_c[c];
-              int q = min(max(static_cast<int>(r >> 32), ln_lo[c]), ln_hi[c]);
-              if (__builtin_expect(static_cast<uint32_t>(r) < ln_w[c], 0)) q = chain_q(a[k][c], rcol + c);
-              b[c] = static_cast<uint32_t>(q);
-            }
-            const uint32_t lo2 = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u);
-            const uint32_t hi2 = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
-            if (cok)
-              __builtin_amdgcn_raw_buffer_store_b32(__builtin_amdgcn_perm(hi2, lo2, 0x05040100u), rq,
-                                                    local[k] * int(e.ldq) + col0, 0, 0);
-          }
-          continue;
         }
         float y[NRC][4];
 #pragma unroll
@@ -799,7 +751,6 @@ static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
   constexpr bool CONV_SPEC = AMODE == A_CONV64 || AMODE == A_PATCH;
   if constexpr (CONV_SPEC || AMODE == A_DENSE) {
     switch (spec_form(e)) {
-      case SPEC_RELU_I8 | SF_LINE: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RELU_I8 | SF_LINE); return;
       case SPEC_RELU_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RELU_I8); return;
       case SPEC_BIAS_F32: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_F32); return;
       default: break;
@@ -812,7 +763,6 @@ static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
       case SPEC_RES_F32: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_F32); return;
       // the same ResNet block forms in f16 graphs
       case SPEC_RELU_I8 | SF_F16: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RELU_I8 | SF_F16); return;
-      case SPEC_RELU_I8 | SF_F16 | SF_LINE: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RELU_I8 | SF_F16 | SF_LINE); return;
       case SPEC_RES_F32_I8 | SF_F16: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_F32_I8 | SF_F16); return;
       case SPEC_BIAS_F32 | SF_F16: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_F32 | SF_F16); return;
       default: break;
@@ -825,7 +775,6 @@ static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
       case SPEC_BIAS_F32_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_F32_I8); return;
       case SPEC_BIAS_RES_F32_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_RES_F32_I8); return;
       case SPEC_BIAS_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_I8); return;
-      case SPEC_BIAS_I8 | SF_LINE: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_I8 | SF_LINE); return;
       case SPEC_BIAS_RES_I8: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_RES_I8); return;
       default: break;
     }

@@ -29,7 +29,6 @@ import numpy as np
 
 from . import _lib as L
 from . import pack
-from . import requant
 
 
 # Type annotations "Graph", "Op" and "Value" name MIRA's IR types (mira/ir.py:34-154); the
@@ -143,19 +142,14 @@ class RocmTarget:
     name = "rocm"
     supports_control_flow = False
 
-    def __init__(self, device: int = 0, debug_acc: bool = False, approx_f32: bool = False,
-                 requant_lines: bool = True):
+    def __init__(self, device: int = 0, debug_acc: bool = False, approx_f32: bool = False):
         """approx_f32: also run the float ops whose NumPy results depend on libm or on BLAS's
         summation order (softmax, f32 matmul of two float tensors, and gelu/sigmoid/tanh
         epilogue steps).  Their results then agree with the reference's to f32 rounding
-        (relative ~1e-6), not bit for bit; every other op stays bit-exact.
-        requant_lines: give int8-only q-op epilogues their exact integer requantization
-        lines (mira_amd.requant), computed at compile time; False keeps the float chain
-        (the same results)."""
+        (relative ~1e-6), not bit for bit; every other op stays bit-exact."""
         self.device = device
         self.debug_acc = debug_acc
         self.approx_f32 = approx_f32
-        self.requant_lines = requant_lines
 
     # ---------------------------------------------------------------- check
 
@@ -369,7 +363,6 @@ class RocmExecutable:
         self.dv: dict["Value", DevValue] = {}
         self.acc: dict["Value", object] = {}      # debug int32 accumulators per q-op result
         self.kernel_counts: dict[str, int] = {}
-        self.n_lines = 0              # q-ops whose int8 output uses requantization lines
         self.launch_cost: list[tuple[str, int, int]] = []
         self.const_bytes = 0
         self._plan()
@@ -803,44 +796,8 @@ class RocmExecutable:
             e.out_xs = fused
         if out.f32 is None and not wants:
             raise L.RocmError(f"{op.kind} result is never read")
-        if fused is not None and out.f32 is None and scale is not None:
-            self._requant_lines(op, e, fused)
         self.keep.append(e)
         return e, fused
-
-    def _requant_lines(self, op: "Op", e, xs: float) -> None:
-        """Integer requantization lines for a q-op whose only output is int8 and whose
-        epilogue is bias, ReLU, ReLU6 or bounds with constant per-column / scalar operands
-        (the forms the contraction kernels compile with lines)."""
-        if not self.target.requant_lines or self.target.debug_acc or op.kind not in ("qmatmul", "qconv2d"):
-            return
-        a = op.attrs
-        q = np.asarray(a["q"])
-        cols = q.shape[0] if op.kind == "qconv2d" else q.shape[1]
-        steps = []
-        for fn, idx, sw in a.get("epilogue", ()):
-            if fn == "relu":
-                steps.append((fn, None, False))
-                continue
-            if sw or fn not in ("add", "maximum", "minimum") or op.inputs[idx] not in self.consts:
-                return
-            v = np.asarray(self._const_value(op.inputs[idx]), np.float32)
-            mode = _bcast_mode(v.shape, op.result.type.shape, op.kind == "qconv2d")
-            if mode == L.BC_SCALAR:
-                v = v.reshape(())
-            elif mode == L.BC_COL:
-                v = v.reshape(-1)
-            else:
-                return
-            steps.append((fn, v, False))
-        k_real = int(q.size // cols)
-        lines = requant.int8_lines(pack.combined_scale(a["x_scale"], a["w_scale"]), steps,
-                                   op.result.type.dtype == "f16", xs, k_real)
-        if lines is None:
-            return
-        t = self._upload(lines.view(np.uint8))
-        e.lines = t.data_ptr()
-        self.n_lines += 1
 
     def _const_operand(self, v: "Value", rshape: tuple, is_conv: bool):
         a = self._const_value(v).astype(np.float32)
@@ -1440,5 +1397,4 @@ class RocmExecutable:
     def report(self) -> str:
         ks = ", ".join(f"{k} x{n}" for k, n in sorted(self.kernel_counts.items()))
         return (f"rocm (MI355X gfx950): {len(self.g.compute_ops())} ops -> {len(self.launches)} kernel launches "
-                f"[{ks}]; {self.const_bytes / 2**20:.2f} MiB of packed constants on device"
-                + (f"; {self.n_lines} int8 epilogues on requantization lines" if self.n_lines else ""))
+                f"[{ks}]; {self.const_bytes / 2**20:.2f} MiB of packed constants on device")

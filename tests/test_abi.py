@@ -5,7 +5,6 @@ import os
 import re
 
 from mira_amd import _lib as L
-from mira_amd import requant
 
 HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "mira_rocm.h")
 
@@ -32,9 +31,6 @@ def test_abi_version_and_struct_sizes():
     assert lib.mr_sizeof(b"mr_epi_step") == C.sizeof(L.EpiStep) == 32
     assert lib.mr_sizeof(b"mr_epilogue") == C.sizeof(L.Epilogue)
     assert lib.mr_sizeof(b"mr_conv_geom") == C.sizeof(L.ConvGeom) == 64
-    assert lib.mr_sizeof(b"mr_requant_line") == C.sizeof(L.RequantLine) == requant.LINE_DTYPE.itemsize == 32
-    assert [f[0] for f in L.RequantLine._fields_][:5] == list(requant.LINE_DTYPE.names)[:5]
-    assert all(getattr(L.RequantLine, f).offset == requant.LINE_DTYPE.fields[f][1] for f in ("c", "m", "w", "lo", "hi"))
     assert lib.mr_sizeof(b"nope") == -1
 
 

@@ -11,7 +11,6 @@ import pytest
 
 from mira_amd import _lib as L
 from mira_amd import pack
-from mira_amd import requant
 from oracle import golden as G
 
 from conftest import bits_equal
@@ -603,96 +602,6 @@ def test_qconv2d_epilogue_forms(lib, form, n, c, h, w, o, k, s, p, d):
         assert bits_equal(yq.cpu().numpy()[:, :o], to_nhwc(G.quantize_activation(want, next_xs)).astype(np.int8))
 
 
-def _lines_tensor(kind, scale, steps, f16, next_xs, k_real, o):
-    """Device requantization lines for an int8-only epilogue: 'fit' as mira_amd.requant
-    computes them (None if it declines), or 'chain': every output flagged (m = 0, c = 0,
-    w = 2^32 - 1), so the kernel's float chain runs for each of them."""
-    if kind == "fit":
-        lines = requant.int8_lines(scale, steps, f16, np.float32(next_xs), k_real)
-        if lines is None:
-            return None, None
-    else:
-        lines = np.zeros(o, requant.LINE_DTYPE)
-        lines["w"], lines["lo"], lines["hi"] = 0xFFFFFFFF, -127, 127
-    t = T(lines.view(np.uint8))
-    return t, lines
-
-
-@pytest.mark.parametrize("lines_kind", ["fit", "chain"])
-@pytest.mark.parametrize("form", ["relu_i8", "bias_i8", "bn_relu6_i8", "relu_i8_f16"])
-@pytest.mark.parametrize("n,c,h,w,o,k,s,p,d", FORM_CONV_CASES)
-def test_qconv2d_requant_lines(lib, lines_kind, form, n, c, h, w, o, k, s, p, d):
-    """int8-only epilogues with requantization lines (mr_requant_line): bit-exact against the
-    oracle on every conv geometry of the form tests, with the lines fitted on the host and
-    with every output sent through the kernel's float chain; geometries whose loader has no
-    line form ignore the lines, with the same results."""
-    torch = _torch()
-    f16 = form.endswith("_f16")
-    rng = np.random.default_rng(n * 1000 + c * 10 + k + 11)
-    x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
-    wt = rng.standard_normal((o, c, k, k)).astype(np.float32)
-    q, ws = G.quantize_array(wt, 0)
-    xs = float(np.abs(x).max()) / 127
-    oh, ow = G.conv_out(h, k, s, p, d), G.conv_out(w, k, s, p, d)
-    M = n * oh * ow
-    bias = (rng.standard_normal((o, 1, 1)) * 0.1).astype(np.float32)
-    zero, six = np.array(0, np.float32), np.array(6, np.float32)
-    if f16:
-        x, bias = (a.astype(np.float16).astype(np.float32) for a in (x, bias))
-    steps = {"relu_i8": (("add", 1, False), ("relu", None, False)), "relu_i8_f16": (("add", 1, False),
-             ("relu", None, False)), "bias_i8": (("add", 1, False),),
-             "bn_relu6_i8": (("add", 1, False), ("maximum", 2, False), ("minimum", 3, False))}[form]
-    attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f16" if f16 else "f32", "stride": (s, s),
-             "padding": (p, p), "dilation": (d, d), "epilogue": steps}
-    want = G.qconv2d([x, bias, zero, six], attrs)
-    next_xs = float(np.abs(want[np.isfinite(want)]).max()) / 127 or 1.0
-    next_xs = float(np.float32(next_xs) * np.float32(0.6))       # some results clamp at 127
-    host = {1: bias.reshape(o), 2: zero, 3: six}
-    host_steps = [(fn, None if i is None else host[i], sw) for fn, i, sw in steps]
-    cscale = pack.combined_scale(xs, ws)
-    lt, lines = _lines_tensor(lines_kind, cscale, host_steps, f16, next_xs, c * k * k, o)
-    if lt is None:
-        pytest.skip("the host declines lines for this epilogue (f16 rounding moves thresholds too far)")
-    cp = pack.c_pad_for(c)
-    xq = empty((n, h, w, cp), torch.int8)
-    L.check(lib.mr_quantize_nchw_nhwc(T(x).data_ptr(), n, c, h, w, xq.data_ptr(), cp, xs, stream()), "q")
-    bl = pack.pack_conv(q, cp)
-    b = T(pack.device_weights(bl))
-    scale = T(cscale)
-    g = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=cp, o=o, oh=oh, ow=ow, kh=k, kw=k, sh=s, sw=s, ph=p, pw=p, dh=d, dw=d)
-    dev = {1: (L.BC_COL, T(bias.reshape(o))), 2: (L.BC_SCALAR, T(zero.reshape(1))), 3: (L.BC_SCALAR, T(six.reshape(1)))}
-    dev_steps = [(fn, 0, None, 0, sw) if i is None else (fn, dev[i][0], dev[i][1], 0, sw) for fn, i, sw in steps]
-    ocp = pack.c_pad_for(o)
-    yq = empty((M, ocp), torch.int8)
-    e = epilogue(dev_steps, scale=scale, out_i8=yq, ldq=ocp, xs=next_xs)
-    e.flags = L.EPI_OUT_F16 if f16 else 0
-    e.lines = lt.data_ptr()
-    L.check(lib.mr_qconv2d(xq.data_ptr(), C.byref(g), b.data_ptr(), bl.shape[1], bl.shape[0], C.byref(e), stream()),
-            "mr_qconv2d")
-    sync()
-    want_q = G.quantize_activation(want, next_xs).astype(np.int8).transpose(0, 2, 3, 1).reshape(M, o)
-    assert bits_equal(yq.cpu().numpy()[:, :o], want_q)
-    assert (want_q == 127).any() and (want_q == (0 if "relu" in form else -127)).any() or form == "bias_i8"
-
-
-def test_requant_lines_need_an_int8_only_epilogue(lib):
-    """Lines with an f32 or int32 output, or misaligned, are refused before any launch."""
-    torch = _torch()
-    a = empty((64, 64), torch.int8)
-    b = T(pack.device_weights(pack.pack_matmul(np.ones((64, 32), np.int8))))
-    lt = T(np.zeros(32, requant.LINE_DTYPE).view(np.uint8))
-    sc = T(np.ones(32))
-    for kw in ({"out_f32": empty((64, 32), torch.float32), "ldo": 32},
-               {"out_acc": empty((64, 32), torch.int32), "ldacc": 32}):
-        e = epilogue(scale=sc, out_i8=empty((64, 32), torch.int8), ldq=32, xs=0.5, **kw)
-        e.lines = lt.data_ptr()
-        assert lib.mr_qmatmul(a.data_ptr(), 64, b.data_ptr(), 64, 32, 64, 32, 64, C.byref(e), stream()) == 1
-        assert b"requantization lines" in lib.mr_last_error()
-    e = epilogue(scale=sc, out_i8=empty((64, 32), torch.int8), ldq=32, xs=0.5)
-    e.lines = lt.data_ptr() + 4
-    assert lib.mr_qmatmul(a.data_ptr(), 64, b.data_ptr(), 64, 32, 64, 32, 64, C.byref(e), stream()) == 1
-
-
 @pytest.mark.parametrize("form", ["relu_i8", "bias_f32", "res_f32_i8"])
 @pytest.mark.parametrize("M,K,N", [(300, 512, 1000), (512, 256, 128), (64, 64, 10)])
 def test_qmatmul_epilogue_forms(lib, form, M, K, N):
@@ -966,8 +875,7 @@ def test_qconv2d_maxpool_f32in_rejects(lib):
                                         ("conv", (2, 64, 56, 56, 64, 3, 1, 1)),      # patch tiles
                                         ("conv", (2, 256, 14, 14, 512, 3, 1, 1)),    # 128x256 tiles
                                         ("conv", (4, 128, 28, 28, 256, 3, 2, 1))])   # stride 2
-@pytest.mark.parametrize("lines_kind", [None, "fit", "chain"])
-def test_int8_epilogue_ties(lib, kind, shape, lines_kind):
+def test_int8_epilogue_ties(lib, kind, shape):
     """bias + ReLU -> int8 where every odd accumulator lands exactly on a rounding midpoint:
     power-of-two scales make y / next_xs = acc / 2 + integer, so the requant must round each
     of these exact ties half to even, as NumPy's rint does."""
@@ -1018,14 +926,9 @@ def test_int8_epilogue_ties(lib, kind, shape, lines_kind):
     odd = (acc.astype(np.int64) % 2 != 0) & (want > 0) & (want < 127 * next_xs)
     assert odd.mean() > 0.15                      # plenty of exact ties in range
     yq = empty((rows, ocp), torch.int8)
-    bd = T(bias)        # named: a temporary's memory could be reused (by the lines) before the kernel runs
+    bd = T(bias)        # named: a temporary's memory could be reused before the kernel runs
     e = epilogue([("add", L.BC_COL, bd, 0, False), ("relu", 0, None, 0, False)], scale=scale, out_i8=yq,
                  ldq=ocp, xs=next_xs)
-    if lines_kind:
-        k_real = K if kind == "matmul" else c * k * k
-        lt, _ = _lines_tensor(lines_kind, pack.combined_scale(xs, ws), [("add", bias, False), ("relu", None, False)],
-                              False, next_xs, k_real, o)
-        e.lines = lt.data_ptr()
     if kind == "matmul":
         L.check(lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), bl.shape[1], bl.shape[0], M, N, K, C.byref(e),
                                stream()), "mr_qmatmul")

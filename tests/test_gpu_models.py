@@ -175,21 +175,6 @@ def test_resnet18_batch2_fused_stem(bn_epilogue, precision):
 
 # ---------------------------------------------------------------- C4 MobileNetV2
 
-@pytest.mark.parametrize("builder,min_lines", [(models.resnet18, 8), (models.mobilenet_v2, 2)])
-def test_requant_lines_in_the_networks(builder, min_lines):
-    """The production target gives the int8-only conv epilogues (ResNet-18's first conv of
-    each block and its downsamples, MobileNetV2's projections) integer requantization
-    lines; outputs equal the oracle's and the float-chain target's bit for bit."""
-    g, _ = _quantized(builder, 2)
-    x = {"x": models.image_batch((2, 3, 224, 224), 5)}
-    on = Runner(g, RocmTarget())
-    off = Runner(g, RocmTarget(requant_lines=False))
-    assert on.executables("rocm")[0].n_lines >= min_lines and off.executables("rocm")[0].n_lines == 0
-    (a,), (b,) = on.run(x), off.run(x)
-    want = oracle_env(g, x)[g.outputs[0]]
-    assert bits_equal(a, want) and bits_equal(b, want)
-
-
 def test_mobilenet_v2_batch1():
     g, _ = _quantized(models.mobilenet_v2, 1, calib_batch=2)
     runner = _compare(g, {"x": models.image_batch((1, 3, 224, 224), 5)}, fallback=False)
