@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MR_ABI_VERSION 7
+#define MR_ABI_VERSION 8
 
 enum mr_status {
   MR_OK = 0,
@@ -322,6 +322,55 @@ int mr_transpose_f32(const float* x, int32_t rank, const int64_t* shape,
  * operand (outer * inner == 0) is a no-op and its pointers may be NULL. */
 int mr_copy_rows_f32(const float* x, int64_t outer, int64_t inner, float* y,
                      int64_t ld, int64_t at, void* stream);
+
+/* ---- a decode step's attention and the greedy loop around it (examples/gpt_text.mira:60-82) */
+
+/* Replaces, for one decode step, the chain mira/ops.py:217-219 matmul(q,
+ * keys^T) -> mul(scale) -> add(mask) -> mira/ops.py:310-313 softmax -> matmul(
+ * ., values), where keys and values are a [B, T, H*hd] cache joined by the
+ * step's own [B, H*hd] row (mira/ops.py:403 concat at slot T): per sequence b
+ * and head h, s_j = (q_bh . k_j) * scale + mask[j] over the T + 1 keys,
+ * p = softmax(s), out_bh = sum_j p_j v_j.  q rows have stride ldq; cache row j
+ * of sequence b is at b * c_bs + j * c_ld; the new rows have strides ld_kn, ld_vn;
+ * mask has T + 1 entries shared by every sequence and head.  out (f32, row
+ * stride ldo) and/or out_i8 (clip(rint(out / xs), +-127), row stride ldq8).
+ * Approximate like the ops it replaces (expf, f32 multiply-adds in key order):
+ * within f32 rounding of NumPy, not bit for bit.  hd in {16, 32, 64},
+ * T + 1 <= 1024; strides multiples of 4 floats, operands 16-byte aligned. */
+int mr_attention_decode_f32(const float* q, int64_t ldq, const float* k_cache,
+                            const float* v_cache, int64_t c_ld, int64_t c_bs,
+                            const float* k_new, int64_t ld_kn, const float* v_new,
+                            int64_t ld_vn, const float* mask, float scale, int64_t B, int32_t H,
+                            int32_t hd, int32_t T, float* out, int64_t ldo,
+                            int8_t* out_i8, int64_t ldq8, float xs, void* stream);
+
+#define MR_DECODE_MAX_CACHES 16
+
+/* Start of one step of the greedy decode loop of examples/gpt_text.mira:66-81
+ * (the reference runs it on the host through mira/backends/cpu.py:44-51), at
+ * position t = *t_io (device int32): h[b, :] = emb[tokens[b, t]] + pos[t]
+ * (one f32 add), the step's mask over the T cache rows and its own row
+ * (mask[j] = 0 for j < t and j == T, neg otherwise), and *t_cur = t for the
+ * step's end.  tokens is [B, ld_tok] int32; emb [V, D], pos [T, D] f32.
+ * Token ids are clamped to [0, V) and t to [0, T) on the device so no read
+ * leaves its table; the caller keeps them in range. */
+int mr_decode_embed(const int32_t* tokens, int64_t ld_tok, const int32_t* t_io,
+                    int32_t* t_cur, const float* emb, int32_t V, const float* pos,
+                    int32_t T, int32_t D, float* h, int64_t B, float* mask,
+                    float neg, void* stream);
+
+/* End of that step at t = *t_cur: rows[k][b, :D] (row stride ld_rows[k]) is
+ * stored at row t of caches[k] (row b * c_bs + t * c_ld) for each of the
+ * n_caches key/value rows; tokens[b, t + 1] becomes the argmax of
+ * logits[b, :V] (NumPy's: first maximum, a NaN first) when t + 1 >= prompt_len
+ * (the prompt's own tokens stay otherwise); *t_io = t + 1.  `rows`, `ld_rows`
+ * and `caches` are host arrays of n_caches <= MR_DECODE_MAX_CACHES entries. */
+int mr_decode_commit(const float* logits, int64_t ldl, int32_t V, int32_t n_caches,
+                     const float* const* rows, const int64_t* ld_rows,
+                     float* const* caches, int64_t c_ld, int64_t c_bs, int32_t D,
+                     int32_t* tokens, int64_t ld_tok, int32_t* t_io,
+                     const int32_t* t_cur, int32_t prompt_len, int32_t T,
+                     int64_t B, void* stream);
 
 #ifdef __cplusplus
 }

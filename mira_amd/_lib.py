@@ -10,7 +10,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "libmira_rocm.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 MAX_EPI = 8
 
 # enum mr_epi_fn
@@ -30,7 +30,9 @@ EXPORTS = [
     "mr_maxpool2d_f32", "mr_mean_hw_f32", "mr_pad_hw_f32", "mr_round_f16_f32",
     "mr_nchw_to_nhwc_f32", "mr_nhwc_to_nchw_f32",
     "mr_layernorm_f32", "mr_softmax_f32", "mr_bmm_f32", "mr_transpose_f32", "mr_copy_rows_f32",
+    "mr_attention_decode_f32", "mr_decode_embed", "mr_decode_commit",
 ]
+DECODE_MAX_CACHES = 16      # MR_DECODE_MAX_CACHES
 
 
 class EpiStep(C.Structure):
@@ -86,6 +88,11 @@ _SIGS = {
     "mr_bmm_f32": ([_p, _p, _i32, _p, _p, _p, _p, _i64, _i64, _i64, C.POINTER(Epilogue), _p], C.c_int),
     "mr_transpose_f32": ([_p, _i32, _p, _p, _p, _p], C.c_int),
     "mr_copy_rows_f32": ([_p, _i64, _i64, _p, _i64, _i64, _p], C.c_int),
+    "mr_attention_decode_f32": ([_p, _i64, _p, _p, _i64, _i64, _p, _i64, _p, _i64, _p, _f32, _i64, _i32, _i32, _i32, _p,
+                                 _i64, _p, _i64, _f32, _p], C.c_int),
+    "mr_decode_embed": ([_p, _i64, _p, _p, _p, _i32, _p, _i32, _i32, _p, _i64, _p, _f32, _p], C.c_int),
+    "mr_decode_commit": ([_p, _i64, _i32, _i32, _p, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _i32, _i32, _i64, _p],
+                         C.c_int),
 }
 
 

@@ -225,6 +225,197 @@ __global__ void __launch_bounds__(256) copy_rows_kernel(const float* __restrict_
   }
 }
 
+// ---------------------------------------------------------------- fused decode attention (approximate)
+
+// One attention of a decode step, the ops MIRA's program spells out one by one (matmul of the
+// query with the transposed keys, the scale and the mask, softmax over the keys, matmul with the
+// values; examples/gpt_text.mira, mira/ops.py:217-219, 310-313): the keys and values are a
+// cache of T rows joined by the step's own row (slot T), read in place.  Approximate like the
+// ops it replaces: expf and f32 multiply-adds in key order, within f32 rounding of NumPy.
+struct AttnArgs {
+  const float* q;            // [B, H*HD] rows (row stride ldq)
+  int64_t ldq;
+  const float* kc;           // caches [B, T, c_ld]: row j of sequence b at b * c_bs + j * c_ld
+  const float* vc;
+  int64_t c_ld, c_bs;
+  const float* kn;           // the step's key / value rows [B, ...] (row strides ldkn, ldvn)
+  const float* vn;
+  int64_t ldkn, ldvn;
+  const float* mask;         // [T + 1], the same for every sequence and head
+  float scale;
+  int32_t B, H, T;
+  float* out;                // [B, H*HD] (row stride ldo), optional
+  int64_t ldo;
+  int8_t* out_i8;            // its int8 copy clip(rint(y / xs)), optional
+  int64_t ldq8;
+  float xs;
+};
+
+// One wave per (sequence, head); lane l takes keys l, l + 64, ...: their scores stay in
+// registers (JMAX * 64 keys at most), the max and the sum of exponentials are butterflies,
+// and each lane's share of the context product is summed over the lanes at the end.
+template <int HD, int JMAX>
+__global__ void __launch_bounds__(256) attention_decode_kernel(const AttnArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t job = blockIdx.x * int64_t(blockDim.x / 64) + (threadIdx.x >> 6);
+  if (job >= int64_t(a.B) * a.H) return;
+  const int64_t b = job / a.H;
+  const int h = static_cast<int>(job - b * a.H);
+  float qv[HD];
+#pragma unroll
+  for (int d = 0; d < HD; d += 4) {
+    const float4 v = *reinterpret_cast<const float4*>(a.q + b * a.ldq + h * HD + d);
+    qv[d] = v.x; qv[d + 1] = v.y; qv[d + 2] = v.z; qv[d + 3] = v.w;
+  }
+  const int nj = a.T + 1;
+  float sc[JMAX];
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < JMAX; ++i) {
+    const int j = lane + 64 * i;
+    sc[i] = -__builtin_inff();
+    if (j < nj) {
+      const float* kr = j < a.T ? a.kc + b * a.c_bs + int64_t(j) * a.c_ld + h * HD : a.kn + b * a.ldkn + h * HD;
+      float acc = 0.0f;
+#pragma unroll
+      for (int d = 0; d < HD; d += 4) {
+        const float4 k = *reinterpret_cast<const float4*>(kr + d);
+        acc = fmaf(qv[d], k.x, acc);
+        acc = fmaf(qv[d + 1], k.y, acc);
+        acc = fmaf(qv[d + 2], k.z, acc);
+        acc = fmaf(qv[d + 3], k.w, acc);
+      }
+      sc[i] = __fadd_rn(__fmul_rn(acc, a.scale), a.mask[j]);
+      m = np_maximum(m, sc[i]);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = np_maximum(m, __shfl_xor(m, o));
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < JMAX; ++i) {
+    const int j = lane + 64 * i;
+    if (j < nj) {
+      sc[i] = expf(__fsub_rn(sc[i], m));
+      sum = __fadd_rn(sum, sc[i]);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum = __fadd_rn(sum, __shfl_xor(sum, o));
+  float ov[HD];
+#pragma unroll
+  for (int d = 0; d < HD; ++d) ov[d] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < JMAX; ++i) {
+    const int j = lane + 64 * i;
+    if (j < nj) {
+      const float pj = __fdiv_rn(sc[i], sum);
+      const float* vr = j < a.T ? a.vc + b * a.c_bs + int64_t(j) * a.c_ld + h * HD : a.vn + b * a.ldvn + h * HD;
+#pragma unroll
+      for (int d = 0; d < HD; d += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(vr + d);
+        ov[d] = fmaf(pj, v.x, ov[d]);
+        ov[d + 1] = fmaf(pj, v.y, ov[d + 1]);
+        ov[d + 2] = fmaf(pj, v.z, ov[d + 2]);
+        ov[d + 3] = fmaf(pj, v.w, ov[d + 3]);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+    for (int d = 0; d < HD; ++d) ov[d] = __fadd_rn(ov[d], __shfl_xor(ov[d], o));
+  if (lane != 0) return;
+  if (a.out) {
+#pragma unroll
+    for (int d = 0; d < HD; d += 4)
+      *reinterpret_cast<float4*>(a.out + b * a.ldo + h * HD + d) = make_float4(ov[d], ov[d + 1], ov[d + 2], ov[d + 3]);
+  }
+  if (a.out_i8) {
+#pragma unroll
+    for (int d = 0; d < HD; d += 4) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) w |= uint32_t(uint8_t(quantize_one(ov[d + c], a.xs))) << (8 * c);
+      *reinterpret_cast<uint32_t*>(a.out_i8 + b * a.ldq8 + h * HD + d) = w;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- the greedy decode loop's own state
+
+// Start of a decode step at position t = *t_io (examples/gpt_text.mira:66-81, the body of
+// `generate`'s loop): the input row of each sequence, emb[token t] + pos[t] (one f32 add, as
+// NumPy adds the two gathered rows), and the step's mask over the T cache rows and the step's
+// own row (0 for rows already written and for its own row, `neg` for the rest).  The position
+// is latched into *t_cur for the step's end (decode_commit_kernel advances *t_io).  Token ids
+// are clamped into [0, V) and t into [0, T) so no read leaves its table; the host keeps both
+// in range.
+__global__ void __launch_bounds__(256) decode_embed_kernel(const int32_t* __restrict__ tokens, int64_t ld_tok,
+                                                           const int32_t* __restrict__ t_io, int32_t* t_cur,
+                                                           const float* __restrict__ emb, int32_t V,
+                                                           const float* __restrict__ pos, int32_t T, int32_t D,
+                                                           float* __restrict__ h, int64_t B, float* __restrict__ mask,
+                                                           float neg) {
+  const int t = min(max(t_io[0], 0), T - 1);
+  const int64_t row = blockIdx.x;
+  if (row < B) {
+    const int tok = min(max(tokens[row * ld_tok + t], 0), V - 1);
+    for (int d = threadIdx.x; d < D; d += blockDim.x)
+      h[row * D + d] = __fadd_rn(emb[int64_t(tok) * D + d], pos[int64_t(t) * D + d]);
+    return;
+  }
+  for (int j = threadIdx.x; j <= T; j += blockDim.x) mask[j] = (j < t || j == T) ? 0.0f : neg;
+  if (threadIdx.x == 0) t_cur[0] = t;
+}
+
+struct CommitArgs {
+  int32_t n;                  // key/value rows to store (<= MR_DECODE_MAX_CACHES)
+  const float* row[MR_DECODE_MAX_CACHES];
+  int64_t ld_row[MR_DECODE_MAX_CACHES];
+  float* cache[MR_DECODE_MAX_CACHES];
+  int64_t c_ld, c_bs;         // cache row stride and per-sequence stride (elements)
+  int32_t D;                  // elements per row
+};
+
+// NumPy's argmax order: a NaN beats every number and the first NaN wins; among numbers the
+// larger wins, and the smaller index on a tie.
+__device__ inline bool argmax_better(float v, int i, float bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
+// End of the step at position t = *t_cur: each sequence's key/value rows go to cache row t,
+// the next token is the argmax of its logits once the prompt is consumed (t + 1 >= prompt_len,
+// else the prompt's own token stays), and *t_io advances to t + 1.  One block per sequence.
+__global__ void __launch_bounds__(64) decode_commit_kernel(const float* __restrict__ logits, int64_t ldl, int32_t V,
+                                                           const CommitArgs c, int32_t* tokens, int64_t ld_tok,
+                                                           int32_t* t_io, const int32_t* __restrict__ t_cur,
+                                                           int32_t prompt_len, int32_t T) {
+  const int64_t b = blockIdx.x;
+  const int t = min(max(t_cur[0], 0), T - 2);
+  const int lane = threadIdx.x;
+  float bv = -__builtin_inff();
+  int bi = 0x7fffffff;
+  for (int i = lane; i < V; i += 64) {
+    const float v = logits[b * ldl + i];
+    if (argmax_better(v, i, bv, bi)) { bv = v; bi = i; }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    if (argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  for (int k = 0; k < c.n; ++k)
+    for (int d = lane; d < c.D; d += 64) c.cache[k][b * c.c_bs + int64_t(t) * c.c_ld + d] = c.row[k][b * c.ld_row[k] + d];
+  if (lane == 0) {
+    if (t + 1 >= prompt_len) tokens[b * ld_tok + t + 1] = bi;
+    if (b == 0) t_io[0] = t + 1;
+  }
+}
+
 static unsigned grid_1d(int64_t total, int block) {
   int64_t g = (total + block - 1) / block;
   const int64_t cap = int64_t(device_cu_count()) * 32;
@@ -334,6 +525,83 @@ int mr_copy_rows_f32(const float* x, int64_t outer, int64_t inner, float* y, int
   hipLaunchKernelGGL(mr::copy_rows_kernel, dim3(mr::grid_1d(outer * inner, 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), x, outer, inner, y, ld, at);
   MR_LAUNCH_CHECK("copy_rows");
+  return MR_OK;
+}
+
+int mr_attention_decode_f32(const float* q, int64_t ldq, const float* k_cache, const float* v_cache, int64_t c_ld,
+                            int64_t c_bs, const float* k_new, int64_t ld_kn, const float* v_new, int64_t ld_vn,
+                            const float* mask,
+                            float scale, int64_t B, int32_t H, int32_t hd, int32_t T, float* out, int64_t ldo,
+                            int8_t* out_i8, int64_t ldq8, float xs, void* stream) {
+  MR_REQUIRE(q && k_new && v_new && mask && (T == 0 || (k_cache && v_cache)), "mr_attention_decode_f32: NULL operand");
+  MR_REQUIRE(out || out_i8, "mr_attention_decode_f32: no output");
+  MR_REQUIRE(hd == 16 || hd == 32 || hd == 64, "mr_attention_decode_f32: head width %d not in {16, 32, 64}", hd);
+  MR_REQUIRE(B >= 0 && H > 0 && T >= 0 && T + 1 <= 1024, "mr_attention_decode_f32: needs T + 1 <= 1024 keys");
+  const int64_t w = int64_t(H) * hd;
+  MR_REQUIRE(ldq >= w && ld_kn >= w && ld_vn >= w && c_ld >= w && c_bs >= int64_t(T) * c_ld,
+             "mr_attention_decode_f32: bad strides");
+  MR_REQUIRE(ldq % 4 == 0 && ld_kn % 4 == 0 && ld_vn % 4 == 0 && c_ld % 4 == 0 && c_bs % 4 == 0,
+             "mr_attention_decode_f32: row strides "
+             "must be multiples of 4 floats");
+  auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  MR_REQUIRE(al16(q) && al16(k_new) && al16(v_new) && (T == 0 || (al16(k_cache) && al16(v_cache))),
+             "mr_attention_decode_f32: operands must be 16-byte aligned");
+  if (out) MR_REQUIRE(ldo >= w && ldo % 4 == 0 && al16(out), "mr_attention_decode_f32: bad f32 output");
+  if (out_i8) MR_REQUIRE(ldq8 >= w && ldq8 % 4 == 0 && reinterpret_cast<uintptr_t>(out_i8) % 4 == 0 && xs > 0.0f,
+                         "mr_attention_decode_f32: bad int8 output");
+  if (B == 0) return MR_OK;
+  mr::AttnArgs a = {q, ldq, k_cache, v_cache, c_ld, c_bs, k_new, v_new, ld_kn, ld_vn, mask, scale,
+                    static_cast<int32_t>(B), H, T, out, ldo, out_i8, ldq8, xs};
+  MR_REQUIRE(B * H < (int64_t(1) << 31) && B < (int64_t(1) << 31), "mr_attention_decode_f32: too many heads");
+  const dim3 grid(static_cast<unsigned>((B * H + 3) / 4)), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int jmax = (T + 1 + 63) / 64;
+#define MR_ATTN(HDV, JM) hipLaunchKernelGGL((mr::attention_decode_kernel<HDV, JM>), grid, block, 0, s, a)
+  if (hd == 16) { if (jmax <= 5) MR_ATTN(16, 5); else MR_ATTN(16, 16); }
+  else if (hd == 32) { if (jmax <= 5) MR_ATTN(32, 5); else MR_ATTN(32, 16); }
+  else { if (jmax <= 5) MR_ATTN(64, 5); else MR_ATTN(64, 16); }
+#undef MR_ATTN
+  MR_LAUNCH_CHECK("attention_decode");
+  return MR_OK;
+}
+
+int mr_decode_embed(const int32_t* tokens, int64_t ld_tok, const int32_t* t_io, int32_t* t_cur, const float* emb,
+                    int32_t V, const float* pos, int32_t T, int32_t D, float* h, int64_t B, float* mask, float neg,
+                    void* stream) {
+  MR_REQUIRE(tokens && t_io && t_cur && emb && pos && h && mask, "mr_decode_embed: NULL argument");
+  MR_REQUIRE(V > 0 && T > 0 && D > 0 && B >= 0 && ld_tok >= T, "mr_decode_embed: bad sizes");
+  MR_REQUIRE(B < (int64_t(1) << 31), "mr_decode_embed: too many sequences");
+  hipLaunchKernelGGL(mr::decode_embed_kernel, dim3(static_cast<unsigned>(B + 1)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), tokens, ld_tok, t_io, t_cur, emb, V, pos, T, D, h, B, mask, neg);
+  MR_LAUNCH_CHECK("decode_embed");
+  return MR_OK;
+}
+
+int mr_decode_commit(const float* logits, int64_t ldl, int32_t V, int32_t n_caches, const float* const* rows,
+                     const int64_t* ld_rows, float* const* caches, int64_t c_ld, int64_t c_bs, int32_t D,
+                     int32_t* tokens, int64_t ld_tok, int32_t* t_io, const int32_t* t_cur, int32_t prompt_len,
+                     int32_t T, int64_t B, void* stream) {
+  MR_REQUIRE(logits && tokens && t_io && t_cur, "mr_decode_commit: NULL argument");
+  MR_REQUIRE(V > 0 && ldl >= V && T >= 2 && ld_tok >= T && B >= 0 && D >= 0, "mr_decode_commit: bad sizes");
+  MR_REQUIRE(n_caches >= 0 && n_caches <= MR_DECODE_MAX_CACHES && (n_caches == 0 || (rows && ld_rows && caches)),
+             "mr_decode_commit: 0..%d cache rows", MR_DECODE_MAX_CACHES);
+  MR_REQUIRE(c_ld >= D && c_bs >= (int64_t(T) - 1) * c_ld + D, "mr_decode_commit: bad cache strides");
+  MR_REQUIRE(B < (int64_t(1) << 31), "mr_decode_commit: too many sequences");
+  mr::CommitArgs c = {};
+  c.n = n_caches;
+  for (int k = 0; k < n_caches; ++k) {
+    MR_REQUIRE(rows[k] && caches[k] && ld_rows[k] >= D, "mr_decode_commit: bad cache row %d", k);
+    c.row[k] = rows[k];
+    c.ld_row[k] = ld_rows[k];
+    c.cache[k] = caches[k];
+  }
+  c.c_ld = c_ld;
+  c.c_bs = c_bs;
+  c.D = D;
+  if (B == 0) return MR_OK;
+  hipLaunchKernelGGL(mr::decode_commit_kernel, dim3(static_cast<unsigned>(B)), dim3(64), 0,
+                     static_cast<hipStream_t>(stream), logits, ldl, V, c, tokens, ld_tok, t_io, t_cur, prompt_len, T);
+  MR_LAUNCH_CHECK("decode_commit");
   return MR_OK;
 }
 

@@ -457,6 +457,8 @@ class RocmExecutable:
         self._pinned: dict["Value", object] = {}     # pinned host buffers of upload()
         self._upload_done = None                     # event after upload()'s last DMA
         self.canon: dict["Value", object] = {}     # C-order copies of NHWC values (_c_order)
+        self.i8_preset: dict = {}      # value -> int8 copies an earlier kernel already wrote
+        self._plan_attention()
         self._plan_views()
         for v in g.inputs:
             self._emit_input(v)
@@ -488,6 +490,82 @@ class RocmExecutable:
             if _is_contig(s, st):
                 return base, shape, _contig(shape), [v] + chain
         return v, shape, _contig(shape), []
+
+    def _only_feeds(self, v: "Value", op: "Op") -> bool:
+        """Is every read of v, and of the reshapes/transposes made of it, an input of `op`?"""
+        us = self.users.get(v, [])
+        return bool(us) and v not in self.g.outputs and all(
+            u is op or (u.kind in ("reshape", "transpose") and self._only_feeds(u.result, op)) for u in us)
+
+    def _plan_attention(self) -> None:
+        """Decode-step attention run as one mr_attention_decode_f32 launch (approx_f32 only): the
+        chain matmul(q4, k4) with epilogue mul(scalar scale), add(mask over the keys) ->
+        softmax(last axis) -> matmul(., v4), where q4 [B, H, 1, hd] is a head view of a [B, D]
+        query, and k4 [B, H, hd, T+1] / v4 [B, H, T+1, hd] are head views of concat(cache
+        [B, T, D], row [B, 1, D]) along axis 1.  The two matmuls, the softmax and both concats
+        are not run; the kernel reads the caches and the step's rows in place."""
+        self.attn: dict = {}
+        if not self.target.approx_f32:
+            return
+        g, users = self.g, self.users
+        for sm in g.ops:
+            if sm.kind != "softmax" or not self._device_op(sm):
+                continue
+            sc = sm.inputs[0]
+            A = sc.producer
+            if A is None or A.kind != "matmul" or not self._is_bmm(A) or users.get(sc) != [sm] or sc in g.outputs:
+                continue
+            r = sm.result.type.rank
+            bus = users.get(sm.result, [])
+            if r != 4 or sm.attrs["axis"] % r != 3 or len(bus) != 1 or sm.result in g.outputs:
+                continue
+            Bop = bus[0]
+            if Bop.kind != "matmul" or not self._is_bmm(Bop) or Bop.inputs[0] is not sm.result:
+                continue
+            if any(v.type.dtype != "f32" for v in (*A.inputs[:2], A.result, Bop.inputs[1], Bop.result)):
+                continue
+            qb, qs, qst, _ = self._view_chain(A.inputs[0])
+            kb, ks, kst, _ = self._view_chain(A.inputs[1])
+            vb, vs, vst, _ = self._view_chain(Bop.inputs[1])
+            if len(qs) != 4:
+                continue
+            Bn, H, one, hd = qs
+            if one != 1 or hd not in (16, 32, 64):
+                continue
+            D = H * hd
+            T1 = ks[3] if len(ks) == 4 else -1
+            if ks != (Bn, H, hd, T1) or vs != (Bn, H, T1, hd) or T1 < 1 or T1 > 1024 or \
+                    tuple(A.result.type.shape) != (Bn, H, 1, T1) or tuple(Bop.result.type.shape) != (Bn, H, 1, hd):
+                continue
+            if qb.type.shape != (Bn, D) or qst != (D, hd, qst[2], 1):
+                continue
+            if kst != (T1 * D, hd, 1, D) or vst != (T1 * D, hd, D, 1):
+                continue
+            cats = []
+            for base, user in ((kb, A), (vb, Bop)):
+                c = base.producer
+                if c is None or c.kind != "concat" or c.attrs["axis"] % 3 != 1 or len(c.inputs) != 2 or \
+                        base.type.shape != (Bn, T1, D) or not self._only_feeds(base, user):
+                    break
+                cache, row = c.inputs
+                rb, rs, rst, _ = self._view_chain(row)
+                if cache.type.shape != (Bn, T1 - 1, D) or rb.type.shape != (Bn, D) or \
+                        row.type.shape != (Bn, 1, D) or cache in self.images:
+                    break
+                cats.append((c, cache, rb))
+            if len(cats) != 2:
+                continue
+            epi = A.attrs.get("epilogue", ())
+            if len(epi) != 2 or epi[0][0] != "mul" or epi[1][0] != "add" or epi[0][2] or epi[1][2]:
+                continue
+            sv, mv = A.inputs[epi[0][1]], A.inputs[epi[1][1]]
+            if sv not in self.consts or sv.type.numel != 1 or mv.type.numel != T1 or \
+                    tuple(mv.type.shape)[-1] != T1 or mv.type.dtype != "f32":
+                continue
+            self.attn[Bop] = {"q": qb, "kc": cats[0][1], "kn": cats[0][2], "vc": cats[1][1], "vn": cats[1][2],
+                              "mask": mv, "scale": float(np.asarray(self._const_value(sv)).reshape(())),
+                              "B": Bn, "H": H, "hd": hd, "T": T1 - 1}
+            self.skip.update((A, sm, cats[0][0], cats[1][0]))
 
     def _plan_views(self) -> None:
         """Two ways of not copying, decided before any buffer exists:
@@ -850,7 +928,50 @@ class RocmExecutable:
         w = op.inputs[1]
         if w.producer is not None and w.producer.kind == "dequantize":
             return self._emit_w8_matmul(op)
+        if op in self.attn:
+            return self._emit_attention(op)
         return self._emit_bmm(op)
+
+    def _emit_attention(self, op: "Op") -> None:
+        """The fused decode attention planned by _plan_attention, at its context matmul.  When
+        the context feeds an int8 consumer through a head-merging view ([B, H, 1, hd] ->
+        [B, 1, H, hd] -> [B, D]), the kernel writes that int8 copy too."""
+        torch = _t()
+        a = self.attn[op]
+        Bn, H, hd, T = a["B"], a["H"], a["hd"], a["T"]
+        D = H * hd
+        q, kc, vc = self._c_order(a["q"]), self._c_order(a["kc"]), self._c_order(a["vc"])
+        kn, vn, mask = self._c_order(a["kn"]), self._c_order(a["vn"]), self._c_order(a["mask"])
+        if kc.stride() != vc.stride() or kc.stride(2) != 1 or q.stride(1) != 1 or kn.stride(1) != 1 or \
+                vn.stride(1) != 1 or not mask.is_contiguous():
+            raise L.RocmError("attention operands are not row-major views")
+        out = self._new_dv(op.result)
+        if out.f32 is None:
+            out.f32 = torch.empty(op.result.type.shape, dtype=torch.float32, device=self.dev)
+        y = out.f32
+        q8, ld8, xs = None, 0, 1.0
+        t = self.users.get(op.result, [])
+        if len(t) == 1 and t[0].kind == "transpose" and tuple(t[0].attrs["perm"]) == (0, 2, 1, 3):
+            rs = self.users.get(t[0].result, [])
+            if len(rs) == 1 and rs[0].kind == "reshape" and tuple(rs[0].result.type.shape) == (Bn, D):
+                r = rs[0].result
+                wants = self.need_i8.get(r, [])
+                if wants:
+                    xs, ld8 = wants[0], pack.row_stride_for(D)
+                    q8 = torch.empty((Bn, ld8), dtype=torch.int8, device=self.dev)
+                    self.i8_preset[r] = {xs: (q8, ld8)}
+        lib, scale = self.lib, a["scale"]
+        c_ld, c_bs = kc.stride(1), kc.stride(0)
+        args = (q, q.stride(0), kc, vc, c_ld, c_bs, kn, kn.stride(0), vn, vn.stride(0), mask, scale, Bn, H, hd, T, y,
+                D, q8, ld8, xs)
+        self.keep.append(args)
+        self._add("attention", lambda s: L.check(lib.mr_attention_decode_f32(
+            args[0].data_ptr(), args[1], args[2].data_ptr(), args[3].data_ptr(), c_ld, c_bs, args[6].data_ptr(),
+            args[7], args[8].data_ptr(), args[9], args[10].data_ptr(), scale, Bn, H, hd, T, y.data_ptr(), D,
+            _ptr(q8), ld8, xs, s), "mr_attention_decode_f32"),
+            nbytes=4 * (2 * Bn * (T + 1) * D + Bn * D + (T + 1)) + 4 * Bn * D + (Bn * ld8 if q8 is not None else 0),
+            nops=4 * Bn * (T + 1) * D)
+        self._finish_i8(out, None)
 
     def _emit_w8_matmul(self, op: "Op") -> None:
         """Weight-only int8 matmul (checked by _check_w8_matmul): the int8 weights are packed
@@ -1100,6 +1221,7 @@ class RocmExecutable:
         src_v, r = op.inputs[0], op.result
         x = self._src(src_v)
         d = DevValue(r, nhwc=r in self.images)
+        d.i8.update(self.i8_preset.get(r, {}))
         self.dv[r] = d
         if r not in self.need_f32 and r not in self.need_i8:
             return

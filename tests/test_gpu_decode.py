@@ -493,3 +493,114 @@ def test_device_decoder_batch512_matches_host_loop():
             assert int(dec.t.item()) == i + 1
     assert np.array_equal(dec.tokens.cpu().numpy(), want_tok)
     assert bits_equal(dec.logits.cpu().numpy(), want_logits[-1])
+
+
+# ---------------------------------------------------------------- fused decode attention and the loop kernels
+
+@pytest.mark.parametrize("B,H,hd,T", [(1, 4, 16, 272), (5, 4, 16, 40), (3, 2, 32, 0), (2, 2, 64, 700), (512, 4, 16, 272)])
+def test_attention_decode_within_tolerance(lib, B, H, hd, T):
+    """mr_attention_decode_f32 against the chain it replaces, in float64: scores of the query
+    with the T cache keys and the new key, times the scale, plus the mask; softmax; the
+    context.  Within 1e-5 of the float64 context's magnitude sum over the values; the int8 copy
+    is the quantizer applied to the kernel's own f32 result."""
+    torch = _torch()
+    rng = np.random.default_rng(B * 7 + T)
+    D = H * hd
+    q = rng.standard_normal((B, D)).astype(np.float32)
+    kc, vc = (rng.standard_normal((B, T, D)).astype(np.float32) for _ in range(2))
+    kn, vn = (rng.standard_normal((B, D)).astype(np.float32) for _ in range(2))
+    mask = np.where(rng.random(T + 1) < 0.3, -10000.0, 0.0).astype(np.float32)
+    mask[T] = 0.0
+    scale = np.float32(1.0 / np.sqrt(hd))
+    keys = np.concatenate([kc, kn[:, None]], axis=1).astype(np.float64).reshape(B, T + 1, H, hd)
+    vals = np.concatenate([vc, vn[:, None]], axis=1).astype(np.float64).reshape(B, T + 1, H, hd)
+    s = np.einsum("bhd,bjhd->bhj", q.astype(np.float64).reshape(B, H, hd), keys) * scale + mask
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    want = np.einsum("bhj,bjhd->bhd", p, vals).reshape(B, D)
+    mag = np.einsum("bhj,bjhd->bhd", p, np.abs(vals)).reshape(B, D)
+    y = empty((B, D), torch.float32)
+    ld8 = pack.row_stride_for(D)
+    y8 = empty((B, ld8), torch.int8)
+    xs = np.float32(np.abs(want).max() / 127)
+    qd, kcd, vcd, knd, vnd, md = T_(q), T_(kc), T_(vc), T_(kn), T_(vn), T_(mask)
+    L.check(lib.mr_attention_decode_f32(qd.data_ptr(), D, kcd.data_ptr() if T else None, vcd.data_ptr() if T else None,
+                                        D, T * D, knd.data_ptr(), D, vnd.data_ptr(), D, md.data_ptr(), float(scale), B,
+                                        H, hd, T, y.data_ptr(), D, y8.data_ptr(), ld8, float(xs), stream()), "attention")
+    sync()
+    got = y.cpu().numpy()
+    _close(got, want, scale=mag, rtol=0, atol=1e-5)
+    assert bits_equal(y8.cpu().numpy()[:, :D], G.quantize_activation(got, xs).astype(np.int8))
+
+
+def test_attention_decode_rejects(lib):
+    t = T_(np.zeros((4, 64), np.float32))
+    args = lambda hd, T, ldq: (t.data_ptr(), ldq, t.data_ptr(), t.data_ptr(), 64, 64 * T, t.data_ptr(), 64,
+                               t.data_ptr(), 64, t.data_ptr(), 1.0, 1, 64 // hd, hd, T, t.data_ptr(), 64, None, 0, 1.0,
+                               stream())
+    assert lib.mr_attention_decode_f32(*args(8, 3, 64)) == 1          # head width 8
+    assert lib.mr_attention_decode_f32(*args(16, 1024, 64)) == 1      # 1025 keys
+    assert lib.mr_attention_decode_f32(*args(16, 3, 62)) == 1         # query stride
+
+
+def test_decode_embed_and_commit_exact(lib):
+    """The loop-state kernels against NumPy: the embedding + position row (one f32 add), the
+    mask row, the counter latch; then the cache row writes, NumPy's argmax (first maximum,
+    a NaN first), the prompt kept while t + 1 < prompt_len, and the counter advance."""
+    torch = _torch()
+    rng = np.random.default_rng(3)
+    B, T, D, V, P = 6, 20, 8, 11, 5
+    emb = rng.standard_normal((V, D)).astype(np.float32)
+    pos = rng.standard_normal((T, D)).astype(np.float32)
+    tokens = rng.integers(0, V, (B, T)).astype(np.int32)
+    caches = [rng.standard_normal((B, T, D)).astype(np.float32) for _ in range(3)]
+    rows = [rng.standard_normal((B, D)).astype(np.float32) for _ in range(3)]
+    logits = rng.standard_normal((B, V)).astype(np.float32)
+    logits[1, [2, 7]] = 9.0                     # a tie: the first index wins
+    logits[2, [4, 9]] = np.nan                  # NaNs: the first NaN wins
+    logits[3, :] = -np.inf
+    logits[4, 6] = np.inf
+    tok_d, emb_d, pos_d = T_(tokens), T_(emb), T_(pos)
+    cache_d = [T_(c) for c in caches]
+    row_d = [T_(r) for r in rows]
+    lg_d = T_(logits)
+    h = empty((B, D), torch.float32)
+    mask = empty((T + 1,), torch.float32)
+    for t in (0, P - 2, P - 1, T - 2):
+        state = T_(np.array([t, -1], np.int32))
+        st = state.data_ptr()
+        L.check(lib.mr_decode_embed(tok_d.data_ptr(), T, st, st + 4, emb_d.data_ptr(), V, pos_d.data_ptr(), T, D,
+                                    h.data_ptr(), B, mask.data_ptr(), -10000.0, stream()), "embed")
+        sync()
+        assert bits_equal(h.cpu().numpy(), (emb[tokens[:, t]] + pos[t]).astype(np.float32))
+        want_mask = np.full(T + 1, -10000.0, np.float32)
+        want_mask[:t] = 0.0
+        want_mask[T] = 0.0
+        assert bits_equal(mask.cpu().numpy(), want_mask)
+        assert list(state.cpu().numpy()) == [t, t]
+        before = tok_d.cpu().numpy()
+        rp = (C.c_void_p * 3)(*[r.data_ptr() for r in row_d])
+        ld = (C.c_int64 * 3)(D, D, D)
+        cp = (C.c_void_p * 3)(*[c.data_ptr() for c in cache_d])
+        L.check(lib.mr_decode_commit(lg_d.data_ptr(), V, V, 3, rp, ld, cp, D, T * D, D, tok_d.data_ptr(), T, st,
+                                     st + 4, P, T, B, stream()), "commit")
+        sync()
+        assert list(state.cpu().numpy()) == [t + 1, t]
+        for c, r, cd in zip(caches, rows, cache_d):
+            c[:, t] = r
+            assert bits_equal(cd.cpu().numpy(), c)
+        after = tok_d.cpu().numpy()
+        want_tok = before.copy()
+        if t + 1 >= P:
+            want_tok[:, t + 1] = np.argmax(logits, axis=1)
+        assert np.array_equal(after, want_tok)
+    assert list(np.argmax(logits, axis=1)[1:5]) == [2, 4, 0, 6]
+
+
+def test_gpt_step_approx_mode_fuses_attention():
+    """approx_f32: each layer's attention (scores, scale, mask, softmax, context, and the cache
+    concatenations) is one launch, which also writes the int8 input of the out projection."""
+    cfg, params, g = _gpt(2)
+    exe = Runner(g, RocmTarget(approx_f32=True)).executables("rocm")[0]
+    k = exe.kernel_counts
+    assert k.get("attention") == cfg.L and not {"softmax", "bmm_f32", "concat", "quantize"} & set(k), k

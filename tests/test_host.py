@@ -347,13 +347,25 @@ def test_gpt_placement_by_mode():
     assert [s.device for s in segs] == ["rocm"] and not reasons
 
 
-class _OracleStepExecutable:
-    """Stands in for the rocm executable of the decode step on the CPU: the same device_input /
-    device_output / launch surface over CPU tensors, launch() evaluating the step with the oracle."""
+class _RecordingLib:
+    """Stands in for libmira_rocm.so on the CPU: records the decode-loop calls, computes nothing."""
+
+    def __init__(self):
+        self.calls = []
+
+    def __getattr__(self, name):
+        def call(*args):
+            self.calls.append((name, args))
+            return 0
+        return call
+
+
+class _StepExecutable:
+    """The device_input / device_output / launch surface of a step executable over CPU tensors."""
 
     def __init__(self, g):
         import torch
-        self.g, self.dev = g, torch.device("cpu")
+        self.g, self.dev, self.lib = g, torch.device("cpu"), _RecordingLib()
         self.inputs = {v: torch.zeros(v.type.shape, dtype=torch.float32) for v in g.inputs}
         self.outputs = {v: torch.zeros(v.type.shape, dtype=torch.float32) for v in g.outputs}
 
@@ -364,23 +376,20 @@ class _OracleStepExecutable:
         return self.outputs[v]
 
     def launch(self):
-        import torch
-        feeds = {v.name: t.numpy().copy() for v, t in self.inputs.items()}
-        for v, arr in zip(self.g.outputs, G.run_graph(self.g, feeds)):
-            self.outputs[v].copy_(torch.from_numpy(np.asarray(arr, np.float32)))
+        self.lib.calls.append(("step", ()))
 
 
-def test_device_decoder_loop_on_cpu():
-    """harness.decode.DeviceDecoder's loop (embedding/position rows, mask rows, cache writes,
-    argmax, the prompt guard, the step counter) run on CPU tensors around the oracle's step
-    gives the tokens of models.gpt_decode; a step past the context raises instead of indexing
-    out of range."""
+def test_decode_loop_host_protocol():
+    """mira_amd.decode.DecodeLoop on the host side: each step queues the embed kernel, the
+    step's launches and the commit kernel in that order, with the tables, the caches' layout,
+    the counters and the prompt length; prompts are validated (shape, token range), and a step
+    past the context raises instead of being queued."""
     from harness.decode import DeviceDecoder
 
     class FakeRunner:
         def __init__(self, g):
             self.graph, self.devices = g, ["rocm"]
-            self.exe = _OracleStepExecutable(g)
+            self.exe = _StepExecutable(g)
 
         def executables(self, device=None):
             return [self.exe]
@@ -388,14 +397,32 @@ def test_device_decoder_loop_on_cpu():
     cfg = models.GPTConfig()
     params = models.gpt_params(cfg, 0)
     g = LW.prepare(models.gpt_decode_step(cfg, 2, params))
+    runner = FakeRunner(g)
+    dec = DeviceDecoder(runner, cfg, params, 2)
+    calls = runner.exe.lib.calls
     prompt = np.random.default_rng(4).integers(0, cfg.V, (2, 16)).astype(np.int32)
-    want, _ = models.gpt_decode(lambda f: G.run_graph(g, f), cfg, params, prompt, 12)
-    dec = DeviceDecoder(FakeRunner(g), cfg, params, 2)
-    assert np.array_equal(dec.decode(prompt, 12), want)
+    dec.reset(prompt)
+    assert np.array_equal(dec.tokens[:, :16].numpy(), prompt) and not dec.tokens[:, 16:].any()
+    dec.run_steps(3)
+    assert [c[0] for c in calls] == ["mr_decode_embed", "step", "mr_decode_commit"] * 3
+    emb = calls[0][1]
+    assert emb[5] == cfg.V and emb[7] == cfg.T and emb[8] == cfg.D and emb[10] == 2 and emb[12] == -10000.0
+    commit = calls[2][1]
+    assert commit[2] == cfg.V and commit[3] == 2 * cfg.L and commit[9] == cfg.D and commit[14] == 16
+    assert (commit[7], commit[8]) == (cfg.D, cfg.T * cfg.D)          # cache row and sequence strides
+    assert commit[12] == emb[2] and commit[13] == emb[3] == emb[2] + 4   # the counter and its latch
+    with pytest.raises(ValueError):
+        dec.reset(np.full((2, 16), cfg.V, np.int32))                 # token id past the vocabulary
+    with pytest.raises(ValueError):
+        dec.reset(np.zeros((3, 16), np.int32))                       # another batch
     dec.reset(prompt)
     dec.steps_done = cfg.T - 1            # as after a full-context decode
+    n = len(calls)
     with pytest.raises(RuntimeError):
         dec.step()
+    assert len(calls) == n
+    with pytest.raises(RuntimeError):
+        dec.run_steps(1, use_graph=True)                             # no graph captured
 
 
 def test_division_magic_is_exact():
