@@ -77,6 +77,7 @@ class DecodeLoop:
         self.prompt_len = 0
         self.steps_done = 0       # host copy of t: a step at t writes token t + 1, so t + 1 < T
         self.graph = None
+        self.graph_steps = 0
         self._graph_prompt_len = None
 
     @property
@@ -132,10 +133,16 @@ class DecodeLoop:
         self._advance()
         self._queue(self._stream())
 
-    def capture(self) -> None:
-        """Record one step as a HIP graph for the current prompt length (a warm-up step runs
-        first, outside the capture; reset() rewinds the state afterwards)."""
+    def capture(self, steps: int = 1) -> None:
+        """Record `steps` consecutive decode steps as one HIP graph for the current prompt length
+        (every step reads its position from the device counter, so the same launches repeat).
+        With steps = prompt length + new tokens - 1 the whole greedy decode is one graph launch:
+        the loop of examples/gpt_text.mira:66-81 runs on the device from start to end.  A
+        warm-up step runs first, outside the capture; the state is rewound afterwards, so
+        reset() must load a prompt before the graph is replayed."""
         torch = _t()
+        if not 1 <= steps < self.T:
+            raise ValueError(f"{steps} steps do not fit a {self.T}-token context")
         dev = self.exe.dev
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
@@ -146,21 +153,31 @@ class DecodeLoop:
         torch.cuda.current_stream(dev).wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self._queue(torch.cuda.current_stream(dev).cuda_stream)       # recorded, not run
+            stream = torch.cuda.current_stream(dev).cuda_stream
+            for _ in range(steps):
+                self._queue(stream)            # recorded, not run
         torch.cuda.synchronize(dev)
         self._graph_prompt_len = self.prompt_len
+        self.graph_steps = steps
         self.state.zero_()
         self.steps_done = 0
 
     def run_steps(self, n: int, use_graph: bool = False) -> None:
-        if use_graph and (self.graph is None or self._graph_prompt_len != self.prompt_len):
-            raise RuntimeError("capture() first (for this prompt length)")
+        """n more decode steps: queued eagerly, or as replays of the captured graph (n must be a
+        multiple of its step count)."""
+        if use_graph:
+            if self.graph is None or self._graph_prompt_len != self.prompt_len:
+                raise RuntimeError("capture() first (for this prompt length)")
+            if n % self.graph_steps:
+                raise ValueError(f"{n} steps are not whole replays of a {self.graph_steps}-step graph")
+            for _ in range(n // self.graph_steps):
+                for _ in range(self.graph_steps):
+                    self._advance()
+                self.graph.replay()
+            return
         for _ in range(n):
             self._advance()
-            if use_graph:
-                self.graph.replay()
-            else:
-                self._queue(self._stream())
+            self._queue(self._stream())
 
     def decode(self, prompt: np.ndarray, new_tokens: int, use_graph: bool = False) -> np.ndarray:
         """Greedy decode: the prompt [B, P], then new_tokens argmax tokens; returns [B, P + new]."""

@@ -460,6 +460,7 @@ class RocmExecutable:
         self.i8_preset: dict = {}      # value -> int8 copies an earlier kernel already wrote
         self._plan_attention()
         self._plan_views()
+        self._plan_shared_input_matmuls()
         for v in g.inputs:
             self._emit_input(v)
         for op in g.ops:
@@ -566,6 +567,48 @@ class RocmExecutable:
                               "mask": mv, "scale": float(np.asarray(self._const_value(sv)).reshape(())),
                               "B": Bn, "H": H, "hd": hd, "T": T1 - 1}
             self.skip.update((A, sm, cats[0][0], cats[1][0]))
+
+    def _row_slice_ok(self, v: "Value") -> bool:
+        """Can v's f32 copy be a column slice of a wider buffer (rows with a stride)?  Only when
+        nothing reads it as a C-order buffer: it is a graph output (copied out by strides), or
+        it feeds a fused attention (which takes row strides), views that are never run, ops
+        that are not run, or reshapes of its rows that only such ops read."""
+        for u in self.users.get(v, []):
+            if u in self.skip or u in self.virtual:
+                continue
+            if u.kind == "reshape" and u.result not in self.g.outputs and self._row_slice_ok(u.result) and \
+                    all(w in self.skip for w in self.users.get(u.result, [])):
+                continue
+            return False
+        return True
+
+    def _plan_shared_input_matmuls(self) -> None:
+        """q-ops that read the same int8 activation at the same x_scale, without an epilogue and
+        with f32 results only (a transformer's query/key/value projections) run as one
+        mr_qmatmul over their weights side by side: each result is a column slice of one
+        [rows, sum N] buffer.  Only results whose readers take row strides (see
+        _row_slice_ok) join such a group."""
+        self.row_group: dict = {}       # first op of a group -> the group's ops
+        if self.target.debug_acc:
+            return
+        groups: dict = {}
+        for op in self.g.ops:
+            if op.kind != "qmatmul" or not self._device_op(op) or op.attrs.get("epilogue") or \
+                    op.result.type.dtype != "f32" or op.result.type.rank != 2 or self.need_i8.get(op.result) or \
+                    op.inputs[0] in self.images:
+                continue
+            if not self._row_slice_ok(op.result):
+                continue
+            groups.setdefault((op.inputs[0], _f32key(op.attrs["x_scale"])), []).append(op)
+        for ops in groups.values():
+            if len(ops) < 2:
+                continue
+            self.row_group[ops[0]] = ops
+            self.skip.update(ops[1:])
+            for op in ops:
+                for u in self.users.get(op.result, []):
+                    if u.kind == "reshape" and u not in self.virtual and u not in self.skip:
+                        self.skip.add(u)          # read only by ops that are not run
 
     def _plan_views(self) -> None:
         """Two ways of not copying, decided before any buffer exists:
@@ -902,7 +945,37 @@ class RocmExecutable:
         self.acc[op.result] = t
         return t
 
+    def _emit_qmatmul_group(self, ops: list) -> None:
+        """One launch for q-ops sharing their int8 input (planned by _plan_shared_input_matmuls):
+        the weights packed side by side, each result a column slice of the output rows."""
+        torch = _t()
+        x = self._src(ops[0].inputs[0])
+        xs = _f32key(ops[0].attrs["x_scale"])
+        xq, lda = x.i8[xs] if xs in x.i8 else self._quantize_to(x, xs)
+        q = np.concatenate([np.asarray(op.attrs["q"], np.int8) for op in ops], axis=1)
+        ws = np.concatenate([np.asarray(op.attrs["w_scale"], np.float32).reshape(-1) for op in ops])
+        K, N = q.shape
+        bl = pack.pack_matmul(q)
+        b = self._upload(pack.device_weights(bl))
+        scale = self._upload(pack.combined_scale(ops[0].attrs["x_scale"], ws))
+        M = int(np.prod(ops[0].result.type.shape[:-1], dtype=np.int64))
+        y = torch.empty((M, N), dtype=torch.float32, device=self.dev)
+        at = 0
+        for op in ops:
+            n = op.result.type.shape[-1]
+            self.dv[op.result] = DevValue(op.result, nhwc=False, f32=y[:, at:at + n])
+            at += n
+        e = L.Epilogue()
+        e.scale, e.out_f32, e.ldo = scale.data_ptr(), y.data_ptr(), N
+        self.keep.append(e)
+        lib, kp, npad = self.lib, bl.shape[1], bl.shape[0]
+        self._add("qmatmul", lambda s: L.check(
+            lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), kp, npad, M, N, K, C.byref(e), s), "mr_qmatmul"),
+            nbytes=M * K + K * N + 8 * N + 4 * M * N, nops=2 * M * N * K)
+
     def _emit_qmatmul(self, op: "Op") -> None:
+        if op in self.row_group:
+            return self._emit_qmatmul_group(self.row_group[op])
         a = op.attrs
         x = self._src(op.inputs[0])
         q = np.asarray(a["q"], np.int8)
@@ -1472,7 +1545,8 @@ class RocmExecutable:
 
     def device_output(self, v: "Value"):
         """The device f32 buffer (graph layout) that `launch` leaves output v in; it is rewritten
-        by the next launch.  Only for values stored in C order (not NHWC images)."""
+        by the next launch.  Only for values stored in C order (not NHWC images); the rows of a
+        result computed beside others (_plan_shared_input_matmuls) are a strided view."""
         d = self._src(v)
         if d.nhwc or d.f32 is None:
             raise L.RocmError(f"{v} has no C-order f32 copy on the device")

@@ -396,6 +396,17 @@ def test_device_decoder_matches_host_loop(batch, new):
     graph_tok = dec.tokens[:, :16 + new].cpu().numpy()
     assert np.array_equal(graph_tok, want_tok)
     assert bits_equal(dec.logits.cpu().numpy(), want_logits[-1])
+    # every step of the decode recorded as one graph: the whole loop is one launch
+    dec.reset(prompt)
+    dec.capture(steps)
+    dec.reset(prompt)
+    dec.run_steps(steps, use_graph=True)
+    torch.cuda.synchronize()
+    assert int(dec.t.item()) == steps and dec.graph_steps == steps
+    assert np.array_equal(dec.tokens[:, :16 + new].cpu().numpy(), want_tok)
+    assert bits_equal(dec.logits.cpu().numpy(), want_logits[-1])
+    with pytest.raises(ValueError):
+        dec.run_steps(steps - 1, use_graph=True)
 
 
 # ---------------------------------------------------------------- batch 512: the decode that bench.py times
@@ -599,8 +610,10 @@ def test_decode_embed_and_commit_exact(lib):
 
 def test_gpt_step_approx_mode_fuses_attention():
     """approx_f32: each layer's attention (scores, scale, mask, softmax, context, and the cache
-    concatenations) is one launch, which also writes the int8 input of the out projection."""
+    concatenations) is one launch, which also writes the int8 input of the out projection, and
+    the query/key/value projections of a layer are one q-op launch: 16 launches per step."""
     cfg, params, g = _gpt(2)
     exe = Runner(g, RocmTarget(approx_f32=True)).executables("rocm")[0]
     k = exe.kernel_counts
     assert k.get("attention") == cfg.L and not {"softmax", "bmm_f32", "concat", "quantize"} & set(k), k
+    assert k["qmatmul"] == 4 * cfg.L + 1 and len(exe.launches) == 16
