@@ -49,8 +49,8 @@ def apply_epilogue(y: np.ndarray, operands: list, steps) -> np.ndarray:
 
 
 def conv2d_f32(x: np.ndarray, w: np.ndarray, a: dict, dt=np.float32) -> np.ndarray:
-    """NCHW x OIHW -> NCHW convolution in `dt` (f32; f64 makes integer operands exact):
-    im2col + one GEMM, or per tap for grouped convs."""
+    """NCHW x OIHW -> NCHW convolution in `dt` (f64 for the integer accumulators of qconv2d,
+    where any order is exact): im2col + one GEMM, or per tap for grouped convs."""
     (sh, sw), (ph, pw) = a["stride"], a["padding"]
     dh, dw = a.get("dilation", (1, 1))
     g = a.get("groups", 1)
@@ -84,6 +84,28 @@ def conv2d_f32(x: np.ndarray, w: np.ndarray, a: dict, dt=np.float32) -> np.ndarr
     return np.ascontiguousarray(acc.transpose(0, 3, 1, 2))
 
 
+def conv2d_taps_f32(x: np.ndarray, w: np.ndarray, a: dict) -> np.ndarray:
+    """The f32 convolution as MIRA's golden model sums it (mira/ops.py:256-276): one grouped
+    einsum per kernel tap over the padded input, added into an f32 accumulator in (i, j) tap
+    order.  Float results (calibration peaks, the cpu fallback) then carry MIRA's roundings
+    bit for bit, which one im2col product would not."""
+    (sh, sw), (ph, pw) = a["stride"], a["padding"]
+    dh, dw = a.get("dilation", (1, 1))
+    g = a.get("groups", 1)
+    x, w = _f32(x), _f32(w)
+    n, c, h, wd = x.shape
+    o, cg, kh, kw = w.shape
+    oh, ow = conv_out(h, kh, sh, ph, dh), conv_out(wd, kw, sw, pw, dw)
+    xp = np.pad(x, ((0, 0), (0, 0), (ph, ph), (pw, pw)))
+    wg = w.reshape(g, o // g, cg, kh, kw)
+    acc = np.zeros((n, g, o // g, oh, ow), np.float32)
+    for i in range(kh):
+        for j in range(kw):
+            xt = xp[:, :, i * dh:i * dh + sh * (oh - 1) + 1:sh, j * dw:j * dw + sw * (ow - 1) + 1:sw]
+            acc += np.einsum("ngchw,goc->ngohw", xt.reshape(n, g, cg, oh, ow), wg[:, :, :, i, j], optimize=True)
+    return acc.reshape(n, o, oh, ow)
+
+
 def quantize_activation(x: np.ndarray, x_scale: float) -> np.ndarray:
     """clip(rint(x / f32(x_scale)), +-127) in f32 arithmetic, as int64."""
     return np.clip(np.rint(_f32(x) / np.float32(x_scale)), -127, 127).astype(np.int64)
@@ -104,7 +126,7 @@ def evaluate(kind: str, xs: list, a: dict) -> np.ndarray:
     if kind == "matmul":
         return apply_epilogue(_f32(xs[0]) @ _f32(xs[1]), xs, a.get("epilogue", ())).astype(dt)
     if kind == "conv2d":
-        return apply_epilogue(conv2d_f32(xs[0], xs[1], a), xs, a.get("epilogue", ())).astype(dt)
+        return apply_epilogue(conv2d_taps_f32(xs[0], xs[1], a), xs, a.get("epilogue", ())).astype(dt)
     if kind == "qmatmul":
         acc = quantize_activation(xs[0], a["x_scale"]) @ a["q"].astype(np.int64)
         y = (acc.astype(np.float64) * (np.float64(a["x_scale"]) * a["w_scale"].astype(np.float64))).astype(np.float32)

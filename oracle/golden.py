@@ -94,7 +94,8 @@ def epilogue_ref(acc: np.ndarray, xs: list, epilogue) -> np.ndarray:
 # ---------------------------------------------------------------- matmul / conv (mira/ops.py:217-279)
 
 def matmul(xs: list, attrs: dict) -> np.ndarray:
-    """mira/ops.py:217-219.  f32 BLAS order: parity unpinned beyond tolerance."""
+    """mira/ops.py:217-219.  f32 BLAS order: bit parity unpinned; pinned to the rounding bound
+    of any f32 summation order against a float64 brute force (tests/test_oracle.py)."""
     acc = np.matmul(f32(xs[0]), f32(xs[1]))
     return epilogue_ref(acc, xs, attrs.get("epilogue", ())).astype(xs[0].dtype)
 

@@ -99,9 +99,7 @@ def test_w8a8_attrs_match_mira(case):
         assert np.array_equal(a.attrs["w_scale"], b.attrs["w_scale"])
         assert a.attrs.get("epilogue", ()) == b.attrs.get("epilogue", ())
         assert a.attrs["dtype"] == b.attrs["dtype"] and a.result.type == b.result.type
-        after_conv = a.inputs[0].producer is not None and a.inputs[0].producer.kind in ("maxpool2d", "reshape")
-        tol = 1e-6 if after_conv else 0.0
-        assert abs(a.attrs["x_scale"] - b.attrs["x_scale"]) <= tol * b.attrs["x_scale"]
+        assert a.attrs["x_scale"] == b.attrs["x_scale"]
 
 
 # ---------------------------------------------------------------- oracle vs MIRA (CPU)

@@ -361,6 +361,39 @@ def test_transpose_and_concat_brute_force():
         assert z[a, b_, c, d] == (x[a, b_, c, d] if b_ < 2 else -x[a, b_, c, d])
 
 
+@pytest.mark.parametrize("ashape,wshape", [((5, 7), (7, 3)), ((2, 3, 1, 64), (2, 3, 64, 273)),
+                                           ((4, 1, 8, 32), (1, 3, 32, 16)), ((1, 1), (1, 1)), ((9, 300), (300, 2))])
+def test_f32_matmul_within_its_rounding_bound(ashape, wshape):
+    """oracle.matmul (mira/ops.py:217-219, NumPy/BLAS f32 order) against a float64 brute force
+    of the same broadcast product, written as explicit loops over the batch and the output:
+    every element within K * 2^-24 * (|a| @ |w|) plus one f32 ulp of the result, the bound
+    for any summation order of K products in f32; a dropped term, a wrong operand index or a
+    transposed operand misses it by far."""
+    rng = np.random.default_rng(sum(ashape) + sum(wshape))
+    a = rng.standard_normal(ashape).astype(np.float32)
+    w = rng.standard_normal(wshape).astype(np.float32)
+    got = G.matmul([a, w], {})
+    K = ashape[-1]
+    bshape = np.broadcast_shapes(ashape[:-2], wshape[:-2])
+    ab = np.broadcast_to(a, bshape + ashape[-2:]).astype(np.float64)
+    wb = np.broadcast_to(w, bshape + wshape[-2:]).astype(np.float64)
+    want = np.zeros(bshape + (ashape[-2], wshape[-1]))
+    mag = np.zeros_like(want)
+    for idx in np.ndindex(*bshape) if bshape else [()]:
+        for m in range(ashape[-2]):
+            for n in range(wshape[-1]):
+                terms = ab[idx + (m,)] * wb[idx + (slice(None), n)]
+                want[idx + (m, n)] = terms.sum()
+                mag[idx + (m, n)] = np.abs(terms).sum()
+    assert got.shape == want.shape and got.dtype == np.float32
+    bound = K * 2.0 ** -24 * mag + np.spacing(np.abs(got).astype(np.float32)).astype(np.float64)
+    assert (np.abs(got.astype(np.float64) - want) <= bound).all()
+    # the bound is not vacuous: the same product with its last K term dropped misses it
+    if K > 1:
+        dropped = np.matmul(a[..., :-1], w[..., :-1, :]).astype(np.float64)
+        assert (np.abs(dropped - want) > bound).any()
+
+
 def test_epilogue_operand_order():
     acc = np.array([5.0, -3.0], np.float32)
     other = np.array([2.0, 4.0], np.float32)
