@@ -223,6 +223,18 @@ def test_onnx_import_resnet18_batch2():
     assert runner.devices == ["rocm"]
 
 
+def test_onnx_import_mobilenet_v2_batch2():
+    """A torchvision-layout MobileNetV2 written as ONNX and read by this repository's importer
+    (as the reference imports torchvision's, tests/test_onnx.py:150-159): every op on rocm --
+    the int8 pointwise and stem convs, the f32 depthwise convs, ReLU6, the residual adds, the
+    average pool and the classifier; accumulators and outputs bit-exact."""
+    import torch_onnx_nets as N
+    _, data = N.mobilenet_v2(2, seed=3)
+    g = _imported(data, (2, 3, 224, 224))
+    runner = _compare(g, {"x": models.image_batch((2, 3, 224, 224), 6)}, fallback=False)
+    assert runner.devices == ["rocm"]
+
+
 @pytest.mark.parametrize("opset", [10, 13])
 def test_onnx_import_edge_net(opset):
     """The importer's less common forms on rocm: an asymmetric pad before a 4-channel conv, a

@@ -81,6 +81,21 @@ def test_resnet18_matches_torch():
     np.testing.assert_allclose(got, want, rtol=1e-3, atol=1e-4 * np.abs(want).max())
 
 
+def test_mobilenet_v2_matches_torch():
+    """The torchvision-layout MobileNetV2 (depthwise groups, ReLU6 as Clip, residual adds)
+    imports to a graph whose f32 forward pass is torch's."""
+    import torch
+    net, data = N.mobilenet_v2(2)
+    g = OI.import_model(data)
+    kinds = [op.kind for op in g.compute_ops()]
+    assert kinds.count("conv2d") == 52 and kinds.count("add") >= 10
+    x = np.random.default_rng(2).uniform(0, 1, (2, 3, 224, 224)).astype(np.float32)
+    (got,) = G.run_graph(g, {"x": x})
+    with torch.no_grad():
+        want = net(torch.from_numpy(x)).numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-3, atol=1e-4 * np.abs(want).max())
+
+
 def test_resnet18_lowers_like_the_builder():
     """The imported ResNet-18 and the harness's builder (BN as mul + add, the importer's
     layout) lower to the same W8A8 op sequence: 20 q-convolutions and one q-matmul with the

@@ -161,3 +161,74 @@ def edge_net(batch: int, opset: int, seed: int = 1):
     out = m.node("Gemm", [flat, m.init(_np(fc.weight)), m.init(_np(fc.bias) * 2)], transB=1, alpha=0.5, beta=0.5)
     m.output(out, (batch, 10))
     return forward, m.bytes()
+
+
+# torchvision's MobileNetV2 stages: (expansion t, output channels c, blocks n, first stride s)
+MNV2_STAGES = ((1, 16, 1, 1), (6, 24, 2, 2), (6, 32, 3, 2), (6, 64, 4, 2), (6, 96, 3, 1), (6, 160, 3, 2),
+               (6, 320, 1, 1))
+
+
+def mobilenet_v2(batch: int, seed: int = 0, classes: int = 1000):
+    """torchvision's MobileNetV2 layout in torch (random weights and BN statistics): a 3x3/2
+    stem, inverted residual blocks (1x1 expansion + BN + ReLU6, 3x3 depthwise + BN + ReLU6,
+    1x1 linear projection + BN, the residual add where stride 1 keeps the width), a 1x1 conv to
+    1280 channels, global average pooling and the classifier; and its ONNX bytes (opset 13,
+    BatchNormalization nodes, ReLU6 as Clip with min/max inputs)."""
+    torch = _torch()
+    nn = torch.nn
+    gen = torch.Generator().manual_seed(seed)
+    torch.manual_seed(seed)
+
+    def cbr(cin, cout, k, s, groups=1, relu=True):
+        layers = [nn.Conv2d(cin, cout, k, s, (k - 1) // 2, groups=groups, bias=False), nn.BatchNorm2d(cout)]
+        return nn.Sequential(*layers, *([nn.ReLU6()] if relu else []))
+
+    class Block(nn.Module):
+        def __init__(self, cin, cout, stride, t):
+            super().__init__()
+            hid = cin * t
+            self.res = stride == 1 and cin == cout
+            self.layers = nn.Sequential(*([cbr(cin, hid, 1, 1)] if t != 1 else []), cbr(hid, hid, 3, stride, hid),
+                                        cbr(hid, cout, 1, 1, relu=False))
+
+        def forward(self, x):
+            return x + self.layers(x) if self.res else self.layers(x)
+
+    class Net(nn.Module):
+        def __init__(self):
+            super().__init__()
+            feats, cin = [cbr(3, 32, 3, 2)], 32
+            for t, c, n, s in MNV2_STAGES:
+                for i in range(n):
+                    feats.append(Block(cin, c, s if i == 0 else 1, t))
+                    cin = c
+            feats.append(cbr(cin, 1280, 1, 1))
+            self.features = nn.Sequential(*feats)
+            self.fc = nn.Linear(1280, classes)
+
+        def forward(self, x):
+            return self.fc(torch.flatten(nn.functional.adaptive_avg_pool2d(self.features(x), 1), 1))
+
+    net = Net().eval()
+    for mod in net.modules():
+        if isinstance(mod, nn.BatchNorm2d):
+            _randomize_bn(mod, gen)
+    m = Model(13)
+    e = Emitter(m)
+
+    def emit_cbr(x, seq):
+        y = e.bn(e.conv(x, seq[0]), seq[1])
+        return e.relu6(y) if len(seq) == 3 else y
+
+    h = m.input("x", (batch, 3, 224, 224))
+    for f in net.features:
+        if isinstance(f, Block):
+            y = h
+            for seq in f.layers:
+                y = emit_cbr(y, seq)
+            h = m.node("Add", [h, y]) if f.res else y
+        else:
+            h = emit_cbr(h, f)
+    out = e.linear(e.gap_flatten(h), net.fc)
+    m.output(out, (batch, classes))
+    return net, m.bytes()
