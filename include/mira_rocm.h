@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MR_ABI_VERSION 8
+#define MR_ABI_VERSION 9
 
 enum mr_status {
   MR_OK = 0,
@@ -164,6 +164,15 @@ int mr_quantize_f16_nchw_nhwc(const float* x, int32_t n, int32_t c, int32_t h, i
  * ((k / 64) * n_pad + n) * 64 + k % 64. */
 int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int64_t n_pad,
                int64_t M, int64_t N, int64_t K, const mr_epilogue* epi, void* stream);
+
+/* The same for decode shapes whose activation rows are still f32: mira/ops.py:602-603
+ * quantize_activation (x / x_scale, as mr_quantize_rows) fused into :616-620, so a
+ * decode step's first layer needs no separate quantize launch.  x is [M, ldx] f32
+ * (ldx >= K); results equal mr_quantize_rows + mr_qmatmul bit for bit.  M <= 8 and
+ * k_pad <= 4096 (MR_EUNSUPPORTED otherwise). */
+int mr_qmatmul_f32in(const float* x, int64_t ldx, float x_scale, const int8_t* b,
+                     int64_t k_pad, int64_t n_pad, int64_t M, int64_t N, int64_t K,
+                     const mr_epilogue* epi, void* stream);
 
 /* Replaces, for decode-shaped matmuls of the int8 weight-only mode
  * (mira/quantize.py:45-68), mira/ops.py:217-219 _matmul_ref fed by the

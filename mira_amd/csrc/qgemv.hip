@@ -100,70 +100,121 @@ __global__ void __launch_bounds__(256) qgemv_kernel(const GemvArgs g, const EpiD
 }
 
 // The same product with the weight stream laid along the packed rows: a
-// workgroup of KW waves owns 16 adjacent columns; lane l reads the 16-byte
-// quarter l % 4 of column n0 + l / 4 in a K step, so one wave-wide load is the
-// 1 KB run of those 16 columns' 64-byte K-step rows (the packed layout keeps
-// a K step of consecutive columns contiguous), and wave w covers its share of
-// the K steps.  Each column's four lanes reduce by shuffles, the KW waves
-// through LDS, and the first 16 * M threads finish one element each with the
-// same epilogue.  The sums are exact int32, so the order does not matter.
-// Taken for k_pad <= 4096 (at most KS_MAXS steps per wave, all in flight at
-// once): 5.2 -> 4.7 us on a 4096x4096 layer at M = 1, 16.7 -> 11.8 us at M = 8.
-// Longer K stays on qgemv_kernel, whose lanes share each activation load between
-// two columns (at K = 16384 and M = 3 it is 1.5x faster than this one).
-constexpr int KS_COLS = 16;   // columns per workgroup
-constexpr int KS_MAXS = 8;    // K steps a lane has in flight at once
+// workgroup of KW waves owns COLS adjacent columns; the LPC = 64 / COLS lanes of
+// a column read consecutive 16-byte chunks of its 64-byte K-step rows, SPL =
+// LPC / 4 steps per wave-wide load, so one load is COLS runs of SPL * 64 bytes
+// (the packed layout keeps a K step of consecutive columns contiguous: with 16
+// columns one load is the 1 KB run of their rows), and wave w covers its share of
+// the K steps.  Each column's lanes reduce by shuffles, the KW waves through LDS,
+// and the first COLS * M threads finish one element each with the same epilogue.
+// The sums are exact int32, so the order does not matter.  Taken for k_pad <= 4096
+// (every load of a lane in flight at once): 5.2 -> 4.7 us on a 4096x4096 layer at
+// M = 1, 16.7 -> 11.8 us at M = 8.  Fewer columns per workgroup spread a narrow
+// layer over more CUs (4096 -> 1000 at M = 1: 63 workgroups of 16 columns, or 250
+// of 4).  Longer K stays on qgemv_kernel, whose lanes share each activation load
+// between two columns (at K = 16384 and M = 3 it is 1.5x faster than this one).
+//
+// F32IN: the activation rows arrive as f32 and each workgroup quantizes them into
+// LDS first (mr_quantize_rows's arithmetic, mira/ops.py:602-603), after its weight
+// loads are issued, so the separate quantize launch of a decode step's first layer
+// disappears behind the weight stream's latency.
+constexpr int KS_MAXS = 8;    // wave-wide loads a lane has in flight at once
+constexpr int KS_KMAX = 4096; // largest k_pad of this kernel (8 waves x 8 steps x 64 bytes)
 
-template <int MR, int KW>
-__global__ void __launch_bounds__(KW * 64) qgemv_ks_kernel(const GemvArgs g, const EpiDev e) {
-  __shared__ int red[KW][MR][KS_COLS];
+template <int MR, int KW, int COLS, bool F32IN>
+__global__ void __launch_bounds__(KW * 64) qgemv_ks_kernel(const GemvArgs g, const EpiDev e, const float* x,
+                                                            int64_t ldx, float xs) {
+  constexpr int LPC = 64 / COLS;   // lanes per column
+  constexpr int SPL = LPC / 4;     // K steps per wave-wide load
+  static_assert(KW * KS_MAXS * 64 >= KS_KMAX, "one pass covers k_pad");
+  __shared__ int red[KW][MR][COLS];
+  __shared__ __attribute__((aligned(16))) int8_t xq[F32IN ? MR : 1][F32IN ? KS_KMAX : 16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n0 = blockIdx.x * KS_COLS;
-  const int col = lane >> 2, quarter = lane & 3;
+  const int n0 = blockIdx.x * COLS;
+  const int col = lane / LPC, j = lane % LPC;
   const int ksteps = g.k_pad / 64;
-  const int per_wave = (ksteps + KW - 1) / KW;
+  // each wave's share of the steps, a whole number of loads (SPL steps each)
+  const int per_wave = ((ksteps + KW - 1) / KW + SPL - 1) / SPL * SPL;
   const int s_begin = wave * per_wave, s_end = min(s_begin + per_wave, ksteps);
-  const int8_t* bcol = g.b + int64_t(n0 + col) * 64 + quarter * 16;   // n0 + 16 <= n_pad
+  const int8_t* bcol = g.b + int64_t(n0 + col) * 64 + (j & 3) * 16;   // n0 + COLS <= n_pad
   const int64_t kstep = int64_t(g.n_pad) * 64;
+  v4i w[KS_MAXS];
+#pragma unroll
+  for (int i = 0; i < KS_MAXS; ++i) {
+    const int s = min(s_begin + i * SPL + (j >> 2), ksteps - 1);   // past the share: re-read, unused
+    w[i] = *reinterpret_cast<const v4i*>(bcol + s * kstep);
+  }
+  if constexpr (F32IN) {
+    // quantize the rows into LDS, 4 bytes per thread and word, zero past K: every
+    // thread's loads first (16-byte ones where the rows allow), then the arithmetic
+    constexpr int NQ = MR * KS_KMAX / 4 / (KW * 64);   // words per thread at most
+    const int words = g.k_pad >> 2;
+    const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
+    float4 v[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int i = threadIdx.x + u * KW * 64;
+      const int m = i / words, k0 = (i - m * words) * 4;
+      v[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (m < g.M && k0 < g.lda) {
+        const float* xr = x + m * ldx + k0;
+        if (vec && k0 + 3 < g.lda) {
+          v[u] = *reinterpret_cast<const float4*>(xr);
+        } else {
+          v[u].x = xr[0];
+          if (k0 + 1 < g.lda) v[u].y = xr[1];
+          if (k0 + 2 < g.lda) v[u].z = xr[2];
+          if (k0 + 3 < g.lda) v[u].w = xr[3];
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int i = threadIdx.x + u * KW * 64;
+      if (i >= MR * words) break;
+      const int m = i / words, k0 = (i - m * words) * 4;
+      const float f[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+      uint32_t packed = 0;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (m < g.M && k0 + t < g.lda) packed |= uint32_t(uint8_t(quantize_one(f[t], xs))) << (8 * t);
+      *reinterpret_cast<uint32_t*>(&xq[m][k0]) = packed;
+    }
+    __syncthreads();
+  }
   int acc[MR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) acc[m] = 0;
-  for (int s0 = s_begin; s0 < s_end; s0 += KS_MAXS) {
-    v4i w[KS_MAXS];
 #pragma unroll
-    for (int i = 0; i < KS_MAXS; ++i) {
-      const int s = min(s0 + i, s_end - 1);   // past the share: reread its last step, unused
-      w[i] = *reinterpret_cast<const v4i*>(bcol + s * kstep);
-    }
+  for (int i = 0; i < KS_MAXS; ++i) {
+    const int s = s_begin + i * SPL + (j >> 2);
+    if (s_begin + i * SPL >= s_end) break;
+    if (s >= s_end) continue;
+    const int64_t k = int64_t(s) * 64 + (j & 3) * 16;
 #pragma unroll
-    for (int i = 0; i < KS_MAXS; ++i) {
-      const int s = s0 + i;
-      if (s >= s_end) break;
-      const int64_t k = int64_t(s) * 64 + quarter * 16;
+    for (int m = 0; m < MR; ++m) {
+      if (m >= g.M) break;
+      v4i xv = {0, 0, 0, 0};
+      if constexpr (F32IN)
+        xv = *reinterpret_cast<const v4i*>(&xq[m][k]);
+      else if (k < g.lda)   // bytes past lda meet zero weights (k >= K); lda % 16 == 0 keeps a chunk whole
+        xv = *reinterpret_cast<const v4i*>(g.a + m * g.lda + k);
 #pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        if (m >= g.M) break;
-        // bytes past lda meet zero weights (k >= K); lda % 16 == 0 keeps a chunk whole
-        v4i x = {0, 0, 0, 0};
-        if (k < g.lda) x = *reinterpret_cast<const v4i*>(g.a + m * g.lda + k);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc[m] = __builtin_amdgcn_sdot4(x[q], w[i][q], acc[m], false);
-      }
+      for (int q = 0; q < 4; ++q) acc[m] = __builtin_amdgcn_sdot4(xv[q], w[i][q], acc[m], false);
     }
   }
 #pragma unroll
-  for (int m = 0; m < MR; ++m) {
-    acc[m] += __shfl_xor(acc[m], 1, 64);
-    acc[m] += __shfl_xor(acc[m], 2, 64);
-  }
-  if (quarter == 0) {
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int off = 1; off < LPC; off <<= 1) acc[m] += __shfl_xor(acc[m], off, 64);
+  if (j == 0) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) red[wave][m][col] = acc[m];
   }
   __syncthreads();
   const int t = threadIdx.x;
-  if (t < MR * KS_COLS) {
-    const int m = t / KS_COLS, c = t % KS_COLS, n = n0 + c;
+  if (t < MR * COLS) {
+    const int m = t / COLS, c = t % COLS, n = n0 + c;
     if (m < g.M && n < g.N) {
       int32_t v = 0;
 #pragma unroll
@@ -269,6 +320,35 @@ __global__ void __launch_bounds__(256) w8gemv_kernel(const float* __restrict__ x
     }
 }
 
+// The weight-row stream for M <= 8, k_pad <= 4096: 16 columns per workgroup where
+// that gives every CU one, else 8 or 4 (n0 + COLS <= n_pad: n_pad % 32 == 0).
+template <bool F32IN, int MR>
+static void ks_launch_m(const GemvArgs& g, const EpiDev& e, const float* x, int64_t ldx, float xs,
+                        hipStream_t stream) {
+  const int64_t cus = device_cu_count();
+  const int cols = (g.N + 15) / 16 >= cus ? 16 : (g.N + 7) / 8 >= cus ? 8 : 4;
+  const dim3 grid(static_cast<unsigned>((g.N + cols - 1) / cols)), block(512);
+  if (cols == 16)
+    hipLaunchKernelGGL((qgemv_ks_kernel<MR, 8, 16, F32IN>), grid, block, 0, stream, g, e, x, ldx, xs);
+  else if (cols == 8)
+    hipLaunchKernelGGL((qgemv_ks_kernel<MR, 8, 8, F32IN>), grid, block, 0, stream, g, e, x, ldx, xs);
+  else
+    hipLaunchKernelGGL((qgemv_ks_kernel<MR, 8, 4, F32IN>), grid, block, 0, stream, g, e, x, ldx, xs);
+}
+
+template <bool F32IN>
+static void ks_launch(const GemvArgs& g, const EpiDev& e, const float* x, int64_t ldx, float xs,
+                      hipStream_t stream) {
+  if (g.M == 1)
+    ks_launch_m<F32IN, 1>(g, e, x, ldx, xs, stream);
+  else if (g.M == 2)
+    ks_launch_m<F32IN, 2>(g, e, x, ldx, xs, stream);
+  else if (g.M <= 4)
+    ks_launch_m<F32IN, 4>(g, e, x, ldx, xs, stream);
+  else
+    ks_launch_m<F32IN, 8>(g, e, x, ldx, xs, stream);
+}
+
 // M <= 8 rows: returns MR_EUNSUPPORTED for larger M (the caller uses the tiled kernel).
 int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int64_t n_pad, int64_t M,
                 int64_t N, const EpiDev& e, hipStream_t stream) {
@@ -281,16 +361,8 @@ int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, in
   g.n_pad = static_cast<int32_t>(n_pad);
   g.N = static_cast<int32_t>(N);
   g.M = static_cast<int32_t>(M);
-  if (k_pad <= 64 * 8 * KS_MAXS) {   // 8 waves, at most KS_MAXS K steps each
-    const dim3 grid(static_cast<unsigned>((N + KS_COLS - 1) / KS_COLS));   // n0 < N, n0 + 16 <= n_pad
-    if (M == 1)
-      hipLaunchKernelGGL((qgemv_ks_kernel<1, 8>), grid, dim3(512), 0, stream, g, e);
-    else if (M == 2)
-      hipLaunchKernelGGL((qgemv_ks_kernel<2, 8>), grid, dim3(512), 0, stream, g, e);
-    else if (M <= 4)
-      hipLaunchKernelGGL((qgemv_ks_kernel<4, 8>), grid, dim3(512), 0, stream, g, e);
-    else
-      hipLaunchKernelGGL((qgemv_ks_kernel<8, 8>), grid, dim3(512), 0, stream, g, e);
+  if (k_pad <= KS_KMAX) {
+    ks_launch<false>(g, e, nullptr, 0, 0.0f, stream);
     MR_LAUNCH_CHECK("qgemv");
     return MR_OK;
   }
@@ -317,6 +389,40 @@ int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, in
 }
 
 }  // namespace mr
+
+extern "C" int mr_qmatmul_f32in(const float* x, int64_t ldx, float x_scale, const int8_t* b, int64_t k_pad,
+                                int64_t n_pad, int64_t M, int64_t N, int64_t K, const mr_epilogue* epi,
+                                void* stream) {
+  MR_REQUIRE(x && b, "mr_qmatmul_f32in: NULL operand");
+  MR_REQUIRE(M >= 0 && N > 0 && K > 0, "mr_qmatmul_f32in: bad sizes M=%lld N=%lld K=%lld", (long long)M,
+             (long long)N, (long long)K);
+  MR_REQUIRE(ldx >= K && x_scale > 0.0f, "mr_qmatmul_f32in: ldx %lld < K %lld or x_scale %g <= 0", (long long)ldx,
+             (long long)K, (double)x_scale);
+  MR_REQUIRE(k_pad >= K && k_pad % 64 == 0, "mr_qmatmul_f32in: k_pad %lld must be >= K and a multiple of 64",
+             (long long)k_pad);
+  MR_REQUIRE(n_pad >= N && n_pad % 32 == 0 && N < (int64_t(1) << 30),
+             "mr_qmatmul_f32in: n_pad %lld must be >= N and a multiple of 32", (long long)n_pad);
+  MR_REQUIRE(reinterpret_cast<uintptr_t>(b) % 16 == 0, "mr_qmatmul_f32in: weights must be 16-byte aligned");
+  if (M > 8 || k_pad > mr::KS_KMAX) {
+    mr::set_error("mr_qmatmul_f32in: M=%lld rows, k_pad %lld: the fused quantize takes M <= 8 and k_pad <= %d",
+                  (long long)M, (long long)k_pad, mr::KS_KMAX);
+    return MR_EUNSUPPORTED;
+  }
+  mr::EpiDev e;
+  const int rc = mr::make_epi(epi, N, true, &e);
+  if (rc != MR_OK) return rc;
+  if (M == 0) return MR_OK;
+  mr::GemvArgs g = {};
+  g.lda = K;   // columns of x
+  g.b = b;
+  g.k_pad = static_cast<int32_t>(k_pad);
+  g.n_pad = static_cast<int32_t>(n_pad);
+  g.N = static_cast<int32_t>(N);
+  g.M = static_cast<int32_t>(M);
+  mr::ks_launch<true>(g, e, x, ldx, x_scale, static_cast<hipStream_t>(stream));
+  MR_LAUNCH_CHECK("qgemv_f32in");
+  return MR_OK;
+}
 
 extern "C" int mr_w8_matmul_f32(const float* x, int64_t ldx, const int8_t* b, const float* w_scale, int32_t w_f16,
                                 int64_t k_pad, int64_t n_pad, int64_t M, int64_t N, int64_t K,

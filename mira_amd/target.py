@@ -102,6 +102,7 @@ FLOAT_DTYPES = ("f32", "f16")
 IMAGE_OPS = ("qconv2d", "conv2d", "maxpool2d", "pad", "reduce_mean")
 
 W8_STREAM_ROWS = 64   # mr_w8_matmul_f32 streams the weights once per 8 rows when K % 4 != 0
+F32IN_MAX_ROWS, F32IN_MAX_K = 8, 4096     # mr_qmatmul_f32in's decode shapes (k_pad <= 4096)
 
 
 _UNARY_CODES = {L.EPI_FN[f] for f in L.EPI_UNARY}
@@ -461,6 +462,7 @@ class RocmExecutable:
         self._plan_attention()
         self._plan_views()
         self._plan_shared_input_matmuls()
+        self._plan_f32in_matmuls()
         for v in g.inputs:
             self._emit_input(v)
         for op in g.ops:
@@ -609,6 +611,29 @@ class RocmExecutable:
                 for u in self.users.get(op.result, []):
                     if u.kind == "reshape" and u not in self.virtual and u not in self.skip:
                         self.skip.add(u)          # read only by ops that are not run
+
+    def _plan_f32in_matmuls(self) -> None:
+        """A decode-shaped qmatmul (at most 8 rows, K <= 4096) that is the only reader of a
+        segment input's int8 copy quantizes the input's f32 rows itself (mr_qmatmul_f32in):
+        the first layer of an MLP step at batch 1 then needs no quantize launch."""
+        self.f32in: dict = {}       # qmatmul op -> the segment input whose f32 rows it reads
+        g = self.g
+        for op in g.ops:
+            if op.kind != "qmatmul" or not self._device_op(op) or op in self.row_group:
+                continue
+            v, xs = op.inputs[0], _f32key(op.attrs["x_scale"])
+            K = int(np.shape(op.attrs["q"])[0])
+            if v not in g.inputs or v in self.images or v in self.prealias or v.type.rank < 1 or \
+                    pack.roundup(K, 64) > F32IN_MAX_K or not 1 <= DevValue(v, nhwc=False).rows <= F32IN_MAX_ROWS:
+                continue
+            if any(c.inputs[0] is v for c in self.input_casts):
+                continue
+            readers = [u for u in g.ops if u.kind in ("qmatmul", "qconv2d") and u.inputs[0] is v and
+                       _f32key(u.attrs["x_scale"]) == xs]
+            if readers != [op]:
+                continue
+            self.f32in[op] = v
+            self.need_i8[v] = [t for t in self.need_i8.get(v, []) if t != xs]
 
     def _plan_views(self) -> None:
         """Two ways of not copying, decided before any buffer exists:
@@ -977,10 +1002,12 @@ class RocmExecutable:
         if op in self.row_group:
             return self._emit_qmatmul_group(self.row_group[op])
         a = op.attrs
-        x = self._src(op.inputs[0])
         q = np.asarray(a["q"], np.int8)
         K, N = q.shape
         xs = _f32key(a["x_scale"])
+        if op in self.f32in:
+            return self._emit_qmatmul_f32in(op, self.staging[self.f32in[op]])
+        x = self._src(op.inputs[0])
         xq, lda = x.i8[xs] if xs in x.i8 else self._quantize_to(x, xs)
         bl = pack.pack_matmul(q)
         b = self._upload(pack.device_weights(bl))
@@ -995,6 +1022,27 @@ class RocmExecutable:
         self._add("qmatmul", lambda s: L.check(
             lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), kp, npad, M, N, K, C.byref(e), s), "mr_qmatmul"),
             nbytes=M * K + K * N + self._epi_bytes(e, M, N), nops=2 * M * N * K)
+        self._finish_i8(out, fused)
+
+    def _emit_qmatmul_f32in(self, op: "Op", x) -> None:
+        """A qmatmul whose input is the f32 rows x (planned by _plan_f32in_matmuls)."""
+        a = op.attrs
+        q = np.asarray(a["q"], np.int8)
+        K, N = q.shape
+        bl = pack.pack_matmul(q)
+        b = self._upload(pack.device_weights(bl))
+        scale = self._upload(pack.combined_scale(a["x_scale"], a["w_scale"]))
+        out = self._new_dv(op.result)
+        e, fused = self._epilogue(op, out, False, 1, scale)
+        acc = self._acc_buffer(op, out.rows, N)
+        if acc is not None:
+            e.out_acc, e.ldacc = acc.data_ptr(), N
+        M = out.rows
+        xs = _f32key(a["x_scale"])
+        lib, kp, npad = self.lib, bl.shape[1], bl.shape[0]
+        self._add("qmatmul", lambda s: L.check(
+            lib.mr_qmatmul_f32in(x.data_ptr(), K, xs, b.data_ptr(), kp, npad, M, N, K, C.byref(e), s),
+            "mr_qmatmul_f32in"), nbytes=4 * M * K + K * N + self._epi_bytes(e, M, N), nops=2 * M * N * K)
         self._finish_i8(out, fused)
 
     def _emit_matmul(self, op: "Op") -> None:

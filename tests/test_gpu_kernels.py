@@ -105,7 +105,8 @@ def _run_qmatmul(lib, x, q, ws, xs, steps_np, next_xs=None):
                                    (25088, 384, 96),      # short K, under one 128x128 tile per CU: 64x32
                                    (25088, 64, 384),      # short K, N > 128: 128x64
                                    (3, 4096, 1000), (8, 512, 65), (2, 64, 64), (5, 192, 130),   # weight stream
-                                   (2, 5000, 96), (1, 8192, 40)])   # k_pad > 4096: lane groups per column pair
+                                   (2, 5000, 96), (1, 8192, 40),    # k_pad > 4096: lane groups per column pair
+                                   (2, 1024, 3000)])                # weight stream, 8 columns per workgroup
 def test_qmatmul_bias_relu_requant(lib, M, K, N):
     rng = np.random.default_rng(M * 7 + N)
     x = rng.standard_normal((M, K)).astype(np.float32)
@@ -122,6 +123,65 @@ def test_qmatmul_bias_relu_requant(lib, M, K, N):
     assert np.array_equal(acc, want_acc.astype(np.int32))
     assert bits_equal(y, want)
     assert bits_equal(yq, G.quantize_activation(want, next_xs).astype(np.int8))
+
+
+@pytest.mark.parametrize("M,K,N,pad", [(1, 4096, 4096, 0), (1, 4096, 1000, 0), (3, 100, 77, 1), (8, 4096, 130, 0),
+                                       (5, 1000, 33, 3), (2, 64, 2048, 0), (4, 4032, 3000, 4)])
+def test_qmatmul_f32in_equals_quantize_then_qmatmul(lib, M, K, N, pad):
+    """mr_qmatmul_f32in (the quantize inside the decode-shaped kernel) against the oracle and
+    against mr_quantize_rows + mr_qmatmul, bit for bit; pad > 0 makes the rows' stride
+    K + pad floats, so rows are not 16-byte aligned and the scalar loads run."""
+    torch = _torch()
+    rng = np.random.default_rng(M * 13 + N)
+    ldx = K + pad
+    xfull = rng.standard_normal((M, ldx)).astype(np.float32)
+    x = np.ascontiguousarray(xfull[:, :K])
+    w = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    q, ws = G.quantize_array(w, 1)
+    xs = float(np.abs(x).max()) / 127
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32",
+             "epilogue": (("add", 1, False), ("relu", None, False))}
+    want_acc = G.qmatmul_acc(x, attrs)
+    want = G.qmatmul([x, bias], attrs)
+    next_xs = float(np.abs(want).max()) / 127 or 1.0
+    acc_ref, y_ref, yq_ref = _run_qmatmul(lib, x, q, ws, xs, [("add", L.BC_COL, bias, False), ("relu", 0, None, False)],
+                                          next_xs)
+    bl = pack.pack_matmul(q)
+    b = T(pack.device_weights(bl))
+    scale = T(pack.combined_scale(xs, ws))
+    bias_t = T(bias)
+    acc = empty((M, N), torch.int32)
+    y = empty((M, N), torch.float32)
+    ldq = pack.row_stride_for(N)
+    yq = empty((M, ldq), torch.int8)
+    e = epilogue([("add", L.BC_COL, bias_t, 0, False), ("relu", 0, None, 0, False)], scale=scale, out_f32=y, ldo=N,
+                 out_i8=yq, ldq=ldq, xs=next_xs, out_acc=acc, ldacc=N)
+    xd = T(xfull)
+    L.check(lib.mr_qmatmul_f32in(xd.data_ptr(), ldx, xs, b.data_ptr(), bl.shape[1], bl.shape[0], M, N, K, C.byref(e),
+                                 stream()), "mr_qmatmul_f32in")
+    sync()
+    assert np.array_equal(acc.cpu().numpy(), want_acc.astype(np.int32))
+    assert np.array_equal(acc.cpu().numpy(), acc_ref)
+    assert bits_equal(y.cpu().numpy(), want) and bits_equal(y.cpu().numpy(), y_ref)
+    assert bits_equal(yq.cpu().numpy()[:, :N], yq_ref)
+
+
+def test_qmatmul_f32in_rejects(lib):
+    torch = _torch()
+    x = empty((16, 4096), torch.float32)
+    b = empty((64, 4096), torch.int8)
+    sc = empty((64,), torch.float64)
+    y = empty((16, 64), torch.float32)
+    e = epilogue(scale=sc, out_f32=y, ldo=64)
+    assert lib.mr_qmatmul_f32in(x.data_ptr(), 4096, 0.1, b.data_ptr(), 4096, 64, 9, 64, 4096, C.byref(e),
+                                stream()) == 3       # 9 rows: unsupported
+    assert lib.mr_qmatmul_f32in(x.data_ptr(), 4160, 0.1, b.data_ptr(), 4160, 64, 1, 64, 4100, C.byref(e),
+                                stream()) == 3       # k_pad past 4096 (nothing is launched)
+    assert lib.mr_qmatmul_f32in(x.data_ptr(), 100, 0.1, b.data_ptr(), 4096, 64, 1, 64, 4096, C.byref(e),
+                                stream()) == 1       # ldx < K
+    assert lib.mr_qmatmul_f32in(x.data_ptr(), 4096, 0.0, b.data_ptr(), 4096, 64, 1, 64, 4096, C.byref(e),
+                                stream()) == 1       # x_scale 0
 
 
 @pytest.mark.parametrize("M", [200, 4])

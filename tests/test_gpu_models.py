@@ -120,7 +120,8 @@ def test_mlp50m_batch1_whole_network():
     """Batch 1 (the decode-shaped weight-streaming qmatmul), all four layers."""
     g, _ = _quantized(models.mlp_50m, 1, (2, 3), "normal", calib_batch=8)
     runner = _compare(g, {"x": models.normal_batch((1, 4096), 1)}, fallback=False)
-    assert runner.executables("rocm")[0].kernel_counts.get("qmatmul") == 4
+    # the first layer quantizes the f32 input rows itself: four launches in all
+    assert runner.executables("rocm")[0].kernel_counts == {"qmatmul": 4}
 
 
 def test_mlp50m_batch8():
