@@ -91,12 +91,20 @@ typedef struct mr_epi_step {
  *   out_f32[row*ldo+col] = y                (if out_f32)
  *   out_i8[row*ldq+col]  = clip(rint(y / out_xs), +-127)
  *                                           (mira/ops.py:602-603, the next q-op's input)
- *   out_acc[row*ldacc+col] = acc            (int32 accumulator, if out_acc) */
+ *   out_acc[row*ldacc+col] = acc            (int32 accumulator, if out_acc)
+ * f16 values may also be stored as IEEE halves, which holds them exactly and moves
+ * half the bytes (entry points that take these flags say so; others return
+ * MR_EUNSUPPORTED):
+ *   MR_EPI_OUT_H16   out_f32 points to halves: y is rounded to f16 (as MR_EPI_OUT_F16)
+ *                    and stored as a half; ldo counts halves
+ *   MR_EPI_FULL_H16  every MR_BC_FULL operand holds halves (ld counts halves) */
 #define MR_EPI_OUT_F16 1
+#define MR_EPI_OUT_H16 2
+#define MR_EPI_FULL_H16 4
 
 typedef struct mr_epilogue {
   int32_t n_steps;
-  int32_t flags;      /* MR_EPI_OUT_F16 or 0 */
+  int32_t flags;      /* MR_EPI_OUT_F16 | MR_EPI_OUT_H16 | MR_EPI_FULL_H16, or 0 */
   mr_epi_step steps[MR_MAX_EPI];
   const double* scale;
   float* out_f32;
@@ -273,9 +281,11 @@ int mr_maxpool2d_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c,
 int mr_round_f16_f32(const float* x, int64_t n, float* y, void* stream);
 
 /* mira/ops.py:318-343 reduce_mean over H,W (NumPy order: pairwise f32 sum,
- * then f32(f64(sum) / count)).  NHWC f32 [n,hw,c] -> [n,c]; optional int8. */
+ * then f32(f64(sum) / count)).  NHWC f32 [n,hw,c] -> [n,c]; optional int8.
+ * out_f16 != 0: the mean is rounded to f16 first (an f16 graph's reduce_mean,
+ * whose .astype(float16) then feeds y and the quantize). */
 int mr_mean_hw_f32(const float* x, int32_t n, int32_t hw, int32_t c, float* y,
-                   int8_t* yq, int32_t ldq, float xs, void* stream);
+                   int8_t* yq, int32_t ldq, float xs, int32_t out_f16, void* stream);
 
 /* mira/ops.py:461-470 pad with a constant on H and W of an NHWC tensor. */
 int mr_pad_hw_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c,

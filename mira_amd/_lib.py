@@ -19,6 +19,8 @@ EPI_FN = {"add": 1, "sub": 2, "mul": 3, "div": 4, "maximum": 5, "minimum": 6, "r
 EPI_UNARY = ("relu", "gelu", "sigmoid", "tanh")
 EPI_APPROX = ("gelu", "sigmoid", "tanh")     # libm steps: not bit-identical to NumPy
 EPI_OUT_F16 = 1     # mr_epilogue.flags: round results to f16 (the op's dtype is f16)
+EPI_OUT_H16 = 2     # ... and store them as IEEE halves (out_f32 points to halves)
+EPI_FULL_H16 = 4    # full-shape operands hold IEEE halves
 # enum mr_bcast
 BC_SCALAR, BC_COL, BC_ROW, BC_FULL = 0, 1, 2, 3
 
@@ -79,7 +81,7 @@ _SIGS = {
     "mr_dwconv2d_f32": ([_p, C.POINTER(ConvGeom), _p, C.POINTER(Epilogue), _p], C.c_int),
     "mr_maxpool2d_f32": ([_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p, _p, _i32, _f32,
                           _p], C.c_int),
-    "mr_mean_hw_f32": ([_p, _i32, _i32, _i32, _p, _p, _i32, _f32, _p], C.c_int),
+    "mr_mean_hw_f32": ([_p, _i32, _i32, _i32, _p, _p, _i32, _f32, _i32, _p], C.c_int),
     "mr_pad_hw_f32": ([_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p], C.c_int),
     "mr_round_f16_f32": ([_p, _i64, _p, _p], C.c_int),
     "mr_nchw_to_nhwc_f32": ([_p, _i32, _i32, _i32, _i32, _p, _p], C.c_int),

@@ -19,7 +19,7 @@ void set_error(const char* fmt, ...) {
 
 int device_cu_count() { return g_cu_count > 0 ? g_cu_count : 256; }
 
-int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out) {
+int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out, bool allow_h16) {
   MR_REQUIRE(epi != nullptr, "epilogue descriptor is NULL");
   MR_REQUIRE(epi->n_steps >= 0 && epi->n_steps <= MR_MAX_EPI, "epilogue has %d steps (max %d)",
              epi->n_steps, MR_MAX_EPI);
@@ -29,7 +29,12 @@ int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out)
     MR_REQUIRE(epi->scale == nullptr, "this kernel has no int32 accumulator to dequantize");
   }
   MR_REQUIRE(epi->out_f32 || epi->out_i8 || epi->out_acc, "epilogue writes no output");
-  MR_REQUIRE((epi->flags & ~MR_EPI_OUT_F16) == 0, "unknown epilogue flags 0x%x", epi->flags);
+  MR_REQUIRE((epi->flags & ~(MR_EPI_OUT_F16 | MR_EPI_OUT_H16 | MR_EPI_FULL_H16)) == 0, "unknown epilogue flags 0x%x",
+             epi->flags);
+  if ((epi->flags & (MR_EPI_OUT_H16 | MR_EPI_FULL_H16)) && !allow_h16) {
+    set_error("this kernel does not take f16 values stored as halves (epilogue flags 0x%x)", epi->flags);
+    return MR_EUNSUPPORTED;
+  }
   if (epi->out_f32) MR_REQUIRE(epi->ldo >= cols, "ldo %lld < cols %lld", (long long)epi->ldo, (long long)cols);
   if (epi->out_i8) {
     MR_REQUIRE(epi->ldq >= cols, "ldq %lld < cols %lld", (long long)epi->ldq, (long long)cols);
@@ -64,7 +69,9 @@ int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out)
   out->out_i8 = epi->out_i8;
   out->ldq = epi->ldq;
   out->out_xs = epi->out_xs;
-  out->f16 = (epi->flags & MR_EPI_OUT_F16) != 0;
+  out->out_h16 = (epi->flags & MR_EPI_OUT_H16) != 0;
+  out->full_h16 = (epi->flags & MR_EPI_FULL_H16) != 0;
+  out->f16 = (epi->flags & (MR_EPI_OUT_F16 | MR_EPI_OUT_H16)) != 0;
   out->out_acc = epi->out_acc;
   out->ldacc = epi->ldacc;
   out->out_rxs = epi->out_i8 ? 1.0 / static_cast<double>(epi->out_xs) : 0.0;

@@ -238,14 +238,15 @@ __global__ void __launch_bounds__(256) maxpool_kernel(const float* __restrict__ 
 // sum by the intp count in a double-precision loop and casts back.
 __global__ void __launch_bounds__(256) mean_hw_kernel(const float* __restrict__ x, int n, int hw, int c,
                                                       float* __restrict__ y, int8_t* __restrict__ yq, int ldq,
-                                                      float xs) {
+                                                      float xs, int out_f16) {
   const int64_t total = int64_t(n) * c;
   for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
        t += (int64_t)gridDim.x * blockDim.x) {
     const int ch = static_cast<int>(t % c);
     const int64_t img = t / c;
     const float s = pairwise_sum(x + img * hw * c + ch, hw, c);
-    const float m = static_cast<float>(__ddiv_rn(static_cast<double>(s), static_cast<double>(hw)));
+    float m = static_cast<float>(__ddiv_rn(static_cast<double>(s), static_cast<double>(hw)));
+    if (out_f16) m = round_f16(m);   // an f16 op's .astype(float16), before the next q-op's quantize
     if (y) y[t] = m;
     if (yq) yq[img * ldq + ch] = quantize_one(m, xs);
   }
@@ -400,7 +401,7 @@ int mr_maxpool2d_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c,
 }
 
 int mr_mean_hw_f32(const float* x, int32_t n, int32_t hw, int32_t c, float* y, int8_t* yq, int32_t ldq, float xs,
-                   void* stream) {
+                   int32_t out_f16, void* stream) {
   MR_REQUIRE(x && (y || yq), "mr_mean_hw_f32: NULL argument");
   MR_REQUIRE(n >= 0 && hw > 0 && c > 0, "mr_mean_hw_f32: bad shape");
   if (yq) {
@@ -410,7 +411,7 @@ int mr_mean_hw_f32(const float* x, int32_t n, int32_t hw, int32_t c, float* y, i
   const int64_t total = int64_t(n) * c;
   if (total == 0) return MR_OK;
   hipLaunchKernelGGL(mr::mean_hw_kernel, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), x, n, hw, c, y, yq, ldq, xs);
+                     static_cast<hipStream_t>(stream), x, n, hw, c, y, yq, ldq, xs, out_f16 != 0);
   MR_LAUNCH_CHECK("mean_hw");
   return MR_OK;
 }

@@ -150,6 +150,8 @@ struct EpiDev {
   int64_t ldq;
   float out_xs;
   int32_t f16;     // round results to f16 after the steps (MR_EPI_OUT_F16)
+  int32_t out_h16; // out_f32 holds IEEE halves (MR_EPI_OUT_H16; implies f16)
+  int32_t full_h16;  // MR_BC_FULL operands hold IEEE halves (MR_EPI_FULL_H16)
   int32_t* out_acc;
   int64_t ldacc;
   double out_rxs;  // fl64(1 / out_xs), computed on the host
@@ -170,6 +172,23 @@ struct EpiDev {
   const float* lo_ptr;  // NULL with f_lo set: relu (maximum with +0)
   const float* hi_ptr;
 };
+
+// Element i of an array of IEEE halves that an f32 pointer stands for (an f16 value
+// stored as a half: the conversion back is exact).
+__device__ __forceinline__ float half_at(const float* p, int64_t i) {
+  return __half2float(reinterpret_cast<const __half*>(p)[i]);
+}
+
+// The half in the low 16 bits of b, as a float (exact).
+__device__ __forceinline__ float half_bits(uint32_t b) {
+  return __half2float(__ushort_as_half(static_cast<unsigned short>(b & 0xffffu)));
+}
+
+// Two f16 values (floats already rounded to f16, so the conversions are exact) as halves,
+// a in the low 16 bits.
+__device__ __forceinline__ uint32_t pack_halves(float a, float b) {
+  return uint32_t(__half_as_ushort(__float2half_rn(a))) | (uint32_t(__half_as_ushort(__float2half_rn(b))) << 16);
+}
 
 // NumPy's maximum(y, b) / minimum(y, b) for a bound b that is the same for the
 // whole wave: an unordered compare and a select.  !(y <= b) holds for y > b
@@ -208,6 +227,7 @@ __device__ __forceinline__ float epi_generic(const EpiDev& e, float y, int64_t r
     if (mode == MR_BC_SCALAR) o = p[0];
     else if (mode == MR_BC_COL) o = p[col];
     else if (mode == MR_BC_ROW) o = p[row * e.steps[s].ld];
+    else if (e.full_h16) o = half_at(p, row * e.steps[s].ld + col);
     else o = p[row * e.steps[s].ld + col];
     y = e.steps[s].swapped ? epi_binary(fn, o, y) : epi_binary(fn, y, o);
   }
@@ -218,7 +238,7 @@ __device__ __forceinline__ float epi_generic(const EpiDev& e, float y, int64_t r
 __device__ __forceinline__ float epi_fixed(const EpiDev& e, float y, int64_t row, int64_t col) {
   if (e.f_mul) y = __fmul_rn(y, e.mul_ptr[col]);
   if (e.f_col) y = __fadd_rn(y, e.col_ptr[col]);
-  if (e.f_full) y = __fadd_rn(y, e.full_ptr[row * e.full_ld + col]);
+  if (e.f_full) y = __fadd_rn(y, e.full_h16 ? half_at(e.full_ptr, row * e.full_ld + col) : e.full_ptr[row * e.full_ld + col]);
   if (e.f_lo) y = np_maximum(y, e.lo_ptr ? e.lo_ptr[0] : 0.0f);
   if (e.f_hi) y = np_minimum(y, e.hi_ptr[0]);
   return y;
@@ -237,7 +257,12 @@ __device__ __forceinline__ float epi_steps(const EpiDev& e, float y, int64_t row
 // Write the outputs for one finished result element.
 __device__ __forceinline__ void epi_store(const EpiDev& e, float y, int64_t row, int64_t col) {
   if (e.f16) y = round_f16(y);
-  if (e.out_f32) e.out_f32[row * e.ldo + col] = y;
+  if (e.out_f32) {
+    if (e.out_h16)
+      reinterpret_cast<__half*>(e.out_f32)[row * e.ldo + col] = __float2half_rn(y);
+    else
+      e.out_f32[row * e.ldo + col] = y;
+  }
   if (e.out_i8) e.out_i8[row * e.ldq + col] = quantize_rcp(y, e.out_rxs);
 }
 
@@ -254,7 +279,8 @@ constexpr int BUF_DWORD3 = 0x00020000;
 
 // ---------------------------------------------------------------- host-side epilogue validation
 
-int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out);
+// allow_h16: the caller's kernels implement MR_EPI_OUT_H16 / MR_EPI_FULL_H16
+int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out, bool allow_h16 = false);
 
 // Decode-shaped qmatmul (M <= 8 rows): weight-streaming kernel; MR_EUNSUPPORTED for larger M.
 int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int64_t n_pad, int64_t M, int64_t N,
@@ -276,7 +302,9 @@ int w8gemm_launch(const float* x, int64_t ldx, const int8_t* b, const float* w_s
 constexpr int EF_GENERIC = 0, EF_FIXED = 1, EF_SPEC = 0x100;
 constexpr int SF_COL = 1, SF_FULL = 2, SF_LO = 4, SF_HI = 8, SF_F32 = 16, SF_I8 = 32;
 constexpr int SF_MUL = 64;   // no compiled form has it: a leading mul runs the EF_FIXED path
-constexpr int SF_F16 = 128;  // results rounded to f16 (compiled for the ResNet-style forms only)
+constexpr int SF_F16 = 128;  // results rounded to f16 (compiled for the ResNet-style forms only); the
+                             // f32 result and the residual may then be stored as halves (EpiDev
+                             // out_h16 / full_h16, read at run time)
 // the forms with compiled kernels: bias+ReLU -> int8; bias+residual+ReLU -> f32
 // and/or int8; bias -> f32 (ResNet blocks, downsample and fc layers, MLPs)
 constexpr int SPEC_RELU_I8 = SF_COL | SF_LO | SF_I8;
@@ -308,13 +336,13 @@ inline int spec_form(const EpiDev& e) {
   if (e.f_mul) f |= SF_MUL;
   if (e.f_col) f |= SF_COL;
   if (e.f_full) {
-    if (!al(e.full_ptr, e.full_ld, 16)) return -1;
+    if (!al(e.full_ptr, e.full_ld, e.full_h16 ? 8 : 16)) return -1;
     f |= SF_FULL;
   }
   if (e.f_lo) f |= SF_LO;
   if (e.f_hi) f |= SF_HI;
   if (e.out_f32) {
-    if (!al(e.out_f32, e.ldo, 16)) return -1;
+    if (!al(e.out_f32, e.ldo, e.out_h16 ? 8 : 16)) return -1;
     f |= SF_F32;
   }
   if (e.out_i8) {

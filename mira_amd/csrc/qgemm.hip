@@ -34,6 +34,7 @@
 
 namespace mr {
 
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -182,8 +183,8 @@ __device__ __forceinline__ uint32_t quantize4_med3(const float (&y)[4], double r
 
 __device__ __forceinline__ void load_cols4(const EpiDev& e, int col0, int N, EpiCols4& c) {
   bool vec = col0 + 3 < N && (e.ldo % 4 == 0) && (e.ldq % 4 == 0) && (e.ldacc % 4 == 0) &&
-             (reinterpret_cast<uintptr_t>(e.out_f32) % 16 == 0) && (reinterpret_cast<uintptr_t>(e.out_i8) % 4 == 0) &&
-             (reinterpret_cast<uintptr_t>(e.out_acc) % 16 == 0);
+             (reinterpret_cast<uintptr_t>(e.out_f32) % (e.out_h16 ? 8 : 16) == 0) &&
+             (reinterpret_cast<uintptr_t>(e.out_i8) % 4 == 0) && (reinterpret_cast<uintptr_t>(e.out_acc) % 16 == 0);
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     c.scale[k] = col0 + k < N ? e.scale[col0 + k] : 0.0;
@@ -194,7 +195,8 @@ __device__ __forceinline__ void load_cols4(const EpiDev& e, int col0, int N, Epi
   c.hi = e.f_hi ? e.hi_ptr[0] : 0.0f;
   c.lo_nan = c.lo != c.lo;
   c.hi_nan = c.hi != c.hi;
-  if (e.f_full) vec = vec && (e.full_ld % 4 == 0) && (reinterpret_cast<uintptr_t>(e.full_ptr) % 16 == 0);
+  if (e.f_full)
+    vec = vec && (e.full_ld % 4 == 0) && (reinterpret_cast<uintptr_t>(e.full_ptr) % (e.full_h16 ? 8 : 16) == 0);
   c.vec = vec;
 }
 
@@ -216,14 +218,25 @@ __device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, c
       for (int k = 0; k < 4; ++k) y[k] = __fadd_rn(y[k], c.colv[k]);
     }
     if (e.f_full) {
-      const float* p = e.full_ptr + row * e.full_ld + col0;
       float o[4];
-      if (c.vec) {
-        const float4 v = *reinterpret_cast<const float4*>(p);
-        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
-      } else {
+      if (e.full_h16) {
+        const __half* p = reinterpret_cast<const __half*>(e.full_ptr) + row * e.full_ld + col0;
+        if (c.vec) {
+          const uint2 v = *reinterpret_cast<const uint2*>(p);
+          o[0] = half_bits(v.x); o[1] = half_bits(v.x >> 16); o[2] = half_bits(v.y); o[3] = half_bits(v.y >> 16);
+        } else {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) o[k] = col0 + k < N ? p[k] : 0.0f;
+          for (int k = 0; k < 4; ++k) o[k] = col0 + k < N ? __half2float(p[k]) : 0.0f;
+        }
+      } else {
+        const float* p = e.full_ptr + row * e.full_ld + col0;
+        if (c.vec) {
+          const float4 v = *reinterpret_cast<const float4*>(p);
+          o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) o[k] = col0 + k < N ? p[k] : 0.0f;
+        }
       }
 #pragma unroll
       for (int k = 0; k < 4; ++k) y[k] = __fadd_rn(y[k], o[k]);
@@ -247,7 +260,13 @@ __device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, c
   }
   if (c.vec) {
     if (e.out_acc) *reinterpret_cast<v4i*>(e.out_acc + row * e.ldacc + col0) = acc;
-    if (e.out_f32) *reinterpret_cast<float4*>(e.out_f32 + row * e.ldo + col0) = make_float4(y[0], y[1], y[2], y[3]);
+    if (e.out_f32) {
+      if (e.out_h16)
+        *reinterpret_cast<uint2*>(reinterpret_cast<__half*>(e.out_f32) + row * e.ldo + col0) =
+            make_uint2(pack_halves(y[0], y[1]), pack_halves(y[2], y[3]));
+      else
+        *reinterpret_cast<float4*>(e.out_f32 + row * e.ldo + col0) = make_float4(y[0], y[1], y[2], y[3]);
+    }
     if (e.out_i8) {
       uint32_t packed = 0;
 #pragma unroll
@@ -273,7 +292,7 @@ __device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, c
 // workgroup per CU hides more of that latency than the registers it costs.
 template <int BM, int BN, int WM, int WN, int STAGES, int AMODE, int EF, int KB = 64>
 __global__ void __launch_bounds__(WM* WN * 64)
-    __attribute__((amdgpu_waves_per_eu((AMODE == A_PATCH && BN == 64) ? 4 : 1)))
+    __attribute__((amdgpu_waves_per_eu((AMODE == A_PATCH && BN == 64) || (BM == 128 && BN == 256 && KB == 64) ? 4 : 1)))
     qgemm_kernel(const GemmArgs g, const EpiDev e) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM;
@@ -654,29 +673,40 @@ __global__ void __launch_bounds__(WM* WN * 64)
         constexpr int NR = EP_ROWS / RSTEP;
         static_assert(EP_ROWS % RSTEP == 0, "epilogue rows per thread");
         // rows in flight at once: all of them, or 4 when each also holds a residual
-        constexpr int NRC = S_FULL && NR > 4 ? 4 : NR;
+        // (2 for the 128x256 tiles held to 128 VGPRs, whose residual forms would spill with 4)
+        constexpr int NRC = S_FULL && NR > 4 ? (BM == 128 && BN == 256 && KB == 64 ? 2 : 4) : NR;
         static_assert(NR % NRC == 0, "epilogue row chunks");
         // residual rows of chunk c (rows past the tile re-read its last row); the
         // next chunk's are loaded before this chunk's stores, which the compiler
         // may not move loads across
-        auto load_res = [&](int c0, float4 (&res)[S_FULL ? NRC : 1]) __attribute__((always_inline)) {
+        // residual rows as raw bits: 4 floats, or (an f16 graph's halves) 4 halves in x, y
+        const bool res_h16 = S_F16 && e.full_h16;
+        const bool out_h16 = S_F16 && e.out_h16;
+        auto load_res = [&](int c0, v4i (&res)[S_FULL ? NRC : 1]) __attribute__((always_inline)) {
           if constexpr (S_FULL) {
 #pragma unroll
             for (int k = 0; k < NRC; ++k) {
               const int rr = threadIdx.x / CG + (c0 + k) * RSTEP;
               const int lk = (rr >> 5) * TM + pass * 32 + (rr & 31);
               const int64_t r = mbase + min(lk, mvalid - 1);
-              res[k] = *reinterpret_cast<const float4*>(e.full_ptr + r * e.full_ld + rcol);
+              if (res_h16) {
+                const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(e.full_ptr) +
+                                                                r * e.full_ld + rcol);
+                res[k] = v4i{int(h.x), int(h.y), 0, 0};
+              } else {
+                res[k] = *reinterpret_cast<const v4i*>(e.full_ptr + r * e.full_ld + rcol);
+              }
             }
           }
         };
         // the tile's result rows as raw buffers: a row past mvalid lies past num_records,
         // so its store is dropped by the hardware, and offsets are 32-bit
         const __amdgpu_buffer_rsrc_t rf = __builtin_amdgcn_make_buffer_rsrc(
-            e.out_f32 + mbase * e.ldo, 0, S_F32 ? mvalid * int(e.ldo) * 4 : 0, BUF_DWORD3);
+            reinterpret_cast<char*>(e.out_f32) + mbase * e.ldo * (out_h16 ? 2 : 4), 0,
+            S_F32 ? mvalid * int(e.ldo) * (out_h16 ? 2 : 4) : 0, BUF_DWORD3);
         const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
             e.out_i8 + mbase * e.ldq, 0, S_I8 ? mvalid * int(e.ldq) : 0, BUF_DWORD3);
-        float4 res_cur[S_FULL ? NRC : 1], res_next[S_FULL ? NRC : 1];
+        v4i res_cur[S_FULL ? NRC : 1], res_next[S_FULL ? NRC : 1];
         load_res(0, res_cur);
 #pragma unroll
         for (int k0 = 0; k0 < NR; k0 += NRC) {
@@ -691,8 +721,15 @@ __global__ void __launch_bounds__(WM* WN * 64)
         float y[NRC][4];
 #pragma unroll
         for (int k = 0; k < NRC; ++k) {
-          const float o[4] = {res_cur[S_FULL ? k : 0].x, res_cur[S_FULL ? k : 0].y, res_cur[S_FULL ? k : 0].z,
-                              res_cur[S_FULL ? k : 0].w};
+          const v4i rb = res_cur[S_FULL ? k : 0];
+          float o[4];
+          if (res_h16) {
+            o[0] = half_bits(uint32_t(rb[0])); o[1] = half_bits(uint32_t(rb[0]) >> 16);
+            o[2] = half_bits(uint32_t(rb[1])); o[3] = half_bits(uint32_t(rb[1]) >> 16);
+          } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o[c] = __int_as_float(rb[c]);
+          }
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             float t = dequant(a[k][c], cols.scale[c]);
@@ -710,13 +747,22 @@ __global__ void __launch_bounds__(WM* WN * 64)
           const int lr = local[k];       // rows past mvalid: dropped by the resource's bound
           if (!cok) continue;
           if constexpr (S_F32) {
-            const v4i v = {int(__float_as_uint(y[k][0])), int(__float_as_uint(y[k][1])),
-                           int(__float_as_uint(y[k][2])), int(__float_as_uint(y[k][3]))};
-            const int off = (lr * int(e.ldo) + col0) * 4;
-            if (e.nt_f32)
-              __builtin_amdgcn_raw_buffer_store_b128(v, rf, off, 0, 2);   // nt
-            else
-              __builtin_amdgcn_raw_buffer_store_b128(v, rf, off, 0, 0);
+            if (out_h16) {
+              const v2i v = {int(pack_halves(y[k][0], y[k][1])), int(pack_halves(y[k][2], y[k][3]))};
+              const int off = (lr * int(e.ldo) + col0) * 2;
+              if (e.nt_f32)
+                __builtin_amdgcn_raw_buffer_store_b64(v, rf, off, 0, 2);   // nt
+              else
+                __builtin_amdgcn_raw_buffer_store_b64(v, rf, off, 0, 0);
+            } else {
+              const v4i v = {int(__float_as_uint(y[k][0])), int(__float_as_uint(y[k][1])),
+                             int(__float_as_uint(y[k][2])), int(__float_as_uint(y[k][3]))};
+              const int off = (lr * int(e.ldo) + col0) * 4;
+              if (e.nt_f32)
+                __builtin_amdgcn_raw_buffer_store_b128(v, rf, off, 0, 2);   // nt
+              else
+                __builtin_amdgcn_raw_buffer_store_b128(v, rf, off, 0, 0);
+            }
           }
           if constexpr (S_I8)
             __builtin_amdgcn_raw_buffer_store_b32(quantize4_med3(y[k], e.out_rxs), rq, lr * int(e.ldq) + col0, 0, 0);
@@ -765,6 +811,8 @@ static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
       case SPEC_RELU_I8 | SF_F16: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RELU_I8 | SF_F16); return;
       case SPEC_RES_F32_I8 | SF_F16: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_F32_I8 | SF_F16); return;
       case SPEC_BIAS_F32 | SF_F16: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_F32 | SF_F16); return;
+      case SPEC_RES_I8 | SF_F16: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_I8 | SF_F16); return;
+      case SPEC_RES_F32 | SF_F16: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_F32 | SF_F16); return;
       default: break;
     }
   }
@@ -863,7 +911,7 @@ static bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 1
 // launch (MobileNetV2's 231 MB expansions feeding their depthwise convs), stay cached.
 static bool stream_f32(const EpiDev& e, int64_t M) {
   if (!e.out_f32) return false;
-  const int64_t bytes = M * e.ldo * 4;
+  const int64_t bytes = M * e.ldo * (e.out_h16 ? 2 : 4);
   return bytes >= (int64_t(256) << 20) || (e.fixed && e.f_full && bytes >= (int64_t(96) << 20));
 }
 
@@ -887,7 +935,7 @@ int mr_qmatmul(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int
              (long long)mr::MAX_EXACT_K);
   MR_REQUIRE(mr::aligned16(a) && mr::aligned16(b), "mr_qmatmul: operands must be 16-byte aligned");
   mr::EpiDev e;
-  int rc = mr::make_epi(epi, N, true, &e);
+  int rc = mr::make_epi(epi, N, true, &e, true);
   if (rc != MR_OK) return rc;
   if (M == 0) return MR_OK;
   e.nt_f32 = mr::stream_f32(e, M);
@@ -944,7 +992,7 @@ int mr_qconv2d(const int8_t* x, const mr_conv_geom* cg, const int8_t* b, int64_t
              "overflow", (long long)mr::MAX_EXACT_K);
   MR_REQUIRE(mr::aligned16(x) && mr::aligned16(b), "mr_qconv2d: operands must be 16-byte aligned");
   mr::EpiDev e;
-  const int rc = mr::make_epi(epi, G.o, true, &e);
+  const int rc = mr::make_epi(epi, G.o, true, &e, true);
   if (rc != MR_OK) return rc;
   const int64_t M = int64_t(G.n) * oh * ow;
   if (M == 0) return MR_OK;

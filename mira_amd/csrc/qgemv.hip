@@ -409,7 +409,7 @@ extern "C" int mr_qmatmul_f32in(const float* x, int64_t ldx, float x_scale, cons
     return MR_EUNSUPPORTED;
   }
   mr::EpiDev e;
-  const int rc = mr::make_epi(epi, N, true, &e);
+  const int rc = mr::make_epi(epi, N, true, &e, true);
   if (rc != MR_OK) return rc;
   if (M == 0) return MR_OK;
   mr::GemvArgs g = {};

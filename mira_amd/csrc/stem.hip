@@ -363,15 +363,24 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
     const int top = p * PS - PPL;
     const bool pad_rows = top < 0 || top + PK > a.OH;
     const int64_t row0 = (int64_t(img) * a.POH + p) * a.POW;
+    // f32 results, or (an f16 graph's values stored as halves) 2-byte halves
+    const int fb = e.out_h16 ? 2 : 4;
     const __amdgpu_buffer_rsrc_t rf = __builtin_amdgcn_make_buffer_rsrc(
-        e.out_f32 + row0 * e.ldo, 0, e.out_f32 ? a.POW * int(e.ldo) * 4 : 0, BUF_DWORD3);
+        reinterpret_cast<char*>(e.out_f32) + row0 * e.ldo * fb, 0, e.out_f32 ? a.POW * int(e.ldo) * fb : 0,
+        BUF_DWORD3);
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
         e.out_i8 + row0 * e.ldq, 0, e.out_i8 ? a.POW * int(e.ldq) : 0, BUF_DWORD3);
+    auto store_f = [&](float y, __amdgpu_buffer_rsrc_t r, uint32_t of) __attribute__((always_inline)) {
+      if (e.out_h16)
+        __builtin_amdgcn_raw_buffer_store_b16(__half_as_ushort(__float2half_rn(y)), r, of, 0, 0);
+      else
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), r, of, 0, 0);
+    };
     auto offs = [&](int j, int t, uint32_t& of, uint32_t& oq) __attribute__((always_inline)) {
       const int ch = j * 32 + (lane & 31);
       const int pc = wave * PPW + 8 * half + t;
       const bool ok = ((col_ok >> t) & 1) && ch < a.O;
-      of = ok ? uint32_t((pc * int(e.ldo) + ch) * 4) : 0x80000000u;
+      of = ok ? uint32_t((pc * int(e.ldo) + ch) * fb) : 0x80000000u;
       oq = ok ? uint32_t(pc * int(e.ldq) + ch) : 0x80000000u;
     };
     if constexpr (EF >= EF_SPEC) {
@@ -387,7 +396,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
             if constexpr ((EF & SF_LO) != 0) y = y > lo ? y : lo;
             if constexpr ((EF & SF_HI) != 0) y = y < hi ? y : hi;
             if constexpr ((EF & SF_F16) != 0) y = round_f16(y);
-            if constexpr ((EF & SF_F32) != 0) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rf, of, 0, 0);
+            if constexpr ((EF & SF_F32) != 0) store_f(y, rf, of);
             if constexpr ((EF & SF_I8) != 0) {
               const float tq = rintf(static_cast<float>(__dmul_rn(static_cast<double>(y), e.out_rxs)));
               __builtin_amdgcn_raw_buffer_store_b8(
@@ -425,7 +434,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
           if (e.f16) y = round_f16(y);
           if (!pad_inert) y = np_maximum(y, padded ? a.pad_value : -INFINITY);
         }
-        if (e.out_f32) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rf, of, 0, 0);
+        if (e.out_f32) store_f(y, rf, of);
         if (e.out_i8) __builtin_amdgcn_raw_buffer_store_b8(quantize_rcp(y, e.out_rxs), rq, oq, 0, 0);
       }
   };
@@ -576,7 +585,7 @@ static int stem_setup(const char* who, const mr_conv_geom* cg, const int8_t* b, 
     return MR_EUNSUPPORTED;
   }
   MR_REQUIRE(reinterpret_cast<uintptr_t>(b) % 16 == 0, "%s: misaligned weights", who);
-  const int rc = make_epi(epi, G.o, true, e);
+  const int rc = make_epi(epi, G.o, true, e, true);
   if (rc != MR_OK) return rc;
   MR_REQUIRE(!epi->out_acc, "%s: no int32 accumulator output (the convolution is not stored)", who);
   StemArgs a = {};

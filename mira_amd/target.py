@@ -73,6 +73,7 @@ class DevValue:
     f32: object = None                           # torch tensor (NHWC or row-major)
     i8: dict = field(default_factory=dict)       # f32 x_scale -> (torch int8 tensor, row stride)
     alias_of: Optional["DevValue"] = None
+    half: bool = False                           # f32 holds an f16 value's IEEE halves (torch float16)
 
     @property
     def rows(self) -> int:
@@ -93,9 +94,12 @@ class DevValue:
 
 
 # Result dtypes the kernels produce.  f16 values (the reference's default precision for
-# accelerator targets, mira/passes.py:206-253) stay stored as f32 on the device: every op
-# computes in f32 as the reference's ops do (mira/ops.py:43-44) and rounds its result to
-# f16 where the reference casts it (.astype(float16)), so f16 results are bit-exact too.
+# accelerator targets, mira/passes.py:206-253): every op computes in f32 as the reference's
+# ops do (mira/ops.py:43-44) and rounds its result to f16 where the reference casts it
+# (.astype(float16)), so f16 results are bit-exact too.  They are stored as IEEE halves
+# where the producer and every reader take halves (_plan_half_storage: the results of the
+# int8 convolutions and the fused stem that only convolutions read, as their input's int8
+# copy or as the residual), else as the f32 they equal exactly.
 FLOAT_DTYPES = ("f32", "f16")
 
 # ops whose rank-4 operands and results are images, stored NHWC
@@ -463,6 +467,7 @@ class RocmExecutable:
         self._plan_views()
         self._plan_shared_input_matmuls()
         self._plan_f32in_matmuls()
+        self._plan_half_storage()
         for v in g.inputs:
             self._emit_input(v)
         for op in g.ops:
@@ -635,6 +640,42 @@ class RocmExecutable:
             self.f32in[op] = v
             self.need_i8[v] = [t for t in self.need_i8.get(v, []) if t != xs]
 
+    def _full_operand_reader(self, u: "Op", v: "Value") -> bool:
+        """Does the q-op u read v only as its int8 input (inputs[0]: the copy v's producer
+        writes) and/or as the one full-shape operand of its epilogue?"""
+        if u.kind not in ("qconv2d", "qmatmul") or not self._device_op(u):
+            return False
+        is_conv = u.kind == "qconv2d"
+        full = [idx for _, idx, _ in u.attrs.get("epilogue", ()) if idx is not None and
+                u.inputs[idx] not in self.consts and
+                _bcast_mode(u.inputs[idx].type.shape, u.result.type.shape, is_conv) == L.BC_FULL]
+        steps = {idx for _, idx, _ in u.attrs.get("epilogue", ()) if idx is not None}
+        for i, x in enumerate(u.inputs):
+            if x is not v or i == 0:
+                continue
+            if i not in steps or i not in full or len(set(u.inputs[j] for j in full)) != 1:
+                return False
+        return True
+
+    def _plan_half_storage(self) -> None:
+        """f16 values stored as IEEE halves (mr_epilogue's MR_EPI_OUT_H16 / MR_EPI_FULL_H16):
+        an f16 result of an int8 convolution or of the fused stem that is not a segment
+        output, whose producer writes at most one int8 copy, and that only q-ops read -- as
+        their int8 input or as the residual of their epilogue.  The halves hold the same
+        values as the f32 copies would, in half the bytes."""
+        self.half: set = set()
+        g = self.g
+        stem_convs = {conv for conv, _ in self.fused_stem.values()}
+        for op in g.ops:
+            if not ((op.kind == "qconv2d" and self._device_op(op) and op not in stem_convs) or
+                    (op.kind == "maxpool2d" and op in self.fused_stem)):
+                continue
+            v = op.result
+            if v.type.dtype != "f16" or v in g.outputs or v not in self.need_f32 or len(self.need_i8.get(v, [])) > 1:
+                continue
+            if all(self._full_operand_reader(u, v) for u in self.users.get(v, [])):
+                self.half.add(v)
+
     def _plan_views(self) -> None:
         """Two ways of not copying, decided before any buffer exists:
         * a transpose whose result is read only as a matmul operand (directly or through
@@ -775,11 +816,11 @@ class RocmExecutable:
         """Allocate v's f32 copy if anything reads it; int8 copies only for segment inputs
         (producers allocate the ones they write)."""
         torch = _t()
-        d = DevValue(v, nhwc=v in self.images)
+        d = DevValue(v, nhwc=v in self.images, half=v in self.half)
         if v in self.need_f32:
             s = v.type.shape
             shape = (s[0], s[2], s[3], s[1]) if d.nhwc else s
-            d.f32 = torch.empty(shape, dtype=torch.float32, device=self.dev)
+            d.f32 = torch.empty(shape, dtype=torch.float16 if d.half else torch.float32, device=self.dev)
         if with_i8:
             for xs in self.need_i8.get(v, []):
                 d.i8[xs] = (torch.empty((d.rows, d.i8_ld()), dtype=torch.int8, device=self.dev), d.i8_ld())
@@ -874,12 +915,13 @@ class RocmExecutable:
     def _epi_bytes(e, rows: int, cols: int) -> int:
         """Bytes the epilogue moves: full-shape operands read, f32/int8 results written."""
         n = 8 * cols if e.scale else 0
+        full_b = 2 if e.flags & L.EPI_FULL_H16 else 4
         for i in range(e.n_steps):
             st = e.steps[i]
             if st.fn not in _UNARY_CODES:
-                n += {L.BC_SCALAR: 4, L.BC_COL: 4 * cols, L.BC_ROW: 4 * rows, L.BC_FULL: 4 * rows * cols}[st.mode]
+                n += {L.BC_SCALAR: 4, L.BC_COL: 4 * cols, L.BC_ROW: 4 * rows, L.BC_FULL: full_b * rows * cols}[st.mode]
         if e.out_f32:
-            n += 4 * rows * cols
+            n += (2 if e.flags & L.EPI_OUT_H16 else 4) * rows * cols
         if e.out_i8:
             n += rows * cols
         return n
@@ -889,6 +931,8 @@ class RocmExecutable:
     def _quantize_to(self, d: DevValue, xs: float):
         """Schedule a standalone quantize of d's f32 copy (mira/ops.py:602-603)."""
         torch = _t()
+        if d.half:
+            raise L.RocmError("internal: a half-stored value has no standalone quantize")
         ld = d.i8_ld()
         q = torch.empty((d.rows, ld), dtype=torch.int8, device=self.dev)
         lib, src, rows, cols = self.lib, d.f32, d.rows, d.cols
@@ -914,6 +958,8 @@ class RocmExecutable:
         rshape = op.result.type.shape
         e.n_steps = len(steps)
         e.flags = L.EPI_OUT_F16 if op.result.type.dtype == "f16" else 0
+        if out.half:
+            e.flags |= L.EPI_OUT_H16
         for i, (fn, idx, sw) in enumerate(steps):
             st = e.steps[i]
             st.fn = L.EPI_FN[fn]
@@ -927,6 +973,10 @@ class RocmExecutable:
                 mode = _bcast_mode(v.type.shape, rshape, is_conv)
                 t = self.dv[v].f32
                 ld = out.cols if mode == L.BC_FULL else 1
+                if self.dv[v].half:
+                    if mode != L.BC_FULL:
+                        raise L.RocmError(f"{op.kind}: a half-stored operand must be full-shape")
+                    e.flags |= L.EPI_FULL_H16
             st.mode, st.ptr, st.ld = mode, t.data_ptr(), ld
         e.scale = _ptr(scale)
         e.out_f32 = _ptr(out.f32)
@@ -1296,11 +1346,9 @@ class RocmExecutable:
         x = self._src(op.inputs[0])
         n, c, h, w = op.inputs[0].type.shape
         out = self._new_dv(op.result)
-        f16 = op.result.type.dtype == "f16"
-        if f16 and out.f32 is None:
-            out.f32 = _t().empty((out.rows, out.cols), dtype=_t().float32, device=self.dev)
+        f16 = int(op.result.type.dtype == "f16")      # the kernel rounds the mean to f16 first
         wants = self.need_i8.get(op.result, [])
-        fused = wants[0] if wants and not f16 else None     # f16: quantize the rounded mean
+        fused = wants[0] if wants else None
         yq, ld = None, 0
         if fused is not None:
             ld = out.i8_ld()
@@ -1309,10 +1357,8 @@ class RocmExecutable:
         lib, xt, yt = self.lib, x.f32, out.f32
         xsv = fused if fused is not None else 1.0
         self._add("mean_hw", lambda s: L.check(lib.mr_mean_hw_f32(
-            xt.data_ptr(), n, h * w, c, _ptr(yt), _ptr(yq), ld, xsv, s), "mr_mean_hw_f32"),
+            xt.data_ptr(), n, h * w, c, _ptr(yt), _ptr(yq), ld, xsv, f16, s), "mr_mean_hw_f32"),
             nbytes=4 * n * h * w * c + (4 if yt is not None else 0) * n * c + (n * ld if yq is not None else 0))
-        if f16:
-            self._round_f16(yt, yt)
         self._finish_i8(out, fused)
 
     def _round_f16(self, src, dst) -> None:

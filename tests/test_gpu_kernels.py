@@ -607,16 +607,27 @@ FORM_CONV_CASES = [
 ]
 
 
-# forms of an f16 graph (results rounded to f16; operands are f16 values)
-F16_FORMS = ["relu_i8_f16", "res_f32_i8_f16", "bias_f32_f16", "bias_relu6_f32_f16"]
+# forms of an f16 graph (results rounded to f16; operands are f16 values); _h16: the
+# residual and the f32 result stored as IEEE halves, _h16r: only the residual
+F16_FORMS = ["relu_i8_f16", "res_f32_i8_f16", "bias_f32_f16", "bias_relu6_f32_f16",
+             "res_f32_i8_h16", "res_i8_h16", "res_f32_h16", "bias_f32_h16", "res_f32_i8_h16r", "res_f32_h16r",
+             "bias_res_f32_i8_h16", "bn_res_f32_i8_h16"]
+
+
+def _form_parts(form):
+    """(base form, f16 graph, residual as halves, f32 result as halves)"""
+    for suffix, res_h, out_h in (("_h16r", True, False), ("_h16", True, True), ("_f16", False, False)):
+        if form.endswith(suffix):
+            return form[:-len(suffix)], True, res_h, out_h
+    return form, False, False, False
 
 
 @pytest.mark.parametrize("form", list(FORMS) + F16_FORMS)
 @pytest.mark.parametrize("n,c,h,w,o,k,s,p,d", FORM_CONV_CASES)
 def test_qconv2d_epilogue_forms(lib, form, n, c, h, w, o, k, s, p, d):
     torch = _torch()
-    f16 = form.endswith("_f16")
-    steps, want_f32, want_i8 = FORMS[form[:-4] if f16 else form]
+    base, f16, res_h16, out_h16 = _form_parts(form)
+    steps, want_f32, want_i8 = FORMS[base]
     rng = np.random.default_rng(n * 1000 + c * 10 + k + 7)
     x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
     wt = rng.standard_normal((o, c, k, k)).astype(np.float32)
@@ -641,25 +652,40 @@ def test_qconv2d_epilogue_forms(lib, form, n, c, h, w, o, k, s, p, d):
     b = T(pack.device_weights(bl))
     scale = T(pack.combined_scale(xs, ws))
     g = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=cp, o=o, oh=oh, ow=ow, kh=k, kw=k, sh=s, sw=s, ph=p, pw=p, dh=d, dw=d)
-    operands = {1: (L.BC_COL, T(bias.reshape(o)), 0), 2: (L.BC_FULL, T(res.transpose(0, 2, 3, 1).reshape(M, o)), o),
+    res_nhwc = res.transpose(0, 2, 3, 1).reshape(M, o)
+    operands = {1: (L.BC_COL, T(bias.reshape(o)), 0),
+                2: (L.BC_FULL, T(res_nhwc.astype(np.float16) if res_h16 else res_nhwc), o),
                 3: (L.BC_SCALAR, T(zero.reshape(1)), 0), 4: (L.BC_SCALAR, T(six.reshape(1)), 0),
                 5: (L.BC_COL, T(bn.reshape(o)), 0)}
     dev_steps = [(fn, 0, None, 0, sw) if idx is None else (fn, operands[idx][0], operands[idx][1], operands[idx][2], sw)
                  for fn, idx, sw in steps]
-    y = empty((M, o), torch.float32) if want_f32 else None
+    y = empty((M, o), torch.float16 if out_h16 else torch.float32) if want_f32 else None
     ocp = pack.c_pad_for(o)
     yq = empty((M, ocp), torch.int8) if want_i8 else None
     e = epilogue(dev_steps, scale=scale, out_f32=y, ldo=o if want_f32 else 0, out_i8=yq, ldq=ocp if want_i8 else 0,
                  xs=next_xs)
-    e.flags = L.EPI_OUT_F16 if f16 else 0
+    e.flags = (L.EPI_OUT_F16 if f16 else 0) | (L.EPI_OUT_H16 if out_h16 else 0) | (L.EPI_FULL_H16 if res_h16 else 0)
     L.check(lib.mr_qconv2d(xq.data_ptr(), C.byref(g), b.data_ptr(), bl.shape[1], bl.shape[0], C.byref(e), stream()),
             "mr_qconv2d")
     sync()
     to_nhwc = lambda a: a.transpose(0, 2, 3, 1).reshape(M, o)
     if want_f32:
-        assert bits_equal(y.cpu().numpy(), to_nhwc(want).astype(np.float32))
+        assert bits_equal(y.cpu().numpy().astype(np.float32), to_nhwc(want).astype(np.float32))
     if want_i8:
         assert bits_equal(yq.cpu().numpy()[:, :o], to_nhwc(G.quantize_activation(want, next_xs)).astype(np.int8))
+
+
+def test_half_storage_flags_rejected_where_unsupported(lib):
+    """Kernels without half-storage paths refuse the MR_EPI_*_H16 flags."""
+    torch = _torch()
+    x = empty((2, 8, 8, 16), torch.float32)
+    wt = empty((9, 16), torch.float32)
+    y = empty((128, 16), torch.float16)
+    e = epilogue(out_f32=y, ldo=16)
+    e.flags = L.EPI_OUT_H16
+    g = L.ConvGeom(n=2, h=8, w=8, c=16, c_pad=16, o=16, oh=8, ow=8, kh=3, kw=3, sh=1, sw=1, ph=1, pw=1, dh=1, dw=1)
+    assert lib.mr_dwconv2d_f32(x.data_ptr(), C.byref(g), wt.data_ptr(), C.byref(e), stream()) == 3
+    assert "halves" in lib.mr_last_error().decode()
 
 
 @pytest.mark.parametrize("form", ["relu_i8", "bias_f32", "res_f32_i8"])
@@ -768,17 +794,27 @@ def test_maxpool_with_folded_pad(lib):
 
 
 @pytest.mark.parametrize("hw", [(7, 7), (1, 5), (14, 14), (56, 56)])
-def test_mean_hw(lib, hw):
+@pytest.mark.parametrize("f16", [False, True])
+def test_mean_hw(lib, hw, f16):
+    """The mean over H*W in NumPy's order; with f16 (an f16 graph) its f16 rounding, and the
+    int8 quantize of that rounded mean."""
     torch = _torch()
     rng = np.random.default_rng(hw[0])
     n, c = 3, 512
     x = (rng.standard_normal((n, c) + hw) * 4).astype(np.float32)
+    if f16:
+        x = x.astype(np.float16).astype(np.float32)
     want = G.reduce("reduce_mean", [x], {"axes": (2, 3), "keepdims": True}).reshape(n, c)
+    if f16:
+        want = want.astype(np.float16).astype(np.float32)
+    xs = float(np.abs(want).max()) / 127
     y = empty((n, c), torch.float32)
-    L.check(lib.mr_mean_hw_f32(T(x.transpose(0, 2, 3, 1)).data_ptr(), n, hw[0] * hw[1], c, y.data_ptr(), None, 0,
-                               1.0, stream()), "mean")
+    yq = empty((n, c), torch.int8)
+    L.check(lib.mr_mean_hw_f32(T(x.transpose(0, 2, 3, 1)).data_ptr(), n, hw[0] * hw[1], c, y.data_ptr(),
+                               yq.data_ptr(), c, xs, int(f16), stream()), "mean")
     sync()
     assert bits_equal(y.cpu().numpy(), want)
+    assert bits_equal(yq.cpu().numpy(), G.quantize_activation(want, xs).astype(np.int8))
 
 
 def test_pad_and_layouts(lib):

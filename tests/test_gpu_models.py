@@ -168,6 +168,10 @@ def test_resnet18_batch2_fused_stem(bn_epilogue, precision):
     exe = runner.executables("rocm")[0]
     assert exe.kernel_counts.get("qconv2d_maxpool") == 1 and "maxpool2d" not in exe.kernel_counts
     assert "input" not in exe.kernel_counts
+    # in the f16 graph the stem's pooled output and the residual path are stored as halves
+    halves = [d for d in exe.dv.values() if d.half]
+    assert (len(halves) > 0) == (precision == "f16")
+    assert all(str(d.f32.dtype) == "torch.float16" for d in halves)
     x = models.image_batch((2, 3, 224, 224), 5)
     (got,) = runner.run({"x": x})
     (want,) = G.run_graph(g, {"x": x})
