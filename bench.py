@@ -369,15 +369,32 @@ def bench_gpt(args) -> int:
 
 
 def _host_description() -> dict:
-    """CPU model, logical CPUs, NumPy version and the BLAS library the baseline runs on."""
+    """CPU model, logical CPUs, physical cores, the CPUs this process may run on, NumPy
+    version and the BLAS library the baseline runs on."""
     model = "unknown"
+    cores: set = set()
+    phys = core = None
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "model name" and model == "unknown":
+                model = val
+            elif key == "physical id":
+                phys = val
+            elif key == "core id":
+                core = val
+            elif not key and core is not None:      # blank line: end of one logical CPU
+                cores.add((phys, core))
+                phys = core = None
+        if core is not None:
+            cores.add((phys, core))
     except OSError:
         pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = None
     blas = []
     try:
         from threadpoolctl import threadpool_info
@@ -385,7 +402,8 @@ def _host_description() -> dict:
                 for p in threadpool_info()]
     except Exception:
         pass
-    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "numpy": np.__version__, "blas": blas}
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "physical_cores": len(cores) or None,
+            "cpus_allowed": allowed, "numpy": np.__version__, "blas": blas}
 
 
 def cpu_baseline(peaks, macs_per_image: int, runs: int = 5) -> dict:
