@@ -23,7 +23,8 @@
 // separate quantize pass (a full int8 copy of the image written and read
 // back) disappears, and so does the global-load latency of the main loop.
 //
-// A workgroup owns BAND pooled rows of one image.  It walks the convolution
+// A workgroup owns a band of pooled rows of one image (BAND of them, fewer when the
+// batch is too small to give every CU a workgroup).  It walks the convolution
 // rows their windows cover, one at a time; each of its 4 waves computes, as
 // one 32-pixel MFMA block row (x 64 channels, weights in LDS), the 32
 // convolution columns that its pooled columns' windows cover (for a 3-wide
@@ -37,6 +38,7 @@
 // row has been folded in.
 #include "mr_common.hpp"
 
+#include <algorithm>
 #include <climits>
 #include <type_traits>
 
@@ -45,7 +47,7 @@ namespace mr {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int BAND = 8;           // pooled rows per workgroup
+constexpr int BAND = 8;           // pooled rows per workgroup, at most
 // f32-input kernels: input rows live in an LDS ring of STEM_RING rows; each
 // convolution row fetches the rows the one STEM_PD rows later needs
 constexpr int STEM_RING = 16;
@@ -67,6 +69,7 @@ struct StemArgs {
   int32_t row_bytes;   // packed bytes per kernel row
   int32_t N, H, W, O, OH, OW, KH, KW, SH, SW, PH, PW, DH, DW;
   int32_t ppt, POH, POW;  // pool top pad, pooled size
+  int32_t band;           // pooled rows per workgroup (1 .. BAND)
   float pad_value;
 };
 
@@ -86,10 +89,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: keeps per-wave values scalar
   const int half = lane >> 5;
-  const int bands = (a.POH + BAND - 1) / BAND;
+  const int bands = (a.POH + a.band - 1) / a.band;
   const int img = blockIdx.x / bands;
-  const int pr0 = (blockIdx.x - img * bands) * BAND;
-  const int pr_end = min(pr0 + BAND, a.POH);
+  const int pr0 = (blockIdx.x - img * bands) * a.band;
+  const int pr_end = min(pr0 + a.band, a.POH);
   // the convolution rows this band walks
   const int cr_first = max(2 * pr0 - PPL, 0);
   const int cr_last = min(2 * (pr_end - 1) + 1, a.OH - 1);
@@ -612,7 +615,12 @@ static int stem_setup(const char* who, const mr_conv_geom* cg, const int8_t* b, 
   a.POH = poh;
   a.POW = pow_;
   a.pad_value = pad_value;
-  const int64_t bands = (poh + BAND - 1) / BAND;
+  // BAND pooled rows per workgroup, or fewer where that leaves CUs without two
+  // workgroups (ResNet-18 at batch 1: 56 workgroups of one pooled row, not 7 of 8)
+  const int64_t cus = device_cu_count();
+  a.band = static_cast<int32_t>(std::min<int64_t>(BAND, std::max<int64_t>(1, (int64_t(G.n) * poh + 2 * cus - 1) /
+                                                                                   (2 * cus))));
+  const int64_t bands = (poh + a.band - 1) / a.band;
   MR_REQUIRE(int64_t(G.n) * bands < (int64_t(1) << 31), "%s: too many images", who);
   *out = a;
   *pool3 = pool_3_2_1;
@@ -638,7 +646,7 @@ int mr_qconv2d_maxpool(const int8_t* x, const mr_conv_geom* cg, const int8_t* b,
   a.x = x;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool rb2 = a.row_bytes == 32;   // kw 5..8 (else kw <= 4, 16 bytes per kernel row)
-  const dim3 grid(static_cast<unsigned>(int64_t(a.N) * ((poh + mr::BAND - 1) / mr::BAND)));
+  const dim3 grid(static_cast<unsigned>(int64_t(a.N) * ((poh + a.band - 1) / a.band)));
   const int ksub = rb2 ? a.KH : (a.KH + 1) / 2;        // 32-byte K steps holding real kernel rows
   const bool launched = pool3 ? mr::launch_stem_pool<3>(ksub, rb2, grid, s, a, e)
                               : mr::launch_stem_pool<2>(ksub, rb2, grid, s, a, e);
@@ -688,7 +696,7 @@ int mr_qconv2d_maxpool_f32in(const float* x, float x_scale, int32_t round_f16, c
   a.xf = x;
   a.rxs = 1.0 / static_cast<double>(x_scale);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(int64_t(a.N) * ((poh + mr::BAND - 1) / mr::BAND)));
+  const dim3 grid(static_cast<unsigned>(int64_t(a.N) * ((poh + a.band - 1) / a.band)));
   const int xin = round_f16 ? mr::XIN_F16 : mr::XIN_F32;
   if (pool3) {
     if (xin == mr::XIN_F16) mr::launch_stem_pool_f32in<3, mr::XIN_F16>(a.KH, grid, lds, s, a, e);
