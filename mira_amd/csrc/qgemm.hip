@@ -858,10 +858,19 @@ static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
     // what limits how many share a CU (LDS), so it is 3 stages, or none when K is
     // one 64-byte step (MobileNetV2 B=128: 3-channel stem 100 -> 90 us with 3
     // stages instead of 4, 32 -> 16 projection 53 -> 45 us)
-    if (g.k_tiles == 1)
+    if (g.k_tiles == 1) {
       launch_cfg<64, 32, 2, 1, 1, AMODE>(g, e, stream);
-    else
+    } else if constexpr (AMODE == A_DENSE || AMODE == A_CONV64) {
+      // a long K on a grid this small is a chain of ring stages per workgroup, each
+      // paying the load latency: 128-byte stages halve the chain where every row
+      // holds two whole 64-byte steps (ResNet-18 at batch 1, layer 4: 72 -> 36 stages)
+      if (g.k_tiles >= 8 && g.k_tiles % 2 == 0 && (AMODE == A_DENSE || g.C_pad % 128 == 0))
+        launch_cfg<64, 32, 2, 1, 3, AMODE, 128>(g, e, stream);
+      else
+        launch_cfg<64, 32, 2, 1, 3, AMODE>(g, e, stream);
+    } else {
       launch_cfg<64, 32, 2, 1, 3, AMODE>(g, e, stream);
+    }
   } else if (AMODE == A_DENSE && g.k_pad <= 1024) {
     // short K (the 1x1 convolutions of a MobileNet): the launch is bound by its
     // result stores, and small tiles -- more workgroups, shorter epilogues --

@@ -106,7 +106,8 @@ def _run_qmatmul(lib, x, q, ws, xs, steps_np, next_xs=None):
                                    (25088, 64, 384),      # short K, N > 128: 128x64
                                    (3, 4096, 1000), (8, 512, 65), (2, 64, 64), (5, 192, 130),   # weight stream
                                    (2, 5000, 96), (1, 8192, 40),    # k_pad > 4096: lane groups per column pair
-                                   (2, 1024, 3000)])                # weight stream, 8 columns per workgroup
+                                   (2, 1024, 3000),                 # weight stream, 8 columns per workgroup
+                                   (96, 1024, 256), (40, 4000, 70)])  # small grids: 64x32 tiles, 128-byte stages
 def test_qmatmul_bias_relu_requant(lib, M, K, N):
     rng = np.random.default_rng(M * 7 + N)
     x = rng.standard_normal((M, K)).astype(np.float32)
@@ -604,6 +605,8 @@ FORM_CONV_CASES = [
     (2, 64, 15, 15, 160, 3, 2, 1, 1),     # stride 2, 64-channel loader, 160 columns: last tile partial
     (4, 24, 56, 56, 144, 1, 1, 0, 1),     # 1x1 expansion, K in one step, large grid: 64x64 tiles, no ring
     (2, 16, 128, 128, 96, 1, 1, 0, 1),    # 1x1 expansion 16 -> 96, large grid: 128x128 tiles, no ring
+    (1, 512, 7, 7, 512, 3, 1, 1, 1),      # batch-1 layer 4: a 16-tile grid, 64x32 tiles with 128-byte stages
+    (1, 192, 9, 9, 96, 3, 2, 1, 1),       # small grid, c_pad 192: 64x32 tiles with 64-byte stages
 ]
 
 
