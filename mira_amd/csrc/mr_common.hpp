@@ -254,11 +254,13 @@ __device__ __forceinline__ float epi_steps(const EpiDev& e, float y, int64_t row
   return e.f16 ? round_f16(y) : y;
 }
 
-// Write the outputs for one finished result element.
+// Write the outputs for one finished result element.  H16 = false leaves out the store
+// of an f16 result as a half (for callers whose epilogues never have one).
+template <bool H16 = true>
 __device__ __forceinline__ void epi_store(const EpiDev& e, float y, int64_t row, int64_t col) {
   if (e.f16) y = round_f16(y);
   if (e.out_f32) {
-    if (e.out_h16)
+    if (H16 && e.out_h16)
       reinterpret_cast<__half*>(e.out_f32)[row * e.ldo + col] = __float2half_rn(y);
     else
       e.out_f32[row * e.ldo + col] = y;
@@ -302,9 +304,10 @@ int w8gemm_launch(const float* x, int64_t ldx, const int8_t* b, const float* w_s
 constexpr int EF_GENERIC = 0, EF_FIXED = 1, EF_SPEC = 0x100;
 constexpr int SF_COL = 1, SF_FULL = 2, SF_LO = 4, SF_HI = 8, SF_F32 = 16, SF_I8 = 32;
 constexpr int SF_MUL = 64;   // no compiled form has it: a leading mul runs the EF_FIXED path
-constexpr int SF_F16 = 128;  // results rounded to f16 (compiled for the ResNet-style forms only); the
-                             // f32 result and the residual may then be stored as halves (EpiDev
-                             // out_h16 / full_h16, read at run time)
+constexpr int SF_F16 = 128;  // results rounded to f16 (compiled for the ResNet-style forms only)
+// an f16 graph's residual read as halves (EpiDev full_h16) / its f32 result stored as halves
+// (out_h16); EF_SPEC is 0x100, so these sit above it
+constexpr int SF_H16R = 512, SF_H16O = 1024;
 // the forms with compiled kernels: bias+ReLU -> int8; bias+residual+ReLU -> f32
 // and/or int8; bias -> f32 (ResNet blocks, downsample and fc layers, MLPs)
 constexpr int SPEC_RELU_I8 = SF_COL | SF_LO | SF_I8;
@@ -337,13 +340,13 @@ inline int spec_form(const EpiDev& e) {
   if (e.f_col) f |= SF_COL;
   if (e.f_full) {
     if (!al(e.full_ptr, e.full_ld, e.full_h16 ? 8 : 16)) return -1;
-    f |= SF_FULL;
+    f |= SF_FULL | (e.full_h16 ? SF_H16R : 0);
   }
   if (e.f_lo) f |= SF_LO;
   if (e.f_hi) f |= SF_HI;
   if (e.out_f32) {
     if (!al(e.out_f32, e.ldo, e.out_h16 ? 8 : 16)) return -1;
-    f |= SF_F32;
+    f |= SF_F32 | (e.out_h16 ? SF_H16O : 0);
   }
   if (e.out_i8) {
     if (!al(e.out_i8, e.ldq, 4)) return -1;

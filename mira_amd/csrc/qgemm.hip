@@ -31,6 +31,7 @@
 #include "mr_common.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace mr {
 
@@ -202,7 +203,10 @@ __device__ __forceinline__ void load_cols4(const EpiDev& e, int col0, int N, Epi
 
 // Dequantize, apply the epilogue to, and store result row `row`, columns
 // col0 .. col0+3 (mira/ops.py:616-620 / 630-634, then 192-199).
-template <bool FIXED>
+// H16: the f16-as-halves paths are compiled in (read at run time from EpiDev); the
+// compiled forms without halves leave them out, which keeps their fall-back rows inside
+// the register budget.
+template <bool FIXED, bool H16 = true>
 __device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, const v4i& acc, int64_t row, int col0,
                                           int N) {
   float y[4];
@@ -219,7 +223,7 @@ __device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, c
     }
     if (e.f_full) {
       float o[4];
-      if (e.full_h16) {
+      if (H16 && e.full_h16) {
         const __half* p = reinterpret_cast<const __half*>(e.full_ptr) + row * e.full_ld + col0;
         if (c.vec) {
           const uint2 v = *reinterpret_cast<const uint2*>(p);
@@ -261,7 +265,7 @@ __device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, c
   if (c.vec) {
     if (e.out_acc) *reinterpret_cast<v4i*>(e.out_acc + row * e.ldacc + col0) = acc;
     if (e.out_f32) {
-      if (e.out_h16)
+      if (H16 && e.out_h16)
         *reinterpret_cast<uint2*>(reinterpret_cast<__half*>(e.out_f32) + row * e.ldo + col0) =
             make_uint2(pack_halves(y[0], y[1]), pack_halves(y[2], y[3]));
       else
@@ -278,7 +282,7 @@ __device__ __forceinline__ void store_row4(const EpiDev& e, const EpiCols4& c, c
     for (int k = 0; k < 4; ++k) {
       if (col0 + k >= N) break;
       if (e.out_acc) e.out_acc[row * e.ldacc + col0 + k] = acc[k];
-      epi_store(e, y[k], row, col0 + k);
+      epi_store<H16>(e, y[k], row, col0 + k);
     }
   }
 }
@@ -682,23 +686,22 @@ __global__ void __launch_bounds__(WM* WN * 64)
         // residual rows of chunk c (rows past the tile re-read its last row); the
         // next chunk's are loaded before this chunk's stores, which the compiler
         // may not move loads across
-        // residual rows as raw bits: 4 floats, or (an f16 graph's halves) 4 halves in x, y
-        const bool res_h16 = S_F16 && e.full_h16;
-        const bool out_h16 = S_F16 && e.out_h16;
-        auto load_res = [&](int c0, v4i (&res)[S_FULL ? NRC : 1]) __attribute__((always_inline)) {
+        // an f16 graph's residual read as halves and f32 result stored as halves
+        constexpr bool res_h16 = EF & SF_H16R, out_h16 = EF & SF_H16O;
+        // residual rows: 4 floats, or 4 halves (uint2)
+        using ResT = std::conditional_t<res_h16, uint2, float4>;
+        auto load_res = [&](int c0, ResT (&res)[S_FULL ? NRC : 1]) __attribute__((always_inline)) {
           if constexpr (S_FULL) {
 #pragma unroll
             for (int k = 0; k < NRC; ++k) {
               const int rr = threadIdx.x / CG + (c0 + k) * RSTEP;
               const int lk = (rr >> 5) * TM + pass * 32 + (rr & 31);
               const int64_t r = mbase + min(lk, mvalid - 1);
-              if (res_h16) {
-                const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(e.full_ptr) +
-                                                                r * e.full_ld + rcol);
-                res[k] = v4i{int(h.x), int(h.y), 0, 0};
-              } else {
-                res[k] = *reinterpret_cast<const v4i*>(e.full_ptr + r * e.full_ld + rcol);
-              }
+              if constexpr (res_h16)
+                res[k] = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(e.full_ptr) +
+                                                         r * e.full_ld + rcol);
+              else
+                res[k] = *reinterpret_cast<const float4*>(e.full_ptr + r * e.full_ld + rcol);
             }
           }
         };
@@ -709,7 +712,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
             S_F32 ? mvalid * int(e.ldo) * (out_h16 ? 2 : 4) : 0, BUF_DWORD3);
         const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
             e.out_i8 + mbase * e.ldq, 0, S_I8 ? mvalid * int(e.ldq) : 0, BUF_DWORD3);
-        v4i res_cur[S_FULL ? NRC : 1], res_next[S_FULL ? NRC : 1];
+        ResT res_cur[S_FULL ? NRC : 1], res_next[S_FULL ? NRC : 1];
         load_res(0, res_cur);
 #pragma unroll
         for (int k0 = 0; k0 < NR; k0 += NRC) {
@@ -724,14 +727,12 @@ __global__ void __launch_bounds__(WM* WN * 64)
         float y[NRC][4];
 #pragma unroll
         for (int k = 0; k < NRC; ++k) {
-          const v4i rb = res_cur[S_FULL ? k : 0];
+          const ResT rb = res_cur[S_FULL ? k : 0];
           float o[4];
-          if (res_h16) {
-            o[0] = half_bits(uint32_t(rb[0])); o[1] = half_bits(uint32_t(rb[0]) >> 16);
-            o[2] = half_bits(uint32_t(rb[1])); o[3] = half_bits(uint32_t(rb[1]) >> 16);
+          if constexpr (res_h16) {
+            o[0] = half_bits(rb.x); o[1] = half_bits(rb.x >> 16); o[2] = half_bits(rb.y); o[3] = half_bits(rb.y >> 16);
           } else {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) o[c] = __int_as_float(rb[c]);
+            o[0] = rb.x; o[1] = rb.y; o[2] = rb.z; o[3] = rb.w;
           }
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
@@ -750,7 +751,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
           const int lr = local[k];       // rows past mvalid: dropped by the resource's bound
           if (!cok) continue;
           if constexpr (S_F32) {
-            if (out_h16) {
+            if constexpr (out_h16) {
               const v2i v = {int(pack_halves(y[k][0], y[k][1])), int(pack_halves(y[k][2], y[k][3]))};
               const int off = (lr * int(e.ldo) + col0) * 2;
               if (e.nt_f32)
@@ -781,7 +782,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
       if (local >= mvalid || col0 >= g.N) continue;
       const int64_t row = mbase + local;
       const v4i a = *reinterpret_cast<const v4i*>(ep + rr * EP_LD + cgi * 4);
-      store_row4<EF != EF_GENERIC>(e, cols, a, row, col0, g.N);
+      store_row4<EF != EF_GENERIC, EF < EF_SPEC || (EF & (SF_H16R | SF_H16O)) != 0>(e, cols, a, row, col0, g.N);
     }
   }
 }
@@ -816,6 +817,13 @@ static void launch_cfg(GemmArgs g, const EpiDev& e, hipStream_t stream) {
       case SPEC_BIAS_F32 | SF_F16: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_F32 | SF_F16); return;
       case SPEC_RES_I8 | SF_F16: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_I8 | SF_F16); return;
       case SPEC_RES_F32 | SF_F16: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_F32 | SF_F16); return;
+      // and with their f16 values stored as halves (a residual path of halves; the last
+      // block's f32 result for a reader that takes f32)
+      case SPEC_RES_F32_I8 | SF_F16 | SF_H16R | SF_H16O:
+        MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_F32_I8 | SF_F16 | SF_H16R | SF_H16O); return;
+      case SPEC_RES_I8 | SF_F16 | SF_H16R: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_I8 | SF_F16 | SF_H16R); return;
+      case SPEC_RES_F32 | SF_F16 | SF_H16R: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_RES_F32 | SF_F16 | SF_H16R); return;
+      case SPEC_BIAS_F32 | SF_F16 | SF_H16O: MR_QGEMM_LAUNCH(EF_SPEC | SPEC_BIAS_F32 | SF_F16 | SF_H16O); return;
       default: break;
     }
   }
@@ -858,16 +866,23 @@ static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
     // what limits how many share a CU (LDS), so it is 3 stages, or none when K is
     // one 64-byte step (MobileNetV2 B=128: 3-channel stem 100 -> 90 us with 3
     // stages instead of 4, 32 -> 16 projection 53 -> 45 us)
+    const int64_t tiles = (g.M + 63) / 64 * ((g.N + 31) / 32);
     if (g.k_tiles == 1) {
       launch_cfg<64, 32, 2, 1, 1, AMODE>(g, e, stream);
-    } else if constexpr (AMODE == A_DENSE || AMODE == A_CONV64) {
-      // a long K on a grid this small is a chain of ring stages per workgroup, each
-      // paying the load latency: 128-byte stages halve the chain where every row
-      // holds two whole 64-byte steps (ResNet-18 at batch 1, layer 4: 72 -> 36 stages)
-      if (g.k_tiles >= 8 && g.k_tiles % 2 == 0 && (AMODE == A_DENSE || g.C_pad % 128 == 0))
-        launch_cfg<64, 32, 2, 1, 3, AMODE, 128>(g, e, stream);
-      else
-        launch_cfg<64, 32, 2, 1, 3, AMODE>(g, e, stream);
+    } else if (g.k_tiles >= 8 && tiles <= cus) {
+      // a long K on a grid of at most one tile per CU is a chain of ring stages per
+      // workgroup, each paying the load latency, and LDS is no constraint: six stages
+      // in flight, and 128-byte stages where every row holds two whole 64-byte steps,
+      // which halves the chain (ResNet-18 at batch 1, layer 4: 72 -> 36 stages, 25.6
+      // -> 19.5 us per conv)
+      if constexpr (AMODE == A_DENSE || AMODE == A_CONV64) {
+        if (g.k_tiles % 2 == 0 && (AMODE == A_DENSE || g.C_pad % 128 == 0)) {
+          launch_cfg<64, 32, 2, 1, 6, AMODE, 128>(g, e, stream);
+          MR_LAUNCH_CHECK("qgemm");
+          return MR_OK;
+        }
+      }
+      launch_cfg<64, 32, 2, 1, 6, AMODE>(g, e, stream);
     } else {
       launch_cfg<64, 32, 2, 1, 3, AMODE>(g, e, stream);
     }

@@ -490,10 +490,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) s
 
 template <int KS, int RBV, int PK, int XIN>
 static void launch_stem(dim3 grid, size_t lds, hipStream_t s, const StemArgs& a, const EpiDev& e) {
-  if (spec_form(e) == SPEC_RELU_F32_I8)
+  // the stem stores halves (out_h16) through a run-time branch of its own
+  const int form = spec_form(e) & ~SF_H16O;
+  if (form == SPEC_RELU_F32_I8)
     hipLaunchKernelGGL((stem_pool_kernel<KS, RBV, PK, EF_SPEC | SPEC_RELU_F32_I8, XIN>), grid, dim3(256), lds, s, a,
                        e);
-  else if (spec_form(e) == (SPEC_RELU_F32_I8 | SF_F16))
+  else if (form == (SPEC_RELU_F32_I8 | SF_F16))
     hipLaunchKernelGGL((stem_pool_kernel<KS, RBV, PK, EF_SPEC | SPEC_RELU_F32_I8 | SF_F16, XIN>), grid, dim3(256), lds,
                        s, a, e);
   else if (e.fixed)
