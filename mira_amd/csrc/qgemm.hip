@@ -869,8 +869,8 @@ static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
     const int64_t tiles = (g.M + 63) / 64 * ((g.N + 31) / 32);
     if (g.k_tiles == 1) {
       launch_cfg<64, 32, 2, 1, 1, AMODE>(g, e, stream);
-    } else if (g.k_tiles >= 8 && tiles <= cus) {
-      // a long K on a grid of at most one tile per CU is a chain of ring stages per
+    } else if (g.k_tiles >= 8 && tiles <= 2 * cus) {
+      // a long K on a grid of at most two tiles per CU is a chain of ring stages per
       // workgroup, each paying the load latency, and LDS is no constraint: six stages
       // in flight, and 128-byte stages where every row holds two whole 64-byte steps,
       // which halves the chain (ResNet-18 at batch 1, layer 4: 72 -> 36 stages, 25.6
