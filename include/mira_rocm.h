@@ -295,6 +295,12 @@ int mr_pad_hw_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c,
 /* Layout changes at segment boundaries: NCHW <-> NHWC, f32. */
 int mr_nchw_to_nhwc_f32(const float* x, int32_t n, int32_t c, int32_t h, int32_t w,
                         float* y, void* stream);
+
+/* NCHW f32 -> NHWC f32 with c_pad >= c channels per pixel (c_pad % 4 == 0),
+ * channels c .. c_pad - 1 zero: the input of a weight-only convolution whose
+ * channel count is not a multiple of 4 (a 3-channel stem); exact (a copy). */
+int mr_nchw_to_nhwc_pad_f32(const float* x, int32_t n, int32_t c, int32_t h, int32_t w,
+                            float* y, int32_t c_pad, void* stream);
 int mr_nhwc_to_nchw_f32(const float* x, int32_t n, int32_t c, int32_t h, int32_t w,
                         float* y, void* stream);
 

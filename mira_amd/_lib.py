@@ -30,7 +30,7 @@ EXPORTS = [
     "mr_qmatmul", "mr_qmatmul_f32in", "mr_w8_matmul_f32", "mr_w8_conv2d_f32", "mr_qconv2d", "mr_qconv2d_maxpool",
     "mr_qconv2d_maxpool_f32in", "mr_dwconv2d_f32",
     "mr_maxpool2d_f32", "mr_mean_hw_f32", "mr_pad_hw_f32", "mr_round_f16_f32",
-    "mr_nchw_to_nhwc_f32", "mr_nhwc_to_nchw_f32",
+    "mr_nchw_to_nhwc_f32", "mr_nchw_to_nhwc_pad_f32", "mr_nhwc_to_nchw_f32",
     "mr_layernorm_f32", "mr_softmax_f32", "mr_bmm_f32", "mr_transpose_f32", "mr_copy_rows_f32",
     "mr_attention_decode_f32", "mr_decode_embed", "mr_decode_commit",
 ]
@@ -85,6 +85,7 @@ _SIGS = {
     "mr_pad_hw_f32": ([_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p], C.c_int),
     "mr_round_f16_f32": ([_p, _i64, _p, _p], C.c_int),
     "mr_nchw_to_nhwc_f32": ([_p, _i32, _i32, _i32, _i32, _p, _p], C.c_int),
+    "mr_nchw_to_nhwc_pad_f32": ([_p, _i32, _i32, _i32, _i32, _p, _i32, _p], C.c_int),
     "mr_nhwc_to_nchw_f32": ([_p, _i32, _i32, _i32, _i32, _p, _p], C.c_int),
     "mr_layernorm_f32": ([_p, _i64, _i32, _p, _p, _f32, _i32, _p, _p, _i64, _f32, _p], C.c_int),
     "mr_softmax_f32": ([_p, _i64, _i32, _i32, _p, _p], C.c_int),

@@ -291,6 +291,25 @@ __global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict_
   }
 }
 
+// NCHW f32 -> NHWC f32 with c_pad >= c channels per pixel, channels c .. c_pad - 1 zero:
+// thread t writes one 16-byte group of 4 channels of one pixel (c_pad % 4 == 0).
+__global__ void __launch_bounds__(256) nchw_to_nhwc_pad_kernel(const float* __restrict__ x, int c, int64_t hw,
+                                                               int c_pad, int64_t total, float* __restrict__ y) {
+  const int groups = c_pad >> 2;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    const int g = static_cast<int>(t % groups);
+    const int64_t pix = t / groups;           // image * hw + p
+    const int64_t img = pix / hw, p = pix - img * hw;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ch = 4 * g + j;
+      v[j] = ch < c ? x[(img * c + ch) * hw + p] : 0.0f;
+    }
+    *reinterpret_cast<float4*>(y + pix * c_pad + 4 * g) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
+
 static int transpose(const float* x, int n, int rows, int cols, float* y, hipStream_t s) {
   dim3 grid((cols + 31) / 32, (rows + 31) / 32, n);
   hipLaunchKernelGGL(transpose_kernel, grid, dim3(32, 8), 0, s, x, rows, cols, y);
@@ -449,6 +468,21 @@ int mr_nchw_to_nhwc_f32(const float* x, int32_t n, int32_t c, int32_t h, int32_t
   MR_REQUIRE(n >= 0 && c > 0 && h > 0 && w > 0 && n < 65536, "mr_nchw_to_nhwc_f32: bad shape");
   if (n == 0) return MR_OK;
   return mr::transpose(x, n, c, h * w, y, static_cast<hipStream_t>(stream));
+}
+
+int mr_nchw_to_nhwc_pad_f32(const float* x, int32_t n, int32_t c, int32_t h, int32_t w, float* y, int32_t c_pad,
+                            void* stream) {
+  MR_REQUIRE(x && y && x != y, "mr_nchw_to_nhwc_pad_f32: bad pointers");
+  MR_REQUIRE(n >= 0 && c > 0 && h > 0 && w > 0, "mr_nchw_to_nhwc_pad_f32: bad shape");
+  MR_REQUIRE(c_pad >= c && c_pad % 4 == 0, "mr_nchw_to_nhwc_pad_f32: c_pad %d must be >= c and a multiple of 4",
+             c_pad);
+  MR_REQUIRE(reinterpret_cast<uintptr_t>(y) % 16 == 0, "mr_nchw_to_nhwc_pad_f32: y must be 16-byte aligned");
+  const int64_t total = int64_t(n) * h * w * (c_pad / 4);
+  if (total == 0) return MR_OK;
+  hipLaunchKernelGGL(mr::nchw_to_nhwc_pad_kernel, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, c, int64_t(h) * w, c_pad, total, y);
+  MR_LAUNCH_CHECK("nchw_to_nhwc_pad");
+  return MR_OK;
 }
 
 int mr_nhwc_to_nchw_f32(const float* x, int32_t n, int32_t c, int32_t h, int32_t w, float* y, void* stream) {

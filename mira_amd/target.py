@@ -291,8 +291,9 @@ class RocmTarget:
     def _check_w8_conv2d(self, op: "Op") -> Optional[str]:
         """Convolutions of the weight-only int8 mode: an f32 conv2d (groups 1) over a
         `dequantize` [O, C, KH, KW] weight, as an implicit GEMM on f32 MFMAs.  The kernel
-        reads the NHWC image 4 channels at a time, so C must be a multiple of 4 (a 3-channel
-        stem stays on the CPU).  Like the weight-only matmul it matches the reference to f32
+        reads the NHWC image 4 channels at a time: a graph input whose channel count is not a
+        multiple of 4 (a 3-channel stem) is copied to NHWC with its channels padded to 4, zero
+        weights for the padding.  Like the weight-only matmul it matches the reference to f32
         rounding, not bit for bit."""
         x, w = op.inputs[0], op.inputs[1]
         p = w.producer
@@ -302,9 +303,10 @@ class RocmTarget:
         if x.type.rank != 4 or x.type.dtype not in FLOAT_DTYPES:
             return "weight-only int8 convolution needs an NCHW float input"
         n, c, h, wd = x.type.shape
-        if c % 4 != 0:
-            return f"weight-only int8 convolution runs on rocm for channel counts divisible by 4, not {c}"
-        if n * h * wd * c * 4 >= 2 ** 31:
+        if c % 4 != 0 and x.producer is not None:
+            return (f"weight-only int8 convolution of {c} channels (not a multiple of 4) runs on rocm only on a "
+                    f"graph input, which the target copies to NHWC with the channels padded to 4")
+        if n * h * wd * pack.roundup(c, 4) * 4 >= 2 ** 31:
             return "weight-only int8 convolution: an input of 2 GiB or more"
         return self._check_epilogue(op, op.result.type.shape, True, first_operand=2)
 
@@ -421,6 +423,8 @@ class RocmExecutable:
                     self.need_f32.add(pad_op.inputs[0])
             else:
                 for v in op.inputs:
+                    if v is op.inputs[0] and self._padded_w8_input(op):
+                        continue            # read through its own channel-padded NHWC copy
                     if v not in self.consts or op.kind not in ("conv2d", "matmul") or v is op.inputs[0]:
                         self.need_f32.add(v)
         # reshapes: the input must provide what the output's consumers read; a reshape
@@ -477,6 +481,15 @@ class RocmExecutable:
         for v in g.outputs:
             if v in self.consts and v not in self.dv:
                 self._const_dv(v)
+
+    def _padded_w8_input(self, op: "Op") -> bool:
+        """A weight-only convolution over a graph input whose channel count is not a multiple
+        of 4: it reads its own channel-padded NHWC copy of the input (_emit_w8_conv2d)."""
+        x = op.inputs[0]
+        w = op.inputs[1] if len(op.inputs) > 1 else None
+        return (op.kind == "conv2d" and w is not None and w in self.consts and
+                self.consts[w].kind == "dequantize" and x in self.g.inputs and x.type.rank == 4 and
+                x.type.shape[1] % 4 != 0)
 
     def _is_bmm(self, op: "Op") -> bool:
         w = op.inputs[1] if op.kind == "matmul" else None
@@ -1204,13 +1217,27 @@ class RocmExecutable:
         each run is one mr_w8_conv2d_f32 implicit GEMM over the NHWC f32 image."""
         a = op.attrs
         xv = op.inputs[0]
-        x = self._src(xv)
         n, c, h, w = xv.type.shape
         wa = self.consts[op.inputs[1]].attrs
         q = np.asarray(wa["q"], np.int8)
         o, _, kh, kw = q.shape
         (sh, sw), (ph, pw), (dh, dw), _ = conv_params(a)
         _, _, oh, ow = op.result.type.shape
+        lib = self.lib
+        if c % 4:
+            # a graph input of c channels (checked): an NHWC copy with the channels padded to
+            # 4, and zero weights for them
+            c4 = pack.roundup(c, 4)
+            stage = self.staging[xv]
+            xt = _t().empty((n, h, w, c4), dtype=_t().float32, device=self.dev)
+            # c is rebound to c4 below: the launch takes the input's own count as a default
+            self._add("input", lambda s, c=c: L.check(lib.mr_nchw_to_nhwc_pad_f32(stage.data_ptr(), n, c, h, w,
+                                                                                   xt.data_ptr(), c4, s),
+                                                      "mr_nchw_to_nhwc_pad_f32"), nbytes=4 * n * h * w * (c + c4))
+            q = np.concatenate([q, np.zeros((o, c4 - c, kh, kw), np.int8)], axis=1)
+            c = c4
+        else:
+            xt = self._src(xv).f32
         cp = pack.roundup(c, 16)                   # the packed taps' channel stride
         bl = pack.pack_conv(q, cp)
         b = self._upload(pack.device_weights(bl))
@@ -1221,7 +1248,7 @@ class RocmExecutable:
         self.keep.append(geom)
         out = self._new_dv(op.result)
         e, fused = self._epilogue(op, out, True, 2, None)
-        lib, xt, kp, npad = self.lib, x.f32, bl.shape[1], bl.shape[0]
+        kp, npad = bl.shape[1], bl.shape[0]
         rows = n * oh * ow
         self._add("w8conv2d", lambda s: L.check(
             lib.mr_w8_conv2d_f32(xt.data_ptr(), C.byref(geom), b.data_ptr(), ws.data_ptr(), w16, kp, npad, C.byref(e),

@@ -838,6 +838,29 @@ def test_pad_and_layouts(lib):
     assert bits_equal(padded.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("n,c,h,w,c_pad", [(2, 3, 7, 9, 4), (1, 3, 224, 224, 4), (3, 5, 4, 6, 8), (2, 1, 3, 3, 4)])
+def test_nchw_to_nhwc_pad(lib, n, c, h, w, c_pad):
+    """The channel-padded NHWC copy of a weight-only convolution's input: the channels in
+    order, then zeros (NaN-filled output first, so every element is written)."""
+    torch = _torch()
+    x = np.random.default_rng(c * 31 + h).standard_normal((n, c, h, w)).astype(np.float32)
+    y = torch.full((n, h, w, c_pad), float("nan"), dtype=torch.float32, device="cuda")
+    L.check(lib.mr_nchw_to_nhwc_pad_f32(T(x).data_ptr(), n, c, h, w, y.data_ptr(), c_pad, stream()), "pad")
+    sync()
+    want = np.zeros((n, h, w, c_pad), np.float32)
+    want[..., :c] = x.transpose(0, 2, 3, 1)
+    assert bits_equal(y.cpu().numpy(), want)
+
+
+def test_nchw_to_nhwc_pad_rejects(lib):
+    """c_pad below c or not a multiple of 4 is an argument error, nothing launched."""
+    torch = _torch()
+    x = empty((1, 3, 4, 4), torch.float32)
+    y = empty((1, 4, 4, 8), torch.float32)
+    for c_pad in (2, 6):
+        assert lib.mr_nchw_to_nhwc_pad_f32(x.data_ptr(), 1, 3, 4, 4, y.data_ptr(), c_pad, stream()) == 1
+
+
 # ---------------------------------------------------------------- fused stem (conv -> pad -> maxpool)
 
 @pytest.mark.parametrize("n,c,h,o,k,s,p,pool,pst,ppad,pval,neg", [

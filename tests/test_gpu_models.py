@@ -409,18 +409,39 @@ def test_weight_only_mlp50m_batch4096():
     assert np.abs(got - want).max() <= W8_MODEL_TOL * np.abs(want).max()
 
 
-@pytest.mark.parametrize("builder,convs", [(models.resnet18, 19), (models.mobilenet_v2, 33)])
-def test_weight_only_cnn_batch2(builder, convs):
+@pytest.mark.parametrize("builder,convs,devices", [(models.resnet18, 20, ["rocm"]),
+                                                    (models.mobilenet_v2, 33, ["cpu", "rocm"])])
+def test_weight_only_cnn_batch2(builder, convs, devices):
     """Weight-only ResNet-18 and MobileNetV2: every dense convolution over a dequantize weight
-    whose input has a channel count divisible by 4 on rocm (the 3-channel stems, and the two
-    MobileNetV2 convolutions whose weights are under 1024 elements and stay f32, run on the
-    CPU; depthwise weights are materialized in f32 and stay bit-exact), within f32 rounding
-    of the oracle compounded over the network."""
+    on rocm, ResNet-18's 3-channel stem through a channel-padded NHWC copy of the image (the
+    two MobileNetV2 convolutions whose weights are under 1024 elements stay f32 and run on
+    the CPU; depthwise weights are materialized in f32 and stay bit-exact), within f32
+    rounding of the oracle compounded over the network."""
     g = _weight_only(builder(batch=2, seed=0))
     runner, (got,), (want,) = _run_weight_only(g, {"x": models.image_batch((2, 3, 224, 224), 7)})
     n = sum(exe.kernel_counts.get("w8conv2d", 0) for exe in runner.executables("rocm"))
     assert n == convs, n
+    assert runner.devices[:2] == devices, runner.devices
     assert np.abs(got - want).max() <= W8_MODEL_TOL * np.abs(want).max()
+
+
+def test_weight_only_stem_alone():
+    """A lone 3-channel weight-only 7x7/2 convolution with a bias and relu: the padded copy
+    and its zero weight channel against the oracle, at batch 1 and 3."""
+    from harness.graph import Graph
+    rng = np.random.default_rng(21)
+    for n in (1, 3):
+        g = Graph("stem")
+        x = g.input("x", (n, 3, 61, 57))
+        w = g.const(rng.standard_normal((16, 3, 7, 7)).astype(np.float32))
+        b = g.const(rng.standard_normal((1, 16, 1, 1)).astype(np.float32))
+        y = g.op("relu", [g.op("add", [g.op("conv2d", [x, w], {"stride": (2, 2), "padding": (3, 3)}), b])])
+        g.outputs = [y]
+        g = _weight_only(g)
+        runner, (got,), (want,) = _run_weight_only(g, {"x": rng.standard_normal((n, 3, 61, 57)).astype(np.float32)})
+        assert runner.devices == ["rocm"]
+        assert sum(exe.kernel_counts.get("w8conv2d", 0) for exe in runner.executables("rocm")) == 1
+        assert np.abs(got - want).max() <= W8_MODEL_TOL * np.abs(want).max()
 
 
 def test_weight_only_mlp_mira_batch64():

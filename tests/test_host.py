@@ -170,6 +170,27 @@ def test_check_decisions_weight_only():
         assert (r is None) if ok else ("K % 4 == 0" in r)
 
 
+def test_check_decisions_weight_only_stem():
+    """A weight-only convolution whose channel count is not a multiple of 4 runs on rocm when
+    it reads a graph input (the target makes a channel-padded NHWC copy) and stays on the CPU
+    when another op produces its input."""
+    from harness.graph import Graph
+    t = RocmTarget()
+    rng = np.random.default_rng(0)
+    g = Graph("stem")
+    x = g.input("x", (1, 3, 32, 32))
+    y = g.op("conv2d", [x, g.const(rng.standard_normal((16, 3, 7, 7)).astype(np.float32))],
+             {"stride": (2, 2), "padding": (3, 3)})
+    z = g.op("conv2d", [g.op("relu", [x]), g.const(rng.standard_normal((16, 3, 7, 7)).astype(np.float32))],
+             {"stride": (2, 2), "padding": (3, 3)})
+    g.outputs = [y, z]
+    LW.prepare(g)
+    LW.weight_only(g)
+    first, second = [op for op in g.compute_ops() if op.kind == "conv2d"]
+    assert t.check(first) is None
+    assert "graph input" in t.check(second)
+
+
 def test_check_decisions():
     t = RocmTarget()
     g = models.mlp_mira(batch=4)
