@@ -114,10 +114,13 @@ __global__ void __launch_bounds__(256) qgemv_kernel(const GemvArgs g, const EpiD
 // of 4).  Longer K stays on qgemv_kernel, whose lanes share each activation load
 // between two columns (at K = 16384 and M = 3 it is 1.5x faster than this one).
 //
-// F32IN: the activation rows arrive as f32 and each workgroup quantizes them into
-// LDS first (mr_quantize_rows's arithmetic, mira/ops.py:602-603), after its weight
-// loads are issued, so the separate quantize launch of a decode step's first layer
-// disappears behind the weight stream's latency.
+// The activation rows are staged in LDS, and their loads are issued before the
+// weight stream's: the vector-memory counter completes in issue order, so a row
+// load issued after the weights would wait for all of them, and one per K step
+// made each lane's later steps serial L2 round trips.  F32IN: the rows arrive as
+// f32 and each workgroup quantizes them into LDS (mr_quantize_rows's arithmetic,
+// mira/ops.py:602-603) while its weights are in flight, so the separate quantize
+// launch of a decode step's first layer disappears behind the weight stream.
 constexpr int KS_MAXS = 8;    // wave-wide loads a lane has in flight at once
 constexpr int KS_KMAX = 4096; // largest k_pad of this kernel (8 waves x 8 steps x 64 bytes)
 
@@ -126,9 +129,10 @@ __global__ void __launch_bounds__(KW * 64) qgemv_ks_kernel(const GemvArgs g, con
                                                             int64_t ldx, float xs) {
   constexpr int LPC = 64 / COLS;   // lanes per column
   constexpr int SPL = LPC / 4;     // K steps per wave-wide load
+  constexpr int NT = KW * 64;      // threads
   static_assert(KW * KS_MAXS * 64 >= KS_KMAX, "one pass covers k_pad");
   __shared__ int red[KW][MR][COLS];
-  __shared__ __attribute__((aligned(16))) int8_t xq[F32IN ? MR : 1][F32IN ? KS_KMAX : 16];
+  __shared__ __attribute__((aligned(16))) int8_t xq[MR][KS_KMAX];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * COLS;
   const int col = lane / LPC, j = lane % LPC;
@@ -138,50 +142,68 @@ __global__ void __launch_bounds__(KW * 64) qgemv_ks_kernel(const GemvArgs g, con
   const int s_begin = wave * per_wave, s_end = min(s_begin + per_wave, ksteps);
   const int8_t* bcol = g.b + int64_t(n0 + col) * 64 + (j & 3) * 16;   // n0 + COLS <= n_pad
   const int64_t kstep = int64_t(g.n_pad) * 64;
+
+  // the rows' loads: F32IN 4 f32 words per thread and load (16-byte loads where the
+  // rows allow), else 16 int8 bytes (lda % 16 == 0 and a 16-byte aligned: a chunk
+  // is all below lda or all past it); zeros past the rows' ends
+  constexpr int XB = F32IN ? 4 : 16;                        // row bytes per thread and load
+  constexpr int NQ = (MR * KS_KMAX / XB + NT - 1) / NT;     // loads per thread at most
+  const int per_row = g.k_pad / XB;
+  float4 vf[F32IN ? NQ : 1];
+  v4i vi[F32IN ? 1 : NQ];
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) {
+    const int i = threadIdx.x + u * NT;
+    const int m = i / per_row, k0 = (i - m * per_row) * XB;
+    if constexpr (F32IN) {
+      const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
+      vf[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (m < g.M && k0 < g.lda) {
+        const float* xr = x + m * ldx + k0;
+        if (vec && k0 + 3 < g.lda) {
+          vf[u] = *reinterpret_cast<const float4*>(xr);
+        } else {
+          vf[u].x = xr[0];
+          if (k0 + 1 < g.lda) vf[u].y = xr[1];
+          if (k0 + 2 < g.lda) vf[u].z = xr[2];
+          if (k0 + 3 < g.lda) vf[u].w = xr[3];
+        }
+      }
+    } else {
+      vi[u] = v4i{0, 0, 0, 0};
+      if (m < g.M && k0 < g.lda) vi[u] = *reinterpret_cast<const v4i*>(g.a + m * g.lda + k0);
+    }
+  }
+  // then the weight stream, every load of a lane in flight at once
   v4i w[KS_MAXS];
 #pragma unroll
   for (int i = 0; i < KS_MAXS; ++i) {
     const int s = min(s_begin + i * SPL + (j >> 2), ksteps - 1);   // past the share: re-read, unused
     w[i] = *reinterpret_cast<const v4i*>(bcol + s * kstep);
   }
-  if constexpr (F32IN) {
-    // quantize the rows into LDS, 4 bytes per thread and word, zero past K: every
-    // thread's loads first (16-byte ones where the rows allow), then the arithmetic
-    constexpr int NQ = MR * KS_KMAX / 4 / (KW * 64);   // words per thread at most
-    const int words = g.k_pad >> 2;
-    const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
-    float4 v[NQ];
+  // the rows into LDS (quantized for F32IN) while the weights arrive
 #pragma unroll
-    for (int u = 0; u < NQ; ++u) {
-      const int i = threadIdx.x + u * KW * 64;
-      const int m = i / words, k0 = (i - m * words) * 4;
-      v[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (m < g.M && k0 < g.lda) {
-        const float* xr = x + m * ldx + k0;
-        if (vec && k0 + 3 < g.lda) {
-          v[u] = *reinterpret_cast<const float4*>(xr);
-        } else {
-          v[u].x = xr[0];
-          if (k0 + 1 < g.lda) v[u].y = xr[1];
-          if (k0 + 2 < g.lda) v[u].z = xr[2];
-          if (k0 + 3 < g.lda) v[u].w = xr[3];
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < NQ; ++u) {
-      const int i = threadIdx.x + u * KW * 64;
-      if (i >= MR * words) break;
-      const int m = i / words, k0 = (i - m * words) * 4;
-      const float f[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+  for (int u = 0; u < NQ; ++u) {
+    const int i = threadIdx.x + u * NT;
+    if (i >= MR * per_row) break;
+    const int m = i / per_row, k0 = (i - m * per_row) * XB;
+    if (m >= g.M) break;
+    if constexpr (F32IN) {
+      const float f[4] = {vf[u].x, vf[u].y, vf[u].z, vf[u].w};
       uint32_t packed = 0;
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        if (m < g.M && k0 + t < g.lda) packed |= uint32_t(uint8_t(quantize_one(f[t], xs))) << (8 * t);
+        if (k0 + t < g.lda) packed |= uint32_t(uint8_t(quantize_one(f[t], xs))) << (8 * t);
       *reinterpret_cast<uint32_t*>(&xq[m][k0]) = packed;
+    } else {
+      *reinterpret_cast<v4i*>(&xq[m][k0]) = vi[u];
     }
-    __syncthreads();
   }
+  // every wave's LDS stores done before any wave reads: an LDS-only wait and the
+  // barrier, so the weight loads stay in flight across it (__syncthreads would
+  // wait for them); the memory clobber keeps the compiler from moving LDS
+  // accesses across
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   int acc[MR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) acc[m] = 0;
@@ -190,15 +212,11 @@ __global__ void __launch_bounds__(KW * 64) qgemv_ks_kernel(const GemvArgs g, con
     const int s = s_begin + i * SPL + (j >> 2);
     if (s_begin + i * SPL >= s_end) break;
     if (s >= s_end) continue;
-    const int64_t k = int64_t(s) * 64 + (j & 3) * 16;
+    const int k = s * 64 + (j & 3) * 16;
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       if (m >= g.M) break;
-      v4i xv = {0, 0, 0, 0};
-      if constexpr (F32IN)
-        xv = *reinterpret_cast<const v4i*>(&xq[m][k]);
-      else if (k < g.lda)   // bytes past lda meet zero weights (k >= K); lda % 16 == 0 keeps a chunk whole
-        xv = *reinterpret_cast<const v4i*>(g.a + m * g.lda + k);
+      const v4i xv = *reinterpret_cast<const v4i*>(&xq[m][k]);
 #pragma unroll
       for (int q = 0; q < 4; ++q) acc[m] = __builtin_amdgcn_sdot4(xv[q], w[i][q], acc[m], false);
     }
