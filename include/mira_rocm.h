@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MR_ABI_VERSION 9
+#define MR_ABI_VERSION 10
 
 enum mr_status {
   MR_OK = 0,
@@ -263,6 +263,23 @@ int mr_qconv2d_maxpool_f32in(const float* x, float x_scale, int32_t round_f16, c
  * NULL).  x NHWC f32 [n,h,w,c], w f32 [kh][kw][c]. */
 int mr_dwconv2d_f32(const float* x, const mr_conv_geom* g, const float* w,
                     const mr_epilogue* epi, void* stream);
+
+/* A 1x1 qconv2d whose f32 result only a 3x3 depthwise conv reads, as one
+ * launch (a MobileNet block's expansion and depthwise convolution; replaces
+ * mira/ops.py:630-634 followed by mira/ops.py:265-276 with groups == C).  The
+ * expansion: x NHWC int8 rows of ldx bytes (K real channels, ldx % 16 == 0),
+ * packed weights b [k_pad/64][n_pad][64] with n_pad >= dw->c, and its epilogue
+ * epi_expand (the dequant scale, bias -> maximum -> minimum, no outputs: its
+ * result is never stored).  The depthwise conv: geometry dw (3x3, padding 1,
+ * stride 1 or 2, c == o == c_pad, c % 4 == 0), weights w_dw f32 [3][3][c]
+ * and epi_dw (bias -> maximum -> minimum, an int8 output and optionally an f32
+ * one).  Bit-exact with mr_qconv2d followed by mr_dwconv2d_f32: the expanded
+ * values are recomputed for each output tile's halo with the same arithmetic
+ * and never leave the chip.  MR_EUNSUPPORTED for other epilogues, f16
+ * rounding or k_pad > 192 (the caller then makes the two launches). */
+int mr_qconv1x1_dw3x3(const int8_t* x, int64_t ldx, const int8_t* b, int64_t k_pad, int64_t n_pad, int64_t K,
+                      const mr_epilogue* epi_expand, const mr_conv_geom* dw, const float* w_dw,
+                      const mr_epilogue* epi_dw, void* stream);
 
 /* ---- adjuncts ---------------------------------------------------------- */
 

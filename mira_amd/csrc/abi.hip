@@ -19,7 +19,7 @@ void set_error(const char* fmt, ...) {
 
 int device_cu_count() { return g_cu_count > 0 ? g_cu_count : 256; }
 
-int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out, bool allow_h16) {
+int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out, bool allow_h16, bool need_output) {
   MR_REQUIRE(epi != nullptr, "epilogue descriptor is NULL");
   MR_REQUIRE(epi->n_steps >= 0 && epi->n_steps <= MR_MAX_EPI, "epilogue has %d steps (max %d)",
              epi->n_steps, MR_MAX_EPI);
@@ -28,7 +28,7 @@ int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out,
   } else {
     MR_REQUIRE(epi->scale == nullptr, "this kernel has no int32 accumulator to dequantize");
   }
-  MR_REQUIRE(epi->out_f32 || epi->out_i8 || epi->out_acc, "epilogue writes no output");
+  MR_REQUIRE(!need_output || epi->out_f32 || epi->out_i8 || epi->out_acc, "epilogue writes no output");
   MR_REQUIRE((epi->flags & ~(MR_EPI_OUT_F16 | MR_EPI_OUT_H16 | MR_EPI_FULL_H16)) == 0, "unknown epilogue flags 0x%x",
              epi->flags);
   if ((epi->flags & (MR_EPI_OUT_H16 | MR_EPI_FULL_H16)) && !allow_h16) {

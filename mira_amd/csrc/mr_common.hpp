@@ -275,14 +275,36 @@ __device__ __forceinline__ float dequant(int32_t acc, double scale) {
   return static_cast<float>(__dmul_rn(static_cast<double>(acc), scale));
 }
 
+// Workgroup barrier without a memory fence: what it orders is established by a wait
+// before it (a counted vmcnt wait for LDS DMA, or operands already consumed).  The
+// signal fences keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void block_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Barrier after LDS stores that other waves read next.  s_barrier does not
+// wait for the wave's own outstanding LDS operations, so the stores are first
+// drained (lgkmcnt 0; vmcnt and expcnt untouched): without this a wave can
+// read a row another wave has issued but not yet written.
+__device__ __forceinline__ void lds_store_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // vmcnt 63, expcnt 7, lgkmcnt 0
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Word 3 of a raw buffer resource (32-bit elements) on gfx9: loads past num_records
 // return 0 and stores past it are dropped, which the kernels use for bounds.
 constexpr int BUF_DWORD3 = 0x00020000;
 
 // ---------------------------------------------------------------- host-side epilogue validation
 
-// allow_h16: the caller's kernels implement MR_EPI_OUT_H16 / MR_EPI_FULL_H16
-int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out, bool allow_h16 = false);
+// allow_h16: the caller's kernels implement MR_EPI_OUT_H16 / MR_EPI_FULL_H16; need_output =
+// false for an intermediate result that a fused kernel consumes without storing it
+int make_epi(const mr_epilogue* epi, int64_t cols, bool need_scale, EpiDev* out, bool allow_h16 = false,
+             bool need_output = true);
 
 // Decode-shaped qmatmul (M <= 8 rows): weight-streaming kernel; MR_EUNSUPPORTED for larger M.
 int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, int64_t n_pad, int64_t M, int64_t N,

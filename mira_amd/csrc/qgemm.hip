@@ -109,26 +109,6 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// Workgroup barrier without a memory fence: the LDS-DMA completion it orders
-// is established by the counted vmcnt wait before it.  The signal fences keep
-// the compiler from moving memory accesses across it.
-__device__ __forceinline__ void block_barrier() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-// Barrier after LDS stores that other waves read next.  s_barrier does not
-// wait for the wave's own outstanding LDS operations, so the stores are first
-// drained (lgkmcnt 0; vmcnt and expcnt untouched): without this a wave can
-// read a row another wave has issued but not yet written.
-__device__ __forceinline__ void lds_store_barrier() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0xC07F);   // vmcnt 63, expcnt 7, lgkmcnt 0
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 __device__ __forceinline__ void dma16(const void* src, int8_t* lds_dst) {
   __builtin_amdgcn_global_load_lds(src, (lds_void*)lds_dst, 16, 0, 0);
 }

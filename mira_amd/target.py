@@ -472,6 +472,7 @@ class RocmExecutable:
         self._plan_shared_input_matmuls()
         self._plan_f32in_matmuls()
         self._plan_half_storage()
+        self._plan_expand_dw()
         for v in g.inputs:
             self._emit_input(v)
         for op in g.ops:
@@ -669,6 +670,58 @@ class RocmExecutable:
             if i not in steps or i not in full or len(set(u.inputs[j] for j in full)) != 1:
                 return False
         return True
+
+    def _relu6_epilogue(self, op: "Op") -> bool:
+        """The epilogue is add(per-channel constant) -> maximum(scalar constant) or relu ->
+        minimum(scalar constant), none swapped: the form mr_qconv1x1_dw3x3 runs."""
+        steps = tuple(op.attrs.get("epilogue", ()))
+        if len(steps) != 3 or any(sw for _fn, _i, sw in steps):
+            return False
+        (f0, i0, _), (f1, i1, _), (f2, i2, _) = steps
+        rshape = op.result.type.shape
+
+        def mode(idx):
+            v = op.inputs[idx]
+            return _bcast_mode(np.shape(self._const_value(v)), rshape, True) if v in self.consts else None
+        return (f0 == "add" and mode(i0) == L.BC_COL and f2 == "minimum" and mode(i2) == L.BC_SCALAR and
+                (f1 == "relu" or (f1 == "maximum" and mode(i1) == L.BC_SCALAR)))
+
+    def _plan_expand_dw(self) -> None:
+        """A 1x1 q-convolution whose f32 result only a 3x3 depthwise convolution reads (a
+        MobileNet block's expansion) runs inside that convolution's launch
+        (mr_qconv1x1_dw3x3): the expanded tensor is never stored.  Both epilogues bias ->
+        ReLU6, f32 graphs, the depthwise result read as int8."""
+        self.expand_dw: dict = {}           # depthwise op -> its expansion q-op
+        if self.target.debug_acc:
+            return
+        g = self.g
+        for op in g.ops:
+            if op.kind != "conv2d" or not self._device_op(op) or len(op.inputs) < 2:
+                continue
+            v, w = op.inputs[0], op.inputs[1]
+            e = v.producer
+            if w not in self.consts or self.consts[w].kind != "const" or e is None or e.kind != "qconv2d":
+                continue
+            if not self._device_op(e) or e in self.virtual or v in g.outputs or self.users.get(v, []) != [op]:
+                continue
+            (sh, sw), (ph, pw), (dh, dw), groups = conv_params(op.attrs)
+            n, c, h, wd = v.type.shape
+            if groups != c or np.shape(self._const_value(w)) != (c, 1, 3, 3) or sh != sw or sh not in (1, 2) or \
+                    (ph, pw) != (1, 1) or (dh, dw) != (1, 1) or c % 4:
+                continue
+            q = np.asarray(e.attrs["q"])
+            (esh, esw), (eph, epw), (edh, edw), eg = conv_params(e.attrs)
+            cin = e.inputs[0].type.shape[1]
+            if q.shape[2:] != (1, 1) or (esh, esw, eph, epw, edh, edw, eg) != (1, 1, 0, 0, 1, 1, 1) or \
+                    not 4 < cin <= 192:
+                continue
+            if v.type.dtype != "f32" or op.result.type.dtype != "f32" or v in self.half or op.result in self.half:
+                continue
+            if not self.need_i8.get(op.result) or not self._relu6_epilogue(e) or not self._relu6_epilogue(op):
+                continue
+            self.expand_dw[op] = e
+            self.skip.add(e)
+            self.need_f32.discard(v)
 
     def _plan_half_storage(self) -> None:
         """f16 values stored as IEEE halves (mr_epilogue's MR_EPI_OUT_H16 / MR_EPI_FULL_H16):
@@ -1259,7 +1312,10 @@ class RocmExecutable:
 
     def _emit_conv2d(self, op: "Op") -> None:
         """Depthwise f32 convolution (groups == C, one filter per channel); a weight-only
-        int8 convolution goes to _emit_w8_conv2d."""
+        int8 convolution goes to _emit_w8_conv2d, and one fused with the 1x1 expansion
+        before it (_plan_expand_dw) to _emit_expand_dw."""
+        if op in self.expand_dw:
+            return self._emit_expand_dw(op, self.expand_dw[op])
         wp = op.inputs[1].producer
         if wp is not None and wp.kind == "dequantize" and conv_params(op.attrs)[3] == 1:
             return self._emit_w8_conv2d(op)
@@ -1281,6 +1337,46 @@ class RocmExecutable:
         self._add("dwconv2d", lambda s: L.check(
             lib.mr_dwconv2d_f32(xt.data_ptr(), C.byref(geom), wdev.data_ptr(), C.byref(e), s), "mr_dwconv2d_f32"),
             nbytes=4 * n * c * h * w + 4 * c * kh * kw + self._epi_bytes(e, n * oh * ow, c))
+        self._finish_i8(out, fused)
+
+    def _emit_expand_dw(self, op: "Op", ex: "Op") -> None:
+        """The expansion q-op `ex` and the depthwise convolution `op` as one mr_qconv1x1_dw3x3
+        launch: the expansion's epilogue has no outputs (its result is never stored), the
+        depthwise one writes op's copies."""
+        xv = ex.inputs[0]
+        x = self._src(xv)
+        xs = _f32key(ex.attrs["x_scale"])
+        xq, cp = x.i8[xs] if xs in x.i8 else self._quantize_to(x, xs)
+        q = np.asarray(ex.attrs["q"], np.int8)
+        bl = pack.pack_conv(q, cp)
+        b = self._upload(pack.device_weights(bl))
+        scale = self._upload(pack.combined_scale(ex.attrs["x_scale"], ex.attrs["w_scale"]))
+        ee = L.Epilogue()
+        steps = ex.attrs["epilogue"]
+        ee.n_steps = len(steps)
+        for i, (fn, idx, _sw) in enumerate(steps):
+            ee.steps[i].fn = L.EPI_FN[fn]
+            if idx is not None:
+                mode, t, ld = self._const_operand(ex.inputs[idx], ex.result.type.shape, True)
+                ee.steps[i].mode, ee.steps[i].ptr, ee.steps[i].ld = mode, t.data_ptr(), ld
+        ee.scale = scale.data_ptr()
+        self.keep.append(ee)
+        n, c, h, w = ex.result.type.shape
+        _, _, oh, ow = op.result.type.shape
+        (s, _), _, _, _ = conv_params(op.attrs)
+        wt = self._const_value(op.inputs[1]).astype(np.float32)              # [C, 1, 3, 3]
+        wdev = self._upload(np.ascontiguousarray(wt[:, 0].transpose(1, 2, 0)))   # [3, 3, C]
+        geom = L.ConvGeom(n=n, h=h, w=w, c=c, c_pad=c, o=c, oh=oh, ow=ow, kh=3, kw=3, sh=s, sw=s, ph=1, pw=1, dh=1,
+                          dw=1)
+        self.keep.append(geom)
+        out = self._new_dv(op.result)
+        e, fused = self._epilogue(op, out, True, 2, None)
+        lib, kp, npad, cin = self.lib, bl.shape[1], bl.shape[0], xv.type.shape[1]
+        self._add("expand_dw", lambda st: L.check(
+            lib.mr_qconv1x1_dw3x3(xq.data_ptr(), cp, b.data_ptr(), kp, npad, cin, C.byref(ee), C.byref(geom),
+                                  wdev.data_ptr(), C.byref(e), st), "mr_qconv1x1_dw3x3"),
+            nbytes=n * h * w * cp + c * cin + 36 * c + self._epi_bytes(e, n * oh * ow, c),
+            nops=2 * n * h * w * c * cin)
         self._finish_i8(out, fused)
 
     def _emit_fused_stem(self, op: "Op") -> None:

@@ -778,6 +778,105 @@ def test_dwconv_relu6(lib, n, c, h, s, k, form, ldo_pad):
                       G.quantize_activation(want, xs_next).astype(np.int8).transpose(0, 2, 3, 1).reshape(M, c))
 
 
+# ---------------------------------------------------------------- fused 1x1 expansion + 3x3 depthwise
+
+def _expand_dw_case(lib, n, k, c, h, s, f32_out, seed):
+    """A MobileNet block's expansion (1x1 qconv2d, bias, ReLU6 -> f32) and depthwise
+    conv (3x3, bias, ReLU6 -> int8 and optionally f32) as one mr_qconv1x1_dw3x3 launch.
+    Returns (rc, got int8, got f32 or None, want int8, want f32)."""
+    torch = _torch()
+    rng = np.random.default_rng(seed)
+    x = rng.uniform(-1, 1, (n, k, h, h)).astype(np.float32)
+    we = rng.standard_normal((c, k, 1, 1)).astype(np.float32)
+    q, ws = G.quantize_array(we, 0)
+    xs = float(np.abs(x).max()) / 127
+    be = (rng.standard_normal((c, 1, 1)) * 0.5).astype(np.float32)
+    wd = (rng.standard_normal((c, 1, 3, 3)) * 0.5).astype(np.float32)
+    bd = (rng.standard_normal((c, 1, 1)) * 0.5).astype(np.float32)
+    zero, six = np.array(0, np.float32), np.array(6, np.float32)
+    r6 = (("add", 1, False), ("maximum", 2, False), ("minimum", 3, False))
+    ea = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "stride": (1, 1), "padding": (0, 0), "epilogue": r6}
+    want_e = G.qconv2d([x, be, zero, six], ea)
+    da = {"stride": (s, s), "padding": (1, 1), "groups": c,
+          "epilogue": (("add", 2, False), ("maximum", 3, False), ("minimum", 4, False))}
+    want = G.conv2d([want_e, wd, bd, zero, six], da)
+    oh = want.shape[2]
+    next_xs = float(np.abs(want).max()) / 127 or 1.0
+    want_q = G.quantize_activation(want, next_xs).astype(np.int8).transpose(0, 2, 3, 1).reshape(-1, c)
+    cp = pack.c_pad_for(k)
+    xq = empty((n, h, h, cp), torch.int8)
+    L.check(lib.mr_quantize_nchw_nhwc(T(x).data_ptr(), n, k, h, h, xq.data_ptr(), cp, xs, stream()), "q")
+    bl = pack.pack_conv(q, cp)
+    b = T(pack.device_weights(bl))
+    keep = [T(be.reshape(c)), T(zero.reshape(1)), T(six.reshape(1)), T(bd.reshape(c)),
+            T(pack.combined_scale(xs, ws)), T(np.ascontiguousarray(wd[:, 0].transpose(1, 2, 0)))]
+    bet, zt, st, bdt, scale, wdt = keep
+    ee = epilogue([("add", L.BC_COL, bet, 0, False), ("maximum", L.BC_SCALAR, zt, 0, False),
+                   ("minimum", L.BC_SCALAR, st, 0, False)], scale=scale)
+    M = n * oh * oh
+    ldq = pack.c_pad_for(c)
+    yq = torch.full((M, ldq), 99, dtype=torch.int8, device="cuda")
+    y = torch.full((M, c), float("nan"), dtype=torch.float32, device="cuda") if f32_out else None
+    ed = epilogue([("add", L.BC_COL, bdt, 0, False), ("maximum", L.BC_SCALAR, zt, 0, False),
+                   ("minimum", L.BC_SCALAR, st, 0, False)], out_f32=y, ldo=c, out_i8=yq, ldq=ldq, xs=next_xs)
+    g = L.ConvGeom(n=n, h=h, w=h, c=c, c_pad=c, o=c, oh=oh, ow=oh, kh=3, kw=3, sh=s, sw=s, ph=1, pw=1, dh=1, dw=1)
+    rc = lib.mr_qconv1x1_dw3x3(xq.data_ptr(), cp, b.data_ptr(), bl.shape[1], bl.shape[0], k, C.byref(ee), C.byref(g),
+                               wdt.data_ptr(), C.byref(ed), stream())
+    sync()
+    got_q = yq.cpu().numpy()
+    assert (got_q[:, c:] == 99).all()          # nothing written past the c channels
+    got = y.cpu().numpy() if f32_out else None
+    return rc, got_q[:, :c], got, want_q, want.transpose(0, 2, 3, 1).reshape(-1, c)
+
+
+@pytest.mark.parametrize("n,k,c,h,s,f32_out", [
+    (2, 16, 96, 112, 2, False),     # MobileNetV2 block 2 (k_pad 64, stride 2, 7x7 tiles)
+    (2, 24, 144, 56, 1, False),     # 144 channels: a half-empty last 32-channel block; 14x14 tiles
+    (2, 24, 144, 56, 2, True),      # with the f32 result too
+    (1, 32, 192, 28, 1, False),
+    (3, 64, 384, 14, 1, False),     # 12 channel blocks split over workgroups
+    (2, 96, 576, 14, 2, False),     # k_pad 128
+    (2, 160, 960, 7, 1, True),      # k_pad 192, one 7x7 tile per image
+    (2, 40, 100, 17, 2, False),     # ragged: K 40 (row stride 48), 100 channels, odd image
+    (1, 16, 36, 13, 1, False),      # partial tiles (13 = 7 + 6), 36 channels
+    (2, 8, 32, 9, 1, True),         # K below one 16-byte chunk of the 16-byte row stride
+])
+def test_qconv1x1_dw3x3(lib, n, k, c, h, s, f32_out):
+    rc, got_q, got, want_q, want = _expand_dw_case(lib, n, k, c, h, s, f32_out, n * 100 + k + c + h)
+    assert rc == 0, lib.mr_last_error()
+    assert bits_equal(got_q, want_q)
+    if f32_out:
+        assert bits_equal(got, want)
+
+
+def test_qconv1x1_dw3x3_rejects(lib):
+    """Forms it has no kernel for return MR_EUNSUPPORTED (the target makes two launches);
+    an expansion epilogue that stores its result is an argument error."""
+    torch = _torch()
+    x = empty((1, 8, 8, 256), torch.int8)
+    b = empty((4, 64, 64), torch.int8)
+    w = empty((9, 64), torch.float32)
+    z, six, bias, sc = empty((1,), torch.float32), empty((1,), torch.float32), empty((64,), torch.float32), \
+        empty((64,), torch.float64)
+    r6 = [("add", L.BC_COL, bias, 0, False), ("maximum", L.BC_SCALAR, z, 0, False),
+          ("minimum", L.BC_SCALAR, six, 0, False)]
+    yq = empty((64, 64), torch.int8)
+    g = L.ConvGeom(n=1, h=8, w=8, c=64, c_pad=64, o=64, oh=8, ow=8, kh=3, kw=3, sh=1, sw=1, ph=1, pw=1, dh=1, dw=1)
+    ed = epilogue(r6, out_i8=yq, ldq=64, xs=0.1)
+
+    def call(ee, k_pad=64, K=64, dw=ed):
+        return lib.mr_qconv1x1_dw3x3(x.data_ptr(), 256, b.data_ptr(), k_pad, 64, K, C.byref(ee), C.byref(g),
+                                     w.data_ptr(), C.byref(dw), stream())
+    assert call(epilogue(r6, scale=sc), k_pad=256, K=256) == 3             # k_pad above 192
+    assert call(epilogue(r6[:2], scale=sc)) == 3                          # ReLU without the upper bound
+    f16 = epilogue(r6, scale=sc)
+    f16.flags = L.EPI_OUT_F16
+    assert call(f16) == 3                                                 # f16 rounding
+    assert call(epilogue(r6, scale=sc, out_i8=yq, ldq=64, xs=0.1)) == 1    # the expansion stores its result
+    assert call(epilogue(r6, scale=sc), dw=epilogue(r6, out_f32=empty((64, 64), torch.float32), ldo=64)) == 1
+    sync()
+
+
 def test_maxpool_with_folded_pad(lib):
     torch = _torch()
     rng = np.random.default_rng(12)
