@@ -137,6 +137,14 @@ expand_dw_kernel(const ExpandDwArgs a, const EpiDev ex, const EpiDev dw) {
     y = max_bound(y, ex_lo, ex_lo_nan);
     return min_bound(y, ex_hi, ex_hi_nan);
   };
+  // With a finite bias and bounds lo <= hi the expanded value is never NaN, and the two
+  // bounds are one median (v_med3_f32): equal to them up to the sign of a zero result, which
+  // the depthwise sums cannot see (they start from +0, and +0 + -0 = +0 in round to
+  // nearest).  Taken when every lane of the wave qualifies.
+  const bool ex_med3 = __all(isfinite(ebias) && !ex_lo_nan && !ex_hi_nan && ex_lo <= ex_hi);
+  auto expand_med3 = [&](int32_t v) __attribute__((always_inline)) {
+    return __builtin_amdgcn_fmed3f(__fadd_rn(dequant(v, escale), ebias), ex_lo, ex_hi);
+  };
 
   for (; id < a.total; id += gridDim.x) {
     const int img = id / a.tiles, tile = id - img * a.tiles;
@@ -175,13 +183,24 @@ expand_dw_kernel(const ExpandDwArgs a, const EpiDev ex, const EpiDev dw) {
     // the expansion epilogue (lane: column lane % 32, rows 8 (r / 4) + 4 (lane / 32) + r % 4
     // of each block) into E, every row of the blocks (region pixels outside the image are
     // zeroed afterwards)
+    if (ex_med3) {
 #pragma unroll
-    for (int j = 0; j < RPW; ++j) {
-      const int rb = wave + 4 * j;
-      if (rb >= PB) continue;
+      for (int j = 0; j < RPW; ++j) {
+        const int rb = wave + 4 * j;
+        if (rb >= PB) continue;
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        E[(rb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * EST + (lane & 31)] = expand(acc[j][r]);
+        for (int r = 0; r < 16; ++r)
+          E[(rb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * EST + (lane & 31)] = expand_med3(acc[j][r]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < RPW; ++j) {
+        const int rb = wave + 4 * j;
+        if (rb >= PB) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          E[(rb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * EST + (lane & 31)] = expand(acc[j][r]);
+      }
     }
     lds_store_barrier();   // E written
     if (!interior) {

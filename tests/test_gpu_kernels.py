@@ -780,7 +780,7 @@ def test_dwconv_relu6(lib, n, c, h, s, k, form, ldo_pad):
 
 # ---------------------------------------------------------------- fused 1x1 expansion + 3x3 depthwise
 
-def _expand_dw_case(lib, n, k, c, h, s, f32_out, seed):
+def _expand_dw_case(lib, n, k, c, h, s, f32_out, seed, inf_bias=False):
     """A MobileNet block's expansion (1x1 qconv2d, bias, ReLU6 -> f32) and depthwise
     conv (3x3, bias, ReLU6 -> int8 and optionally f32) as one mr_qconv1x1_dw3x3 launch.
     Returns (rc, got int8, got f32 or None, want int8, want f32)."""
@@ -791,6 +791,8 @@ def _expand_dw_case(lib, n, k, c, h, s, f32_out, seed):
     q, ws = G.quantize_array(we, 0)
     xs = float(np.abs(x).max()) / 127
     be = (rng.standard_normal((c, 1, 1)) * 0.5).astype(np.float32)
+    if inf_bias:    # channels whose expansion saturates: the exact (non-median) epilogue path
+        be[3], be[5] = np.inf, -np.inf
     wd = (rng.standard_normal((c, 1, 3, 3)) * 0.5).astype(np.float32)
     bd = (rng.standard_normal((c, 1, 1)) * 0.5).astype(np.float32)
     zero, six = np.array(0, np.float32), np.array(6, np.float32)
@@ -847,6 +849,14 @@ def test_qconv1x1_dw3x3(lib, n, k, c, h, s, f32_out):
     assert bits_equal(got_q, want_q)
     if f32_out:
         assert bits_equal(got, want)
+
+
+def test_qconv1x1_dw3x3_infinite_bias(lib):
+    """A first channel block whose expansion bias holds +inf and -inf takes the exact
+    maximum/minimum epilogue (ReLU6 gives 6 and 0 there), the other blocks the median one."""
+    rc, got_q, got, want_q, want = _expand_dw_case(lib, 2, 24, 96, 20, 1, True, 5, inf_bias=True)
+    assert rc == 0, lib.mr_last_error()
+    assert bits_equal(got_q, want_q) and bits_equal(got, want)
 
 
 def test_qconv1x1_dw3x3_rejects(lib):
