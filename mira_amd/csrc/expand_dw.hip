@@ -19,6 +19,7 @@
 // bit-exact (the accumulation order of each depthwise output is the row-major
 // tap order of dwconv3x3_kernel, a separate multiply and add per tap).
 #include <algorithm>
+#include <type_traits>
 
 #include "mr_common.hpp"
 
@@ -221,41 +222,53 @@ expand_dw_kernel(const ExpandDwArgs a, const EpiDev ex, const EpiDev dw) {
 #pragma unroll
       for (int k = 0; k < 9; ++k) w9[k] = wl[k][q];
       const float4 dbias = wl[9][q];
+      // int8 only, finite biases and bounds lo <= hi: the sums are finite, so the bounds are
+      // one median, exact up to the sign of a zero, which quantizes to the same byte
+      const bool dw_med3 = !DF32 && __all(isfinite(dbias.x) && isfinite(dbias.y) && isfinite(dbias.z) &&
+                                          isfinite(dbias.w) && !dw_lo_nan && !dw_hi_nan && dw_lo <= dw_hi);
+      auto slots = [&](auto med3) __attribute__((always_inline)) {
 #pragma unroll 1
-      for (int sl = 0; sl < NSLOT; ++sl) {
-        const int pi = (t >> 3) + sl * 32;
-        if (pi >= T * T) break;
-        const int oy = pi / T, ox = pi - oy * T;
-        const int oh = oh0 + oy, ow = ow0 + ox;
-        if (oh >= a.OH || ow >= a.OW) continue;
-        float acc4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int sl = 0; sl < NSLOT; ++sl) {
+          const int pi = (t >> 3) + sl * 32;
+          if (pi >= T * T) break;
+          const int oy = pi / T, ox = pi - oy * T;
+          const int oh = oh0 + oy, ow = ow0 + ox;
+          if (oh >= a.OH || ow >= a.OW) continue;
+          float acc4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int ki = 0; ki < 3; ++ki)
+          for (int ki = 0; ki < 3; ++ki)
 #pragma unroll
-          for (int kj = 0; kj < 3; ++kj) {
-            const float4 xv = *reinterpret_cast<const float4*>(E + ((oy * S + ki) * IR + ox * S + kj) * EST + 4 * q);
-            const float4 w = w9[ki * 3 + kj];
-            acc4[0] = __fadd_rn(acc4[0], __fmul_rn(xv.x, w.x));
-            acc4[1] = __fadd_rn(acc4[1], __fmul_rn(xv.y, w.y));
-            acc4[2] = __fadd_rn(acc4[2], __fmul_rn(xv.z, w.z));
-            acc4[3] = __fadd_rn(acc4[3], __fmul_rn(xv.w, w.w));
+            for (int kj = 0; kj < 3; ++kj) {
+              const float4 xv = *reinterpret_cast<const float4*>(E + ((oy * S + ki) * IR + ox * S + kj) * EST + 4 * q);
+              const float4 w = w9[ki * 3 + kj];
+              acc4[0] = __fadd_rn(acc4[0], __fmul_rn(xv.x, w.x));
+              acc4[1] = __fadd_rn(acc4[1], __fmul_rn(xv.y, w.y));
+              acc4[2] = __fadd_rn(acc4[2], __fmul_rn(xv.z, w.z));
+              acc4[3] = __fadd_rn(acc4[3], __fmul_rn(xv.w, w.w));
+            }
+          const float bias[4] = {dbias.x, dbias.y, dbias.z, dbias.w};
+          float y[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const float v = __fadd_rn(acc4[c], bias[c]);
+            if constexpr (decltype(med3)::value)
+              y[c] = __builtin_amdgcn_fmed3f(v, dw_lo, dw_hi);
+            else
+              y[c] = min_bound(max_bound(v, dw_lo, dw_lo_nan), dw_hi, dw_hi_nan);
           }
-        const float bias[4] = {dbias.x, dbias.y, dbias.z, dbias.w};
-        float y[4];
+          const int64_t pix = (int64_t(img) * a.OH + oh) * a.OW + ow;
+          if constexpr (DF32)
+            *reinterpret_cast<float4*>(dw.out_f32 + pix * dw.ldo + cq) = make_float4(y[0], y[1], y[2], y[3]);
+          uint32_t packed = 0;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          float v = __fadd_rn(acc4[c], bias[c]);
-          v = max_bound(v, dw_lo, dw_lo_nan);
-          y[c] = min_bound(v, dw_hi, dw_hi_nan);
+          for (int c = 0; c < 4; ++c) packed |= uint32_t(uint8_t(quantize_rcp(y[c], dw.out_rxs))) << (8 * c);
+          *reinterpret_cast<uint32_t*>(dw.out_i8 + pix * dw.ldq + cq) = packed;
         }
-        const int64_t pix = (int64_t(img) * a.OH + oh) * a.OW + ow;
-        if constexpr (DF32)
-          *reinterpret_cast<float4*>(dw.out_f32 + pix * dw.ldo + cq) = make_float4(y[0], y[1], y[2], y[3]);
-        uint32_t packed = 0;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) packed |= uint32_t(uint8_t(quantize_rcp(y[c], dw.out_rxs))) << (8 * c);
-        *reinterpret_cast<uint32_t*>(dw.out_i8 + pix * dw.ldq + cq) = packed;
-      }
+      };
+      if (dw_med3)
+        slots(std::true_type{});
+      else
+        slots(std::false_type{});
     }
   }
 }
