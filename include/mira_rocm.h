@@ -281,6 +281,17 @@ int mr_qconv1x1_dw3x3(const int8_t* x, int64_t ldx, const int8_t* b, int64_t k_p
                       const mr_epilogue* epi_expand, const mr_conv_geom* dw, const float* w_dw,
                       const mr_epilogue* epi_dw, void* stream);
 
+/* The same fusion when the first convolution is a network's 3x3 stem (padding 1,
+ * stride 1 or 2) over an image of at most 4 channels stored 4 bytes per pixel
+ * (mr_quantize_nchw_nhwc with c_pad 4): `stem` is its geometry (c_pad 4, o ==
+ * dw->c, output == the depthwise input), b its packed weights in the stem
+ * layout (mira_amd.pack.pack_conv(q, 4): kernel row i in the 16-byte chunk i,
+ * k_pad 64).  Everything else as mr_qconv1x1_dw3x3; bit-exact with mr_qconv2d
+ * followed by mr_dwconv2d_f32. */
+int mr_qstem3x3_dw3x3(const int8_t* x, const mr_conv_geom* stem, const int8_t* b, int64_t k_pad, int64_t n_pad,
+                      const mr_epilogue* epi_stem, const mr_conv_geom* dw, const float* w_dw,
+                      const mr_epilogue* epi_dw, void* stream);
+
 /* ---- adjuncts ---------------------------------------------------------- */
 
 /* mira/ops.py:293-296 maxpool2d with the -inf/constant pad of

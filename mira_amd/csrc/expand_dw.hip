@@ -36,10 +36,15 @@ struct ExpandDwArgs {
   int32_t H, W, C, OH, OW;
   int32_t tiles_w, tiles;   // output tiles per tile row, per image
   int32_t total;            // tiles of the whole batch
+  int32_t Hin, Win, SS;     // STEM: the 3x3 convolution's input size and stride
 };
 
 // S: depthwise stride; T: output tile edge; KP: k_pad of the 1x1 weights;
 // DF32: the depthwise result is also stored as f32 (besides its int8 copy).
+// STEM: the first convolution is instead a 3x3 one (padding 1, stride SS) over a
+// 4-byte-per-pixel image (3 channels and a zero), its weights in the stem layout
+// (kernel row ki in the 16-byte chunk ki: three 4-byte taps and a zero word), so
+// the A row of a region pixel is its nine input pixels gathered into those chunks.
 // blockIdx.y: the 32-channel block, whose weights and column constants a
 // workgroup loads once; it then walks tiles blockIdx.x, + gridDim.x, ..., loading
 // the next tile's region into registers while it computes the current one.  The
@@ -54,7 +59,7 @@ constexpr int ed_occupancy() {
   return 163840 / bytes >= 4 ? 4 : 163840 / bytes;
 }
 
-template <int S, int T, int KP, bool DF32>
+template <int S, int T, int KP, bool DF32, bool STEM>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ed_occupancy<S, T, KP>())))
 expand_dw_kernel(const ExpandDwArgs a, const EpiDev ex, const EpiDev dw) {
   constexpr int IR = (T - 1) * S + 3;   // input region edge
@@ -90,8 +95,19 @@ expand_dw_kernel(const ExpandDwArgs a, const EpiDev ex, const EpiDev dw) {
       const int p = i / KC, kc = i - p * KC;
       const int ih = ih0 + p / IR, iw = iw0 + p % IR;
       va[u] = v4i{0, 0, 0, 0};
-      if (i < P * KC && unsigned(ih) < unsigned(a.H) && unsigned(iw) < unsigned(a.W) && kc * 16 < a.ldx)
-        va[u] = *reinterpret_cast<const v4i*>(a.x + ((int64_t(img) * a.H + ih) * a.W + iw) * a.ldx + kc * 16);
+      if constexpr (STEM) {
+        // kernel row kc of region pixel (ih, iw)'s 3x3 window: three 4-byte input pixels
+        const int iy = ih * a.SS - 1 + kc, ix0 = iw * a.SS - 1;
+        if (i < P * KC && kc < 3 && unsigned(iy) < unsigned(a.Hin)) {
+          const int32_t* row = reinterpret_cast<const int32_t*>(a.x) + (int64_t(img) * a.Hin + iy) * a.Win;
+#pragma unroll
+          for (int j = 0; j < 3; ++j)
+            if (unsigned(ix0 + j) < unsigned(a.Win)) va[u][j] = row[ix0 + j];
+        }
+      } else {
+        if (i < P * KC && unsigned(ih) < unsigned(a.H) && unsigned(iw) < unsigned(a.W) && kc * 16 < a.ldx)
+          va[u] = *reinterpret_cast<const v4i*>(a.x + ((int64_t(img) * a.H + ih) * a.W + iw) * a.ldx + kc * 16);
+      }
     }
   };
   int id = blockIdx.x;
@@ -273,13 +289,13 @@ expand_dw_kernel(const ExpandDwArgs a, const EpiDev ex, const EpiDev dw) {
   }
 }
 
-template <int S, int T, int KP>
+template <int S, int T, int KP, bool STEM = false>
 static void expand_dw_launch(const ExpandDwArgs& a, const EpiDev& ex, const EpiDev& dw, dim3 grid,
                              hipStream_t stream) {
   if (dw.out_f32)
-    hipLaunchKernelGGL((expand_dw_kernel<S, T, KP, true>), grid, dim3(256), 0, stream, a, ex, dw);
+    hipLaunchKernelGGL((expand_dw_kernel<S, T, KP, true, STEM>), grid, dim3(256), 0, stream, a, ex, dw);
   else
-    hipLaunchKernelGGL((expand_dw_kernel<S, T, KP, false>), grid, dim3(256), 0, stream, a, ex, dw);
+    hipLaunchKernelGGL((expand_dw_kernel<S, T, KP, false, STEM>), grid, dim3(256), 0, stream, a, ex, dw);
 }
 
 template <int S, int T>
@@ -298,68 +314,103 @@ static bool relu6_form(const EpiDev& e) {
   return e.fixed && !e.f_mul && e.f_col && !e.f_full && e.f_lo && e.f_hi && !e.f16 && !e.out_acc;
 }
 
-}  // namespace mr
-
-extern "C" int mr_qconv1x1_dw3x3(const int8_t* x, int64_t ldx, const int8_t* b, int64_t k_pad, int64_t n_pad,
-                                 int64_t K, const mr_epilogue* epi_expand, const mr_conv_geom* dwg,
-                                 const float* w_dw, const mr_epilogue* epi_dw, void* stream) {
-  MR_REQUIRE(x && b && epi_expand && dwg && w_dw && epi_dw, "mr_qconv1x1_dw3x3: NULL argument");
+// Checks and launch shared by both entry points: the depthwise geometry, both epilogues,
+// the launch (stem: the first convolution's 3x3 geometry, else the 1x1 expansion's).
+static int expand_dw_run(const char* fn, const int8_t* x, int64_t ldx, const int8_t* b, int64_t k_pad,
+                         int64_t n_pad, const mr_epilogue* epi_expand, const mr_conv_geom* dwg, const float* w_dw,
+                         const mr_epilogue* epi_dw, void* stream, const mr_conv_geom* stem) {
+  MR_REQUIRE(x && b && epi_expand && dwg && w_dw && epi_dw, "%s: NULL argument", fn);
   const mr_conv_geom& G = *dwg;
   MR_REQUIRE(G.n >= 0 && G.h > 0 && G.w > 0 && G.c > 0 && G.o == G.c && G.c_pad == G.c,
-             "mr_qconv1x1_dw3x3: bad depthwise geometry (o == c == c_pad)");
+             "%s: bad depthwise geometry (o == c == c_pad)", fn);
   MR_REQUIRE(G.kh == 3 && G.kw == 3 && G.dh == 1 && G.dw == 1 && G.ph == 1 && G.pw == 1 && G.sh == G.sw &&
                  (G.sh == 1 || G.sh == 2),
-             "mr_qconv1x1_dw3x3: the depthwise convolution must be 3x3, padding 1, stride 1 or 2");
+             "%s: the depthwise convolution must be 3x3, padding 1, stride 1 or 2", fn);
   const int32_t oh = (G.h + 2 - 3) / G.sh + 1, ow = (G.w + 2 - 3) / G.sw + 1;
-  MR_REQUIRE(oh == G.oh && ow == G.ow, "mr_qconv1x1_dw3x3: output %dx%d does not match (%dx%d)", G.oh, G.ow, oh, ow);
-  MR_REQUIRE(G.c % 4 == 0, "mr_qconv1x1_dw3x3: channel count %d must be a multiple of 4", G.c);
-  MR_REQUIRE(K > 0 && ldx >= K && ldx % 16 == 0, "mr_qconv1x1_dw3x3: ldx %lld must be >= K and a multiple of 16",
-             (long long)ldx);
-  MR_REQUIRE(k_pad >= K && k_pad % 64 == 0, "mr_qconv1x1_dw3x3: k_pad %lld must be >= K and a multiple of 64",
-             (long long)k_pad);
-  MR_REQUIRE(n_pad >= G.c && n_pad % 32 == 0, "mr_qconv1x1_dw3x3: n_pad %lld must be >= c and a multiple of 32",
+  MR_REQUIRE(oh == G.oh && ow == G.ow, "%s: output %dx%d does not match (%dx%d)", fn, G.oh, G.ow, oh, ow);
+  MR_REQUIRE(G.c % 4 == 0, "%s: channel count %d must be a multiple of 4", fn, G.c);
+  MR_REQUIRE(n_pad >= G.c && n_pad % 32 == 0, "%s: n_pad %lld must be >= c and a multiple of 32", fn,
              (long long)n_pad);
-  MR_REQUIRE(mr::aligned16(x) && mr::aligned16(b) && mr::aligned16(w_dw),
-             "mr_qconv1x1_dw3x3: x, b and w_dw must be 16-byte aligned");
+  MR_REQUIRE(aligned16(x) && aligned16(b) && aligned16(w_dw), "%s: x, b and w_dw must be 16-byte aligned", fn);
   MR_REQUIRE(!epi_expand->out_f32 && !epi_expand->out_i8 && !epi_expand->out_acc,
-             "mr_qconv1x1_dw3x3: the expansion's result is not stored (its epilogue has no outputs)");
-  MR_REQUIRE(epi_dw->out_i8 != nullptr, "mr_qconv1x1_dw3x3: the depthwise result needs its int8 copy");
-  mr::EpiDev ex, dw;
-  int rc = mr::make_epi(epi_expand, G.c, true, &ex, false, false);
+             "%s: the first convolution's result is not stored (its epilogue has no outputs)", fn);
+  MR_REQUIRE(epi_dw->out_i8 != nullptr, "%s: the depthwise result needs its int8 copy", fn);
+  EpiDev ex, dw;
+  int rc = make_epi(epi_expand, G.c, true, &ex, false, false);
   if (rc != MR_OK) return rc;
-  rc = mr::make_epi(epi_dw, G.c, false, &dw);
+  rc = make_epi(epi_dw, G.c, false, &dw);
   if (rc != MR_OK) return rc;
-  if (k_pad > 192 || !mr::relu6_form(ex) || !mr::relu6_form(dw)) {
-    mr::set_error("mr_qconv1x1_dw3x3: compiled for k_pad <= 192 and bias -> maximum -> minimum epilogues on both "
-                  "convolutions without f16 rounding");
+  if (k_pad > 192 || !relu6_form(ex) || !relu6_form(dw)) {
+    set_error("%s: compiled for k_pad <= 192 and bias -> maximum -> minimum epilogues on both convolutions "
+              "without f16 rounding", fn);
     return MR_EUNSUPPORTED;
   }
   MR_REQUIRE(dw.ldq % 4 == 0 && reinterpret_cast<uintptr_t>(dw.out_i8) % 4 == 0 &&
-                 (!dw.out_f32 || (dw.ldo % 4 == 0 && mr::aligned16(dw.out_f32))) && mr::aligned16(dw.col_ptr),
-             "mr_qconv1x1_dw3x3: depthwise outputs and bias must be aligned for 4-channel runs");
+                 (!dw.out_f32 || (dw.ldo % 4 == 0 && aligned16(dw.out_f32))) && aligned16(dw.col_ptr),
+             "%s: depthwise outputs and bias must be aligned for 4-channel runs", fn);
   if (G.n == 0) return MR_OK;
   const int T = G.sh == 1 && oh >= 14 ? 14 : 7;
-  mr::ExpandDwArgs a = {};
+  ExpandDwArgs a = {};
   a.x = x;
   a.b = b;
   a.wdw = w_dw;
   a.ldx = static_cast<int32_t>(ldx);
   a.n_pad = static_cast<int32_t>(n_pad);
   a.H = G.h; a.W = G.w; a.C = G.c; a.OH = oh; a.OW = ow;
+  if (stem) {
+    a.Hin = stem->h; a.Win = stem->w; a.SS = stem->sh;
+  }
   a.tiles_w = (ow + T - 1) / T;
   a.tiles = a.tiles_w * ((oh + T - 1) / T);
   const int n_cb = (G.c + 31) / 32;
   const int64_t total = int64_t(G.n) * a.tiles;
-  MR_REQUIRE(total < (int64_t(1) << 31), "mr_qconv1x1_dw3x3: too many tiles");
+  MR_REQUIRE(total < (int64_t(1) << 31), "%s: too many tiles", fn);
   a.total = static_cast<int32_t>(total);
   // workgroups per channel block: about eight per CU over all blocks, each walking its
   // share of the tiles
-  const int64_t per_cb = std::max<int64_t>(1, std::min<int64_t>(total, (8 * mr::device_cu_count() + n_cb - 1) / n_cb));
+  const int64_t per_cb = std::max<int64_t>(1, std::min<int64_t>(total, (8 * device_cu_count() + n_cb - 1) / n_cb));
   const dim3 grid(static_cast<unsigned>(per_cb), static_cast<unsigned>(n_cb));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (G.sh == 2) mr::expand_dw_kp<2, 7>(k_pad, a, ex, dw, grid, s);
-  else if (T == 14) mr::expand_dw_kp<1, 14>(k_pad, a, ex, dw, grid, s);
-  else mr::expand_dw_kp<1, 7>(k_pad, a, ex, dw, grid, s);
-  MR_LAUNCH_CHECK("qconv1x1_dw3x3");
+  if (stem) {
+    if (G.sh == 2) expand_dw_launch<2, 7, 64, true>(a, ex, dw, grid, s);
+    else if (T == 14) expand_dw_launch<1, 14, 64, true>(a, ex, dw, grid, s);
+    else expand_dw_launch<1, 7, 64, true>(a, ex, dw, grid, s);
+  } else {
+    if (G.sh == 2) expand_dw_kp<2, 7>(k_pad, a, ex, dw, grid, s);
+    else if (T == 14) expand_dw_kp<1, 14>(k_pad, a, ex, dw, grid, s);
+    else expand_dw_kp<1, 7>(k_pad, a, ex, dw, grid, s);
+  }
+  MR_LAUNCH_CHECK(fn);
   return MR_OK;
+}
+
+}  // namespace mr
+
+extern "C" int mr_qconv1x1_dw3x3(const int8_t* x, int64_t ldx, const int8_t* b, int64_t k_pad, int64_t n_pad,
+                                 int64_t K, const mr_epilogue* epi_expand, const mr_conv_geom* dwg,
+                                 const float* w_dw, const mr_epilogue* epi_dw, void* stream) {
+  MR_REQUIRE(K > 0 && ldx >= K && ldx % 16 == 0, "mr_qconv1x1_dw3x3: ldx %lld must be >= K and a multiple of 16",
+             (long long)ldx);
+  MR_REQUIRE(k_pad >= K && k_pad % 64 == 0, "mr_qconv1x1_dw3x3: k_pad %lld must be >= K and a multiple of 64",
+             (long long)k_pad);
+  return mr::expand_dw_run("mr_qconv1x1_dw3x3", x, ldx, b, k_pad, n_pad, epi_expand, dwg, w_dw, epi_dw, stream,
+                           nullptr);
+}
+
+extern "C" int mr_qstem3x3_dw3x3(const int8_t* x, const mr_conv_geom* stem, const int8_t* b, int64_t k_pad,
+                                 int64_t n_pad, const mr_epilogue* epi_stem, const mr_conv_geom* dwg,
+                                 const float* w_dw, const mr_epilogue* epi_dw, void* stream) {
+  MR_REQUIRE(stem && dwg, "mr_qstem3x3_dw3x3: NULL geometry");
+  const mr_conv_geom& g = *stem;
+  MR_REQUIRE(g.kh == 3 && g.kw == 3 && g.c > 0 && g.c <= 4 && g.c_pad == 4 && g.ph == 1 && g.pw == 1 &&
+                 g.dh == 1 && g.dw == 1 && g.sh == g.sw && (g.sh == 1 || g.sh == 2),
+             "mr_qstem3x3_dw3x3: the first convolution must be 3x3, padding 1, stride 1 or 2, over at most 4 "
+             "channels stored 4 per pixel");
+  MR_REQUIRE(g.h > 0 && g.w > 0 && g.oh == (g.h - 1) / g.sh + 1 && g.ow == (g.w - 1) / g.sw + 1,
+             "mr_qstem3x3_dw3x3: output %dx%d does not match the input %dx%d", g.oh, g.ow, g.h, g.w);
+  MR_REQUIRE(g.n == dwg->n && g.o == dwg->c && g.oh == dwg->h && g.ow == dwg->w,
+             "mr_qstem3x3_dw3x3: the depthwise input must be the first convolution's output");
+  MR_REQUIRE(k_pad == 64, "mr_qstem3x3_dw3x3: the stem-layout weights have k_pad 64, not %lld", (long long)k_pad);
+  MR_REQUIRE(int64_t(g.n) * g.h * g.w < (int64_t(1) << 31), "mr_qstem3x3_dw3x3: image too large");
+  return mr::expand_dw_run("mr_qstem3x3_dw3x3", x, 4, b, k_pad, n_pad, epi_stem, dwg, w_dw, epi_dw, stream, stem);
 }

@@ -689,7 +689,8 @@ class RocmExecutable:
     def _plan_expand_dw(self) -> None:
         """A 1x1 q-convolution whose f32 result only a 3x3 depthwise convolution reads (a
         MobileNet block's expansion) runs inside that convolution's launch
-        (mr_qconv1x1_dw3x3): the expanded tensor is never stored.  Both epilogues bias ->
+        (mr_qconv1x1_dw3x3), and so does a 3x3 stem over an image of at most 4 channels
+        (mr_qstem3x3_dw3x3): the expanded tensor is never stored.  Both epilogues bias ->
         ReLU6, f32 graphs, the depthwise result read as int8."""
         self.expand_dw: dict = {}           # depthwise op -> its expansion q-op
         if self.target.debug_acc:
@@ -712,8 +713,12 @@ class RocmExecutable:
             q = np.asarray(e.attrs["q"])
             (esh, esw), (eph, epw), (edh, edw), eg = conv_params(e.attrs)
             cin = e.inputs[0].type.shape[1]
-            if q.shape[2:] != (1, 1) or (esh, esw, eph, epw, edh, edw, eg) != (1, 1, 0, 0, 1, 1, 1) or \
-                    not 4 < cin <= 192:
+            expansion = q.shape[2:] == (1, 1) and (esh, esw, eph, epw, edh, edw, eg) == (1, 1, 0, 0, 1, 1, 1) and \
+                4 < cin <= 192
+            # a 3x3 stem over a 4-byte-per-pixel image (mr_qstem3x3_dw3x3)
+            stem = q.shape[2:] == (3, 3) and esh == esw and esh in (1, 2) and (eph, epw, edh, edw, eg) == \
+                (1, 1, 1, 1, 1) and cin <= 4
+            if not (expansion or stem):
                 continue
             if v.type.dtype != "f32" or op.result.type.dtype != "f32" or v in self.half or op.result in self.half:
                 continue
@@ -1341,8 +1346,8 @@ class RocmExecutable:
 
     def _emit_expand_dw(self, op: "Op", ex: "Op") -> None:
         """The expansion q-op `ex` and the depthwise convolution `op` as one mr_qconv1x1_dw3x3
-        launch: the expansion's epilogue has no outputs (its result is never stored), the
-        depthwise one writes op's copies."""
+        launch (mr_qstem3x3_dw3x3 when `ex` is a 3x3 stem): the expansion's epilogue has no
+        outputs (its result is never stored), the depthwise one writes op's copies."""
         xv = ex.inputs[0]
         x = self._src(xv)
         xs = _f32key(ex.attrs["x_scale"])
@@ -1372,11 +1377,23 @@ class RocmExecutable:
         out = self._new_dv(op.result)
         e, fused = self._epilogue(op, out, True, 2, None)
         lib, kp, npad, cin = self.lib, bl.shape[1], bl.shape[0], xv.type.shape[1]
-        self._add("expand_dw", lambda st: L.check(
-            lib.mr_qconv1x1_dw3x3(xq.data_ptr(), cp, b.data_ptr(), kp, npad, cin, C.byref(ee), C.byref(geom),
-                                  wdev.data_ptr(), C.byref(e), st), "mr_qconv1x1_dw3x3"),
-            nbytes=n * h * w * cp + c * cin + 36 * c + self._epi_bytes(e, n * oh * ow, c),
-            nops=2 * n * h * w * c * cin)
+        if q.shape[2:] == (3, 3):
+            _, _, hi, wi = xv.type.shape
+            (ss, _), _, _, _ = conv_params(ex.attrs)
+            sg = L.ConvGeom(n=n, h=hi, w=wi, c=cin, c_pad=cp, o=c, oh=h, ow=w, kh=3, kw=3, sh=ss, sw=ss, ph=1, pw=1,
+                            dh=1, dw=1)
+            self.keep.append(sg)
+            self._add("expand_dw", lambda st: L.check(
+                lib.mr_qstem3x3_dw3x3(xq.data_ptr(), C.byref(sg), b.data_ptr(), kp, npad, C.byref(ee), C.byref(geom),
+                                      wdev.data_ptr(), C.byref(e), st), "mr_qstem3x3_dw3x3"),
+                nbytes=n * hi * wi * cp + c * cin * 9 + 36 * c + self._epi_bytes(e, n * oh * ow, c),
+                nops=2 * n * h * w * c * cin * 9)
+        else:
+            self._add("expand_dw", lambda st: L.check(
+                lib.mr_qconv1x1_dw3x3(xq.data_ptr(), cp, b.data_ptr(), kp, npad, cin, C.byref(ee), C.byref(geom),
+                                      wdev.data_ptr(), C.byref(e), st), "mr_qconv1x1_dw3x3"),
+                nbytes=n * h * w * cp + c * cin + 36 * c + self._epi_bytes(e, n * oh * ow, c),
+                nops=2 * n * h * w * c * cin)
         self._finish_i8(out, fused)
 
     def _emit_fused_stem(self, op: "Op") -> None:

@@ -865,6 +865,63 @@ def test_qconv1x1_dw3x3_infinite_bias(lib, f32_out):
         assert bits_equal(got, want)
 
 
+@pytest.mark.parametrize("n,cin,c,h,ss,s", [
+    (2, 3, 32, 224, 2, 1),      # MobileNetV2's stem and first depthwise conv (14x14 tiles)
+    (2, 3, 32, 30, 2, 1),       # partial tiles
+    (1, 3, 16, 17, 2, 2),       # odd image, depthwise stride 2
+    (2, 2, 48, 20, 1, 1),       # stride-1 stem, 2 channels, 48 outputs (a half-empty channel block)
+])
+def test_qstem3x3_dw3x3(lib, n, cin, c, h, ss, s):
+    """The 3x3 stem (over an image stored 4 bytes per pixel) fused with the depthwise conv
+    that reads its result: against the oracle's qconv2d and depthwise conv2d, bit for bit."""
+    torch = _torch()
+    rng = np.random.default_rng(n * 7 + c + h)
+    x = rng.uniform(-1, 1, (n, cin, h, h)).astype(np.float32)
+    we = rng.standard_normal((c, cin, 3, 3)).astype(np.float32)
+    q, ws = G.quantize_array(we, 0)
+    xs = float(np.abs(x).max()) / 127
+    be = (rng.standard_normal((c, 1, 1)) * 0.5).astype(np.float32)
+    wd = (rng.standard_normal((c, 1, 3, 3)) * 0.5).astype(np.float32)
+    bd = (rng.standard_normal((c, 1, 1)) * 0.5).astype(np.float32)
+    zero, six = np.array(0, np.float32), np.array(6, np.float32)
+    r6 = (("add", 1, False), ("maximum", 2, False), ("minimum", 3, False))
+    ea = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "stride": (ss, ss), "padding": (1, 1),
+          "epilogue": r6}
+    want_e = G.qconv2d([x, be, zero, six], ea)
+    sh = want_e.shape[2]
+    want = G.conv2d([want_e, wd, bd, zero, six], {"stride": (s, s), "padding": (1, 1), "groups": c,
+                                                   "epilogue": (("add", 2, False), ("maximum", 3, False),
+                                                                ("minimum", 4, False))})
+    oh = want.shape[2]
+    next_xs = float(np.abs(want).max()) / 127 or 1.0
+    want_q = G.quantize_activation(want, next_xs).astype(np.int8).transpose(0, 2, 3, 1).reshape(-1, c)
+    xq = empty((n, h, h, 4), torch.int8)
+    L.check(lib.mr_quantize_nchw_nhwc(T(x).data_ptr(), n, cin, h, h, xq.data_ptr(), 4, xs, stream()), "q")
+    bl = pack.pack_conv(q, 4)
+    assert bl.shape[1] == 64
+    b = T(pack.device_weights(bl))
+    keep = [T(be.reshape(c)), T(zero.reshape(1)), T(six.reshape(1)), T(bd.reshape(c)),
+            T(pack.combined_scale(xs, ws)), T(np.ascontiguousarray(wd[:, 0].transpose(1, 2, 0)))]
+    bet, zt, st, bdt, scale, wdt = keep
+    ee = epilogue([("add", L.BC_COL, bet, 0, False), ("maximum", L.BC_SCALAR, zt, 0, False),
+                   ("minimum", L.BC_SCALAR, st, 0, False)], scale=scale)
+    M = n * oh * oh
+    ldq = pack.c_pad_for(c)
+    yq = torch.full((M, ldq), 99, dtype=torch.int8, device="cuda")
+    ed = epilogue([("add", L.BC_COL, bdt, 0, False), ("maximum", L.BC_SCALAR, zt, 0, False),
+                   ("minimum", L.BC_SCALAR, st, 0, False)], out_i8=yq, ldq=ldq, xs=next_xs)
+    sg = L.ConvGeom(n=n, h=h, w=h, c=cin, c_pad=4, o=c, oh=sh, ow=sh, kh=3, kw=3, sh=ss, sw=ss, ph=1, pw=1, dh=1,
+                    dw=1)
+    g = L.ConvGeom(n=n, h=sh, w=sh, c=c, c_pad=c, o=c, oh=oh, ow=oh, kh=3, kw=3, sh=s, sw=s, ph=1, pw=1, dh=1, dw=1)
+    rc = lib.mr_qstem3x3_dw3x3(xq.data_ptr(), C.byref(sg), b.data_ptr(), bl.shape[1], bl.shape[0], C.byref(ee),
+                               C.byref(g), wdt.data_ptr(), C.byref(ed), stream())
+    sync()
+    assert rc == 0, lib.mr_last_error()
+    got = yq.cpu().numpy()
+    assert (got[:, c:] == 99).all()
+    assert bits_equal(got[:, :c], want_q)
+
+
 def test_qconv1x1_dw3x3_rejects(lib):
     """Forms it has no kernel for return MR_EUNSUPPORTED (the target makes two launches);
     an expansion epilogue that stores its result is an argument error."""
