@@ -1,7 +1,7 @@
 """Benchmark: W8A8 ResNet-18 inference on one MI355X through the rocm target.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 256] [--no-cpu-baseline]
-    python bench.py --workload mlp50m|mlp50m-int8|mobilenetv2 [--batch B] [--steps K] [--warmup W]
+    python bench.py --workload mlp50m|mlp50m-int8|mobilenetv2|mobilenetv2-f16 [--batch B] [--steps K] [--warmup W]
     python bench.py --per-launch [--workload W] [--batch B]
 
 A step is one inference of the whole batch (all 20 int8 implicit-GEMM convs,
@@ -22,14 +22,14 @@ kernels    = every launch kind of the step: its summed launch durations and its
 --workload mlp50m / mobilenetv2 time the other W8A8 networks the same way and
 print one JSON line with their per-kind breakdown (no cpu baseline): the 50M
 MLP at batch 1 runs its four layers on the decode-shaped weight-streaming
-qmatmul kernel, MobileNetV2 its 17 depthwise convolutions on the f32
-depthwise kernel; both are HBM-bound.  mlp50m-int8 is the same MLP in the
+qmatmul kernel, MobileNetV2 its 17 depthwise convolutions fused with the
+convolutions before them (the expanded tensors never stored).  mlp50m-int8 is the same MLP in the
 int8 weight-only mode (f32 activations, int8 weights dequantized in
 registers), batch 1: four weight-streaming f32 matmul launches.
 resnet18-onnx is ResNet-18 laid out as MIRA's ONNX importer emits it (BN as a
 per-channel mul + add in each conv epilogue instead of folded weights);
-resnet18-f16 is the f16 graph (MIRA's default precision for accelerator
-targets), every result rounded to f16 and stored as f32.
+resnet18-f16 and mobilenetv2-f16 are the f16 graphs (MIRA's default precision
+for accelerator targets), every result rounded to f16.
 gpt-decode times greedy decoding with the character-level GPT (default batch 1;
 16-token prompt, --tokens generated): the whole loop resident on the GPU, one
 HIP graph replay per step, in microseconds per token, beside the eager launch
@@ -84,7 +84,7 @@ def build_workload(name: str, batch: int):
         return g, models.normal_batch(g.inputs[0].type.shape, 7)
     if name == "mlp50m":
         builder, cb, seeds, gen = models.mlp_50m, 8, (2, 3), models.normal_batch
-    elif name == "mobilenetv2":
+    elif name in ("mobilenetv2", "mobilenetv2-f16"):
         builder, cb, seeds, gen = models.mobilenet_v2, 2, (11, 12), models.image_batch
     elif name == "resnet18-onnx":
         def builder(batch, seed):
@@ -584,6 +584,7 @@ def main() -> int:
                     help="default 256 (resnet18), 1 (mlp50m, mlp50m-int8), 128 (mobilenetv2)")
     ap.add_argument("--workload", default="resnet18",
                     choices=["resnet18", "resnet18-onnx", "resnet18-f16", "mlp50m", "mlp50m-int8", "mobilenetv2",
+                             "mobilenetv2-f16",
                              "gpt-decode"])
     ap.add_argument("--tokens", type=int, default=256, help="gpt-decode: tokens generated per sequence")
     ap.add_argument("--per-launch", action="store_true", help="per-launch time against each launch's roofline")
@@ -608,7 +609,7 @@ def main() -> int:
         return 2
     if args.batch is None:
         args.batch = {"resnet18": 256, "resnet18-onnx": 256, "resnet18-f16": 256, "mlp50m": 1, "mlp50m-int8": 1,
-                      "mobilenetv2": 128, "gpt-decode": 1}[args.workload]
+                      "mobilenetv2": 128, "mobilenetv2-f16": 128, "gpt-decode": 1}[args.workload]
     if args.workload == "gpt-decode":
         return bench_gpt(args)
     if args.per_launch:

@@ -45,6 +45,9 @@ struct ExpandDwArgs {
 // 4-byte-per-pixel image (3 channels and a zero), its weights in the stem layout
 // (kernel row ki in the 16-byte chunk ki: three 4-byte taps and a zero word), so
 // the A row of a region pixel is its nine input pixels gathered into those chunks.
+// F16: an f16 graph's pair: each expanded value and each depthwise result rounded to f16
+// after its epilogue, as the two launches round them (the taps stay exact f32 products of
+// f16 values, summed in f32).
 // blockIdx.y: the 32-channel block, whose weights and column constants a
 // workgroup loads once; it then walks tiles blockIdx.x, + gridDim.x, ..., loading
 // the next tile's region into registers while it computes the current one.  The
@@ -59,7 +62,7 @@ constexpr int ed_occupancy() {
   return 163840 / bytes >= 4 ? 4 : 163840 / bytes;
 }
 
-template <int S, int T, int KP, bool DF32, bool STEM>
+template <int S, int T, int KP, bool DF32, bool STEM, bool F16>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ed_occupancy<S, T, KP>())))
 expand_dw_kernel(const ExpandDwArgs a, const EpiDev ex, const EpiDev dw) {
   constexpr int IR = (T - 1) * S + 3;   // input region edge
@@ -152,7 +155,8 @@ expand_dw_kernel(const ExpandDwArgs a, const EpiDev ex, const EpiDev dw) {
     float y = dequant(v, escale);
     y = __fadd_rn(y, ebias);
     y = max_bound(y, ex_lo, ex_lo_nan);
-    return min_bound(y, ex_hi, ex_hi_nan);
+    y = min_bound(y, ex_hi, ex_hi_nan);
+    return F16 ? round_f16(y) : y;
   };
   // With a finite bias and bounds lo <= hi the expanded value is never NaN, and the two
   // bounds are one median (v_med3_f32): equal to them up to the sign of a zero result, which
@@ -160,7 +164,8 @@ expand_dw_kernel(const ExpandDwArgs a, const EpiDev ex, const EpiDev dw) {
   // nearest).  Taken when every lane of the wave qualifies.
   const bool ex_med3 = __all(isfinite(ebias) && !ex_lo_nan && !ex_hi_nan && ex_lo <= ex_hi);
   auto expand_med3 = [&](int32_t v) __attribute__((always_inline)) {
-    return __builtin_amdgcn_fmed3f(__fadd_rn(dequant(v, escale), ebias), ex_lo, ex_hi);
+    const float y = __builtin_amdgcn_fmed3f(__fadd_rn(dequant(v, escale), ebias), ex_lo, ex_hi);
+    return F16 ? round_f16(y) : y;
   };
 
   for (; id < a.total; id += gridDim.x) {
@@ -271,6 +276,7 @@ expand_dw_kernel(const ExpandDwArgs a, const EpiDev ex, const EpiDev dw) {
               y[c] = __builtin_amdgcn_fmed3f(v, dw_lo, dw_hi);
             else
               y[c] = min_bound(max_bound(v, dw_lo, dw_lo_nan), dw_hi, dw_hi_nan);
+            if constexpr (F16) y[c] = round_f16(y[c]);
           }
           const int64_t pix = (int64_t(img) * a.OH + oh) * a.OW + ow;
           if constexpr (DF32)
@@ -292,10 +298,17 @@ expand_dw_kernel(const ExpandDwArgs a, const EpiDev ex, const EpiDev dw) {
 template <int S, int T, int KP, bool STEM = false>
 static void expand_dw_launch(const ExpandDwArgs& a, const EpiDev& ex, const EpiDev& dw, dim3 grid,
                              hipStream_t stream) {
-  if (dw.out_f32)
-    hipLaunchKernelGGL((expand_dw_kernel<S, T, KP, true, STEM>), grid, dim3(256), 0, stream, a, ex, dw);
-  else
-    hipLaunchKernelGGL((expand_dw_kernel<S, T, KP, false, STEM>), grid, dim3(256), 0, stream, a, ex, dw);
+  if (dw.f16) {
+    if (dw.out_f32)
+      hipLaunchKernelGGL((expand_dw_kernel<S, T, KP, true, STEM, true>), grid, dim3(256), 0, stream, a, ex, dw);
+    else
+      hipLaunchKernelGGL((expand_dw_kernel<S, T, KP, false, STEM, true>), grid, dim3(256), 0, stream, a, ex, dw);
+  } else {
+    if (dw.out_f32)
+      hipLaunchKernelGGL((expand_dw_kernel<S, T, KP, true, STEM, false>), grid, dim3(256), 0, stream, a, ex, dw);
+    else
+      hipLaunchKernelGGL((expand_dw_kernel<S, T, KP, false, STEM, false>), grid, dim3(256), 0, stream, a, ex, dw);
+  }
 }
 
 template <int S, int T>
@@ -309,9 +322,9 @@ static int expand_dw_kp(int64_t k_pad, const ExpandDwArgs& a, const EpiDev& ex, 
 
 static bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
-// bias (per column) -> maximum -> minimum, nothing else, no f16 rounding
+// bias (per column) -> maximum -> minimum, nothing else
 static bool relu6_form(const EpiDev& e) {
-  return e.fixed && !e.f_mul && e.f_col && !e.f_full && e.f_lo && e.f_hi && !e.f16 && !e.out_acc;
+  return e.fixed && !e.f_mul && e.f_col && !e.f_full && e.f_lo && e.f_hi && !e.out_acc;
 }
 
 // Checks and launch shared by both entry points: the depthwise geometry, both epilogues,
@@ -340,9 +353,9 @@ static int expand_dw_run(const char* fn, const int8_t* x, int64_t ldx, const int
   if (rc != MR_OK) return rc;
   rc = make_epi(epi_dw, G.c, false, &dw);
   if (rc != MR_OK) return rc;
-  if (k_pad > 192 || !relu6_form(ex) || !relu6_form(dw)) {
-    set_error("%s: compiled for k_pad <= 192 and bias -> maximum -> minimum epilogues on both convolutions "
-              "without f16 rounding", fn);
+  if (k_pad > 192 || !relu6_form(ex) || !relu6_form(dw) || ex.f16 != dw.f16) {
+    set_error("%s: compiled for k_pad <= 192 and bias -> maximum -> minimum epilogues on both convolutions, "
+              "both with or both without f16 rounding", fn);
     return MR_EUNSUPPORTED;
   }
   MR_REQUIRE(dw.ldq % 4 == 0 && reinterpret_cast<uintptr_t>(dw.out_i8) % 4 == 0 &&

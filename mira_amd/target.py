@@ -691,7 +691,8 @@ class RocmExecutable:
         MobileNet block's expansion) runs inside that convolution's launch
         (mr_qconv1x1_dw3x3), and so does a 3x3 stem over an image of at most 4 channels
         (mr_qstem3x3_dw3x3): the expanded tensor is never stored.  Both epilogues bias ->
-        ReLU6, f32 graphs, the depthwise result read as int8."""
+        ReLU6, f32 or f16 graphs (values not stored as halves), the depthwise result read as
+        int8."""
         self.expand_dw: dict = {}           # depthwise op -> its expansion q-op
         if self.target.debug_acc:
             return
@@ -720,7 +721,8 @@ class RocmExecutable:
                 (1, 1, 1, 1, 1) and cin <= 4
             if not (expansion or stem):
                 continue
-            if v.type.dtype != "f32" or op.result.type.dtype != "f32" or v in self.half or op.result in self.half:
+            if v.type.dtype != op.result.type.dtype or v.type.dtype not in FLOAT_DTYPES or v in self.half or \
+                    op.result in self.half:
                 continue
             if not self.need_i8.get(op.result) or not self._relu6_epilogue(e) or not self._relu6_epilogue(op):
                 continue
@@ -1359,6 +1361,7 @@ class RocmExecutable:
         ee = L.Epilogue()
         steps = ex.attrs["epilogue"]
         ee.n_steps = len(steps)
+        ee.flags = L.EPI_OUT_F16 if ex.result.type.dtype == "f16" else 0
         for i, (fn, idx, _sw) in enumerate(steps):
             ee.steps[i].fn = L.EPI_FN[fn]
             if idx is not None:

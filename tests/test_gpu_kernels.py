@@ -780,7 +780,7 @@ def test_dwconv_relu6(lib, n, c, h, s, k, form, ldo_pad):
 
 # ---------------------------------------------------------------- fused 1x1 expansion + 3x3 depthwise
 
-def _expand_dw_case(lib, n, k, c, h, s, f32_out, seed, inf_bias=False):
+def _expand_dw_case(lib, n, k, c, h, s, f32_out, seed, inf_bias=False, f16=False):
     """A MobileNet block's expansion (1x1 qconv2d, bias, ReLU6 -> f32) and depthwise
     conv (3x3, bias, ReLU6 -> int8 and optionally f32) as one mr_qconv1x1_dw3x3 launch.
     Returns (rc, got int8, got f32 or None, want int8, want f32)."""
@@ -798,12 +798,17 @@ def _expand_dw_case(lib, n, k, c, h, s, f32_out, seed, inf_bias=False):
     if inf_bias:    # and depthwise outputs that saturate
         bd[6], bd[9] = np.inf, -np.inf
     zero, six = np.array(0, np.float32), np.array(6, np.float32)
+    if f16:     # an f16 graph: f16 constants, both results rounded to f16
+        be, wd, bd, zero, six = (a.astype(np.float16) for a in (be, wd, bd, zero, six))
     r6 = (("add", 1, False), ("maximum", 2, False), ("minimum", 3, False))
-    ea = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "stride": (1, 1), "padding": (0, 0), "epilogue": r6}
+    ea = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f16" if f16 else "f32", "stride": (1, 1),
+          "padding": (0, 0), "epilogue": r6}
     want_e = G.qconv2d([x, be, zero, six], ea)
     da = {"stride": (s, s), "padding": (1, 1), "groups": c,
           "epilogue": (("add", 2, False), ("maximum", 3, False), ("minimum", 4, False))}
     want = G.conv2d([want_e, wd, bd, zero, six], da)
+    assert want.dtype == (np.float16 if f16 else np.float32)
+    be, wd, bd, zero, six = (np.asarray(a, np.float32) for a in (be, wd, bd, zero, six))
     oh = want.shape[2]
     next_xs = float(np.abs(want).max()) / 127 or 1.0
     want_q = G.quantize_activation(want, next_xs).astype(np.int8).transpose(0, 2, 3, 1).reshape(-1, c)
@@ -823,6 +828,8 @@ def _expand_dw_case(lib, n, k, c, h, s, f32_out, seed, inf_bias=False):
     y = torch.full((M, c), float("nan"), dtype=torch.float32, device="cuda") if f32_out else None
     ed = epilogue([("add", L.BC_COL, bdt, 0, False), ("maximum", L.BC_SCALAR, zt, 0, False),
                    ("minimum", L.BC_SCALAR, st, 0, False)], out_f32=y, ldo=c, out_i8=yq, ldq=ldq, xs=next_xs)
+    if f16:
+        ee.flags = ed.flags = L.EPI_OUT_F16
     g = L.ConvGeom(n=n, h=h, w=h, c=c, c_pad=c, o=c, oh=oh, ow=oh, kh=3, kw=3, sh=s, sw=s, ph=1, pw=1, dh=1, dw=1)
     rc = lib.mr_qconv1x1_dw3x3(xq.data_ptr(), cp, b.data_ptr(), bl.shape[1], bl.shape[0], k, C.byref(ee), C.byref(g),
                                wdt.data_ptr(), C.byref(ed), stream())
@@ -830,7 +837,7 @@ def _expand_dw_case(lib, n, k, c, h, s, f32_out, seed, inf_bias=False):
     got_q = yq.cpu().numpy()
     assert (got_q[:, c:] == 99).all()          # nothing written past the c channels
     got = y.cpu().numpy() if f32_out else None
-    return rc, got_q[:, :c], got, want_q, want.transpose(0, 2, 3, 1).reshape(-1, c)
+    return rc, got_q[:, :c], got, want_q, want.astype(np.float32).transpose(0, 2, 3, 1).reshape(-1, c)
 
 
 @pytest.mark.parametrize("n,k,c,h,s,f32_out", [
@@ -847,6 +854,18 @@ def _expand_dw_case(lib, n, k, c, h, s, f32_out, seed, inf_bias=False):
 ])
 def test_qconv1x1_dw3x3(lib, n, k, c, h, s, f32_out):
     rc, got_q, got, want_q, want = _expand_dw_case(lib, n, k, c, h, s, f32_out, n * 100 + k + c + h)
+    assert rc == 0, lib.mr_last_error()
+    assert bits_equal(got_q, want_q)
+    if f32_out:
+        assert bits_equal(got, want)
+
+
+@pytest.mark.parametrize("n,k,c,h,s,f32_out", [(2, 16, 96, 56, 2, False), (2, 24, 144, 28, 1, True),
+                                                (1, 160, 960, 7, 1, False)])
+def test_qconv1x1_dw3x3_f16(lib, n, k, c, h, s, f32_out):
+    """The f16 graph's pair: f16 constants, the expanded values and the depthwise results
+    rounded to f16 after their epilogues (the f32 result holds those f16 values)."""
+    rc, got_q, got, want_q, want = _expand_dw_case(lib, n, k, c, h, s, f32_out, n + k + c, f16=True)
     assert rc == 0, lib.mr_last_error()
     assert bits_equal(got_q, want_q)
     if f32_out:
@@ -944,7 +963,7 @@ def test_qconv1x1_dw3x3_rejects(lib):
     assert call(epilogue(r6[:2], scale=sc)) == 3                          # ReLU without the upper bound
     f16 = epilogue(r6, scale=sc)
     f16.flags = L.EPI_OUT_F16
-    assert call(f16) == 3                                                 # f16 rounding
+    assert call(f16) == 3                                       # f16 rounding on one convolution only
     assert call(epilogue(r6, scale=sc, out_i8=yq, ldq=64, xs=0.1)) == 1    # the expansion stores its result
     assert call(epilogue(r6, scale=sc), dw=epilogue(r6, out_f32=empty((64, 64), torch.float32), ldo=64)) == 1
     sync()

@@ -207,6 +207,19 @@ def test_mobilenet_v2_batch2_fused_expansions():
     assert bits_equal(got, want)
 
 
+def test_mobilenet_v2_f16_batch2_fused_expansions():
+    """MIRA's default precision on rocm (the f16 graph), production path: the same 17 fused
+    launches with their f16 rounding, bit-exact against the oracle's f16 graph."""
+    g, _ = _quantized(models.mobilenet_v2, 2, precision="f16")
+    runner = Runner(g, RocmTarget())
+    exe = runner.executables("rocm")[0]
+    assert exe.kernel_counts.get("expand_dw") == 17 and "dwconv2d" not in exe.kernel_counts, exe.kernel_counts
+    x = models.image_batch((2, 3, 224, 224), 5)
+    (got,) = runner.run({"x": x})
+    (want,) = G.run_graph(g, {"x": x})
+    assert bits_equal(got, want)
+
+
 def test_mobilenet_v2_batch128_rows():
     _rows_match_small_run(models.mobilenet_v2, 128, [0, 7, 10, 23, 53, 64, 100, 127], "uniform", runs=2)
 
