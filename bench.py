@@ -458,6 +458,32 @@ def copy_calibration() -> int:
     return 0
 
 
+def blas_reference() -> int:
+    """The vendor int8 GEMM (torch._int_mm, hipBLASLt) on the GEMM shapes of ResNet-18's 3x3
+    convolutions at batch 256 (M = output pixels, K = 9 x input channels, N = output channels),
+    already in im2col form, and on 8192^3: the reference the implicit-GEMM conv kernels are
+    compared with.  HIP events around 20 calls after 3 warm-up calls."""
+    import torch
+    torch.manual_seed(0)
+    shapes = [("layer1 3x3", 802816, 576, 64), ("layer2 3x3", 200704, 1152, 128),
+              ("layer3 3x3", 50176, 2304, 256), ("layer4 3x3", 12544, 4608, 512), ("8192^3", 8192, 8192, 8192)]
+    for name, M, K, N in shapes:
+        a = torch.randint(-127, 127, (M, K), dtype=torch.int8, device="cuda")
+        b = torch.randint(-127, 127, (N, K), dtype=torch.int8, device="cuda").t()
+        for _ in range(3):
+            torch._int_mm(a, b)
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record()
+        for _ in range(20):
+            torch._int_mm(a, b)
+        en.record()
+        torch.cuda.synchronize()
+        us = st.elapsed_time(en) * 1000 / 20
+        log(f"{name:12s} M={M} K={K} N={N}: {us:8.1f} us {2 * M * N * K / us / 1e6:8.1f} TOP/s")
+        del a, b
+    return 0
+
+
 def summarize_counters(d: str) -> int:
     """Summarize rocprofv3 --pmc CSV output of bench.py and of --copy-calibration.
 
@@ -590,6 +616,8 @@ def main() -> int:
     ap.add_argument("--per-launch", action="store_true", help="per-launch time against each launch's roofline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true", help="run the plain copy used to scale counters")
+    ap.add_argument("--blas-reference", action="store_true",
+                    help="time hipBLASLt's int8 GEMM (torch._int_mm) on ResNet-18's conv GEMM shapes")
     ap.add_argument("--summarize-counters", metavar="DIR", help="summarize rocprofv3 --pmc CSV output in DIR")
     ap.add_argument("--summarize-mfma", metavar="DIR", help="MFMA utilisation from rocprofv3 --pmc CSV output in DIR/mfma")
     ap.add_argument("--summarize-sq", metavar="DIR", help="issue/wait/LDS counters from rocprofv3 --pmc output in "
@@ -601,6 +629,8 @@ def main() -> int:
         return summarize_mfma(args.summarize_mfma)
     if args.summarize_sq:
         return summarize_sq(args.summarize_sq)
+    if args.blas_reference:
+        return blas_reference()
     if args.copy_calibration:
         return copy_calibration()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
