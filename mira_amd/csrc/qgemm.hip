@@ -847,7 +847,12 @@ static int launch(const GemmArgs& g, const EpiDev& e, hipStream_t stream) {
     // one 64-byte step (MobileNetV2 B=128: 3-channel stem 100 -> 90 us with 3
     // stages instead of 4, 32 -> 16 projection 53 -> 45 us)
     const int64_t tiles = (g.M + 63) / 64 * ((g.N + 31) / 32);
-    if (g.k_tiles == 1) {
+    if (g.k_tiles == 1 && AMODE == A_DENSE && tiles >= 32 * cus) {
+      // a very large grid of one-step tiles (MobileNetV2's 112x112 32 -> 16 projection at
+      // batch 128: 25 088 tiles of 64x32): 128-row tiles (two waves of 64x32) halve the
+      // workgroups and their fixed costs
+      launch_cfg<128, 32, 2, 1, 1, AMODE>(g, e, stream);
+    } else if (g.k_tiles == 1) {
       launch_cfg<64, 32, 2, 1, 1, AMODE>(g, e, stream);
     } else if (g.k_tiles >= 8 && tiles <= 2 * cus) {
       // a long K on a grid of at most two tiles per CU is a chain of ring stages per

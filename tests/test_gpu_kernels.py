@@ -107,7 +107,8 @@ def _run_qmatmul(lib, x, q, ws, xs, steps_np, next_xs=None):
                                    (3, 4096, 1000), (8, 512, 65), (2, 64, 64), (5, 192, 130),   # weight stream
                                    (2, 5000, 96), (1, 8192, 40),    # k_pad > 4096: lane groups per column pair
                                    (2, 1024, 3000),                 # weight stream, 8 columns per workgroup
-                                   (96, 1024, 256), (40, 4000, 70)])  # small grids: 64x32 tiles, 128-byte stages
+                                   (96, 1024, 256), (40, 4000, 70),   # small grids: 64x32 tiles, 128-byte stages
+                                   (600000, 48, 24)])                 # one K step on a huge grid: 128x32 tiles
 def test_qmatmul_bias_relu_requant(lib, M, K, N):
     rng = np.random.default_rng(M * 7 + N)
     x = rng.standard_normal((M, K)).astype(np.float32)
@@ -607,6 +608,7 @@ FORM_CONV_CASES = [
     (2, 16, 128, 128, 96, 1, 1, 0, 1),    # 1x1 expansion 16 -> 96, large grid: 128x128 tiles, no ring
     (1, 512, 7, 7, 512, 3, 1, 1, 1),      # batch-1 layer 4: a 16-tile grid, 64x32 tiles with 128-byte stages
     (1, 192, 9, 9, 96, 3, 2, 1, 1),       # small grid, c_pad 192: 64x32 tiles with 64-byte stages
+    (42, 32, 112, 112, 16, 1, 1, 0, 1),   # 1x1 projection, one K step on over 32 64-row tiles per CU: 128x32
 ]
 
 
