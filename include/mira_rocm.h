@@ -182,6 +182,16 @@ int mr_qmatmul_f32in(const float* x, int64_t ldx, float x_scale, const int8_t* b
                      int64_t k_pad, int64_t n_pad, int64_t M, int64_t N, int64_t K,
                      const mr_epilogue* epi, void* stream);
 
+/* The same when the f32 rows are a layernorm's input and the q-op reads only its
+ * int8 copy (a transformer decode step's projections after a layernorm): each row
+ * of K elements is normalised as mr_layernorm_f32 does (mira/ops.py:356-360: gain
+ * gamma[K], bias beta[K], eps; rounded to f16 when round_f16), quantized with
+ * x_scale, then multiplied; bit-exact with mr_layernorm_f32 (int8 output) followed
+ * by mr_qmatmul.  M <= 8 and k_pad <= 1024 (MR_EUNSUPPORTED otherwise). */
+int mr_qmatmul_lnin(const float* x, int64_t ldx, const float* gamma, const float* beta, float eps,
+                    int32_t round_f16, float x_scale, const int8_t* b, int64_t k_pad, int64_t n_pad,
+                    int64_t M, int64_t N, int64_t K, const mr_epilogue* epi, void* stream);
+
 /* Replaces, for decode-shaped matmuls of the int8 weight-only mode
  * (mira/quantize.py:45-68), mira/ops.py:217-219 _matmul_ref fed by the
  * dequantize constant of mira/ops.py:581-589:

@@ -27,7 +27,7 @@ BC_SCALAR, BC_COL, BC_ROW, BC_FULL = 0, 1, 2, 3
 EXPORTS = [
     "mr_abi_version", "mr_last_error", "mr_sizeof", "mr_init",
     "mr_quantize_rows", "mr_quantize_nchw_nhwc", "mr_quantize_f16_nchw_nhwc",
-    "mr_qmatmul", "mr_qmatmul_f32in", "mr_w8_matmul_f32", "mr_w8_conv2d_f32", "mr_qconv2d", "mr_qconv2d_maxpool",
+    "mr_qmatmul", "mr_qmatmul_f32in", "mr_qmatmul_lnin", "mr_w8_matmul_f32", "mr_w8_conv2d_f32", "mr_qconv2d", "mr_qconv2d_maxpool",
     "mr_qconv2d_maxpool_f32in", "mr_dwconv2d_f32", "mr_qconv1x1_dw3x3", "mr_qstem3x3_dw3x3",
     "mr_maxpool2d_f32", "mr_mean_hw_f32", "mr_pad_hw_f32", "mr_round_f16_f32",
     "mr_nchw_to_nhwc_f32", "mr_nchw_to_nhwc_pad_f32", "mr_nhwc_to_nchw_f32",
@@ -71,6 +71,8 @@ _SIGS = {
     "mr_quantize_f16_nchw_nhwc": ([_p, _i32, _i32, _i32, _i32, _p, _i32, _f32, _p], C.c_int),
     "mr_qmatmul": ([_p, _i64, _p, _i64, _i64, _i64, _i64, _i64, C.POINTER(Epilogue), _p], C.c_int),
     "mr_qmatmul_f32in": ([_p, _i64, _f32, _p, _i64, _i64, _i64, _i64, _i64, C.POINTER(Epilogue), _p], C.c_int),
+    "mr_qmatmul_lnin": ([_p, _i64, _p, _p, _f32, _i32, _f32, _p, _i64, _i64, _i64, _i64, _i64, C.POINTER(Epilogue),
+                         _p], C.c_int),
     "mr_w8_matmul_f32": ([_p, _i64, _p, _p, _i32, _i64, _i64, _i64, _i64, _i64, C.POINTER(Epilogue), _p], C.c_int),
     "mr_qconv2d": ([_p, C.POINTER(ConvGeom), _p, _i64, _i64, C.POINTER(Epilogue), _p], C.c_int),
     "mr_w8_conv2d_f32": ([_p, C.POINTER(ConvGeom), _p, _p, _i32, _i64, _i64, C.POINTER(Epilogue), _p], C.c_int),

@@ -15,28 +15,6 @@ namespace mr {
 
 // ---------------------------------------------------------------- layernorm
 
-// Correctly rounded f32 square root (NumPy's np.sqrt), whatever the compiler lowers sqrtf to
-// (clang's __fsqrt_rn is the hardware approximation, within 1 ulp).  Rounding to nearest
-// picks s when the true root lies between the midpoints m- and m+ to s's neighbours; a
-// midpoint has at most 25 significant bits, so m*m is exact in double and the comparison
-// with v is exact (never equal: m*m has more bits than a float).  A faithful first guess
-// is off by at most one ulp, so one correction suffices.
-__device__ inline float sqrt_rn(float v) {
-  float s = sqrtf(v);
-  if (!(v > 0.0f) || !(v < __builtin_inff())) return s;     // +-0, negative, NaN, inf: exact cases
-  const float dn = nextafterf(s, 0.0f), up = nextafterf(s, __builtin_inff());
-  const double x = static_cast<double>(v);
-  const double lo = 0.5 * (static_cast<double>(s) + static_cast<double>(dn));
-  const double hi = 0.5 * (static_cast<double>(s) + static_cast<double>(up));
-  if (__dmul_rn(lo, lo) > x) return dn;
-  if (__dmul_rn(hi, hi) < x) return up;
-  return s;
-}
-
-__device__ inline float mean_of_sum(float s, int d) {
-  return static_cast<float>(__ddiv_rn(static_cast<double>(__fadd_rn(0.0f, s)), static_cast<double>(d)));
-}
-
 // mira/ops.py:356-360 on [rows, d]: mu = mean(x), var = mean((x - mu)^2),
 // y = (x - mu) / sqrt(var + eps) * g + b, rounded to f16 when out_f16, and the
 // optional int8 copy clip(rint(y / xs), +-127) of the next q-op's input.
@@ -53,30 +31,10 @@ __global__ void __launch_bounds__(64) layernorm_kernel(const float* __restrict__
   const int64_t r = blockIdx.x;
   const int lane = threadIdx.x;
   const float* xr = x + r * d;
-  auto elem = [=](int64_t i) { return xr[i]; };
-  float mu;
-  if (d <= 128) {
-    mu = mean_of_sum(wave_pairwise_block(elem, d, lane), d);
-  } else {
-    float s = 0.0f;
-    if (lane == 0) s = pairwise_sum_of(elem, d);
-    mu = mean_of_sum(__shfl(s, 0), d);
-  }
-  auto sq = [=](int64_t i) {
-    const float t = __fsub_rn(xr[i], mu);
-    return __fmul_rn(t, t);
-  };
-  float var;
-  if (d <= 128) {
-    var = mean_of_sum(wave_pairwise_block(sq, d, lane), d);
-  } else {
-    float s = 0.0f;
-    if (lane == 0) s = pairwise_sum_of(sq, d);
-    var = mean_of_sum(__shfl(s, 0), d);
-  }
-  const float sd = sqrt_rn(__fadd_rn(var, eps));
+  float mu, sd;
+  layernorm_row_stats([=](int64_t i) { return xr[i]; }, d, lane, eps, mu, sd);
   for (int i = lane; i < d; i += 64) {
-    float v = __fadd_rn(__fmul_rn(__fdiv_rn(__fsub_rn(xr[i], mu), sd), g[i]), b[i]);
+    float v = layernorm_value(xr[i], mu, sd, g[i], b[i]);
     if (out_f16) v = round_f16(v);
     if (y) y[r * d + i] = v;
     if (yq) yq[r * ldq + i] = quantize_one(v, xs);

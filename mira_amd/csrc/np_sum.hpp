@@ -116,4 +116,64 @@ __device__ inline float wave_pairwise_block(Elem elem, int n, int lane) {
   return __shfl(res, 0);
 }
 
+// ---------------------------------------------------------------- layer normalisation of one row
+
+// Correctly rounded f32 square root (NumPy's np.sqrt), whatever the compiler lowers sqrtf to
+// (clang's __fsqrt_rn is the hardware approximation, within 1 ulp).  Rounding to nearest
+// picks s when the true root lies between the midpoints m- and m+ to s's neighbours; a
+// midpoint has at most 25 significant bits, so m*m is exact in double and the comparison
+// with v is exact (never equal: m*m has more bits than a float).  A faithful first guess
+// is off by at most one ulp, so one correction suffices.
+__device__ inline float sqrt_rn(float v) {
+  float s = sqrtf(v);
+  if (!(v > 0.0f) || !(v < __builtin_inff())) return s;     // +-0, negative, NaN, inf: exact cases
+  const float dn = nextafterf(s, 0.0f), up = nextafterf(s, __builtin_inff());
+  const double x = static_cast<double>(v);
+  const double lo = 0.5 * (static_cast<double>(s) + static_cast<double>(dn));
+  const double hi = 0.5 * (static_cast<double>(s) + static_cast<double>(up));
+  if (__dmul_rn(lo, lo) > x) return dn;
+  if (__dmul_rn(hi, hi) < x) return up;
+  return s;
+}
+
+__device__ inline float mean_of_sum(float s, int d) {
+  return static_cast<float>(__ddiv_rn(static_cast<double>(__fadd_rn(0.0f, s)), static_cast<double>(d)));
+}
+
+// mira/ops.py:356-360 for one row of d elements (read through elem) by one 64-lane wave:
+// mu = mean(x), sd = sqrt(mean((x - mu)^2) + eps).  NumPy's mean is an add-reduce seeded
+// with +0 over the pairwise f32 sum, then the division of that f32 sum by the count in
+// double precision, rounded back to f32; eps is added in f32; the square root is IEEE.
+// Rows of at most 128 elements split the pairwise accumulators over the lanes, longer rows
+// run the pairwise recursion on lane 0.  Every lane ends with mu and sd.
+template <class Elem>
+__device__ inline void layernorm_row_stats(Elem elem, int d, int lane, float eps, float& mu, float& sd) {
+  if (d <= 128) {
+    mu = mean_of_sum(wave_pairwise_block(elem, d, lane), d);
+  } else {
+    float s = 0.0f;
+    if (lane == 0) s = pairwise_sum_of(elem, d);
+    mu = mean_of_sum(__shfl(s, 0), d);
+  }
+  const float m = mu;
+  auto sq = [=](int64_t i) {
+    const float t = __fsub_rn(elem(i), m);
+    return __fmul_rn(t, t);
+  };
+  float var;
+  if (d <= 128) {
+    var = mean_of_sum(wave_pairwise_block(sq, d, lane), d);
+  } else {
+    float s = 0.0f;
+    if (lane == 0) s = pairwise_sum_of(sq, d);
+    var = mean_of_sum(__shfl(s, 0), d);
+  }
+  sd = sqrt_rn(__fadd_rn(var, eps));
+}
+
+// (x - mu) / sd * g + b, each operation rounded once (before any f16 rounding of the result)
+__device__ inline float layernorm_value(float x, float mu, float sd, float g, float b) {
+  return __fadd_rn(__fmul_rn(__fdiv_rn(__fsub_rn(x, mu), sd), g), b);
+}
+
 }  // namespace mr

@@ -11,6 +11,7 @@
 // epilogue / requant of each result element runs on one lane (mira/ops.py:618,
 // 192-199, 602-603).
 #include "mr_common.hpp"
+#include "np_sum.hpp"
 
 namespace mr {
 
@@ -124,15 +125,39 @@ __global__ void __launch_bounds__(256) qgemv_kernel(const GemvArgs g, const EpiD
 constexpr int KS_MAXS = 8;    // wave-wide loads a lane has in flight at once
 constexpr int KS_KMAX = 4096; // largest k_pad of this kernel (8 waves x 8 steps x 64 bytes)
 
-template <int MR, int KW, int COLS, bool F32IN>
-__global__ void __launch_bounds__(KW * 64) qgemv_ks_kernel(const GemvArgs g, const EpiDev e, const float* x,
-                                                            int64_t ldx, float xs) {
+constexpr int LN_KMAX = 1024; // longest row the layer-normalising prologue takes
+
+// The f32 rows of PRE 1 and 2: x [M][ldx] (K = GemvArgs::lda valid columns), the int8
+// scale xs; PRE 2 layer-normalises each row first (gain g, bias b, eps; f16: the normalised
+// values rounded to f16 before the quantize)
+struct RowIn {
+  const float* x;
+  int64_t ldx;
+  float xs;
+  const float* g;
+  const float* b;
+  float eps;
+  int32_t f16;
+};
+
+// PRE 0: int8 rows (GemvArgs::a); 1: f32 rows quantized here (the F32IN prologue);
+// 2: f32 rows layer-normalised and quantized here (mira/ops.py:356-360 with the layernorm
+// kernel's arithmetic, one wave per row)
+template <int MR, int KW, int COLS, int PRE>
+__global__ void __launch_bounds__(KW * 64) qgemv_ks_kernel(const GemvArgs g, const EpiDev e, const RowIn rin) {
+  constexpr bool F32IN = PRE != 0, LN = PRE == 2;
   constexpr int LPC = 64 / COLS;   // lanes per column
   constexpr int SPL = LPC / 4;     // K steps per wave-wide load
   constexpr int NT = KW * 64;      // threads
   static_assert(KW * KS_MAXS * 64 >= KS_KMAX, "one pass covers k_pad");
+  static_assert(!LN || (MR <= KW && 2 * LN_KMAX <= 4 * NT), "one wave per row; gains and biases in one pass");
   __shared__ int red[KW][MR][COLS];
   __shared__ __attribute__((aligned(16))) int8_t xq[MR][KS_KMAX];
+  __shared__ __attribute__((aligned(16))) float xf[LN ? MR : 1][LN ? LN_KMAX : 4];   // LN: the f32 rows
+  __shared__ float gbl[LN ? 2 * LN_KMAX : 1];                                        // LN: gains, biases
+  const float* x = rin.x;
+  const int64_t ldx = rin.ldx;
+  const float xs = rin.xs;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * COLS;
   const int col = lane / LPC, j = lane % LPC;
@@ -146,8 +171,8 @@ __global__ void __launch_bounds__(KW * 64) qgemv_ks_kernel(const GemvArgs g, con
   // the rows' loads: F32IN 4 f32 words per thread and load (16-byte loads where the
   // rows allow), else 16 int8 bytes (lda % 16 == 0 and a 16-byte aligned: a chunk
   // is all below lda or all past it); zeros past the rows' ends
-  constexpr int XB = F32IN ? 4 : 16;                        // row bytes per thread and load
-  constexpr int NQ = (MR * KS_KMAX / XB + NT - 1) / NT;     // loads per thread at most
+  constexpr int XB = F32IN ? 4 : 16;                        // row elements per thread and load
+  constexpr int NQ = (MR * (LN ? LN_KMAX : KS_KMAX) / XB + NT - 1) / NT;   // loads per thread at most
   const int per_row = g.k_pad / XB;
   float4 vf[F32IN ? NQ : 1];
   v4i vi[F32IN ? 1 : NQ];
@@ -174,6 +199,15 @@ __global__ void __launch_bounds__(KW * 64) qgemv_ks_kernel(const GemvArgs g, con
       if (m < g.M && k0 < g.lda) vi[u] = *reinterpret_cast<const v4i*>(g.a + m * g.lda + k0);
     }
   }
+  // LN: the gains and biases ([g | b], 2K floats), before the weights as well
+  float gbv[LN ? 4 : 1];
+  if constexpr (LN) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = threadIdx.x + u * NT;
+      gbv[u] = i < g.lda ? rin.g[i] : i < 2 * g.lda ? rin.b[i - g.lda] : 0.0f;
+    }
+  }
   // then the weight stream, every load of a lane in flight at once
   v4i w[KS_MAXS];
 #pragma unroll
@@ -188,7 +222,9 @@ __global__ void __launch_bounds__(KW * 64) qgemv_ks_kernel(const GemvArgs g, con
     if (i >= MR * per_row) break;
     const int m = i / per_row, k0 = (i - m * per_row) * XB;
     if (m >= g.M) break;
-    if constexpr (F32IN) {
+    if constexpr (LN) {
+      *reinterpret_cast<float4*>(&xf[m][k0]) = vf[u];
+    } else if constexpr (F32IN) {
       const float f[4] = {vf[u].x, vf[u].y, vf[u].z, vf[u].w};
       uint32_t packed = 0;
 #pragma unroll
@@ -197,6 +233,22 @@ __global__ void __launch_bounds__(KW * 64) qgemv_ks_kernel(const GemvArgs g, con
       *reinterpret_cast<uint32_t*>(&xq[m][k0]) = packed;
     } else {
       *reinterpret_cast<v4i*>(&xq[m][k0]) = vi[u];
+    }
+  }
+  if constexpr (LN) {
+    // wave m normalises row m from LDS, as layernorm_kernel does, and quantizes it
+#pragma unroll
+    for (int u = 0; u < 4; ++u) gbl[threadIdx.x + u * NT < 2 * LN_KMAX ? threadIdx.x + u * NT : 0] = gbv[u];
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (wave < g.M) {
+      const int d = g.lda;
+      float mu, sd;
+      layernorm_row_stats([&](int64_t i) { return xf[wave][i]; }, d, lane, rin.eps, mu, sd);
+      for (int i = lane; i < d; i += 64) {
+        float v = layernorm_value(xf[wave][i], mu, sd, gbl[i], gbl[d + i]);
+        if (rin.f16) v = round_f16(v);
+        xq[wave][i] = quantize_one(v, xs);
+      }
     }
   }
   // every wave's LDS stores done before any wave reads: an LDS-only wait and the
@@ -340,31 +392,29 @@ __global__ void __launch_bounds__(256) w8gemv_kernel(const float* __restrict__ x
 
 // The weight-row stream for M <= 8, k_pad <= 4096: 16 columns per workgroup where
 // that gives every CU one, else 8 or 4 (n0 + COLS <= n_pad: n_pad % 32 == 0).
-template <bool F32IN, int MR>
-static void ks_launch_m(const GemvArgs& g, const EpiDev& e, const float* x, int64_t ldx, float xs,
-                        hipStream_t stream) {
+template <int PRE, int MR>
+static void ks_launch_m(const GemvArgs& g, const EpiDev& e, const RowIn& rin, hipStream_t stream) {
   const int64_t cus = device_cu_count();
   const int cols = (g.N + 15) / 16 >= cus ? 16 : (g.N + 7) / 8 >= cus ? 8 : 4;
   const dim3 grid(static_cast<unsigned>((g.N + cols - 1) / cols)), block(512);
   if (cols == 16)
-    hipLaunchKernelGGL((qgemv_ks_kernel<MR, 8, 16, F32IN>), grid, block, 0, stream, g, e, x, ldx, xs);
+    hipLaunchKernelGGL((qgemv_ks_kernel<MR, 8, 16, PRE>), grid, block, 0, stream, g, e, rin);
   else if (cols == 8)
-    hipLaunchKernelGGL((qgemv_ks_kernel<MR, 8, 8, F32IN>), grid, block, 0, stream, g, e, x, ldx, xs);
+    hipLaunchKernelGGL((qgemv_ks_kernel<MR, 8, 8, PRE>), grid, block, 0, stream, g, e, rin);
   else
-    hipLaunchKernelGGL((qgemv_ks_kernel<MR, 8, 4, F32IN>), grid, block, 0, stream, g, e, x, ldx, xs);
+    hipLaunchKernelGGL((qgemv_ks_kernel<MR, 8, 4, PRE>), grid, block, 0, stream, g, e, rin);
 }
 
-template <bool F32IN>
-static void ks_launch(const GemvArgs& g, const EpiDev& e, const float* x, int64_t ldx, float xs,
-                      hipStream_t stream) {
+template <int PRE>
+static void ks_launch(const GemvArgs& g, const EpiDev& e, const RowIn& rin, hipStream_t stream) {
   if (g.M == 1)
-    ks_launch_m<F32IN, 1>(g, e, x, ldx, xs, stream);
+    ks_launch_m<PRE, 1>(g, e, rin, stream);
   else if (g.M == 2)
-    ks_launch_m<F32IN, 2>(g, e, x, ldx, xs, stream);
+    ks_launch_m<PRE, 2>(g, e, rin, stream);
   else if (g.M <= 4)
-    ks_launch_m<F32IN, 4>(g, e, x, ldx, xs, stream);
+    ks_launch_m<PRE, 4>(g, e, rin, stream);
   else
-    ks_launch_m<F32IN, 8>(g, e, x, ldx, xs, stream);
+    ks_launch_m<PRE, 8>(g, e, rin, stream);
 }
 
 // M <= 8 rows: returns MR_EUNSUPPORTED for larger M (the caller uses the tiled kernel).
@@ -380,7 +430,7 @@ int gemv_launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t k_pad, in
   g.N = static_cast<int32_t>(N);
   g.M = static_cast<int32_t>(M);
   if (k_pad <= KS_KMAX) {
-    ks_launch<false>(g, e, nullptr, 0, 0.0f, stream);
+    ks_launch<0>(g, e, RowIn{}, stream);
     MR_LAUNCH_CHECK("qgemv");
     return MR_OK;
   }
@@ -437,8 +487,54 @@ extern "C" int mr_qmatmul_f32in(const float* x, int64_t ldx, float x_scale, cons
   g.n_pad = static_cast<int32_t>(n_pad);
   g.N = static_cast<int32_t>(N);
   g.M = static_cast<int32_t>(M);
-  mr::ks_launch<true>(g, e, x, ldx, x_scale, static_cast<hipStream_t>(stream));
+  mr::RowIn rin = {};
+  rin.x = x;
+  rin.ldx = ldx;
+  rin.xs = x_scale;
+  mr::ks_launch<1>(g, e, rin, static_cast<hipStream_t>(stream));
   MR_LAUNCH_CHECK("qgemv_f32in");
+  return MR_OK;
+}
+
+extern "C" int mr_qmatmul_lnin(const float* x, int64_t ldx, const float* gamma, const float* beta, float eps,
+                               int32_t round_f16, float x_scale, const int8_t* b, int64_t k_pad, int64_t n_pad,
+                               int64_t M, int64_t N, int64_t K, const mr_epilogue* epi, void* stream) {
+  MR_REQUIRE(x && gamma && beta && b, "mr_qmatmul_lnin: NULL operand");
+  MR_REQUIRE(M >= 0 && N > 0 && K > 0, "mr_qmatmul_lnin: bad sizes M=%lld N=%lld K=%lld", (long long)M,
+             (long long)N, (long long)K);
+  MR_REQUIRE(ldx >= K && x_scale > 0.0f, "mr_qmatmul_lnin: ldx %lld < K %lld or x_scale %g <= 0", (long long)ldx,
+             (long long)K, (double)x_scale);
+  MR_REQUIRE(k_pad >= K && k_pad % 64 == 0, "mr_qmatmul_lnin: k_pad %lld must be >= K and a multiple of 64",
+             (long long)k_pad);
+  MR_REQUIRE(n_pad >= N && n_pad % 32 == 0 && N < (int64_t(1) << 30),
+             "mr_qmatmul_lnin: n_pad %lld must be >= N and a multiple of 32", (long long)n_pad);
+  MR_REQUIRE(reinterpret_cast<uintptr_t>(b) % 16 == 0, "mr_qmatmul_lnin: weights must be 16-byte aligned");
+  if (M > 8 || K > mr::LN_KMAX || k_pad > mr::LN_KMAX) {
+    mr::set_error("mr_qmatmul_lnin: M=%lld rows, K=%lld: the fused layer normalisation takes M <= 8 and "
+                  "k_pad <= %d", (long long)M, (long long)K, mr::LN_KMAX);
+    return MR_EUNSUPPORTED;
+  }
+  mr::EpiDev e;
+  const int rc = mr::make_epi(epi, N, true, &e, true);
+  if (rc != MR_OK) return rc;
+  if (M == 0) return MR_OK;
+  mr::GemvArgs g = {};
+  g.lda = K;   // columns of x: the normalised length
+  g.b = b;
+  g.k_pad = static_cast<int32_t>(k_pad);
+  g.n_pad = static_cast<int32_t>(n_pad);
+  g.N = static_cast<int32_t>(N);
+  g.M = static_cast<int32_t>(M);
+  mr::RowIn rin = {};
+  rin.x = x;
+  rin.ldx = ldx;
+  rin.xs = x_scale;
+  rin.g = gamma;
+  rin.b = beta;
+  rin.eps = eps;
+  rin.f16 = round_f16;
+  mr::ks_launch<2>(g, e, rin, static_cast<hipStream_t>(stream));
+  MR_LAUNCH_CHECK("qgemv_lnin");
   return MR_OK;
 }
 

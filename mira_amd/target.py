@@ -107,6 +107,7 @@ IMAGE_OPS = ("qconv2d", "conv2d", "maxpool2d", "pad", "reduce_mean")
 
 W8_STREAM_ROWS = 64   # mr_w8_matmul_f32 streams the weights once per 8 rows when K % 4 != 0
 F32IN_MAX_ROWS, F32IN_MAX_K = 8, 4096     # mr_qmatmul_f32in's decode shapes (k_pad <= 4096)
+LNIN_MAX_K = 1024                          # mr_qmatmul_lnin's rows (k_pad <= 1024)
 
 
 _UNARY_CODES = {L.EPI_FN[f] for f in L.EPI_UNARY}
@@ -471,6 +472,7 @@ class RocmExecutable:
         self._plan_views()
         self._plan_shared_input_matmuls()
         self._plan_f32in_matmuls()
+        self._plan_lnin_matmuls()
         self._plan_half_storage()
         self._plan_expand_dw()
         for v in g.inputs:
@@ -653,6 +655,49 @@ class RocmExecutable:
                 continue
             self.f32in[op] = v
             self.need_i8[v] = [t for t in self.need_i8.get(v, []) if t != xs]
+
+    def _plan_lnin_matmuls(self) -> None:
+        """A layernorm whose result only decode-shaped q-matmuls read, as their int8 input at
+        one x_scale (a transformer decode step's projections after each layernorm), runs inside
+        the launch of each of them, or of their group (mr_qmatmul_lnin): no layernorm launch,
+        no int8 copy of its result."""
+        self.lnin: dict = {}        # qmatmul op (a group's first op) -> the layernorm it runs
+        g = self.g
+        group_of = {o: head for head, ops in self.row_group.items() for o in ops}
+        for ln in g.ops:
+            if ln.kind != "layernorm" or not self._device_op(ln):
+                continue
+            r = ln.result
+            d = r.type.shape[-1]
+            rows = r.type.numel // d if d else 0
+            if r in g.outputs or r in self.need_f32 or r in self.images or pack.roundup(d, 64) > LNIN_MAX_K or \
+                    not 1 <= rows <= F32IN_MAX_ROWS:
+                continue
+            readers = self.users.get(r, [])
+            if not readers or any(u.kind != "qmatmul" or u.inputs[0] is not r or r in u.inputs[1:] or
+                                  (not self._device_op(u) and u not in group_of) for u in readers):
+                continue
+            if len({_f32key(u.attrs["x_scale"]) for u in readers}) != 1:
+                continue
+            # each reading launch (a q-op, or a group's first q-op) normalises the rows itself
+            heads: dict = {}
+            for u in readers:
+                heads.setdefault(group_of.get(u, u), set()).add(u)
+            if any(set(self.row_group.get(h, [h])) != us or h in self.f32in for h, us in heads.items()):
+                continue
+            for h in heads:
+                self.lnin[h] = ln
+            self.skip.add(ln)
+            self.need_i8.pop(r, None)
+
+    def _lnin_launch(self, ln: "Op", xs: float, b, kp: int, npad: int, M: int, N: int, K: int, e):
+        """The launch of a q-matmul that runs the layernorm `ln` on its f32 rows first."""
+        x = self._c_order(ln.inputs[0])
+        gm, bt = self._c_order(ln.inputs[1]), self._c_order(ln.inputs[2])
+        eps, f16, lib = float(ln.attrs["eps"]), int(ln.result.type.dtype == "f16"), self.lib
+        return lambda s: L.check(lib.mr_qmatmul_lnin(x.data_ptr(), K, gm.data_ptr(), bt.data_ptr(), eps, f16, xs,
+                                                     b.data_ptr(), kp, npad, M, N, K, C.byref(e), s),
+                                 "mr_qmatmul_lnin")
 
     def _full_operand_reader(self, u: "Op", v: "Value") -> bool:
         """Does the q-op u read v only as its int8 input (inputs[0]: the copy v's producer
@@ -1097,9 +1142,11 @@ class RocmExecutable:
         """One launch for q-ops sharing their int8 input (planned by _plan_shared_input_matmuls):
         the weights packed side by side, each result a column slice of the output rows."""
         torch = _t()
-        x = self._src(ops[0].inputs[0])
         xs = _f32key(ops[0].attrs["x_scale"])
-        xq, lda = x.i8[xs] if xs in x.i8 else self._quantize_to(x, xs)
+        ln = self.lnin.get(ops[0])
+        if ln is None:
+            x = self._src(ops[0].inputs[0])
+            xq, lda = x.i8[xs] if xs in x.i8 else self._quantize_to(x, xs)
         q = np.concatenate([np.asarray(op.attrs["q"], np.int8) for op in ops], axis=1)
         ws = np.concatenate([np.asarray(op.attrs["w_scale"], np.float32).reshape(-1) for op in ops])
         K, N = q.shape
@@ -1117,9 +1164,13 @@ class RocmExecutable:
         e.scale, e.out_f32, e.ldo = scale.data_ptr(), y.data_ptr(), N
         self.keep.append(e)
         lib, kp, npad = self.lib, bl.shape[1], bl.shape[0]
-        self._add("qmatmul", lambda s: L.check(
-            lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), kp, npad, M, N, K, C.byref(e), s), "mr_qmatmul"),
-            nbytes=M * K + K * N + 8 * N + 4 * M * N, nops=2 * M * N * K)
+        if ln is not None:
+            self._add("qmatmul", self._lnin_launch(ln, xs, b, kp, npad, M, N, K, e),
+                      nbytes=4 * M * K + 8 * K + K * N + 8 * N + 4 * M * N, nops=2 * M * N * K)
+        else:
+            self._add("qmatmul", lambda s: L.check(
+                lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), kp, npad, M, N, K, C.byref(e), s), "mr_qmatmul"),
+                nbytes=M * K + K * N + 8 * N + 4 * M * N, nops=2 * M * N * K)
 
     def _emit_qmatmul(self, op: "Op") -> None:
         if op in self.row_group:
@@ -1130,8 +1181,10 @@ class RocmExecutable:
         xs = _f32key(a["x_scale"])
         if op in self.f32in:
             return self._emit_qmatmul_f32in(op, self.staging[self.f32in[op]])
-        x = self._src(op.inputs[0])
-        xq, lda = x.i8[xs] if xs in x.i8 else self._quantize_to(x, xs)
+        ln = self.lnin.get(op)
+        if ln is None:
+            x = self._src(op.inputs[0])
+            xq, lda = x.i8[xs] if xs in x.i8 else self._quantize_to(x, xs)
         bl = pack.pack_matmul(q)
         b = self._upload(pack.device_weights(bl))
         scale = self._upload(pack.combined_scale(a["x_scale"], a["w_scale"]))
@@ -1142,9 +1195,13 @@ class RocmExecutable:
             e.out_acc, e.ldacc = acc.data_ptr(), N
         M = out.rows
         lib, kp, npad = self.lib, bl.shape[1], bl.shape[0]
-        self._add("qmatmul", lambda s: L.check(
-            lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), kp, npad, M, N, K, C.byref(e), s), "mr_qmatmul"),
-            nbytes=M * K + K * N + self._epi_bytes(e, M, N), nops=2 * M * N * K)
+        if ln is not None:
+            self._add("qmatmul", self._lnin_launch(ln, xs, b, kp, npad, M, N, K, e),
+                      nbytes=4 * M * K + 8 * K + K * N + self._epi_bytes(e, M, N), nops=2 * M * N * K)
+        else:
+            self._add("qmatmul", lambda s: L.check(
+                lib.mr_qmatmul(xq.data_ptr(), lda, b.data_ptr(), kp, npad, M, N, K, C.byref(e), s), "mr_qmatmul"),
+                nbytes=M * K + K * N + self._epi_bytes(e, M, N), nops=2 * M * N * K)
         self._finish_i8(out, fused)
 
     def _emit_qmatmul_f32in(self, op: "Op", x) -> None:

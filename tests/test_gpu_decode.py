@@ -73,6 +73,64 @@ def test_layernorm_bit_exact(lib, rows, d, f16):
     assert bits_equal(yq.cpu().numpy()[:, :d], G.quantize_activation(want, xs).astype(np.int8))
 
 
+@pytest.mark.parametrize("M,d,N,f16", [(1, 64, 192, False), (1, 64, 65, False), (3, 100, 256, False),
+                                       (8, 128, 64, False), (2, 200, 96, False), (1, 1024, 300, False),
+                                       (1, 64, 256, True), (5, 130, 40, True)])
+def test_qmatmul_lnin(lib, M, d, N, f16):
+    """mr_qmatmul_lnin (the layernorm inside the decode-shaped q-matmul) against the oracle's
+    layernorm, quantize and q-matmul, bit for bit: rows of at most 128 elements (the lanes'
+    pairwise sums) and longer ones (lane 0's recursion), f16 rounding of the normalised rows,
+    a constant row (variance 0) and a wide one."""
+    torch = _torch()
+    rng = np.random.default_rng(M * 100 + d + N)
+    x = (rng.standard_normal((M, d)) * rng.uniform(0.05, 40) + rng.uniform(-10, 10)).astype(np.float32)
+    if M >= 3:
+        x[1] = 2.5
+        x[2, : d // 2] *= 100 if f16 else 1e6
+    g = rng.standard_normal(d).astype(np.float32)
+    b = rng.standard_normal(d).astype(np.float32)
+    if f16:
+        x, g, b = (a.astype(np.float16).astype(np.float32) for a in (x, g, b))
+    y = G.layernorm([x.astype(np.float16), g.astype(np.float16), b.astype(np.float16)] if f16 else [x, g, b],
+                    {"eps": 1e-5}).astype(np.float32)
+    xs = float(np.abs(y).max()) / 127
+    w = rng.standard_normal((d, N)).astype(np.float32)
+    q, ws = G.quantize_array(w, 1)
+    bias = rng.standard_normal(N).astype(np.float32)
+    attrs = {"q": q, "w_scale": ws, "x_scale": xs, "dtype": "f32", "epilogue": (("add", 1, False),)}
+    want = G.qmatmul([y, bias], attrs)
+    want_acc = G.qmatmul_acc(y, attrs)
+    bl = pack.pack_matmul(q)
+    keep = [T(x), T(g), T(b), T(pack.device_weights(bl)), T(pack.combined_scale(xs, ws)), T(bias)]
+    xd, gd, bd, bw, scale, bt = keep
+    out = empty((M, N), torch.float32)
+    acc = empty((M, N), torch.int32)
+    e = epilogue([("add", L.BC_COL, bt, 0, False)], scale=scale, out_f32=out, ldo=N, out_acc=acc, ldacc=N)
+    L.check(lib.mr_qmatmul_lnin(xd.data_ptr(), d, gd.data_ptr(), bd.data_ptr(), 1e-5, int(f16), xs, bw.data_ptr(),
+                                bl.shape[1], bl.shape[0], M, N, d, C.byref(e), stream()), "mr_qmatmul_lnin")
+    sync()
+    assert np.array_equal(acc.cpu().numpy(), want_acc.astype(np.int32))
+    assert bits_equal(out.cpu().numpy(), want)
+
+
+def test_qmatmul_lnin_rejects(lib):
+    """More than 8 rows or a row past 1024 elements: MR_EUNSUPPORTED (the caller keeps the
+    layernorm launch); a row stride shorter than the row is an argument error."""
+    torch = _torch()
+    x = empty((16, 2048), torch.float32)
+    g = empty((2048,), torch.float32)
+    bw = empty((32, 2048), torch.int8)
+    y = empty((16, 32), torch.float32)
+    sc = empty((32,), torch.float64)
+    e = epilogue(scale=sc, out_f32=y, ldo=32)
+    call = lambda ldx, k_pad, M, K: lib.mr_qmatmul_lnin(x.data_ptr(), ldx, g.data_ptr(), g.data_ptr(), 1e-5, 0, 0.1,
+                                                        bw.data_ptr(), k_pad, 32, M, 32, K, C.byref(e), stream())
+    assert call(64, 64, 9, 64) == 3
+    assert call(2048, 2048, 1, 2048) == 3
+    assert call(32, 64, 1, 64) == 1
+    sync()
+
+
 def test_layernorm_int8_only_and_errors(lib):
     torch = _torch()
     x = np.random.default_rng(3).standard_normal((6, 48)).astype(np.float32)
@@ -289,15 +347,18 @@ def _step_feeds(cfg, params, batch, t, seed=9):
 
 def test_gpt_step_exact_mode_device_ops():
     """Default mode: layernorm, the head transposes and the cache concats join the W8A8
-    projections on rocm; the attention matmuls, softmax and the gelu projection stay on the
-    CPU; every output bit-exact."""
+    projections on rocm (a layernorm that only rocm projections read runs inside their
+    launches, mr_qmatmul_lnin; each layer's second one feeds the gelu projection on the CPU
+    and keeps its own launch); the attention matmuls, softmax and the gelu projection stay
+    on the CPU; every output bit-exact."""
     cfg, params, g = _gpt(2)
     feeds = _step_feeds(cfg, params, 2, 20)
     runner = Runner(g, RocmTarget(), fallback=G.CPUTarget())
     on_cpu = {op.kind for seg in runner.segments if seg.device == "cpu" for op in seg.graph.compute_ops()}
     assert on_cpu <= {"matmul", "softmax", "qmatmul", "transpose", "reshape", "concat"}, on_cpu
     kinds = {k for exe in runner.executables("rocm") for k in exe.kernel_counts}
-    assert {"layernorm", "concat"} <= kinds
+    assert "concat" in kinds, kinds
+    assert sum(exe.kernel_counts.get("layernorm", 0) for exe in runner.executables("rocm")) == cfg.L
     got = runner.run(feeds)
     want = G.run_graph(g, feeds)
     for a, b in zip(got, want):
@@ -610,10 +671,11 @@ def test_decode_embed_and_commit_exact(lib):
 
 def test_gpt_step_approx_mode_fuses_attention():
     """approx_f32: each layer's attention (scores, scale, mask, softmax, context, and the cache
-    concatenations) is one launch, which also writes the int8 input of the out projection, and
-    the query/key/value projections of a layer are one q-op launch: 16 launches per step."""
+    concatenations) is one launch, which also writes the int8 input of the out projection, the
+    query/key/value projections of a layer are one q-op launch, and each layernorm runs inside
+    the launch of the projections that read it: 11 launches per step."""
     cfg, params, g = _gpt(2)
     exe = Runner(g, RocmTarget(approx_f32=True)).executables("rocm")[0]
     k = exe.kernel_counts
-    assert k.get("attention") == cfg.L and not {"softmax", "bmm_f32", "concat", "quantize"} & set(k), k
-    assert k["qmatmul"] == 4 * cfg.L + 1 and len(exe.launches) == 16
+    assert k.get("attention") == cfg.L and not {"softmax", "bmm_f32", "concat", "quantize", "layernorm"} & set(k), k
+    assert k["qmatmul"] == 4 * cfg.L + 1 and len(exe.launches) == 11
