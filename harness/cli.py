@@ -277,17 +277,58 @@ def _format_expr(e) -> str:
         return repr(e[1])
     if kind == "bool":
         return "true" if e[1] else "false"
-    if kind == "name":
+    if kind in ("name", "dtype"):
         return e[1]
     if kind == "list":
         return "[" + ", ".join(_format_expr(x) for x in e[1]) + "]"
+    if kind == "tuple":
+        return "(" + ", ".join(_format_expr(x) for x in e[1]) + ("," if len(e[1]) == 1 else "") + ")"
     if kind == "neg":
         return f"-{_format_expr(e[1])}"
     if kind == "bin":
         return f"({_format_expr(e[2])} {e[1]} {_format_expr(e[3])})"
+    if kind == "index":
+        return f"{_format_expr(e[1])}[{_format_items(e[2])}]"
     _, name, args, kwargs, _ = e
     return f"{name}(" + ", ".join([_format_expr(a) for a in args] +
                                   [f"{k}={_format_expr(v)}" for k, v in kwargs.items()]) + ")"
+
+
+def _format_items(items) -> str:
+    def one(it):
+        if it[0] == "at":
+            return _format_expr(it[1])
+        return "".join([_format_expr(it[1]) if it[1] is not None else "", ":",
+                        _format_expr(it[2]) if it[2] is not None else ""])
+    return ", ".join(one(it) for it in items)
+
+
+def _format_block(body, indent: str) -> list:
+    out = []
+    for st in body:
+        kind = st[0]
+        if kind == "let":
+            ann = f": {_format_type(st[2])}" if st[2] is not None else ""
+            out.append(f"{indent}let {', '.join(st[1])}{ann} = {_format_expr(st[3])}")
+        elif kind == "assign":
+            out.append(f"{indent}{', '.join(st[1])} = {_format_expr(st[2])}")
+        elif kind == "index_assign":
+            out.append(f"{indent}{st[1]}[{_format_items(st[2])}] = {_format_expr(st[3])}")
+        elif kind == "for":
+            out.append(f"{indent}for {st[1]} in {_format_expr(st[2])}..{_format_expr(st[3])} {{")
+            out += _format_block(st[4], indent + "  ") + [f"{indent}}}"]
+        elif kind == "if":
+            out.append(f"{indent}if {_format_expr(st[1])} {{")
+            out += _format_block(st[2], indent + "  ")
+            if st[3] is not None:
+                out += [f"{indent}}} else {{"] + _format_block(st[3], indent + "  ")
+            out.append(f"{indent}}}")
+        elif kind == "while":
+            out.append(f"{indent}while {_format_expr(st[1])} {{")
+            out += _format_block(st[2], indent + "  ") + [f"{indent}}}"]
+        else:
+            out.append(f"{indent}return {', '.join(_format_expr(v) for v in st[1])}")
+    return out
 
 
 def format_module(fns: dict) -> str:
@@ -295,9 +336,9 @@ def format_module(fns: dict) -> str:
     out = []
     for fn in fns.values():
         params = ", ".join(("const " if p.const else "") + f"{p.name}: {_format_type(p.type)}" for p in fn.params)
-        out.append(f"fn {fn.name}({params}) -> {_format_type(fn.ret)} {{")
-        for st in fn.body:
-            out.append(f"  let {st[1]} = {_format_expr(st[2])}" if st[0] == "let" else f"  return {_format_expr(st[1])}")
+        rets = ", ".join(_format_type(t) for t in fn.rets)
+        out.append(f"fn {fn.name}({params}) -> {rets if len(fn.rets) == 1 else f'({rets})'} {{")
+        out += _format_block(fn.body, "  ")
         out.append("}")
     return "\n".join(out)
 

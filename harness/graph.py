@@ -12,7 +12,9 @@ tests and the benchmark.  Those names are the interface and are kept:
 
 Everything else here is this harness's own: a builder (`Graph.op`) whose
 result types come from the small shape rules below, and a verifier.  There is
-no control flow (the W8A8 configurations have none).
+no control flow (the W8A8 configurations have none).  Integer (i32) values
+appear in index and mask arithmetic; comparisons give 1 / 0 in their operands'
+dtype, as MIRA's do (mira/ops.py:134-140).
 """
 from __future__ import annotations
 
@@ -112,17 +114,26 @@ def _reduce_shape(x: TensorType, a: dict) -> tuple:
     return tuple(d for i, d in enumerate(x.shape) if i not in axes)
 
 
-ELEMENTWISE_UNARY = ("relu", "gelu", "sigmoid", "tanh", "exp", "neg", "abs", "sqrt")
-ELEMENTWISE_BINARY = ("add", "sub", "mul", "div", "maximum", "minimum")
+ELEMENTWISE_UNARY = ("relu", "gelu", "sigmoid", "tanh", "exp", "log", "neg", "abs", "sign", "sqrt")
+ELEMENTWISE_BINARY = ("add", "sub", "mul", "div", "pow", "maximum", "minimum", "greater", "greater_equal", "equal")
+
+
+def _broadcast(*shapes) -> tuple:
+    try:
+        return tuple(np.broadcast_shapes(*shapes))
+    except ValueError:
+        raise ValueError(f"shapes {' and '.join(str(list(s)) for s in shapes)} do not broadcast") from None
 
 
 def result_type(kind: str, ins: list, a: dict) -> TensorType:
-    """The result type of a float op the builders use (shape rules of this harness)."""
+    """The result type of an op the builders use (shape rules of this harness)."""
     t0 = ins[0] if ins else None
     if kind in ELEMENTWISE_UNARY or kind in ("softmax", "layernorm"):
         return t0
     if kind in ELEMENTWISE_BINARY:
-        return TensorType(t0.dtype, np.broadcast_shapes(t0.shape, ins[1].shape))
+        if t0.dtype != ins[1].dtype:
+            raise ValueError(f"{kind}: operands {t0} and {ins[1]} differ in dtype")
+        return TensorType(t0.dtype, _broadcast(t0.shape, ins[1].shape))
     if kind == "matmul":
         return TensorType(t0.dtype, _matmul_shape(t0, ins[1]))
     if kind == "conv2d":
@@ -133,8 +144,35 @@ def result_type(kind: str, ins: list, a: dict) -> TensorType:
         return TensorType(t0.dtype, (n, c, (h - k) // s + 1, (w - k) // s + 1))
     if kind == "pad":
         return TensorType(t0.dtype, tuple(d + lo + hi for d, (lo, hi) in zip(t0.shape, a["pads"])))
-    if kind == "reduce_mean":
+    if kind in ("reduce_mean", "reduce_sum", "reduce_max"):
         return TensorType(t0.dtype, _reduce_shape(t0, a))
+    if kind == "slice":
+        begin, size = tuple(a["begin"]), tuple(a["size"])
+        if len(begin) != t0.rank or len(size) != t0.rank or \
+                any(b < 0 or n < 0 or b + n > d for b, n, d in zip(begin, size, t0.shape)):
+            raise ValueError(f"slice begin {list(begin)} size {list(size)} does not fit {t0}")
+        return TensorType(t0.dtype, size)
+    if kind == "gather":
+        if ins[1].dtype != "i32":
+            raise ValueError(f"gather: indices must be i32, got {ins[1]}")
+        ax = a["axis"] % t0.rank
+        return TensorType(t0.dtype, t0.shape[:ax] + ins[1].shape + t0.shape[ax + 1:])
+    if kind == "where":
+        if ins[1].dtype != ins[2].dtype:
+            raise ValueError(f"where: {ins[1]} and {ins[2]} differ in dtype")
+        return TensorType(ins[1].dtype, _broadcast(t0.shape, ins[1].shape, ins[2].shape))
+    if kind in ("sort", "cumprod"):
+        return t0
+    if kind in ("argmax", "argmin"):
+        ax = a["axis"] % t0.rank
+        keep = a.get("keepdims", False)
+        return TensorType("i32", tuple(1 if i == ax else d for i, d in enumerate(t0.shape)) if keep else
+                          tuple(d for i, d in enumerate(t0.shape) if i != ax))
+    if kind == "broadcast":
+        shape = tuple(a["shape"])
+        if _broadcast(t0.shape, shape) != shape:
+            raise ValueError(f"broadcast: {t0} does not broadcast to {list(shape)}")
+        return TensorType(t0.dtype, shape)
     if kind == "reshape":
         shape = tuple(a["shape"])
         if int(np.prod(shape, dtype=np.int64)) != t0.numel:

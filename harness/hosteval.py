@@ -31,10 +31,19 @@ def _gelu(x):
     return 0.5 * x * (1.0 + np.tanh(0.7978845608028654 * (x + 0.044715 * x ** 3)))
 
 
+def _num(a) -> np.ndarray:
+    """Floats compute in f32; integers stay exact (mira/ops.py:150-152)."""
+    a = np.asarray(a)
+    return a if a.dtype.kind == "i" else _f32(a)
+
+
 UNARY = {"relu": lambda x: np.maximum(x, 0), "gelu": _gelu, "sigmoid": lambda x: 1.0 / (1.0 + np.exp(-x)),
-         "tanh": np.tanh, "exp": np.exp, "neg": np.negative, "abs": np.abs, "sqrt": np.sqrt}
-BINARY = {"add": np.add, "sub": np.subtract, "mul": np.multiply, "div": np.divide, "maximum": np.maximum,
-          "minimum": np.minimum}
+         "tanh": np.tanh, "exp": np.exp, "log": np.log, "neg": np.negative, "abs": np.abs, "sign": np.sign,
+         "sqrt": np.sqrt}
+BINARY = {"add": np.add, "sub": np.subtract, "mul": np.multiply, "div": np.divide, "pow": np.power,
+          "maximum": np.maximum, "minimum": np.minimum, "greater": np.greater, "greater_equal": np.greater_equal,
+          "equal": np.equal}
+REDUCE = {"reduce_sum": np.sum, "reduce_mean": np.mean, "reduce_max": np.max}
 
 
 def apply_epilogue(y: np.ndarray, operands: list, steps) -> np.ndarray:
@@ -120,9 +129,9 @@ def evaluate(kind: str, xs: list, a: dict) -> np.ndarray:
         return (a["q"].astype(np.float32) * a["scale"].reshape(shape)).astype(DTYPES[a["dtype"]])
     dt = xs[0].dtype if xs else np.float32
     if kind in UNARY:
-        return UNARY[kind](_f32(xs[0])).astype(dt)
+        return UNARY[kind](_num(xs[0])).astype(dt)
     if kind in BINARY:
-        return BINARY[kind](_f32(xs[0]), _f32(xs[1])).astype(dt)
+        return BINARY[kind](_num(xs[0]), _num(xs[1])).astype(dt)
     if kind == "matmul":
         return apply_epilogue(_f32(xs[0]) @ _f32(xs[1]), xs, a.get("epilogue", ())).astype(dt)
     if kind == "conv2d":
@@ -143,8 +152,23 @@ def evaluate(kind: str, xs: list, a: dict) -> np.ndarray:
         return win.max(axis=(-2, -1)).astype(dt)
     if kind == "pad":
         return np.pad(xs[0], a["pads"], constant_values=np.asarray(a.get("value", 0)).astype(dt))
-    if kind == "reduce_mean":
-        return np.asarray(_f32(xs[0]).mean(axis=tuple(a["axes"]), keepdims=a.get("keepdims", False))).astype(dt)
+    if kind in REDUCE:
+        return np.asarray(REDUCE[kind](_num(xs[0]), axis=tuple(a["axes"]), keepdims=a.get("keepdims", False))).astype(dt)
+    if kind == "slice":
+        return xs[0][tuple(slice(b, b + n) for b, n in zip(a["begin"], a["size"]))].copy()
+    if kind == "gather":
+        return np.take(xs[0], xs[1], axis=a["axis"])
+    if kind == "where":
+        return np.where(xs[0] != 0, xs[1], xs[2]).astype(xs[1].dtype)
+    if kind == "broadcast":
+        return np.broadcast_to(xs[0], a["shape"]).copy()
+    if kind == "sort":
+        return np.sort(xs[0], axis=a["axis"])
+    if kind == "cumprod":
+        return np.cumprod(_num(xs[0]), axis=a["axis"]).astype(dt)
+    if kind in ("argmax", "argmin"):
+        f = np.argmax if kind == "argmax" else np.argmin
+        return np.asarray(f(xs[0], axis=a["axis"], keepdims=a.get("keepdims", False))).astype(np.int32)
     if kind == "reshape":
         return xs[0].reshape(a["shape"])
     if kind == "transpose":

@@ -22,6 +22,7 @@ The arithmetic of the attrs follows MIRA's definitions:
 """
 from __future__ import annotations
 
+import hashlib
 from typing import Optional, Sequence
 
 import numpy as np
@@ -54,25 +55,117 @@ def _const_array(v) -> Optional[np.ndarray]:
 
 
 # ---------------------------------------------------------------- float passes
+# MIRA's optimizer (mira/passes.py:266-286): f16 lowering, then constant folding,
+# simplification, common-subexpression and dead-code elimination to a fixed point, then
+# epilogue fusion and a last dead-code pass.
 
-def drop_zero_terms(g: Graph) -> int:
-    """x + 0, 0 + x and x - 0 with an all-zero constant disappear when the result has x's type
-    (MIRA's simplify does this, mira/passes.py:56-57; it is why a dense layer with a zero bias
-    reaches the target without an epilogue)."""
-    n = 0
-    for op in list(g.ops):
-        if op.kind not in ("add", "sub"):
+FOLD_LIMIT = 1 << 22          # folded results above this many elements stay ops (mira/passes.py:17)
+
+
+def const_fold(g: Graph) -> bool:
+    """Ops whose inputs are all constants become constants (mira/passes.py:25-37)."""
+    changed = False
+    for op in g.ops:
+        if op.kind == "const" or not op.inputs or op.result.type.numel > FOLD_LIMIT:
             continue
-        a, b = op.inputs
-        for keep, zero in ((a, b), (b, a)) if op.kind == "add" else ((a, b),):
-            z = _const_array(zero)
-            if z is not None and not np.any(z) and keep.type == op.result.type:
-                g.redirect(op.result, keep)
-                g.ops.remove(op)
-                n += 1
-                break
+        vals = [_const_array(v) for v in op.inputs]
+        if any(v is None for v in vals):
+            continue
+        out = hosteval.evaluate(op.kind, vals, op.attrs)
+        op.kind, op.inputs, op.attrs = "const", [], {"value": np.asarray(out, dtype=op.result.type.np_dtype)}
+        changed = True
+    return changed
+
+
+def _splat(v, x: float) -> bool:
+    c = _const_array(v)
+    return c is not None and bool(np.all(c == x))
+
+
+def simplify(g: Graph) -> bool:
+    """Peephole rewrites (mira/passes.py:47-102): x + 0, 0 + x, x - 0, x * 1, 1 * x, x / 1,
+    x ** 1 (when the result keeps x's type), neg(neg x), identity and composed transposes,
+    identity and chained reshapes, same-dtype casts and the exact f16 -> f32 -> f16 round trip."""
+    changed = False
+    for op in list(g.ops):
+        r, ins, k = op.result, op.inputs, op.kind
+        new = None
+        if k in ("add", "sub") and _splat(ins[1], 0) and ins[0].type == r.type:
+            new = ins[0]
+        elif k == "add" and _splat(ins[0], 0) and ins[1].type == r.type:
+            new = ins[1]
+        elif k in ("mul", "div", "pow") and _splat(ins[1], 1) and ins[0].type == r.type:
+            new = ins[0]
+        elif k == "mul" and _splat(ins[0], 1) and ins[1].type == r.type:
+            new = ins[1]
+        elif k == "neg" and ins[0].producer is not None and ins[0].producer.kind == "neg":
+            new = ins[0].producer.inputs[0]
+        elif k == "transpose":
+            perm, inner = tuple(op.attrs["perm"]), ins[0].producer
+            ident = tuple(range(len(perm)))
+            if perm == ident:
+                new = ins[0]
+            elif inner is not None and inner.kind == "transpose":
+                both = tuple(inner.attrs["perm"][p] for p in perm)
+                if both == ident:
+                    new = inner.inputs[0]
+                else:
+                    op.inputs, op.attrs = [inner.inputs[0]], {"perm": both}
+                    changed = True
+        elif k == "reshape":
+            inner = ins[0].producer
+            if tuple(op.attrs["shape"]) == ins[0].type.shape:
+                new = ins[0]
+            elif inner is not None and inner.kind == "reshape":
+                if inner.inputs[0].type.shape == r.type.shape:
+                    new = inner.inputs[0]
+                else:
+                    op.inputs = [inner.inputs[0]]
+                    changed = True
+        elif k == "cast":
+            inner = ins[0].producer
+            if ins[0].type.dtype == op.attrs["dtype"]:
+                new = ins[0]
+            elif inner is not None and inner.kind == "cast" and inner.inputs[0].type == r.type \
+                    and inner.inputs[0].type.dtype == "f16":
+                new = inner.inputs[0]
+        if new is not None and new is not r:
+            g.redirect(r, new)
+            changed = True
+    return changed
+
+
+def _op_key(op: Op) -> tuple:
+    def digest(a):
+        a = np.ascontiguousarray(a)
+        return (a.dtype.str, a.shape, hashlib.sha1(a.tobytes()).hexdigest())
+    if op.kind == "const":
+        return ("const",) + digest(op.attrs["value"])
+    attrs = tuple(sorted((k, digest(v) if isinstance(v, np.ndarray) else repr(v)) for k, v in op.attrs.items()))
+    return (op.kind, tuple(v.id for v in op.inputs), attrs)
+
+
+def cse(g: Graph) -> bool:
+    """Identical ops on identical inputs computed once (mira/passes.py:116-130); constants match
+    on their bytes, confirmed element for element."""
+    seen: dict = {}
+    changed = False
+    for op in g.ops:
+        key = _op_key(op)
+        prev = seen.get(key)
+        if prev is not None and (op.kind != "const" or np.array_equal(prev.attrs["value"], op.attrs["value"])):
+            g.redirect(op.result, prev.result)
+            changed = True
+        else:
+            seen[key] = op
+    return changed
+
+
+def dce(g: Graph) -> bool:
+    """Ops none of whose results reach an output are dropped (mira/passes.py:133-144)."""
+    n = len(g.ops)
     g.prune()
-    return n
+    return len(g.ops) != n
 
 
 def _absorb_step(g: Graph, op: Op, users: dict) -> bool:
@@ -118,41 +211,55 @@ def fuse_epilogues(g: Graph) -> int:
 
 
 def lower_f16(g: Graph) -> None:
-    """MIRA's f16 precision (mira/passes.py:206-253) for a graph without casts: f32 constants
-    are rounded to f16, every f32 result becomes f16, each f32 input is cast to f16 where it
-    enters and each f32 output cast back to f32 where it leaves."""
-    if any(op.kind == "cast" for op in g.ops):
-        raise NotImplementedError("lower_f16: graphs with casts")
+    """MIRA's f16 precision (mira/passes.py:206-253): float constants are rounded to f16, every
+    f32 result becomes f16, each f32 input is cast to f16 where it enters and each f32 output
+    cast back to f32 where it leaves; casts between float types disappear and casts to or from
+    integers stay, aimed at f16."""
     body, g.ops = g.ops, []
+    out_dtypes = [v.type.dtype for v in g.outputs]
+    sub: dict = {}
     for v in g.inputs:
         if v.type.dtype == "f32":
-            c = g.emit("cast", [v], {"dtype": "f16"}, TensorType("f16", v.type.shape))
-            for op in body:
-                op.inputs = [c if x is v else x for x in op.inputs]
+            sub[v] = g.emit("cast", [v], {"dtype": "f16"}, TensorType("f16", v.type.shape))
     for op in body:
-        if op.kind == "const" and op.attrs["value"].dtype == np.float32:
-            op.attrs["value"] = op.attrs["value"].astype(np.float16)
+        op.inputs = [sub.get(x, x) for x in op.inputs]
+        if op.kind == "const":
+            a = op.attrs["value"]
+            if a.dtype.kind == "f":
+                op.attrs["value"] = a.astype(np.float16)
+        elif op.kind == "cast":
+            src = op.inputs[0]
+            target = "f16" if op.attrs["dtype"] in ("f16", "f32") else op.attrs["dtype"]
+            if src.type.dtype == target:
+                sub[op.result] = src
+                continue
+            op.attrs = {**op.attrs, "dtype": target}
         for r in op.results:
             if r.type.dtype == "f32":
                 r.type = TensorType("f16", r.type.shape)
         g.ops.append(op)
     outs = []
-    for v in g.outputs:
-        outs.append(g.emit("cast", [v], {"dtype": "f32"}, TensorType("f32", v.type.shape))
-                    if v.type.dtype == "f16" else v)
+    for v, dt in zip(g.outputs, out_dtypes):
+        v = sub.get(v, v)
+        if dt == "f32" and v.type.dtype != "f32":
+            v = g.emit("cast", [v], {"dtype": "f32"}, TensorType("f32", v.type.shape))
+        outs.append(v)
     g.outputs = outs
 
 
 def prepare(g: Graph, precision: Optional[str] = None) -> Graph:
-    """The float graph as MIRA's optimizer leaves it for these networks: optional f16
-    lowering, zero-term removal, epilogue fusion."""
+    """The float graph as MIRA's optimizer leaves it (mira/passes.py:266-286): optional f16
+    lowering, then const-fold / simplify / CSE / DCE to a fixed point (at most 10 rounds, each
+    running all four), epilogue fusion, DCE."""
     if precision == "f16":
         lower_f16(g)
     elif precision is not None:
         raise ValueError(f"precision {precision!r}: None (f32) or 'f16'")
-    drop_zero_terms(g)
+    for _ in range(10):
+        if not any([const_fold(g), simplify(g), cse(g), dce(g)]):
+            break
     fuse_epilogues(g)
-    g.prune()
+    dce(g)
     g.check()
     return g
 

@@ -1,31 +1,55 @@
-"""A front end for MIRA's source language (.mira), the subset its CNN / MLP programs use:
-the counterpart of mira/lexer.py, mira/parser.py and mira/elaborate.py for the W8A8 path,
-producing this harness's graphs.
+"""A front end for MIRA's source language (.mira): the counterpart of mira/lexer.py,
+mira/parser.py and mira/elaborate.py, producing this harness's graphs.
 
     program   := function*
-    function  := "fn" NAME "(" [param ("," param)*] ")" "->" type "{" statement* "}"
-    param     := ["const"] NAME ":" type
-    type      := DTYPE ["[" dim ("," dim)* "]"]          DTYPE: f32 | f16
+    function  := "fn" NAME "(" [param ("," param)*] ")" "->" (type | "(" type ("," type)* ")") block
+    param     := ["const"] NAME ":" type  |  NAME ":" "int"          (a compile-time integer)
+    type      := DTYPE ["[" dim ("," dim)* "]"]          DTYPE: f32 | f16 | i32
     dim       := integer arithmetic (+ - * /, parentheses) over literals and shape symbols
-    statement := "let" NAME "=" expr  |  "return" expr
-    expr      := the binary operators + - (loosest), * / @ (tighter), unary -, calls
-                 f(arg, ..., name=value), names, numbers, true / false, [lists],
-                 parentheses; "#" starts a comment
+    block     := "{" statement* "}"
+    statement := "let" names [":" type] "=" expr  |  names "=" expr
+               | NAME "[" item ("," item)* "]" "=" expr
+               | "for" NAME "in" expr ".." expr block
+               | "if" expr block ["else" (block | if-statement)]
+               | "while" expr block
+               | "return" expr ("," expr)*
+    names     := NAME ("," NAME)*  |  "(" NAME ("," NAME)* ")"
+    expr      := sum [("<" | "<=" | ">" | ">=" | "==" | "!=") sum]
+    sum       := term (("+" | "-") term)*          term := unary (("*" | "/" | "@") unary)*
+    unary     := "-" unary | power                 power := postfix ["**" unary]
+    postfix   := primary ("[" item ("," item)* "]")*      item := expr | [expr] ":" [expr]
+    primary   := number | true | false | DTYPE | NAME | NAME "(" args ")" | "(" expr ")"
+               | "(" expr "," [expr ("," expr)*] ")" | "[" [expr ("," expr)*] "]"
+    "#" starts a comment; a call's "(" and an index's "[" sit on the line of what they follow.
 
 Elaboration inlines every call of a user function, binding the shape symbols of its
-parameter types from the arguments (a symbol seen twice must agree) and checking the
-result against the declared return type.  The entry function's plain parameters become
-graph inputs; its `const` parameters are weights: given ones are used, the others are
-drawn in declaration order from one seeded generator by MIRA's rule
-(mira/elaborate.py:196-213, 1114-1123; harness.models.mira_random_weight).
+parameter types from the arguments (a symbol seen twice must agree), its `int` parameters
+from compile-time numbers, and checks the results against the declared return types.
+`for` loops are unrolled and `if` on a compile-time condition picks its branch while
+elaborating; a `while` or an `if` on a runtime tensor, indexed assignment and `grad` are
+the control-flow and autodiff half of MIRA's language, which its W8A8 rewrite rejects
+(mira/quantize.py:84-85): this front end reports them as unsupported.  The entry
+function's plain parameters become graph inputs, its `int` parameters take values from
+`dims`; its `const` parameters are weights: given ones are used, the others are drawn in
+declaration order from one seeded generator by MIRA's rule (mira/elaborate.py:196-213,
+1114-1123; harness.models.mira_random_weight).
 
 Shape symbols bound in a function are plain numbers in its body, so `reshape(x, [B, C * H * W])`
-works.  Builtins, with MIRA's parameter names and defaults (mira/elaborate.py:1081-1111):
-relu sigmoid tanh gelu exp abs sqrt (x), maximum / minimum (a, b), matmul(a, b),
-softmax(x, axis=-1), mean(x, axis=all, keepdims=false), transpose(x, perm=swap last two),
-reshape(x, shape) with one -1 allowed, flatten(x, axis=1),
+works.  Builtins, with MIRA's parameter names and defaults (mira/elaborate.py:1070-1111):
+relu sigmoid tanh gelu exp log abs sign sqrt (x) -- on a number they compute at compile
+time --, maximum / minimum (a, b), matmul(a, b), softmax(x, axis=-1),
+sum / mean / max (x, axis=all, keepdims=false), layernorm(x, gamma, beta, eps=1e-5),
+transpose(x, perm=swap last two), reshape(x, shape) with one -1 allowed, flatten(x, axis=1),
+concat(xs, axis=0), cast(x, dtype), slice(x, begin, size), pad(x, pads, value=0),
+broadcast(x, shape), gather(x, indices, axis=0), where(cond, a, b), size(x, axis),
+sort / cumprod (x, axis=-1), argmax / argmin (x, axis=-1, keepdims=false),
+zeros / ones (shape, dtype=f32), full(shape, value, dtype=f32), arange(start, stop, dtype=i32),
 conv2d(x, w, stride=1, padding=0, dilation=1, groups=1),
 maxpool2d / avgpool2d (x, size=2, stride=size, padding=0).
+Indexing follows mira/elaborate.py:617-675: the static subscripts of `x[...]` become one
+slice, axes indexed by a single number are reshaped away, and i32 tensor subscripts become
+gathers.  Comparisons of tensors give 1 / 0 in the operands' dtype: `a < b` is
+greater(b, a), `a <= b` greater_equal(b, a), `a != b` 1 - equal(a, b) (mira/elaborate.py:566-597).
 """
 from __future__ import annotations
 
@@ -35,7 +59,7 @@ from typing import Optional
 
 import numpy as np
 
-from harness.graph import Graph, Value
+from harness.graph import DTYPES, Graph, Value
 from harness.models import mira_random_weight
 
 
@@ -47,12 +71,14 @@ class MiraSyntaxError(ValueError):
 
 _TOKEN = re.compile(r"""
     (?P<ws>[ \t\r]+) | (?P<comment>\#[^\n]*) | (?P<nl>\n)
-  | (?P<num>\d+\.\d*(?:[eE][+-]?\d+)?|\d+[eE][+-]?\d+|\.\d+(?:[eE][+-]?\d+)?|\d+)
+  | (?P<num>\d+\.(?!\.)\d*(?:[eE][+-]?\d+)?|\d+[eE][+-]?\d+|\.\d+(?:[eE][+-]?\d+)?|\d+)
   | (?P<name>[A-Za-z_][A-Za-z_0-9]*)
-  | (?P<op>->|[-+*/@=(),:\[\]{}])
+  | (?P<op>->|\.\.|\*\*|<=|>=|==|!=|[-+*/@=(),:\[\]{}<>])
 """, re.VERBOSE)
 
-KEYWORDS = {"fn", "let", "return", "const"}
+KEYWORDS = {"fn", "let", "return", "const", "for", "in", "while", "if", "else"}
+COMPARE = ("<", "<=", ">", ">=", "==", "!=")
+MAX_UNROLL = 4096
 
 
 @dataclass
@@ -85,8 +111,8 @@ def tokenize(src: str) -> list[Tok]:
 
 @dataclass
 class TypeRef:
-    dtype: str
-    dims: list            # dim expressions (see _parse_dim): int, str, or (op, left, right)
+    dtype: str            # f32 / f16 / i32, or "int" for a compile-time integer parameter
+    dims: list            # dim expressions: int, str, or (op, left, right)
 
 
 @dataclass
@@ -100,12 +126,18 @@ class Param:
 class Fn:
     name: str
     params: list[Param]
-    ret: TypeRef
-    body: list            # ("let", name, expr, line) | ("return", expr, line)
+    rets: list[TypeRef]
+    body: list
     line: int
 
 
-# expressions: ("num", value) ("name", id) ("neg", e) ("bin", op, a, b) ("call", name, args, kwargs, line)
+# statements: ("let", names, TypeRef | None, expr, line)  ("assign", names, expr, line)
+#             ("index_assign", name, items, expr, line)  ("for", var, start, stop, body, line)
+#             ("if", cond, then_body, else_body | None, line)  ("while", cond, body, line)
+#             ("return", [expr, ...], line)
+# expressions: ("num", v) ("bool", v) ("dtype", name) ("name", id) ("neg", e) ("bin", op, a, b)
+#              ("call", name, args, kwargs, line) ("list", items) ("tuple", items)
+#              ("index", base, items, line) with items ("at", e) | ("range", lo | None, hi | None)
 
 
 class _Parser:
@@ -113,7 +145,7 @@ class _Parser:
         self.t, self.i = toks, 0
 
     def peek(self, k: int = 0) -> Tok:
-        return self.t[self.i + k]
+        return self.t[min(self.i + k, len(self.t) - 1)]
 
     def take(self, text: Optional[str] = None, kind: Optional[str] = None) -> Tok:
         tok = self.t[self.i]
@@ -125,6 +157,10 @@ class _Parser:
 
     def at(self, text: str) -> bool:
         return self.t[self.i].text == text and self.t[self.i].kind in ("op", "kw")
+
+    def same_line(self) -> bool:
+        """The current token sits on the line of the one before it."""
+        return self.i > 0 and self.t[self.i].line == self.t[self.i - 1].line
 
     def program(self) -> dict[str, Fn]:
         fns = {}
@@ -141,38 +177,116 @@ class _Parser:
         self.take("(")
         params = []
         while not self.at(")"):
-            const = self.peek().text == "const" and self.peek().kind == "kw"
+            const = self.at("const")
             if const:
                 self.take("const")
             pname = self.take(kind="name").text
             self.take(":")
-            params.append(Param(pname, self.type_ref(), const))
+            tref = self.type_ref(allow_int=not const)
+            params.append(Param(pname, tref, const))
             if not self.at(")"):
                 self.take(",")
         self.take(")")
         self.take("->")
-        ret = self.type_ref()
+        if self.at("("):
+            self.take("(")
+            rets = [self.type_ref()]
+            while self.at(","):
+                self.take(",")
+                rets.append(self.type_ref())
+            self.take(")")
+        else:
+            rets = [self.type_ref()]
+        return Fn(name, params, rets, self.block(), line)
+
+    def block(self) -> list:
         self.take("{")
         body = []
         while not self.at("}"):
-            tok = self.peek()
-            if tok.text == "let" and tok.kind == "kw":
-                self.take("let")
-                lname = self.take(kind="name").text
-                self.take("=")
-                body.append(("let", lname, self.expr(), tok.line))
-            elif tok.text == "return" and tok.kind == "kw":
-                self.take("return")
-                body.append(("return", self.expr(), tok.line))
-            else:
-                raise MiraSyntaxError(f"line {tok.line}: expected 'let' or 'return', found {tok.text!r}")
+            if self.peek().kind == "eof":
+                raise MiraSyntaxError(f"line {self.peek().line}: expected '}}', found end of file")
+            body.append(self.statement())
         self.take("}")
-        return Fn(name, params, ret, body, line)
+        return body
 
-    def type_ref(self) -> TypeRef:
+    def names(self) -> list[str]:
+        paren = self.at("(")
+        if paren:
+            self.take("(")
+        out = [self.take(kind="name").text]
+        while self.at(","):
+            self.take(",")
+            out.append(self.take(kind="name").text)
+        if paren:
+            self.take(")")
+        if len(set(out)) != len(out):
+            raise MiraSyntaxError(f"line {self.peek().line}: the same name appears twice")
+        return out
+
+    def statement(self):
+        tok = self.peek()
+        line = tok.line
+        if tok.kind == "kw":
+            if tok.text == "let":
+                self.take("let")
+                names = self.names()
+                tref = None
+                if self.at(":"):
+                    self.take(":")
+                    tref = self.type_ref()
+                self.take("=")
+                return ("let", names, tref, self.expr(), line)
+            if tok.text == "return":
+                self.take("return")
+                vals = [self.expr()]
+                while self.at(","):
+                    self.take(",")
+                    vals.append(self.expr())
+                return ("return", vals, line)
+            if tok.text == "for":
+                self.take("for")
+                var = self.take(kind="name").text
+                self.take("in")
+                start = self.expr()
+                self.take("..")
+                stop = self.expr()
+                return ("for", var, start, stop, self.block(), line)
+            if tok.text == "if":
+                return self.if_statement()
+            if tok.text == "while":
+                self.take("while")
+                cond = self.expr()
+                return ("while", cond, self.block(), line)
+        if tok.kind == "name" and self.peek(1).text == "[":
+            name = self.take().text
+            self.take("[")
+            items = self.index_items()
+            self.take("=")
+            return ("index_assign", name, items, self.expr(), line)
+        if tok.kind == "name" or (tok.kind == "op" and tok.text == "("):
+            names = self.names()
+            self.take("=")
+            return ("assign", names, self.expr(), line)
+        raise MiraSyntaxError(f"line {line}: expected 'let' or 'return', found {tok.text or 'end of file'!r}")
+
+    def if_statement(self):
+        line = self.take("if").line
+        cond = self.expr()
+        then = self.block()
+        other = None
+        if self.at("else"):
+            self.take("else")
+            other = [self.if_statement()] if self.at("if") else self.block()
+        return ("if", cond, then, other, line)
+
+    def type_ref(self, allow_int: bool = False) -> TypeRef:
         dt = self.take(kind="name")
-        if dt.text not in ("f32", "f16"):
-            raise MiraSyntaxError(f"line {dt.line}: unsupported element type '{dt.text}' (f32, f16)")
+        if dt.text == "int":
+            if not allow_int:
+                raise MiraSyntaxError(f"line {dt.line}: 'int' is only a parameter type (a compile-time integer)")
+            return TypeRef("int", [])
+        if dt.text not in DTYPES:
+            raise MiraSyntaxError(f"line {dt.line}: unsupported element type '{dt.text}' ({', '.join(DTYPES)})")
         dims = []
         if self.at("["):
             self.take("[")
@@ -213,6 +327,15 @@ class _Parser:
         raise MiraSyntaxError(f"line {tok.line}: bad dimension {tok.text!r}")
 
     def expr(self):
+        e = self.sum()
+        if self.peek().kind == "op" and self.peek().text in COMPARE:
+            op = self.take().text
+            e = ("bin", op, e, self.sum())
+            if self.peek().kind == "op" and self.peek().text in COMPARE:
+                raise MiraSyntaxError(f"line {self.peek().line}: comparisons can't be chained; use parentheses")
+        return e
+
+    def sum(self):
         e = self.term()
         while self.at("+") or self.at("-"):
             op = self.take().text
@@ -230,7 +353,35 @@ class _Parser:
         if self.at("-"):
             self.take("-")
             return ("neg", self.unary())
-        return self.primary()
+        base = self.postfix()
+        if self.at("**"):
+            self.take("**")
+            return ("bin", "**", base, self.unary())
+        return base
+
+    def postfix(self):
+        e = self.primary()
+        while self.at("[") and self.same_line():
+            line = self.take("[").line
+            e = ("index", e, self.index_items(), line)
+        return e
+
+    def index_items(self) -> list:
+        """Subscripts up to and including the closing ']'."""
+        items = []
+        while True:
+            lo = None if self.at(":") else self.expr()
+            if self.at(":"):
+                self.take(":")
+                hi = None if (self.at(",") or self.at("]")) else self.expr()
+                items.append(("range", lo, hi))
+            else:
+                items.append(("at", lo))
+            if not self.at(","):
+                break
+            self.take(",")
+        self.take("]")
+        return items
 
     def primary(self):
         tok = self.peek()
@@ -240,8 +391,17 @@ class _Parser:
         if self.at("("):
             self.take("(")
             e = self.expr()
+            if not self.at(","):
+                self.take(")")
+                return e
+            items = [e]
+            while self.at(","):
+                self.take(",")
+                if self.at(")"):
+                    break
+                items.append(self.expr())
             self.take(")")
-            return e
+            return ("tuple", items)
         if self.at("["):       # a literal list (shapes, axes, permutations)
             self.take("[")
             items = []
@@ -255,8 +415,8 @@ class _Parser:
             self.take()
             if tok.text in ("true", "false"):
                 return ("bool", tok.text == "true")
-            if not self.at("("):
-                return ("name", tok.text)
+            if not (self.at("(") and self.same_line()):
+                return ("dtype", tok.text) if tok.text in DTYPES else ("name", tok.text)
             self.take("(")
             args, kwargs = [], {}
             while not self.at(")"):
@@ -334,9 +494,15 @@ def _unify(tref: TypeRef, dtype: str, shape: tuple, env: dict, what: str, line: 
             raise fail(f"{_show_dim(d)} = {_eval_dim(d, env, line)}, got {n}")
 
 
-_UNARY = ("relu", "sigmoid", "tanh", "gelu", "exp", "abs", "sqrt")
-_BINOP = {"+": "add", "-": "sub", "*": "mul", "/": "div"}
+_UNARY = ("relu", "sigmoid", "tanh", "gelu", "exp", "log", "abs", "sign", "sqrt")
+_BINOP = {"+": "add", "-": "sub", "*": "mul", "/": "div", "**": "pow"}
+# MIRA builtins outside this front end (runtime indexing into loop state, autodiff, ...)
+_UNSUPPORTED = ("grad", "dynamic_slice", "dynamic_update_slice", "scatter_add", "erf")
 MAX_DEPTH = 64
+
+
+class DType(str):
+    """A dtype named in an expression (the `f32` of `cast(x, f32)`)."""
 
 
 def _num(v) -> bool:
@@ -346,12 +512,47 @@ def _num(v) -> bool:
 def _describe(v) -> str:
     if isinstance(v, Value):
         return f"tensor {v.type}"
+    if isinstance(v, DType):
+        return f"dtype {v}"
+    if isinstance(v, tuple):
+        return f"{len(v)} values"
+    if isinstance(v, bool):
+        return f"boolean {str(v).lower()}"
     return "list" if isinstance(v, list) else f"number {v}"
+
+
+class Scope:
+    """Names visible in a block; assignment rebinds a name where it was defined."""
+
+    def __init__(self, parent: Optional["Scope"] = None):
+        self.vars: dict = {}
+        self.parent = parent
+
+    def owner(self, name: str) -> Optional["Scope"]:
+        s = self
+        while s is not None and name not in s.vars:
+            s = s.parent
+        return s
+
+    def lookup(self, name: str):
+        s = self.owner(name)
+        return None if s is None else s.vars[name]
+
+    def bindings(self) -> dict:
+        """The whole-number names in sight (shape symbols, int parameters, loop counters)."""
+        chain, s = [], self
+        while s is not None:
+            chain.append(s)
+            s = s.parent
+        out = {}
+        for s in reversed(chain):
+            out.update({k: v for k, v in s.vars.items() if isinstance(v, int) and not isinstance(v, bool)})
+        return out
 
 
 class Elaborator:
     """Inlines the entry function into one Graph (mira/elaborate.py:186-222 for the entry,
-    :279-330 for calls)."""
+    :279-346 for calls, :348-413 for statements)."""
 
     def __init__(self, fns: dict[str, Fn], name: str = "main"):
         self.fns = fns
@@ -365,7 +566,10 @@ class Elaborator:
         if isinstance(v, Value):
             return v
         if _num(v):
-            return self.g.const(np.array(v, dtype=np.float16 if dtype == "f16" else np.float32))
+            if dtype == "i32" and float(v) != int(v):
+                raise MiraSyntaxError(f"line {line}: the number {v} does not mix with an i32 tensor; "
+                                      "cast the tensor to f32 first")
+            return self.g.const(np.array(v, dtype=DTYPES[dtype]))
         raise MiraSyntaxError(f"line {line}: expected a tensor, got {_describe(v)}")
 
     @staticmethod
@@ -385,6 +589,18 @@ class Elaborator:
             raise MiraSyntaxError(f"line {line}: {what} takes one number or two, got {len(xs)}")
         return tuple(xs)
 
+    @staticmethod
+    def flag(v, line: int, what: str) -> bool:
+        if not isinstance(v, bool):
+            raise MiraSyntaxError(f"line {line}: {what} must be true or false")
+        return v
+
+    @staticmethod
+    def dtype(v, line: int) -> str:
+        if not isinstance(v, DType):
+            raise MiraSyntaxError(f"line {line}: expected a dtype like f32 or i32, got {_describe(v)}")
+        return str(v)
+
     # ---- functions
 
     def entry(self, fn_name: str, weights: dict, dims: dict, seed: Optional[int]) -> Graph:
@@ -395,12 +611,18 @@ class Elaborator:
         rng = np.random.default_rng(seed) if seed is not None else None
         args = []
         for p in fn.params:
+            if p.type.dtype == "int":
+                if p.name not in env:
+                    raise MiraSyntaxError(f"line {fn.line}: int parameter '{p.name}' of the entry function needs a "
+                                          f"value (dims={{'{p.name}': ...}})")
+                args.append(env[p.name])
+                continue
             for d in p.type.dims:
                 if isinstance(d, str) and d not in env:
                     raise MiraSyntaxError(f"line {fn.line}: dimension '{d}' of the entry function needs a value "
                                           f"(dims={{'{d}': ...}})")
             shape = tuple(_eval_dim(d, env, fn.line) for d in p.type.dims)
-            npdt = np.float16 if p.type.dtype == "f16" else np.float32
+            npdt = DTYPES[p.type.dtype]
             if p.const:
                 if p.name in weights:
                     arr = np.asarray(weights[p.name])
@@ -409,7 +631,8 @@ class Elaborator:
                                               f"the parameter is {p.type.dtype}{list(shape)}")
                     arr = arr.astype(npdt)
                 elif rng is not None:
-                    arr = mira_random_weight(rng, shape).astype(npdt)
+                    arr = rng.integers(0, 8, shape).astype(npdt) if p.type.dtype == "i32" else \
+                        mira_random_weight(rng, shape, npdt)
                 else:
                     raise MiraSyntaxError(f"line {fn.line}: no value for const parameter '{p.name}' "
                                           "(pass weights, or a seed for random ones)")
@@ -420,10 +643,10 @@ class Elaborator:
         if unknown:
             raise MiraSyntaxError(f"weights given for unknown const parameters: {', '.join(sorted(unknown))}")
         out = self.call_function(fn, args, fn.line, preset=env)
-        self.g.outputs = [out]
+        self.g.outputs = list(out) if isinstance(out, tuple) else [out]
         return self.g
 
-    def call_function(self, fn: Fn, args: list, line: int, preset: Optional[dict] = None) -> Value:
+    def call_function(self, fn: Fn, args: list, line: int, preset: Optional[dict] = None):
         if fn.name in self.stack:
             raise MiraSyntaxError(f"line {line}: recursive call to '{fn.name}'")
         if len(self.stack) >= MAX_DEPTH:
@@ -431,49 +654,162 @@ class Elaborator:
         if len(args) != len(fn.params):
             raise MiraSyntaxError(f"line {line}: '{fn.name}' takes {len(fn.params)} arguments, got {len(args)}")
         env = dict(preset or {})
-        scope: dict = {}
+        tensors: dict = {}
+        for p, a in zip(fn.params, args):          # int parameters first: types may use them
+            if p.type.dtype == "int":
+                env[p.name] = self.int_(a, line, f"argument '{p.name}' of '{fn.name}'")
         for p, a in zip(fn.params, args):
+            if p.type.dtype == "int":
+                continue
             if p.const and self.stack:
                 raise MiraSyntaxError(f"line {fn.line}: 'const' is only allowed on the entry function's parameters")
-            scope[p.name] = a = self.tensor(a, line)
+            tensors[p.name] = a = self.tensor(a, line, p.type.dtype)
             _unify(p.type, a.type.dtype, a.type.shape, env, f"argument '{p.name}' of '{fn.name}'", line, False)
         for p in fn.params:
-            a = scope[p.name]
-            _unify(p.type, a.type.dtype, a.type.shape, env, f"argument '{p.name}' of '{fn.name}'", line, True)
+            if p.name in tensors:
+                a = tensors[p.name]
+                _unify(p.type, a.type.dtype, a.type.shape, env, f"argument '{p.name}' of '{fn.name}'", line, True)
+        scope = Scope()
+        scope.vars.update(env)              # shape symbols are plain numbers inside the body
+        for name, v in tensors.items():
+            if name in env:
+                raise MiraSyntaxError(f"line {fn.line}: parameter '{name}' has the name of a shape dimension")
+            scope.vars[name] = v
         self.stack.append(fn.name)
-        scope = {**env, **scope}            # shape symbols are plain numbers inside the body
-        for st in fn.body:
-            if st[0] == "let":
-                scope[st[1]] = self.expr(st[2], scope, st[3])
-                continue
-            out = self.tensor(self.expr(st[1], scope, st[2]), st[2])
-            _unify(fn.ret, out.type.dtype, out.type.shape, env, f"the result of '{fn.name}'", st[2], True)
+        try:
+            result = self.block(fn.body, scope, nested=False)
+            if result is None:
+                raise MiraSyntaxError(f"line {fn.line}: '{fn.name}' has no return")
+            value, rline = result
+            values = list(value) if isinstance(value, tuple) else [value]
+            if len(values) != len(fn.rets):
+                raise MiraSyntaxError(f"line {rline}: '{fn.name}' returns {len(values)} value(s), its signature "
+                                      f"declares {len(fn.rets)}")
+            out = []
+            for v, tref in zip(values, fn.rets):
+                v = self.tensor(v, rline, tref.dtype)
+                _unify(tref, v.type.dtype, v.type.shape, env, f"the result of '{fn.name}'", rline, True)
+                out.append(v)
+            return tuple(out) if len(fn.rets) > 1 else out[0]
+        finally:
             self.stack.pop()
-            return out
-        raise MiraSyntaxError(f"line {fn.line}: '{fn.name}' has no return")
+
+    # ---- statements
+
+    def block(self, body: list, scope: Scope, nested: bool) -> Optional[tuple]:
+        for i, st in enumerate(body):
+            kind, line = st[0], st[-1]
+            if kind == "let":
+                self.let(st, scope)
+            elif kind == "assign":
+                self.assign(st, scope)
+            elif kind == "for":
+                _, var, start, stop, inner, _ = st
+                lo = self.int_(self.expr(start, scope, line), line, "loop bound")
+                hi = self.int_(self.expr(stop, scope, line), line, "loop bound")
+                if hi - lo > MAX_UNROLL:
+                    raise MiraSyntaxError(f"line {line}: loop of {hi - lo} iterations; at most {MAX_UNROLL} unroll")
+                for it in range(lo, hi):
+                    s = Scope(scope)
+                    s.vars[var] = it
+                    self.block(inner, s, nested=True)
+            elif kind == "if":
+                _, cond, then, other, _ = st
+                c = self.expr(cond, scope, line)
+                if isinstance(c, Value):
+                    raise MiraSyntaxError(f"line {line}: 'if' on a runtime tensor is control flow, which this "
+                                          "front end does not build (MIRA's W8A8 rewrite rejects it)")
+                if not (isinstance(c, bool) or _num(c)):
+                    raise MiraSyntaxError(f"line {line}: an 'if' condition must be a number or a boolean, "
+                                          f"got {_describe(c)}")
+                taken = then if c else other
+                if taken:
+                    self.block(taken, Scope(scope), nested=True)
+            elif kind == "while":
+                raise MiraSyntaxError(f"line {line}: 'while' is control flow, which this front end does not "
+                                      "build (MIRA's W8A8 rewrite rejects it)")
+            elif kind == "index_assign":
+                raise MiraSyntaxError(f"line {line}: indexed assignment ('{st[1]}[...] = ...') is not supported by "
+                                      "this front end")
+            else:   # return
+                if nested:
+                    raise MiraSyntaxError(f"line {line}: 'return' must be the last statement of a function, "
+                                          "not inside for / if")
+                if i != len(body) - 1:
+                    raise MiraSyntaxError(f"line {body[i + 1][-1]}: unreachable code after 'return'")
+                vals = [self.expr(e, scope, line) for e in st[1]]
+                return (vals[0] if len(vals) == 1 else tuple(vals)), line
+        return None
+
+    @staticmethod
+    def destructure(names: list, v, line: int) -> list:
+        if len(names) == 1:
+            if isinstance(v, tuple):
+                raise MiraSyntaxError(f"line {line}: this gives {len(v)} values; unpack them like 'let a, b = ...'")
+            return [v]
+        if not isinstance(v, tuple) or len(v) != len(names):
+            raise MiraSyntaxError(f"line {line}: cannot unpack {_describe(v)} into {len(names)} names")
+        return list(v)
+
+    def let(self, st, scope: Scope) -> None:
+        _, names, tref, e, line = st
+        for n in names:
+            if n in scope.vars:
+                raise MiraSyntaxError(f"line {line}: '{n}' is already defined in this scope; "
+                                      f"use '{n} = ...' to reassign")
+        v = self.expr(e, scope, line)
+        if tref is not None:
+            v = self.tensor(v, line, tref.dtype)
+            _unify(tref, v.type.dtype, v.type.shape, dict(scope.bindings()), f"'{names[0]}'", line, True)
+        for n, x in zip(names, self.destructure(names, v, line)):
+            scope.vars[n] = x
+
+    def assign(self, st, scope: Scope) -> None:
+        _, names, e, line = st
+        values = self.destructure(names, self.expr(e, scope, line), line)
+        for n, v in zip(names, values):
+            owner = scope.owner(n)
+            if owner is None:
+                raise MiraSyntaxError(f"line {line}: assignment to undefined variable '{n}'; declare it with 'let'")
+            old = owner.vars[n]
+            if isinstance(old, Value):
+                v = self.tensor(v, line, old.type.dtype)
+                if v.type != old.type:
+                    raise MiraSyntaxError(f"line {line}: '{n}' has type {old.type}; cannot assign a {v.type}")
+            elif isinstance(v, (Value, tuple)):
+                raise MiraSyntaxError(f"line {line}: '{n}' is a compile-time {_describe(old)}; "
+                                      f"cannot assign a {_describe(v)}")
+            owner.vars[n] = v
 
     # ---- expressions
 
-    def expr(self, e, scope: dict, line: int):
+    def expr(self, e, scope: Scope, line: int):
         kind = e[0]
         if kind in ("num", "bool"):
             return e[1]
+        if kind == "dtype":
+            return DType(e[1])
         if kind == "list":
             return [self.expr(x, scope, line) for x in e[1]]
+        if kind == "tuple":
+            return tuple(self.expr(x, scope, line) for x in e[1])
         if kind == "name":
-            if e[1] not in scope:
+            v = scope.lookup(e[1])
+            if v is None:
                 what = "a function; call it" if e[1] in self.fns or e[1] in BUILTINS else "undefined"
                 raise MiraSyntaxError(f"line {line}: '{e[1]}' is {what}")
-            return scope[e[1]]
+            return v
         if kind == "neg":
             v = self.expr(e[1], scope, line)
             if isinstance(v, Value):
-                return self.g.op("neg", [v])
+                return self.op("neg", [v], {}, line)
             if _num(v):
                 return -v
             raise MiraSyntaxError(f"line {line}: cannot negate a {_describe(v)}")
         if kind == "bin":
             return self.binary(e[1], self.expr(e[2], scope, line), self.expr(e[3], scope, line), line)
+        if kind == "index":
+            return self.index(e, scope)
         _, name, args, kwargs, line = e
         vals = [self.expr(a, scope, line) for a in args]
         kw = {k: self.expr(v, scope, line) for k, v in kwargs.items()}
@@ -481,12 +817,18 @@ class Elaborator:
             if kw:
                 raise MiraSyntaxError(f"line {line}: '{name}' takes no keyword arguments")
             return self.call_function(self.fns[name], vals, line)
+        if name in _UNSUPPORTED:
+            raise MiraSyntaxError(f"line {line}: {name}() is not supported by this front end")
         if name not in BUILTINS:
             raise MiraSyntaxError(f"line {line}: unknown function '{name}'")
         params, handler = BUILTINS[name]
         return handler(self, _bind_args(name, params, vals, kw, line), line)
 
     def binary(self, op: str, a, b, line: int):
+        if op in COMPARE and not isinstance(a, Value) and not isinstance(b, Value):
+            if not all(_num(x) or isinstance(x, bool) for x in (a, b)):
+                raise MiraSyntaxError(f"line {line}: cannot compare {_describe(a)} and {_describe(b)}")
+            return {"<": a < b, "<=": a <= b, ">": a > b, ">=": a >= b, "==": a == b, "!=": a != b}[op]
         if _num(a) and _num(b):
             if op == "@":
                 raise MiraSyntaxError(f"line {line}: '@' needs tensor operands")
@@ -494,15 +836,69 @@ class Elaborator:
                 if b == 0:
                     raise MiraSyntaxError(f"line {line}: division by zero")
                 return a // b if isinstance(a, int) and isinstance(b, int) and a % b == 0 else a / b
-            return {"+": a + b, "-": a - b, "*": a * b}[op]
+            return {"+": a + b, "-": a - b, "*": a * b, "**": a ** b}[op]
         if not isinstance(a, Value) and not isinstance(b, Value):
             raise MiraSyntaxError(f"line {line}: cannot apply '{op}' to {_describe(a)} and {_describe(b)}")
         dtype = a.type.dtype if isinstance(a, Value) else b.type.dtype
         a, b = self.tensor(a, line, dtype), self.tensor(b, line, dtype)
-        try:
-            return self.g.op("matmul" if op == "@" else _BINOP[op], [a, b])
-        except ValueError as err:
-            raise MiraSyntaxError(f"line {line}: {err}") from None
+        if op == "@":
+            return self.op("matmul", [a, b], {}, line)
+        if op in COMPARE:
+            if op == "!=":
+                eq = self.op("equal", [a, b], {}, line)
+                return self.op("sub", [self.tensor(1, line, dtype), eq], {}, line)
+            kind = {"<": "greater", "<=": "greater_equal", ">": "greater", ">=": "greater_equal",
+                    "==": "equal"}[op]
+            return self.op(kind, [b, a] if op in ("<", "<=") else [a, b], {}, line)
+        return self.op(_BINOP[op], [a, b], {}, line)
+
+    def index(self, e, scope: Scope) -> Value:
+        _, base, items, line = e
+        x = self.expr(base, scope, line)
+        if not isinstance(x, Value):
+            raise MiraSyntaxError(f"line {line}: cannot index a {_describe(x)}")
+        shape = x.type.shape
+        if len(items) > len(shape):
+            raise MiraSyntaxError(f"line {line}: {len(items)} subscripts for a rank-{len(shape)} tensor")
+        subs = []         # per axis: ("int", k) | ("range", lo, hi) | ("tensor", value)
+        for axis, d in enumerate(shape):
+            it = items[axis] if axis < len(items) else ("range", None, None)
+            if it[0] == "range":
+                bounds = []
+                for b, default in ((it[1], 0), (it[2], d)):
+                    v = default if b is None else self.expr(b, scope, line)
+                    if isinstance(v, Value):
+                        raise MiraSyntaxError(f"line {line}: slice bounds must be compile-time numbers")
+                    v = self.int_(v, line, "slice bound")
+                    bounds.append(max(0, min(d, v + d if v < 0 else v)))
+                if bounds[1] <= bounds[0]:
+                    raise MiraSyntaxError(f"line {line}: empty slice {bounds[0]}:{bounds[1]} of an axis of size {d}")
+                subs.append(("range", bounds[0], bounds[1]))
+                continue
+            v = self.expr(it[1], scope, line)
+            if isinstance(v, Value):
+                if v.type.dtype != "i32":
+                    raise MiraSyntaxError(f"line {line}: tensor subscripts must be i32, got {v.type}")
+                subs.append(("tensor", v))
+                continue
+            k = self.int_(v, line, "index")
+            if not -d <= k < d:
+                raise MiraSyntaxError(f"line {line}: index {k} is out of range for an axis of size {d}")
+            subs.append(("int", k % d))
+        begin = tuple(s[1] if s[0] != "tensor" else 0 for s in subs)
+        size = tuple(1 if s[0] == "int" else s[2] - s[1] if s[0] == "range" else d for s, d in zip(subs, shape))
+        if size != shape:
+            x = self.op("slice", [x], {"begin": begin, "size": size}, line)
+        kept = [i for i, s in enumerate(subs) if s[0] != "int"]
+        if len(kept) != len(subs):
+            x = self.op("reshape", [x], {"shape": tuple(size[i] for i in kept)}, line)
+        shift = 0
+        for axis, i in enumerate(kept):
+            if subs[i][0] == "tensor":
+                idx = subs[i][1]
+                x = self.op("gather", [x, idx], {"axis": axis + shift}, line)
+                shift += idx.type.rank - 1
+        return x
 
     def op(self, kind: str, ins: list, attrs: dict, line: int) -> Value:
         try:
@@ -513,7 +909,7 @@ class Elaborator:
 
 # ---------------------------------------------------------------- builtins
 # (name, default) parameter lists and handlers, as MIRA's builtin table
-# (mira/elaborate.py:1081-1111) declares them for these operators.
+# (mira/elaborate.py:1070-1111) declares them for these operators.
 
 _REQUIRED = object()
 
@@ -537,7 +933,17 @@ def _bind_args(name: str, params: list, args: list, kw: dict, line: int) -> dict
 
 
 def _unary(kind):
-    return [("x", _REQUIRED)], lambda el, a, line: el.op(kind, [el.tensor(a["x"], line)], {}, line)
+    def h(el, a, line):
+        x = a["x"]
+        if _num(x):         # compile-time arithmetic, as in / sqrt(D)
+            from harness.hosteval import UNARY
+            with np.errstate(all="raise"):
+                try:
+                    return float(UNARY[kind](np.float64(x)))
+                except FloatingPointError:
+                    raise MiraSyntaxError(f"line {line}: {kind}({x}) is undefined") from None
+        return el.op(kind, [el.tensor(x, line)], {}, line)
+    return [("x", _REQUIRED)], h
 
 
 def _binary_fn(kind):
@@ -550,12 +956,13 @@ def _binary_fn(kind):
     return [("a", _REQUIRED), ("b", _REQUIRED)], h
 
 
-def _mean(el, a, line):
-    x = el.tensor(a["x"], line)
-    axes = list(range(x.type.rank)) if a["axis"] is None else el.ints(a["axis"], line, "axis")
-    if not isinstance(a["keepdims"], bool):
-        raise MiraSyntaxError(f"line {line}: keepdims must be true or false")
-    return el.op("reduce_mean", [x], {"axes": tuple(axes), "keepdims": a["keepdims"]}, line)
+def _reduce(kind):
+    def h(el, a, line):
+        x = el.tensor(a["x"], line)
+        axes = list(range(x.type.rank)) if a["axis"] is None else el.ints(a["axis"], line, "axis")
+        keep = el.flag(a["keepdims"], line, "keepdims")
+        return el.op(kind, [x], {"axes": tuple(axes), "keepdims": keep}, line)
+    return [("x", _REQUIRED), ("axis", None), ("keepdims", False)], h
 
 
 def _transpose(el, a, line):
@@ -636,13 +1043,108 @@ def _matmul(el, a, line):
     return el.op("matmul", [el.tensor(a["a"], line), el.tensor(a["b"], line)], {}, line)
 
 
+def _layernorm(el, a, line):
+    eps = a["eps"]
+    if not _num(eps):
+        raise MiraSyntaxError(f"line {line}: layernorm eps must be a number")
+    ins = [el.tensor(a[k], line) for k in ("x", "gamma", "beta")]
+    return el.op("layernorm", ins, {"eps": float(eps)}, line)
+
+
+def _concat(el, a, line):
+    xs = a["xs"]
+    if not isinstance(xs, list) or not xs:
+        raise MiraSyntaxError(f"line {line}: concat() takes a non-empty list of tensors")
+    return el.op("concat", [el.tensor(v, line) for v in xs], {"axis": el.int_(a["axis"], line, "axis")}, line)
+
+
+def _cast(el, a, line):
+    x = el.tensor(a["x"], line)
+    dt = el.dtype(a["dtype"], line)
+    return x if x.type.dtype == dt else el.op("cast", [x], {"dtype": dt}, line)
+
+
+def _slice(el, a, line):
+    return el.op("slice", [el.tensor(a["x"], line)], {"begin": tuple(el.ints(a["begin"], line, "begin")),
+                                                     "size": tuple(el.ints(a["size"], line, "size"))}, line)
+
+
+def _pad(el, a, line):
+    pads = a["pads"]
+    if not isinstance(pads, list) or not all(isinstance(p, list) and len(p) == 2 for p in pads):
+        raise MiraSyntaxError(f"line {line}: pad() takes pads like [[1, 1], [0, 2]], one pair per axis")
+    attrs = {"pads": tuple((el.int_(p[0], line, "pad"), el.int_(p[1], line, "pad")) for p in pads)}
+    if a["value"] != 0:
+        if not _num(a["value"]):
+            raise MiraSyntaxError(f"line {line}: pad value must be a number")
+        attrs["value"] = float(a["value"])
+    return el.op("pad", [el.tensor(a["x"], line)], attrs, line)
+
+
+def _broadcast_fn(el, a, line):
+    return el.op("broadcast", [el.tensor(a["x"], line)], {"shape": tuple(el.ints(a["shape"], line, "shape"))}, line)
+
+
+def _gather(el, a, line):
+    return el.op("gather", [el.tensor(a["x"], line), el.tensor(a["indices"], line, "i32")],
+                 {"axis": el.int_(a["axis"], line, "axis")}, line)
+
+
+def _where(el, a, line):
+    c, x, y = a["cond"], a["a"], a["b"]
+    if not isinstance(c, Value):
+        raise MiraSyntaxError(f"line {line}: where() needs a tensor condition; use if for compile-time choices")
+    vals = [v for v in (x, y) if isinstance(v, Value)]
+    dt = vals[0].type.dtype if vals else "f32"
+    return el.op("where", [c, el.tensor(x, line, dt), el.tensor(y, line, dt)], {}, line)
+
+
+def _size(el, a, line):
+    x = el.tensor(a["x"], line)
+    ax = el.int_(a["axis"], line, "axis")
+    if not -x.type.rank <= ax < x.type.rank:
+        raise MiraSyntaxError(f"line {line}: axis {ax} out of range for {x.type}")
+    return x.type.shape[ax]
+
+
+def _axis_op(kind):
+    return ([("x", _REQUIRED), ("axis", -1)],
+            lambda el, a, line: el.op(kind, [el.tensor(a["x"], line)], {"axis": el.int_(a["axis"], line, "axis")},
+                                      line))
+
+
+def _arg(kind):
+    def h(el, a, line):
+        attrs = {"axis": el.int_(a["axis"], line, "axis"), "keepdims": el.flag(a["keepdims"], line, "keepdims")}
+        return el.op(kind, [el.tensor(a["x"], line)], attrs, line)
+    return [("x", _REQUIRED), ("axis", -1), ("keepdims", False)], h
+
+
+def _filled(value):
+    def h(el, a, line):
+        shape = el.ints(a["shape"], line, "shape")
+        v = a["value"] if value is None else value
+        if not _num(v):
+            raise MiraSyntaxError(f"line {line}: the fill value must be a number")
+        return el.g.const(np.full(shape, v, dtype=DTYPES[el.dtype(a["dtype"], line)]))
+    return h
+
+
+def _arange(el, a, line):
+    start = el.int_(a["start"], line, "start")
+    lo, hi = (0, start) if a["stop"] is None else (start, el.int_(a["stop"], line, "stop"))
+    return el.g.const(np.arange(lo, hi, dtype=DTYPES[el.dtype(a["dtype"], line)]))
+
+
 BUILTINS = {
     **{k: _unary(k) for k in _UNARY},
     "maximum": _binary_fn("maximum"),
     "minimum": _binary_fn("minimum"),
     "matmul": ([("a", _REQUIRED), ("b", _REQUIRED)], _matmul),
     "softmax": ([("x", _REQUIRED), ("axis", -1)], _softmax),
-    "mean": ([("x", _REQUIRED), ("axis", None), ("keepdims", False)], _mean),
+    "sum": _reduce("reduce_sum"),
+    "mean": _reduce("reduce_mean"),
+    "max": _reduce("reduce_max"),
     "transpose": ([("x", _REQUIRED), ("perm", None)], _transpose),
     "reshape": ([("x", _REQUIRED), ("shape", _REQUIRED)], _reshape),
     "flatten": ([("x", _REQUIRED), ("axis", 1)], _flatten),
@@ -650,13 +1152,31 @@ BUILTINS = {
                _conv2d),
     "maxpool2d": ([("x", _REQUIRED), ("size", 2), ("stride", None), ("padding", 0)], _maxpool),
     "avgpool2d": ([("x", _REQUIRED), ("size", 2), ("stride", None), ("padding", 0)], _avgpool),
+    "layernorm": ([("x", _REQUIRED), ("gamma", _REQUIRED), ("beta", _REQUIRED), ("eps", 1e-5)], _layernorm),
+    "concat": ([("xs", _REQUIRED), ("axis", 0)], _concat),
+    "cast": ([("x", _REQUIRED), ("dtype", _REQUIRED)], _cast),
+    "slice": ([("x", _REQUIRED), ("begin", _REQUIRED), ("size", _REQUIRED)], _slice),
+    "pad": ([("x", _REQUIRED), ("pads", _REQUIRED), ("value", 0)], _pad),
+    "broadcast": ([("x", _REQUIRED), ("shape", _REQUIRED)], _broadcast_fn),
+    "gather": ([("x", _REQUIRED), ("indices", _REQUIRED), ("axis", 0)], _gather),
+    "where": ([("cond", _REQUIRED), ("a", _REQUIRED), ("b", _REQUIRED)], _where),
+    "size": ([("x", _REQUIRED), ("axis", _REQUIRED)], _size),
+    "zeros": ([("shape", _REQUIRED), ("dtype", DType("f32"))], _filled(0)),
+    "ones": ([("shape", _REQUIRED), ("dtype", DType("f32"))], _filled(1)),
+    "full": ([("shape", _REQUIRED), ("value", _REQUIRED), ("dtype", DType("f32"))], _filled(None)),
+    "arange": ([("start", _REQUIRED), ("stop", None), ("dtype", DType("i32"))], _arange),
+    "sort": _axis_op("sort"),
+    "cumprod": _axis_op("cumprod"),
+    "argmax": _arg("argmax"),
+    "argmin": _arg("argmin"),
 }
 
 
 def elaborate(src: str, entry: str = "main", weights: Optional[dict] = None, dims: Optional[dict] = None,
               seed: Optional[int] = 0, name: Optional[str] = None) -> Graph:
-    """A .mira program as a harness Graph: the entry function inlined, its shape symbols from
-    `dims`, its const parameters from `weights` or drawn from `seed` (None: all must be given)."""
+    """A .mira program as a harness Graph: the entry function inlined, its shape symbols and
+    int parameters from `dims`, its const parameters from `weights` or drawn from `seed`
+    (None: all must be given)."""
     g = Elaborator(parse(src), name or entry).entry(entry, weights or {}, dims or {}, seed)
     g.check()
     return g

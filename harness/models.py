@@ -28,16 +28,16 @@ def _normal(rng, shape, std):
     return (rng.standard_normal(shape) * std).astype(np.float32)
 
 
-def mira_random_weight(rng, shape) -> np.ndarray:
+def mira_random_weight(rng, shape, dtype=np.float32) -> np.ndarray:
     """The seeded weights MIRA's elaborator gives a const parameter (mira/elaborate.py:1114-1123),
     drawn in parameter order from one generator: rank 1 -> 1 + 0.1 N; rank 4 -> N / sqrt(C*KH*KW);
-    any other rank -> N / sqrt(shape[-2])."""
+    any other rank -> N / sqrt(shape[-2]); each draw rounded once, from f64 to `dtype`."""
     if len(shape) == 0:
-        return np.array(rng.standard_normal(), dtype=np.float32)
+        return np.array(rng.standard_normal(), dtype=dtype)
     if len(shape) == 1:
-        return (1.0 + 0.1 * rng.standard_normal(shape)).astype(np.float32)
+        return (1.0 + 0.1 * rng.standard_normal(shape)).astype(dtype)
     fan_in = int(np.prod(shape[1:])) if len(shape) == 4 else shape[-2]
-    return (rng.standard_normal(shape) / np.sqrt(fan_in)).astype(np.float32)
+    return (rng.standard_normal(shape) / np.sqrt(fan_in)).astype(dtype)
 
 
 # ---------------------------------------------------------------- MLPs

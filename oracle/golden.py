@@ -244,6 +244,18 @@ def dequantize(a: dict) -> np.ndarray:
 
 # ---------------------------------------------------------------- op dispatch (mira/ops.py:704-709)
 
+# ---------------------------------------------------------------- selection (mira/ops.py:426-458)
+
+def slice_(xs: list, a: dict) -> np.ndarray:
+    """mira/ops.py:457-458: the box [begin, begin + size) of every axis, copied."""
+    return xs[0][tuple(slice(b, b + n) for b, n in zip(a["begin"], a["size"]))].copy()
+
+
+def where(xs: list, a: dict) -> np.ndarray:
+    """mira/ops.py:432-433: a where cond is non-zero, else b, in a's dtype (broadcast)."""
+    return np.where(xs[0] != 0, xs[1], xs[2]).astype(xs[1].dtype)
+
+
 def evaluate(kind: str, xs: list, a: dict) -> np.ndarray:
     """mira/ops.py:708-709 for the ops the W8A8 configs use."""
     if kind == "const":
@@ -283,6 +295,19 @@ def evaluate(kind: str, xs: list, a: dict) -> np.ndarray:
         return np.take(table, idx, axis=a["axis"])
     if kind == "concat":
         return np.concatenate(xs, axis=a["axis"])                         # mira/ops.py:402
+    if kind == "slice":
+        return slice_(xs, a)
+    if kind == "where":
+        return where(xs, a)
+    if kind == "broadcast":
+        return np.broadcast_to(xs[0], a["shape"]).copy()                  # mira/ops.py:443
+    if kind == "sort":
+        return np.sort(xs[0], axis=a["axis"])                             # mira/ops.py:419
+    if kind == "cumprod":
+        return np.cumprod(f32(xs[0]), axis=a["axis"]).astype(xs[0].dtype)  # mira/ops.py:420-421
+    if kind in ("argmax", "argmin"):                                      # mira/ops.py:527-530
+        f = np.argmax if kind == "argmax" else np.argmin
+        return np.asarray(f(xs[0], axis=a["axis"], keepdims=a["keepdims"])).astype(np.int32)
     raise NotImplementedError(f"oracle has no semantics for '{kind}'")
 
 

@@ -54,7 +54,7 @@ def epilogue(steps=(), scale=None, out_f32=None, ldo=0, out_i8=None, ldq=0, xs=1
 def oracle_env(g, feeds: dict) -> dict:
     """Every value of a graph evaluated by the oracle, keyed by ir.Value."""
     from oracle import golden as G
-    env = {v: np.asarray(feeds[v.name]).astype(np.float32) for v in g.inputs}
+    env = {v: np.asarray(feeds[v.name]).astype(v.type.np_dtype) for v in g.inputs}
     for op in g.ops:
         env[op.result] = G.evaluate(op.kind, [env[x] for x in op.inputs], op.attrs)
     return env

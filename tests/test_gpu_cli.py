@@ -54,3 +54,33 @@ def test_cli_run_weight_only(capsys):
     assert cli.main(["run", os.path.join(PROGRAMS, "affine_mlp.mira"), "-t", "rocm", "--dim", "B=8",
                      "--quantize", "int8", "--precision", "none", "--check"]) == 0
     assert "PASS" in capsys.readouterr().out
+
+
+# ---------------------------------------------------------------- the rest of MIRA's language on rocm
+
+LANG = {"encoder_block": {"S": 16, "E": 32, "h": 4}, "residual_loop": {"B": 8, "D": 16, "n": 5},
+        "char_lm": {"B": 2, "T": 8, "V": 13, "D": 16, "F": 32, "L": 2}, "selection": {"R": 6, "C": 5}}
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.mark.parametrize("precision", ["auto", None])
+@pytest.mark.parametrize("name", sorted(LANG))
+def test_language_programs_on_rocm(name, precision):
+    """Programs beyond the CNN / MLP subset (attention heads, unrolled loops, token gathers,
+    masks, losses, selection builtins), W8A8-quantized on MIRA's calibration feeds: their
+    q-matmuls (and layernorms) run on rocm, the rest on the host, and every result equals
+    the oracle's evaluation of the same lowered graph and MIRA's own result bit for bit."""
+    z = np.load(os.path.join(GOLDEN, f"mira_lang_{name}.npz"))
+    pick = lambda pre: {k.split(":", 1)[1]: z[k] for k in z.files if k.startswith(pre)}   # noqa: E731
+    feed, calib = pick("feed:"), [pick("calib0:"), pick("calib1:")]
+    prog = cli.compile_file(os.path.join(PROGRAMS, name + ".mira"), "rocm", dims=LANG[name], precision=precision,
+                            quantize="w8a8", calibration=calib)
+    on_rocm = [op.kind for seg in prog.segments if seg.device == "rocm" for op in seg.graph.compute_ops()]
+    assert "qmatmul" in on_rocm, on_rocm
+    print(f"{name} precision={precision} rocm ops {len(on_rocm)}", flush=True)
+    got = prog.run(dict(feed))
+    env = oracle_env(prog.graph, dict(feed))
+    tag = "w8a8_f16" if precision == "auto" else "w8a8_f32"
+    for k, v in enumerate(prog.graph.outputs):
+        assert bits_equal(got[k], env[v]), f"output {k} vs the oracle"
+        assert bits_equal(got[k], z[f"out:{tag}:{k}"]), f"output {k} vs MIRA"

@@ -290,3 +290,151 @@ def test_cli_onnx_model(tmp_path, capsys):
     assert "symbolic" in capsys.readouterr().err
     assert cli.main(["check", str(path), "--shape", "x=5,6"]) == 0
     assert "x: f32[5, 6]" in capsys.readouterr().out
+
+
+# ---------------------------------------------------------------- the rest of the language against MIRA
+
+LANG = {"encoder_block": {"S": 16, "E": 32, "h": 4}, "residual_loop": {"B": 8, "D": 16, "n": 5},
+        "char_lm": {"B": 2, "T": 8, "V": 13, "D": 16, "F": 32, "L": 2}, "selection": {"R": 6, "C": 5}}
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _lang_fixture(name: str):
+    z = np.load(os.path.join(GOLDEN, f"mira_lang_{name}.npz"))
+    doc = __import__("json").loads(str(z["doc"]))
+    pick = lambda pre: {k.split(":", 1)[1]: z[k] for k in z.files if k.startswith(pre)}   # noqa: E731
+    return doc, pick("feed:"), [pick("calib0:"), pick("calib1:")], z
+
+
+def _norm_ours(v):
+    if isinstance(v, np.ndarray):
+        return _sha(v)
+    if isinstance(v, (np.floating, np.integer)):
+        return v.item()
+    if isinstance(v, (tuple, list)):
+        return type(v)(_norm_ours(x) for x in v)
+    return v
+
+
+def _norm_mira(v):
+    if isinstance(v, dict):
+        if "tuple" in v:
+            return tuple(_norm_mira(x) for x in v["tuple"])
+        if "sha256" in v:
+            return v["sha256"]
+        if "float" in v:
+            return float(v["float"])
+    if isinstance(v, list):
+        return [_norm_mira(x) for x in v]
+    return v
+
+
+def _graph_ours(g) -> tuple:
+    ids = {v: ("input", v.name, v.type.dtype, tuple(v.type.shape)) for v in g.inputs}
+    ops = []
+    for i, op in enumerate(g.ops):
+        ids[op.result] = i
+        ops.append((op.kind, tuple(ids[x] for x in op.inputs), tuple(op.result.type.shape), op.result.type.dtype,
+                    {k: _norm_ours(v) for k, v in op.attrs.items()}))
+    return ops, [ids[v] for v in g.outputs]
+
+
+def _graph_mira(doc) -> tuple:
+    ids = {i["id"]: ("input", i["name"], i["dtype"], tuple(i["shape"])) for i in doc["inputs"]}
+    ops = []
+    for i, op in enumerate(doc["ops"]):
+        ids[op["result"]["id"]] = i
+        ops.append((op["kind"], tuple(ids[x] for x in op["inputs"]), tuple(op["result"]["shape"]),
+                    op["result"]["dtype"], {k: _norm_mira(v) for k, v in op["attrs"].items()}))
+    return ops, [ids[v] for v in doc["outputs"]]
+
+
+def _same_graph(ours, theirs):
+    (a, ao), (b, bo) = _graph_ours(ours), _graph_mira(theirs)
+    assert len(a) == len(b), f"{len(a)} ops vs MIRA's {len(b)}"
+    for i, (x, y) in enumerate(zip(a, b)):
+        assert x == y, f"op {i}: {x} != MIRA's {y}"
+    assert ao == bo
+
+
+@pytest.mark.parametrize("name", sorted(LANG))
+def test_language_elaborates_like_mira(name):
+    """Compile-time ints and computed dims, for / if unrolled at elaboration, rebinding,
+    comparisons (a < b as greater(b, a), != as 1 - equal), **, slices and integer subscripts
+    (slice + reshape), i32 subscripts (gather), tuple returns and the selection builtins: the
+    elaborated graph equals the one MIRA's elaborator builds from the same file, op for op,
+    with every seeded constant byte for byte."""
+    doc, *_ = _lang_fixture(name)
+    g = ML.elaborate(_read(os.path.join(PROGRAMS, name + ".mira")), dims=LANG[name])
+    _same_graph(g, doc["elaborated"])
+
+
+@pytest.mark.parametrize("precision", [None, "f16"])
+@pytest.mark.parametrize("name", sorted(LANG))
+def test_language_optimizes_and_runs_like_mira(name, precision):
+    """MIRA's optimizer (f16 lowering with integer casts kept, constant folding of the
+    index arithmetic and masks, simplify, CSE of the per-layer masks, DCE, epilogue
+    fusion) gives the same graph here, and both the host fallback and the oracle reproduce
+    MIRA's results bit for bit on the same feed."""
+    doc, feed, _, z = _lang_fixture(name)
+    tag = "f16" if precision else "f32"
+    prog = cli.compile_file(os.path.join(PROGRAMS, name + ".mira"), "cpu", dims=LANG[name], precision=precision)
+    _same_graph(prog.graph, doc[tag])
+    outs = prog.run(dict(feed))
+    oracle_outs = G.run_graph(prog.graph, dict(feed))
+    for k, (o, r) in enumerate(zip(outs, oracle_outs)):
+        want = z[f"out:{tag}:{k}"]
+        assert o.dtype == want.dtype and bits_equal(o, want), f"output {k} (host)"
+        assert bits_equal(np.asarray(r), want), f"output {k} (oracle)"
+
+
+@pytest.mark.parametrize("precision", [None, "f16"])
+@pytest.mark.parametrize("name", sorted(LANG))
+def test_language_w8a8_like_mira(name, precision):
+    """The W8A8 rewrite of these programs on MIRA's calibration feeds: every q-op's q bytes,
+    w_scale and x_scale, and every other op, equal MIRA's; the oracle's evaluation of the
+    rewritten graph is MIRA's result bit for bit."""
+    doc, feed, calib, z = _lang_fixture(name)
+    tag = "w8a8_f16" if precision else "w8a8_f32"
+    g = cli.load_graph(os.path.join(PROGRAMS, name + ".mira"), "main", None, LANG[name], 0, None)
+    LW.prepare(g, precision=precision)
+    LW.w8a8(g, calib)
+    _same_graph(g, doc[tag])
+    for k, r in enumerate(G.run_graph(g, dict(feed))):
+        assert bits_equal(np.asarray(r), z[f"out:{tag}:{k}"]), f"output {k}"
+
+
+LANG_ERRORS = [
+    ("fn main(x: f32[2]) -> f32[2] { let y = x\n let y = x\n return y }", {}, "'y' is already defined"),
+    ("fn main(x: f32[2]) -> f32[2] { z = x\n return x }", {}, "undefined variable 'z'"),
+    ("fn main(x: f32[2]) -> f32[2] { while x > 0 { x = x - 1 }\n return x }", {}, "'while' is control flow"),
+    ("fn main(x: f32[2]) -> f32[2] { if max(x) > 0 { x = -x }\n return x }", {}, "'if' on a runtime tensor"),
+    ("fn main(x: f32[2]) -> f32[2] { x[0] = 1\n return x }", {}, "indexed assignment"),
+    ("fn main(x: f32[2]) -> f32[2] { return grad(sum(x), x) }", {}, "grad() is not supported"),
+    ("fn main(x: f32[2]) -> f32[2] { return x[0:0] }", {}, "empty slice 0:0"),
+    ("fn main(x: f32[2]) -> f32[2] { return x[2] }", {}, "index 2 is out of range"),
+    ("fn main(x: f32[2]) -> f32[2] { return x[x] }", {}, "must be i32"),
+    ("fn main(x: f32[2]) -> f32[2] { return x < x < x }", {}, "can't be chained"),
+    ("fn main(x: f32[2], n: int) -> f32[2] { return x * n }", {}, "int parameter 'n'"),
+    ("fn f(x: f32[2], n: int) -> f32[2] { return x * n }\nfn main(x: f32[2]) -> f32[2] { return f(x, 1.5) }",
+     {}, "must be a whole number"),
+    ("fn main(x: f32[2]) -> (f32[2], f32[2]) { return x }", {}, "returns 1 value(s)"),
+    ("fn main(x: f32[2]) -> f32[2] { let a, b = x\n return a }", {}, "cannot unpack"),
+    ("fn main(x: i32[2]) -> i32[2] { return x + 0.5 }", {}, "does not mix with an i32 tensor"),
+]
+
+
+@pytest.mark.parametrize("src,kw,match", LANG_ERRORS, ids=[e[2] for e in LANG_ERRORS])
+def test_language_errors(src, kw, match):
+    with pytest.raises(ML.MiraSyntaxError, match=re.escape(match)):
+        ML.elaborate(src, **kw)
+
+
+def test_emit_ast_round_trips():
+    """`emit ast` prints every statement and expression form as source that parses back to
+    the same tree (up to line numbers): formatting the re-parsed text gives the same text,
+    and that text elaborates to the same graph."""
+    for name in LANG:
+        text = cli.format_module(ML.parse(_read(os.path.join(PROGRAMS, name + ".mira"))))
+        assert cli.format_module(ML.parse(text)) == text, name
+        _same_graph(ML.elaborate(text, dims=LANG[name]), _lang_fixture(name)[0]["elaborated"])

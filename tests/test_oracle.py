@@ -361,6 +361,55 @@ def test_transpose_and_concat_brute_force():
         assert z[a, b_, c, d] == (x[a, b_, c, d] if b_ < 2 else -x[a, b_, c, d])
 
 
+def test_slice_where_broadcast_gather_brute_force():
+    """Element by element against index arithmetic written out: slice reads x[i + begin];
+    where takes a where cond != 0 (negative and fractional conditions count as true) in a's
+    dtype, broadcasting all three; broadcast repeats along the size-1 and new leading axes;
+    gather takes rows of the table by i32 index along its axis, index shape in place."""
+    x = np.arange(3 * 4 * 5, dtype=np.float32).reshape(3, 4, 5) - 7
+    y = G.evaluate("slice", [x], {"begin": (1, 0, 2), "size": (2, 3, 3)})
+    assert y.shape == (2, 3, 3)
+    for i, j, k in np.ndindex(*y.shape):
+        assert y[i, j, k] == x[i + 1, j, k + 2]
+    cond = np.array([[0.0], [-0.5], [2.0]], np.float32)
+    a = np.arange(3 * 4, dtype=np.int32).reshape(3, 4)
+    b = np.int32(-1) * np.ones((1, 4), np.int32)
+    w = G.evaluate("where", [cond, a, b], {})
+    assert w.dtype == np.int32 and w.shape == (3, 4)
+    for i, j in np.ndindex(3, 4):
+        assert w[i, j] == (a[i, j] if cond[i, 0] != 0 else -1)
+    r = G.evaluate("broadcast", [np.array([[1.0], [2.0]], np.float32)], {"shape": (3, 2, 4)})
+    for i, j, k in np.ndindex(3, 2, 4):
+        assert r[i, j, k] == j + 1
+    idx = np.array([[2, 0], [1, 2]], np.int32)
+    g = G.evaluate("gather", [x, idx], {"axis": 1})
+    assert g.shape == (3, 2, 2, 5)
+    for i, p, q, k in np.ndindex(*g.shape):
+        assert g[i, p, q, k] == x[i, idx[p, q], k]
+    # sort: ascending along its axis, the same multiset per row; cumprod: running f32
+    # products left to right; argmax / argmin: the first index of the extreme value
+    rows = np.array([[3.0, -1.0, 2.0, -1.0], [0.5, 4.0, 4.0, 0.25]], np.float32)
+    srt = G.evaluate("sort", [rows], {"axis": 1})
+    cum = G.evaluate("cumprod", [rows], {"axis": 1})
+    for i in range(2):
+        assert list(srt[i]) == sorted(rows[i].tolist())
+        run = np.float32(1)
+        for j in range(4):
+            run = np.float32(run * rows[i, j])
+            assert cum[i, j] == run
+    am = G.evaluate("argmax", [rows], {"axis": 1, "keepdims": False})
+    an = G.evaluate("argmin", [rows], {"axis": 1, "keepdims": True})
+    assert am.dtype == np.int32 and list(am) == [0, 1] and an.shape == (2, 1) and list(an[:, 0]) == [1, 3]
+    cmp = {"greater": lambda u, v: u > v, "greater_equal": lambda u, v: u >= v, "equal": lambda u, v: u == v}
+    u = np.array([1, 2, 3], np.int32)
+    v = np.array([[2], [3]], np.int32)
+    for kind, f in cmp.items():
+        m = G.evaluate(kind, [u, v], {})
+        assert m.dtype == np.int32
+        for i, j in np.ndindex(2, 3):
+            assert m[i, j] == (1 if f(u[j], v[i, 0]) else 0)
+
+
 @pytest.mark.parametrize("ashape,wshape", [((5, 7), (7, 3)), ((2, 3, 1, 64), (2, 3, 64, 273)),
                                            ((4, 1, 8, 32), (1, 3, 32, 16)), ((1, 1), (1, 1)), ((9, 300), (300, 2))])
 def test_f32_matmul_within_its_rounding_bound(ashape, wshape):
