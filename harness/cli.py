@@ -73,11 +73,7 @@ class Program:
 
     def summary(self) -> str:
         lines = [f"target {self.target}: {len(self.segments)} segment(s), compiled in {self.compile_seconds:.2f}s"]
-        for i, seg in enumerate(self.segments):
-            ins = ", ".join(f"{v!r}:{v.type}" for v in seg.graph.inputs)
-            lines.append(f"  [{i}] {seg.device:<8} {len(seg.graph.compute_ops()):3d} ops   inputs: {ins}")
-            lines.append("      " + seg.executable.report().replace("\n", "\n      "))
-        return "\n".join(lines)
+        return "\n".join(lines + self.runner.summary_lines())
 
     def placement_report(self) -> str:
         lines = []
@@ -117,7 +113,10 @@ def compile_graph(g: Graph, target: str, precision: Optional[str] = "auto", quan
             rng = np.random.default_rng(0)
             calibration = [{v.name: rng.standard_normal(v.type.shape).astype(v.type.np_dtype) for v in g.inputs}
                            for _ in range(4)]
-        LW.w8a8(g, calibration)
+        try:
+            LW.w8a8(g, calibration)
+        except ValueError as err:
+            raise CompileError(str(err)) from None
     elif quantize == "int8":
         LW.weight_only(g)
     elif quantize is not None:

@@ -11,10 +11,16 @@ tests and the benchmark.  Those names are the interface and are kept:
     graph.inputs, graph.ops, graph.outputs, graph.users(), graph.compute_ops()
 
 Everything else here is this harness's own: a builder (`Graph.op`) whose
-result types come from the small shape rules below, and a verifier.  There is
-no control flow (the W8A8 configurations have none).  Integer (i32) values
-appear in index and mask arithmetic; comparisons give 1 / 0 in their operands'
-dtype, as MIRA's do (mira/ops.py:134-140).
+result types come from the small shape rules below, and a verifier.  Integer
+(i32) values appear in index and mask arithmetic; comparisons give 1 / 0 in
+their operands' dtype, as MIRA's do (mira/ops.py:134-140).
+
+Control flow is structured as in MIRA (mira/ir.py:14-45, 160-183): an `if` op
+owns a `then` and an `else` graph, a `while` op a `cond` and a `body` graph;
+their inputs are the condition (if), the loop state (while), then the values
+each sub-graph captures from enclosing graphs, and their results are the
+branches' outputs / the final loop state.  The W8A8 rewrite rejects them, as
+MIRA's does (mira/quantize.py:84-85); the runner drives them on the host.
 """
 from __future__ import annotations
 
@@ -77,10 +83,16 @@ class Op:
 
     is_const = property(lambda self: self.kind == "const")
     is_constant_like = property(lambda self: self.kind in ("const", "dequantize"))
-    is_control = property(lambda self: False)
+    is_control = property(lambda self: self.kind in ("if", "while"))
+
+    def subgraphs(self) -> list:
+        """(name, Graph) of a control op's sub-graphs, in MIRA's order."""
+        names = ("then", "else") if self.kind == "if" else ("cond", "body") if self.kind == "while" else ()
+        return [(n, self.attrs[n]) for n in names]
 
     def __repr__(self) -> str:
-        return f"{self.result!r} = {self.kind}({', '.join(map(repr, self.inputs))})"
+        res = ", ".join(map(repr, self.results))
+        return f"{res} = {self.kind}({', '.join(map(repr, self.inputs))})"
 
 
 # ---------------------------------------------------------------- shape rules
@@ -163,6 +175,18 @@ def result_type(kind: str, ins: list, a: dict) -> TensorType:
         return TensorType(ins[1].dtype, _broadcast(t0.shape, ins[1].shape, ins[2].shape))
     if kind in ("sort", "cumprod"):
         return t0
+    if kind == "dynamic_slice":
+        size = tuple(a["size"])
+        if ins[1].dtype != "i32" or ins[1].shape != (t0.rank,) or len(size) != t0.rank or \
+                any(n < 0 or n > d for n, d in zip(size, t0.shape)):
+            raise ValueError(f"dynamic_slice: need start i32[{t0.rank}] and a size that fits {t0}")
+        return TensorType(t0.dtype, size)
+    if kind == "dynamic_update_slice":
+        u, st = ins[1], ins[2]
+        if u.dtype != t0.dtype or u.rank != t0.rank or any(n > d for n, d in zip(u.shape, t0.shape)) or \
+                st.dtype != "i32" or st.shape != (t0.rank,):
+            raise ValueError(f"dynamic_update_slice: update {u} at start {st} does not fit {t0}")
+        return t0
     if kind in ("argmax", "argmin"):
         ax = a["axis"] % t0.rank
         keep = a.get("keepdims", False)
@@ -213,6 +237,16 @@ class Graph:
         attrs = dict(attrs or {})
         return self.emit(kind, inputs, attrs, result_type(kind, [v.type for v in inputs], attrs))
 
+    def add_control(self, kind: str, inputs: list, attrs: dict, types: list) -> list:
+        """Append an if / while op with results of the given types; returns the results."""
+        results = [Value(t) for t in types]
+        op = Op(kind, inputs, attrs, results)
+        for r in results:
+            r.producer = op
+        self.ops.append(op)
+        check_control(op)
+        return results
+
     def emit(self, kind: str, inputs: list, attrs: dict, rtype: TensorType) -> Value:
         """Append an op with an explicit result type."""
         v = Value(rtype)
@@ -248,7 +282,8 @@ class Graph:
         self.ops = keep[::-1]
 
     def check(self) -> None:
-        """Every input defined before use, every producer link consistent."""
+        """Every input defined before use, every producer link consistent, every control op's
+        sub-graphs matching its inputs and results (and checked themselves)."""
         seen = set(self.inputs)
         for op in self.ops:
             missing = [v for v in op.inputs if v not in seen]
@@ -257,6 +292,10 @@ class Graph:
             for r in op.results:
                 if r.producer is not op:
                     raise AssertionError(f"{r!r} has the wrong producer")
+            if op.is_control:
+                check_control(op)
+                for _, sub in op.subgraphs():
+                    sub.check()
             seen.update(op.results)
         if any(v not in seen for v in self.outputs):
             raise AssertionError("an output is never defined")
@@ -265,6 +304,34 @@ class Graph:
         lines = [f"graph {self.name}({', '.join(f'{v!r}: {v.type}' for v in self.inputs)})"]
         for op in self.ops:
             extra = f" epilogue={list(op.attrs['epilogue'])}" if "epilogue" in op.attrs else ""
-            lines.append(f"  {op!r} : {op.result.type}{extra}")
+            lines.append(f"  {op!r} : {', '.join(str(r.type) for r in op.results)}{extra}")
+            for name, sub in op.subgraphs():
+                lines.append(f"    {name}: " + str(sub).replace("\n", "\n    "))
         lines.append("  return " + ", ".join(map(repr, self.outputs)))
         return "\n".join(lines)
+
+
+def check_control(op: Op) -> None:
+    """A control op's sub-graphs agree with its inputs and results (mira/ir.py:160-183)."""
+    ins, outs = [v.type for v in op.inputs], [r.type for r in op.results]
+    types = lambda vs: [v.type for v in vs]     # noqa: E731
+    if op.kind == "if":
+        n = op.attrs["n_then"]
+        then, other = op.attrs["then"], op.attrs["else"]
+        if op.inputs[0].type.numel != 1:
+            raise AssertionError("if: the condition must have one element")
+        if types(then.inputs) != ins[1:1 + n] or types(other.inputs) != ins[1 + n:]:
+            raise AssertionError("if: branch inputs do not match the captures")
+        if types(then.outputs) != outs or types(other.outputs) != outs:
+            raise AssertionError("if: branch outputs do not match the results")
+    else:
+        ns, nc = op.attrs["n_state"], op.attrs["n_cond"]
+        cond, body = op.attrs["cond"], op.attrs["body"]
+        state = ins[:ns]
+        if outs != state:
+            raise AssertionError("while: results must match the loop state")
+        if types(cond.inputs) != state + ins[ns:ns + nc] or len(cond.outputs) != 1 or \
+                cond.outputs[0].type.numel != 1:
+            raise AssertionError("while: bad condition graph signature")
+        if types(body.inputs) != state + ins[ns + nc:] or types(body.outputs) != state:
+            raise AssertionError("while: bad body graph signature")

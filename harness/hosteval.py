@@ -120,6 +120,28 @@ def quantize_activation(x: np.ndarray, x_scale: float) -> np.ndarray:
     return np.clip(np.rint(_f32(x) / np.float32(x_scale)), -127, 127).astype(np.int64)
 
 
+def _clamped_starts(start, shape, size) -> list:
+    """Runtime slice starts, each clamped so the window stays inside its axis (mira/ops.py:538-539)."""
+    return [int(min(max(int(b), 0), d - n)) for b, d, n in zip(np.asarray(start).ravel(), shape, size)]
+
+
+def run_control(op, args: list, sub: dict) -> list:
+    """An if / while op from host arrays (mira/backends/cpu.py:38-51); sub maps each sub-graph
+    name to a callable from its input arrays to its output arrays."""
+    if op.kind == "if":
+        n = op.attrs["n_then"]
+        if bool(np.asarray(args[0]).ravel()[0]):
+            return sub["then"](args[1:1 + n])
+        return sub["else"](args[1 + n:])
+    ns, nc = op.attrs["n_state"], op.attrs["n_cond"]
+    state, cond_caps, body_caps = list(args[:ns]), list(args[ns:ns + nc]), list(args[ns + nc:])
+    for _ in range(op.attrs["max_iters"]):
+        if not bool(np.asarray(sub["cond"](state + cond_caps)[0]).ravel()[0]):
+            return state
+        state = list(sub["body"](state + body_caps))
+    raise RuntimeError(f"while loop exceeded {op.attrs['max_iters']} iterations")
+
+
 def evaluate(kind: str, xs: list, a: dict) -> np.ndarray:
     if kind == "const":
         return a["value"]
@@ -162,6 +184,14 @@ def evaluate(kind: str, xs: list, a: dict) -> np.ndarray:
         return np.where(xs[0] != 0, xs[1], xs[2]).astype(xs[1].dtype)
     if kind == "broadcast":
         return np.broadcast_to(xs[0], a["shape"]).copy()
+    if kind == "dynamic_slice":
+        st = _clamped_starts(xs[1], xs[0].shape, a["size"])
+        return xs[0][tuple(slice(b, b + n) for b, n in zip(st, a["size"]))].copy()
+    if kind == "dynamic_update_slice":
+        st = _clamped_starts(xs[2], xs[0].shape, xs[1].shape)
+        out = xs[0].copy()
+        out[tuple(slice(b, b + n) for b, n in zip(st, xs[1].shape))] = xs[1]
+        return out
     if kind == "sort":
         return np.sort(xs[0], axis=a["axis"])
     if kind == "cumprod":
@@ -189,11 +219,20 @@ def evaluate(kind: str, xs: list, a: dict) -> np.ndarray:
     raise NotImplementedError(f"no host evaluation for '{kind}'")
 
 
-def run(g, feeds: dict, watch: Optional[set] = None, peaks: Optional[dict] = None) -> dict:
+def _sub_runner(graph):
+    return lambda arrays: [run(graph, dict(zip(graph.inputs, arrays)))[v] for v in graph.outputs]
+
+
+def run(g, feeds: dict, watch: Optional[set] = None, peaks: Optional[dict] = None, subs: Optional[dict] = None) -> dict:
     """Evaluate g from {input Value: array}; returns every value.  With `watch`, the running
-    max |x| of each watched value is folded into `peaks`."""
+    max |x| of each watched value is folded into `peaks`.  Control ops run their sub-graphs
+    through `subs` ({(op, name): callable}) or, without it, evaluated here."""
     env = {v: np.asarray(feeds[v]).astype(v.type.np_dtype) for v in g.inputs}
     for op in g.ops:
+        if op.is_control:
+            sub = {n: subs[(op, n)] if subs else _sub_runner(sg) for n, sg in op.subgraphs()}
+            env.update(zip(op.results, run_control(op, [env[x] for x in op.inputs], sub)))
+            continue
         env[op.result] = evaluate(op.kind, [env[x] for x in op.inputs], op.attrs)
     if watch:
         for v in watch:
@@ -203,15 +242,27 @@ def run(g, feeds: dict, watch: Optional[set] = None, peaks: Optional[dict] = Non
 
 
 class HostExecutable:
-    def __init__(self, g):
+    """A host segment; its control ops' sub-graphs are compiled by `compile_sub` (the runner
+    partitions them for the target, as MIRA's driver does, mira/compiler.py:83-96)."""
+
+    def __init__(self, g, compile_sub=None):
         self.g = g
+        self.sub = {}
+        for op in g.ops:
+            for name, sg in op.subgraphs():
+                if compile_sub is None:
+                    raise RuntimeError("control flow needs a sub-graph compiler")
+                self.sub[(op, name)] = compile_sub(sg)
 
     def run(self, feeds: dict) -> dict:
-        env = run(self.g, feeds)
+        subs = {k: r.run_values for k, r in self.sub.items()}
+        env = run(self.g, feeds, subs=subs)
         return {v: env[v] for v in self.g.outputs}
 
     def report(self) -> str:
-        return f"host: {len(self.g.compute_ops())} ops evaluated with NumPy"
+        n = sum(op.is_control for op in self.g.ops)
+        return f"host: {len(self.g.compute_ops())} ops evaluated with NumPy" + \
+            (f" ({n} control-flow op(s))" if n else "")
 
 
 class HostTarget:
@@ -221,5 +272,5 @@ class HostTarget:
     def check(self, op) -> Optional[str]:
         return None
 
-    def compile(self, g) -> HostExecutable:
-        return HostExecutable(g)
+    def compile(self, g, compile_sub=None) -> HostExecutable:
+        return HostExecutable(g, compile_sub)

@@ -66,7 +66,7 @@ def const_fold(g: Graph) -> bool:
     """Ops whose inputs are all constants become constants (mira/passes.py:25-37)."""
     changed = False
     for op in g.ops:
-        if op.kind == "const" or not op.inputs or op.result.type.numel > FOLD_LIMIT:
+        if op.kind == "const" or op.is_control or not op.inputs or op.result.type.numel > FOLD_LIMIT:
             continue
         vals = [_const_array(v) for v in op.inputs]
         if any(v is None for v in vals):
@@ -151,6 +151,8 @@ def cse(g: Graph) -> bool:
     seen: dict = {}
     changed = False
     for op in g.ops:
+        if op.is_control:
+            continue
         key = _op_key(op)
         prev = seen.get(key)
         if prev is not None and (op.kind != "const" or np.array_equal(prev.attrs["value"], op.attrs["value"])):
@@ -210,18 +212,24 @@ def fuse_epilogues(g: Graph) -> int:
             return n
 
 
-def lower_f16(g: Graph) -> None:
+def lower_f16(g: Graph, keep_interface: bool = True) -> None:
     """MIRA's f16 precision (mira/passes.py:206-253): float constants are rounded to f16, every
     f32 result becomes f16, each f32 input is cast to f16 where it enters and each f32 output
     cast back to f32 where it leaves; casts between float types disappear and casts to or from
-    integers stay, aimed at f16."""
+    integers stay, aimed at f16.  The sub-graphs of if / while ops are converted completely,
+    inputs and outputs included (keep_interface=False), so loop state stays f16."""
     body, g.ops = g.ops, []
     out_dtypes = [v.type.dtype for v in g.outputs]
     sub: dict = {}
     for v in g.inputs:
         if v.type.dtype == "f32":
-            sub[v] = g.emit("cast", [v], {"dtype": "f16"}, TensorType("f16", v.type.shape))
+            if keep_interface:
+                sub[v] = g.emit("cast", [v], {"dtype": "f16"}, TensorType("f16", v.type.shape))
+            else:
+                v.type = TensorType("f16", v.type.shape)
     for op in body:
+        for _, sg in op.subgraphs():
+            lower_f16(sg, keep_interface=False)
         op.inputs = [sub.get(x, x) for x in op.inputs]
         if op.kind == "const":
             a = op.attrs["value"]
@@ -241,7 +249,7 @@ def lower_f16(g: Graph) -> None:
     outs = []
     for v, dt in zip(g.outputs, out_dtypes):
         v = sub.get(v, v)
-        if dt == "f32" and v.type.dtype != "f32":
+        if keep_interface and dt == "f32" and v.type.dtype != "f32":
             v = g.emit("cast", [v], {"dtype": "f32"}, TensorType("f32", v.type.shape))
         outs.append(v)
     g.outputs = outs
@@ -255,6 +263,9 @@ def prepare(g: Graph, precision: Optional[str] = None) -> Graph:
         lower_f16(g)
     elif precision is not None:
         raise ValueError(f"precision {precision!r}: None (f32) or 'f16'")
+    for op in g.ops:                     # if / while sub-graphs first (mira/passes.py:276-278)
+        for _, sg in op.subgraphs():
+            prepare(sg)
     for _ in range(10):
         if not any([const_fold(g), simplify(g), cse(g), dce(g)]):
             break
@@ -297,6 +308,9 @@ def calibrate(g: Graph, feeds: Sequence[dict]) -> list:
     """Peak |x| of each W8A8 candidate's activation over the calibration feeds ({input name:
     array}), one float per candidate in program order (so a same-shaped graph at another
     batch size can take them)."""
+    if any(op.is_control for op in g.ops):
+        raise ValueError("W8A8 quantization doesn't support programs with data-dependent control flow "
+                         "(mira/quantize.py:84-85)")
     cands = w8a8_candidates(g)
     watch = {op.inputs[0] for op in cands}
     peaks: dict = {}

@@ -25,10 +25,11 @@ mira/parser.py and mira/elaborate.py, producing this harness's graphs.
 Elaboration inlines every call of a user function, binding the shape symbols of its
 parameter types from the arguments (a symbol seen twice must agree), its `int` parameters
 from compile-time numbers, and checks the results against the declared return types.
-`for` loops are unrolled and `if` on a compile-time condition picks its branch while
-elaborating; a `while` or an `if` on a runtime tensor, indexed assignment and `grad` are
-the control-flow and autodiff half of MIRA's language, which its W8A8 rewrite rejects
-(mira/quantize.py:84-85): this front end reports them as unsupported.  The entry
+`for` loops are unrolled and `if` / `while` on compile-time conditions are decided while
+elaborating; on a one-element runtime tensor they become `if` / `while` ops whose
+sub-graphs capture the outer values they read (mira/elaborate.py:128-184, 428-519); indexed
+assignment is a dynamic_update_slice.  `grad` (MIRA's autodiff) is reported as unsupported.
+The entry
 function's plain parameters become graph inputs, its `int` parameters take values from
 `dims`; its `const` parameters are weights: given ones are used, the others are drawn in
 declaration order from one seeded generator by MIRA's rule (mira/elaborate.py:196-213,
@@ -42,6 +43,7 @@ sum / mean / max (x, axis=all, keepdims=false), layernorm(x, gamma, beta, eps=1e
 transpose(x, perm=swap last two), reshape(x, shape) with one -1 allowed, flatten(x, axis=1),
 concat(xs, axis=0), cast(x, dtype), slice(x, begin, size), pad(x, pads, value=0),
 broadcast(x, shape), gather(x, indices, axis=0), where(cond, a, b), size(x, axis),
+dynamic_slice(x, start, size), dynamic_update_slice(x, update, start),
 sort / cumprod (x, axis=-1), argmax / argmin (x, axis=-1, keepdims=false),
 zeros / ones (shape, dtype=f32), full(shape, value, dtype=f32), arange(start, stop, dtype=i32),
 conv2d(x, w, stride=1, padding=0, dilation=1, groups=1),
@@ -78,7 +80,8 @@ _TOKEN = re.compile(r"""
 
 KEYWORDS = {"fn", "let", "return", "const", "for", "in", "while", "if", "else"}
 COMPARE = ("<", "<=", ">", ">=", "==", "!=")
-MAX_UNROLL = 4096
+MAX_UNROLL = 10_000        # iterations of a `for` (or compile-time `while`) unrolled while elaborating
+MAX_ITERS = 100_000        # iterations a runtime `while` may run
 
 
 @dataclass
@@ -497,7 +500,7 @@ def _unify(tref: TypeRef, dtype: str, shape: tuple, env: dict, what: str, line: 
 _UNARY = ("relu", "sigmoid", "tanh", "gelu", "exp", "log", "abs", "sign", "sqrt")
 _BINOP = {"+": "add", "-": "sub", "*": "mul", "/": "div", "**": "pow"}
 # MIRA builtins outside this front end (runtime indexing into loop state, autodiff, ...)
-_UNSUPPORTED = ("grad", "dynamic_slice", "dynamic_update_slice", "scatter_add", "erf")
+_UNSUPPORTED = ("grad", "scatter_add", "erf")
 MAX_DEPTH = 64
 
 
@@ -538,6 +541,15 @@ class Scope:
         s = self.owner(name)
         return None if s is None else s.vars[name]
 
+    def snapshot(self) -> dict:
+        """Every variable in sight: (scope id, name) -> (scope, value)."""
+        out, s = {}, self
+        while s is not None:
+            for n, v in s.vars.items():
+                out[(id(s), n)] = (s, v)
+            s = s.parent
+        return out
+
     def bindings(self) -> dict:
         """The whole-number names in sight (shape symbols, int parameters, loop counters)."""
         chain, s = [], self
@@ -550,14 +562,85 @@ class Scope:
         return out
 
 
+def _restore(snap: dict) -> dict:
+    """Put the snapshotted variables back; returns those that had changed (key -> new value)."""
+    changed = {}
+    for key, (scope, old) in snap.items():
+        new = scope.vars[key[1]]
+        if new is not old:
+            changed[key] = new
+            scope.vars[key[1]] = old
+    return changed
+
+
+def _assigned(body: list) -> list:
+    """Names a block assigns (plainly or by index), nested blocks included, first-seen order."""
+    out: list = []
+    for st in body:
+        if st[0] == "assign":
+            out += [n for n in st[1] if n not in out]
+        elif st[0] == "index_assign" and st[1] not in out:
+            out.append(st[1])
+        subs = {"for": [st[4]] if st[0] == "for" else [], "while": [st[2]] if st[0] == "while" else [],
+                "if": [st[2], st[3] or []] if st[0] == "if" else []}.get(st[0], [])
+        for b in subs:
+            out += [n for n in _assigned(b) if n not in out]
+    return out
+
+
+class _Ctx:
+    """The graph being built and what it captured from the graphs around it."""
+
+    def __init__(self, graph: Graph, parent: Optional["_Ctx"]):
+        self.graph = graph
+        self.parent = parent
+        self.captures: dict = {}          # outer value -> its placeholder input here
+        self.captured_outer: list = []    # the outer values, in input order
+
+    def owns(self, v: Value) -> bool:
+        return v in self.graph.inputs or (v.producer is not None and v.producer in self.graph.ops)
+
+
 class Elaborator:
     """Inlines the entry function into one Graph (mira/elaborate.py:186-222 for the entry,
-    :279-346 for calls, :348-413 for statements)."""
+    :279-346 for calls, :348-528 for statements, :691-724 for indexed assignment)."""
 
     def __init__(self, fns: dict[str, Fn], name: str = "main"):
         self.fns = fns
-        self.g = Graph(name)
+        self.ctx = _Ctx(Graph(name), None)
         self.stack: list[str] = []
+        self.counter = 0
+
+    @property
+    def g(self) -> Graph:
+        return self.ctx.graph
+
+    def local(self, v: Value, ctx: Optional[_Ctx] = None) -> Value:
+        """`v` usable in ctx's graph: captured from an enclosing graph as a new input (a
+        constant is copied instead)."""
+        ctx = ctx or self.ctx
+        if ctx.owns(v):
+            return v
+        if v in ctx.captures:
+            return ctx.captures[v]
+        if ctx.parent is None:
+            raise AssertionError(f"{v!r} is not defined in any enclosing graph")
+        if v.producer is not None and v.producer.kind == "const":
+            c = ctx.graph.const(v.producer.attrs["value"])
+        else:
+            c = Value(v.type)
+            ctx.graph.inputs.append(c)
+            ctx.captured_outer.append(v)
+        ctx.captures[v] = c
+        return c
+
+    def enter(self, label: str) -> _Ctx:
+        self.ctx = _Ctx(Graph(f"{self.g.name}.{label}"), self.ctx)
+        return self.ctx
+
+    def exit(self, ctx: _Ctx) -> None:
+        assert self.ctx is ctx
+        self.ctx = ctx.parent
 
     # ---- values
 
@@ -571,6 +654,10 @@ class Elaborator:
                                       "cast the tensor to f32 first")
             return self.g.const(np.array(v, dtype=DTYPES[dtype]))
         raise MiraSyntaxError(f"line {line}: expected a tensor, got {_describe(v)}")
+
+    def arg(self, v, line: int, dtype: str = "f32") -> Value:
+        """A builtin's tensor argument, made local to the graph being built as it is read."""
+        return self.local(self.tensor(v, line, dtype))
 
     @staticmethod
     def int_(v, line: int, what: str) -> int:
@@ -663,7 +750,7 @@ class Elaborator:
                 continue
             if p.const and self.stack:
                 raise MiraSyntaxError(f"line {fn.line}: 'const' is only allowed on the entry function's parameters")
-            tensors[p.name] = a = self.tensor(a, line, p.type.dtype)
+            tensors[p.name] = a = self.local(self.tensor(a, line, p.type.dtype))
             _unify(p.type, a.type.dtype, a.type.shape, env, f"argument '{p.name}' of '{fn.name}'", line, False)
         for p in fn.params:
             if p.name in tensors:
@@ -687,7 +774,7 @@ class Elaborator:
                                       f"declares {len(fn.rets)}")
             out = []
             for v, tref in zip(values, fn.rets):
-                v = self.tensor(v, rline, tref.dtype)
+                v = self.local(self.tensor(v, rline, tref.dtype))
                 _unify(tref, v.type.dtype, v.type.shape, env, f"the result of '{fn.name}'", rline, True)
                 out.append(v)
             return tuple(out) if len(fn.rets) > 1 else out[0]
@@ -714,23 +801,11 @@ class Elaborator:
                     s.vars[var] = it
                     self.block(inner, s, nested=True)
             elif kind == "if":
-                _, cond, then, other, _ = st
-                c = self.expr(cond, scope, line)
-                if isinstance(c, Value):
-                    raise MiraSyntaxError(f"line {line}: 'if' on a runtime tensor is control flow, which this "
-                                          "front end does not build (MIRA's W8A8 rewrite rejects it)")
-                if not (isinstance(c, bool) or _num(c)):
-                    raise MiraSyntaxError(f"line {line}: an 'if' condition must be a number or a boolean, "
-                                          f"got {_describe(c)}")
-                taken = then if c else other
-                if taken:
-                    self.block(taken, Scope(scope), nested=True)
+                self.if_stmt(st, scope)
             elif kind == "while":
-                raise MiraSyntaxError(f"line {line}: 'while' is control flow, which this front end does not "
-                                      "build (MIRA's W8A8 rewrite rejects it)")
+                self.while_stmt(st, scope)
             elif kind == "index_assign":
-                raise MiraSyntaxError(f"line {line}: indexed assignment ('{st[1]}[...] = ...') is not supported by "
-                                      "this front end")
+                self.index_assign(st, scope)
             else:   # return
                 if nested:
                     raise MiraSyntaxError(f"line {line}: 'return' must be the last statement of a function, "
@@ -781,6 +856,158 @@ class Elaborator:
                                       f"cannot assign a {_describe(v)}")
             owner.vars[n] = v
 
+    @staticmethod
+    def truthy(v, line: int) -> Optional[bool]:
+        """A condition's compile-time truth, or None for a one-element runtime tensor."""
+        if isinstance(v, Value):
+            if v.type.numel != 1:
+                raise MiraSyntaxError(f"line {line}: a condition must be a single value, got {v.type}; "
+                                      "reduce it first (e.g. with max or sum)")
+            return None
+        if isinstance(v, bool) or _num(v):
+            return bool(v)
+        raise MiraSyntaxError(f"line {line}: a condition must be a boolean, a number or a one-element tensor; "
+                              f"got {_describe(v)}")
+
+    def if_stmt(self, st, scope: Scope) -> None:
+        """A compile-time condition picks a branch now; a runtime one builds an `if` op whose
+        branches output every variable either of them changes (mira/elaborate.py:428-465)."""
+        _, cond_e, then, other, line = st
+        cond = self.expr(cond_e, scope, line)
+        static = self.truthy(cond, line)
+        if static is not None:
+            taken = then if static else other
+            if taken:
+                self.block(taken, Scope(scope), nested=True)
+            return
+        n, self.counter = self.counter, self.counter + 1
+        branches = []
+        for label, body in (("then", then), ("else", other or [])):
+            snap = scope.snapshot()
+            ctx = self.enter(f"if{n}.{label}")
+            self.block(body, Scope(scope), nested=True)
+            self.exit(ctx)
+            branches.append((ctx, _restore(snap)))
+        keys = list(dict.fromkeys(k for _, changed in branches for k in changed))
+        snap = scope.snapshot()
+        types = []
+        for key in keys:
+            orig = snap[key][1]
+            if not isinstance(orig, Value):
+                raise MiraSyntaxError(f"line {line}: '{key[1]}' is a compile-time value; it cannot change inside "
+                                      "an 'if' whose condition is only known at runtime")
+            types.append(orig.type)
+        for ctx, changed in branches:
+            ctx.graph.outputs = [self.local(changed.get(k, snap[k][1]), ctx) for k in keys]
+        (then_ctx, _), (else_ctx, _) = branches
+        ins = [self.local(cond)] + [self.local(v) for v in then_ctx.captured_outer] + \
+              [self.local(v) for v in else_ctx.captured_outer]
+        results = self.g.add_control("if", ins, {"then": then_ctx.graph, "else": else_ctx.graph,
+                                                 "n_then": len(then_ctx.captured_outer)}, types)
+        for key, r in zip(keys, results):
+            snap[key][0].vars[key[1]] = r
+
+    def while_stmt(self, st, scope: Scope) -> None:
+        """A compile-time condition unrolls the loop now; a runtime one builds a `while` op whose
+        state is every tensor variable the body assigns (mira/elaborate.py:467-519)."""
+        _, cond_e, body, line = st
+        cond = self.expr(cond_e, scope, line)
+        if self.truthy(cond, line) is not None:
+            for _ in range(MAX_UNROLL):
+                if not self.truthy(self.expr(cond_e, scope, line), line):
+                    return
+                self.block(body, Scope(scope), nested=True)
+            raise MiraSyntaxError(f"line {line}: compile-time while loop ran more than {MAX_UNROLL} iterations")
+        names = []
+        for name in _assigned(body):
+            v = scope.lookup(name)
+            if v is None:
+                continue
+            if not isinstance(v, Value):
+                raise MiraSyntaxError(f"line {line}: '{name}' is a compile-time value; it cannot change inside a "
+                                      "'while' whose condition is only known at runtime")
+            names.append(name)
+        init = [scope.lookup(nm) for nm in names]
+        n, self.counter = self.counter, self.counter + 1
+
+        def state_scope(ctx: _Ctx) -> Scope:
+            s = Scope(scope)
+            for nm, v in zip(names, init):
+                ph = Value(v.type)
+                ctx.graph.inputs.append(ph)
+                s.vars[nm] = ph
+            return s
+
+        cond_ctx = self.enter(f"while{n}.cond")
+        c = self.expr(cond_e, state_scope(cond_ctx), line)
+        if not isinstance(c, Value) or c.type.numel != 1:
+            raise MiraSyntaxError(f"line {line}: the loop condition must stay a one-element tensor")
+        cond_ctx.graph.outputs = [self.local(c)]
+        self.exit(cond_ctx)
+        body_ctx = self.enter(f"while{n}.body")
+        s = state_scope(body_ctx)
+        snap = scope.snapshot()
+        self.block(body, Scope(s), nested=True)
+        if _restore(snap):
+            raise MiraSyntaxError(f"line {line}: a compile-time value changed inside a runtime 'while' loop")
+        body_ctx.graph.outputs = [self.local(s.vars[nm]) for nm in names]
+        self.exit(body_ctx)
+        ins = [self.local(v) for v in init] + [self.local(v) for v in cond_ctx.captured_outer] + \
+              [self.local(v) for v in body_ctx.captured_outer]
+        results = self.g.add_control("while", ins, {"cond": cond_ctx.graph, "body": body_ctx.graph,
+                                                    "n_state": len(names), "n_cond": len(cond_ctx.captured_outer),
+                                                    "max_iters": MAX_ITERS}, [v.type for v in init])
+        for nm, r in zip(names, results):
+            scope.owner(nm).vars[nm] = r
+
+    def start_vector(self, parts: list, line: int) -> Value:
+        """An i32[n] start position from compile-time ints and one-element i32 tensors."""
+        if all(isinstance(p, int) for p in parts):
+            return self.g.const(np.array(parts, dtype=np.int32))
+        pieces = []
+        for p in parts:
+            if isinstance(p, int):
+                pieces.append(self.g.const(np.array([p], dtype=np.int32)))
+            else:
+                if p.type.dtype != "i32" or p.type.numel != 1:
+                    raise MiraSyntaxError(f"line {line}: a runtime position must be a one-element i32 tensor, "
+                                          f"got {p.type}")
+                pieces.append(self.op("reshape", [p], {"shape": (1,)}, line))
+        return self.op("concat", pieces, {"axis": 0}, line)
+
+    def index_assign(self, st, scope: Scope) -> None:
+        """x[subscripts] = value as a dynamic_update_slice of the region (mira/elaborate.py:691-724)."""
+        _, name, items, value, line = st
+        owner = scope.owner(name)
+        if owner is None:
+            raise MiraSyntaxError(f"line {line}: assignment to undefined variable '{name}'; declare it with 'let'")
+        x = owner.vars[name]
+        if not isinstance(x, Value):
+            raise MiraSyntaxError(f"line {line}: '{name}' is a compile-time {_describe(x)}; only tensors are indexed")
+        x = self.local(x)
+        starts, region, vshape = [], [], []
+        for sub, d in zip(self.subscripts(items, x.type.shape, scope, line), x.type.shape):
+            if sub[0] == "int":
+                starts.append(sub[1])
+                region.append(1)
+            elif sub[0] == "range":
+                starts.append(sub[1])
+                region.append(sub[2] - sub[1])
+                vshape.append(sub[2] - sub[1])
+            else:
+                if sub[1].type.numel != 1:
+                    raise MiraSyntaxError(f"line {line}: indexed assignment takes one position per axis")
+                starts.append(sub[1])
+                region.append(1)
+        v = self.tensor(self.expr(value, scope, line), line, x.type.dtype)
+        if v.type.dtype != x.type.dtype:
+            raise MiraSyntaxError(f"line {line}: cannot store a {v.type} into '{name}' ({x.type})")
+        if v.type.shape != tuple(vshape):
+            v = self.op("broadcast", [v], {"shape": tuple(vshape)}, line)
+        v = self.op("reshape", [v], {"shape": tuple(region)}, line)
+        start = self.start_vector(starts, line)
+        owner.vars[name] = self.op("dynamic_update_slice", [x, v, start], {}, line)
+
     # ---- expressions
 
     def expr(self, e, scope: Scope, line: int):
@@ -814,9 +1041,21 @@ class Elaborator:
         vals = [self.expr(a, scope, line) for a in args]
         kw = {k: self.expr(v, scope, line) for k, v in kwargs.items()}
         if name in self.fns:
-            if kw:
-                raise MiraSyntaxError(f"line {line}: '{name}' takes no keyword arguments")
-            return self.call_function(self.fns[name], vals, line)
+            fn = self.fns[name]
+            if len(vals) > len(fn.params):
+                raise MiraSyntaxError(f"line {line}: '{name}' takes {len(fn.params)} arguments, got {len(vals)}")
+            args = vals + [None] * (len(fn.params) - len(vals))
+            for k, v in kw.items():
+                idx = next((i for i, p in enumerate(fn.params) if p.name == k), None)
+                if idx is None:
+                    raise MiraSyntaxError(f"line {line}: '{name}' has no parameter named '{k}'")
+                if args[idx] is not None:
+                    raise MiraSyntaxError(f"line {line}: argument '{k}' given twice")
+                args[idx] = v
+            missing = [p.name for p, a in zip(fn.params, args) if a is None]
+            if missing:
+                raise MiraSyntaxError(f"line {line}: call to '{name}' is missing argument(s): {', '.join(missing)}")
+            return self.call_function(fn, args, line)
         if name in _UNSUPPORTED:
             raise MiraSyntaxError(f"line {line}: {name}() is not supported by this front end")
         if name not in BUILTINS:
@@ -857,7 +1096,27 @@ class Elaborator:
         x = self.expr(base, scope, line)
         if not isinstance(x, Value):
             raise MiraSyntaxError(f"line {line}: cannot index a {_describe(x)}")
+        x = self.local(x)
         shape = x.type.shape
+        subs = self.subscripts(items, shape, scope, line)
+        begin = tuple(s[1] if s[0] != "tensor" else 0 for s in subs)
+        size = tuple(1 if s[0] == "int" else s[2] - s[1] if s[0] == "range" else d for s, d in zip(subs, shape))
+        if size != shape:
+            x = self.op("slice", [x], {"begin": begin, "size": size}, line)
+        kept = [i for i, s in enumerate(subs) if s[0] != "int"]
+        if len(kept) != len(subs):
+            x = self.op("reshape", [x], {"shape": tuple(size[i] for i in kept)}, line)
+        shift = 0
+        for axis, i in enumerate(kept):
+            if subs[i][0] == "tensor":
+                idx = subs[i][1]
+                x = self.op("gather", [x, idx], {"axis": axis + shift}, line)
+                shift += idx.type.rank - 1
+        return x
+
+    def subscripts(self, items: list, shape: tuple, scope: Scope, line: int) -> list:
+        """Per axis ("int", k) | ("range", lo, hi) | ("tensor", i32 value); missing ones are whole
+        ranges (mira/elaborate.py:617-650)."""
         if len(items) > len(shape):
             raise MiraSyntaxError(f"line {line}: {len(items)} subscripts for a rank-{len(shape)} tensor")
         subs = []         # per axis: ("int", k) | ("range", lo, hi) | ("tensor", value)
@@ -879,30 +1138,17 @@ class Elaborator:
             if isinstance(v, Value):
                 if v.type.dtype != "i32":
                     raise MiraSyntaxError(f"line {line}: tensor subscripts must be i32, got {v.type}")
-                subs.append(("tensor", v))
+                subs.append(("tensor", self.local(v)))
                 continue
             k = self.int_(v, line, "index")
             if not -d <= k < d:
                 raise MiraSyntaxError(f"line {line}: index {k} is out of range for an axis of size {d}")
             subs.append(("int", k % d))
-        begin = tuple(s[1] if s[0] != "tensor" else 0 for s in subs)
-        size = tuple(1 if s[0] == "int" else s[2] - s[1] if s[0] == "range" else d for s, d in zip(subs, shape))
-        if size != shape:
-            x = self.op("slice", [x], {"begin": begin, "size": size}, line)
-        kept = [i for i, s in enumerate(subs) if s[0] != "int"]
-        if len(kept) != len(subs):
-            x = self.op("reshape", [x], {"shape": tuple(size[i] for i in kept)}, line)
-        shift = 0
-        for axis, i in enumerate(kept):
-            if subs[i][0] == "tensor":
-                idx = subs[i][1]
-                x = self.op("gather", [x, idx], {"axis": axis + shift}, line)
-                shift += idx.type.rank - 1
-        return x
+        return subs
 
     def op(self, kind: str, ins: list, attrs: dict, line: int) -> Value:
         try:
-            return self.g.op(kind, ins, attrs)
+            return self.g.op(kind, [self.local(v) for v in ins], attrs)
         except ValueError as err:
             raise MiraSyntaxError(f"line {line}: {kind}: {err}") from None
 
@@ -942,7 +1188,7 @@ def _unary(kind):
                     return float(UNARY[kind](np.float64(x)))
                 except FloatingPointError:
                     raise MiraSyntaxError(f"line {line}: {kind}({x}) is undefined") from None
-        return el.op(kind, [el.tensor(x, line)], {}, line)
+        return el.op(kind, [el.arg(x, line)], {}, line)
     return [("x", _REQUIRED)], h
 
 
@@ -958,7 +1204,7 @@ def _binary_fn(kind):
 
 def _reduce(kind):
     def h(el, a, line):
-        x = el.tensor(a["x"], line)
+        x = el.arg(a["x"], line)
         axes = list(range(x.type.rank)) if a["axis"] is None else el.ints(a["axis"], line, "axis")
         keep = el.flag(a["keepdims"], line, "keepdims")
         return el.op(kind, [x], {"axes": tuple(axes), "keepdims": keep}, line)
@@ -966,7 +1212,7 @@ def _reduce(kind):
 
 
 def _transpose(el, a, line):
-    x = el.tensor(a["x"], line)
+    x = el.arg(a["x"], line)
     if a["perm"] is None:
         if x.type.rank < 2:
             raise MiraSyntaxError(f"line {line}: transpose() of a rank-{x.type.rank} tensor needs a perm")
@@ -978,7 +1224,7 @@ def _transpose(el, a, line):
 
 
 def _reshape(el, a, line):
-    x = el.tensor(a["x"], line)
+    x = el.arg(a["x"], line)
     shape = el.ints(a["shape"], line, "shape")
     if shape.count(-1) > 1:
         raise MiraSyntaxError(f"line {line}: reshape: at most one dimension can be -1")
@@ -991,7 +1237,7 @@ def _reshape(el, a, line):
 
 
 def _flatten(el, a, line):
-    x = el.tensor(a["x"], line)
+    x = el.arg(a["x"], line)
     ax = el.int_(a["axis"], line, "axis")
     if not -(x.type.rank + 1) <= ax <= x.type.rank:
         raise MiraSyntaxError(f"line {line}: flatten axis {ax} out of range for {x.type}")
@@ -1006,12 +1252,12 @@ def _conv2d(el, a, line):
         attrs["dilation"] = el.pair(a["dilation"], line, "dilation")
     if a["groups"] != 1:
         attrs["groups"] = el.int_(a["groups"], line, "groups")
-    return el.op("conv2d", [el.tensor(a["x"], line), el.tensor(a["w"], line)], attrs, line)
+    return el.op("conv2d", [el.arg(a["x"], line), el.arg(a["w"], line)], attrs, line)
 
 
 def _pool_input(el, a, line, fill: float) -> Value:
     """Padding for pooling is an explicit pad: -inf for max pooling so that it never wins."""
-    x = el.tensor(a["x"], line)
+    x = el.arg(a["x"], line)
     ph, pw = el.pair(a["padding"], line, "padding")
     if ph or pw:
         x = el.op("pad", [x], {"pads": ((0, 0), (0, 0), (ph, ph), (pw, pw)), "value": fill}, line)
@@ -1036,18 +1282,18 @@ def _avgpool(el, a, line):
 
 
 def _softmax(el, a, line):
-    return el.op("softmax", [el.tensor(a["x"], line)], {"axis": el.int_(a["axis"], line, "axis")}, line)
+    return el.op("softmax", [el.arg(a["x"], line)], {"axis": el.int_(a["axis"], line, "axis")}, line)
 
 
 def _matmul(el, a, line):
-    return el.op("matmul", [el.tensor(a["a"], line), el.tensor(a["b"], line)], {}, line)
+    return el.op("matmul", [el.arg(a["a"], line), el.arg(a["b"], line)], {}, line)
 
 
 def _layernorm(el, a, line):
     eps = a["eps"]
     if not _num(eps):
         raise MiraSyntaxError(f"line {line}: layernorm eps must be a number")
-    ins = [el.tensor(a[k], line) for k in ("x", "gamma", "beta")]
+    ins = [el.arg(a[k], line) for k in ("x", "gamma", "beta")]
     return el.op("layernorm", ins, {"eps": float(eps)}, line)
 
 
@@ -1055,17 +1301,17 @@ def _concat(el, a, line):
     xs = a["xs"]
     if not isinstance(xs, list) or not xs:
         raise MiraSyntaxError(f"line {line}: concat() takes a non-empty list of tensors")
-    return el.op("concat", [el.tensor(v, line) for v in xs], {"axis": el.int_(a["axis"], line, "axis")}, line)
+    return el.op("concat", [el.arg(v, line) for v in xs], {"axis": el.int_(a["axis"], line, "axis")}, line)
 
 
 def _cast(el, a, line):
-    x = el.tensor(a["x"], line)
+    x = el.arg(a["x"], line)
     dt = el.dtype(a["dtype"], line)
     return x if x.type.dtype == dt else el.op("cast", [x], {"dtype": dt}, line)
 
 
 def _slice(el, a, line):
-    return el.op("slice", [el.tensor(a["x"], line)], {"begin": tuple(el.ints(a["begin"], line, "begin")),
+    return el.op("slice", [el.arg(a["x"], line)], {"begin": tuple(el.ints(a["begin"], line, "begin")),
                                                      "size": tuple(el.ints(a["size"], line, "size"))}, line)
 
 
@@ -1078,15 +1324,15 @@ def _pad(el, a, line):
         if not _num(a["value"]):
             raise MiraSyntaxError(f"line {line}: pad value must be a number")
         attrs["value"] = float(a["value"])
-    return el.op("pad", [el.tensor(a["x"], line)], attrs, line)
+    return el.op("pad", [el.arg(a["x"], line)], attrs, line)
 
 
 def _broadcast_fn(el, a, line):
-    return el.op("broadcast", [el.tensor(a["x"], line)], {"shape": tuple(el.ints(a["shape"], line, "shape"))}, line)
+    return el.op("broadcast", [el.arg(a["x"], line)], {"shape": tuple(el.ints(a["shape"], line, "shape"))}, line)
 
 
 def _gather(el, a, line):
-    return el.op("gather", [el.tensor(a["x"], line), el.tensor(a["indices"], line, "i32")],
+    return el.op("gather", [el.arg(a["x"], line), el.arg(a["indices"], line, "i32")],
                  {"axis": el.int_(a["axis"], line, "axis")}, line)
 
 
@@ -1100,7 +1346,7 @@ def _where(el, a, line):
 
 
 def _size(el, a, line):
-    x = el.tensor(a["x"], line)
+    x = el.arg(a["x"], line)
     ax = el.int_(a["axis"], line, "axis")
     if not -x.type.rank <= ax < x.type.rank:
         raise MiraSyntaxError(f"line {line}: axis {ax} out of range for {x.type}")
@@ -1109,15 +1355,35 @@ def _size(el, a, line):
 
 def _axis_op(kind):
     return ([("x", _REQUIRED), ("axis", -1)],
-            lambda el, a, line: el.op(kind, [el.tensor(a["x"], line)], {"axis": el.int_(a["axis"], line, "axis")},
+            lambda el, a, line: el.op(kind, [el.arg(a["x"], line)], {"axis": el.int_(a["axis"], line, "axis")},
                                       line))
 
 
 def _arg(kind):
     def h(el, a, line):
         attrs = {"axis": el.int_(a["axis"], line, "axis"), "keepdims": el.flag(a["keepdims"], line, "keepdims")}
-        return el.op(kind, [el.tensor(a["x"], line)], attrs, line)
+        return el.op(kind, [el.arg(a["x"], line)], attrs, line)
     return [("x", _REQUIRED), ("axis", -1), ("keepdims", False)], h
+
+
+def _start(el, v, line) -> Value:
+    """A start position: an i32 tensor, or a list of ints and one-element i32 tensors."""
+    if isinstance(v, Value):
+        return el.local(v)
+    if not isinstance(v, list):
+        raise MiraSyntaxError(f"line {line}: a start position is a list like [t, 0] or an i32 tensor")
+    return el.start_vector([el.local(p) if isinstance(p, Value) else el.int_(p, line, "start") for p in v], line)
+
+
+def _dynamic_slice(el, a, line):
+    return el.op("dynamic_slice", [el.arg(a["x"], line), _start(el, a["start"], line)],
+                 {"size": tuple(el.ints(a["size"], line, "size"))}, line)
+
+
+def _dynamic_update_slice(el, a, line):
+    x = el.arg(a["x"], line)
+    upd = el.tensor(a["update"], line, x.type.dtype)
+    return el.op("dynamic_update_slice", [x, upd, _start(el, a["start"], line)], {}, line)
 
 
 def _filled(value):
@@ -1165,6 +1431,9 @@ BUILTINS = {
     "ones": ([("shape", _REQUIRED), ("dtype", DType("f32"))], _filled(1)),
     "full": ([("shape", _REQUIRED), ("value", _REQUIRED), ("dtype", DType("f32"))], _filled(None)),
     "arange": ([("start", _REQUIRED), ("stop", None), ("dtype", DType("i32"))], _arange),
+    "dynamic_slice": ([("x", _REQUIRED), ("start", _REQUIRED), ("size", _REQUIRED)], _dynamic_slice),
+    "dynamic_update_slice": ([("x", _REQUIRED), ("update", _REQUIRED), ("start", _REQUIRED)],
+                             _dynamic_update_slice),
     "sort": _axis_op("sort"),
     "cumprod": _axis_op("cumprod"),
     "argmax": _arg("argmax"),

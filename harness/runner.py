@@ -10,7 +10,10 @@ it; segments run in order, each taking host arrays in and giving host arrays
 out.
 
 The grouping is simpler than MIRA's list scheduler: ops stay in program order
-and consecutive ops on one device form a segment.
+and consecutive ops on one device form a segment.  A control op (if / while) runs
+on the host segment that holds it; each of its sub-graphs is split and compiled the
+same way, so the ops of a loop body run on the target (mira/partition.py:74-75,
+mira/backends/cpu.py:18-51).
 """
 from __future__ import annotations
 
@@ -48,7 +51,7 @@ def split(g: Graph, target, cpu_name: str = "cpu") -> tuple:
         device[op] = target.name if why is None else cpu_name
         if why is not None:
             reasons[op] = why
-    while True:
+    while target.name != cpu_name:      # the cpu target keeps everything (mira/partition.py:77-87)
         light = [ops for dev, ops in _groups(compute, device) if dev == target.name
                  and not any(op.kind in HEAVY for op in ops)]
         if not light:
@@ -79,11 +82,19 @@ class Runner:
         self.graph = g
         self.segments, self.reasons = split(g, target, getattr(fallback, "name", "cpu"))
         self.timings: list = []
+        # outputs that are constants belong to no segment (a branch returning a literal)
+        self.const_outputs = {op.result: op.attrs["value"] for op in g.ops
+                              if op.kind == "const" and op.result in g.outputs}
+
+        def compile_sub(sub: Graph) -> "Runner":       # if / while sub-graphs, split the same way
+            return Runner(sub, target, fallback)
+
         for seg in self.segments:
             if seg.device == target.name:
-                seg.executable = target.compile(seg.graph)
+                seg.executable = target.compile(seg.graph) if not any(op.is_control for op in seg.graph.ops) \
+                    else target.compile(seg.graph, compile_sub)
             elif fallback is not None:
-                seg.executable = fallback.compile(seg.graph)
+                seg.executable = fallback.compile(seg.graph, compile_sub)
             else:
                 bad = sorted({f"{op.kind}: {self.reasons.get(op, '?')}" for op in seg.graph.compute_ops()})
                 raise RuntimeError("these ops need a CPU fallback target and none was given: " + "; ".join(bad))
@@ -93,7 +104,7 @@ class Runner:
         return [s.device for s in self.segments]
 
     def run_env(self, feeds: dict) -> dict:
-        env = dict(feeds)
+        env = {**self.const_outputs, **feeds}
         self.timings = []
         for seg in self.segments:
             t0 = time.perf_counter()
@@ -101,10 +112,35 @@ class Runner:
             self.timings.append((seg.device, time.perf_counter() - t0))
         return env
 
+    def run_values(self, arrays: list) -> list:
+        """Outputs in order from the inputs' arrays in order (how a control op runs a sub-graph)."""
+        env = self.run_env(dict(zip(self.graph.inputs, arrays)))
+        return [env[v] for v in self.graph.outputs]
+
     def run(self, feeds: dict) -> list:
         """Outputs in order from {input name: array}."""
         env = self.run_env({v: feeds[v.name] for v in self.graph.inputs})
         return [env[v] for v in self.graph.outputs]
+
+    def placements(self) -> list:
+        """(device, op kind) of every compute op, those of control ops' sub-graphs included."""
+        out = []
+        for seg in self.segments:
+            out += [(seg.device, op.kind) for op in seg.graph.compute_ops()]
+            for sub in getattr(seg.executable, "sub", {}).values():
+                out += sub.placements()
+        return out
+
+    def summary_lines(self, indent: str = "  ") -> list:
+        lines = []
+        for i, seg in enumerate(self.segments):
+            ins = ", ".join(f"{v!r}:{v.type}" for v in seg.graph.inputs)
+            lines.append(f"{indent}[{i}] {seg.device:<8} {len(seg.graph.compute_ops()):3d} ops   inputs: {ins}")
+            lines.append(f"{indent}    " + seg.executable.report().replace("\n", f"\n{indent}    "))
+            for (op, name), sub in getattr(seg.executable, "sub", {}).items():
+                lines.append(f"{indent}    {op.kind} {name}: {sub.graph.name}")
+                lines += sub.summary_lines(indent + "      ")
+        return lines
 
     def executables(self, device: Optional[str] = None) -> list:
         return [s.executable for s in self.segments if device is None or s.device == device]

@@ -246,6 +246,11 @@ def dequantize(a: dict) -> np.ndarray:
 
 # ---------------------------------------------------------------- selection (mira/ops.py:426-458)
 
+def _clamped_starts(start, shape, size) -> list:
+    """mira/ops.py:538-539: each runtime start clamped so the window fits its axis."""
+    return [int(min(max(int(b), 0), d - n)) for b, d, n in zip(np.asarray(start).ravel(), shape, size)]
+
+
 def slice_(xs: list, a: dict) -> np.ndarray:
     """mira/ops.py:457-458: the box [begin, begin + size) of every axis, copied."""
     return xs[0][tuple(slice(b, b + n) for b, n in zip(a["begin"], a["size"]))].copy()
@@ -301,6 +306,14 @@ def evaluate(kind: str, xs: list, a: dict) -> np.ndarray:
         return where(xs, a)
     if kind == "broadcast":
         return np.broadcast_to(xs[0], a["shape"]).copy()                  # mira/ops.py:443
+    if kind == "dynamic_slice":                                           # mira/ops.py:551-554
+        st = _clamped_starts(xs[1], xs[0].shape, a["size"])
+        return xs[0][tuple(slice(b, b + n) for b, n in zip(st, a["size"]))].copy()
+    if kind == "dynamic_update_slice":                                    # mira/ops.py:567-572
+        st = _clamped_starts(xs[2], xs[0].shape, xs[1].shape)
+        out = xs[0].copy()
+        out[tuple(slice(b, b + n) for b, n in zip(st, xs[1].shape))] = xs[1]
+        return out
     if kind == "sort":
         return np.sort(xs[0], axis=a["axis"])                             # mira/ops.py:419
     if kind == "cumprod":
@@ -314,19 +327,45 @@ def evaluate(kind: str, xs: list, a: dict) -> np.ndarray:
 # ---------------------------------------------------------------- graph execution (mira/backends/cpu.py:28-36)
 
 class CPUExecutable:
-    """mira/backends/cpu.py:18-36 for graphs without control flow."""
+    """mira/backends/cpu.py:18-51: ops in order; an if / while op runs its sub-graphs, here
+    evaluated by the oracle itself."""
 
     def __init__(self, g):
         self.g = g
 
     def run(self, feeds: dict) -> dict:
-        env = dict(feeds)
+        return dict(zip(self.g.outputs, self.run_list([feeds[v] for v in self.g.inputs])))
+
+    def run_list(self, args: list) -> list:
+        env = dict(zip(self.g.inputs, args))
         for op in self.g.ops:
-            env[op.result] = evaluate(op.kind, [env[v] for v in op.inputs], op.attrs)
-        return {v: env[v] for v in self.g.outputs}
+            if op.is_control:
+                env.update(zip(op.results, control(op, [env[v] for v in op.inputs])))
+            else:
+                env[op.result] = evaluate(op.kind, [env[v] for v in op.inputs], op.attrs)
+        return [env[v] for v in self.g.outputs]
 
     def report(self) -> str:
         return f"cpu (oracle): {sum(op.kind not in ('const', 'dequantize') for op in self.g.ops)} ops"
+
+
+def control(op, args: list) -> list:
+    """mira/backends/cpu.py:38-51: `if` runs the branch its one-element condition picks on its
+    captures; `while` runs cond then body on the state (plus each one's captures) until the
+    condition is false, at most max_iters times."""
+    if op.kind == "if":
+        n = op.attrs["n_then"]
+        taken = bool(np.asarray(args[0]).ravel()[0])
+        sub = op.attrs["then"] if taken else op.attrs["else"]
+        return CPUExecutable(sub).run_list(args[1:1 + n] if taken else args[1 + n:])
+    ns, nc = op.attrs["n_state"], op.attrs["n_cond"]
+    state, cond_caps, body_caps = list(args[:ns]), list(args[ns:ns + nc]), list(args[ns + nc:])
+    cond, body = CPUExecutable(op.attrs["cond"]), CPUExecutable(op.attrs["body"])
+    for _ in range(op.attrs["max_iters"]):
+        if not bool(np.asarray(cond.run_list(state + cond_caps)[0]).ravel()[0]):
+            return state
+        state = body.run_list(state + body_caps)
+    raise RuntimeError(f"while loop exceeded {op.attrs['max_iters']} iterations")
 
 
 class CPUTarget:

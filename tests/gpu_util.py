@@ -56,5 +56,8 @@ def oracle_env(g, feeds: dict) -> dict:
     from oracle import golden as G
     env = {v: np.asarray(feeds[v.name]).astype(v.type.np_dtype) for v in g.inputs}
     for op in g.ops:
-        env[op.result] = G.evaluate(op.kind, [env[x] for x in op.inputs], op.attrs)
+        if op.is_control:
+            env.update(zip(op.results, G.control(op, [env[x] for x in op.inputs])))
+        else:
+            env[op.result] = G.evaluate(op.kind, [env[x] for x in op.inputs], op.attrs)
     return env

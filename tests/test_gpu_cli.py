@@ -84,3 +84,28 @@ def test_language_programs_on_rocm(name, precision):
     for k, v in enumerate(prog.graph.outputs):
         assert bits_equal(got[k], env[v]), f"output {k} vs the oracle"
         assert bits_equal(got[k], z[f"out:{tag}:{k}"]), f"output {k} vs MIRA"
+
+
+CONTROL = {"fixed_point": {"N": 4, "M": 6, "tol": 1}, "greedy_lm": {"P": 3, "V": 11, "T": 12, "D": 16, "F": 32, "L": 2}}
+
+
+@pytest.mark.parametrize("precision", ["auto", None])
+@pytest.mark.parametrize("name", sorted(CONTROL))
+def test_control_flow_programs_on_rocm(name, precision):
+    """Runtime if / while programs compiled for rocm: the control ops run on the host (the
+    rocm target does not take control flow, mira/partition.py:74-75) and their sub-graphs are
+    split for rocm like any graph -- the greedy decoder's layernorms run on rocm inside every
+    loop iteration -- and every result equals MIRA's, on the feed and on the negated feed."""
+    z = np.load(os.path.join(GOLDEN, f"mira_lang_{name}.npz"))
+    feed = {k.split(":", 1)[1]: z[k] for k in z.files if k.startswith("feed:")}
+    prog = cli.compile_file(os.path.join(PROGRAMS, name + ".mira"), "rocm", dims=CONTROL[name], precision=precision)
+    placed = prog.runner.placements()
+    assert ("cpu", "while") in placed
+    if name == "greedy_lm":
+        assert ("rocm", "layernorm") in placed, placed
+    tag = "f16" if precision == "auto" else "f32"
+    for suffix, f in (("", feed), ("neg", {k: (-v if v.dtype.kind == "f" else v) for k, v in feed.items()})):
+        print(f"{name} precision={precision} feed{suffix}", flush=True)
+        got = prog.run(dict(f))
+        for k, o in enumerate(got):
+            assert bits_equal(np.asarray(o), z[f"out:{tag}{suffix}:{k}"]), f"output {k} {suffix} vs MIRA"

@@ -307,6 +307,8 @@ def _lang_fixture(name: str):
 
 
 def _norm_ours(v):
+    if hasattr(v, "ops") and hasattr(v, "outputs"):
+        return _graph_ours(v)
     if isinstance(v, np.ndarray):
         return _sha(v)
     if isinstance(v, (np.floating, np.integer)):
@@ -318,6 +320,8 @@ def _norm_ours(v):
 
 def _norm_mira(v):
     if isinstance(v, dict):
+        if "graph" in v:
+            return _graph_mira(v["graph"])
         if "tuple" in v:
             return tuple(_norm_mira(x) for x in v["tuple"])
         if "sha256" in v:
@@ -330,22 +334,27 @@ def _norm_mira(v):
 
 
 def _graph_ours(g) -> tuple:
-    ids = {v: ("input", v.name, v.type.dtype, tuple(v.type.shape)) for v in g.inputs}
+    """(ops, outputs) with values named by position: inputs by (name, type), results by
+    (op index, result index); sub-graphs nested the same way."""
+    ids = {v: ("input", i, v.name, v.type.dtype, tuple(v.type.shape)) for i, v in enumerate(g.inputs)}
     ops = []
     for i, op in enumerate(g.ops):
-        ids[op.result] = i
-        ops.append((op.kind, tuple(ids[x] for x in op.inputs), tuple(op.result.type.shape), op.result.type.dtype,
+        ids.update({r: (i, k) for k, r in enumerate(op.results)})
+        ops.append((op.kind, tuple(ids[x] for x in op.inputs),
+                    tuple((tuple(r.type.shape), r.type.dtype) for r in op.results),
                     {k: _norm_ours(v) for k, v in op.attrs.items()}))
     return ops, [ids[v] for v in g.outputs]
 
 
 def _graph_mira(doc) -> tuple:
-    ids = {i["id"]: ("input", i["name"], i["dtype"], tuple(i["shape"])) for i in doc["inputs"]}
+    ids = {v["id"]: ("input", i, v["name"], v["dtype"], tuple(v["shape"])) for i, v in enumerate(doc["inputs"])}
     ops = []
     for i, op in enumerate(doc["ops"]):
-        ids[op["result"]["id"]] = i
-        ops.append((op["kind"], tuple(ids[x] for x in op["inputs"]), tuple(op["result"]["shape"]),
-                    op["result"]["dtype"], {k: _norm_mira(v) for k, v in op["attrs"].items()}))
+        results = op.get("results", [op["result"]])
+        ids.update({r["id"]: (i, k) for k, r in enumerate(results)})
+        ops.append((op["kind"], tuple(ids[x] for x in op["inputs"]),
+                    tuple((tuple(r["shape"]), r["dtype"]) for r in results),
+                    {k: _norm_mira(v) for k, v in op["attrs"].items()}))
     return ops, [ids[v] for v in doc["outputs"]]
 
 
@@ -404,12 +413,57 @@ def test_language_w8a8_like_mira(name, precision):
         assert bits_equal(np.asarray(r), z[f"out:{tag}:{k}"]), f"output {k}"
 
 
+CONTROL = {"fixed_point": {"N": 4, "M": 6, "tol": 1}, "greedy_lm": {"P": 3, "V": 11, "T": 12, "D": 16, "F": 32, "L": 2}}
+
+
+@pytest.mark.parametrize("name", sorted(CONTROL))
+def test_control_flow_elaborates_like_mira(name):
+    """Runtime if (both branches' changed variables as results, captures as inputs) and while
+    (the assigned tensors as loop state, cond and body capturing what they read), indexed
+    assignment as dynamic_update_slice with a start vector, dynamic_slice, token gathers:
+    the elaborated graph and every nested sub-graph equal MIRA's."""
+    doc, *_ = _lang_fixture(name)
+    g = ML.elaborate(_read(os.path.join(PROGRAMS, name + ".mira")), dims=CONTROL[name])
+    _same_graph(g, doc["elaborated"])
+
+
+@pytest.mark.parametrize("precision", [None, "f16"])
+@pytest.mark.parametrize("name", sorted(CONTROL))
+def test_control_flow_optimizes_and_runs_like_mira(name, precision):
+    """MIRA's optimizer on graphs with sub-graphs (each sub-graph optimized; f16 converts the
+    loop state completely) gives the same graphs; the runner drives the if / while ops on the
+    host and reproduces MIRA's results bit for bit, on the feed and on the negated feed (the
+    other branch), as does the oracle."""
+    doc, feed, _, z = _lang_fixture(name)
+    tag = "f16" if precision else "f32"
+    prog = cli.compile_file(os.path.join(PROGRAMS, name + ".mira"), "cpu", dims=CONTROL[name], precision=precision)
+    _same_graph(prog.graph, doc[tag])
+    neg = {k: (-v if v.dtype.kind == "f" else v) for k, v in feed.items()}
+    for suffix, f in (("", feed), ("neg", neg)):
+        outs = prog.run(dict(f))
+        oracle_outs = G.run_graph(prog.graph, dict(f))
+        for k, (o, r) in enumerate(zip(outs, oracle_outs)):
+            want = z[f"out:{tag}{suffix}:{k}"]
+            assert bits_equal(np.asarray(o), want), f"output {k} {suffix} (host)"
+            assert bits_equal(np.asarray(r), want), f"output {k} {suffix} (oracle)"
+
+
+def test_w8a8_rejects_control_flow():
+    """As MIRA's (mira/quantize.py:84-85): no W8A8 of a program with a runtime loop."""
+    with pytest.raises(cli.CompileError, match="control flow"):
+        cli.compile_file(os.path.join(PROGRAMS, "greedy_lm.mira"), "cpu", dims=CONTROL["greedy_lm"], precision=None,
+                         quantize="w8a8")
+
+
 LANG_ERRORS = [
     ("fn main(x: f32[2]) -> f32[2] { let y = x\n let y = x\n return y }", {}, "'y' is already defined"),
     ("fn main(x: f32[2]) -> f32[2] { z = x\n return x }", {}, "undefined variable 'z'"),
-    ("fn main(x: f32[2]) -> f32[2] { while x > 0 { x = x - 1 }\n return x }", {}, "'while' is control flow"),
-    ("fn main(x: f32[2]) -> f32[2] { if max(x) > 0 { x = -x }\n return x }", {}, "'if' on a runtime tensor"),
-    ("fn main(x: f32[2]) -> f32[2] { x[0] = 1\n return x }", {}, "indexed assignment"),
+    ("fn main(x: f32[2]) -> f32[2] { while x > 0 { x = x - 1 }\n return x }", {}, "must be a single value"),
+    ("fn main(x: f32[2]) -> f32[2] { let k = 1\n if max(x) > 0 { k = 2 }\n return x * k }", {},
+     "'k' is a compile-time value"),
+    ("fn main(x: f32[2]) -> f32[2] { y[0] = 1\n return x }", {}, "undefined variable 'y'"),
+    ("fn main(x: f32[2]) -> f32[2] { let t = zeros([], i32)\n while t < 3 { t = t + 1.5 }\n return x }", {},
+     "does not mix with an i32 tensor"),
     ("fn main(x: f32[2]) -> f32[2] { return grad(sum(x), x) }", {}, "grad() is not supported"),
     ("fn main(x: f32[2]) -> f32[2] { return x[0:0] }", {}, "empty slice 0:0"),
     ("fn main(x: f32[2]) -> f32[2] { return x[2] }", {}, "index 2 is out of range"),
