@@ -219,8 +219,8 @@ def evaluate(kind: str, xs: list, a: dict) -> np.ndarray:
     raise NotImplementedError(f"no host evaluation for '{kind}'")
 
 
-def _sub_runner(graph):
-    return lambda arrays: [run(graph, dict(zip(graph.inputs, arrays)))[v] for v in graph.outputs]
+def _sub_runner(graph, watch=None, peaks=None):
+    return lambda arrays: [run(graph, dict(zip(graph.inputs, arrays)), watch, peaks)[v] for v in graph.outputs]
 
 
 def run(g, feeds: dict, watch: Optional[set] = None, peaks: Optional[dict] = None, subs: Optional[dict] = None) -> dict:
@@ -230,12 +230,14 @@ def run(g, feeds: dict, watch: Optional[set] = None, peaks: Optional[dict] = Non
     env = {v: np.asarray(feeds[v]).astype(v.type.np_dtype) for v in g.inputs}
     for op in g.ops:
         if op.is_control:
-            sub = {n: subs[(op, n)] if subs else _sub_runner(sg) for n, sg in op.subgraphs()}
+            sub = {n: subs[(op, n)] if subs else _sub_runner(sg, watch, peaks) for n, sg in op.subgraphs()}
             env.update(zip(op.results, run_control(op, [env[x] for x in op.inputs], sub)))
             continue
         env[op.result] = evaluate(op.kind, [env[x] for x in op.inputs], op.attrs)
     if watch:
         for v in watch:
+            if v not in env:          # computed in another graph (a sub-graph's own run folds it)
+                continue
             m = float(np.abs(_f32(env[v])).max()) if np.size(env[v]) else 0.0
             peaks[v] = max(peaks.get(v, 0.0), m)
     return env

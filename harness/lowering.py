@@ -300,23 +300,39 @@ def _w8a8_weight(op: Op) -> Optional[tuple]:
     return None
 
 
+def _graphs(g: Graph) -> list:
+    """g and every if / while sub-graph inside it, outermost first."""
+    out = [g]
+    for op in g.ops:
+        for _, sg in op.subgraphs():
+            out += _graphs(sg)
+    return out
+
+
 def w8a8_candidates(g: Graph) -> list:
-    return [op for op in g.ops if _w8a8_weight(op) is not None]
+    """Candidates in program order; those inside an if / while sub-graph come at that op's place
+    (sub-graphs in MIRA's order: then, else / cond, body)."""
+    out = []
+    for op in g.ops:
+        if _w8a8_weight(op) is not None:
+            out.append(op)
+        for _, sg in op.subgraphs():
+            out += w8a8_candidates(sg)
+    return out
 
 
 def calibrate(g: Graph, feeds: Sequence[dict]) -> list:
     """Peak |x| of each W8A8 candidate's activation over the calibration feeds ({input name:
     array}), one float per candidate in program order (so a same-shaped graph at another
-    batch size can take them)."""
-    if any(op.is_control for op in g.ops):
-        raise ValueError("W8A8 quantization doesn't support programs with data-dependent control flow "
-                         "(mira/quantize.py:84-85)")
+    batch size can take them).  Candidates inside loop bodies and branches fold their peak over
+    every iteration of every feed; one whose branch never runs keeps a peak of 0 (x_scale 1).
+    MIRA's rewrite stops at control flow (mira/quantize.py:84-85); this one calibrates through it."""
     cands = w8a8_candidates(g)
     watch = {op.inputs[0] for op in cands}
     peaks: dict = {}
     for feed in feeds:
         hosteval.run(g, {v: feed[v.name] for v in g.inputs}, watch, peaks)
-    return [peaks[op.inputs[0]] for op in cands]
+    return [peaks.get(op.inputs[0], 0.0) for op in cands]
 
 
 def w8a8(g: Graph, calibration: Optional[Sequence[dict]] = None, peaks: Optional[Sequence[float]] = None) -> list:
@@ -337,7 +353,8 @@ def w8a8(g: Graph, calibration: Optional[Sequence[dict]] = None, peaks: Optional
         op.kind = "qmatmul" if op.kind == "matmul" else "qconv2d"
         op.inputs = [op.inputs[0]] + op.inputs[2:]
         op.attrs = attrs
-    g.prune()
+    for sg in _graphs(g):
+        sg.prune()
     g.check()
     return list(peaks)
 

@@ -109,3 +109,26 @@ def test_control_flow_programs_on_rocm(name, precision):
         got = prog.run(dict(f))
         for k, o in enumerate(got):
             assert bits_equal(np.asarray(o), z[f"out:{tag}{suffix}:{k}"]), f"output {k} {suffix} vs MIRA"
+
+
+@pytest.mark.parametrize("precision", ["auto", None])
+def test_w8a8_loop_body_on_rocm(precision):
+    """The greedy decoder W8A8-quantized through its while loop (calibration folded over every
+    iteration): 11 of its 13 loop-body q-matmuls and its layernorms run on rocm inside every
+    iteration of the host-driven loop (the two whose epilogue is gelu, a libm call, stay on the
+    host in the exact mode), and the decoded tokens equal the oracle's evaluation of the same
+    quantized program."""
+    dims = CONTROL["greedy_lm"]
+    rng = np.random.default_rng(5)
+    calib = [{"prompt": rng.integers(0, dims["V"], dims["P"]).astype(np.int32)} for _ in range(2)]
+    prog = cli.compile_file(os.path.join(PROGRAMS, "greedy_lm.mira"), "rocm", dims=dims, precision=precision,
+                            quantize="w8a8", calibration=calib)
+    placed = prog.runner.placements()
+    assert placed.count(("rocm", "qmatmul")) == 11 and placed.count(("cpu", "qmatmul")) == 2, placed
+    assert ("rocm", "layernorm") in placed
+    for prompt in ([3, 7, 1], [0, 10, 5]):
+        feed = {"prompt": np.array(prompt, np.int32)}
+        print(f"greedy_lm w8a8 precision={precision} prompt={prompt}", flush=True)
+        (got,) = prog.run(dict(feed))
+        want = oracle_env(prog.graph, feed)[prog.graph.outputs[0]]
+        assert bits_equal(np.asarray(got), want), (got, want)

@@ -448,11 +448,49 @@ def test_control_flow_optimizes_and_runs_like_mira(name, precision):
             assert bits_equal(np.asarray(r), want), f"output {k} {suffix} (oracle)"
 
 
-def test_w8a8_rejects_control_flow():
-    """As MIRA's (mira/quantize.py:84-85): no W8A8 of a program with a runtime loop."""
-    with pytest.raises(cli.CompileError, match="control flow"):
-        cli.compile_file(os.path.join(PROGRAMS, "greedy_lm.mira"), "cpu", dims=CONTROL["greedy_lm"], precision=None,
-                         quantize="w8a8")
+def test_w8a8_calibrates_loop_bodies(monkeypatch):
+    """Beyond MIRA (whose rewrite stops at control flow, mira/quantize.py:84-85): the matmuls
+    inside the greedy decoder's while body are W8A8 candidates, each calibrated on the largest
+    |activation| over every iteration of every calibration feed.  The peaks are checked against
+    the oracle's own loop, instrumented to record every value of every iteration; the rewritten
+    program then runs on the host exactly as the oracle evaluates it."""
+    path = os.path.join(PROGRAMS, "greedy_lm.mira")
+    dims = CONTROL["greedy_lm"]
+    g = cli.load_graph(path, "main", None, dims, 0, None)
+    LW.prepare(g)
+    cands = LW.w8a8_candidates(g)
+    (loop,) = [op for op in g.ops if op.kind == "while"]
+    in_body = [op for op in cands if op in loop.attrs["body"].ops]
+    assert len(in_body) == 2 * 6 + 1 and len(cands) == len(in_body)     # 6 per layer, 2 layers, the head
+    rng = np.random.default_rng(5)
+    calib = [{"prompt": rng.integers(0, dims["V"], dims["P"]).astype(np.int32)} for _ in range(2)]
+    watch = {op.inputs[0] for op in cands}
+    seen: dict = {}
+
+    def run_list(self, args):
+        env = dict(zip(self.g.inputs, args))
+        for op in self.g.ops:
+            if op.is_control:
+                env.update(zip(op.results, G.control(op, [env[v] for v in op.inputs])))
+            else:
+                env[op.result] = G.evaluate(op.kind, [env[v] for v in op.inputs], op.attrs)
+        for v in watch & env.keys():
+            seen[v] = max(seen.get(v, 0.0), float(np.abs(env[v].astype(np.float32)).max()))
+        return [env[v] for v in self.g.outputs]
+
+    monkeypatch.setattr(G.CPUExecutable, "run_list", run_list)
+    for feed in calib:
+        G.run_graph(g, feed)
+    monkeypatch.undo()
+    assert LW.calibrate(g, calib) == [seen[op.inputs[0]] for op in cands]
+    prog = cli.compile_file(path, "cpu", dims=dims, precision=None, quantize="w8a8", calibration=calib)
+    body = next(o for o in prog.graph.ops if o.kind == "while").attrs["body"]
+    kinds = [op.kind for op in body.ops]
+    assert kinds.count("qmatmul") == 13 and "matmul" in kinds        # the attention's runtime products stay f32
+    feed = {"prompt": np.array([3, 7, 1], np.int32)}
+    (host,) = prog.run(feed)
+    (oracle,) = G.run_graph(prog.graph, feed)
+    assert bits_equal(host, oracle)
 
 
 LANG_ERRORS = [
