@@ -596,9 +596,16 @@ class _Ctx:
         self.parent = parent
         self.captures: dict = {}          # outer value -> its placeholder input here
         self.captured_outer: list = []    # the outer values, in input order
+        self._owned: set = set()          # inputs and results of the ops seen so far
+        self._synced = 0
 
     def owns(self, v: Value) -> bool:
-        return v in self.graph.inputs or (v.producer is not None and v.producer in self.graph.ops)
+        ops = self.graph.ops
+        for op in ops[self._synced:]:
+            self._owned.update(op.results)
+        self._synced = len(ops)
+        self._owned.update(self.graph.inputs)
+        return v in self._owned
 
 
 class Elaborator:
