@@ -22,7 +22,7 @@ from typing import Optional
 
 from .graph import Graph
 
-HEAVY = {"matmul", "conv2d", "qmatmul", "qconv2d", "softmax", "layernorm", "maxpool2d"}
+HEAVY = {"matmul", "conv2d", "qmatmul", "qconv2d", "softmax", "layernorm", "maxpool2d", "while", "if"}
 
 
 class Segment:

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MR_ABI_VERSION 10
+#define MR_ABI_VERSION 11
 
 enum mr_status {
   MR_OK = 0,
@@ -317,6 +317,25 @@ int mr_maxpool2d_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c,
  * reduce_mean): y[i] = f32(f16(x[i])), round to nearest even, over n floats
  * (y == x allowed).  f16 tensors stay stored as f32 on the device. */
 int mr_round_f16_f32(const float* x, int64_t n, float* y, void* stream);
+
+/* The functions of mr_elementwise_f32 beyond the epilogue codes MR_EPI_ADD .. MR_EPI_RELU. */
+enum mr_ew_fn {
+  MR_EW_GREATER = 11,
+  MR_EW_GREATER_EQUAL = 12,
+  MR_EW_EQUAL = 13,
+  MR_EW_NEG = 14,
+  MR_EW_ABS = 15
+};
+
+/* Replaces mira/ops.py:163-169 for one standalone elementwise op (add, sub, mul, div,
+ * maximum, minimum, greater, greater_equal, equal; relu, neg, abs) inside a loop the
+ * target runs on the device: y[i] over an output of shape[4] (rank <= 4, leading 1s),
+ * a and b read at the element strides a_stride[4] / b_stride[4] (0 on broadcast axes;
+ * b and b_stride unused by unary functions), computed in f32 with NumPy's float32
+ * semantics (NaN through maximum / minimum, comparisons giving 1 / 0), rounded to f16
+ * when round_f16 is set.  Host arrays shape / a_stride / b_stride are read at the call. */
+int mr_elementwise_f32(int32_t fn, const float* a, const int64_t* a_stride, const float* b, const int64_t* b_stride,
+                       float* y, const int64_t* shape, int32_t round_f16, void* stream);
 
 /* mira/ops.py:318-343 reduce_mean over H,W (NumPy order: pairwise f32 sum,
  * then f32(f64(sum) / count)).  NHWC f32 [n,hw,c] -> [n,c]; optional int8.

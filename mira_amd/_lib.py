@@ -10,7 +10,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "libmira_rocm.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 MAX_EPI = 8
 
 # enum mr_epi_fn
@@ -21,6 +21,10 @@ EPI_APPROX = ("gelu", "sigmoid", "tanh")     # libm steps: not bit-identical to 
 EPI_OUT_F16 = 1     # mr_epilogue.flags: round results to f16 (the op's dtype is f16)
 EPI_OUT_H16 = 2     # ... and store them as IEEE halves (out_f32 points to halves)
 EPI_FULL_H16 = 4    # full-shape operands hold IEEE halves
+# enum mr_ew_fn (mr_elementwise_f32 beyond the epilogue codes)
+EW_FN = {"add": 1, "sub": 2, "mul": 3, "div": 4, "maximum": 5, "minimum": 6, "relu": 7,
+         "greater": 11, "greater_equal": 12, "equal": 13, "neg": 14, "abs": 15}
+EW_UNARY = ("relu", "neg", "abs")
 # enum mr_bcast
 BC_SCALAR, BC_COL, BC_ROW, BC_FULL = 0, 1, 2, 3
 
@@ -32,7 +36,7 @@ EXPORTS = [
     "mr_maxpool2d_f32", "mr_mean_hw_f32", "mr_pad_hw_f32", "mr_round_f16_f32",
     "mr_nchw_to_nhwc_f32", "mr_nchw_to_nhwc_pad_f32", "mr_nhwc_to_nchw_f32",
     "mr_layernorm_f32", "mr_softmax_f32", "mr_bmm_f32", "mr_transpose_f32", "mr_copy_rows_f32",
-    "mr_attention_decode_f32", "mr_decode_embed", "mr_decode_commit",
+    "mr_attention_decode_f32", "mr_decode_embed", "mr_decode_commit", "mr_elementwise_f32",
 ]
 DECODE_MAX_CACHES = 16      # MR_DECODE_MAX_CACHES
 
@@ -101,6 +105,7 @@ _SIGS = {
     "mr_attention_decode_f32": ([_p, _i64, _p, _p, _i64, _i64, _p, _i64, _p, _i64, _p, _f32, _i64, _i32, _i32, _i32, _p,
                                  _i64, _p, _i64, _f32, _p], C.c_int),
     "mr_decode_embed": ([_p, _i64, _p, _p, _p, _i32, _p, _i32, _i32, _p, _i64, _p, _f32, _p], C.c_int),
+    "mr_elementwise_f32": ([_i32, _p, C.POINTER(_i64), _p, C.POINTER(_i64), _p, C.POINTER(_i64), _i32, _p], C.c_int),
     "mr_decode_commit": ([_p, _i64, _i32, _i32, _p, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _i32, _i32, _i64, _p],
                          C.c_int),
 }

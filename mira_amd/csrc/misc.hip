@@ -200,6 +200,48 @@ __global__ void __launch_bounds__(256) round_f16_kernel(const float* __restrict_
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) y[i] = round_f16(x[i]);
 }
 
+// ---------------------------------------------------------------- standalone elementwise
+
+// An elementwise op over an output of rank <= 4 (dims n[0..3], leading 1s), each operand
+// read through element strides (0 on its broadcast axes): mira/ops.py:163-169, computed in
+// f32 as NumPy does for float32 operands, then rounded to f16 for an f16 op.  Comparisons
+// give 1 / 0 (mira/ops.py:134-140).
+struct EwShape {
+  int64_t n[4];
+  int64_t sa[4];
+  int64_t sb[4];
+};
+
+__device__ __forceinline__ float ew_apply(int fn, float a, float b) {
+  switch (fn) {
+    case MR_EPI_RELU: return np_maximum(a, 0.0f);
+    case MR_EW_GREATER: return a > b ? 1.0f : 0.0f;
+    case MR_EW_GREATER_EQUAL: return a >= b ? 1.0f : 0.0f;
+    case MR_EW_EQUAL: return a == b ? 1.0f : 0.0f;
+    case MR_EW_NEG: return -a;
+    case MR_EW_ABS: return fabsf(a);
+    default: return epi_binary(fn, a, b);
+  }
+}
+
+__global__ void __launch_bounds__(256) elementwise_kernel(int fn, const float* __restrict__ a,
+                                                          const float* __restrict__ b, float* __restrict__ y,
+                                                          const EwShape sh, int64_t total, int f16) {
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total; i += stride) {
+    int64_t r = i, ia = 0, ib = 0;
+#pragma unroll
+    for (int d = 3; d >= 0; --d) {
+      const int64_t c = r % sh.n[d];
+      r /= sh.n[d];
+      ia += c * sh.sa[d];
+      ib += c * sh.sb[d];
+    }
+    float v = ew_apply(fn, a[ia], b ? b[ib] : 0.0f);
+    y[i] = f16 ? round_f16(v) : v;
+  }
+}
+
 // ---------------------------------------------------------------- maxpool
 
 template <typename Idx>
@@ -460,6 +502,30 @@ int mr_round_f16_f32(const float* x, int64_t n, float* y, void* stream) {
   hipLaunchKernelGGL(mr::round_f16_kernel, dim3(mr::grid_1d(n, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
                      x, n, y);
   MR_LAUNCH_CHECK("round_f16");
+  return MR_OK;
+}
+
+int mr_elementwise_f32(int32_t fn, const float* a, const int64_t* a_stride, const float* b, const int64_t* b_stride,
+                       float* y, const int64_t* shape, int32_t round_f16, void* stream) {
+  const bool unary = fn == MR_EPI_RELU || fn == MR_EW_NEG || fn == MR_EW_ABS;
+  const bool binary = (fn >= MR_EPI_ADD && fn <= MR_EPI_MIN) || fn == MR_EW_GREATER || fn == MR_EW_GREATER_EQUAL ||
+                      fn == MR_EW_EQUAL;
+  MR_REQUIRE(unary || binary, "mr_elementwise_f32: unknown function %d", fn);
+  MR_REQUIRE(a && a_stride && y && shape, "mr_elementwise_f32: NULL argument");
+  MR_REQUIRE(!binary || (b && b_stride), "mr_elementwise_f32: a binary function needs b and its strides");
+  mr::EwShape sh = {};
+  int64_t total = 1;
+  for (int d = 0; d < 4; ++d) {
+    MR_REQUIRE(shape[d] >= 0 && a_stride[d] >= 0 && (!binary || b_stride[d] >= 0), "mr_elementwise_f32: bad shape");
+    sh.n[d] = shape[d];
+    sh.sa[d] = a_stride[d];
+    sh.sb[d] = binary ? b_stride[d] : 0;
+    total *= shape[d];
+  }
+  if (total == 0) return MR_OK;
+  hipLaunchKernelGGL(mr::elementwise_kernel, dim3(mr::grid_1d(total, 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), fn, a, binary ? b : nullptr, y, sh, total, round_f16 ? 1 : 0);
+  MR_LAUNCH_CHECK("elementwise");
   return MR_OK;
 }
 

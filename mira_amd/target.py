@@ -143,10 +143,16 @@ def _ptr(t) -> int:
 MAX_EXACT_K = 133144
 
 
+# a device loop (a while / if the target runs) carries float values of at most this rank
+LOOP_MAX_RANK = 3
+
+
 class RocmTarget:
     """MIRA Target for one MI355X (gfx950)."""
     name = "rocm"
-    supports_control_flow = False
+    # while / if ops whose sub-graphs run here entirely run as device loops
+    # (mira/partition.py:74-75); others stay with the host, their sub-graphs split as usual
+    supports_control_flow = True
 
     def __init__(self, device: int = 0, debug_acc: bool = False, approx_f32: bool = False):
         """approx_f32: also run the float ops whose NumPy results depend on libm or on BLAS's
@@ -162,7 +168,7 @@ class RocmTarget:
     def check(self, op: "Op") -> Optional[str]:
         """None if the rocm kernels run `op` with the golden model's exact arithmetic."""
         if op.is_control:
-            return "control flow runs on the host"
+            return self._check_control(op)
         if any(r.type.dtype not in FLOAT_DTYPES for r in op.results):
             return "the rocm target computes f32 and f16 graphs only"
         k = op.kind
@@ -328,7 +334,37 @@ class RocmTarget:
                 return f"runtime epilogue operand {v.type} broadcasts onto {list(shape)} in a way rocm can't index"
         return None
 
-    def compile(self, g: "Graph") -> "RocmExecutable":
+    def _check_control(self, op: "Op") -> Optional[str]:
+        """A while / if runs as a device loop when its values are floats of rank <= 3 and
+        every op of its sub-graphs runs here (standalone elementwise ops included)."""
+        for _, sg in op.subgraphs():
+            for v in [*op.inputs, *op.results, *sg.inputs, *sg.outputs]:
+                if v.type.dtype not in FLOAT_DTYPES:
+                    return "control flow with integer values runs on the host (its sub-graphs split for rocm)"
+                if v.type.rank > LOOP_MAX_RANK:
+                    return f"a device loop carries values of rank <= {LOOP_MAX_RANK}"
+            for sop in sg.ops:
+                if sop.is_constant_like:
+                    continue
+                why = self.check_in_loop(sop)
+                if why is not None:
+                    return f"control flow whose sub-graph holds {sop.kind} ({why}) runs on the host"
+        return None
+
+    def check_in_loop(self, op: "Op") -> Optional[str]:
+        """check() for an op of a device loop's sub-graph: also standalone elementwise ops
+        (mr_elementwise_f32), which elsewhere stay with their neighbours on the host."""
+        if op.kind in L.EW_FN:
+            if any(v.type.dtype not in FLOAT_DTYPES for v in [*op.inputs, *op.results]):
+                return "elementwise ops run on rocm for f32 and f16"
+            if op.result.type.rank > 4:
+                return "elementwise ops run on rocm for rank <= 4"
+            return None
+        return self.check(op)
+
+    def compile(self, g: "Graph", compile_sub=None) -> "RocmExecutable":
+        """compile_sub (MIRA's sub-graph compiler) is not needed: a device loop's sub-graphs are
+        compiled here."""
         return RocmExecutable(g, self)
 
 
@@ -351,7 +387,7 @@ def _bcast_mode(oshape: tuple, rshape: tuple, is_conv: bool) -> Optional[int]:
 class RocmExecutable:
     """A compiled rocm segment: device buffers, packed constants and a launch list."""
 
-    def __init__(self, g: "Graph", target: RocmTarget):
+    def __init__(self, g: "Graph", target: RocmTarget, in_loop: bool = False):
         torch = _t()
         self.g = g
         self.target = target
@@ -363,7 +399,7 @@ class RocmExecutable:
         L.check(self.lib.mr_init(target.device), "mr_init")
         for op in g.ops:
             if not op.is_constant_like:
-                reason = target.check(op)
+                reason = target.check_in_loop(op) if in_loop else target.check(op)
                 if reason:
                     raise L.RocmError(f"rocm cannot run {op.kind}: {reason}")
         self.launches: list[tuple[str, Callable[[int], None]]] = []
@@ -1761,6 +1797,116 @@ class RocmExecutable:
             at += inner
         self._publish(out, y)
 
+    def _emit_elementwise(self, op: "Op") -> None:
+        """A standalone elementwise op of a device loop (mira/ops.py:163-169): one
+        mr_elementwise_f32 launch over the C-order result, operands broadcast by strides."""
+        import ctypes as C
+        fn = L.EW_FN[op.kind]
+        shape = tuple(op.result.type.shape)
+        full = (1,) * (4 - len(shape)) + shape
+
+        def operand(v):
+            """v's buffer as a view of v's shape and its element strides padded to rank 4
+            (0 on broadcast axes); a strided view (a column slice of a shared-input q-op's
+            result) is read through its own strides."""
+            t = self._c_order(v)
+            try:
+                t = t.view(v.type.shape) if tuple(t.shape) != tuple(v.type.shape) else t
+            except RuntimeError:
+                raise L.RocmError(f"elementwise operand {v} is not addressable as {v.type}") from None
+            vs = (1,) * (4 - v.type.rank) + tuple(v.type.shape)
+            ts = (0,) * (4 - v.type.rank) + tuple(t.stride())
+            return t, (C.c_int64 * 4)(*[0 if d == 1 else st for d, st in zip(vs, ts)])
+
+        a, sa = operand(op.inputs[0])
+        b, sb = operand(op.inputs[1]) if op.kind not in L.EW_UNARY else (None, (C.c_int64 * 4)(0, 0, 0, 0))
+        sh = (C.c_int64 * 4)(*full)
+        self.keep += [sa, sb, sh]
+        out, y = self._c_order_out(op)
+        lib, f16 = self.lib, int(op.result.type.dtype == "f16")
+        n = op.result.type.numel
+        self._add("elementwise", lambda s: L.check(lib.mr_elementwise_f32(fn, a.data_ptr(), sa, _ptr(b), sb,
+                                                                          y.data_ptr(), sh, f16, s),
+                                                   "mr_elementwise_f32"),
+                  nbytes=4 * (a.numel() + (b.numel() if b is not None else 0) + n))
+        self._publish(out, y)
+
+    def _loop_results(self, op: "Op") -> list:
+        torch = _t()
+        outs = []
+        for r in op.results:
+            d = self._new_dv(r)
+            if d.f32 is None:
+                d.f32 = torch.empty(r.type.shape, dtype=torch.float32, device=self.dev)
+            outs.append(d)
+        return outs
+
+    @staticmethod
+    def _feed(sub: "RocmExecutable", values: list) -> None:
+        for ph, t in zip(sub.g.inputs, values):
+            sub.device_input(ph).copy_(t.reshape(ph.type.shape))
+
+    def _emit_while(self, op: "Op") -> None:
+        """A while op run on the device (mira/backends/cpu.py:44-51's semantics): the loop
+        state lives in the op's result buffers; each iteration copies state and captures into
+        the cond sub-executable, reads its one-element result back, and if it is non-zero runs
+        the body and copies its outputs into the state.  Nothing but that flag leaves the GPU."""
+        ns, nc = op.attrs["n_state"], op.attrs["n_cond"]
+        cond_g, body_g = op.attrs["cond"], op.attrs["body"]
+        cond = RocmExecutable(cond_g, self.target, in_loop=True)
+        body = RocmExecutable(body_g, self.target, in_loop=True)
+        ins = [self._c_order(v) for v in op.inputs]
+        init, cond_caps, body_caps = ins[:ns], ins[ns:ns + nc], ins[ns + nc:]
+        outs = self._loop_results(op)
+        state = [d.f32 for d in outs]
+        max_iters = int(op.attrs["max_iters"])
+        feed = self._feed
+
+        def run(_stream) -> None:
+            for t, src in zip(state, init):
+                t.copy_(src.reshape(t.shape))
+            for _ in range(max_iters):
+                feed(cond, state + cond_caps)
+                cond.launch()
+                if float(cond.device_output(cond_g.outputs[0]).reshape(-1)[0].item()) == 0.0:
+                    return
+                feed(body, state + body_caps)
+                body.launch()
+                for t, o in zip(state, body_g.outputs):
+                    t.copy_(body.device_output(o).reshape(t.shape))
+            raise L.RocmError(f"while loop exceeded {max_iters} iterations")
+
+        self.keep += [cond, body]
+        self._add("while", run)
+        for d in outs:
+            self._finish_i8(d, None)
+
+    def _emit_if(self, op: "Op") -> None:
+        """An if op run on the device (mira/backends/cpu.py:39-43's semantics): the condition's
+        one element is read back, the taken branch's sub-executable runs on its captures and
+        its outputs are copied into the op's results."""
+        n = op.attrs["n_then"]
+        then_g, else_g = op.attrs["then"], op.attrs["else"]
+        branches = (RocmExecutable(then_g, self.target, in_loop=True),
+                    RocmExecutable(else_g, self.target, in_loop=True))
+        ins = [self._c_order(v) for v in op.inputs]
+        cond, caps = ins[0], (ins[1:1 + n], ins[1 + n:])
+        outs = self._loop_results(op)
+        feed = self._feed
+
+        def run(_stream) -> None:
+            k = 0 if float(cond.reshape(-1)[0].item()) != 0.0 else 1
+            sub = branches[k]
+            feed(sub, caps[k])
+            sub.launch()
+            for d, o in zip(outs, sub.g.outputs):
+                d.f32.copy_(sub.device_output(o).reshape(d.f32.shape))
+
+        self.keep += list(branches)
+        self._add("if", run)
+        for d in outs:
+            self._finish_i8(d, None)
+
     def _emit_bmm(self, op: "Op") -> None:
         """f32 matmul of two float tensors with NumPy's batch broadcasting (mira/ops.py:217-219;
         approx_f32 only), the epilogue fused."""
@@ -1888,3 +2034,8 @@ class RocmExecutable:
         ks = ", ".join(f"{k} x{n}" for k, n in sorted(self.kernel_counts.items()))
         return (f"rocm (MI355X gfx950): {len(self.g.compute_ops())} ops -> {len(self.launches)} kernel launches "
                 f"[{ks}]; {self.const_bytes / 2**20:.2f} MiB of packed constants on device")
+
+
+for _kind in L.EW_FN:
+    if not hasattr(RocmExecutable, f"_emit_{_kind}"):
+        setattr(RocmExecutable, f"_emit_{_kind}", RocmExecutable._emit_elementwise)

@@ -18,7 +18,7 @@ this compiles it with MIRA's own driver (mira/compiler.py:252-312) at fixed dims
 and runs every compiled program with MIRA's cpu target on the stored feed.  Only these data
 files travel; the reference never does.
 
-The programs tests/programs/{fixed_point,greedy_lm}.mira add runtime `if` / `while` (with
+The programs tests/programs/{fixed_point,greedy_lm,device_loop}.mira add runtime `if` / `while` (with
 captures, indexed assignment and dynamic slices); MIRA's W8A8 rewrite rejects control flow, so
 those have the f32 and f16 variants only, each also run on the feed with its float inputs
 negated (the other branch of fixed_point's `if`).
@@ -49,7 +49,8 @@ CASES = [("encoder_block", {"S": 16, "E": 32, "h": 4}),
 # programs with runtime if / while (MIRA's W8A8 rejects control flow: f32 and f16 only); each
 # also runs on the negated feed, which takes the other branch of fixed_point's if
 CONTROL = [("fixed_point", {"N": 4, "M": 6, "tol": 1}),
-           ("greedy_lm", {"P": 3, "V": 11, "T": 12, "D": 16, "F": 32, "L": 2})]
+           ("greedy_lm", {"P": 3, "V": 11, "T": 12, "D": 16, "F": 32, "L": 2}),
+           ("device_loop", {"B": 8, "D": 32, "n": 5})]
 
 
 def _jsonable(v):

@@ -86,7 +86,8 @@ def test_language_programs_on_rocm(name, precision):
         assert bits_equal(got[k], z[f"out:{tag}:{k}"]), f"output {k} vs MIRA"
 
 
-CONTROL = {"fixed_point": {"N": 4, "M": 6, "tol": 1}, "greedy_lm": {"P": 3, "V": 11, "T": 12, "D": 16, "F": 32, "L": 2}}
+CONTROL = {"fixed_point": {"N": 4, "M": 6, "tol": 1}, "greedy_lm": {"P": 3, "V": 11, "T": 12, "D": 16, "F": 32, "L": 2},
+           "device_loop": {"B": 8, "D": 32, "n": 5}}
 
 
 @pytest.mark.parametrize("precision", ["auto", None])
@@ -132,3 +133,27 @@ def test_w8a8_loop_body_on_rocm(precision):
         (got,) = prog.run(dict(feed))
         want = oracle_env(prog.graph, feed)[prog.graph.outputs[0]]
         assert bits_equal(np.asarray(got), want), (got, want)
+
+
+@pytest.mark.parametrize("precision", ["auto", None])
+def test_device_loop_on_rocm(precision):
+    """A while loop with float state, W8A8-quantized through the loop, runs on the device:
+    the while op (and the if nested in its body) is a rocm op, its cond / body / branch
+    sub-graphs nested rocm executables (the q-matmul, its fused epilogue, the standalone
+    mul / add / greater on mr_elementwise_f32), the state in device buffers and one flag
+    read back per iteration.  Both results equal the oracle's evaluation of the same
+    quantized program bit for bit, on two feeds (state reset between runs)."""
+    dims = CONTROL["device_loop"]
+    rng = np.random.default_rng(5)
+    calib = [{"x": rng.standard_normal((dims["B"], dims["D"])).astype(np.float32)} for _ in range(2)]
+    prog = cli.compile_file(os.path.join(PROGRAMS, "device_loop.mira"), "rocm", dims=dims, precision=precision,
+                            quantize="w8a8", calibration=calib)
+    placed = prog.runner.placements()
+    assert ("rocm", "while") in placed and not any(dev == "cpu" for dev, _ in placed), placed
+    for seed in (1, 2):
+        feed = {"x": np.random.default_rng(seed).standard_normal((dims["B"], dims["D"])).astype(np.float32)}
+        print(f"device_loop precision={precision} seed={seed}", flush=True)
+        got = prog.run(dict(feed))
+        env = oracle_env(prog.graph, feed)
+        for k, v in enumerate(prog.graph.outputs):
+            assert bits_equal(np.asarray(got[k]), env[v]), f"output {k}"

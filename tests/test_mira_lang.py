@@ -413,7 +413,8 @@ def test_language_w8a8_like_mira(name, precision):
         assert bits_equal(np.asarray(r), z[f"out:{tag}:{k}"]), f"output {k}"
 
 
-CONTROL = {"fixed_point": {"N": 4, "M": 6, "tol": 1}, "greedy_lm": {"P": 3, "V": 11, "T": 12, "D": 16, "F": 32, "L": 2}}
+CONTROL = {"fixed_point": {"N": 4, "M": 6, "tol": 1}, "greedy_lm": {"P": 3, "V": 11, "T": 12, "D": 16, "F": 32, "L": 2},
+           "device_loop": {"B": 8, "D": 32, "n": 5}}
 
 
 @pytest.mark.parametrize("name", sorted(CONTROL))
@@ -530,3 +531,31 @@ def test_emit_ast_round_trips():
         text = cli.format_module(ML.parse(_read(os.path.join(PROGRAMS, name + ".mira"))))
         assert cli.format_module(ML.parse(text)) == text, name
         _same_graph(ML.elaborate(text, dims=LANG[name]), _lang_fixture(name)[0]["elaborated"])
+
+
+def test_device_loop_decisions():
+    """Which while / if ops the rocm target runs on the device: the float-state loop once
+    W8A8 has made its matmul a q-op (its body's standalone mul / add / greater and nested if
+    accepted there, and only there), in f32 and f16; not while an f32 matmul (BLAS order)
+    remains, and never with integer state (the other programs)."""
+    from mira_amd.target import RocmTarget
+    t = RocmTarget()
+    dims = CONTROL["device_loop"]
+    rng = np.random.default_rng(5)
+    calib = [{"x": rng.standard_normal((dims["B"], dims["D"])).astype(np.float32)} for _ in range(2)]
+    for precision in (None, "f16"):
+        g = cli.load_graph(os.path.join(PROGRAMS, "device_loop.mira"), "main", None, dims, 0, None)
+        LW.prepare(g, precision)
+        loop = next(op for op in g.ops if op.kind == "while")
+        assert "f32 matmul" in t.check(loop)
+        LW.w8a8(g, calib)
+        assert t.check(loop) is None
+        body = [op for op in loop.attrs["body"].ops if op.kind != "const"]
+        assert sorted({op.kind for op in body}) == ["add", "greater", "if", "mul", "qmatmul"]
+        assert t.check(next(op for op in body if op.kind == "mul")) == "'mul' has no rocm kernel"
+        assert t.check_in_loop(next(op for op in body if op.kind == "mul")) is None
+    for name in ("fixed_point", "greedy_lm"):
+        g = cli.load_graph(os.path.join(PROGRAMS, name + ".mira"), "main", None, CONTROL[name], 0, None)
+        LW.prepare(g)
+        loop = next(op for op in g.ops if op.kind == "while")
+        assert "integer values" in t.check(loop)
