@@ -1254,3 +1254,60 @@ def test_int8_epilogue_ties(lib, kind, shape):
                                stream()), "mr_qconv2d")
     sync()
     assert bits_equal(yq.cpu().numpy()[:, :o], G.quantize_activation(want, next_xs).astype(np.int8))
+
+
+# ---------------------------------------------------------------- standalone elementwise (device loops)
+
+EW_SHAPES = [((4, 5), (4, 5)), ((4, 5), (5,)), ((3, 1, 5), (1, 4, 5)), ((), (2, 3)), ((2, 3, 4, 5), (1, 3, 1, 5)),
+             ((7,), ()), ((1,), (6, 1)), ((33, 17), (33, 1))]
+
+
+def _ew_strides(shape, full):
+    pad = (1,) * (4 - len(shape)) + tuple(shape)
+    st, acc = [0, 0, 0, 0], 1
+    for d in range(3, -1, -1):
+        st[d] = 0 if pad[d] == 1 else acc
+        acc *= pad[d]
+    return (C.c_int64 * 4)(*st)
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("fn", sorted(L.EW_FN))
+def test_elementwise(fn, f16):
+    """mr_elementwise_f32 against the oracle's elementwise op (mira/ops.py:163-169) bit for
+    bit: every function, operands broadcast along any axes up to rank 4 (scalars included),
+    NaN / +-inf / +-0 among the inputs, and the f16 rounding of an f16 op."""
+    lib = L.load()
+    rng = np.random.default_rng(L.EW_FN[fn] * 7 + f16)
+    unary = fn in L.EW_UNARY
+    special = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1.0, -1.0, 65504.0], np.float32)
+    for ashape, bshape in EW_SHAPES:
+        a = (rng.standard_normal(ashape) * 3).astype(np.float32)
+        b = (rng.standard_normal(bshape) * 3).astype(np.float32)
+        for x in (a, b):
+            flat = x.reshape(-1)
+            k = min(flat.size, special.size)
+            flat[:k] = rng.permutation(special)[:k]
+        if f16:
+            a, b = a.astype(np.float16), b.astype(np.float16)
+        full = tuple(ashape) if unary else tuple(np.broadcast_shapes(ashape, bshape))
+        pad = (1,) * (4 - len(full)) + full
+        y = empty(full, _torch().float32)
+        at, bt = T(a.astype(np.float32)), T(b.astype(np.float32))
+        print(f"elementwise {fn} f16={f16} {ashape} {bshape}", flush=True)
+        L.check(lib.mr_elementwise_f32(L.EW_FN[fn], at.data_ptr(), _ew_strides(ashape, full),
+                                       None if unary else bt.data_ptr(), None if unary else _ew_strides(bshape, full),
+                                       y.data_ptr(), (C.c_int64 * 4)(*pad), int(f16), stream()), "mr_elementwise_f32")
+        sync()
+        want = G.evaluate(fn, [a] if unary else [a, b], {}).astype(np.float32)
+        assert bits_equal(y.cpu().numpy(), want), (fn, ashape, bshape)
+
+
+def test_elementwise_rejects():
+    lib = L.load()
+    x = empty((4,), _torch().float32)
+    st = (C.c_int64 * 4)(0, 0, 0, 1)
+    sh = (C.c_int64 * 4)(1, 1, 1, 4)
+    assert lib.mr_elementwise_f32(99, x.data_ptr(), st, x.data_ptr(), st, x.data_ptr(), sh, 0, stream()) != 0
+    assert lib.mr_elementwise_f32(L.EW_FN["add"], x.data_ptr(), st, None, None, x.data_ptr(), sh, 0, stream()) != 0
+    assert lib.mr_elementwise_f32(L.EW_FN["neg"], None, st, None, None, x.data_ptr(), sh, 0, stream()) != 0
