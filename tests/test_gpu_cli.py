@@ -157,3 +157,24 @@ def test_device_loop_on_rocm(precision):
         env = oracle_env(prog.graph, feed)
         for k, v in enumerate(prog.graph.outputs):
             assert bits_equal(np.asarray(got[k]), env[v]), f"output {k}"
+
+
+def test_device_loop_iteration_limit():
+    """A device while loop that would run past its max_iters raises after that many
+    iterations (mira/backends/cpu.py:51), every kernel finishing normally: the limit is
+    forced from the host on the compiled graph (5 iterations needed, 3 allowed)."""
+    from harness import lowering as LW
+    from harness.runner import Runner
+    from mira_amd._lib import RocmError
+    from mira_amd.target import RocmTarget
+    dims = CONTROL["device_loop"]
+    rng = np.random.default_rng(5)
+    calib = [{"x": rng.standard_normal((dims["B"], dims["D"])).astype(np.float32)} for _ in range(2)]
+    g = cli.load_graph(os.path.join(PROGRAMS, "device_loop.mira"), "main", None, dims, 0, None)
+    LW.prepare(g)
+    LW.w8a8(g, calib)
+    next(op for op in g.ops if op.kind == "while").attrs["max_iters"] = 3
+    runner = Runner(g, RocmTarget())
+    assert runner.devices == ["rocm"]
+    with pytest.raises(RocmError, match="exceeded 3 iterations"):
+        runner.run({"x": calib[0]["x"]})
