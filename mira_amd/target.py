@@ -1850,7 +1850,9 @@ class RocmExecutable:
         """A while op run on the device (mira/backends/cpu.py:44-51's semantics): the loop
         state lives in the op's result buffers; each iteration copies state and captures into
         the cond sub-executable, reads its one-element result back, and if it is non-zero runs
-        the body and copies its outputs into the state.  Nothing but that flag leaves the GPU."""
+        the body and copies its outputs into the state.  Nothing but that flag leaves the GPU;
+        reading it synchronises the stream, so an executable holding a device loop is not
+        captured into a HIP graph."""
         ns, nc = op.attrs["n_state"], op.attrs["n_cond"]
         cond_g, body_g = op.attrs["cond"], op.attrs["body"]
         cond = RocmExecutable(cond_g, self.target, in_loop=True)
