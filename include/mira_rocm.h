@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MR_ABI_VERSION 11
+#define MR_ABI_VERSION 12
 
 enum mr_status {
   MR_OK = 0,
@@ -336,6 +336,49 @@ enum mr_ew_fn {
  * when round_f16 is set.  Host arrays shape / a_stride / b_stride are read at the call. */
 int mr_elementwise_f32(int32_t fn, const float* a, const int64_t* a_stride, const float* b, const int64_t* b_stride,
                        float* y, const int64_t* shape, int32_t round_f16, void* stream);
+
+/* ---- device loops: integer and data-movement ops ------------------------
+ * Inside a while / if the target runs on the device, every value is 4 bytes per
+ * element: f32, f16 values held as f32, and i32 values held as their own bits in the
+ * same buffers.  Positions read from device memory are clamped into range. */
+
+enum mr_dtype { MR_DT_F32 = 0, MR_DT_F16 = 1, MR_DT_I32 = 2 };
+
+/* mr_elementwise_f32 for i32 operands (mira/ops.py:163-169 with integers exact): add,
+ * sub, mul wrapping around; maximum, minimum, greater, greater_equal, equal (1 / 0);
+ * relu, neg, abs. */
+int mr_elementwise_i32(int32_t fn, const int32_t* a, const int64_t* a_stride, const int32_t* b,
+                       const int64_t* b_stride, int32_t* y, const int64_t* shape, void* stream);
+
+/* Replaces mira/ops.py:405-406 between i32 and f32 / f16 over n elements: integers round
+ * to nearest (to f16 in one rounding); floats truncate toward zero, NaN, infinities and
+ * values outside int32 giving INT_MIN (NumPy on x86). */
+int mr_cast_32(const void* x, int64_t n, int32_t from, int32_t to, void* y, void* stream);
+
+/* Replaces mira/ops.py:479-484 gather along axis 0: y[i, :] = table[idx[i], :] over rows of
+ * row_elems 4-byte elements; negative indices count from the end (NumPy's take), indices
+ * still out of range are clamped (NumPy raises). */
+int mr_gather_rows_32(const void* table, int64_t rows, int64_t row_elems, const int32_t* idx, int64_t n_idx,
+                      void* y, void* stream);
+
+/* Replaces mira/ops.py:551-554: y = x[start : start + size] over shape[4] / size[4] (leading
+ * axes 1 up to the value's rank), start a device i32[rank] clamped as mira/ops.py:538-539. */
+int mr_dynamic_slice_32(const void* x, const int64_t* shape, const int32_t* start, int32_t rank,
+                        const int64_t* size, void* y, void* stream);
+
+/* Replaces mira/ops.py:567-572: y = x with the window [start, start + size) replaced by upd
+ * (y != x), start clamped as above. */
+int mr_dynamic_update_slice_32(const void* x, const int64_t* shape, const void* upd, const int64_t* size,
+                               const int32_t* start, int32_t rank, void* y, void* stream);
+
+/* Replaces mira/ops.py:527-528 argmax over the last axis of rows x n f32 values: the first
+ * index of the maximum, the first NaN if there is one. */
+int mr_argmax_f32(const float* x, int64_t rows, int64_t n, int32_t* y, void* stream);
+
+/* Replaces mira/ops.py:432-433: y = where(cond != 0, a, b) over shape[4], all three read
+ * through broadcast strides; cond_int: cond holds i32 (else f32, true when non-zero or NaN). */
+int mr_where_32(const void* cond, int32_t cond_int, const int64_t* c_stride, const void* a, const int64_t* a_stride,
+                const void* b, const int64_t* b_stride, void* y, const int64_t* shape, void* stream);
 
 /* mira/ops.py:318-343 reduce_mean over H,W (NumPy order: pairwise f32 sum,
  * then f32(f64(sum) / count)).  NHWC f32 [n,hw,c] -> [n,c]; optional int8.

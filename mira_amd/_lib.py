@@ -10,7 +10,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "libmira_rocm.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 MAX_EPI = 8
 
 # enum mr_epi_fn
@@ -37,7 +37,10 @@ EXPORTS = [
     "mr_nchw_to_nhwc_f32", "mr_nchw_to_nhwc_pad_f32", "mr_nhwc_to_nchw_f32",
     "mr_layernorm_f32", "mr_softmax_f32", "mr_bmm_f32", "mr_transpose_f32", "mr_copy_rows_f32",
     "mr_attention_decode_f32", "mr_decode_embed", "mr_decode_commit", "mr_elementwise_f32",
+    "mr_elementwise_i32", "mr_cast_32", "mr_gather_rows_32", "mr_dynamic_slice_32", "mr_dynamic_update_slice_32",
+    "mr_argmax_f32", "mr_where_32",
 ]
+DT = {"f32": 0, "f16": 1, "i32": 2}       # enum mr_dtype
 DECODE_MAX_CACHES = 16      # MR_DECODE_MAX_CACHES
 
 
@@ -105,6 +108,14 @@ _SIGS = {
     "mr_attention_decode_f32": ([_p, _i64, _p, _p, _i64, _i64, _p, _i64, _p, _i64, _p, _f32, _i64, _i32, _i32, _i32, _p,
                                  _i64, _p, _i64, _f32, _p], C.c_int),
     "mr_decode_embed": ([_p, _i64, _p, _p, _p, _i32, _p, _i32, _i32, _p, _i64, _p, _f32, _p], C.c_int),
+    "mr_elementwise_i32": ([_i32, _p, C.POINTER(_i64), _p, C.POINTER(_i64), _p, C.POINTER(_i64), _p], C.c_int),
+    "mr_cast_32": ([_p, _i64, _i32, _i32, _p, _p], C.c_int),
+    "mr_gather_rows_32": ([_p, _i64, _i64, _p, _i64, _p, _p], C.c_int),
+    "mr_dynamic_slice_32": ([_p, C.POINTER(_i64), _p, _i32, C.POINTER(_i64), _p, _p], C.c_int),
+    "mr_dynamic_update_slice_32": ([_p, C.POINTER(_i64), _p, C.POINTER(_i64), _p, _i32, _p, _p], C.c_int),
+    "mr_argmax_f32": ([_p, _i64, _i64, _p, _p], C.c_int),
+    "mr_where_32": ([_p, _i32, C.POINTER(_i64), _p, C.POINTER(_i64), _p, C.POINTER(_i64), _p, C.POINTER(_i64), _p],
+                    C.c_int),
     "mr_elementwise_f32": ([_i32, _p, C.POINTER(_i64), _p, C.POINTER(_i64), _p, C.POINTER(_i64), _i32, _p], C.c_int),
     "mr_decode_commit": ([_p, _i64, _i32, _i32, _p, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _i32, _i32, _i64, _p],
                          C.c_int),

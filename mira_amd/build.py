@@ -22,7 +22,7 @@ CSRC = PKG / "csrc"
 LIB = PKG / "libmira_rocm.so"
 ARCH = "gfx950"
 
-SOURCES = ["abi.hip", "quantize.hip", "qgemm.hip", "qgemv.hip", "w8gemm.hip", "misc.hip", "stem.hip", "decode.hip", "expand_dw.hip"]
+SOURCES = ["abi.hip", "quantize.hip", "qgemm.hip", "qgemv.hip", "w8gemm.hip", "misc.hip", "stem.hip", "decode.hip", "expand_dw.hip", "loop.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -138,12 +138,22 @@ def _ptr(t) -> int:
     return 0 if t is None else t.data_ptr()
 
 
+def _truthy(t, v) -> bool:
+    """A device loop's one-element condition, read back (an i32 value is held as its bits)."""
+    x = t.reshape(-1)[:1]
+    if v.type.dtype == "i32":
+        x = x.view(_t().int32)
+    return bool(x.item() != 0)
+
+
 # Longest contraction whose int32 accumulator cannot overflow: K * 127 * 127 < 2^31
 # (the library rejects longer ones).
 MAX_EXACT_K = 133144
 
 
-# a device loop (a while / if the target runs) carries float values of at most this rank
+# a device loop (a while / if the target runs) carries values of these dtypes and of at
+# most this rank; i32 values are held as their bits in the 4-byte buffers
+LOOP_DTYPES = ("f32", "f16", "i32")
 LOOP_MAX_RANK = 3
 
 
@@ -335,12 +345,12 @@ class RocmTarget:
         return None
 
     def _check_control(self, op: "Op") -> Optional[str]:
-        """A while / if runs as a device loop when its values are floats of rank <= 3 and
-        every op of its sub-graphs runs here (standalone elementwise ops included)."""
+        """A while / if runs as a device loop when its values are f32 / f16 / i32 of rank <= 3
+        and every op of its sub-graphs runs here (check_in_loop)."""
         for _, sg in op.subgraphs():
             for v in [*op.inputs, *op.results, *sg.inputs, *sg.outputs]:
-                if v.type.dtype not in FLOAT_DTYPES:
-                    return "control flow with integer values runs on the host (its sub-graphs split for rocm)"
+                if v.type.dtype not in LOOP_DTYPES:
+                    return f"control flow with {v.type.dtype} values runs on the host (its sub-graphs split for rocm)"
                 if v.type.rank > LOOP_MAX_RANK:
                     return f"a device loop carries values of rank <= {LOOP_MAX_RANK}"
             for sop in sg.ops:
@@ -352,13 +362,32 @@ class RocmTarget:
         return None
 
     def check_in_loop(self, op: "Op") -> Optional[str]:
-        """check() for an op of a device loop's sub-graph: also standalone elementwise ops
-        (mr_elementwise_f32), which elsewhere stay with their neighbours on the host."""
-        if op.kind in L.EW_FN:
-            if any(v.type.dtype not in FLOAT_DTYPES for v in [*op.inputs, *op.results]):
-                return "elementwise ops run on rocm for f32 and f16"
-            if op.result.type.rank > 4:
-                return "elementwise ops run on rocm for rank <= 4"
+        """check() for an op of a device loop's sub-graph, which may also hold what a loop's
+        bookkeeping needs and elsewhere stays on the host: standalone elementwise ops (f32 /
+        f16 / i32), casts to and from i32, gathers along axis 0, dynamic slices and updates,
+        argmax over the last axis, where, static slices, and reshapes / concats of i32."""
+        vals = [*op.inputs, *op.results]
+        k = op.kind
+        if any(v.type.dtype not in LOOP_DTYPES for v in vals):
+            return "device loops hold f32, f16 and i32 values"
+        if any(v.type.rank > 4 for v in vals):
+            return "device loops hold values of rank <= 4"
+        ints = any(v.type.dtype == "i32" for v in vals)
+        if k in L.EW_FN:
+            if len({v.type.dtype for v in op.inputs}) != 1 or (ints and k == "div"):
+                return "elementwise operands of one dtype (no integer division)"
+            return None
+        if k == "cast":
+            return None
+        if k == "gather":
+            return None if op.attrs["axis"] % op.inputs[0].type.rank == 0 else "gather runs on rocm along axis 0"
+        if k in ("dynamic_slice", "dynamic_update_slice", "where", "slice"):
+            return None
+        if k == "argmax":
+            x = op.inputs[0]
+            return None if x.type.dtype in FLOAT_DTYPES and op.attrs["axis"] % x.type.rank == x.type.rank - 1 else \
+                "argmax runs on rocm over the last axis of a float tensor"
+        if k in ("reshape", "concat") and ints:
             return None
         return self.check(op)
 
@@ -1045,7 +1074,8 @@ class RocmExecutable:
         """A constant used as a data input: upload it in its device layout."""
         if v in self.dv:
             return self.dv[v]
-        a = self._const_value(v).astype(np.float32)
+        a = self._const_value(v)
+        a = a.astype(np.int32).view(np.float32) if v.type.dtype == "i32" else a.astype(np.float32)
         d = DevValue(v, nhwc=v in self.images)
         d.f32 = self._upload(a.transpose(0, 2, 3, 1) if d.nhwc else a)
         self.dv[v] = d
@@ -1609,6 +1639,18 @@ class RocmExecutable:
         values are already stored as f32, so the result shares the input's buffers."""
         x = self._src(op.inputs[0])
         r = op.result
+        if "i32" in (r.type.dtype, op.inputs[0].type.dtype):     # device loops: through mr_cast_32
+            if r.type.dtype == op.inputs[0].type.dtype:
+                self.dv[r] = DevValue(r, nhwc=False, f32=x.f32)
+                return
+            xt = self._c_order(op.inputs[0])
+            out, y = self._c_order_out(op)
+            lib, n = self.lib, r.type.numel
+            src, dst = L.DT[op.inputs[0].type.dtype], L.DT[r.type.dtype]
+            self._add("cast", lambda s: L.check(lib.mr_cast_32(xt.data_ptr(), n, src, dst, y.data_ptr(), s),
+                                                "mr_cast_32"), nbytes=8 * n)
+            self._publish(out, y)
+            return
         if op in self.input_casts or r.type.dtype == "f32" or op.inputs[0].type.dtype == "f16":
             self.dv[r] = DevValue(r, nhwc=x.nhwc, f32=x.f32, i8=x.i8)
             self._finish_i8(self.dv[r], None)
@@ -1825,10 +1867,116 @@ class RocmExecutable:
         out, y = self._c_order_out(op)
         lib, f16 = self.lib, int(op.result.type.dtype == "f16")
         n = op.result.type.numel
-        self._add("elementwise", lambda s: L.check(lib.mr_elementwise_f32(fn, a.data_ptr(), sa, _ptr(b), sb,
-                                                                          y.data_ptr(), sh, f16, s),
-                                                   "mr_elementwise_f32"),
-                  nbytes=4 * (a.numel() + (b.numel() if b is not None else 0) + n))
+        nbytes = 4 * (a.numel() + (b.numel() if b is not None else 0) + n)
+        if op.inputs[0].type.dtype == "i32":
+            self._add("elementwise", lambda s: L.check(lib.mr_elementwise_i32(fn, a.data_ptr(), sa, _ptr(b), sb,
+                                                                              y.data_ptr(), sh, s),
+                                                       "mr_elementwise_i32"), nbytes=nbytes)
+        else:
+            self._add("elementwise", lambda s: L.check(lib.mr_elementwise_f32(fn, a.data_ptr(), sa, _ptr(b), sb,
+                                                                              y.data_ptr(), sh, f16, s),
+                                                       "mr_elementwise_f32"), nbytes=nbytes)
+        self._publish(out, y)
+
+    @staticmethod
+    def _shape4(shape) -> object:
+        import ctypes as C
+        return (C.c_int64 * 4)(*((1,) * (4 - len(shape)) + tuple(shape)))
+
+    def _bcast4(self, v, full) -> tuple:
+        """v's C-order buffer and its element strides broadcast onto `full` (rank <= 4)."""
+        import ctypes as C
+        t = self._c_order(v)
+        try:
+            t = t.view(v.type.shape) if tuple(t.shape) != tuple(v.type.shape) else t
+        except RuntimeError:
+            raise L.RocmError(f"operand {v} is not addressable as {v.type}") from None
+        vs = (1,) * (4 - v.type.rank) + tuple(v.type.shape)
+        ts = (0,) * (4 - v.type.rank) + tuple(t.stride())
+        st = (C.c_int64 * 4)(*[0 if d == 1 else x for d, x in zip(vs, ts)])
+        self.keep.append(st)
+        return t, st
+
+    def _emit_gather(self, op: "Op") -> None:
+        """mira/ops.py:479-484 along axis 0: rows of the table picked by i32 indices."""
+        table, idx, r = op.inputs[0], op.inputs[1], op.result
+        tt, it = self._c_order(table), self._c_order(idx)
+        rows = table.type.shape[0]
+        row = int(np.prod(table.type.shape[1:], dtype=np.int64))
+        out, y = self._c_order_out(op)
+        lib, n_idx = self.lib, idx.type.numel
+        self._add("gather", lambda s: L.check(lib.mr_gather_rows_32(tt.data_ptr(), rows, row, it.data_ptr(), n_idx,
+                                                                    y.data_ptr(), s), "mr_gather_rows_32"),
+                  nbytes=4 * (n_idx + 2 * n_idx * row))
+        self._publish(out, y)
+
+    def _window_start(self, start_v) -> object:
+        return self._c_order(start_v)
+
+    def _emit_dynamic_slice(self, op: "Op") -> None:
+        """mira/ops.py:551-554: the window at a runtime start (an i32 vector on the device)."""
+        x, r = op.inputs[0], op.result
+        xt, st = self._c_order(x), self._window_start(op.inputs[1])
+        shape, size = self._shape4(x.type.shape), self._shape4(op.attrs["size"])
+        self.keep += [shape, size]
+        out, y = self._c_order_out(op)
+        lib, rank = self.lib, x.type.rank
+        self._add("dynamic_slice", lambda s: L.check(lib.mr_dynamic_slice_32(
+            xt.data_ptr(), shape, st.data_ptr(), rank, size, y.data_ptr(), s), "mr_dynamic_slice_32"),
+            nbytes=8 * r.type.numel)
+        self._publish(out, y)
+
+    def _emit_slice(self, op: "Op") -> None:
+        """mira/ops.py:457-458: a static window, through the dynamic-slice kernel with a
+        constant start."""
+        x, r = op.inputs[0], op.result
+        xt = self._c_order(x)
+        st = self._upload(np.asarray(op.attrs["begin"], np.int32))
+        shape, size = self._shape4(x.type.shape), self._shape4(op.attrs["size"])
+        self.keep += [shape, size]
+        out, y = self._c_order_out(op)
+        lib, rank = self.lib, x.type.rank
+        self._add("slice", lambda s: L.check(lib.mr_dynamic_slice_32(
+            xt.data_ptr(), shape, st.data_ptr(), rank, size, y.data_ptr(), s), "mr_dynamic_slice_32"),
+            nbytes=8 * r.type.numel)
+        self._publish(out, y)
+
+    def _emit_dynamic_update_slice(self, op: "Op") -> None:
+        """mira/ops.py:567-572: a copy of x with the window at a runtime start replaced."""
+        x, upd, r = op.inputs[0], op.inputs[1], op.result
+        xt, ut, st = self._c_order(x), self._c_order(upd), self._window_start(op.inputs[2])
+        shape, size = self._shape4(x.type.shape), self._shape4(upd.type.shape)
+        self.keep += [shape, size]
+        out, y = self._c_order_out(op)
+        lib, rank = self.lib, x.type.rank
+        self._add("dynamic_update_slice", lambda s: L.check(lib.mr_dynamic_update_slice_32(
+            xt.data_ptr(), shape, ut.data_ptr(), size, st.data_ptr(), rank, y.data_ptr(), s),
+            "mr_dynamic_update_slice_32"), nbytes=8 * r.type.numel)
+        self._publish(out, y)
+
+    def _emit_argmax(self, op: "Op") -> None:
+        """mira/ops.py:527-528 over the last axis (first maximum, first NaN)."""
+        x, r = op.inputs[0], op.result
+        xt = self._c_order(x)
+        n = x.type.shape[-1]
+        rows = x.type.numel // n
+        out, y = self._c_order_out(op)
+        lib = self.lib
+        self._add("argmax", lambda s: L.check(lib.mr_argmax_f32(xt.data_ptr(), rows, n, y.data_ptr(), s),
+                                              "mr_argmax_f32"), nbytes=4 * (rows * n + rows))
+        self._publish(out, y)
+
+    def _emit_where(self, op: "Op") -> None:
+        """mira/ops.py:432-433, the three operands broadcast by strides."""
+        full = tuple(op.result.type.shape)
+        (ct, cs), (at, as_), (bt, bs) = (self._bcast4(v, full) for v in op.inputs)
+        sh = self._shape4(full)
+        self.keep.append(sh)
+        out, y = self._c_order_out(op)
+        lib, cint = self.lib, int(op.inputs[0].type.dtype == "i32")
+        self._add("where", lambda s: L.check(lib.mr_where_32(ct.data_ptr(), cint, cs, at.data_ptr(), as_,
+                                                             bt.data_ptr(), bs, y.data_ptr(), sh, s), "mr_where_32"),
+                  nbytes=16 * op.result.type.numel)
         self._publish(out, y)
 
     def _loop_results(self, op: "Op") -> list:
@@ -1870,7 +2018,7 @@ class RocmExecutable:
             for _ in range(max_iters):
                 feed(cond, state + cond_caps)
                 cond.launch()
-                if float(cond.device_output(cond_g.outputs[0]).reshape(-1)[0].item()) == 0.0:
+                if not _truthy(cond.device_output(cond_g.outputs[0]), cond_g.outputs[0]):
                     return
                 feed(body, state + body_caps)
                 body.launch()
@@ -1897,7 +2045,7 @@ class RocmExecutable:
         feed = self._feed
 
         def run(_stream) -> None:
-            k = 0 if float(cond.reshape(-1)[0].item()) != 0.0 else 1
+            k = 0 if _truthy(cond, op.inputs[0]) else 1
             sub = branches[k]
             feed(sub, caps[k])
             sub.launch()
@@ -1960,7 +2108,10 @@ class RocmExecutable:
         if self._upload_done is not None:
             self._upload_done.synchronize()       # the pinned buffers are free again
         for v in self.g.inputs:
-            arr = np.ascontiguousarray(np.asarray(feeds[v], dtype=np.float32)).reshape(-1)
+            if v.type.dtype == "i32":      # held as its bits (device loops)
+                arr = np.ascontiguousarray(np.asarray(feeds[v], dtype=np.int32)).view(np.float32).reshape(-1)
+            else:
+                arr = np.ascontiguousarray(np.asarray(feeds[v], dtype=np.float32)).reshape(-1)
             if arr.size != v.type.numel:
                 raise ValueError(f"input {v}: {arr.size} elements for {v.type}")
             pin = self._pinned.get(v)
@@ -2014,7 +2165,8 @@ class RocmExecutable:
                                                      torch.cuda.current_stream(self.dev).cuda_stream),
                         "mr_nhwc_to_nchw_f32")
                 t = canon
-            out[v] = t.reshape(v.type.shape).cpu().numpy().astype(v.type.np_dtype)
+            host = t.reshape(v.type.shape).cpu().numpy()
+            out[v] = host.view(np.int32) if v.type.dtype == "i32" else host.astype(v.type.np_dtype)
         return out
 
     def run(self, feeds: dict) -> dict:

@@ -178,3 +178,34 @@ def test_device_loop_iteration_limit():
     assert runner.devices == ["rocm"]
     with pytest.raises(RocmError, match="exceeded 3 iterations"):
         runner.run({"x": calib[0]["x"]})
+
+
+@pytest.mark.parametrize("quantize", [None, "w8a8"])
+@pytest.mark.parametrize("precision", [None, "f16"])
+def test_greedy_decoder_device_loop(precision, quantize):
+    """The greedy KV-cache decoder's while loop run on the device in the approximate mode:
+    token buffer, step counter, embedding gathers, position and cache windows (dynamic
+    slices and updates), masks, attention, argmax and the prompt-or-prediction where, all
+    on rocm with the integer state held in device buffers.  The decoded tokens equal the
+    oracle's (the attention's f32 products and softmax agree to f32 rounding, which moves no
+    argmax here), for two prompts."""
+    from harness import hosteval, lowering as LW
+    from harness.runner import Runner
+    from mira_amd.target import RocmTarget
+    dims = CONTROL["greedy_lm"]
+    g = cli.load_graph(os.path.join(PROGRAMS, "greedy_lm.mira"), "main", None, dims, 0, None)
+    LW.prepare(g, precision)
+    if quantize:
+        rng = np.random.default_rng(5)
+        LW.w8a8(g, [{"prompt": rng.integers(0, dims["V"], dims["P"]).astype(np.int32)} for _ in range(2)])
+    runner = Runner(g, RocmTarget(approx_f32=True), fallback=hosteval.HostTarget())
+    placed = runner.placements()
+    # the loop on rocm; before it, the prompt's write into the token buffer (an integer op
+    # outside any loop) on the host
+    assert placed == [("cpu", "dynamic_update_slice"), ("rocm", "while")], placed
+    for prompt in ([3, 7, 1], [0, 10, 5]):
+        feed = {"prompt": np.array(prompt, np.int32)}
+        print(f"greedy_lm device loop precision={precision} quantize={quantize} prompt={prompt}", flush=True)
+        (got,) = runner.run(dict(feed))
+        want = oracle_env(g, feed)[g.outputs[0]]
+        assert np.array_equal(np.asarray(got), want), (got, want)

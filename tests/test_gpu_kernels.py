@@ -1311,3 +1311,126 @@ def test_elementwise_rejects():
     assert lib.mr_elementwise_f32(99, x.data_ptr(), st, x.data_ptr(), st, x.data_ptr(), sh, 0, stream()) != 0
     assert lib.mr_elementwise_f32(L.EW_FN["add"], x.data_ptr(), st, None, None, x.data_ptr(), sh, 0, stream()) != 0
     assert lib.mr_elementwise_f32(L.EW_FN["neg"], None, st, None, None, x.data_ptr(), sh, 0, stream()) != 0
+
+
+# ---------------------------------------------------------------- device-loop kernels (i32 held as bits)
+
+def _bits(a: np.ndarray):
+    """A 4-byte array as the float32 tensor holding its bits (how device loops store i32)."""
+    return T(np.ascontiguousarray(a).view(np.float32))
+
+
+def _unbits(t, dtype) -> np.ndarray:
+    return t.cpu().numpy().view(dtype)
+
+
+def test_elementwise_i32():
+    """mr_elementwise_i32 against the oracle on int32 (NumPy wraps add / sub / mul / neg / abs
+    at the int32 limits): every function but div, broadcast shapes, the extremes."""
+    lib = L.load()
+    rng = np.random.default_rng(21)
+    edge = np.array([np.iinfo(np.int32).min, np.iinfo(np.int32).max, -1, 0, 1, 46341, -46341], np.int32)
+    for fn in sorted(k for k in L.EW_FN if k != "div"):
+        unary = fn in L.EW_UNARY
+        for ashape, bshape in EW_SHAPES:
+            a = rng.integers(-2**31, 2**31, ashape, dtype=np.int64).astype(np.int32)
+            b = rng.integers(-50, 50, bshape, dtype=np.int64).astype(np.int32)
+            for x in (a, b):
+                flat = x.reshape(-1)
+                flat[:min(flat.size, edge.size)] = edge[:min(flat.size, edge.size)]
+            full = tuple(ashape) if unary else tuple(np.broadcast_shapes(ashape, bshape))
+            pad = (1,) * (4 - len(full)) + full
+            y = empty(full, _torch().float32)
+            at, bt = _bits(a), _bits(b)
+            print(f"elementwise_i32 {fn} {ashape} {bshape}", flush=True)
+            L.check(lib.mr_elementwise_i32(L.EW_FN[fn], at.data_ptr(), _ew_strides(ashape, full),
+                                           None if unary else bt.data_ptr(),
+                                           None if unary else _ew_strides(bshape, full),
+                                           y.data_ptr(), (C.c_int64 * 4)(*pad), stream()), "mr_elementwise_i32")
+            sync()
+            with np.errstate(over="ignore"):
+                want = G.evaluate(fn, [a] if unary else [a, b], {})
+            assert np.array_equal(_unbits(y, np.int32), want), (fn, ashape, bshape)
+
+
+def test_cast_32():
+    """mr_cast_32 against NumPy's astype: int32 -> f32 / f16 (one rounding), f32 / f16 ->
+    int32 (toward zero; NaN, infinities and out-of-range values give INT_MIN on x86)."""
+    lib = L.load()
+    ints = np.array([0, 1, -1, 7, 2**24 + 1, -(2**24 + 3), 65519, 65520, 2**31 - 1, -2**31, 123456789], np.int32)
+    floats = np.array([0.0, -0.0, 2.5, -2.5, 0.99, -0.99, 3e9, -3e9, 2147483520.0, -2147483648.0, np.nan, np.inf,
+                       -np.inf, 65504.0, 1e-30], np.float32)
+    for src, dst, x in (("i32", "f32", ints), ("i32", "f16", ints), ("f32", "i32", floats),
+                        ("f16", "i32", floats.astype(np.float16))):
+        y = empty(x.shape, _torch().float32)
+        xt = _bits(x) if src == "i32" else T(x.astype(np.float32))
+        print(f"cast {src} -> {dst}", flush=True)
+        L.check(lib.mr_cast_32(xt.data_ptr(), x.size, L.DT[src], L.DT[dst], y.data_ptr(), stream()), "mr_cast_32")
+        sync()
+        with np.errstate(invalid="ignore"):
+            want = G.evaluate("cast", [x], {"dtype": dst})
+        got = _unbits(y, np.int32) if dst == "i32" else y.cpu().numpy()
+        assert bits_equal(got, want.astype(np.int32 if dst == "i32" else np.float32)), (src, dst, got, want)
+
+
+def test_gather_dynamic_slices_argmax_where():
+    """mr_gather_rows_32 (negative indices from the end), mr_dynamic_slice_32 and
+    mr_dynamic_update_slice_32 (starts out of range clamped, rank 1 to 3), mr_argmax_f32
+    (ties to the first, the first NaN, rows longer than a wave) and mr_where_32 (f32 and
+    i32 conditions, NaN and -0 among them, broadcast) against the oracle bit for bit."""
+    lib = L.load()
+    torch = _torch()
+    rng = np.random.default_rng(31)
+    table = rng.standard_normal((7, 5)).astype(np.float32)
+    idx = np.array([[0, -1], [6, -7], [3, 3]], np.int32)
+    y = empty((3, 2, 5), torch.float32)
+    it = _bits(idx)
+    tt = T(table)
+    L.check(lib.mr_gather_rows_32(tt.data_ptr(), 7, 5, it.data_ptr(), idx.size, y.data_ptr(), stream()), "gather")
+    sync()
+    assert bits_equal(y.cpu().numpy(), G.evaluate("gather", [table, idx], {"axis": 0}))
+    for shape, size, start in (((4, 6, 5), (2, 3, 5), (3, -2, 4)), ((4, 6, 5), (1, 6, 1), (0, 2, 9)),
+                               ((12,), (1,), (11,)), ((12,), (3,), (-5,)), ((3, 8), (3, 2), (1, 7))):
+        x = rng.standard_normal(shape).astype(np.float32)
+        st = np.array(start, np.int32)
+        pad = lambda s: (C.c_int64 * 4)(*((1,) * (4 - len(s)) + tuple(s)))      # noqa: E731
+        xt, stt = T(x), _bits(st)
+        ys = empty(size, torch.float32)
+        print(f"dynamic slice {shape} {size} {start}", flush=True)
+        L.check(lib.mr_dynamic_slice_32(xt.data_ptr(), pad(shape), stt.data_ptr(), len(shape), pad(size),
+                                        ys.data_ptr(), stream()), "dynamic_slice")
+        upd = rng.standard_normal(size).astype(np.float32)
+        ut = T(upd)
+        yu = empty(shape, torch.float32)
+        L.check(lib.mr_dynamic_update_slice_32(xt.data_ptr(), pad(shape), ut.data_ptr(), pad(size), stt.data_ptr(),
+                                               len(shape), yu.data_ptr(), stream()), "dynamic_update_slice")
+        sync()
+        assert bits_equal(ys.cpu().numpy(), G.evaluate("dynamic_slice", [x, st], {"size": size}))
+        assert bits_equal(yu.cpu().numpy(), G.evaluate("dynamic_update_slice", [x, upd, st], {}))
+    for rows, n in ((9, 33), (3, 70), (5, 1), (2, 200)):
+        x = rng.integers(-3, 4, (rows, n)).astype(np.float32)     # many ties
+        x[0, n // 2] = np.nan
+        if rows > 1:
+            x[1, :] = -np.inf
+        if rows > 2 and n > 3:
+            x[2, 3] = np.nan
+            x[2, 1] = np.nan
+        xt = T(x)
+        ya = empty((rows,), torch.float32)
+        print(f"argmax {rows}x{n}", flush=True)
+        L.check(lib.mr_argmax_f32(xt.data_ptr(), rows, n, ya.data_ptr(), stream()), "argmax")
+        sync()
+        assert np.array_equal(_unbits(ya, np.int32), G.evaluate("argmax", [x], {"axis": 1, "keepdims": False}))
+    cond_f = np.array([[0.0], [-0.0], [np.nan], [2.0]], np.float32)
+    cond_i = np.array([[0], [np.iinfo(np.int32).min], [1], [0]], np.int32)
+    a = rng.standard_normal((4, 3)).astype(np.float32)
+    b = rng.standard_normal((1, 3)).astype(np.float32)
+    for cond, cint in ((cond_f, 0), (cond_i, 1)):
+        ct = _bits(cond) if cint else T(cond)
+        at, bt = T(a), T(b)
+        yw = empty((4, 3), torch.float32)
+        L.check(lib.mr_where_32(ct.data_ptr(), cint, _ew_strides(cond.shape, (4, 3)), at.data_ptr(),
+                                _ew_strides(a.shape, (4, 3)), bt.data_ptr(), _ew_strides(b.shape, (4, 3)),
+                                yw.data_ptr(), (C.c_int64 * 4)(1, 1, 4, 3), stream()), "where")
+        sync()
+        assert bits_equal(yw.cpu().numpy(), G.evaluate("where", [cond, a, b], {}))

@@ -536,8 +536,9 @@ def test_emit_ast_round_trips():
 def test_device_loop_decisions():
     """Which while / if ops the rocm target runs on the device: the float-state loop once
     W8A8 has made its matmul a q-op (its body's standalone mul / add / greater and nested if
-    accepted there, and only there), in f32 and f16; not while an f32 matmul (BLAS order)
-    remains, and never with integer state (the other programs)."""
+    accepted there, and only there), in f32 and f16; not while an f32 matmul (BLAS order,
+    exact mode) or an op rocm lacks (reduce_max) remains; the greedy decoder, integer state
+    and all, in the approximate mode."""
     from mira_amd.target import RocmTarget
     t = RocmTarget()
     dims = CONTROL["device_loop"]
@@ -554,8 +555,10 @@ def test_device_loop_decisions():
         assert sorted({op.kind for op in body}) == ["add", "greater", "if", "mul", "qmatmul"]
         assert t.check(next(op for op in body if op.kind == "mul")) == "'mul' has no rocm kernel"
         assert t.check_in_loop(next(op for op in body if op.kind == "mul")) is None
-    for name in ("fixed_point", "greedy_lm"):
+    for name, blocker in (("fixed_point", "reduce_max"), ("greedy_lm", "f32 matmul")):
         g = cli.load_graph(os.path.join(PROGRAMS, name + ".mira"), "main", None, CONTROL[name], 0, None)
         LW.prepare(g)
         loop = next(op for op in g.ops if op.kind == "while")
-        assert "integer values" in t.check(loop)
+        assert blocker in t.check(loop)
+        if name == "greedy_lm":     # integer state, gathers, dynamic windows, argmax: all on rocm
+            assert RocmTarget(approx_f32=True).check(loop) is None
