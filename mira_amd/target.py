@@ -446,6 +446,9 @@ class RocmExecutable:
         g = self.g
         users = g.users()
         self.users = users
+        # producers inside this graph only: an input of a segment split from a larger graph
+        # keeps its producer there, in another segment
+        self.prod = {r: op for op in g.ops for r in op.results}
         self.consts = {op.result: op for op in g.ops if op.is_constant_like}
         # rank-4 values that an image op reads or writes live NHWC on the device; other
         # rank-4 values (attention heads [b, s, h, d], say) keep the graph's C order
@@ -479,9 +482,9 @@ class RocmExecutable:
                 for v in op.inputs[1:]:
                     self.need_f32.add(v)
             elif op.kind == "maxpool2d" and self._foldable_pad(op.inputs[0]):
-                pad_op = op.inputs[0].producer
+                pad_op = self._producer(op.inputs[0])
                 self.folded_pads.add(pad_op)
-                conv = pad_op.inputs[0].producer
+                conv = self._producer(pad_op.inputs[0])
                 if self._stem_fusable(conv, pad_op, op):
                     self.fused_stem[op] = (conv, pad_op)
                     self.skip.add(conv)
@@ -559,16 +562,20 @@ class RocmExecutable:
                 self.consts[w].kind == "dequantize" and x in self.g.inputs and x.type.rank == 4 and
                 x.type.shape[1] % 4 != 0)
 
+    def _producer(self, v: "Value") -> Optional["Op"]:
+        """The op of this graph that makes v (None for the graph's inputs)."""
+        return self.prod.get(v)
+
     def _is_bmm(self, op: "Op") -> bool:
         w = op.inputs[1] if op.kind == "matmul" else None
-        return w is not None and not (w.producer is not None and w.producer.kind == "dequantize")
+        return w is not None and not (self._producer(w) is not None and self._producer(w).kind == "dequantize")
 
     def _view_chain(self, v: "Value") -> tuple:
         """(base, shape, strides, chain): v as a strided view of `base`, the first value up its
         chain of reshapes and transposes that has its own C-order buffer; `chain` lists the
         values passed on the way (v first).  A reshape of a view that is not contiguous stops
         the walk (that value is then the base)."""
-        p = v.producer
+        p = self._producer(v)
         shape = tuple(v.type.shape)
         if p is not None and v not in self.images and p.kind in ("transpose", "reshape") and \
                 p.inputs[0] not in self.images and p.inputs[0] not in self.consts:
@@ -601,7 +608,7 @@ class RocmExecutable:
             if sm.kind != "softmax" or not self._device_op(sm):
                 continue
             sc = sm.inputs[0]
-            A = sc.producer
+            A = self._producer(sc)
             if A is None or A.kind != "matmul" or not self._is_bmm(A) or users.get(sc) != [sm] or sc in g.outputs:
                 continue
             r = sm.result.type.rank
@@ -632,7 +639,7 @@ class RocmExecutable:
                 continue
             cats = []
             for base, user in ((kb, A), (vb, Bop)):
-                c = base.producer
+                c = self._producer(base)
                 if c is None or c.kind != "concat" or c.attrs["axis"] % 3 != 1 or len(c.inputs) != 2 or \
                         base.type.shape != (Bn, T1, D) or not self._only_feeds(base, user):
                     break
@@ -811,7 +818,7 @@ class RocmExecutable:
             if op.kind != "conv2d" or not self._device_op(op) or len(op.inputs) < 2:
                 continue
             v, w = op.inputs[0], op.inputs[1]
-            e = v.producer
+            e = self._producer(v)
             if w not in self.consts or self.consts[w].kind != "const" or e is None or e.kind != "qconv2d":
                 continue
             if not self._device_op(e) or e in self.virtual or v in g.outputs or self.users.get(v, []) != [op]:
@@ -949,7 +956,7 @@ class RocmExecutable:
         5-8 taps, no dilation, an even column stride, a row stride of at most 2, and input rows
         of at most 64 four-pixel groups."""
         x = conv.inputs[0]
-        p = x.producer
+        p = self._producer(x)
         f16 = p is not None and p in self.input_casts
         v = p.inputs[0] if f16 else x
         if v not in self.g.inputs or v in self.g.outputs or x in self.g.outputs:
@@ -989,7 +996,7 @@ class RocmExecutable:
         return True
 
     def _foldable_pad(self, v: "Value") -> bool:
-        p = v.producer
+        p = self._producer(v)
         if p is None or p.kind != "pad" or v in self.g.outputs or len(self.users.get(v, [])) != 1:
             return False
         pads = tuple(tuple(x) for x in p.attrs["pads"])
@@ -1293,7 +1300,7 @@ class RocmExecutable:
 
     def _emit_matmul(self, op: "Op") -> None:
         w = op.inputs[1]
-        if w.producer is not None and w.producer.kind == "dequantize":
+        if self._producer(w) is not None and self._producer(w).kind == "dequantize":
             return self._emit_w8_matmul(op)
         if op in self.attn:
             return self._emit_attention(op)
@@ -1446,7 +1453,7 @@ class RocmExecutable:
         before it (_plan_expand_dw) to _emit_expand_dw."""
         if op in self.expand_dw:
             return self._emit_expand_dw(op, self.expand_dw[op])
-        wp = op.inputs[1].producer
+        wp = self._producer(op.inputs[1])
         if wp is not None and wp.kind == "dequantize" and conv_params(op.attrs)[3] == 1:
             return self._emit_w8_conv2d(op)
         a = op.attrs
@@ -1567,8 +1574,8 @@ class RocmExecutable:
         v = op.inputs[0]
         pt = pl = 0
         pad_value = 0.0
-        if v.producer is not None and v.producer in self.folded_pads:
-            p = v.producer
+        if self._producer(v) is not None and self._producer(v) in self.folded_pads:
+            p = self._producer(v)
             pads = tuple(tuple(x) for x in p.attrs["pads"])
             pt, pl = pads[2][0], pads[3][0]
             pad_value = float(np.asarray(p.attrs.get("value", 0)).astype(np.float32))

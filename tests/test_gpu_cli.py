@@ -209,3 +209,33 @@ def test_greedy_decoder_device_loop(precision, quantize):
         (got,) = runner.run(dict(feed))
         want = oracle_env(g, feed)[g.outputs[0]]
         assert np.array_equal(np.asarray(got), want), (got, want)
+
+
+@pytest.mark.parametrize("quantize", [None, "w8a8"])
+def test_greedy_decoder_host_loop_segments(quantize):
+    """The same decoder with its loop driven from the host and the body split into rocm and
+    cpu segments.  One rocm segment's attention matmul reads a key view whose transpose ran
+    in a cpu segment: the rocm executable must treat that input as its own buffer rather than
+    follow the transpose back into the other segment.  Tokens equal the oracle's."""
+    from harness import hosteval, lowering as LW
+    from harness.runner import Runner
+    from mira_amd.target import RocmTarget
+
+    class HostLoops(RocmTarget):
+        def _check_control(self, op):
+            return "loops driven from the host"
+
+    dims = CONTROL["greedy_lm"]
+    g = cli.load_graph(os.path.join(PROGRAMS, "greedy_lm.mira"), "main", None, dims, 0, None)
+    LW.prepare(g)
+    if quantize:
+        rng = np.random.default_rng(5)
+        LW.w8a8(g, [{"prompt": rng.integers(0, dims["V"], dims["P"]).astype(np.int32)} for _ in range(2)])
+    runner = Runner(g, HostLoops(approx_f32=True), fallback=hosteval.HostTarget())
+    assert ("cpu", "while") in runner.placements()
+    for prompt in ([3, 7, 1], [0, 10, 5]):
+        feed = {"prompt": np.array(prompt, np.int32)}
+        print(f"greedy_lm host loop quantize={quantize} prompt={prompt}", flush=True)
+        (got,) = runner.run(dict(feed))
+        want = oracle_env(g, feed)[g.outputs[0]]
+        assert np.array_equal(np.asarray(got), want), (got, want)
