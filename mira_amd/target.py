@@ -164,14 +164,20 @@ class RocmTarget:
     # (mira/partition.py:74-75); others stay with the host, their sub-graphs split as usual
     supports_control_flow = True
 
-    def __init__(self, device: int = 0, debug_acc: bool = False, approx_f32: bool = False):
+    def __init__(self, device: int = 0, debug_acc: bool = False, approx_f32: bool = False,
+                 graph_loops: bool = True):
         """approx_f32: also run the float ops whose NumPy results depend on libm or on BLAS's
         summation order (softmax, f32 matmul of two float tensors, and gelu/sigmoid/tanh
         epilogue steps).  Their results then agree with the reference's to f32 rounding
-        (relative ~1e-6), not bit for bit; every other op stays bit-exact."""
+        (relative ~1e-6), not bit for bit; every other op stays bit-exact.
+        graph_loops: a while loop run on the device records its condition step and its body
+        step as two HIP graphs after the first iteration and replays them, one launch each
+        per iteration instead of one per kernel and copy (off: every iteration is queued
+        kernel by kernel)."""
         self.device = device
         self.debug_acc = debug_acc
         self.approx_f32 = approx_f32
+        self.graph_loops = graph_loops
 
     # ---------------------------------------------------------------- check
 
@@ -2007,7 +2013,12 @@ class RocmExecutable:
         the cond sub-executable, reads its one-element result back, and if it is non-zero runs
         the body and copies its outputs into the state.  Nothing but that flag leaves the GPU;
         reading it synchronises the stream, so an executable holding a device loop is not
-        captured into a HIP graph."""
+        captured into a HIP graph.  With the target's graph_loops, the two steps (copies and
+        launches) are recorded as HIP graphs after the first iteration, which ran them eagerly,
+        and replayed from then on; every buffer they touch is fixed at planning, so a replay
+        does what the eager step does.  Sub-graphs that hold control ops of their own read
+        flags on the host and stay eager."""
+        torch = _t()
         ns, nc = op.attrs["n_state"], op.attrs["n_cond"]
         cond_g, body_g = op.attrs["cond"], op.attrs["body"]
         cond = RocmExecutable(cond_g, self.target, in_loop=True)
@@ -2018,19 +2029,44 @@ class RocmExecutable:
         state = [d.f32 for d in outs]
         max_iters = int(op.attrs["max_iters"])
         feed = self._feed
+        flag = cond.device_output(cond_g.outputs[0])
+        dev = self.dev
+
+        def cond_step() -> None:
+            feed(cond, state + cond_caps)
+            cond.launch()
+
+        def body_step() -> None:
+            feed(body, state + body_caps)
+            body.launch()
+            for t, o in zip(state, body_g.outputs):
+                t.copy_(body.device_output(o).reshape(t.shape))
+
+        steps = [cond_step, body_step]
+        capture = self.target.graph_loops and not any(
+            o.is_control for sg in (cond_g, body_g) for o in sg.ops)
+
+        def record() -> None:
+            graphs = []
+            for fn in (cond_step, body_step):
+                gr = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gr):
+                    fn()                            # recorded, not run
+                graphs.append(gr)
+            steps[:] = [gr.replay for gr in graphs]
+            self.keep.extend(graphs)
 
         def run(_stream) -> None:
             for t, src in zip(state, init):
                 t.copy_(src.reshape(t.shape))
-            for _ in range(max_iters):
-                feed(cond, state + cond_caps)
-                cond.launch()
-                if not _truthy(cond.device_output(cond_g.outputs[0]), cond_g.outputs[0]):
+            for it in range(max_iters):
+                steps[0]()
+                if not _truthy(flag, cond_g.outputs[0]):
                     return
-                feed(body, state + body_caps)
-                body.launch()
-                for t, o in zip(state, body_g.outputs):
-                    t.copy_(body.device_output(o).reshape(t.shape))
+                steps[1]()
+                if it == 0 and capture and steps[0] is cond_step:
+                    torch.cuda.current_stream(dev).synchronize()
+                    record()
             raise L.RocmError(f"while loop exceeded {max_iters} iterations")
 
         self.keep += [cond, body]

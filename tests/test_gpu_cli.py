@@ -180,15 +180,18 @@ def test_device_loop_iteration_limit():
         runner.run({"x": calib[0]["x"]})
 
 
+@pytest.mark.parametrize("graph_loops", [True, False])
 @pytest.mark.parametrize("quantize", [None, "w8a8"])
 @pytest.mark.parametrize("precision", [None, "f16"])
-def test_greedy_decoder_device_loop(precision, quantize):
+def test_greedy_decoder_device_loop(precision, quantize, graph_loops):
     """The greedy KV-cache decoder's while loop run on the device in the approximate mode:
     token buffer, step counter, embedding gathers, position and cache windows (dynamic
     slices and updates), masks, attention, argmax and the prompt-or-prediction where, all
     on rocm with the integer state held in device buffers.  The decoded tokens equal the
     oracle's (the attention's f32 products and softmax agree to f32 rounding, which moves no
-    argmax here), for two prompts."""
+    argmax here), for two prompts.  With graph_loops the condition and body steps are
+    recorded as HIP graphs after the first iteration: every later iteration of both prompts
+    is a replay, with the flag read back (a synchronisation) between replays."""
     from harness import hosteval, lowering as LW
     from harness.runner import Runner
     from mira_amd.target import RocmTarget
@@ -198,17 +201,22 @@ def test_greedy_decoder_device_loop(precision, quantize):
     if quantize:
         rng = np.random.default_rng(5)
         LW.w8a8(g, [{"prompt": rng.integers(0, dims["V"], dims["P"]).astype(np.int32)} for _ in range(2)])
-    runner = Runner(g, RocmTarget(approx_f32=True), fallback=hosteval.HostTarget())
+    runner = Runner(g, RocmTarget(approx_f32=True, graph_loops=graph_loops), fallback=hosteval.HostTarget())
     placed = runner.placements()
     # the loop on rocm; before it, the prompt's write into the token buffer (an integer op
     # outside any loop) on the host
     assert placed == [("cpu", "dynamic_update_slice"), ("rocm", "while")], placed
     for prompt in ([3, 7, 1], [0, 10, 5]):
         feed = {"prompt": np.array(prompt, np.int32)}
-        print(f"greedy_lm device loop precision={precision} quantize={quantize} prompt={prompt}", flush=True)
+        print(f"greedy_lm device loop precision={precision} quantize={quantize} graph_loops={graph_loops} "
+              f"prompt={prompt}", flush=True)
         (got,) = runner.run(dict(feed))
         want = oracle_env(g, feed)[g.outputs[0]]
         assert np.array_equal(np.asarray(got), want), (got, want)
+    import torch
+    recorded = sum(isinstance(k, torch.cuda.CUDAGraph) for seg in runner.segments
+                   for k in getattr(seg.executable, "keep", []))
+    assert recorded == (2 if graph_loops else 0)
 
 
 @pytest.mark.parametrize("quantize", [None, "w8a8"])
