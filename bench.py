@@ -34,6 +34,9 @@ gpt-decode times greedy decoding with the character-level GPT (default batch 1;
 16-token prompt, --tokens generated): the whole loop resident on the GPU, one
 HIP graph replay per step, in microseconds per token, beside the eager launch
 loop and the bit-exact mode driven from the host.
+greedy-loop times the same kind of decoder written as a MIRA program with a
+runtime while loop, compiled whole for the device (approx_f32), in microseconds
+per token, beside the eager loop, the host-driven loop and the host evaluator.
 """
 from __future__ import annotations
 
@@ -258,6 +261,62 @@ def graph_replay_ms(exe, stream, steps: int, warmup: int) -> float:
         if a.shape != b.shape or a.tobytes() != b.tobytes():
             raise SystemExit(f"graph replay output {k} differs from the eager launches")
     return start.elapsed_time(stop) / steps
+
+
+def bench_greedy_loop(args) -> int:
+    """The greedy KV-cache decoder written in MIRA's language (tests/programs/greedy_lm.mira:
+    one attention head, L=2, D=64, F=128, vocab 65, a 16-token prompt and a context of T=272),
+    its runtime while loop compiled whole for rocm in approx_f32 mode: token buffer, counter,
+    gathers, cache windows, attention and argmax run in device buffers, one flag read back per
+    iteration.  Timed: the runner's whole run (prompt upload, the loop's T-1 iterations, the
+    token download) with the condition and body steps replayed as HIP graphs, beside the same
+    loop launched kernel by kernel, the loop driven from the host with its body split into
+    rocm segments, and the host evaluator alone."""
+    import torch
+    from harness import cli, hosteval, lowering as LW
+    from harness.runner import Runner
+    from mira_amd.target import RocmTarget
+    dims = {"P": 16, "V": 65, "T": 272, "D": 64, "F": 128, "L": 2}
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "programs", "greedy_lm.mira")
+    g = LW.prepare(cli.load_graph(path, "main", None, dims, 0, None))
+    feed = {"prompt": np.random.default_rng(4).integers(0, dims["V"], dims["P"]).astype(np.int32)}
+    iters = dims["T"] - 1
+
+    class HostLoops(RocmTarget):
+        def _check_control(self, op):
+            return "loops driven from the host"
+
+    def timed(runner, reps: int) -> tuple:
+        runner.run(dict(feed))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            (tok,) = runner.run(dict(feed))
+        return (time.perf_counter() - t0) / reps, np.asarray(tok)
+
+    graphs = Runner(g, RocmTarget(approx_f32=True), fallback=hosteval.HostTarget())
+    eager = Runner(g, RocmTarget(approx_f32=True, graph_loops=False), fallback=hosteval.HostTarget())
+    split = Runner(g, HostLoops(approx_f32=True), fallback=hosteval.HostTarget())
+    host = Runner(g, hosteval.HostTarget())
+    reps = max(args.steps // 4, 1)
+    graph_s, tok = timed(graphs, reps)
+    eager_s, tok_eager = timed(eager, reps)
+    split_s, tok_split = timed(split, 1)
+    host_s, tok_host = timed(host, 1)
+    assert np.array_equal(tok, tok_eager) and np.array_equal(tok, tok_split), "rocm loop modes disagree"
+    log(f"greedy loop: {1e6 * graph_s / iters:.1f} us/token (graphs), {1e6 * eager_s / iters:.1f} (eager), "
+        f"{1e6 * split_s / iters:.1f} (host-driven), {1e6 * host_s / iters:.1f} (host evaluator)")
+    print(json.dumps({
+        "workload": "greedy-loop", "program": "tests/programs/greedy_lm.mira", "dims": dims,
+        "placements": graphs.placements(), "iterations": iters, "seconds": round(graph_s, 6),
+        "us_per_token": round(1e6 * graph_s / iters, 2),
+        "eager_us_per_token": round(1e6 * eager_s / iters, 2),
+        "host_driven_us_per_token": round(1e6 * split_s / iters, 2),
+        "host_evaluator_us_per_token": round(1e6 * host_s / iters, 2),
+        "tokens_equal_host_evaluator": bool(np.array_equal(tok, tok_host)),
+        "mode": "approx_f32", "dtype": "f32", "data": "synthetic",
+        "timed": f"wall clock of the runner's whole run, mean of {reps}, after one untimed run"}))
+    return 0
 
 
 def bench_gpt(args) -> int:
@@ -611,7 +670,7 @@ def main() -> int:
     ap.add_argument("--workload", default="resnet18",
                     choices=["resnet18", "resnet18-onnx", "resnet18-f16", "mlp50m", "mlp50m-int8", "mobilenetv2",
                              "mobilenetv2-f16",
-                             "gpt-decode"])
+                             "gpt-decode", "greedy-loop"])
     ap.add_argument("--tokens", type=int, default=256, help="gpt-decode: tokens generated per sequence")
     ap.add_argument("--per-launch", action="store_true", help="per-launch time against each launch's roofline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -639,9 +698,12 @@ def main() -> int:
         return 2
     if args.batch is None:
         args.batch = {"resnet18": 256, "resnet18-onnx": 256, "resnet18-f16": 256, "mlp50m": 1, "mlp50m-int8": 1,
-                      "mobilenetv2": 128, "mobilenetv2-f16": 128, "gpt-decode": 1}[args.workload]
+                      "mobilenetv2": 128, "mobilenetv2-f16": 128, "gpt-decode": 1,
+                      "greedy-loop": 1}[args.workload]
     if args.workload == "gpt-decode":
         return bench_gpt(args)
+    if args.workload == "greedy-loop":
+        return bench_greedy_loop(args)
     if args.per_launch:
         return per_launch(args)
     if args.workload != "resnet18":

@@ -422,9 +422,14 @@ def _bcast_mode(oshape: tuple, rshape: tuple, is_conv: bool) -> Optional[int]:
 class RocmExecutable:
     """A compiled rocm segment: device buffers, packed constants and a launch list."""
 
-    def __init__(self, g: "Graph", target: RocmTarget, in_loop: bool = False):
+    def __init__(self, g: "Graph", target: RocmTarget, in_loop: bool = False, bind: Optional[dict] = None):
+        """bind: graph input -> a contiguous f32 device tensor of its size that the launches read
+        the input from in place of a staging buffer of their own (a device loop's state and
+        captures); `bound` lists the inputs that took it."""
         torch = _t()
         self.g = g
+        self.bind = bind or {}
+        self.bound: set = set()
         self.target = target
         self.lib = L.load()
         if not torch.cuda.is_available():
@@ -1031,6 +1036,11 @@ class RocmExecutable:
         torch = _t()
         lib = self.lib
         stage = self.prealias.get(v)
+        bound = self.bind.get(v)
+        if stage is None and bound is not None and bound.is_contiguous() and bound.numel() == v.type.numel and \
+                not any(op.inputs[0] is v for op in self.input_casts):     # those round it in place
+            stage = bound.view(v.type.shape)
+            self.bound.add(v)
         if stage is None:
             stage = torch.empty(v.type.shape, dtype=torch.float32, device=self.dev)
         self.staging[v] = stage
@@ -2005,28 +2015,43 @@ class RocmExecutable:
     @staticmethod
     def _feed(sub: "RocmExecutable", values: list) -> None:
         for ph, t in zip(sub.g.inputs, values):
-            sub.device_input(ph).copy_(t.reshape(ph.type.shape))
+            if ph not in sub.bound:
+                sub.device_input(ph).copy_(t.reshape(ph.type.shape))
+
+    def _loop_body(self, body_g: "Graph", state: list, caps: list) -> "RocmExecutable":
+        """The body sub-executable reading the loop state and captures in place.  Its outputs
+        are copied into the state one after another, so an output stored in another slot's
+        buffer would be read after that slot was overwritten: such a body gets staging
+        buffers of its own instead."""
+        body = RocmExecutable(body_g, self.target, in_loop=True, bind=dict(zip(body_g.inputs, state + caps)))
+        for k, o in enumerate(body_g.outputs):
+            p = body.device_output(o).untyped_storage().data_ptr()
+            if any(j != k and t.untyped_storage().data_ptr() == p for j, t in enumerate(state)):
+                return RocmExecutable(body_g, self.target, in_loop=True)
+        return body
 
     def _emit_while(self, op: "Op") -> None:
         """A while op run on the device (mira/backends/cpu.py:44-51's semantics): the loop
-        state lives in the op's result buffers; each iteration copies state and captures into
-        the cond sub-executable, reads its one-element result back, and if it is non-zero runs
-        the body and copies its outputs into the state.  Nothing but that flag leaves the GPU;
-        reading it synchronises the stream, so an executable holding a device loop is not
-        captured into a HIP graph.  With the target's graph_loops, the two steps (copies and
-        launches) are recorded as HIP graphs after the first iteration, which ran them eagerly,
+        state lives in the op's result buffers, which the cond and body sub-executables read in
+        place, as they read the captures; each iteration runs the cond, reads its one-element
+        result back, and if it is non-zero runs the body and copies its outputs into the state.
+        Nothing but that flag leaves the GPU; reading it synchronises the stream, so an
+        executable holding a device loop is not captured into a HIP graph.  With the target's
+        graph_loops, the two steps (copies and launches) are recorded as HIP graphs after the first iteration, which ran them eagerly,
         and replayed from then on; every buffer they touch is fixed at planning, so a replay
         does what the eager step does.  Sub-graphs that hold control ops of their own read
         flags on the host and stay eager."""
         torch = _t()
         ns, nc = op.attrs["n_state"], op.attrs["n_cond"]
         cond_g, body_g = op.attrs["cond"], op.attrs["body"]
-        cond = RocmExecutable(cond_g, self.target, in_loop=True)
-        body = RocmExecutable(body_g, self.target, in_loop=True)
         ins = [self._c_order(v) for v in op.inputs]
         init, cond_caps, body_caps = ins[:ns], ins[ns:ns + nc], ins[ns + nc:]
         outs = self._loop_results(op)
         state = [d.f32 for d in outs]
+        # both steps read the state and the captures in place: only the body's outputs are
+        # copied, into the state, once per iteration
+        cond = RocmExecutable(cond_g, self.target, in_loop=True, bind=dict(zip(cond_g.inputs, state + cond_caps)))
+        body = self._loop_body(body_g, state, body_caps)
         max_iters = int(op.attrs["max_iters"])
         feed = self._feed
         flag = cond.device_output(cond_g.outputs[0])
