@@ -442,7 +442,17 @@ int mr_bmm_f32(const float* a, const float* w, int32_t nb, const int64_t* bdim, 
   // lanes along k when w's k axis is the contiguous one and long enough to give every
   // lane work, else along n
   auto log2_ceil = [](int64_t v) { int l = 0; while ((int64_t(1) << l) < v && l < 6) ++l; return l; };
-  const int nb_log2 = (p.swk == 1 && p.swn != 1 && K >= 64) ? 6 - log2_ceil(K) : log2_ceil(N);
+  const bool along_k = p.swk == 1 && p.swn != 1 && K >= 64;
+  int nb_log2 = along_k ? 6 - log2_ceil(K) : log2_ceil(N);
+  // along n with too few rows to fill the GPU (a decode step's [1, K] x [K, N]), each lane's
+  // serial k loop is the latency: narrow the column block until a lane walks at most 8 k
+  // (one batch of loads in flight), down to 4 columns per wave
+  if (!along_k) {
+    const int64_t rows = p.batches * M;
+    while (nb_log2 > 2 && rows * ((N + (int64_t(1) << nb_log2) - 1) >> nb_log2) < 1024 &&
+           (K << nb_log2) > 64 * 8)
+      --nb_log2;
+  }
   const int64_t jobs = p.batches * M * ((N + (int64_t(1) << nb_log2) - 1) >> nb_log2);
   hipLaunchKernelGGL(mr::bmm_f32_kernel, dim3(mr::grid_1d(jobs * 64, 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), p, e, nb_log2, jobs);

@@ -214,7 +214,10 @@ def _bstrides(shape, rs):
 @pytest.mark.parametrize("ashape,wshape", [((1, 4, 1, 16), (1, 4, 16, 273)), ((1, 4, 1, 273), (1, 4, 273, 16)),
                                            ((2, 3, 5, 7), (7, 9)), ((4, 1, 8, 32), (1, 3, 32, 16)),
                                            ((64, 128), (128, 96)), ((2, 1, 3, 2, 5, 6), (2, 2, 1, 2, 6, 4)),
-                                           ((2, 1, 2, 3, 2, 5, 6), (2, 2, 1, 3, 2, 6, 4))])
+                                           ((2, 1, 2, 3, 2, 5, 6), (2, 2, 1, 3, 2, 6, 4)),
+                                           # decode-shaped rows: column blocks narrowed to 8 and 4
+                                           ((1, 64), (64, 65)), ((1, 128), (128, 64)),
+                                           ((1, 1000), (1000, 300)), ((1, 2, 1, 128), (1, 2, 128, 64))])
 def test_bmm_f32_within_tolerance(lib, ashape, wshape):
     """a @ w with NumPy batch broadcasting and a scale+mask epilogue: every element within
     1e-5 of the float64 product's magnitude sum (|a| @ |w|), the bound for any f32 order, plus
