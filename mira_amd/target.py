@@ -1954,6 +1954,16 @@ class RocmExecutable:
         constant start."""
         x, r = op.inputs[0], op.result
         xt = self._c_order(x)
+        begin, sz, full = list(op.attrs["begin"]), list(op.attrs["size"]), list(x.type.shape)
+        # a window that is one contiguous run of x's C-order buffer (size-1 axes, then one
+        # partial axis, then whole axes) is a view of it, as reshape is
+        a = next((i for i, z in enumerate(sz) if z != 1), len(sz))
+        if r not in self.images and xt.is_contiguous() and \
+                all(begin[i] == 0 and sz[i] == full[i] for i in range(a + 1, len(sz))):
+            off = sum(b * int(np.prod(full[i + 1:], dtype=np.int64)) for i, b in enumerate(begin))
+            self.dv[r] = DevValue(r, nhwc=False, f32=xt.reshape(-1).narrow(0, off, r.type.numel).view(r.type.shape))
+            self._finish_i8(self.dv[r], None)
+            return
         st = self._upload(np.asarray(op.attrs["begin"], np.int32))
         shape, size = self._shape4(x.type.shape), self._shape4(op.attrs["size"])
         self.keep += [shape, size]
