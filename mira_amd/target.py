@@ -1851,15 +1851,27 @@ class RocmExecutable:
         ld = int(np.prod(r.type.shape[axis:], dtype=np.int64))
         at = 0
         lib = self.lib
+        # this op's own buffer has no other writer: its constant pieces (the fixed entries of a
+        # window start such as [l, t, 0]) are copied once, here, and never again
+        prefill = op not in self.concat_out
+        filled = False
         for v in op.inputs:
             inner = int(np.prod(v.type.shape[axis:], dtype=np.int64))
             if outer * inner == 0 or v in self.prealias:      # empty, or already in place
                 at += inner
                 continue
             x = self._c_order(v)
+            if prefill and v in self.consts:
+                L.check(lib.mr_copy_rows_f32(x.data_ptr(), outer, inner, y.data_ptr(), ld, at,
+                                             _t().cuda.current_stream(self.dev).cuda_stream), "mr_copy_rows_f32")
+                filled = True
+                at += inner
+                continue
             self._add("concat", lambda s, x=x, inner=inner, at=at: L.check(lib.mr_copy_rows_f32(
                 x.data_ptr(), outer, inner, y.data_ptr(), ld, at, s), "mr_copy_rows_f32"), nbytes=8 * outer * inner)
             at += inner
+        if filled:          # done before any launch, whichever stream that is queued on
+            _t().cuda.current_stream(self.dev).synchronize()
         self._publish(out, y)
 
     def _emit_elementwise(self, op: "Op") -> None:
