@@ -22,17 +22,18 @@ TARGETS = ["rocm"]
 
 
 def get_target(name: str, **options):
-    """The rocm branch of MIRA's get_target: options device (int), debug_acc (bool) and
+    """The rocm branch of MIRA's get_target: options device (int), debug_acc (bool),
     approx_f32 (bool: also run softmax, f32 matmuls of two tensors and libm epilogue steps,
-    to f32 rounding instead of bit for bit)."""
+    to f32 rounding instead of bit for bit) and graph_loops (bool, default True: a while loop
+    run on the device replays its condition and body steps as HIP graphs)."""
     if name != "rocm":
         raise ValueError(f"unknown target '{name}' (this package provides: rocm)")
     from .target import RocmTarget
-    unknown = set(options) - {"device", "debug_acc", "approx_f32"}
+    unknown = set(options) - {"device", "debug_acc", "approx_f32", "graph_loops"}
     if unknown:
         raise ValueError(f"unknown rocm target options: {sorted(unknown)}")
     return RocmTarget(device=options.get("device", 0), debug_acc=options.get("debug_acc", False),
-                      approx_f32=options.get("approx_f32", False))
+                      approx_f32=options.get("approx_f32", False), graph_loops=options.get("graph_loops", True))
 
 
 __all__ = ["get_target", "TARGETS"]

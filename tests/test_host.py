@@ -489,3 +489,16 @@ def test_check_rejects_int8_operands_past_the_kernel_limits():
     assert t.check(qconv(1024, 64, 180)) is None            # 2.12e9 bytes, under 2^31
     assert "2 GiB" in t.check(qconv(1024, 64, 200))
     assert "pixels" in t.check(qconv(2 ** 16, 4, 256))
+
+
+def test_get_target_options():
+    """The registry branch builds a RocmTarget from MIRA's keyword options (no GPU needed to
+    build one) and rejects names it does not know."""
+    from mira_amd import get_target
+    t = get_target("rocm", approx_f32=True, graph_loops=False)
+    assert (t.device, t.debug_acc, t.approx_f32, t.graph_loops) == (0, False, True, False)
+    assert get_target("rocm").graph_loops
+    with pytest.raises(ValueError, match="unknown rocm target options"):
+        get_target("rocm", graph_loop=True)
+    with pytest.raises(ValueError, match="unknown target"):
+        get_target("npu-sim")
